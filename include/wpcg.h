@@ -1,0 +1,168 @@
+/*
+ * wpcg.h -- C ABI of the MI355X (gfx950) decode backend for WPC-quantized
+ * weights: the drop-in boundary for the reference's quantized GEMV path.
+ *
+ * Plain C types only: opaque handles, pointers, sizes, int status codes. No
+ * exceptions or panics cross this boundary. Every call returns WPCG_OK or an
+ * error code; wpcg_last_error_string() describes the last failure on the
+ * calling thread.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository,
+ * jpytka666-jpg/wpc-engine):
+ *   trait Linear            wpc-runtime/src/weights.rs:17-22
+ *   trait EmbeddingTable    wpc-runtime/src/weights.rs:25-31
+ *   WpcModelDataV4          wpc-runtime/src/wpc_weights_v4.rs:39-99
+ *   WpcLinearV4             wpc-runtime/src/wpc_weights_v4.rs:117-194
+ *   WpcEmbeddingV4          wpc-runtime/src/wpc_weights_v4.rs:196-273
+ *   WpcModelDataV3/LinearV3/EmbeddingV3  wpc-runtime/src/wpc_weights_v3.rs
+ *
+ * Device pointers, streams and threading:
+ *   - `*_dev` arguments are device pointers on the handle's device;
+ *     `wpcg_stream` is a hipStream_t passed as void*, NULL meaning the
+ *     context's own stream. Device calls are stream-ordered and return
+ *     before the work completes; `*_host` twins are synchronous.
+ *   - Handles may be used from several threads; calls on one handle that
+ *     use its internal staging buffers (`*_host`) are serialized internally.
+ */
+#ifndef WPCG_H
+#define WPCG_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+#define WPCG_OK             0
+#define WPCG_E_IO           1 /* file missing or unreadable                   */
+#define WPCG_E_FORMAT       2 /* malformed meta / block range / block_size    */
+#define WPCG_E_SHAPE        3 /* in_features % 128, block-count mismatch      */
+#define WPCG_E_NOTFOUND     4 /* tensor name absent from the meta             */
+#define WPCG_E_DEVICE       5 /* no usable GPU, or a HIP runtime failure      */
+#define WPCG_E_ARG          6 /* NULL handle / pointer, bad enum, bad size    */
+#define WPCG_E_NOMEM        7 /* host or device allocation failed             */
+#define WPCG_E_UNSUPPORTED  8 /* valid request this build does not provide    */
+
+/* ---- enums ---- */
+#define WPCG_SCHEME_V3 3 /* 6-bit codes, 100-byte blocks (wpc-format/src/lib.rs:202-292) */
+#define WPCG_SCHEME_V4 4 /* 4-bit codes, 68-byte blocks  (wpc-format/src/lib.rs:318-391) */
+
+/* GEMV arithmetic. EXACT reproduces matvec_v4_fused / matvec_v3_fused
+ * (wpc-eval/src/fused_kernel.rs:163-189, 237-271) bit for bit: eight fp32
+ * accumulators with dequant fma(code, scale, zp), then hsum_avx2's order.
+ * FAST regroups each block as scale*sum(code*x) + zp*sum(x) with fp32
+ * accumulation; it is within the reference's 1e-4 relative tolerance but
+ * not bit-identical. */
+#define WPCG_MODE_EXACT 0
+#define WPCG_MODE_FAST  1
+
+/* Dequantization rounding. FMA: fma(code, scale, zp), one rounding, as the
+ * AVX2 GEMV does. TWO: zp + code*scale, two roundings, as row_decode_into_v4
+ * and the scalar fallbacks do (wpc_weights_v4.rs:111, fused_kernel.rs:289). */
+#define WPCG_ROUND_FMA 0
+#define WPCG_ROUND_TWO 1
+
+typedef struct wpcg_ctx wpcg_ctx;
+typedef struct wpcg_artifact wpcg_artifact;
+typedef struct wpcg_linear wpcg_linear;
+typedef struct wpcg_event wpcg_event;
+typedef void* wpcg_stream;
+
+/* ---- library ---- */
+const char* wpcg_last_error_string(void);
+const char* wpcg_version(void);
+int wpcg_device_count(int* n);
+
+/* ---- context: one GPU plus a default stream (no reference counterpart:
+ * the reference is CPU-only; this is the device the handles live on) ---- */
+int wpcg_ctx_create(int device, wpcg_ctx** out);
+int wpcg_ctx_destroy(wpcg_ctx* ctx);
+int wpcg_ctx_stream(wpcg_ctx* ctx, wpcg_stream* out);
+int wpcg_ctx_sync(wpcg_ctx* ctx);
+
+/* Device memory and copies on the context's stream (synchronous copies). */
+int wpcg_dev_alloc(wpcg_ctx* ctx, size_t bytes, void** out_dev);
+int wpcg_dev_free(wpcg_ctx* ctx, void* dev);
+int wpcg_memcpy_h2d(wpcg_ctx* ctx, void* dst_dev, const void* src, size_t bytes);
+int wpcg_memcpy_d2h(wpcg_ctx* ctx, void* dst, const void* src_dev, size_t bytes);
+int wpcg_memcpy_d2d(wpcg_ctx* ctx, void* dst_dev, const void* src_dev, size_t bytes);
+
+/* Timing events recorded on a stream (NULL = context stream). */
+int wpcg_event_create(wpcg_ctx* ctx, wpcg_event** out);
+int wpcg_event_destroy(wpcg_event* ev);
+int wpcg_event_record(wpcg_event* ev, wpcg_stream stream);
+int wpcg_event_elapsed_ms(wpcg_event* start, wpcg_event* stop, float* ms);
+
+/* ---- artifact: model_v{3,4}.meta + model_v{3,4}.wpc ----
+ * Replaces WpcModelDataV4::open (wpc_weights_v4.rs:46-77) and its v3 twin:
+ * reads the JSON meta ({"layers":[{"name","shape","offset_bytes",
+ * "size_bytes"}],"block_size"}), requires block_size == 128, memory-maps the
+ * .wpc file. Errors: E_IO (missing/unreadable), E_FORMAT (bad JSON,
+ * block_size != 128). */
+int wpcg_artifact_open(const char* dir, int scheme, wpcg_artifact** out);
+int wpcg_artifact_close(wpcg_artifact* a);
+/* tensor_range + blocks_for (wpc_weights_v4.rs:80-98): the tensor's bytes in
+ * the mapping. E_NOTFOUND for an unknown name; E_FORMAT when size is not a
+ * whole number of blocks or the range exceeds the file. */
+int wpcg_artifact_tensor(wpcg_artifact* a, const char* name, const void** bytes,
+                         uint64_t* size);
+int wpcg_artifact_tensor_count(wpcg_artifact* a, uint64_t* n);
+
+/* ---- Linear ----
+ * Replaces WpcLinearV4::new (wpc_weights_v4.rs:127-155) / WpcLinearV3::new:
+ * E_SHAPE unless in_f % 128 == 0 and the tensor holds out_f*(in_f/128)
+ * blocks. The blocks are transcoded on the host into the device layout and
+ * uploaded; `bias` (host, out_f floats) may be NULL. */
+int wpcg_linear_create(wpcg_ctx* ctx, wpcg_artifact* a, const char* name, uint64_t out_f,
+                       uint64_t in_f, const float* bias, wpcg_linear** out);
+/* The same from blocks in memory (reference on-disk byte layout). */
+int wpcg_linear_from_blocks(wpcg_ctx* ctx, int scheme, const void* blocks, uint64_t nbytes,
+                            uint64_t out_f, uint64_t in_f, const float* bias,
+                            wpcg_linear** out);
+int wpcg_linear_destroy(wpcg_linear* lin);
+/* Linear::in_features / out_features (weights.rs:18-19) */
+int wpcg_linear_shape(wpcg_linear* lin, uint64_t* out_f, uint64_t* in_f);
+int wpcg_linear_set_mode(wpcg_linear* lin, int mode);
+/* Device bytes the weights occupy (codes + block parameters). */
+int wpcg_linear_device_bytes(wpcg_linear* lin, uint64_t* bytes);
+
+/* Linear::matvec (weights.rs:20-21, wpc_weights_v4.rs:165-193):
+ * y = W x (+ bias); y is fully overwritten. x_dev: in_f floats, y_dev:
+ * out_f floats; x and y must not overlap. */
+int wpcg_linear_matvec(wpcg_linear* lin, const float* x_dev, float* y_dev, wpcg_stream stream);
+/* Host-pointer twin with exactly Linear::matvec's synchronous semantics. */
+int wpcg_linear_matvec_host(wpcg_linear* lin, const float* x, float* y);
+
+/* EmbeddingTable::embed (weights.rs:28; wpc_weights_v4.rs:241-249): decode
+ * row `token` into out (in_f floats) as zp + code*scale with two roundings.
+ * EmbeddingTable::logits (weights.rs:30) is wpcg_linear_matvec on the same
+ * table. E_ARG when token >= out_f. */
+int wpcg_linear_embed(wpcg_linear* lin, uint32_t token, float* out_dev, wpcg_stream stream);
+int wpcg_linear_embed_host(wpcg_linear* lin, uint32_t token, float* out);
+
+/* Whole-matrix dequantization to fp32, row-major [out_f][in_f], natural
+ * weight order, in the given rounding (WPCG_ROUND_*). For parity checks. */
+int wpcg_linear_dequant(wpcg_linear* lin, int rounding, float* w_dev, wpcg_stream stream);
+
+/* A second device copy of the same weights (device-to-device; no reference
+ * counterpart). Used to rotate a working set larger than the 256 MB
+ * Infinity Cache when measuring HBM-bound throughput. */
+int wpcg_linear_clone(wpcg_linear* lin, wpcg_linear** out);
+
+/* ---- HIP graphs over the context stream (no reference counterpart) ----
+ * wpcg_graph_begin starts capturing the context's stream; device calls with
+ * stream NULL are then recorded instead of run, until wpcg_graph_end
+ * instantiates them. Synchronous *_host calls must not be made while
+ * capturing. */
+typedef struct wpcg_graph wpcg_graph;
+int wpcg_graph_begin(wpcg_ctx* ctx);
+int wpcg_graph_end(wpcg_ctx* ctx, wpcg_graph** out);
+int wpcg_graph_launch(wpcg_graph* g, wpcg_stream stream);
+int wpcg_graph_destroy(wpcg_graph* g);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* WPCG_H */
