@@ -80,7 +80,7 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--scheme", type=int, default=3, choices=(3, 4))
-    ap.add_argument("--mode", default="exact", choices=("exact", "fast"))
+    ap.add_argument("--mode", default="fast", choices=("exact", "fast"))
     ap.add_argument("--min-bytes", type=float, default=1.0e9,
                     help="rotated working set, bytes (>= 1 GB defeats the 256 MB MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -108,7 +108,7 @@ def main():
     xs = {c: synth.random_x(c, seed=c) for c in sorted({c for _, _, c in QWEN3_4B})}
 
     ctx = wpcg.Context(0)
-    base = [wpcg.WpcLinear.from_blocks(ctx, scheme, b, r, c).set_mode(mode)
+    base = [wpcg.WpcLinear.from_blocks(ctx, scheme, b, r, c)
             for b, (_, r, c) in zip(blocks, QWEN3_4B)]
     step_bytes = sum(gemv_bytes(r, c, scheme) for _, r, c in QWEN3_4B)
     weight_bytes = sum(l.device_bytes() for l in base)
@@ -117,35 +117,51 @@ def main():
         f"({copies * weight_bytes / 1e9:.2f} GB rotated)")
     sets = [base] + [[l.clone() for l in base] for _ in range(copies - 1)]
     xb = {c: ctx.upload(x) for c, x in xs.items()}
-    yb = {r: ctx.alloc(4 * r) for r in sorted({r for _, r, _ in QWEN3_4B})}
+    yb = {name: ctx.alloc(4 * r) for name, r, _ in QWEN3_4B}
+    names = [n for n, _, _ in QWEN3_4B]
 
     def one_round():
+        # one step per copy: q/k/v share their input and one launch, as do
+        # gate/up; o and down run alone (their inputs come from other ops)
         for s in sets:
-            for lin, (_, r, c) in zip(s, QWEN3_4B):
-                lin.matvec_dev(xb[c], yb[r])
+            L = dict(zip(names, s))
+            wpcg.matvec_multi([L["q_proj"], L["k_proj"], L["v_proj"]], [xb[2560]] * 3,
+                              [yb["q_proj"], yb["k_proj"], yb["v_proj"]])
+            L["o_proj"].matvec_dev(xb[4096], yb["o_proj"])
+            wpcg.matvec_multi([L["gate_proj"], L["up_proj"]], [xb[2560]] * 2,
+                              [yb["gate_proj"], yb["up_proj"]])
+            L["down_proj"].matvec_dev(xb[9728], yb["down_proj"])
 
-    graph = ctx.capture(one_round)  # `copies` steps per replay
-    launches = max(1, -(-args.warmup // copies))
-    reps = max(1, -(-args.steps // copies))
-    steps = reps * copies
-    log(f"warm-up {launches * copies} steps")
-    for _ in range(launches):
-        graph.launch()
-    ctx.sync()
-    e0, e1 = ctx.event(), ctx.event()
-    log(f"timing {steps} steps ({steps * len(QWEN3_4B)} GEMV launches)")
-    e0.record()
-    for _ in range(reps):
-        graph.launch()
-    e1.record()
-    ms = e0.elapsed_ms(e1)
-    ctx.sync()
-    secs = ms / 1e3
-    value = step_bytes * steps / secs / 1e9
-    n_launch = steps * len(QWEN3_4B)
-    avg_launch_us = ms * 1e3 / n_launch
-    log(f"{value:.1f} GB/s ({100 * value / PEAK_GBPS:.1f}% of peak), {ms / steps * 1e3:.2f} us/step, "
-        f"avg GEMV launch {avg_launch_us:.2f} us")
+    def measure(mode):
+        for s in sets:
+            for l in s:
+                l.set_mode(mode)
+        graph = ctx.capture(one_round)  # `copies` steps per replay
+        launches = max(1, -(-args.warmup // copies))
+        reps = max(1, -(-args.steps // copies))
+        for _ in range(launches):
+            graph.launch()
+        ctx.sync()
+        e0, e1 = ctx.event(), ctx.event()
+        e0.record()
+        for _ in range(reps):
+            graph.launch()
+        e1.record()
+        ms = e0.elapsed_ms(e1)
+        ctx.sync()
+        steps = reps * copies
+        n_launch = steps * (4 if mode == wpcg.MODE_FAST else len(QWEN3_4B))
+        return (step_bytes * steps / (ms / 1e3) / 1e9, ms, steps, launches * copies,
+                ms * 1e3 / n_launch, n_launch)
+
+    other = "exact" if args.mode == "fast" else "fast"
+    log(f"timing {other} mode")
+    o_val = measure(wpcg.MODE_EXACT if other == "exact" else wpcg.MODE_FAST)[0]
+    log(f"{other}: {o_val:.1f} GB/s ({100 * o_val / PEAK_GBPS:.1f}% of peak)")
+    log(f"timing {args.mode} mode, {args.steps} steps")
+    value, ms, steps, warm, avg_launch_us, n_launch = measure(mode)
+    log(f"{args.mode}: {value:.1f} GB/s ({100 * value / PEAK_GBPS:.1f}% of peak), "
+        f"{ms / steps * 1e3:.2f} us/step, {n_launch} launches, avg {avg_launch_us:.2f} us")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -160,7 +176,7 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": launches * copies,
+        "warmup": warm,
         "ms_per_step": round(ms / steps, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -174,6 +190,8 @@ def main():
             "mode": args.mode,
             "bytes_per_step": step_bytes,
             "pct_of_peak": round(100 * value / PEAK_GBPS, 2),
+            "launches_per_step": n_launch // steps,
+            f"{other}_mode_gbps": round(o_val, 2),
         },
         "roofline": {
             "bound": "hbm",

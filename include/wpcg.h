@@ -76,7 +76,10 @@ const char* wpcg_version(void);
 int wpcg_device_count(int* n);
 
 /* ---- context: one GPU plus a default stream (no reference counterpart:
- * the reference is CPU-only; this is the device the handles live on) ---- */
+ * the reference is CPU-only; this is the device the handles live on) ----
+ * Handles created on a context (linears, events, graphs) keep it alive:
+ * after wpcg_ctx_destroy the caller must not use `ctx` again, but existing
+ * handles keep working, and the stream is released with the last of them. */
 int wpcg_ctx_create(int device, wpcg_ctx** out);
 int wpcg_ctx_destroy(wpcg_ctx* ctx);
 int wpcg_ctx_stream(wpcg_ctx* ctx, wpcg_stream* out);
@@ -125,6 +128,16 @@ int wpcg_linear_destroy(wpcg_linear* lin);
 /* Linear::in_features / out_features (weights.rs:18-19) */
 int wpcg_linear_shape(wpcg_linear* lin, uint64_t* out_f, uint64_t* in_f);
 int wpcg_linear_set_mode(wpcg_linear* lin, int mode);
+/* FAST mode splits K over `kslices` workgroups per 32-row tile group
+ * (0 = the library's choice for the shape; capped so a slice holds at most
+ * 32 blocks). Replaces the matrix's split-K workspace: graphs captured
+ * earlier with this linear must be destroyed first. No reference
+ * counterpart (a tuning knob). */
+int wpcg_linear_set_kslices(wpcg_linear* lin, int kslices);
+int wpcg_linear_kslices(wpcg_linear* lin, int* kslices);
+/* The split wpcg_linear_set_kslices would use for an out_f x in_f matrix
+ * (host-only query; every slice is non-empty and holds at most 32 blocks). */
+int wpcg_plan_kslices(uint64_t out_f, uint64_t in_f, int requested, int* kslices);
 /* Device bytes the weights occupy (codes + block parameters). */
 int wpcg_linear_device_bytes(wpcg_linear* lin, uint64_t* bytes);
 
@@ -134,6 +147,15 @@ int wpcg_linear_device_bytes(wpcg_linear* lin, uint64_t* bytes);
 int wpcg_linear_matvec(wpcg_linear* lin, const float* x_dev, float* y_dev, wpcg_stream stream);
 /* Host-pointer twin with exactly Linear::matvec's synchronous semantics. */
 int wpcg_linear_matvec_host(wpcg_linear* lin, const float* x, float* y);
+
+/* n independent matvecs, ys[i] = W_i xs[i] (+ bias_i), issued together: FAST
+ * members of one scheme share one launch (up to 8 per launch), EXACT members
+ * launch one by one. Matrices that read the same input (q/k/v, gate/up, the
+ * experts of a token) fill the GPU together. The linears' outputs must not
+ * overlap each other or any input. No reference counterpart: the reference
+ * calls Linear::matvec once per matrix (qwen3_moe_model.rs:430-432, 516-517). */
+int wpcg_linear_matvec_multi(int n, wpcg_linear* const* lins, const float* const* xs,
+                             float* const* ys, wpcg_stream stream);
 
 /* EmbeddingTable::embed (weights.rs:28; wpc_weights_v4.rs:241-249): decode
  * row `token` into out (in_f floats) as zp + code*scale with two roundings.

@@ -159,3 +159,20 @@ def test_synth_v3_packing_matches_the_oracle_codec():
     packed = synth.pack_v3_codes(codes)
     for r in range(20):
         assert np.array_equal(packed[r], O.v3_pack(codes[r]))
+
+
+def test_fast_split_plan_never_makes_an_empty_slice():
+    # FAST mode splits each row's nb blocks into slices of ceil(nb/k) blocks;
+    # every slice must start inside the row (an empty trailing slice would
+    # address blocks past the end of the matrix) and fit the 32-block LDS
+    # stage. Checked for every block count and requested split.
+    for nb in range(1, 161):
+        for req in [0] + list(range(1, nb + 3)):
+            for rows in (16, 1024, 9728):
+                k = wpcg.plan_kslices(rows, nb * 128, req)
+                nbk = -(-nb // k)
+                assert 1 <= k <= nb and nbk <= 32, (nb, req, k)
+                assert (k - 1) * nbk < nb <= k * nbk, (nb, req, k, nbk)
+    with pytest.raises(wpcg.WpcgError) as e:
+        wpcg.plan_kslices(4, 100)
+    assert e.value.code == wpcg.E_SHAPE

@@ -31,6 +31,19 @@ int hip_fail(hipError_t e, const char* what)
     return fail(WPCG_E_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+void ctx_retain(wpcg_ctx* c) { c->refs.fetch_add(1, std::memory_order_relaxed); }
+
+void ctx_release(wpcg_ctx* c)
+{
+    if (c->refs.fetch_sub(1, std::memory_order_acq_rel) != 1) return;
+    (void)hipSetDevice(c->device);
+    if (c->stream) {
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipStreamDestroy(c->stream);
+    }
+    delete c;
+}
+
 namespace {
 
 hipStream_t pick(wpcg_ctx* ctx, wpcg_stream s)
@@ -58,32 +71,85 @@ void free_matrix(DeviceMatrix& m)
     m.params = nullptr;
 }
 
-// Transcodes reference blocks to the device planes and uploads them in
-// chunks (bounded host staging).
-int upload_matrix(wpcg_ctx* ctx, int scheme, const uint8_t* blocks, uint64_t n_blocks,
-                  DeviceMatrix& m)
+void free_plan(FastPlan& p)
 {
-    const uint64_t nbk = n_blocks ? n_blocks : 1;
-    WPCG_HIP(hipMalloc(&m.codes, nbk * 64));
-    WPCG_HIP(hipMalloc(&m.params, nbk * 4));
-    if (scheme == 3) WPCG_HIP(hipMalloc(&m.hp, nbk * 32));
-    const uint64_t chunk = 1u << 16;
-    std::vector<uint8_t> c(chunk * 64), h(scheme == 3 ? chunk * 32 : 0);
-    std::vector<uint32_t> p(chunk);
-    const uint64_t bpb = block_bytes(scheme);
-    for (uint64_t b0 = 0; b0 < n_blocks; b0 += chunk) {
-        const uint64_t n = std::min(chunk, n_blocks - b0);
-        if (scheme == 4)
-            transcode_v4(blocks + b0 * bpb, n, c.data(), p.data());
-        else
-            transcode_v3(blocks + b0 * bpb, n, c.data(), h.data(), p.data());
-        WPCG_HIP(hipMemcpyAsync(m.codes + b0 * 64, c.data(), n * 64, hipMemcpyHostToDevice, ctx->stream));
-        WPCG_HIP(hipMemcpyAsync(m.params + b0, p.data(), n * 4, hipMemcpyHostToDevice, ctx->stream));
-        if (scheme == 3)
-            WPCG_HIP(hipMemcpyAsync(m.hp + b0 * 32, h.data(), n * 32, hipMemcpyHostToDevice, ctx->stream));
-        WPCG_HIP(hipStreamSynchronize(ctx->stream));
+    if (p.part) (void)hipFree(p.part);
+    if (p.counters) (void)hipFree(p.counters);
+    p.part = nullptr;
+    p.counters = nullptr;
+}
+
+// Device bytes of the three planes, rows padded to a 16-row tile.
+uint64_t plane_blocks(const DeviceMatrix& m) { return std::max<uint64_t>(1, m.rows_pad * m.nb); }
+
+int alloc_matrix(DeviceMatrix& m)
+{
+    const uint64_t nb = plane_blocks(m);
+    WPCG_HIP(hipMalloc(&m.codes, nb * 64));
+    WPCG_HIP(hipMalloc(&m.params, nb * 4));
+    if (m.scheme == 3) WPCG_HIP(hipMalloc(&m.hp, nb * 32));
+    return WPCG_OK;
+}
+
+// Transcodes reference blocks to the device planes and uploads them in
+// chunks of whole 16-row tiles (bounded host staging). Padding rows stay 0.
+int upload_matrix(wpcg_ctx* ctx, const uint8_t* blocks, DeviceMatrix& m)
+{
+    if (int rc = alloc_matrix(m)) return rc;
+    const uint64_t nb = m.nb, pb = plane_blocks(m);
+    hipStream_t s = ctx->stream;
+    WPCG_HIP(hipMemsetAsync(m.codes, 0, pb * 64, s));
+    WPCG_HIP(hipMemsetAsync(m.params, 0, pb * 4, s));
+    if (m.hp) WPCG_HIP(hipMemsetAsync(m.hp, 0, pb * 32, s));
+    if (nb == 0 || m.rows == 0) return hipStreamSynchronize(s) == hipSuccess ? WPCG_OK : fail(WPCG_E_DEVICE, "sync");
+    const uint64_t bpb = block_bytes(m.scheme);
+    // ~4 MiB of codes per chunk, a whole number of tiles
+    uint64_t chunk_rows = std::max<uint64_t>(TILE_ROWS, ((1u << 16) / nb) / TILE_ROWS * TILE_ROWS);
+    std::vector<uint8_t> c(chunk_rows * nb * 64), h(m.scheme == 3 ? chunk_rows * nb * 32 : 0);
+    std::vector<uint32_t> p(chunk_rows * nb);
+    for (uint64_t r0 = 0; r0 < m.rows; r0 += chunk_rows) {
+        const uint64_t n = std::min(chunk_rows, m.rows - r0);
+        const uint64_t ntile_rows = (n + TILE_ROWS - 1) / TILE_ROWS * TILE_ROWS;
+        std::fill(p.begin(), p.begin() + ntile_rows * nb, 0u);
+        transcode_rows(m.scheme, blocks + r0 * nb * bpb, 0, n, nb, c.data(), h.data(), p.data());
+        WPCG_HIP(hipMemcpyAsync(m.codes + r0 * nb * 64, c.data(), n * nb * 64, hipMemcpyHostToDevice, s));
+        WPCG_HIP(hipMemcpyAsync(m.params + r0 * nb, p.data(), ntile_rows * nb * 4, hipMemcpyHostToDevice, s));
+        if (m.hp)
+            WPCG_HIP(hipMemcpyAsync(m.hp + r0 * nb * 32, h.data(), n * nb * 32, hipMemcpyHostToDevice, s));
+        WPCG_HIP(hipStreamSynchronize(s));
     }
     return WPCG_OK;
+}
+
+// Workspace for FAST mode's split-K: partial sums and self-resetting
+// counters, fixed for the matrix's lifetime (captured graphs keep using it).
+int plan_kslices(uint64_t rows, uint64_t nb, int kg)
+{
+    const int kmin = (int)std::max<uint64_t>(1, (nb + FAST_MAXBK - 1) / FAST_MAXBK);
+    const int k = kg > 0 ? std::max(kmin, std::min(kg, (int)std::max<uint64_t>(1, nb)))
+                         : fast_kslices(rows, nb);
+    return fast_normalize_kslices(nb, k);
+}
+
+int make_plan(const DeviceMatrix& m, FastPlan& plan, hipStream_t s, int kg = 0)
+{
+    plan.kg = plan_kslices(m.rows, m.nb, kg);
+    if (plan.kg <= 1) return WPCG_OK;
+    const uint64_t tiles = m.rows_pad / TILE_ROWS;
+    const uint64_t tgroups = (tiles + FAST_TILES - 1) / FAST_TILES;
+    WPCG_HIP(hipMalloc(&plan.part, (uint64_t)plan.kg * m.rows_pad * sizeof(float)));
+    WPCG_HIP(hipMalloc(&plan.counters, std::max<uint64_t>(1, tgroups) * sizeof(uint32_t)));
+    WPCG_HIP(hipMemsetAsync(plan.counters, 0, std::max<uint64_t>(1, tgroups) * sizeof(uint32_t), s));
+    WPCG_HIP(hipStreamSynchronize(s));
+    return WPCG_OK;
+}
+
+hipError_t run_gemv(wpcg_linear* L, const float* x, float* y, hipStream_t s)
+{
+    // K = 0 has no blocks to stream: the EXACT kernel writes 0 (+ bias)
+    if (L->mode == WPCG_MODE_EXACT || L->m.nb == 0) return launch_gemv_exact(L->m, x, L->bias, y, s);
+    GemvJob job{&L->m, &L->plan, x, L->bias, y};
+    return launch_gemv_fast(&job, 1, s);
 }
 
 }  // namespace
@@ -138,11 +204,8 @@ int wpcg_ctx_destroy(wpcg_ctx* ctx)
 {
     if (!ctx) return WPCG_OK;
     (void)hipSetDevice(ctx->device);
-    if (ctx->stream) {
-        (void)hipStreamSynchronize(ctx->stream);
-        (void)hipStreamDestroy(ctx->stream);
-    }
-    delete ctx;
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    ctx_release(ctx);
     return WPCG_OK;
 }
 
@@ -200,6 +263,7 @@ int wpcg_event_create(wpcg_ctx* ctx, wpcg_event** out)
     if (!ev) return fail(WPCG_E_NOMEM, "event allocation");
     ev->ctx = ctx;
     WPCG_HIP(hipEventCreate(&ev->ev));
+    ctx_retain(ctx);
     *out = ev.release();
     return WPCG_OK;
 }
@@ -209,6 +273,7 @@ int wpcg_event_destroy(wpcg_event* ev)
     if (!ev) return WPCG_OK;
     (void)hipSetDevice(ev->ctx->device);
     (void)hipEventDestroy(ev->ev);
+    ctx_release(ev->ctx);
     delete ev;
     return WPCG_OK;
 }
@@ -332,20 +397,22 @@ int wpcg_linear_from_blocks(wpcg_ctx* ctx, int scheme, const void* blocks, uint6
     L->m.rows = out_f;
     L->m.cols = in_f;
     L->m.nb = in_f / 128;
-    if (int rc = upload_matrix(ctx, scheme, static_cast<const uint8_t*>(blocks), expected, L->m)) {
-        free_matrix(L->m);
-        return rc;
-    }
-    if (bias) {
+    L->m.rows_pad = pad_rows(out_f);
+    int rc = upload_matrix(ctx, static_cast<const uint8_t*>(blocks), L->m);
+    if (rc == WPCG_OK) rc = make_plan(L->m, L->plan, ctx->stream);
+    if (rc == WPCG_OK && bias) {
         hipError_t e = hipMalloc(&L->bias, (out_f ? out_f : 1) * sizeof(float));
         if (e == hipSuccess)
             e = hipMemcpy(L->bias, bias, out_f * sizeof(float), hipMemcpyHostToDevice);
-        if (e != hipSuccess) {
-            free_matrix(L->m);
-            if (L->bias) (void)hipFree(L->bias);
-            return hip_fail(e, "bias upload");
-        }
+        if (e != hipSuccess) rc = hip_fail(e, "bias upload");
     }
+    if (rc != WPCG_OK) {
+        free_matrix(L->m);
+        free_plan(L->plan);
+        if (L->bias) (void)hipFree(L->bias);
+        return rc;
+    }
+    ctx_retain(ctx);
     *out = L.release();
     return WPCG_OK;
 }
@@ -376,9 +443,11 @@ int wpcg_linear_destroy(wpcg_linear* L)
     (void)hipSetDevice(L->ctx->device);
     (void)hipStreamSynchronize(L->ctx->stream);
     free_matrix(L->m);
+    free_plan(L->plan);
     if (L->bias) (void)hipFree(L->bias);
     if (L->x_stage) (void)hipFree(L->x_stage);
     if (L->y_stage) (void)hipFree(L->y_stage);
+    ctx_release(L->ctx);
     delete L;
     return WPCG_OK;
 }
@@ -399,6 +468,37 @@ int wpcg_linear_set_mode(wpcg_linear* L, int mode)
     return WPCG_OK;
 }
 
+int wpcg_linear_set_kslices(wpcg_linear* L, int kslices)
+{
+    if (!L) return fail(WPCG_E_ARG, "null linear");
+    if (kslices < 0) return fail(WPCG_E_ARG, "kslices must be >= 0");
+    if (int rc = check_ctx(L->ctx)) return rc;
+    WPCG_HIP(hipStreamSynchronize(L->ctx->stream));
+    free_plan(L->plan);
+    if (int rc = make_plan(L->m, L->plan, L->ctx->stream, kslices)) {
+        free_plan(L->plan);
+        L->plan.kg = 1;
+        return rc;
+    }
+    return WPCG_OK;
+}
+
+int wpcg_linear_kslices(wpcg_linear* L, int* kslices)
+{
+    if (!L || !kslices) return fail(WPCG_E_ARG, "null argument");
+    *kslices = L->plan.kg;
+    return WPCG_OK;
+}
+
+int wpcg_plan_kslices(uint64_t out_f, uint64_t in_f, int requested, int* kslices)
+{
+    if (!kslices) return fail(WPCG_E_ARG, "null output");
+    if (in_f % 128 != 0) return fail(WPCG_E_SHAPE, "in_features must be a multiple of 128");
+    if (requested < 0) return fail(WPCG_E_ARG, "requested must be >= 0");
+    *kslices = plan_kslices(out_f, in_f / 128, requested);
+    return WPCG_OK;
+}
+
 int wpcg_linear_device_bytes(wpcg_linear* L, uint64_t* bytes)
 {
     if (!L || !bytes) return fail(WPCG_E_ARG, "null argument");
@@ -413,7 +513,46 @@ int wpcg_linear_matvec(wpcg_linear* L, const float* x, float* y, wpcg_stream str
     if (int rc = check_ctx(L->ctx)) return rc;
     if (L->m.rows == 0) return WPCG_OK;
     if (!y || (!x && L->m.cols)) return fail(WPCG_E_ARG, "null x or y");
-    WPCG_HIP(launch_gemv(L->m, L->mode, x, L->bias, y, pick(L->ctx, stream)));
+    WPCG_HIP(run_gemv(L, x, y, pick(L->ctx, stream)));
+    return WPCG_OK;
+}
+
+int wpcg_linear_matvec_multi(int n, wpcg_linear* const* lins, const float* const* xs,
+                             float* const* ys, wpcg_stream stream)
+{
+    if (n < 0 || (n > 0 && (!lins || !xs || !ys))) return fail(WPCG_E_ARG, "null argument");
+    if (n == 0) return WPCG_OK;
+    wpcg_ctx* ctx = nullptr;
+    for (int i = 0; i < n; i++) {
+        if (!lins[i]) return fail(WPCG_E_ARG, "null linear in group");
+        if (!ctx) ctx = lins[i]->ctx;
+        if (lins[i]->ctx->device != ctx->device)
+            return fail(WPCG_E_ARG, "linears of one group must share a device");
+        if (lins[i]->m.rows && (!ys[i] || (!xs[i] && lins[i]->m.cols)))
+            return fail(WPCG_E_ARG, "null x or y in group");
+    }
+    if (int rc = check_ctx(ctx)) return rc;
+    hipStream_t s = pick(ctx, stream);
+    // FAST members of one scheme share launches of up to MAX_JOBS; EXACT
+    // members run one launch each.
+    for (int scheme : {3, 4}) {
+        GemvJob jobs[MAX_JOBS];
+        int nj = 0;
+        for (int i = 0; i < n; i++) {
+            wpcg_linear* L = lins[i];
+            if (L->m.scheme != scheme || L->m.rows == 0) continue;
+            if (L->mode == WPCG_MODE_EXACT || L->m.nb == 0) {
+                WPCG_HIP(launch_gemv_exact(L->m, xs[i], L->bias, ys[i], s));
+                continue;
+            }
+            jobs[nj++] = GemvJob{&L->m, &L->plan, xs[i], L->bias, ys[i]};
+            if (nj == MAX_JOBS) {
+                WPCG_HIP(launch_gemv_fast(jobs, nj, s));
+                nj = 0;
+            }
+        }
+        if (nj) WPCG_HIP(launch_gemv_fast(jobs, nj, s));
+    }
     return WPCG_OK;
 }
 
@@ -429,7 +568,7 @@ int wpcg_linear_matvec_host(wpcg_linear* L, const float* x, float* y)
     hipStream_t s = L->ctx->stream;
     if (L->m.cols)
         WPCG_HIP(hipMemcpyAsync(L->x_stage, x, L->m.cols * sizeof(float), hipMemcpyHostToDevice, s));
-    WPCG_HIP(launch_gemv(L->m, L->mode, L->x_stage, L->bias, L->y_stage, s));
+    WPCG_HIP(run_gemv(L, L->x_stage, L->y_stage, s));
     WPCG_HIP(hipMemcpyAsync(y, L->y_stage, L->m.rows * sizeof(float), hipMemcpyDeviceToHost, s));
     WPCG_HIP(hipStreamSynchronize(s));
     return WPCG_OK;
@@ -476,8 +615,12 @@ int wpcg_linear_clone(wpcg_linear* L, wpcg_linear** out)
     c->m.codes = c->m.hp = nullptr;
     c->m.params = nullptr;
     c->mode = L->mode;
-    const uint64_t nb = std::max<uint64_t>(1, L->m.rows * L->m.nb);
+    const uint64_t nb = plane_blocks(L->m);
     hipStream_t s = L->ctx->stream;
+    if (int rc = make_plan(c->m, c->plan, s)) {
+        free_plan(c->plan);
+        return rc;
+    }
     auto dup = [&](void** dst, const void* src, size_t n) -> hipError_t {
         hipError_t e = hipMalloc(dst, n);
         if (e == hipSuccess) e = hipMemcpyAsync(*dst, src, n, hipMemcpyDeviceToDevice, s);
@@ -490,9 +633,11 @@ int wpcg_linear_clone(wpcg_linear* L, wpcg_linear** out)
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
         free_matrix(c->m);
+        free_plan(c->plan);
         if (c->bias) (void)hipFree(c->bias);
         return hip_fail(e, "clone");
     }
+    ctx_retain(c->ctx);
     *out = c.release();
     return WPCG_OK;
 }
@@ -518,6 +663,7 @@ int wpcg_graph_end(wpcg_ctx* ctx, wpcg_graph** out)
         (void)hipGraphDestroy(g->graph);
         return hip_fail(e, "hipGraphInstantiate");
     }
+    ctx_retain(ctx);
     *out = g.release();
     return WPCG_OK;
 }
@@ -536,6 +682,7 @@ int wpcg_graph_destroy(wpcg_graph* g)
     (void)hipSetDevice(g->ctx->device);
     if (g->exec) (void)hipGraphExecDestroy(g->exec);
     if (g->graph) (void)hipGraphDestroy(g->graph);
+    ctx_release(g->ctx);
     delete g;
     return WPCG_OK;
 }

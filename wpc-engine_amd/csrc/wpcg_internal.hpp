@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <atomic>
 #include <cstdint>
 #include <mutex>
 #include <string>
@@ -24,35 +25,78 @@ int hip_fail(hipError_t e, const char* what);
         if (e_ != hipSuccess) return ::wpcg::hip_fail(e_, #call);   \
     } while (0)
 
-// ---- device layouts -----------------------------------------------------
+// ---- device layout ------------------------------------------------------
 // Both schemes keep the reference's bytes per block (68 for v4, 100 for v3)
-// but split each block into planes that vector loads can reach:
-//   params[row][blk]   u32 = zero_point f16 | scale f16 << 16
-//   codes[row][blk][64]  the 64 nibble-pair bytes, stored "lane-major":
-//                      dev[l*8 + g] = ref[g*8 + l]   (l, g < 8)
-//                      so the eight bytes that AVX2 lane l of the reference
-//                      kernel consumes are one contiguous 8-byte word.
-//   hp[row][blk][32]   (v3 only) the two-plane high bits, also lane-major:
-//                      dev[l*4 + m] = hp[m*8 + l]    (l < 8, m < 4)
+// but split each block into planes that vector loads can reach. Rows are
+// padded to a multiple of 16 (one matrix-core tile); padding is zero.
+//
+//   codes[row][blk][64]  the 64 nibble-pair bytes of the reference block in
+//                        "paired-lane" order: the eight bytes that AVX2 lane
+//                        L of the reference kernel reads (ref bytes g*8+L,
+//                        g < 8) sit at dev[(L&3)*16 + (L>>2)*8 + g], so
+//                        lane L alone is one 8-byte word and lanes L, L+4
+//                        together are one 16-byte word.
+//   hp[row][blk][32]     (v3) the two-plane high bits, same pairing:
+//                        dev[(L&3)*8 + (L>>2)*4 + m] = hp[m*8 + L]  (m < 4)
+//   params[row/16][blk][row%16]  u32 zero_point f16 | scale f16 << 16,
+//                        16-row tile-major so one 16-byte load returns the
+//                        parameters of four consecutive rows.
+constexpr int TILE_ROWS = 16;
+
+inline uint64_t pad_rows(uint64_t rows) { return (rows + TILE_ROWS - 1) / TILE_ROWS * TILE_ROWS; }
+
+inline uint64_t code_off(int L, int g) { return (uint64_t)((L & 3) * 16 + (L >> 2) * 8 + g); }
+inline uint64_t hp_off(int L, int m) { return (uint64_t)((L & 3) * 8 + (L >> 2) * 4 + m); }
+
 struct DeviceMatrix {
     int scheme = 0;
     uint64_t rows = 0, cols = 0, nb = 0;  // nb = cols / 128 blocks per row
+    uint64_t rows_pad = 0;
     uint8_t* codes = nullptr;
     uint8_t* hp = nullptr;
     uint32_t* params = nullptr;
 };
 
+// Split of a FAST-mode GEMV over workgroups, fixed at creation so captured
+// graphs keep valid workspace pointers.
+struct FastPlan {
+    int kg = 1;               // K-slices across workgroups
+    float* part = nullptr;    // [kg][rows_pad] partial sums (kg > 1)
+    uint32_t* counters = nullptr;  // one per tile group, self-resetting
+};
+
 // Host transcodes from the reference's on-disk blocks (AoS) to the planes
-// above. `threads` splits rows across std::threads.
-void transcode_v4(const uint8_t* blocks, uint64_t n_blocks, uint8_t* codes, uint32_t* params);
-void transcode_v3(const uint8_t* blocks, uint64_t n_blocks, uint8_t* lp, uint8_t* hp,
-                  uint32_t* params);
+// above, for rows [r0, r0 + nrows) of a matrix with nb blocks per row.
+// `codes`/`hp` point at row r0; `params` at the matrix's parameter base.
+void transcode_rows(int scheme, const uint8_t* blocks, uint64_t r0, uint64_t nrows, uint64_t nb,
+                    uint8_t* codes, uint8_t* hp, uint32_t* params_tile_major);
 
 // ---- kernel launchers (gemv.hip) ----------------------------------------
-hipError_t launch_gemv(const DeviceMatrix& m, int mode, const float* x, const float* bias,
-                       float* y, hipStream_t s);
+struct GemvJob {
+    const DeviceMatrix* m;
+    const FastPlan* plan;
+    const float* x;
+    const float* bias;
+    float* y;
+};
+constexpr int FAST_TILES = 2;  // 16-row tiles per FAST workgroup
+constexpr int FAST_MAXBK = 32; // blocks per FAST K-slice (the slice's x digits live in LDS)
+hipError_t launch_gemv_exact(const DeviceMatrix& m, const float* x, const float* bias, float* y,
+                             hipStream_t s);
+// All jobs must share the scheme. At most MAX_JOBS per launch.
+constexpr int MAX_JOBS = 8;
+hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s);
 hipError_t launch_embed(const DeviceMatrix& m, uint32_t row, float* out, hipStream_t s);
 hipError_t launch_dequant(const DeviceMatrix& m, int rounding, float* w, hipStream_t s);
+int fast_kslices(uint64_t rows, uint64_t nb);
+// Slices of nbk = ceil(nb/kg) blocks; returns the number of non-empty
+// slices, ceil(nb/nbk), so that every slice starts inside the row.
+inline int fast_normalize_kslices(uint64_t nb, int kg)
+{
+    if (nb == 0 || kg <= 1) return 1;
+    const uint64_t nbk = (nb + kg - 1) / kg;
+    return (int)((nb + nbk - 1) / nbk);
+}
 
 // ---- minimal JSON (for model_v{3,4}.meta) ---------------------------------
 struct MetaEntry {
@@ -67,10 +111,19 @@ int parse_meta(const std::string& text, std::unordered_map<std::string, MetaEntr
 }  // namespace wpcg
 
 // ---- handle definitions ----------------------------------------------------
+// A context lives until wpcg_ctx_destroy has been called AND every handle
+// created on it (linears, events, graphs) has been destroyed: each holds a
+// reference, so handles may be released in any order.
 struct wpcg_ctx {
     int device = 0;
     hipStream_t stream = nullptr;
+    std::atomic<int> refs{1};
 };
+
+namespace wpcg {
+void ctx_retain(wpcg_ctx* c);
+void ctx_release(wpcg_ctx* c);
+}  // namespace wpcg
 
 struct wpcg_artifact {
     int scheme = 0;
@@ -82,6 +135,7 @@ struct wpcg_artifact {
 struct wpcg_linear {
     wpcg_ctx* ctx = nullptr;
     wpcg::DeviceMatrix m;
+    wpcg::FastPlan plan;
     float* bias = nullptr;  // device, out_f floats, or null
     int mode = WPCG_MODE_EXACT;
     // staging for the synchronous *_host twins

@@ -78,6 +78,9 @@ _SIGS = {
     "wpcg_linear_destroy": (C.c_int, [_p]),
     "wpcg_linear_shape": (C.c_int, [_p, _u64p, _u64p]),
     "wpcg_linear_set_mode": (C.c_int, [_p, C.c_int]),
+    "wpcg_linear_set_kslices": (C.c_int, [_p, C.c_int]),
+    "wpcg_linear_kslices": (C.c_int, [_p, C.POINTER(C.c_int)]),
+    "wpcg_plan_kslices": (C.c_int, [_u64, _u64, C.c_int, C.POINTER(C.c_int)]),
     "wpcg_linear_device_bytes": (C.c_int, [_p, _u64p]),
     "wpcg_linear_matvec": (C.c_int, [_p, _p, _p, _p]),
     "wpcg_linear_matvec_host": (C.c_int, [_p, _p, _p]),
@@ -85,6 +88,7 @@ _SIGS = {
     "wpcg_linear_embed_host": (C.c_int, [_p, C.c_uint32, _p]),
     "wpcg_linear_dequant": (C.c_int, [_p, C.c_int, _p, _p]),
     "wpcg_linear_clone": (C.c_int, [_p, _pp]),
+    "wpcg_linear_matvec_multi": (C.c_int, [C.c_int, _pp, _pp, _pp, _p]),
     "wpcg_graph_begin": (C.c_int, [_p]),
     "wpcg_graph_end": (C.c_int, [_p, _pp]),
     "wpcg_graph_launch": (C.c_int, [_p, _p]),
@@ -116,6 +120,20 @@ def _np_ptr(a: np.ndarray):
     return a.ctypes.data_as(C.c_void_p)
 
 
+def matvec_multi(lins, xs, ys, stream=None):
+    """ys[i] = lins[i] @ xs[i] for device buffers, grouped into shared launches."""
+    n = len(lins)
+    arr = (C.c_void_p * n)
+    check(lib.wpcg_linear_matvec_multi(n, arr(*[l.h for l in lins]), arr(*[x.ptr for x in xs]),
+                                       arr(*[y.ptr for y in ys]), stream))
+
+
+def plan_kslices(out_f: int, in_f: int, requested: int = 0) -> int:
+    k = C.c_int()
+    check(lib.wpcg_plan_kslices(out_f, in_f, requested, C.byref(k)))
+    return k.value
+
+
 def device_count() -> int:
     n = C.c_int(0)
     rc = lib.wpcg_device_count(C.byref(n))
@@ -137,6 +155,8 @@ def gpu_used() -> bool:
 
 def hard_exit(code: int = 0):
     for ctx in list(_live):
+        if not ctx.h:
+            continue
         try:
             ctx.sync()
             ctx.close()
@@ -355,6 +375,15 @@ class WpcLinear:
     def set_mode(self, mode: int):
         check(lib.wpcg_linear_set_mode(self.h, mode))
         return self
+
+    def set_kslices(self, k: int):
+        check(lib.wpcg_linear_set_kslices(self.h, k))
+        return self
+
+    def kslices(self) -> int:
+        k = C.c_int()
+        check(lib.wpcg_linear_kslices(self.h, C.byref(k)))
+        return k.value
 
     def device_bytes(self) -> int:
         n = C.c_uint64()
