@@ -164,15 +164,18 @@ def test_synth_v3_packing_matches_the_oracle_codec():
 def test_fast_split_plan_never_makes_an_empty_slice():
     # FAST mode splits each row's nb blocks into slices of ceil(nb/k) blocks;
     # every slice must start inside the row (an empty trailing slice would
-    # address blocks past the end of the matrix) and fit the 32-block LDS
-    # stage. Checked for every block count and requested split.
+    # address blocks past the end of the matrix) and fit the LDS stage: 64
+    # blocks with one 16-row tile per workgroup, 32 with two (matrices of
+    # 512 tiles or more). Checked for every block count and requested split.
     for nb in range(1, 161):
         for req in [0] + list(range(1, nb + 3)):
-            for rows in (16, 1024, 9728):
+            for rows, most in ((16, 64), (1024, 64), (8176, 64), (8177, 32), (9728, 32)):
                 k = wpcg.plan_kslices(rows, nb * 128, req)
                 nbk = -(-nb // k)
-                assert 1 <= k <= nb and nbk <= 32, (nb, req, k)
+                assert 1 <= k <= nb and nbk <= most, (nb, req, rows, k)
                 assert (k - 1) * nbk < nb <= k * nbk, (nb, req, k, nbk)
+                if req == 0:  # the default is the fewest slices that fit
+                    assert k == -(-nb // most), (nb, rows, k)
     with pytest.raises(wpcg.WpcgError) as e:
         wpcg.plan_kslices(4, 100)
     assert e.value.code == wpcg.E_SHAPE

@@ -89,6 +89,8 @@ SHAPES = [
     (3, 9728, 2560),
     (3, 2560, 9728),
     (3, 37, 640),
+    (4, 8200, 640),    # two tiles per workgroup, odd tile count (513)
+    (3, 8195, 8320),   # two tiles per workgroup, 65 blocks: two K-slices
 ]
 
 

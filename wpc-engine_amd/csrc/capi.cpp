@@ -111,11 +111,16 @@ int upload_matrix(wpcg_ctx* ctx, const uint8_t* blocks, DeviceMatrix& m)
         const uint64_t n = std::min(chunk_rows, m.rows - r0);
         const uint64_t ntile_rows = (n + TILE_ROWS - 1) / TILE_ROWS * TILE_ROWS;
         std::fill(p.begin(), p.begin() + ntile_rows * nb, 0u);
+        if (n != ntile_rows) {  // padding rows of a ragged last tile
+            std::fill(c.begin(), c.begin() + ntile_rows * nb * 64, 0);
+            std::fill(h.begin(), h.end(), 0);
+        }
+        // planes are tile-major, so whole tiles of rows are contiguous
         transcode_rows(m.scheme, blocks + r0 * nb * bpb, 0, n, nb, c.data(), h.data(), p.data());
-        WPCG_HIP(hipMemcpyAsync(m.codes + r0 * nb * 64, c.data(), n * nb * 64, hipMemcpyHostToDevice, s));
+        WPCG_HIP(hipMemcpyAsync(m.codes + r0 * nb * 64, c.data(), ntile_rows * nb * 64, hipMemcpyHostToDevice, s));
         WPCG_HIP(hipMemcpyAsync(m.params + r0 * nb, p.data(), ntile_rows * nb * 4, hipMemcpyHostToDevice, s));
         if (m.hp)
-            WPCG_HIP(hipMemcpyAsync(m.hp + r0 * nb * 32, h.data(), n * nb * 32, hipMemcpyHostToDevice, s));
+            WPCG_HIP(hipMemcpyAsync(m.hp + r0 * nb * 32, h.data(), ntile_rows * nb * 32, hipMemcpyHostToDevice, s));
         WPCG_HIP(hipStreamSynchronize(s));
     }
     return WPCG_OK;
@@ -125,7 +130,8 @@ int upload_matrix(wpcg_ctx* ctx, const uint8_t* blocks, DeviceMatrix& m)
 // counters, fixed for the matrix's lifetime (captured graphs keep using it).
 int plan_kslices(uint64_t rows, uint64_t nb, int kg)
 {
-    const int kmin = (int)std::max<uint64_t>(1, (nb + FAST_MAXBK - 1) / FAST_MAXBK);
+    const uint64_t mb = fast_max_slice(rows);
+    const int kmin = (int)std::max<uint64_t>(1, (nb + mb - 1) / mb);
     const int k = kg > 0 ? std::max(kmin, std::min(kg, (int)std::max<uint64_t>(1, nb)))
                          : fast_kslices(rows, nb);
     return fast_normalize_kslices(nb, k);
@@ -135,11 +141,10 @@ int make_plan(const DeviceMatrix& m, FastPlan& plan, hipStream_t s, int kg = 0)
 {
     plan.kg = plan_kslices(m.rows, m.nb, kg);
     if (plan.kg <= 1) return WPCG_OK;
-    const uint64_t tiles = m.rows_pad / TILE_ROWS;
-    const uint64_t tgroups = (tiles + FAST_TILES - 1) / FAST_TILES;
+    const uint64_t tiles = std::max<uint64_t>(1, m.rows_pad / TILE_ROWS);
     WPCG_HIP(hipMalloc(&plan.part, (uint64_t)plan.kg * m.rows_pad * sizeof(float)));
-    WPCG_HIP(hipMalloc(&plan.counters, std::max<uint64_t>(1, tgroups) * sizeof(uint32_t)));
-    WPCG_HIP(hipMemsetAsync(plan.counters, 0, std::max<uint64_t>(1, tgroups) * sizeof(uint32_t), s));
+    WPCG_HIP(hipMalloc(&plan.counters, tiles * sizeof(uint32_t)));
+    WPCG_HIP(hipMemsetAsync(plan.counters, 0, tiles * sizeof(uint32_t), s));
     WPCG_HIP(hipStreamSynchronize(s));
     return WPCG_OK;
 }
@@ -617,7 +622,7 @@ int wpcg_linear_clone(wpcg_linear* L, wpcg_linear** out)
     c->mode = L->mode;
     const uint64_t nb = plane_blocks(L->m);
     hipStream_t s = L->ctx->stream;
-    if (int rc = make_plan(c->m, c->plan, s)) {
+    if (int rc = make_plan(c->m, c->plan, s, L->plan.kg)) {  // same split: same results
         free_plan(c->plan);
         return rc;
     }

@@ -1,6 +1,7 @@
 // Dequant-GEMV kernels for gfx950 (CDNA4, wave64) over WPC blocks of 128
 // weights (v4: 4-bit codes, v3: 6-bit codes in two planes). Device layout:
-// see wpcg_internal.hpp (paired-lane code bytes, 16-row tile-major params).
+// see wpcg_internal.hpp (per 16-row tile and block, one contiguous record of
+// code bytes in paired-lane order, one of high bits, one of parameters).
 //
 // EXACT mode reproduces the reference's AVX2 row kernels bit for bit:
 //   matvec_v4_fused (wpc-eval/src/fused_kernel.rs:237-271)
@@ -14,8 +15,8 @@
 // FAST mode puts the dot products on the matrix cores. Codes are exact int8
 // (0..15 or 0..63). Each 128-value block b of x is written as
 //   x ~= s_b * Q / 2^21,  s_b = max|x_b| / 127,  Q = rint(x * 127*2^21 / max|x_b|)
-// and Q = d0*2^21 + d1*2^14 + d2*2^7 + d3 with int8 digits d0 in [-127,127],
-// d1..d3 in [-64,64]. v_mfma_i32_16x16x64_i8 then gives the exact integer
+// and Q = d0*2^21 + d1*2^14 + d2*2^7 + d3 with int8 digits d0 = Q >> 21 in
+// [-128,127], d1..d3 in [0,127]. v_mfma_i32_16x16x64_i8 then gives the exact integer
 // dots D_j = sum(code * d_j) for the four digit columns of a 16-row tile,
 // and each block adds
 //   scale * s_b * (D0 + D1*2^-7 + D2*2^-14 + D3*2^-21) + zp * sum(x_b)
@@ -34,8 +35,10 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ int dcode_off(int L, int g) { return (L & 3) * 16 + (L >> 2) * 8 + g; }
-__device__ __forceinline__ int dhp_off(int L, int m) { return (L & 3) * 8 + (L >> 2) * 4 + m; }
+// Byte of row r (of its tile) that AVX2 lane L reads first, within a block's
+// code record (1 KiB) or high-plane record (512 B).
+__device__ __forceinline__ int dcode_pos(int r, int L) { return ((L & 3) * 16 + r) * 16 + (L >> 2) * 8; }
+__device__ __forceinline__ int dhp_pos(int r, int L) { return ((L & 3) * 16 + r) * 8 + (L >> 2) * 4; }
 __device__ __forceinline__ size_t param_idx(size_t row, size_t nb, size_t blk)
 {
     return ((row / TILE_ROWS) * nb + blk) * TILE_ROWS + row % TILE_ROWS;
@@ -126,7 +129,7 @@ __global__ __launch_bounds__(EX_WG) void k_gemv_exact(const uint8_t* __restrict_
     const int L = threadIdx.x & 7;
     const int row = blockIdx.x * (EX_WG / 8) + (threadIdx.x >> 3);
     const bool active = row < rows;
-    const size_t rb = (size_t)row * (size_t)nb;  // rows are padded: in range
+    const size_t tb = (size_t)blockIdx.x * (size_t)nb;  // this tile's first block record
     const uint32_t* pp = params + (size_t)blockIdx.x * nb * TILE_ROWS + (row & (TILE_ROWS - 1));
     float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += EX_SEG) {
@@ -134,20 +137,21 @@ __global__ __launch_bounds__(EX_WG) void k_gemv_exact(const uint8_t* __restrict_
         __syncthreads();
         stage_x(xs, x, b0, nbs);
         __syncthreads();
-        const uint8_t* cp = codes + (rb + b0) * 64 + dcode_off(L, 0);
+        // per block, the workgroup reads one contiguous 1 KiB code record
+        const uint8_t* cp = codes + (tb + b0) * CODE_REC + dcode_pos(threadIdx.x >> 3, L);
         const float* xl = xs + L * XS_LANE;
         if constexpr (SCHEME == 4) {
 #pragma unroll 4
             for (int s = 0; s < nbs; s++) {
-                const uint2 c = *reinterpret_cast<const uint2*>(cp + (size_t)s * 64);
+                const uint2 c = *reinterpret_cast<const uint2*>(cp + (size_t)s * CODE_REC);
                 acc = v4_exact_block(c, pp[(size_t)(b0 + s) * TILE_ROWS], xl + s * XS_BLK, acc);
             }
         } else {
-            const uint8_t* hq = hp + (rb + b0) * 32 + dhp_off(L, 0);
+            const uint8_t* hq = hp + (tb + b0) * HP_REC + dhp_pos(threadIdx.x >> 3, L);
 #pragma unroll 4
             for (int s = 0; s < nbs; s++) {
-                const uint2 c = *reinterpret_cast<const uint2*>(cp + (size_t)s * 64);
-                const uint32_t h = *reinterpret_cast<const uint32_t*>(hq + (size_t)s * 32);
+                const uint2 c = *reinterpret_cast<const uint2*>(cp + (size_t)s * CODE_REC);
+                const uint32_t h = *reinterpret_cast<const uint32_t*>(hq + (size_t)s * HP_REC);
                 acc = v3_exact_block(c, h, pp[(size_t)(b0 + s) * TILE_ROWS], xl + s * XS_BLK, acc);
             }
         }
@@ -162,6 +166,14 @@ __global__ __launch_bounds__(EX_WG) void k_gemv_exact(const uint8_t* __restrict_
 }
 
 // ============================================================ FAST mode
+// Buffer resource over [base, base + bytes): raw buffer loads at offsets
+// past `bytes` return zeros and access no memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+constexpr int CPOL_NT = 2;  // non-temporal: streamed weights are read once
+
 struct FastProblem {
     const uint8_t* codes;
     const uint8_t* hp;
@@ -171,18 +183,20 @@ struct FastProblem {
     const float* bias;
     float* part;
     uint32_t* counters;
-    int rows, rows_pad, nb, kg, wg_begin, pad_;
+    int rows, rows_pad, nb, kg, wg_begin, tw;  // tw: 16-row tiles per workgroup
 };
 struct FastBatch {
     FastProblem p[MAX_JOBS];
     int n;
 };
 
-constexpr int FAST_WG = 256;  // 4 waves: FAST_TILES tiles x KS K-interleaved waves
-constexpr int MAXBK = FAST_MAXBK;  // blocks per K-slice (LDS digits: 16 KiB)
-constexpr int NDIG = 4;       // int8 digits per x value
-constexpr int HALF = 4 * NDIG * 16;  // fragment bytes per MFMA half: 4 groups x digits x 16
-constexpr int FRAG = 2 * HALF;       // per block
+constexpr int FAST_WG = 512;        // 8 waves
+constexpr int QB = 8;               // most blocks one wave puts through the matrix cores
+constexpr int NDIG = 4;             // int8 digits per x value
+constexpr int HALF = 4 * NDIG * 16; // fragment bytes per MFMA half: 4 groups x digits x 16
+constexpr int FRAG = 2 * HALF;      // per block
+constexpr int MAXBK = FAST_MAXBK;   // most blocks of one K-slice (one tile per workgroup)
+static_assert(MAXBK == QB * 8, "slice = 8 waves x QB blocks");
 
 // Byte position of digit 0 of x index k (0..127) in a block's fragment area.
 // MFMA half h = k>>6 covers 64 k; lane group g = k&3; byte (k>>3)&7 + 8*((k>>2)&1).
@@ -195,188 +209,229 @@ __device__ __forceinline__ int frag_pos(int k)
 }
 
 // Q = d0*2^21 + d1*2^14 + d2*2^7 + d3 with |Q| <= 127*2^21 (+ rounding):
-// d0 = floor((Q + 2^20) / 2^21) in [-127, 127], the rest in [-64, 64].
-__device__ __forceinline__ void put_digits(int8_t* blk, int k, float v, float inv)
+// d0 = Q >> 21 (arithmetic) in [-128, 127] and d1, d2, d3 the three 7-bit
+// fields of Q mod 2^21, in [0, 127]. `pos` is frag_pos(k).
+__device__ __forceinline__ void put_digits(int8_t* blk, int pos, float v, float inv)
 {
     const int Q = (int)rintf(v * inv);
-    const int d0 = (Q + (1 << 20)) >> 21;
-    const int r1 = Q - (d0 << 21);
-    const int d1 = (r1 + (1 << 13)) >> 14;
-    const int r2 = r1 - (d1 << 14);
-    const int d2 = (r2 + 64) >> 7;
-    const int d3 = r2 - (d2 << 7);
-    int8_t* p = blk + frag_pos(k);
-    p[0] = (int8_t)d0;
-    p[16] = (int8_t)d1;
-    p[32] = (int8_t)d2;
-    p[48] = (int8_t)d3;
+    int8_t* p = blk + pos;
+    p[0] = (int8_t)(Q >> 21);
+    p[16] = (int8_t)((Q >> 14) & 127);
+    p[32] = (int8_t)((Q >> 7) & 127);
+    p[48] = (int8_t)(Q & 127);
+}
+
+// DPP lane exchange inside rows of 16 lanes (full row and bank masks).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int DPP_XOR1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int DPP_HALF_MIRROR = 0x141; // lane i <-> 7-i within each 8
+constexpr int DPP_MIRROR = 0x140;      // lane i <-> 15-i within each 16
+
+// Sum over the 8 lanes of each half-row; every lane of the 8 ends with the
+// same value (each step adds a lane and its partner, which commute).
+__device__ __forceinline__ float sum8(float v)
+{
+    v += dpp<DPP_XOR1>(v);
+    v += dpp<DPP_XOR2>(v);
+    return v + dpp<DPP_HALF_MIRROR>(v);
+}
+
+__device__ __forceinline__ float lane_of(float v, int l)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
 // One row of the block epilogue, branch-free: the digit dot d (lanes of
-// columns 0..3) scaled by scale*s_b, and the zero-point term zp*sum(x_b)
-// (kept by every lane, used from column 4).
+// columns 0..3) times scale*s_b, and the zero-point term zp*sum(x_b) (kept
+// by every lane, used from column 4). `p` is zp f16 | scale f16 << 16.
 __device__ __forceinline__ void fast_step(float& acc, float& zacc, int d, uint32_t p, float sb, float Sb)
 {
-    acc = __builtin_fmaf((float)d, h2f(p >> 16) * sb, acc);
+    acc = __builtin_fmaf((float)d * sb, h2f(p >> 16), acc);
     zacc = __builtin_fmaf(h2f(p & 0xFFFFu), Sb, zacc);
 }
 
+// A workgroup of 8 waves computes tw (1 or 2) 16-row tiles over one K-slice
+// of nbl <= 8*QB/tw blocks.
+//   prep:  the slice's x becomes int8 digit fragments in LDS, shared by all
+//          waves; a wave takes two blocks at a time (32 lanes, 4 values each).
+//   dots:  wave w works on tile w / kw (kw = 8/tw waves per tile) over the
+//          contiguous kq-th part of the slice (kq = w % kw), in branch-free
+//          groups of four blocks: a block past the part's end reads zeros
+//          everywhere and adds exactly 0, and the groups' LDS reads, MFMAs
+//          and scaling overlap.
+//   sum:   the kw parts of a tile are added in part order (deterministic).
 template <int SCHEME>
 __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
 {
-    constexpr int KS = 4 / FAST_TILES;
-    __shared__ __align__(16) int8_t xq[MAXBK * FRAG];
-    __shared__ float xsc[MAXBK], xsum[MAXBK];
-    __shared__ float red[4][TILE_ROWS];
-    __shared__ __align__(16) uint32_t spar[FAST_TILES * MAXBK * TILE_ROWS];
+    // A wave's last group of four may reach up to 2 blocks past the slice:
+    // those blocks' codes are zero, their digits are never written (any
+    // int8 is harmless) and their scales are zeroed below (a stale NaN is not).
+    __shared__ __align__(16) int8_t xq[(MAXBK + 4) * FRAG];     // digits of the slice
+    __shared__ __align__(8) float2 xs[MAXBK + 4];              // {s_b, sum(x_b)}
+    __shared__ __align__(16) uint32_t spar[8][QB * TILE_ROWS]; // parameters, per wave
+    __shared__ float red[8][TILE_ROWS];
     __shared__ int s_last;
-    static_assert(FAST_TILES * MAXBK * 4 == FAST_WG, "one parameter chunk per thread");
 
     const int wgid = blockIdx.x;
+    // The problem this workgroup belongs to: the problems' first workgroups
+    // are read together, then the problem itself is read through the
+    // kernel-argument segment (indexing the by-value argument with a
+    // variable would copy it to scratch memory).
     int pi = 0;
 #pragma unroll
-    for (int i = 1; i < MAX_JOBS; i++)
-        if (i < B.n && wgid >= B.p[i].wg_begin) pi = i;
-    const FastProblem& P = B.p[pi];
-    const int nb = P.nb, kg = P.kg;
+    for (int i = 1; i < MAX_JOBS; i++) pi += (i < B.n && wgid >= B.p[i].wg_begin) ? 1 : 0;
+    typedef const __attribute__((address_space(4))) FastBatch* KargPtr;
+    const KargPtr kargs = (KargPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    const auto& P = kargs->p[pi];
+    const int nb = P.nb, kg = P.kg, tw = P.tw;
     const int local = wgid - P.wg_begin;
-    const int kgi = local % kg, tg = local / kg;
+    const int kgi = local % kg, tg = local / kg;  // K-slice, tile group
     const int nbk = (nb + kg - 1) / kg;
     const int b0 = kgi * nbk;
     const int nbl = max(0, min(nb, b0 + nbk) - b0);
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int ti = wave / KS, kw = wave % KS;  // this wave's tile and K interleave
-    const int T = tg * FAST_TILES + ti;
     const int ntiles = P.rows_pad / TILE_ROWS;
-    const int r = lane & 15, g = lane >> 4, j = lane & 15;
-    // An empty slice (possible only for a caller-side split; the host never
-    // makes one) still issues the clamped prologue loads: keep them in range.
-    const int bb = min(b0, nb - 1);
-    const int last = max(nbl - 1, 0);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int kw = 8 / tw;                           // waves per tile
+    const int T = tg * tw + wave / kw, kq = wave % kw;
+    const int q = (nbl + kw - 1) / kw;               // blocks per part (<= QB)
+    const int qw = T < ntiles ? max(0, min(q, nbl - kq * q)) : 0;  // this wave's blocks
+    const int wb = b0 + kq * q;                      // its first block
+    const int g = lane >> 4, j = lane & 15;
 
-    // Prologue. Vector-memory loads complete in issue order, so they go out
-    // as: x (for the digit prep; L2-resident), block parameters (to LDS),
-    // then this wave's first PF blocks of weights (HBM). The prep waits only
-    // for the first two while the weights are still in flight. All loads are
-    // unconditional with clamped indices (a clamped duplicate is not used),
-    // which keeps the compiler's wait counts exact.
-    constexpr int XB = MAXBK / 4;  // prep blocks per wave
-    float xv0[XB], xv1[XB];
+    // Loads, all issued before any use: x (L2-resident), then parameters,
+    // then weights (HBM): one memory round trip. Each is a buffer load over
+    // exactly the bytes it may touch, so a load past the end returns zeros
+    // without a memory access and every load can be unconditional.
+    // x pair p = wave + 8*i: blocks 2p, 2p+1; lane l holds x[4(l&31) .. +3]
+    // of block 2p + (l>>5).
+    constexpr int XP = MAXBK / 16;  // pairs per wave
+    const auto xrs = buf_rsrc(P.x + (size_t)b0 * 128, nbl * 512);
+    u32x4 xv[XP];
 #pragma unroll
-    for (int k = 0; k < XB; k++) {
-        const float* xb = P.x + (size_t)(bb + min(wave + 4 * k, last)) * 128;
-        xv0[k] = xb[lane];
-        xv1[k] = xb[lane + 64];
-    }
-    __builtin_amdgcn_sched_barrier(0);  // keep the issue order described above
-    // parameters of the workgroup's tiles: chunk (tt, bl, q) of 16 bytes
-    // holds rows 4q..4q+3 of tile tt, block bl
-    const int pchunk = threadIdx.x;  // FAST_TILES * MAXBK * 4 == FAST_WG
-    const int pq = pchunk & 3, pbl = (pchunk >> 2) % MAXBK, ptt = (pchunk >> 2) / MAXBK;
-    const uint4 pv = *reinterpret_cast<const uint4*>(
-        P.params + ((size_t)min(tg * FAST_TILES + ptt, ntiles - 1) * nb + bb + min(pbl, last)) *
-                       TILE_ROWS + 4 * pq);
+    for (int i = 0; i < XP; i++)
+        xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
+    const size_t rec = (size_t)min(T, ntiles - 1) * nb + wb;
+    // lane l: rows 4(l&3)..+3 of block l>>2 (blocks past QB are not kept)
+    const auto prs = buf_rsrc(P.params + rec * TILE_ROWS, qw * 64);
+    const u32x4 pv = __builtin_amdgcn_raw_buffer_load_b128(prs, lane * 16, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    const size_t row = (size_t)min(T, ntiles - 1) * TILE_ROWS + r;
-    const uint8_t* cp = P.codes + (row * nb + bb) * 64 + g * 16;
-    const uint8_t* hq = P.hp + (row * nb + bb) * 32 + g * 8;
-    constexpr int PF = 8;  // blocks of weights in flight per wave
-    u32x4 c[PF];
-    u32x2 h[PF];
+    const auto crs = buf_rsrc(P.codes + rec * CODE_REC, qw * (int)CODE_REC);
+    const auto hrs = buf_rsrc((SCHEME == 3 ? P.hp : P.codes) + rec * HP_REC, SCHEME == 3 ? qw * (int)HP_REC : 0);
+    u32x4 c[QB];
+    u32x2 h[QB];
 #pragma unroll
-    for (int i = 0; i < PF; i++) {
-        const int bl = min(kw + KS * i, last);
-        c[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(cp + (size_t)bl * 64));
+    for (int i = 0; i < QB; i++) {
+        c[i] = __builtin_amdgcn_raw_buffer_load_b128(crs, i * (int)CODE_REC + lane * 16, 0, CPOL_NT);
         if constexpr (SCHEME == 3)
-            h[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(hq + (size_t)bl * 32));
+            h[i] = __builtin_amdgcn_raw_buffer_load_b64(hrs, i * (int)HP_REC + lane * 8, 0, CPOL_NT);
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- x -> int8 digit fragments for blocks [b0, b0+nbl), one wave per block
+    // ---- x -> int8 digits. x ~= s_b * Q / 2^21 with s_b = M/127; the scale
+    // and its inverse need only agree to fp32 rounding, so both come from one
+    // reciprocal.
+    {
+        const int hi = lane >> 5, k0 = 4 * (lane & 31);
+        const int pos0 = frag_pos(k0), pos1 = frag_pos(k0 + 1), pos2 = frag_pos(k0 + 2), pos3 = frag_pos(k0 + 3);
 #pragma unroll
-    for (int k = 0; k < XB; k++) {
-        const int bl = wave + 4 * k;
-        if (bl >= nbl) break;
-        const float v0 = xv0[k], v1 = xv1[k];
-        float m = fmaxf(fabsf(v0), fabsf(v1));
-        float s = v0 + v1;
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            m = fmaxf(m, __shfl_xor(m, o));
-            s += __shfl_xor(s, o);
-        }
-        const float inv = m > 0.0f ? (127.0f * 2097152.0f) / m : 0.0f;
-        int8_t* dst = xq + bl * FRAG;
-        put_digits(dst, lane, v0, inv);
-        put_digits(dst, lane + 64, v1, inv);
-        if (lane == 0) {
-            xsc[bl] = m / 127.0f;
-            xsum[bl] = s;
+        for (int i = 0; i < XP; i++) {
+            const int p = wave + 8 * i;
+            if (2 * p < nbl) {
+                const float v0 = __uint_as_float(xv[i].x), v1 = __uint_as_float(xv[i].y);
+                const float v2 = __uint_as_float(xv[i].z), v3 = __uint_as_float(xv[i].w);
+                float m = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+                float s = (v0 + v1) + (v2 + v3);
+                m = fmaxf(m, dpp<DPP_XOR1>(m));
+                m = fmaxf(m, dpp<DPP_XOR2>(m));
+                m = fmaxf(m, dpp<DPP_HALF_MIRROR>(m));
+                m = fmaxf(m, dpp<DPP_MIRROR>(m));
+                s = sum8(s);
+                s += dpp<DPP_MIRROR>(s);
+                // rows of 16 -> the two blocks (lanes 0..31 and 32..63)
+                const float Ma = fmaxf(lane_of(m, 0), lane_of(m, 16));
+                const float Mb = fmaxf(lane_of(m, 32), lane_of(m, 48));
+                const float Sa = lane_of(s, 0) + lane_of(s, 16);
+                const float Sb = lane_of(s, 32) + lane_of(s, 48);
+                const float M = hi ? Mb : Ma;
+                const float inv = M > 0.0f ? (127.0f * 2097152.0f) * __builtin_amdgcn_rcpf(M) : 0.0f;
+                int8_t* dst = xq + (2 * p + hi) * FRAG;
+                put_digits(dst, pos0, v0, inv);
+                put_digits(dst, pos1, v1, inv);
+                put_digits(dst, pos2, v2, inv);
+                put_digits(dst, pos3, v3, inv);
+                if ((lane & 31) == 0) xs[2 * p + hi] = make_float2(M * (1.0f / 127.0f), hi ? Sb : Sa);
+            }
         }
     }
-    if (pbl < nbl) *reinterpret_cast<uint4*>(spar + ((ptt * MAXBK + pbl) * TILE_ROWS + 4 * pq)) = pv;
+    if (lane < QB * 4) *reinterpret_cast<u32x4*>(spar[wave] + lane * 4) = pv;
+    if (threadIdx.x < 4) xs[nbl + threadIdx.x] = make_float2(0.0f, 0.0f);  // == prep's value if written
     __syncthreads();
 
-    // ---- matrix-core phase: wave -> (tile, K-interleave)
-    const bool zcol = j == NDIG;
+    // ---- matrix-core phase
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
     float z0 = 0.f, z1 = 0.f, z2 = 0.f, z3 = 0.f;
-    if (T < ntiles) {
-        const int8_t* xf = xq + g * (NDIG * 16) + j * 16;
-        const uint32_t* sp = spar + ti * MAXBK * TILE_ROWS + 4 * g;
+    {
+        const int lb = kq * q;  // the part's first block within the slice
+        // lanes of columns >= 4 read digit column j&3 (finite, weighted 0 below)
+        const int8_t* xf = xq + lb * FRAG + g * (NDIG * 16) + (j & 3) * 16;
+        const float2* xsp = xs + lb;
+        const uint32_t* sp = spar[wave] + 4 * g;
         const uint32_t M = 0x0F0F0F0Fu;
-        const int nw = (nbl - kw + KS - 1) / KS;  // blocks of this wave
-        for (int i0 = 0; i0 < nw; i0 += PF) {
-            if (i0 > 0) {
 #pragma unroll
-                for (int i = 0; i < PF; i++) {
-                    const int bl = min(kw + KS * (i0 + i), last);
-                    c[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(cp + (size_t)bl * 64));
-                    if constexpr (SCHEME == 3)
-                        h[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(hq + (size_t)bl * 32));
-                }
-            }
+        for (int i0 = 0; i0 < QB; i0 += 4) {
+            if (i0 < qw) {
+                // this group's LDS operands first, so their latencies overlap
+                v4i B0[4], B1[4];
+                u32x4 pr[4];
+                float2 sc[4];
 #pragma unroll
-            for (int i = 0; i < PF; i++) {
-                if (i0 + i >= nw) break;
-                const int bl = kw + KS * (i0 + i);
-                v4i A0, A1;
-                A0.x = c[i].x & M; A0.y = c[i].y & M; A0.z = c[i].z & M; A0.w = c[i].w & M;
-                A1.x = (c[i].x >> 4) & M; A1.y = (c[i].y >> 4) & M;
-                A1.z = (c[i].z >> 4) & M; A1.w = (c[i].w >> 4) & M;
-                if constexpr (SCHEME == 3) {
-                    // top two bits: group g holds AVX lanes g (h.x) and g+4 (h.y)
-                    const uint32_t T6 = 0x30303030u, hx = h[i].x, hy = h[i].y;
-                    A0.x |= (hx << 4) & T6; A0.y |= (hx << 2) & T6;
-                    A0.z |= (hy << 4) & T6; A0.w |= (hy << 2) & T6;
-                    A1.x |= hx & T6;        A1.y |= (hx >> 2) & T6;
-                    A1.z |= hy & T6;        A1.w |= (hy >> 2) & T6;
+                for (int u = 0; u < 4; u++) {
+                    B0[u] = *reinterpret_cast<const v4i*>(xf + (i0 + u) * FRAG);
+                    B1[u] = *reinterpret_cast<const v4i*>(xf + (i0 + u) * FRAG + HALF);
+                    pr[u] = *reinterpret_cast<const u32x4*>(sp + (i0 + u) * TILE_ROWS);
+                    sc[u] = xsp[i0 + u];
                 }
-                v4i B0 = {0, 0, 0, 0}, B1 = {0, 0, 0, 0};
-                if (j < NDIG) {
-                    B0 = *reinterpret_cast<const v4i*>(xf + bl * FRAG);
-                    B1 = *reinterpret_cast<const v4i*>(xf + bl * FRAG + HALF);
+#pragma unroll
+                for (int i = i0; i < i0 + 4; i++) {
+                    const int u = i - i0;
+                    v4i A0, A1;
+                    A0.x = c[i].x & M; A0.y = c[i].y & M; A0.z = c[i].z & M; A0.w = c[i].w & M;
+                    A1.x = (c[i].x >> 4) & M; A1.y = (c[i].y >> 4) & M;
+                    A1.z = (c[i].z >> 4) & M; A1.w = (c[i].w >> 4) & M;
+                    if constexpr (SCHEME == 3) {
+                        // top two bits: group g holds AVX lanes g (h.x) and g+4 (h.y)
+                        const uint32_t T6 = 0x30303030u, hx = h[i].x, hy = h[i].y;
+                        A0.x |= (hx << 4) & T6; A0.y |= (hx << 2) & T6;
+                        A0.z |= (hy << 4) & T6; A0.w |= (hy << 2) & T6;
+                        A1.x |= hx & T6;        A1.y |= (hx >> 2) & T6;
+                        A1.z |= hy & T6;        A1.w |= (hy >> 2) & T6;
+                    }
+                    v4i d = {0, 0, 0, 0};
+                    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0[u], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1[u], d, 0, 0, 0);
+                    fast_step(a0, z0, d.x, pr[u].x, sc[u].x, sc[u].y);
+                    fast_step(a1, z1, d.y, pr[u].y, sc[u].x, sc[u].y);
+                    fast_step(a2, z2, d.z, pr[u].z, sc[u].x, sc[u].y);
+                    fast_step(a3, z3, d.w, pr[u].w, sc[u].x, sc[u].y);
                 }
-                v4i d = {0, 0, 0, 0};
-                d = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0, d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1, d, 0, 0, 0);
-                const uint4 pr = *reinterpret_cast<const uint4*>(sp + bl * TILE_ROWS);
-                const float sb = xsc[bl], Sb = xsum[bl];
-                fast_step(a0, z0, d.x, pr.x, sb, Sb);
-                fast_step(a1, z1, d.y, pr.y, sb, Sb);
-                fast_step(a2, z2, d.z, pr.z, sb, Sb);
-                fast_step(a3, z3, d.w, pr.w, sb, Sb);
             }
         }
     }
-    // digit weights 2^(-7j), then sum columns 0..7 (columns 5..7 hold zeros;
-    // rows 4g..4g+3 live in lanes 16g..16g+7)
-    const float wj = j < NDIG ? __builtin_ldexpf(1.0f, -7 * j) : 1.0f;
-    a0 *= wj; a1 *= wj; a2 *= wj; a3 *= wj;
-    if (zcol) { a0 = z0; a1 = z1; a2 = z2; a3 = z3; }
-    a0 += __shfl_xor(a0, 1); a1 += __shfl_xor(a1, 1); a2 += __shfl_xor(a2, 1); a3 += __shfl_xor(a3, 1);
-    a0 += __shfl_xor(a0, 2); a1 += __shfl_xor(a1, 2); a2 += __shfl_xor(a2, 2); a3 += __shfl_xor(a3, 2);
-    a0 += __shfl_xor(a0, 4); a1 += __shfl_xor(a1, 4); a2 += __shfl_xor(a2, 4); a3 += __shfl_xor(a3, 4);
+    // digit weights 2^(-7j) on columns 0..3, the zero-point sum on column 4,
+    // 0 elsewhere; then the sum over columns 0..7 (rows 4g..4g+3 in lanes
+    // 16g..16g+7)
+    const float wj = j < NDIG ? __builtin_ldexpf(1.0f, -7 * j) : 0.0f;
+    const bool zcol = j == NDIG;
+    a0 = zcol ? z0 : a0 * wj;
+    a1 = zcol ? z1 : a1 * wj;
+    a2 = zcol ? z2 : a2 * wj;
+    a3 = zcol ? z3 : a3 * wj;
+    a0 = sum8(a0); a1 = sum8(a1); a2 = sum8(a2); a3 = sum8(a3);
     if (j == 0) {
         red[wave][4 * g + 0] = a0;
         red[wave][4 * g + 1] = a1;
@@ -387,14 +442,12 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
 
     const int t = threadIdx.x;
     const int tt = t >> 4, rr = t & 15;
-    const int TT = tg * FAST_TILES + tt;
-    const size_t orow = (size_t)TT * TILE_ROWS + rr;
-    const bool mine = t < FAST_TILES * TILE_ROWS && TT < ntiles;
-    float sum = 0.f;
-    if (mine) {
-        sum = red[tt * KS][rr];
-#pragma unroll
-        for (int k = 1; k < KS; k++) sum += red[tt * KS + k][rr];
+    const bool mine = t < tw * TILE_ROWS && tg * tw + tt < ntiles;
+    const size_t orow = (size_t)(tg * tw + tt) * TILE_ROWS + rr;
+    float sum = 0.0f;
+    if (mine) {  // the tile's parts in order
+        sum = red[tt * kw][rr];
+        for (int k = 1; k < kw; k++) sum += red[tt * kw + k][rr];
     }
     if (kg == 1) {
         if (mine && orow < (size_t)P.rows) P.y[orow] = P.bias ? sum + P.bias[orow] : sum;
@@ -436,14 +489,15 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
 }
 
 // ============================================================ decode helpers
-__device__ __forceinline__ uint32_t code_at(const uint8_t* codes, const uint8_t* hp, size_t blk,
-                                            int kk, int scheme)
+__device__ __forceinline__ uint32_t code_at(const uint8_t* codes, const uint8_t* hp, size_t row,
+                                            size_t b, int nb, int kk, int scheme)
 {
-    const int L = kk & 7, G = kk >> 3;
-    const uint8_t byte = codes[blk * 64 + dcode_off(L, G & 7)];
+    const int L = kk & 7, G = kk >> 3, r = (int)(row % TILE_ROWS);
+    const size_t rec = (row / TILE_ROWS) * (size_t)nb + b;
+    const uint8_t byte = codes[rec * CODE_REC + dcode_pos(r, L) + (G & 7)];
     uint32_t code = G < 8 ? (byte & 15u) : (byte >> 4);
     if (scheme == 3) {
-        const uint8_t hb = hp[blk * 32 + dhp_off(L, G & 3)];
+        const uint8_t hb = hp[rec * HP_REC + dhp_pos(r, L) + (G & 3)];
         code |= ((hb >> (2 * (G >> 2))) & 3u) << 4;
     }
     return code;
@@ -459,8 +513,7 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ codes
 {
     const int k = blockIdx.x * 256 + threadIdx.x;
     if (k >= nb * 128) return;
-    const size_t blk = row * (size_t)nb + (size_t)(k >> 7);
-    const uint32_t code = code_at(codes, hp, blk, k & 127, SCHEME);
+    const uint32_t code = code_at(codes, hp, row, (size_t)(k >> 7), nb, k & 127, SCHEME);
     const uint32_t p = params[param_idx(row, nb, k >> 7)];
     out[k] = __fadd_rn(h2f(p & 0xFFFFu), __fmul_rn((float)code, h2f(p >> 16)));
 }
@@ -476,7 +529,7 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ cod
     if (i >= n) return;
     const size_t blk = i >> 7;
     const size_t row = blk / nb, b = blk % nb;
-    const uint32_t code = code_at(codes, hp, blk, (int)(i & 127), SCHEME);
+    const uint32_t code = code_at(codes, hp, row, b, nb, (int)(i & 127), SCHEME);
     const uint32_t p = params[param_idx(row, nb, b)];
     const float zp = h2f(p & 0xFFFFu), sc = h2f(p >> 16);
     w[i] = rounding == WPCG_ROUND_FMA ? __builtin_fmaf((float)code, sc, zp)
@@ -489,18 +542,9 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ cod
 int fast_kslices(uint64_t rows, uint64_t nb)
 {
     if (nb == 0) return 1;
-    constexpr int KS = 4 / FAST_TILES;
-    const uint64_t tiles = pad_rows(rows) / TILE_ROWS;
-    const uint64_t tgroups = (tiles + FAST_TILES - 1) / FAST_TILES;
-    uint64_t kg = (nb + MAXBK - 1) / MAXBK;
-    // more K-slices until the launch has >= 512 workgroups, keeping at least
-    // two blocks per wave
-    while (tgroups * kg < 512) {
-        const uint64_t nbk = (nb + kg) / (kg + 1);
-        if (nbk < 2 * KS) break;
-        kg++;
-    }
-    return fast_normalize_kslices(nb, (int)kg);
+    // as few K-slices as fit: a split costs a cross-workgroup handoff
+    const uint64_t mb = fast_max_slice(rows);
+    return fast_normalize_kslices(nb, (int)((nb + mb - 1) / mb));
 }
 
 hipError_t launch_gemv_exact(const DeviceMatrix& m, const float* x, const float* bias, float* y,
@@ -542,8 +586,9 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         P.nb = (int)m.nb;
         P.kg = jobs[i].plan->kg;
         P.wg_begin = wgs;
-        const int tgroups = (int)((m.rows_pad / TILE_ROWS + FAST_TILES - 1) / FAST_TILES);
-        wgs += tgroups * P.kg;
+        P.tw = fast_tiles_per_wg(m.rows);
+        const int tiles = (int)(m.rows_pad / TILE_ROWS);
+        wgs += (tiles + P.tw - 1) / P.tw * P.kg;
     }
     if (wgs == 0) return hipSuccess;
     (void)hipGetLastError();  // report only this launch

@@ -58,13 +58,15 @@ void transcode_rows(int scheme, const uint8_t* blocks, uint64_t r0, uint64_t nro
     parallel_rows(nrows, [&](uint64_t a, uint64_t b) {
         for (uint64_t r = a; r < b; r++) {
             const uint64_t row = r0 + r;
+            const int tr = (int)(r % TILE_ROWS);
+            const uint64_t t = r / TILE_ROWS;  // tile relative to `codes`/`hp`
             for (uint64_t k = 0; k < nb; k++) {
                 const uint8_t* blk = blocks + (r * nb + k) * bpb;
                 params[((row / TILE_ROWS) * nb + k) * TILE_ROWS + row % TILE_ROWS] = rd_params(blk);
-                uint8_t* dc = codes + (r * nb + k) * 64;
+                uint8_t* dc = codes + (t * nb + k) * CODE_REC;
                 if (scheme == 4) {
                     for (int L = 0; L < 8; L++)
-                        for (int g = 0; g < 8; g++) dc[code_off(L, g)] = blk[4 + g * 8 + L];
+                        for (int g = 0; g < 8; g++) dc[code_pos(tr, L) + g] = blk[4 + g * 8 + L];
                 } else {
                     uint8_t c[128], lp[64], h[32];
                     v3_unpack(blk + 4, c);
@@ -72,10 +74,10 @@ void transcode_rows(int scheme, const uint8_t* blocks, uint64_t r0, uint64_t nro
                     for (int j = 0; j < 32; j++)
                         h[j] = (uint8_t)(((c[j] >> 4) & 3) | ((c[j + 32] >> 4) & 3) << 2 |
                                          ((c[j + 64] >> 4) & 3) << 4 | ((c[j + 96] >> 4) & 3) << 6);
-                    uint8_t* dh = hp + (r * nb + k) * 32;
+                    uint8_t* dh = hp + (t * nb + k) * HP_REC;
                     for (int L = 0; L < 8; L++) {
-                        for (int g = 0; g < 8; g++) dc[code_off(L, g)] = lp[g * 8 + L];
-                        for (int m = 0; m < 4; m++) dh[hp_off(L, m)] = h[m * 8 + L];
+                        for (int g = 0; g < 8; g++) dc[code_pos(tr, L) + g] = lp[g * 8 + L];
+                        for (int m = 0; m < 4; m++) dh[hp_pos(tr, L) + m] = h[m * 8 + L];
                     }
                 }
             }

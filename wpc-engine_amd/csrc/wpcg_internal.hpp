@@ -29,24 +29,28 @@ int hip_fail(hipError_t e, const char* what);
 // Both schemes keep the reference's bytes per block (68 for v4, 100 for v3)
 // but split each block into planes that vector loads can reach. Rows are
 // padded to a multiple of 16 (one matrix-core tile); padding is zero.
+// Every plane is tile-major: the data of block `blk` of the 16 rows of tile
+// t is one contiguous record, so one wave's 16-byte-per-lane load of a
+// block is a single fully used 1 KiB span.
 //
-//   codes[row][blk][64]  the 64 nibble-pair bytes of the reference block in
-//                        "paired-lane" order: the eight bytes that AVX2 lane
-//                        L of the reference kernel reads (ref bytes g*8+L,
-//                        g < 8) sit at dev[(L&3)*16 + (L>>2)*8 + g], so
-//                        lane L alone is one 8-byte word and lanes L, L+4
-//                        together are one 16-byte word.
-//   hp[row][blk][32]     (v3) the two-plane high bits, same pairing:
-//                        dev[(L&3)*8 + (L>>2)*4 + m] = hp[m*8 + L]  (m < 4)
-//   params[row/16][blk][row%16]  u32 zero_point f16 | scale f16 << 16,
-//                        16-row tile-major so one 16-byte load returns the
-//                        parameters of four consecutive rows.
+//   codes[t][blk][1024]  the 64 nibble-pair bytes of each of the 16 rows'
+//                        reference blocks. AVX2 lane L of the reference
+//                        kernel reads ref bytes g*8+L (g < 8) of row r; they
+//                        sit at code_pos(r, L) + g, so lane L alone is one
+//                        8-byte word and lanes L, L+4 together are one
+//                        16-byte word, at ((L&3)*16 + r)*16.
+//   hp[t][blk][512]      (v3) the two-plane high bits, same pairing:
+//                        hp[m*8 + L] of row r at hp_pos(r, L) + m  (m < 4)
+//   params[t][blk][16]   u32 zero_point f16 | scale f16 << 16 of row t*16+i
+//                        at i, so one 16-byte load returns four rows.
 constexpr int TILE_ROWS = 16;
+constexpr uint64_t CODE_REC = 1024;  // code bytes per (tile, block)
+constexpr uint64_t HP_REC = 512;     // high-plane bytes per (tile, block)
 
 inline uint64_t pad_rows(uint64_t rows) { return (rows + TILE_ROWS - 1) / TILE_ROWS * TILE_ROWS; }
 
-inline uint64_t code_off(int L, int g) { return (uint64_t)((L & 3) * 16 + (L >> 2) * 8 + g); }
-inline uint64_t hp_off(int L, int m) { return (uint64_t)((L & 3) * 8 + (L >> 2) * 4 + m); }
+inline uint64_t code_pos(int r, int L) { return (uint64_t)(((L & 3) * 16 + r) * 16 + (L >> 2) * 8); }
+inline uint64_t hp_pos(int r, int L) { return (uint64_t)(((L & 3) * 16 + r) * 8 + (L >> 2) * 4); }
 
 struct DeviceMatrix {
     int scheme = 0;
@@ -62,12 +66,14 @@ struct DeviceMatrix {
 struct FastPlan {
     int kg = 1;               // K-slices across workgroups
     float* part = nullptr;    // [kg][rows_pad] partial sums (kg > 1)
-    uint32_t* counters = nullptr;  // one per tile group, self-resetting
+    uint32_t* counters = nullptr;  // one per workgroup tile group, self-resetting
 };
 
 // Host transcodes from the reference's on-disk blocks (AoS) to the planes
 // above, for rows [r0, r0 + nrows) of a matrix with nb blocks per row.
-// `codes`/`hp` point at row r0; `params` at the matrix's parameter base.
+// r0 is a multiple of 16 and `codes`/`hp` point at tile r0/16's records;
+// `params` at the matrix's parameter base. Bytes of padding rows in the
+// last tile are left as they are (the caller zeroes them).
 void transcode_rows(int scheme, const uint8_t* blocks, uint64_t r0, uint64_t nrows, uint64_t nb,
                     uint8_t* codes, uint8_t* hp, uint32_t* params_tile_major);
 
@@ -79,8 +85,11 @@ struct GemvJob {
     const float* bias;
     float* y;
 };
-constexpr int FAST_TILES = 2;  // 16-row tiles per FAST workgroup
-constexpr int FAST_MAXBK = 32; // blocks per FAST K-slice (the slice's x digits live in LDS)
+// FAST mode: a workgroup computes fast_tiles_per_wg 16-row tiles over a
+// K-slice of at most fast_max_slice blocks (the slice's x digits live in LDS).
+constexpr int FAST_MAXBK = 64;
+inline int fast_tiles_per_wg(uint64_t rows) { return pad_rows(rows) / TILE_ROWS >= 512 ? 2 : 1; }
+inline uint64_t fast_max_slice(uint64_t rows) { return FAST_MAXBK / fast_tiles_per_wg(rows); }
 hipError_t launch_gemv_exact(const DeviceMatrix& m, const float* x, const float* bias, float* y,
                              hipStream_t s);
 // All jobs must share the scheme. At most MAX_JOBS per launch.
