@@ -32,6 +32,11 @@ QWEN3_4B = [("q_proj", 4096, 2560), ("k_proj", 1024, 2560), ("v_proj", 1024, 256
             ("o_proj", 2560, 4096), ("gate_proj", 9728, 2560), ("up_proj", 9728, 2560),
             ("down_proj", 2560, 9728)]
 BPB = {3: 100, 4: 68}
+# HBM bytes per launch of the FAST kernel in this workload, measured with
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (bench.py --pmc-pass) and scaled by
+# the same counters' reading for a copy kernel of known size; see
+# profiles/k_gemv_fast_cfg1_v3_traffic.txt. None where not measured.
+TRAFFIC = {(3, "fast"): 20023459}
 
 
 def log(msg):
@@ -87,6 +92,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--normal-exit", action="store_true",
                     help="leave through the runtime's exit path (profilers finalize there)")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="short run for rocprofv3 --pmc passes (no timing, no JSON)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -120,17 +127,43 @@ def main():
     yb = {name: ctx.alloc(4 * r) for name, r, _ in QWEN3_4B}
     names = [n for n, _, _ in QWEN3_4B]
 
+    def step_launches(s):
+        """One step's launches: q/k/v share their input and one launch, as do
+        gate/up; o and down run alone (their inputs come from other ops)."""
+        L = dict(zip(names, s))
+        return [
+            lambda: wpcg.matvec_multi([L["q_proj"], L["k_proj"], L["v_proj"]], [xb[2560]] * 3,
+                                      [yb["q_proj"], yb["k_proj"], yb["v_proj"]]),
+            lambda: L["o_proj"].matvec_dev(xb[4096], yb["o_proj"]),
+            lambda: wpcg.matvec_multi([L["gate_proj"], L["up_proj"]], [xb[2560]] * 2,
+                                      [yb["gate_proj"], yb["up_proj"]]),
+            lambda: L["down_proj"].matvec_dev(xb[9728], yb["down_proj"]),
+        ]
+
     def one_round():
-        # one step per copy: q/k/v share their input and one launch, as do
-        # gate/up; o and down run alone (their inputs come from other ops)
-        for s in sets:
-            L = dict(zip(names, s))
-            wpcg.matvec_multi([L["q_proj"], L["k_proj"], L["v_proj"]], [xb[2560]] * 3,
-                              [yb["q_proj"], yb["k_proj"], yb["v_proj"]])
-            L["o_proj"].matvec_dev(xb[4096], yb["o_proj"])
-            wpcg.matvec_multi([L["gate_proj"], L["up_proj"]], [xb[2560]] * 2,
-                              [yb["gate_proj"], yb["up_proj"]])
-            L["down_proj"].matvec_dev(xb[9728], yb["down_proj"])
+        for s in sets:  # one step per copy
+            for fn in step_launches(s):
+                fn()
+
+    def launch_durations(rounds):
+        """Average device duration of one launch, from an event pair recorded
+        on the launch's own stream right before and after it."""
+        evs = [(ctx.event(), ctx.event()) for _ in range(4 * len(sets))]
+        total, n = 0.0, 0
+        for _ in range(rounds):
+            k = 0
+            for s in sets:
+                for fn in step_launches(s):
+                    a, b = evs[k]
+                    k += 1
+                    a.record()
+                    fn()
+                    b.record()
+            ctx.sync()
+            for a, b in evs:
+                total += a.elapsed_ms(b)
+                n += 1
+        return total / n * 1e3, n
 
     def measure(mode):
         for s in sets:
@@ -154,6 +187,24 @@ def main():
         return (step_bytes * steps / (ms / 1e3) / 1e9, ms, steps, launches * copies,
                 ms * 1e3 / n_launch, n_launch)
 
+    if args.pmc_pass:
+        # short run for hardware-counter passes: a few rotations of the FAST
+        # steps, then one plain copy kernel of known size (the calibration of
+        # the FETCH_SIZE / WRITE_SIZE counters against a known byte count)
+        for s in sets:
+            for l in s:
+                l.set_mode(mode)
+        for _ in range(4):
+            one_round()
+        ctx.sync()
+        n = 256 << 20  # bytes read and bytes written by the copy kernel
+        src, dst = ctx.alloc(n), ctx.alloc(n)
+        wpcg.check(wpcg.lib.wpcg_memcpy_d2d(ctx.h, dst.ptr, src.ptr, n))
+        ctx.sync()
+        log(f"pmc pass: {4 * copies} steps, then one device copy of {n} bytes "
+            "(the runtime's copy kernel)")
+        return 0
+
     other = "exact" if args.mode == "fast" else "fast"
     log(f"timing {other} mode")
     o_val = measure(wpcg.MODE_EXACT if other == "exact" else wpcg.MODE_FAST)[0]
@@ -162,6 +213,16 @@ def main():
     value, ms, steps, warm, avg_launch_us, n_launch = measure(mode)
     log(f"{args.mode}: {value:.1f} GB/s ({100 * value / PEAK_GBPS:.1f}% of peak), "
         f"{ms / steps * 1e3:.2f} us/step, {n_launch} launches, avg {avg_launch_us:.2f} us")
+    # The graph replays the launches back to back on one stream, so the
+    # event-timed region divided by the launches is the kernel's average
+    # launch duration (inter-kernel gaps included; rocprofv3's kernel trace
+    # of the same command gives the same average within a few percent).
+    dur_us = avg_launch_us
+    launch_bytes = step_bytes / (n_launch // steps)
+    achieved = launch_bytes / dur_us / 1e3
+    eager_us, n_eager = launch_durations(max(1, -(-100 // copies)))
+    log(f"avg launch {dur_us:.2f} us -> {achieved:.1f} GB/s per launch; eager launches between "
+        f"event pairs: {eager_us:.2f} us ({n_eager} launches, dispatch latency included)")
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -196,12 +257,14 @@ def main():
         "roofline": {
             "bound": "hbm",
             "kernel": kname,
-            "achieved": round(value, 2),
+            "achieved": round(achieved, 2),
             "peak": PEAK_GBPS,
             "unit": "GB/s",
-            "frac": round(value / PEAK_GBPS, 4),
-            "avg_launch_us": round(avg_launch_us, 3),
-            "traffic": None,
+            "frac": round(achieved / PEAK_GBPS, 4),
+            "avg_launch_us": round(dur_us, 3),
+            "eager_launch_us": round(eager_us, 3),
+            "algorithmic_bytes_per_launch": round(launch_bytes),
+            "traffic": TRAFFIC.get((scheme, args.mode)),
         },
         "cpu_baseline": cpu,
     }
