@@ -128,15 +128,17 @@ int wpcg_linear_destroy(wpcg_linear* lin);
 /* Linear::in_features / out_features (weights.rs:18-19) */
 int wpcg_linear_shape(wpcg_linear* lin, uint64_t* out_f, uint64_t* in_f);
 int wpcg_linear_set_mode(wpcg_linear* lin, int mode);
-/* FAST mode splits K over `kslices` workgroups per 32-row tile group
- * (0 = the library's choice for the shape; capped so a slice holds at most
- * 32 blocks). Replaces the matrix's split-K workspace: graphs captured
+/* FAST mode splits K over `kslices` workgroups per group of output rows
+ * (0 = the library's choice for the shape). A workgroup covers 16 rows, or
+ * 32 for matrices of 8192 rows or more, and a slice at most 64 blocks (32
+ * with 32 rows); requests are raised to that minimum and capped at one
+ * block per slice. Replaces the matrix's split-K workspace: graphs captured
  * earlier with this linear must be destroyed first. No reference
  * counterpart (a tuning knob). */
 int wpcg_linear_set_kslices(wpcg_linear* lin, int kslices);
 int wpcg_linear_kslices(wpcg_linear* lin, int* kslices);
 /* The split wpcg_linear_set_kslices would use for an out_f x in_f matrix
- * (host-only query; every slice is non-empty and holds at most 32 blocks). */
+ * (host-only query; every slice is non-empty and within the limits above). */
 int wpcg_plan_kslices(uint64_t out_f, uint64_t in_f, int requested, int* kslices);
 /* Device bytes the weights occupy (codes + block parameters). */
 int wpcg_linear_device_bytes(wpcg_linear* lin, uint64_t* bytes);
