@@ -174,8 +174,14 @@ def test_fast_split_plan_never_makes_an_empty_slice():
                 nbk = -(-nb // k)
                 assert 1 <= k <= nb and nbk <= most, (nb, req, rows, k)
                 assert (k - 1) * nbk < nb <= k * nbk, (nb, req, k, nbk)
-                if req == 0:  # the default is the fewest slices that fit
-                    assert k == -(-nb // most), (nb, rows, k)
+                if req == 0:
+                    # the default: the fewest slices that fit, or, when that
+                    # is more than one, slices of at most half the maximum
+                    raw = -(-nb // most)
+                    if raw > 1:
+                        raw = -(-nb // (most // 2))
+                    nbk_raw = -(-nb // raw)
+                    assert k == -(-nb // nbk_raw), (nb, rows, k)
     with pytest.raises(wpcg.WpcgError) as e:
         wpcg.plan_kslices(4, 100)
     assert e.value.code == wpcg.E_SHAPE

@@ -542,9 +542,13 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ cod
 int fast_kslices(uint64_t rows, uint64_t nb)
 {
     if (nb == 0) return 1;
-    // as few K-slices as fit: a split costs a cross-workgroup handoff
+    // As few K-slices as fit: a split costs a cross-workgroup handoff. When
+    // a split is needed anyway, slices of half the maximum leave each wave
+    // one group of four blocks, which is faster than two groups.
     const uint64_t mb = fast_max_slice(rows);
-    return fast_normalize_kslices(nb, (int)((nb + mb - 1) / mb));
+    uint64_t kg = (nb + mb - 1) / mb;
+    if (kg > 1) kg = (nb + mb / 2 - 1) / (mb / 2);
+    return fast_normalize_kslices(nb, (int)kg);
 }
 
 hipError_t launch_gemv_exact(const DeviceMatrix& m, const float* x, const float* bias, float* y,
