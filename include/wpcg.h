@@ -151,7 +151,7 @@ int wpcg_linear_matvec(wpcg_linear* lin, const float* x_dev, float* y_dev, wpcg_
 int wpcg_linear_matvec_host(wpcg_linear* lin, const float* x, float* y);
 
 /* n independent matvecs, ys[i] = W_i xs[i] (+ bias_i), issued together: FAST
- * members of one scheme share one launch (up to 8 per launch), EXACT members
+ * members of one scheme share one launch (up to 16 per launch), EXACT members
  * launch one by one. Matrices that read the same input (q/k/v, gate/up, the
  * experts of a token) fill the GPU together. The linears' outputs must not
  * overlap each other or any input. No reference counterpart: the reference
@@ -174,6 +174,63 @@ int wpcg_linear_dequant(wpcg_linear* lin, int rounding, float* w_dev, wpcg_strea
  * counterpart). Used to rotate a working set larger than the 256 MB
  * Infinity Cache when measuring HBM-bound throughput. */
 int wpcg_linear_clone(wpcg_linear* lin, wpcg_linear** out);
+
+/* ---- fp32 dense linear: the MoE router ----
+ * Replaces DenseLinear (wpc-runtime/src/weights.rs:35-79), which the
+ * Qwen3-MoE model builds for `mlp.gate.weight` (qwen3_moe_model.rs:182-187).
+ * `w` is host [out_f][in_f] row-major fp32, `bias` host out_f floats or NULL.
+ * EXACT matches DenseLinear::matvec bit for bit (index-order sums, product
+ * and sum rounded separately); FAST sums in parallel. */
+typedef struct wpcg_dense wpcg_dense;
+int wpcg_dense_create(wpcg_ctx* ctx, const float* w, uint64_t out_f, uint64_t in_f,
+                      const float* bias, wpcg_dense** out);
+int wpcg_dense_destroy(wpcg_dense* d);
+int wpcg_dense_set_mode(wpcg_dense* d, int mode);
+int wpcg_dense_matvec(wpcg_dense* d, const float* x_dev, float* y_dev, wpcg_stream stream);
+
+/* softmax_inplace (wpc-runtime/src/norm.rs:28-43) over n floats in place,
+ * bit for bit: exp is the reference host libm's expf. */
+int wpcg_softmax(wpcg_ctx* ctx, float* x_dev, uint32_t n, wpcg_stream stream);
+
+/* Qwen3MoeModel::route (qwen3_moe_model.rs:376-402): the top_k largest of n
+ * probabilities (ties to the lowest index, NaN never chosen), written in
+ * descending order to ids/weights (top_k each); with norm_topk the weights
+ * are divided by their sum. Slots left unfilled get id -1, weight 0.
+ * n <= 512, top_k <= n. */
+int wpcg_route(wpcg_ctx* ctx, const float* probs_dev, uint32_t n, uint32_t top_k, int norm_topk,
+               int32_t* ids_dev, float* weights_dev, wpcg_stream stream);
+
+/* out[i] = silu(g[i]) * u[i], silu(g) = g / (1 + exp(-g)), as the expert
+ * and dense MLPs compute it (qwen3_moe_model.rs:518-522, model.rs:527-531). */
+int wpcg_silu_mul(wpcg_ctx* ctx, const float* g_dev, const float* u_dev, float* out_dev,
+                  uint64_t n, wpcg_stream stream);
+
+/* ---- Qwen3-MoE sparse MLP of one layer ----
+ * Replaces the router + route + expert loop of Qwen3MoeModel::forward_token
+ * (qwen3_moe_model.rs:500-530) with the experts' weights resident on the
+ * device. n_exp experts, each gate/up [inter x hidden] and down
+ * [hidden x inter] in `scheme` blocks; the router [n_exp x hidden] fp32.
+ * The routing stays on the device: the chosen experts' GEMVs read their ids
+ * from device memory. EXACT mode is bit-identical to the reference; FAST
+ * uses the FAST GEMV and router. */
+typedef struct wpcg_moe wpcg_moe;
+int wpcg_moe_create(wpcg_ctx* ctx, int scheme, uint32_t n_exp, uint32_t hidden, uint32_t inter,
+                    uint32_t top_k, int norm_topk, wpcg_moe** out);
+int wpcg_moe_destroy(wpcg_moe* m);
+int wpcg_moe_set_router(wpcg_moe* m, const float* w);
+/* Expert e's three matrices, blocks in the reference layout (as
+ * WpcLinearV4::new takes them for experts.{e}.{gate,up,down}_proj.weight). */
+int wpcg_moe_set_expert(wpcg_moe* m, uint32_t e, const void* gate, const void* up,
+                        const void* down);
+/* All experts of layer `layer` from an artifact: tensors
+ * model.layers.{layer}.mlp.experts.{e}.{gate,up,down}_proj.weight. */
+int wpcg_moe_load_experts(wpcg_moe* m, wpcg_artifact* a, uint32_t layer);
+int wpcg_moe_set_mode(wpcg_moe* m, int mode);
+/* out = sum over the router's top_k experts of weight * down(silu(gate x) *
+ * up x), in chosen order. ids/weights (top_k each, device) receive the
+ * routing when non-NULL. x and out must not overlap. */
+int wpcg_moe_forward(wpcg_moe* m, const float* x_dev, float* out_dev, int32_t* ids_dev,
+                     float* weights_dev, wpcg_stream stream);
 
 /* ---- HIP graphs over the context stream (no reference counterpart) ----
  * wpcg_graph_begin starts capturing the context's stream; device calls with

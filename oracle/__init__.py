@@ -79,6 +79,9 @@ def lib():
         "or_argmax": (C.c_uint32, [_f32p, _sz]),
         "or_silu_mul": (C.c_float, [C.c_float, C.c_float]),
         "or_route": (_sz, [_f32p, _sz, _sz, C.c_int, _i32p, _f32p]),
+        "or_silu_mul_array": (None, [_f32p, _f32p, _f32p, _sz]),
+        "or_moe_ffn_v4": (None, [_f32p, _sz, _sz, _sz, _sz, C.c_int, C.c_void_p, _f32p, _f32p,
+                                 _i32p, _f32p, C.c_int, C.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -281,3 +284,32 @@ def route(scores, top_k: int, norm_topk: bool):
     w = np.zeros(max(top_k, 1), np.float32)
     n = lib().or_route(scores, scores.size, top_k, int(norm_topk), ids, w)
     return ids[:n].copy(), w[:n].copy()
+
+
+def silu_mul_array(g, u) -> np.ndarray:
+    g, u = _f32(g), _f32(u)
+    out = np.empty_like(g)
+    lib().or_silu_mul_array(g, u, out, g.size)
+    return out
+
+
+class _Expert(C.Structure):
+    _fields_ = [("gate", C.c_void_p), ("up", C.c_void_p), ("down", C.c_void_p)]
+
+
+def moe_ffn_v4(router_w, experts, x, top_k: int, norm_topk: bool = True,
+               kernel: int = KERNEL_FUSED, threads: int = 4):
+    """or_moe_ffn_v4: (mlp_out, ids, weights). experts: [(gate, up, down)]
+    reference v4 blocks per expert; router_w [n_exp, hidden] fp32."""
+    router_w = np.ascontiguousarray(router_w, np.float32)
+    n_exp, hidden = router_w.shape
+    x = _f32(x)
+    keep = [tuple(np.ascontiguousarray(b, np.uint8) for b in e) for e in experts]
+    inter = keep[0][0].size // 68 // (hidden // 128)
+    arr = (_Expert * n_exp)(*[_Expert(g.ctypes.data, u.ctypes.data, d.ctypes.data) for g, u, d in keep])
+    out = np.empty(hidden, np.float32)
+    ids = np.empty(top_k, np.int32)
+    w = np.empty(top_k, np.float32)
+    lib().or_moe_ffn_v4(router_w.ravel(), n_exp, hidden, inter, top_k, int(bool(norm_topk)),
+                        C.cast(arr, C.c_void_p), x, out, ids, w, kernel, threads)
+    return out, ids, w

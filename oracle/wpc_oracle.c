@@ -623,6 +623,10 @@ float or_silu_mul(float g, float u)
     return silu * u;
 }
 
+void or_silu_mul_array(const float* g, const float* u, float* out, size_t n)
+{
+    for (size_t i = 0; i < n; i++) out[i] = or_silu_mul(g[i], u[i]);
+}
 /* Qwen3MoeModel::route (qwen3_moe_model.rs:376-402): k strict-`>` scans, so
  * ties go to the lowest index; then divide by the (sequential) sum of the k
  * weights when norm_topk and that sum is positive. */

@@ -100,6 +100,8 @@ void     or_rms_norm(const float* x, const float* w, size_t n, float eps, float*
 void     or_apply_rope(float* x, size_t d, size_t pos, double theta);
 uint32_t or_argmax(const float* logits, size_t n);
 float    or_silu_mul(float g, float u);
+/* out[i] = or_silu_mul(g[i], u[i]) for i < n */
+void     or_silu_mul_array(const float* g, const float* u, float* out, size_t n);
 
 /* Qwen3MoeModel::route (qwen3_moe_model.rs:376-402). Returns the number of
  * experts chosen (top_k unless fewer are selectable). */

@@ -44,8 +44,6 @@ void ctx_release(wpcg_ctx* c)
     delete c;
 }
 
-namespace {
-
 hipStream_t pick(wpcg_ctx* ctx, wpcg_stream s)
 {
     return s ? reinterpret_cast<hipStream_t>(s) : ctx->stream;
@@ -58,8 +56,6 @@ int check_ctx(wpcg_ctx* ctx)
     return WPCG_OK;
 }
 
-const char* meta_name(int scheme) { return scheme == 4 ? "model_v4.meta" : "model_v3.meta"; }
-const char* wpc_name(int scheme) { return scheme == 4 ? "model_v4.wpc" : "model_v3.wpc"; }
 uint64_t block_bytes(int scheme) { return scheme == 4 ? 68 : 100; }
 
 void free_matrix(DeviceMatrix& m)
@@ -79,30 +75,28 @@ void free_plan(FastPlan& p)
     p.counters = nullptr;
 }
 
-// Device bytes of the three planes, rows padded to a 16-row tile.
 uint64_t plane_blocks(const DeviceMatrix& m) { return std::max<uint64_t>(1, m.rows_pad * m.nb); }
 
-int alloc_matrix(DeviceMatrix& m)
+int alloc_planes(DeviceMatrix& m, uint64_t count, hipStream_t s)
 {
-    const uint64_t nb = plane_blocks(m);
+    const uint64_t nb = std::max<uint64_t>(1, count * plane_blocks(m));
     WPCG_HIP(hipMalloc(&m.codes, nb * 64));
     WPCG_HIP(hipMalloc(&m.params, nb * 4));
     if (m.scheme == 3) WPCG_HIP(hipMalloc(&m.hp, nb * 32));
+    WPCG_HIP(hipMemsetAsync(m.codes, 0, nb * 64, s));
+    WPCG_HIP(hipMemsetAsync(m.params, 0, nb * 4, s));
+    if (m.hp) WPCG_HIP(hipMemsetAsync(m.hp, 0, nb * 32, s));
+    WPCG_HIP(hipStreamSynchronize(s));
     return WPCG_OK;
 }
 
-// Transcodes reference blocks to the device planes and uploads them in
-// chunks of whole 16-row tiles (bounded host staging). Padding rows stay 0.
-int upload_matrix(wpcg_ctx* ctx, const uint8_t* blocks, DeviceMatrix& m)
+int upload_rows(wpcg_ctx* ctx, const uint8_t* blocks, const DeviceMatrix& m, uint64_t tile0)
 {
-    if (int rc = alloc_matrix(m)) return rc;
-    const uint64_t nb = m.nb, pb = plane_blocks(m);
+    const uint64_t nb = m.nb;
+    if (nb == 0 || m.rows == 0) return WPCG_OK;
     hipStream_t s = ctx->stream;
-    WPCG_HIP(hipMemsetAsync(m.codes, 0, pb * 64, s));
-    WPCG_HIP(hipMemsetAsync(m.params, 0, pb * 4, s));
-    if (m.hp) WPCG_HIP(hipMemsetAsync(m.hp, 0, pb * 32, s));
-    if (nb == 0 || m.rows == 0) return hipStreamSynchronize(s) == hipSuccess ? WPCG_OK : fail(WPCG_E_DEVICE, "sync");
     const uint64_t bpb = block_bytes(m.scheme);
+    const uint64_t base = tile0 * TILE_ROWS * nb;  // first block record of the range
     // ~4 MiB of codes per chunk, a whole number of tiles
     uint64_t chunk_rows = std::max<uint64_t>(TILE_ROWS, ((1u << 16) / nb) / TILE_ROWS * TILE_ROWS);
     std::vector<uint8_t> c(chunk_rows * nb * 64), h(m.scheme == 3 ? chunk_rows * nb * 32 : 0);
@@ -117,17 +111,16 @@ int upload_matrix(wpcg_ctx* ctx, const uint8_t* blocks, DeviceMatrix& m)
         }
         // planes are tile-major, so whole tiles of rows are contiguous
         transcode_rows(m.scheme, blocks + r0 * nb * bpb, 0, n, nb, c.data(), h.data(), p.data());
-        WPCG_HIP(hipMemcpyAsync(m.codes + r0 * nb * 64, c.data(), ntile_rows * nb * 64, hipMemcpyHostToDevice, s));
-        WPCG_HIP(hipMemcpyAsync(m.params + r0 * nb, p.data(), ntile_rows * nb * 4, hipMemcpyHostToDevice, s));
+        const uint64_t off = base + r0 * nb;
+        WPCG_HIP(hipMemcpyAsync(m.codes + off * 64, c.data(), ntile_rows * nb * 64, hipMemcpyHostToDevice, s));
+        WPCG_HIP(hipMemcpyAsync(m.params + off, p.data(), ntile_rows * nb * 4, hipMemcpyHostToDevice, s));
         if (m.hp)
-            WPCG_HIP(hipMemcpyAsync(m.hp + r0 * nb * 32, h.data(), ntile_rows * nb * 32, hipMemcpyHostToDevice, s));
+            WPCG_HIP(hipMemcpyAsync(m.hp + off * 32, h.data(), ntile_rows * nb * 32, hipMemcpyHostToDevice, s));
         WPCG_HIP(hipStreamSynchronize(s));
     }
     return WPCG_OK;
 }
 
-// Workspace for FAST mode's split-K: partial sums and self-resetting
-// counters, fixed for the matrix's lifetime (captured graphs keep using it).
 int plan_kslices(uint64_t rows, uint64_t nb, int kg)
 {
     const uint64_t mb = fast_max_slice(rows);
@@ -137,7 +130,7 @@ int plan_kslices(uint64_t rows, uint64_t nb, int kg)
     return fast_normalize_kslices(nb, k);
 }
 
-int make_plan(const DeviceMatrix& m, FastPlan& plan, hipStream_t s, int kg = 0)
+int make_plan(const DeviceMatrix& m, FastPlan& plan, hipStream_t s, int kg)
 {
     plan.kg = plan_kslices(m.rows, m.nb, kg);
     if (plan.kg <= 1) return WPCG_OK;
@@ -147,6 +140,18 @@ int make_plan(const DeviceMatrix& m, FastPlan& plan, hipStream_t s, int kg = 0)
     WPCG_HIP(hipMemsetAsync(plan.counters, 0, tiles * sizeof(uint32_t), s));
     WPCG_HIP(hipStreamSynchronize(s));
     return WPCG_OK;
+}
+
+namespace {
+
+const char* meta_name(int scheme) { return scheme == 4 ? "model_v4.meta" : "model_v3.meta"; }
+const char* wpc_name(int scheme) { return scheme == 4 ? "model_v4.wpc" : "model_v3.wpc"; }
+
+// Transcodes reference blocks to the device planes and uploads them.
+int upload_matrix(wpcg_ctx* ctx, const uint8_t* blocks, DeviceMatrix& m)
+{
+    if (int rc = alloc_planes(m, 1, ctx->stream)) return rc;
+    return upload_rows(ctx, blocks, m, 0);
 }
 
 hipError_t run_gemv(wpcg_linear* L, const float* x, float* y, hipStream_t s)

@@ -117,15 +117,31 @@ __device__ __forceinline__ float v3_exact_block(uint2 c, uint32_t h, uint32_t p,
     return acc;
 }
 
+// With `sel` set, the planes stack experts of rows_pad rows each and the
+// GEMV is expert sel[sel_k]'s (a negative id writes y = 0).
 template <int SCHEME>
 __global__ __launch_bounds__(EX_WG) void k_gemv_exact(const uint8_t* __restrict__ codes,
                                                       const uint8_t* __restrict__ hp,
                                                       const uint32_t* __restrict__ params,
                                                       const float* __restrict__ x,
                                                       const float* __restrict__ bias,
-                                                      float* __restrict__ y, int rows, int nb)
+                                                      float* __restrict__ y, int rows, int nb,
+                                                      const int32_t* __restrict__ sel, int sel_k,
+                                                      int rows_pad)
 {
     __shared__ __align__(16) float xs[EX_SEG * XS_BLK];
+    if (sel) {
+        const int e = sel[sel_k];
+        if (e < 0) {
+            const int r = blockIdx.x * (EX_WG / 8) + (threadIdx.x >> 3);
+            if (r < rows && (threadIdx.x & 7) == 0) y[r] = 0.0f;
+            return;
+        }
+        const size_t t0 = (size_t)e * (rows_pad / TILE_ROWS) * nb;
+        codes += t0 * CODE_REC;
+        if (SCHEME == 3) hp += t0 * HP_REC;
+        params += t0 * TILE_ROWS;
+    }
     const int L = threadIdx.x & 7;
     const int row = blockIdx.x * (EX_WG / 8) + (threadIdx.x >> 3);
     const bool active = row < rows;
@@ -183,7 +199,12 @@ struct FastProblem {
     const float* bias;
     float* part;
     uint32_t* counters;
+    // Expert selection: with sel set, the matrix stacks experts of rows_pad
+    // rows each and this problem is expert sel[sel_k] (its rows only; a
+    // negative id gives y = 0).
+    const int32_t* sel;
     int rows, rows_pad, nb, kg, wg_begin, tw;  // tw: 16-row tiles per workgroup
+    int sel_k, pad_;
 };
 struct FastBatch {
     FastProblem p[MAX_JOBS];
@@ -289,6 +310,18 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
     const KargPtr kargs = (KargPtr)__builtin_amdgcn_kernarg_segment_ptr();
     const auto& P = kargs->p[pi];
     const int nb = P.nb, kg = P.kg, tw = P.tw;
+    const uint8_t* codes = P.codes;
+    const uint8_t* hplane = SCHEME == 3 ? P.hp : P.codes;
+    const uint32_t* params = P.params;
+    bool live = true;
+    if (P.sel) {  // the routed expert's rows of a stacked matrix
+        const int e = P.sel[P.sel_k];
+        live = e >= 0;
+        const size_t t0 = (size_t)max(e, 0) * (P.rows_pad / TILE_ROWS) * nb;  // tile-block records
+        codes += t0 * CODE_REC;
+        hplane += t0 * HP_REC;
+        params += t0 * TILE_ROWS;
+    }
     const int local = wgid - P.wg_begin;
     const int kgi = local % kg, tg = local / kg;  // K-slice, tile group
     const int nbk = (nb + kg - 1) / kg;
@@ -299,7 +332,7 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
     const int kw = 8 / tw;                           // waves per tile
     const int T = tg * tw + wave / kw, kq = wave % kw;
     const int q = (nbl + kw - 1) / kw;               // blocks per part (<= QB)
-    const int qw = T < ntiles ? max(0, min(q, nbl - kq * q)) : 0;  // this wave's blocks
+    const int qw = live && T < ntiles ? max(0, min(q, nbl - kq * q)) : 0;  // this wave's blocks
     const int wb = b0 + kq * q;                      // its first block
     const int g = lane >> 4, j = lane & 15;
 
@@ -317,11 +350,11 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
         xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
     const size_t rec = (size_t)min(T, ntiles - 1) * nb + wb;
     // lane l: rows 4(l&3)..+3 of block l>>2 (blocks past QB are not kept)
-    const auto prs = buf_rsrc(P.params + rec * TILE_ROWS, qw * 64);
+    const auto prs = buf_rsrc(params + rec * TILE_ROWS, qw * 64);
     const u32x4 pv = __builtin_amdgcn_raw_buffer_load_b128(prs, lane * 16, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
-    const auto crs = buf_rsrc(P.codes + rec * CODE_REC, qw * (int)CODE_REC);
-    const auto hrs = buf_rsrc((SCHEME == 3 ? P.hp : P.codes) + rec * HP_REC, SCHEME == 3 ? qw * (int)HP_REC : 0);
+    const auto crs = buf_rsrc(codes + rec * CODE_REC, qw * (int)CODE_REC);
+    const auto hrs = buf_rsrc(hplane + rec * HP_REC, SCHEME == 3 ? qw * (int)HP_REC : 0);
     u32x4 c[QB];
     u32x2 h[QB];
 #pragma unroll
@@ -552,17 +585,17 @@ int fast_kslices(uint64_t rows, uint64_t nb)
 }
 
 hipError_t launch_gemv_exact(const DeviceMatrix& m, const float* x, const float* bias, float* y,
-                             hipStream_t s)
+                             hipStream_t s, const int32_t* sel, int sel_k)
 {
     const int rows = (int)m.rows, nb = (int)m.nb;
     dim3 grid((unsigned)(m.rows_pad / (EX_WG / 8)));
     (void)hipGetLastError();  // report only this launch
     if (m.scheme == 4)
         hipLaunchKernelGGL(k_gemv_exact<4>, grid, dim3(EX_WG), 0, s, m.codes, m.hp, m.params, x,
-                           bias, y, rows, nb);
+                           bias, y, rows, nb, sel, sel_k, (int)m.rows_pad);
     else
         hipLaunchKernelGGL(k_gemv_exact<3>, grid, dim3(EX_WG), 0, s, m.codes, m.hp, m.params, x,
-                           bias, y, rows, nb);
+                           bias, y, rows, nb, sel, sel_k, (int)m.rows_pad);
     return hipGetLastError();
 }
 
@@ -590,6 +623,8 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         P.nb = (int)m.nb;
         P.kg = jobs[i].plan->kg;
         P.wg_begin = wgs;
+        P.sel = jobs[i].sel;
+        P.sel_k = jobs[i].sel_k;
         P.tw = fast_tiles_per_wg(m.rows);
         const int tiles = (int)(m.rows_pad / TILE_ROWS);
         wgs += (tiles + P.tw - 1) / P.tw * P.kg;

@@ -1,0 +1,207 @@
+// Qwen3-MoE sparse-MLP pieces on gfx950: the fp32 router (DenseLinear),
+// softmax, top-k routing, SiLU*up and the weighted combine of the chosen
+// experts' outputs. The expert GEMVs themselves are the dequant-GEMV kernels
+// (gemv.hip) with device-side expert selection, so a routed layer needs no
+// host round trip.
+//
+// Every piece here reproduces the reference's arithmetic exactly, operation
+// for operation (Rust does not contract or reassociate): products and sums
+// round separately, sums run in index order, exp is the host libm's expf
+// (ref_expf.h). The FAST router is the one exception (a parallel sum).
+#include <hip/hip_runtime.h>
+
+#define REF_EXPF_FN __device__ __forceinline__
+#include "ref_expf.h"
+#include "wpcg_internal.hpp"
+
+namespace wpcg {
+namespace {
+
+// ---- DenseLinear::matvec (wpc-runtime/src/weights.rs:59-78) -------------
+// y[r] = sum_i W[r][i] * x[i], index order. The device keeps W transposed,
+// wt[i*out_f + r], so step i of a wave's 64 rows is one coalesced load.
+__global__ __launch_bounds__(64) void k_dense_exact(const float* __restrict__ wt,
+                                                    const float* __restrict__ x,
+                                                    const float* __restrict__ bias,
+                                                    float* __restrict__ y, int out_f, int in_f)
+{
+    const int r = blockIdx.x * 64 + threadIdx.x;
+    const float* col = wt + min(r, out_f - 1);
+    float acc = 0.0f;
+#pragma unroll 16
+    for (int i = 0; i < in_f; i++) acc = __fadd_rn(acc, __fmul_rn(col[(size_t)i * out_f], x[i]));
+    if (r < out_f) y[r] = bias ? __fadd_rn(acc, bias[r]) : acc;
+}
+
+// FAST: one wave per row over the transposed layout's column, lanes strided
+// over i, fixed-order tree sum (deterministic, not the reference's order).
+__global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ wt,
+                                                    const float* __restrict__ x,
+                                                    const float* __restrict__ bias,
+                                                    float* __restrict__ y, int out_f, int in_f)
+{
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int rr = min(r, out_f - 1);
+    float acc = 0.0f;
+    for (int i = lane; i < in_f; i += 64) acc = fmaf(wt[(size_t)i * out_f + rr], x[i], acc);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+    if (r < out_f && lane == 0) y[r] = bias ? acc + bias[r] : acc;
+}
+
+// ---- softmax_inplace (wpc-runtime/src/norm.rs:28-43) ---------------------
+// max (f32::max drops NaN like fmaxf; order-free), e_i = exp(x_i - max),
+// sum in index order, then x_i = e_i / sum when sum > 0. One workgroup.
+constexpr int SM_WG = 256;
+__global__ __launch_bounds__(SM_WG) void k_softmax(float* __restrict__ x, int n)
+{
+    __shared__ float red[SM_WG / 64];
+    __shared__ float s_sum;
+    float m = -INFINITY;
+    for (int i = threadIdx.x; i < n; i += SM_WG) m = fmaxf(m, x[i]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int i = threadIdx.x; i < n; i += SM_WG) x[i] = ref_expf(__fsub_rn(x[i], m));
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float s = 0.0f;
+        for (int i = 0; i < n; i++) s = __fadd_rn(s, x[i]);
+        s_sum = s;
+    }
+    __syncthreads();
+    const float s = s_sum;
+    if (s > 0.0f)
+        for (int i = threadIdx.x; i < n; i += SM_WG) x[i] = __fdiv_rn(x[i], s);
+}
+
+// ---- Qwen3MoeModel::route (qwen3_moe_model.rs:376-402) -------------------
+// top_k strict-`>` scans: each takes the largest remaining value, the lowest
+// index on ties, and never a NaN or -inf (`score > best` with best starting
+// at -inf). With norm_topk the chosen weights are divided by their sum
+// (taken in chosen order) when it is positive. Unfilled slots get id -1,
+// weight 0. One wave; n <= 64*RT_PER.
+constexpr int RT_PER = 8;
+__global__ __launch_bounds__(64) void k_route(const float* __restrict__ p, int n, int top_k,
+                                              int norm_topk, int32_t* __restrict__ ids,
+                                              float* __restrict__ w)
+{
+    const int lane = threadIdx.x;
+    float v[RT_PER];
+#pragma unroll
+    for (int j = 0; j < RT_PER; j++) {
+        const int i = lane + 64 * j;
+        v[j] = i < n ? p[i] : -INFINITY;
+        if (!(v[j] > -INFINITY)) v[j] = -INFINITY;  // NaN is never chosen
+    }
+    int got = 0;
+    for (int k = 0; k < top_k; k++) {
+        // best (value, index) of this lane, then of the wave
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < RT_PER; j++)
+            if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int oi = __shfl_xor(bi, o);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if (!(bv > -INFINITY)) break;  // nothing left to choose
+#pragma unroll
+        for (int j = 0; j < RT_PER; j++)
+            if (lane + 64 * j == bi) v[j] = -INFINITY;
+        if (lane == 0) { ids[k] = bi; w[k] = bv; }
+        got = k + 1;
+    }
+    if (lane == 0) {
+        for (int k = got; k < top_k; k++) { ids[k] = -1; w[k] = 0.0f; }
+        if (norm_topk) {  // lane 0 rereads its own writes
+            float s = 0.0f;
+            for (int k = 0; k < got; k++) s = __fadd_rn(s, w[k]);
+            if (s > 0.0f)
+                for (int k = 0; k < got; k++) w[k] = __fdiv_rn(w[k], s);
+        }
+    }
+}
+
+// ---- SiLU(g) * u (qwen3_moe_model.rs:518-522, model.rs:527-531) ----------
+__global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ g,
+                                                  const float* __restrict__ u,
+                                                  float* __restrict__ out, size_t n)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float gv = g[i];
+    const float silu = __fdiv_rn(gv, __fadd_rn(1.0f, ref_expf(-gv)));
+    out[i] = __fmul_rn(silu, u[i]);
+}
+
+// ---- mlp_out = sum over chosen k of w_k * y_k (qwen3_moe_model.rs:526-528)
+// in chosen order from 0; slots with id < 0 were never run.
+__global__ __launch_bounds__(256) void k_combine(const float* __restrict__ ys,
+                                                 const int32_t* __restrict__ ids,
+                                                 const float* __restrict__ w, int top_k,
+                                                 float* __restrict__ out, int h)
+{
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= h) return;
+    float acc = 0.0f;
+    for (int k = 0; k < top_k; k++)
+        if (ids[k] >= 0) acc = __fadd_rn(acc, __fmul_rn(w[k], ys[(size_t)k * h + i]));
+    out[i] = acc;
+}
+
+}  // namespace
+
+hipError_t launch_dense(const float* wt, int out_f, int in_f, int mode, const float* x,
+                        const float* bias, float* y, hipStream_t s)
+{
+    (void)hipGetLastError();
+    if (mode == WPCG_MODE_EXACT)
+        hipLaunchKernelGGL(k_dense_exact, dim3((out_f + 63) / 64), dim3(64), 0, s, wt, x, bias, y,
+                           out_f, in_f);
+    else
+        hipLaunchKernelGGL(k_dense_fast, dim3((out_f + 3) / 4), dim3(256), 0, s, wt, x, bias, y,
+                           out_f, in_f);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax(float* x, int n, hipStream_t s)
+{
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k_softmax, dim3(1), dim3(SM_WG), 0, s, x, n);
+    return hipGetLastError();
+}
+
+int route_max_n() { return 64 * RT_PER; }
+
+hipError_t launch_route(const float* p, int n, int top_k, int norm_topk, int32_t* ids, float* w,
+                        hipStream_t s)
+{
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k_route, dim3(1), dim3(64), 0, s, p, n, top_k, norm_topk, ids, w);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const float* g, const float* u, float* out, size_t n, hipStream_t s)
+{
+    if (n == 0) return hipSuccess;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k_silu_mul, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, g, u, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine(const float* ys, const int32_t* ids, const float* w, int top_k,
+                          float* out, int h, hipStream_t s)
+{
+    if (h == 0) return hipSuccess;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k_combine, dim3((h + 255) / 256), dim3(256), 0, s, ys, ids, w, top_k, out, h);
+    return hipGetLastError();
+}
+
+}  // namespace wpcg

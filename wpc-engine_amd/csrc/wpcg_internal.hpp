@@ -78,12 +78,17 @@ void transcode_rows(int scheme, const uint8_t* blocks, uint64_t r0, uint64_t nro
                     uint8_t* codes, uint8_t* hp, uint32_t* params_tile_major);
 
 // ---- kernel launchers (gemv.hip) ----------------------------------------
+// One GEMV y = W x (+ bias). With `sel` set, `m` describes one expert
+// (rows, rows_pad, nb) and its planes are the first of a stack of experts;
+// the job is expert sel[sel_k] of the stack (device-resident routing).
 struct GemvJob {
     const DeviceMatrix* m;
     const FastPlan* plan;
     const float* x;
     const float* bias;
     float* y;
+    const int32_t* sel = nullptr;
+    int sel_k = 0;
 };
 // FAST mode: a workgroup computes fast_tiles_per_wg 16-row tiles over a
 // K-slice of at most fast_max_slice blocks (the slice's x digits live in LDS).
@@ -91,9 +96,9 @@ constexpr int FAST_MAXBK = 64;
 inline int fast_tiles_per_wg(uint64_t rows) { return pad_rows(rows) / TILE_ROWS >= 512 ? 2 : 1; }
 inline uint64_t fast_max_slice(uint64_t rows) { return FAST_MAXBK / fast_tiles_per_wg(rows); }
 hipError_t launch_gemv_exact(const DeviceMatrix& m, const float* x, const float* bias, float* y,
-                             hipStream_t s);
+                             hipStream_t s, const int32_t* sel = nullptr, int sel_k = 0);
 // All jobs must share the scheme. At most MAX_JOBS per launch.
-constexpr int MAX_JOBS = 8;
+constexpr int MAX_JOBS = 16;
 hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s);
 hipError_t launch_embed(const DeviceMatrix& m, uint32_t row, float* out, hipStream_t s);
 hipError_t launch_dequant(const DeviceMatrix& m, int rounding, float* w, hipStream_t s);
@@ -106,6 +111,35 @@ inline int fast_normalize_kslices(uint64_t nb, int kg)
     const uint64_t nbk = (nb + kg - 1) / kg;
     return (int)((nb + nbk - 1) / nbk);
 }
+
+// ---- host helpers shared by the C ABI files (capi*.cpp) -----------------
+hipStream_t pick(wpcg_ctx* ctx, wpcg_stream s);  // NULL = the context stream
+int check_ctx(wpcg_ctx* ctx);                     // non-null, device current
+uint64_t block_bytes(int scheme);                 // 68 (v4) / 100 (v3)
+void free_matrix(DeviceMatrix& m);
+void free_plan(FastPlan& p);
+uint64_t plane_blocks(const DeviceMatrix& m);     // rows_pad * nb (at least 1)
+// Zeroed planes for `count` matrices of m's shape, stacked tile after tile.
+int alloc_planes(DeviceMatrix& m, uint64_t count, hipStream_t s);
+// Transcodes m.rows rows of reference blocks into m's planes from tile
+// `tile0` on (synchronous; bounded host staging). Padding rows stay 0.
+int upload_rows(wpcg_ctx* ctx, const uint8_t* blocks, const DeviceMatrix& m, uint64_t tile0);
+// FAST split-K: slices for a rows x nb matrix (kg 0 = the library's choice)
+// and the workspace for it, fixed for the matrix's lifetime (captured
+// graphs keep using it).
+int plan_kslices(uint64_t rows, uint64_t nb, int kg);
+int make_plan(const DeviceMatrix& m, FastPlan& plan, hipStream_t s, int kg = 0);
+
+// ---- MoE pieces (moe.hip) -------------------------------------------------
+hipError_t launch_dense(const float* wt, int out_f, int in_f, int mode, const float* x,
+                        const float* bias, float* y, hipStream_t s);
+hipError_t launch_softmax(float* x, int n, hipStream_t s);
+int route_max_n();
+hipError_t launch_route(const float* p, int n, int top_k, int norm_topk, int32_t* ids, float* w,
+                        hipStream_t s);
+hipError_t launch_silu_mul(const float* g, const float* u, float* out, size_t n, hipStream_t s);
+hipError_t launch_combine(const float* ys, const int32_t* ids, const float* w, int top_k,
+                          float* out, int h, hipStream_t s);
 
 // ---- minimal JSON (for model_v{3,4}.meta) ---------------------------------
 struct MetaEntry {
@@ -151,6 +185,29 @@ struct wpcg_linear {
     std::mutex host_mu;
     float* x_stage = nullptr;
     float* y_stage = nullptr;
+};
+
+struct wpcg_dense {
+    wpcg_ctx* ctx = nullptr;
+    uint64_t out_f = 0, in_f = 0;
+    float* wt = nullptr;    // device, transposed: wt[i*out_f + r] = W[r][i]
+    float* bias = nullptr;  // device or null
+    int mode = WPCG_MODE_EXACT;
+};
+
+// One layer's routed experts. The three projections are stored as stacks:
+// expert e's gate rows are tiles [e*T, (e+1)*T) of `gate` (T = the
+// expert's tile count), likewise up and down, so a routed GEMV finds its
+// expert from the id alone. The DeviceMatrix fields describe one expert.
+struct wpcg_moe {
+    wpcg_ctx* ctx = nullptr;
+    int scheme = 4, mode = WPCG_MODE_EXACT, norm_topk = 1;
+    uint32_t n_exp = 0, hidden = 0, inter = 0, top_k = 0;
+    wpcg_dense* router = nullptr;
+    wpcg::DeviceMatrix gate, up, down;
+    wpcg::FastPlan plan;  // kg = 1 for every expert shape (checked at creation)
+    float *scores = nullptr, *w = nullptr, *g = nullptr, *u = nullptr, *h = nullptr, *ys = nullptr;
+    int32_t* ids = nullptr;
 };
 
 struct wpcg_event {

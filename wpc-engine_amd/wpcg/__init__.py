@@ -89,6 +89,21 @@ _SIGS = {
     "wpcg_linear_dequant": (C.c_int, [_p, C.c_int, _p, _p]),
     "wpcg_linear_clone": (C.c_int, [_p, _pp]),
     "wpcg_linear_matvec_multi": (C.c_int, [C.c_int, _pp, _pp, _pp, _p]),
+    "wpcg_dense_create": (C.c_int, [_p, _p, _u64, _u64, _p, _pp]),
+    "wpcg_dense_destroy": (C.c_int, [_p]),
+    "wpcg_dense_set_mode": (C.c_int, [_p, C.c_int]),
+    "wpcg_dense_matvec": (C.c_int, [_p, _p, _p, _p]),
+    "wpcg_softmax": (C.c_int, [_p, _p, C.c_uint32, _p]),
+    "wpcg_route": (C.c_int, [_p, _p, C.c_uint32, C.c_uint32, C.c_int, _p, _p, _p]),
+    "wpcg_silu_mul": (C.c_int, [_p, _p, _p, _p, _u64, _p]),
+    "wpcg_moe_create": (C.c_int, [_p, C.c_int, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                  C.c_int, _pp]),
+    "wpcg_moe_destroy": (C.c_int, [_p]),
+    "wpcg_moe_set_router": (C.c_int, [_p, _p]),
+    "wpcg_moe_set_expert": (C.c_int, [_p, C.c_uint32, _p, _p, _p]),
+    "wpcg_moe_load_experts": (C.c_int, [_p, _p, C.c_uint32]),
+    "wpcg_moe_set_mode": (C.c_int, [_p, C.c_int]),
+    "wpcg_moe_forward": (C.c_int, [_p, _p, _p, _p, _p, _p]),
     "wpcg_graph_begin": (C.c_int, [_p]),
     "wpcg_graph_end": (C.c_int, [_p, _pp]),
     "wpcg_graph_launch": (C.c_int, [_p, _p]),
@@ -450,3 +465,133 @@ class WpcLinearV3(WpcLinearV4):
 
 WpcEmbeddingV4 = WpcLinearV4
 WpcEmbeddingV3 = WpcLinearV3
+
+
+# ------------------------------------------------------------------ MoE pieces
+class DenseLinear:
+    """fp32 dense matrix on the GPU (DenseLinear, weights.rs:35-79; the
+    Qwen3-MoE router)."""
+
+    def __init__(self, ctx: Context, w, bias=None):
+        w = np.ascontiguousarray(w, np.float32)
+        self.ctx, (self._out, self._in) = ctx, w.shape
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        h = C.c_void_p()
+        check(lib.wpcg_dense_create(ctx.h if ctx else None, _np_ptr(w), self._out, self._in,
+                                    None if b is None else _np_ptr(b), C.byref(h)))
+        self.h = h
+
+    def in_features(self) -> int:
+        return self._in
+
+    def out_features(self) -> int:
+        return self._out
+
+    def set_mode(self, mode: int):
+        check(lib.wpcg_dense_set_mode(self.h, mode))
+        return self
+
+    def matvec_dev(self, x: DeviceBuffer, y: DeviceBuffer, stream=None):
+        check(lib.wpcg_dense_matvec(self.h, x.ptr, y.ptr, stream))
+
+    def matvec(self, x) -> np.ndarray:
+        xb = self.ctx.upload(np.ascontiguousarray(x, np.float32))
+        yb = self.ctx.alloc(4 * self._out)
+        self.matvec_dev(xb, yb)
+        self.ctx.sync()
+        return yb.read(np.float32, self._out)
+
+    def close(self):
+        if self.h:
+            lib.wpcg_dense_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def softmax(ctx: Context, x) -> np.ndarray:
+    """softmax_inplace (norm.rs:28-43) on the GPU, returned to the host."""
+    x = np.ascontiguousarray(x, np.float32)
+    b = ctx.upload(x)
+    check(lib.wpcg_softmax(ctx.h, b.ptr, x.size, None))
+    ctx.sync()
+    return b.read(np.float32, x.size)
+
+
+def route(ctx: Context, probs, top_k: int, norm_topk: bool = True):
+    """Qwen3MoeModel::route (qwen3_moe_model.rs:376-402) on the GPU:
+    (ids int32[top_k], weights float32[top_k])."""
+    p = np.ascontiguousarray(probs, np.float32)
+    b, ib, wb = ctx.upload(p), ctx.alloc(4 * top_k), ctx.alloc(4 * top_k)
+    check(lib.wpcg_route(ctx.h, b.ptr, p.size, top_k, int(bool(norm_topk)), ib.ptr, wb.ptr, None))
+    ctx.sync()
+    return ib.read(np.int32, top_k), wb.read(np.float32, top_k)
+
+
+def silu_mul(ctx: Context, g, u) -> np.ndarray:
+    g = np.ascontiguousarray(g, np.float32)
+    u = np.ascontiguousarray(u, np.float32)
+    gb, ub, ob = ctx.upload(g), ctx.upload(u), ctx.alloc(4 * g.size)
+    check(lib.wpcg_silu_mul(ctx.h, gb.ptr, ub.ptr, ob.ptr, g.size, None))
+    ctx.sync()
+    return ob.read(np.float32, g.size)
+
+
+class MoeLayer:
+    """The routed-expert MLP of one Qwen3-MoE layer, resident on the GPU
+    (qwen3_moe_model.rs:500-530)."""
+
+    def __init__(self, ctx: Context, scheme: int, n_exp: int, hidden: int, inter: int,
+                 top_k: int, norm_topk: bool = True):
+        self.ctx = ctx
+        self.n_exp, self.hidden, self.inter, self.top_k = n_exp, hidden, inter, top_k
+        h = C.c_void_p()
+        check(lib.wpcg_moe_create(ctx.h if ctx else None, scheme, n_exp, hidden, inter, top_k,
+                                  int(bool(norm_topk)), C.byref(h)))
+        self.h = h
+
+    def set_router(self, w):
+        w = np.ascontiguousarray(w, np.float32)
+        assert w.shape == (self.n_exp, self.hidden)
+        check(lib.wpcg_moe_set_router(self.h, _np_ptr(w)))
+        return self
+
+    def set_expert(self, e: int, gate, up, down):
+        g, u, d = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
+        check(lib.wpcg_moe_set_expert(self.h, e, _np_ptr(g), _np_ptr(u), _np_ptr(d)))
+        return self
+
+    def load_experts(self, data: "WpcModelData", layer: int):
+        check(lib.wpcg_moe_load_experts(self.h, data.h, layer))
+        return self
+
+    def set_mode(self, mode: int):
+        check(lib.wpcg_moe_set_mode(self.h, mode))
+        return self
+
+    def forward_dev(self, x: DeviceBuffer, out: DeviceBuffer, ids=None, weights=None, stream=None):
+        check(lib.wpcg_moe_forward(self.h, x.ptr, out.ptr, ids.ptr if ids else None,
+                                   weights.ptr if weights else None, stream))
+
+    def forward(self, x):
+        """(out float32[hidden], ids int32[top_k], weights float32[top_k])"""
+        xb = self.ctx.upload(np.ascontiguousarray(x, np.float32))
+        ob, ib, wb = self.ctx.alloc(4 * self.hidden), self.ctx.alloc(4 * self.top_k), self.ctx.alloc(4 * self.top_k)
+        self.forward_dev(xb, ob, ib, wb)
+        self.ctx.sync()
+        return ob.read(np.float32, self.hidden), ib.read(np.int32, self.top_k), wb.read(np.float32, self.top_k)
+
+    def close(self):
+        if self.h:
+            lib.wpcg_moe_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
