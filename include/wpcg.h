@@ -175,6 +175,13 @@ int wpcg_linear_dequant(wpcg_linear* lin, int rounding, float* w_dev, wpcg_strea
  * Infinity Cache when measuring HBM-bound throughput. */
 int wpcg_linear_clone(wpcg_linear* lin, wpcg_linear** out);
 
+/* ---- encoder (host only) ----
+ * encode_tensor_v4 / encode_tensor_v3 (wpc-core/src/quant_encoder.rs:49-57,
+ * 88-96): n fp32 values (n % 128 == 0) to n/128 blocks of 68 / 100 bytes in
+ * the reference layout, as the artifact compiler writes them. Multithreaded;
+ * needs no GPU. */
+int wpcg_encode(int scheme, const float* w, uint64_t n, void* out_blocks);
+
 /* ---- fp32 dense linear: the MoE router ----
  * Replaces DenseLinear (wpc-runtime/src/weights.rs:35-79), which the
  * Qwen3-MoE model builds for `mlp.gate.weight` (qwen3_moe_model.rs:182-187).
@@ -231,6 +238,68 @@ int wpcg_moe_set_mode(wpcg_moe* m, int mode);
  * routing when non-NULL. x and out must not overlap. */
 int wpcg_moe_forward(wpcg_moe* m, const float* x_dev, float* out_dev, int32_t* ids_dev,
                      float* weights_dev, wpcg_stream stream);
+
+/* rms_norm (wpc-runtime/src/norm.rs:4-13): out = x * (1 / sqrt(mean(x^2) +
+ * eps)) * w over n floats. EXACT sums the squares in index order (bit for
+ * bit the reference); FAST sums them as a tree. */
+int wpcg_rms_norm(wpcg_ctx* ctx, const float* x_dev, const float* w_dev, uint32_t n, float eps,
+                  float* out_dev, int mode, wpcg_stream stream);
+
+/* ---- device-resident decode step ----
+ * A dense Qwen3 (n_experts == 0, SwiGLU MLP) or Qwen3-MoE decoder whose
+ * weights, fp32 KV cache, activations, position and tokens stay on the GPU.
+ * One step is Model::forward_token (wpc-runtime/src/model.rs:419-547) or
+ * Qwen3MoeModel::forward_token (qwen3_moe_model.rs:406-542) followed by
+ * argmax (sampling.rs:3-14); it runs as one replayed HIP graph. EXACT mode
+ * reproduces the reference's logits bit for bit; FAST mode uses the FAST
+ * GEMV and router and tree sums for the long RMSNorm reductions. */
+typedef struct {
+    uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim;
+    uint32_t inter;                          /* dense MLP width (n_experts == 0)   */
+    uint32_t vocab;
+    uint32_t n_experts, top_k, moe_inter;    /* Qwen3-MoE (n_experts > 0)          */
+    int32_t norm_topk;                       /* renormalise the top-k weights      */
+    int32_t tied;                            /* logits from the embedding table    */
+    uint32_t max_pos;                        /* KV-cache length                    */
+    float eps;                               /* RMSNorm epsilon                    */
+    double rope_theta;
+} wpcg_model_config;
+typedef struct wpcg_model wpcg_model;
+int wpcg_model_create(wpcg_ctx* ctx, int scheme, const wpcg_model_config* cfg, wpcg_model** out);
+int wpcg_model_destroy(wpcg_model* m);
+/* A tensor by the reference's name: quantized matrices (model.embed_tokens,
+ * lm_head, model.layers.{l}.self_attn.{q,k,v,o}_proj, mlp.{gate,up,down}_proj,
+ * mlp.experts.{e}.{gate,up,down}_proj; all `.weight`) take blocks in the
+ * model's scheme; model.norm, {input,post_attention}_layernorm,
+ * self_attn.{q,k}_norm and the router mlp.gate take fp32. E_NOTFOUND for a
+ * name the config has no place for, E_SHAPE for a size that disagrees. */
+int wpcg_model_set_tensor(wpcg_model* m, const char* name, const void* data, uint64_t nbytes);
+/* Every quantized matrix of the config from an artifact (the fp32 tensors,
+ * which the reference reads from safetensors, go through set_tensor). */
+int wpcg_model_load_artifact(wpcg_model* m, wpcg_artifact* a);
+int wpcg_model_set_mode(wpcg_model* m, int mode);
+/* Empty the KV cache (position 0). */
+int wpcg_model_reset(wpcg_model* m);
+int wpcg_model_position(wpcg_model* m, uint32_t* pos);
+/* One step at the next position with input `token`: logits (host, vocab
+ * floats) and/or their argmax, either may be NULL. E_ARG when the cache is
+ * full. */
+int wpcg_model_forward_token(wpcg_model* m, uint32_t token, float* logits, uint32_t* argmax);
+/* Greedy generation from position 0: the prompt, then n_new tokens, each
+ * the argmax of the previous step's logits, written to out (n_new ids).
+ * Steps run back to back on the device with no host round trip.
+ * decode_ms (may be NULL) receives the time of the n_new-1 steps after the
+ * prompt. */
+int wpcg_model_generate(wpcg_model* m, const uint32_t* prompt, uint32_t n_prompt, uint32_t n_new,
+                        uint32_t* out, float* decode_ms);
+
+/* Diagnostics, no reference counterpart: copies n floats of one of the
+ * decode step's device buffers as the last step left them. which: 0
+ * residual, 1 normed (after the final norm), 2 q (normed, rotated), 3 k and
+ * 4 v (the last layer's projections), 5 attention output, 6 attention
+ * weights [n_heads][max_pos], 7 logits, 8 MoE output, 9 K cache, 10 V cache
+ * ([layer][kv_head][max_pos][head_dim]). */
+int wpcg_model_debug_read(wpcg_model* m, int which, float* out, uint64_t n);
 
 /* ---- HIP graphs over the context stream (no reference counterpart) ----
  * wpcg_graph_begin starts capturing the context's stream; device calls with

@@ -80,6 +80,10 @@ def lib():
         "or_silu_mul": (C.c_float, [C.c_float, C.c_float]),
         "or_route": (_sz, [_f32p, _sz, _sz, C.c_int, _i32p, _f32p]),
         "or_silu_mul_array": (None, [_f32p, _f32p, _f32p, _sz]),
+        "or_kv_cache_new": (C.c_void_p, [C.c_void_p, _sz]),
+        "or_kv_cache_free": (None, [C.c_void_p]),
+        "or_kv_cache_len": (_sz, [C.c_void_p]),
+        "or_forward_token_v4": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, _f32p, C.c_int, C.c_int]),
         "or_moe_ffn_v4": (None, [_f32p, _sz, _sz, _sz, _sz, C.c_int, C.c_void_p, _f32p, _f32p,
                                  _i32p, _f32p, C.c_int, C.c_int]),
     }
@@ -313,3 +317,74 @@ def moe_ffn_v4(router_w, experts, x, top_k: int, norm_topk: bool = True,
     lib().or_moe_ffn_v4(router_w.ravel(), n_exp, hidden, inter, top_k, int(bool(norm_topk)),
                         C.cast(arr, C.c_void_p), x, out, ids, w, kernel, threads)
     return out, ids, w
+
+
+
+class _Cfg(C.Structure):
+    _fields_ = [(f, C.c_size_t) for f in ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim",
+                                          "inter", "vocab", "n_exp", "top_k", "moe_inter")] + [
+        ("norm_topk", C.c_int), ("tied", C.c_int), ("rope_theta", C.c_double), ("eps", C.c_float)]
+
+
+class _Layer(C.Structure):
+    _fields_ = [(f, C.c_void_p) for f in ("input_ln", "post_ln", "q_norm", "k_norm", "q", "k", "v", "o",
+                                          "gate", "up", "down", "router", "experts")]
+
+
+class _Model(C.Structure):
+    _fields_ = [("cfg", _Cfg), ("embed", C.c_void_p), ("lm_head", C.c_void_p),
+                ("final_norm", C.c_void_p), ("layers", C.c_void_p)]
+
+
+class Model:
+    """or_forward_token_v4: the reference's dense Qwen3 / Qwen3-MoE decode
+    step on the CPU (v4 weights). cfg: dict with the wpcg.ModelConfig field
+    names; tensors: {reference name: array}."""
+
+    def __init__(self, cfg: dict, tensors: dict, max_pos: int, kernel: int = KERNEL_FUSED,
+                 threads: int = 8):
+        self.cfg, self.kernel, self.threads = cfg, kernel, threads
+        self.keep = {k: np.ascontiguousarray(v) for k, v in tensors.items()}
+        T = self.keep
+        ptr = lambda n: T[n].ctypes.data if n in T else None  # noqa: E731
+        L = cfg["n_layers"]
+        self.layers = (_Layer * L)()
+        self.expert_arrays = []
+        for l in range(L):
+            p = f"model.layers.{l}."
+            lay = self.layers[l]
+            lay.input_ln, lay.post_ln = ptr(p + "input_layernorm.weight"), ptr(p + "post_attention_layernorm.weight")
+            lay.q_norm, lay.k_norm = ptr(p + "self_attn.q_norm.weight"), ptr(p + "self_attn.k_norm.weight")
+            lay.q, lay.k = ptr(p + "self_attn.q_proj.weight"), ptr(p + "self_attn.k_proj.weight")
+            lay.v, lay.o = ptr(p + "self_attn.v_proj.weight"), ptr(p + "self_attn.o_proj.weight")
+            if cfg["n_experts"]:
+                E = cfg["n_experts"]
+                arr = (_Expert * E)(*[_Expert(ptr(p + f"mlp.experts.{e}.gate_proj.weight"),
+                                              ptr(p + f"mlp.experts.{e}.up_proj.weight"),
+                                              ptr(p + f"mlp.experts.{e}.down_proj.weight")) for e in range(E)])
+                self.expert_arrays.append(arr)
+                lay.router, lay.experts = ptr(p + "mlp.gate.weight"), C.cast(arr, C.c_void_p)
+            else:
+                lay.gate, lay.up = ptr(p + "mlp.gate_proj.weight"), ptr(p + "mlp.up_proj.weight")
+                lay.down = ptr(p + "mlp.down_proj.weight")
+        c = _Cfg(cfg["n_layers"], cfg["hidden"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"],
+                 cfg["inter"], cfg["vocab"], cfg["n_experts"], cfg["top_k"], cfg["moe_inter"],
+                 int(cfg["norm_topk"]), int(cfg["tied"]), float(cfg["rope_theta"]), float(cfg["eps"]))
+        self.model = _Model(c, ptr("model.embed_tokens.weight"), ptr("lm_head.weight"),
+                            ptr("model.norm.weight"), C.cast(self.layers, C.c_void_p))
+        self.cache = lib().or_kv_cache_new(C.byref(self.model.cfg), max_pos)
+
+    def forward_token(self, token: int) -> np.ndarray:
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        rc = lib().or_forward_token_v4(C.byref(self.model), token, self.cache, logits, self.kernel,
+                                       self.threads)
+        assert rc == 0, rc
+        return logits
+
+    def close(self):
+        if self.cache:
+            lib().or_kv_cache_free(self.cache)
+            self.cache = None
+
+    def __del__(self):
+        self.close()

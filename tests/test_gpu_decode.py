@@ -1,0 +1,111 @@
+"""GPU tests of the device-resident decode step against the oracle's
+restatement of Model::forward_token (model.rs:419-547) and
+Qwen3MoeModel::forward_token (qwen3_moe_model.rs:406-542) with greedy
+argmax (sampling.rs:3-14), on seeded synthetic v4 models (weights
+~N(0, 0.02) encoded as the artifact compiler does, norms 1.0).
+
+EXACT mode: the logits of every step are bit-identical to the oracle's, and
+greedy generation gives the same token ids for 64 steps. FAST mode: the
+step's logits stay within 1e-3 of the logit range of the EXACT ones, and its
+greedy ids are reported against EXACT's (they may part after a near tie)."""
+import numpy as np
+import pytest
+
+import oracle as O
+import wpcg
+from wpcg import synth
+
+pytestmark = pytest.mark.gpu
+
+DENSE = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, inter=512, vocab=1000,
+             n_experts=0, top_k=0, moe_inter=0, norm_topk=1, tied=1, max_pos=96, eps=1e-6,
+             rope_theta=1e6)
+MOE = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, inter=0, vocab=1000,
+           n_experts=16, top_k=4, moe_inter=128, norm_topk=1, tied=0, max_pos=96, eps=1e-6,
+           rope_theta=1e6)
+# Qwen3-30B-A3B shapes (config 3) with two of the 48 layers
+QWEN3_MOE_2L = dict(n_layers=2, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=128, inter=0,
+                    vocab=151936, n_experts=128, top_k=8, moe_inter=768, norm_topk=1, tied=0,
+                    max_pos=80, eps=1e-6, rope_theta=1e6)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = wpcg.Context(0)
+    yield c
+    c.close()
+
+
+def build(ctx, cfg, seed):
+    tensors = dict(synth.model_tensors(cfg, 4, seed, wpcg.encode))
+    m = wpcg.Model(ctx, 4, wpcg.ModelConfig(**cfg))
+    for name, arr in tensors.items():
+        m.set_tensor(name, arr)
+    kern = O.KERNEL_AVX2 if O.have_avx2() else O.KERNEL_FUSED
+    ref = O.Model(cfg, tensors, cfg["max_pos"], kern, 16)
+    return m, ref
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("name,cfg,n_prompt,n_new,seed", [("dense", DENSE, 8, 64, 101),
+                                                          ("moe", MOE, 8, 64, 202),
+                                                          ("qwen3-moe-2L", QWEN3_MOE_2L, 12, 64, 303)])
+def test_exact_decode_is_bit_identical(ctx, name, cfg, n_prompt, n_new, seed):
+    print(f"[gpu] decode {name}: building", flush=True)
+    m, ref = build(ctx, cfg, seed)
+    rng = np.random.default_rng(3)
+    prompt = rng.integers(0, cfg["vocab"], n_prompt).astype(np.uint32)
+    # step by step, feeding the oracle's own greedy choice back in
+    print(f"[gpu] decode {name}: {n_prompt} prompt + {n_new} greedy steps", flush=True)
+    ids = []
+    tok = int(prompt[0])
+    for step in range(n_prompt + n_new - 1):
+        r = ref.forward_token(tok)
+        g, a = m.forward_token(tok)
+        assert np.array_equal(bits(g), bits(r)), f"{name}: logits differ at step {step}"
+        assert a == int(np.argmax(r)) or r[a] == r.max()
+        nxt = O.argmax(r)
+        assert a == nxt, f"{name}: argmax {a} vs {nxt} at step {step}"
+        if step + 1 < n_prompt:
+            tok = int(prompt[step + 1])
+        else:
+            ids.append(nxt)
+            tok = nxt
+    assert m.position() == n_prompt + n_new - 1
+    # the same greedy run entirely on the device
+    out, _ = m.generate(prompt, n_new)
+    assert list(out[: len(ids)]) == ids, f"{name}: generate() diverges from the stepwise run"
+    print(f"[gpu] decode {name}: {n_new} greedy ids identical, e.g. {ids[:8]}", flush=True)
+
+    # FAST mode: logits of the first prompt step close to EXACT's, greedy run reported
+    m.set_mode(wpcg.MODE_FAST).reset()
+    g, _ = m.forward_token(int(prompt[0]))
+    m.reset()
+    m.set_mode(wpcg.MODE_EXACT)
+    e, _ = m.forward_token(int(prompt[0]))
+    span = float(e.max() - e.min())
+    assert np.max(np.abs(g - e)) <= 1e-3 * span, f"{name}: FAST logits far from EXACT"
+    m.set_mode(wpcg.MODE_FAST)
+    fout, _ = m.generate(prompt, n_new)
+    same = int(np.argmax(np.concatenate([fout != out, [True]])))
+    print(f"[gpu] decode {name}: FAST greedy ids match EXACT for {same} of {n_new} steps", flush=True)
+    m.close()
+    ref.close()
+
+
+def test_decode_errors(ctx):
+    cfg = dict(DENSE)
+    m = wpcg.Model(ctx, 4, wpcg.ModelConfig(**cfg))
+    with pytest.raises(wpcg.WpcgError) as e:  # nothing loaded yet
+        m.forward_token(1)
+    assert e.value.code == wpcg.E_ARG and "model.embed_tokens.weight" in wpcg.last_error()
+    with pytest.raises(wpcg.WpcgError) as e:
+        m.set_tensor("model.layers.9.self_attn.q_proj.weight", np.zeros(68, np.uint8))
+    assert e.value.code == wpcg.E_NOTFOUND
+    with pytest.raises(wpcg.WpcgError) as e:
+        m.set_tensor("model.norm.weight", np.ones(3, np.float32))
+    assert e.value.code == wpcg.E_SHAPE
+    m.close()

@@ -50,6 +50,20 @@ def test_dense_exact_bit_identical_and_fast_close(ctx, out_f, in_f):
         d.close()
 
 
+@pytest.mark.parametrize("n", [1, 64, 128, 2048, 2560, 5000])
+def test_rms_norm_bit_identical(ctx, n):
+    # many scales, so the square root and the divisions see many exponents
+    print(f"[gpu] rms_norm {n}", flush=True)
+    rng = np.random.default_rng(n + 1)
+    w = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    for rep in range(40):
+        x = (rng.standard_normal(n) * np.float32(10.0 ** rng.uniform(-6, 4))).astype(np.float32)
+        got = wpcg.rms_norm(ctx, x, w, 1e-6)
+        assert same(got, O.rms_norm(x, w, 1e-6)), rep
+        fast = wpcg.rms_norm(ctx, x, w, 1e-6, wpcg.MODE_FAST)
+        assert np.allclose(fast, got, rtol=1e-5, atol=0), rep
+
+
 @pytest.mark.parametrize("n", [1, 2, 128, 1000, 4097])
 def test_softmax_bit_identical(ctx, n):
     print(f"[gpu] softmax {n}", flush=True)

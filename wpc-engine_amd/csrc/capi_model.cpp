@@ -1,0 +1,552 @@
+// The extern "C" boundary for the device-resident decode step: a dense
+// Qwen3 or Qwen3-MoE decoder whose weights, KV cache, activations, position
+// and tokens all stay on the GPU. One step (Model::forward_token,
+// model.rs:419-547; Qwen3MoeModel::forward_token, qwen3_moe_model.rs:406-542)
+// plus the greedy argmax (sampling.rs:3-14) is a fixed sequence of launches
+// that is captured once as a HIP graph and replayed per token.
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "wpcg_internal.hpp"
+
+using namespace wpcg;
+
+namespace {
+
+struct Layer {
+    float *in_ln = nullptr, *post_ln = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    wpcg_linear *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+    wpcg_linear *gate = nullptr, *up = nullptr, *down = nullptr;  // dense MLP
+    wpcg_moe* moe = nullptr;                                       // sparse MLP
+    std::vector<uint8_t> experts_set;                              // 3 bits per expert
+};
+
+}  // namespace
+
+struct wpcg_model {
+    wpcg_ctx* ctx = nullptr;
+    int scheme = 4, mode = WPCG_MODE_EXACT;
+    wpcg_model_config cfg{};
+    std::vector<Layer> layers;
+    wpcg_linear *embed = nullptr, *lm_head = nullptr;
+    float* final_norm = nullptr;
+    float *cos_t = nullptr, *sin_t = nullptr;  // [max_pos][head_dim/2]
+    float *kc = nullptr, *vc = nullptr;        // [layer][kv_head][max_pos][head_dim]
+    DecodeState* st = nullptr;
+    uint32_t* tokens = nullptr;                // [max_pos + 1]
+    float *residual = nullptr, *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
+    float *attn = nullptr, *scores = nullptr, *mlp = nullptr, *g = nullptr, *u = nullptr,
+          *h = nullptr, *logits = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    int graph_mode = -1;
+    std::vector<void*> allocs;
+};
+
+namespace {
+
+int set_dev_f32(wpcg_model* m, float** dst, const void* data, uint64_t nbytes, uint64_t n,
+                const std::string& name)
+{
+    if (nbytes != n * 4) return fail(WPCG_E_SHAPE, name + ": expected " + std::to_string(n) + " fp32 values");
+    if (!*dst) {
+        WPCG_HIP(hipMalloc(dst, n * 4));
+        m->allocs.push_back(*dst);
+    }
+    WPCG_HIP(hipMemcpy(*dst, data, nbytes, hipMemcpyHostToDevice));
+    return WPCG_OK;
+}
+
+int set_linear(wpcg_model* m, wpcg_linear** dst, const void* data, uint64_t nbytes, uint64_t out_f,
+               uint64_t in_f, const std::string& name)
+{
+    wpcg_linear* l = nullptr;
+    if (int rc = wpcg_linear_from_blocks(m->ctx, m->scheme, data, nbytes, out_f, in_f, nullptr, &l))
+        return fail(rc, name + ": " + wpcg_last_error_string());
+    l->mode = m->mode;
+    if (*dst) wpcg_linear_destroy(*dst);
+    *dst = l;
+    return WPCG_OK;
+}
+
+void free_model(wpcg_model* m)
+{
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    for (auto& L : m->layers) {
+        for (wpcg_linear* l : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down})
+            if (l) wpcg_linear_destroy(l);
+        if (L.moe) wpcg_moe_destroy(L.moe);
+    }
+    if (m->embed) wpcg_linear_destroy(m->embed);
+    if (m->lm_head) wpcg_linear_destroy(m->lm_head);
+    for (void* p : m->allocs) (void)hipFree(p);
+}
+
+void drop_graph(wpcg_model* m)
+{
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    m->exec = nullptr;
+    m->graph = nullptr;
+    m->graph_mode = -1;
+}
+
+// First missing tensor, or "" when the model is complete.
+std::string missing(const wpcg_model* m)
+{
+    const wpcg_model_config& c = m->cfg;
+    if (!m->embed) return "model.embed_tokens.weight";
+    if (!c.tied && !m->lm_head) return "lm_head.weight";
+    if (!m->final_norm) return "model.norm.weight";
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        const Layer& L = m->layers[l];
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        if (!L.in_ln) return p + "input_layernorm.weight";
+        if (!L.post_ln) return p + "post_attention_layernorm.weight";
+        if (!L.q_norm) return p + "self_attn.q_norm.weight";
+        if (!L.k_norm) return p + "self_attn.k_norm.weight";
+        if (!L.q) return p + "self_attn.q_proj.weight";
+        if (!L.k) return p + "self_attn.k_proj.weight";
+        if (!L.v) return p + "self_attn.v_proj.weight";
+        if (!L.o) return p + "self_attn.o_proj.weight";
+        if (c.n_experts == 0) {
+            if (!L.gate) return p + "mlp.gate_proj.weight";
+            if (!L.up) return p + "mlp.up_proj.weight";
+            if (!L.down) return p + "mlp.down_proj.weight";
+        } else {
+            if (!L.moe->router) return p + "mlp.gate.weight";
+            for (uint32_t e = 0; e < c.n_experts; e++)
+                if (L.experts_set[e] != 7) return p + "mlp.experts." + std::to_string(e) + ".*";
+        }
+    }
+    return "";
+}
+
+// One decode step on stream s: the token at tokens[pos] through every layer,
+// logits, argmax, position + 1.
+int enqueue_step(wpcg_model* m, hipStream_t s)
+{
+    const wpcg_model_config& c = m->cfg;
+    const int H = (int)c.hidden, hd = (int)c.head_dim, nh = (int)c.n_heads, nkv = (int)c.n_kv_heads;
+    const int qd = nh * hd, kvd = nkv * hd, mode = m->mode;
+    const float scale = 1.0f / std::sqrt((float)hd);  // model.rs: 1/sqrt(head_dim) in f32
+    WPCG_HIP(launch_embed_tok(m->embed->m, m->tokens, m->st, m->residual, s));
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        Layer& L = m->layers[l];
+        WPCG_HIP(launch_rms_norm(mode, m->residual, L.in_ln, H, c.eps, m->normed, s));
+        wpcg_linear* qkv[3] = {L.q, L.k, L.v};
+        const float* xs[3] = {m->normed, m->normed, m->normed};
+        float* ys[3] = {m->q, m->k, m->v};
+        if (int rc = wpcg_linear_matvec_multi(3, qkv, xs, ys, s)) return rc;
+        float* kc = m->kc + (size_t)l * nkv * c.max_pos * hd;
+        float* vc = m->vc + (size_t)l * nkv * c.max_pos * hd;
+        WPCG_HIP(launch_head_norm_rope(mode, m->q, m->k, m->v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps,
+                                       m->cos_t, m->sin_t, m->st, kc, vc, s));
+        WPCG_HIP(launch_attention(mode, m->q, kc, vc, nh, nkv, hd, (int)c.max_pos, scale, m->st,
+                                  m->scores, m->attn, s));
+        // residual += o_proj(attn): the residual is the GEMV's bias and output
+        {
+            float* saved = L.o->bias;
+            L.o->bias = m->residual;
+            const int rc = wpcg_linear_matvec(L.o, m->attn, m->residual, s);
+            L.o->bias = saved;
+            if (rc) return rc;
+        }
+        WPCG_HIP(launch_rms_norm(mode, m->residual, L.post_ln, H, c.eps, m->normed, s));
+        if (c.n_experts) {
+            if (int rc = wpcg_moe_forward(L.moe, m->normed, m->mlp, nullptr, nullptr, s)) return rc;
+            WPCG_HIP(launch_add(m->residual, m->mlp, H, s));
+        } else {
+            wpcg_linear* gu[2] = {L.gate, L.up};
+            const float* x2[2] = {m->normed, m->normed};
+            float* y2[2] = {m->g, m->u};
+            if (int rc = wpcg_linear_matvec_multi(2, gu, x2, y2, s)) return rc;
+            WPCG_HIP(launch_silu_mul(m->g, m->u, m->h, c.inter, s));
+            float* saved = L.down->bias;
+            L.down->bias = m->residual;
+            const int rc = wpcg_linear_matvec(L.down, m->h, m->residual, s);
+            L.down->bias = saved;
+            if (rc) return rc;
+        }
+        (void)qd;
+        (void)kvd;
+    }
+    WPCG_HIP(launch_rms_norm(mode, m->residual, m->final_norm, H, c.eps, m->normed, s));
+    wpcg_linear* head = c.tied ? m->embed : m->lm_head;
+    if (int rc = wpcg_linear_matvec(head, m->normed, m->logits, s)) return rc;
+    WPCG_HIP(launch_argmax_next(m->logits, (int)c.vocab, m->st, m->tokens, s));
+    return WPCG_OK;
+}
+
+int ensure_graph(wpcg_model* m)
+{
+    if (m->exec && m->graph_mode == m->mode) return WPCG_OK;
+    drop_graph(m);
+    hipStream_t s = m->ctx->stream;
+    WPCG_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    const int rc = enqueue_step(m, s);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc != WPCG_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+    }
+    if (e != hipSuccess) return hip_fail(e, "capture of the decode step");
+    m->graph = g;
+    WPCG_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+    m->graph_mode = m->mode;
+    return WPCG_OK;
+}
+
+int ready(wpcg_model* m)
+{
+    const std::string miss = missing(m);
+    if (!miss.empty()) return fail(WPCG_E_ARG, "tensor not set: " + miss);
+    if (int rc = check_ctx(m->ctx)) return rc;
+    return ensure_graph(m);
+}
+
+}  // namespace
+
+extern "C" {
+
+int wpcg_rms_norm(wpcg_ctx* ctx, const float* x_dev, const float* w_dev, uint32_t n, float eps,
+                  float* out_dev, int mode, wpcg_stream stream)
+{
+    if (!x_dev || !w_dev || !out_dev) return fail(WPCG_E_ARG, "null argument");
+    if (n == 0) return fail(WPCG_E_ARG, "empty vector");
+    if (mode != WPCG_MODE_EXACT && mode != WPCG_MODE_FAST) return fail(WPCG_E_ARG, "bad mode");
+    if (int rc = check_ctx(ctx)) return rc;
+    WPCG_HIP(launch_rms_norm(mode, x_dev, w_dev, (int)n, eps, out_dev, pick(ctx, stream)));
+    return WPCG_OK;
+}
+
+int wpcg_model_create(wpcg_ctx* ctx, int scheme, const wpcg_model_config* cfg, wpcg_model** out)
+{
+    if (!out) return fail(WPCG_E_ARG, "null output");
+    *out = nullptr;
+    if (!cfg) return fail(WPCG_E_ARG, "null config");
+    if (scheme != WPCG_SCHEME_V3 && scheme != WPCG_SCHEME_V4) return fail(WPCG_E_ARG, "scheme must be 3 or 4");
+    const wpcg_model_config& c = *cfg;
+    if (!c.n_layers || !c.hidden || !c.n_heads || !c.n_kv_heads || !c.head_dim || !c.vocab || !c.max_pos)
+        return fail(WPCG_E_ARG, "every size in the config must be positive");
+    if (c.n_heads % c.n_kv_heads || c.head_dim % 2 || c.head_dim > 256)
+        return fail(WPCG_E_SHAPE, "n_heads must be a multiple of n_kv_heads; head_dim even, <= 256");
+    if (c.hidden % 128 || (c.n_heads * c.head_dim) % 128 || (c.n_experts == 0 && c.inter % 128))
+        return fail(WPCG_E_SHAPE, "matrix input sizes must be multiples of 128");
+    if (c.n_experts == 0 && !c.inter) return fail(WPCG_E_ARG, "dense model needs intermediate_size");
+    if (int rc = check_ctx(ctx)) return rc;
+    std::unique_ptr<wpcg_model> m(new (std::nothrow) wpcg_model);
+    if (!m) return fail(WPCG_E_NOMEM, "model allocation");
+    m->ctx = ctx;
+    m->scheme = scheme;
+    m->cfg = c;
+    m->layers.resize(c.n_layers);
+    int rc = WPCG_OK;
+    for (uint32_t l = 0; l < c.n_layers && rc == WPCG_OK && c.n_experts; l++) {
+        rc = wpcg_moe_create(ctx, scheme, c.n_experts, c.hidden, c.moe_inter, c.top_k, c.norm_topk,
+                             &m->layers[l].moe);
+        m->layers[l].experts_set.assign(c.n_experts, 0);
+    }
+    const size_t hd = c.head_dim, half = hd / 2, qd = c.n_heads * hd, kvd = c.n_kv_heads * hd;
+    const size_t inter = c.n_experts ? c.moe_inter : c.inter;
+    auto dev = [&](void** p, size_t bytes) {
+        if (rc != WPCG_OK) return;
+        hipError_t e = hipMalloc(p, std::max<size_t>(bytes, 4));
+        if (e != hipSuccess) {
+            rc = hip_fail(e, "model workspace");
+            return;
+        }
+        m->allocs.push_back(*p);
+    };
+    dev((void**)&m->cos_t, (size_t)c.max_pos * half * 4);
+    dev((void**)&m->sin_t, (size_t)c.max_pos * half * 4);
+    const size_t cache = (size_t)c.n_layers * kvd * c.max_pos * 4;
+    dev((void**)&m->kc, cache);
+    dev((void**)&m->vc, cache);
+    dev((void**)&m->st, sizeof(DecodeState));
+    dev((void**)&m->tokens, ((size_t)c.max_pos + 1) * 4);
+    dev((void**)&m->residual, c.hidden * 4u);
+    dev((void**)&m->normed, c.hidden * 4u);
+    dev((void**)&m->q, qd * 4);
+    dev((void**)&m->k, kvd * 4);
+    dev((void**)&m->v, kvd * 4);
+    dev((void**)&m->attn, qd * 4);
+    dev((void**)&m->scores, (size_t)c.n_heads * c.max_pos * 4);
+    dev((void**)&m->mlp, c.hidden * 4u);
+    dev((void**)&m->g, inter * 4);
+    dev((void**)&m->u, inter * 4);
+    dev((void**)&m->h, inter * 4);
+    dev((void**)&m->logits, (size_t)c.vocab * 4);
+    if (rc == WPCG_OK) {
+        // RoPE angles as rope.rs:29-33 computes them: f64 pow, sin, cos, cast to f32
+        std::vector<float> cs((size_t)c.max_pos * half), sn((size_t)c.max_pos * half);
+        for (size_t p = 0; p < c.max_pos; p++)
+            for (size_t i = 0; i < half; i++) {
+                const double inv_freq = std::pow(c.rope_theta, -(2.0 * (double)i) / (double)hd);
+                const double angle = (double)p * inv_freq;
+                cs[p * half + i] = (float)std::cos(angle);
+                sn[p * half + i] = (float)std::sin(angle);
+            }
+        hipError_t e = hipMemcpy(m->cos_t, cs.data(), cs.size() * 4, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemcpy(m->sin_t, sn.data(), sn.size() * 4, hipMemcpyHostToDevice);
+        DecodeState st{0, 0, c.max_pos, 0};
+        if (e == hipSuccess) e = hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice);
+        if (e != hipSuccess) rc = hip_fail(e, "model tables");
+    }
+    if (rc != WPCG_OK) {
+        free_model(m.get());
+        return rc;
+    }
+    ctx_retain(ctx);
+    *out = m.release();
+    return WPCG_OK;
+}
+
+int wpcg_model_destroy(wpcg_model* m)
+{
+    if (!m) return WPCG_OK;
+    (void)hipSetDevice(m->ctx->device);
+    (void)hipStreamSynchronize(m->ctx->stream);
+    free_model(m);
+    ctx_release(m->ctx);
+    delete m;
+    return WPCG_OK;
+}
+
+int wpcg_model_set_tensor(wpcg_model* m, const char* name_c, const void* data, uint64_t nbytes)
+{
+    if (!m || !name_c || !data) return fail(WPCG_E_ARG, "null argument");
+    if (int rc = check_ctx(m->ctx)) return rc;
+    drop_graph(m);
+    const wpcg_model_config& c = m->cfg;
+    const std::string name(name_c);
+    const uint64_t qd = (uint64_t)c.n_heads * c.head_dim, kvd = (uint64_t)c.n_kv_heads * c.head_dim;
+    if (name == "model.embed_tokens.weight") return set_linear(m, &m->embed, data, nbytes, c.vocab, c.hidden, name);
+    if (name == "lm_head.weight") return set_linear(m, &m->lm_head, data, nbytes, c.vocab, c.hidden, name);
+    if (name == "model.norm.weight") return set_dev_f32(m, &m->final_norm, data, nbytes, c.hidden, name);
+    const std::string pre = "model.layers.";
+    if (name.compare(0, pre.size(), pre) != 0) return fail(WPCG_E_NOTFOUND, "unknown tensor " + name);
+    size_t dot = name.find('.', pre.size());
+    if (dot == std::string::npos) return fail(WPCG_E_NOTFOUND, "unknown tensor " + name);
+    uint32_t l = 0;
+    try {
+        l = (uint32_t)std::stoul(name.substr(pre.size(), dot - pre.size()));
+    } catch (...) {
+        return fail(WPCG_E_NOTFOUND, "unknown tensor " + name);
+    }
+    if (l >= c.n_layers) return fail(WPCG_E_NOTFOUND, "layer out of range: " + name);
+    Layer& L = m->layers[l];
+    const std::string t = name.substr(dot + 1);
+    if (t == "input_layernorm.weight") return set_dev_f32(m, &L.in_ln, data, nbytes, c.hidden, name);
+    if (t == "post_attention_layernorm.weight") return set_dev_f32(m, &L.post_ln, data, nbytes, c.hidden, name);
+    if (t == "self_attn.q_norm.weight") return set_dev_f32(m, &L.q_norm, data, nbytes, c.head_dim, name);
+    if (t == "self_attn.k_norm.weight") return set_dev_f32(m, &L.k_norm, data, nbytes, c.head_dim, name);
+    if (t == "self_attn.q_proj.weight") return set_linear(m, &L.q, data, nbytes, qd, c.hidden, name);
+    if (t == "self_attn.k_proj.weight") return set_linear(m, &L.k, data, nbytes, kvd, c.hidden, name);
+    if (t == "self_attn.v_proj.weight") return set_linear(m, &L.v, data, nbytes, kvd, c.hidden, name);
+    if (t == "self_attn.o_proj.weight") return set_linear(m, &L.o, data, nbytes, c.hidden, qd, name);
+    if (c.n_experts == 0) {
+        if (t == "mlp.gate_proj.weight") return set_linear(m, &L.gate, data, nbytes, c.inter, c.hidden, name);
+        if (t == "mlp.up_proj.weight") return set_linear(m, &L.up, data, nbytes, c.inter, c.hidden, name);
+        if (t == "mlp.down_proj.weight") return set_linear(m, &L.down, data, nbytes, c.hidden, c.inter, name);
+        return fail(WPCG_E_NOTFOUND, "unknown tensor " + name);
+    }
+    if (t == "mlp.gate.weight") {
+        if (nbytes != (uint64_t)c.n_experts * c.hidden * 4)
+            return fail(WPCG_E_SHAPE, name + ": expected [n_experts, hidden] fp32");
+        return wpcg_moe_set_router(L.moe, static_cast<const float*>(data));
+    }
+    const std::string ep = "mlp.experts.";
+    if (t.compare(0, ep.size(), ep) == 0) {
+        const size_t d2 = t.find('.', ep.size());
+        if (d2 == std::string::npos) return fail(WPCG_E_NOTFOUND, "unknown tensor " + name);
+        uint32_t e = 0;
+        try {
+            e = (uint32_t)std::stoul(t.substr(ep.size(), d2 - ep.size()));
+        } catch (...) {
+            return fail(WPCG_E_NOTFOUND, "unknown tensor " + name);
+        }
+        if (e >= c.n_experts) return fail(WPCG_E_NOTFOUND, "expert out of range: " + name);
+        const std::string proj = t.substr(d2 + 1);
+        wpcg_moe* moe = L.moe;
+        const uint64_t bpb = block_bytes(m->scheme);
+        DeviceMatrix* dm = nullptr;
+        int bit = 0;
+        if (proj == "gate_proj.weight") { dm = &moe->gate; bit = 1; }
+        else if (proj == "up_proj.weight") { dm = &moe->up; bit = 2; }
+        else if (proj == "down_proj.weight") { dm = &moe->down; bit = 4; }
+        else return fail(WPCG_E_NOTFOUND, "unknown tensor " + name);
+        if (nbytes != dm->rows * dm->nb * bpb)  // WpcLinearV4::new's block-count assert
+            return fail(WPCG_E_SHAPE, name + ": block count does not match the expert shape");
+        if (int rc = upload_rows(m->ctx, static_cast<const uint8_t*>(data), *dm, e * (dm->rows_pad / TILE_ROWS)))
+            return rc;
+        L.experts_set[e] |= (uint8_t)bit;
+        return WPCG_OK;
+    }
+    return fail(WPCG_E_NOTFOUND, "unknown tensor " + name);
+}
+
+int wpcg_model_load_artifact(wpcg_model* m, wpcg_artifact* a)
+{
+    if (!m || !a) return fail(WPCG_E_ARG, "null argument");
+    if (a->scheme != m->scheme) return fail(WPCG_E_ARG, "artifact scheme differs from the model's");
+    std::vector<std::string> names = {"model.embed_tokens.weight"};
+    if (!m->cfg.tied) names.push_back("lm_head.weight");
+    for (uint32_t l = 0; l < m->cfg.n_layers; l++) {
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        for (const char* t : {"self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+                              "self_attn.o_proj.weight"})
+            names.push_back(p + t);
+        if (m->cfg.n_experts == 0) {
+            for (const char* t : {"mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight"})
+                names.push_back(p + t);
+        } else {
+            for (uint32_t e = 0; e < m->cfg.n_experts; e++)
+                for (const char* t : {"gate_proj.weight", "up_proj.weight", "down_proj.weight"})
+                    names.push_back(p + "mlp.experts." + std::to_string(e) + "." + t);
+        }
+    }
+    for (const std::string& n : names) {
+        const void* bytes = nullptr;
+        uint64_t size = 0;
+        if (int rc = wpcg_artifact_tensor(a, n.c_str(), &bytes, &size)) return rc;
+        if (int rc = wpcg_model_set_tensor(m, n.c_str(), bytes, size)) return rc;
+    }
+    return WPCG_OK;
+}
+
+int wpcg_model_set_mode(wpcg_model* m, int mode)
+{
+    if (!m || (mode != WPCG_MODE_EXACT && mode != WPCG_MODE_FAST)) return fail(WPCG_E_ARG, "null model or bad mode");
+    m->mode = mode;
+    auto lin = [mode](wpcg_linear* l) { if (l) l->mode = mode; };
+    lin(m->embed);
+    lin(m->lm_head);
+    for (auto& L : m->layers) {
+        for (wpcg_linear* l : {L.q, L.k, L.v, L.o, L.gate, L.up, L.down}) lin(l);
+        if (L.moe) wpcg_moe_set_mode(L.moe, mode);
+    }
+    return WPCG_OK;
+}
+
+int wpcg_model_reset(wpcg_model* m)
+{
+    if (!m) return fail(WPCG_E_ARG, "null model");
+    if (int rc = check_ctx(m->ctx)) return rc;
+    DecodeState st{0, 0, m->cfg.max_pos, 0};
+    WPCG_HIP(hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice));
+    return WPCG_OK;
+}
+
+int wpcg_model_position(wpcg_model* m, uint32_t* pos)
+{
+    if (!m || !pos) return fail(WPCG_E_ARG, "null argument");
+    if (int rc = check_ctx(m->ctx)) return rc;
+    DecodeState st;
+    WPCG_HIP(hipStreamSynchronize(m->ctx->stream));
+    WPCG_HIP(hipMemcpy(&st, m->st, sizeof st, hipMemcpyDeviceToHost));
+    *pos = st.pos;
+    return WPCG_OK;
+}
+
+int wpcg_model_forward_token(wpcg_model* m, uint32_t token, float* logits, uint32_t* argmax)
+{
+    if (!m) return fail(WPCG_E_ARG, "null model");
+    if (token >= m->cfg.vocab) return fail(WPCG_E_ARG, "token id out of range");
+    if (int rc = ready(m)) return rc;
+    hipStream_t s = m->ctx->stream;
+    DecodeState st;
+    WPCG_HIP(hipStreamSynchronize(s));
+    WPCG_HIP(hipMemcpy(&st, m->st, sizeof st, hipMemcpyDeviceToHost));
+    if (st.pos >= m->cfg.max_pos) return fail(WPCG_E_ARG, "KV cache full (max_pos reached)");
+    // every token comes from the host: keep the argmax out of tokens[]
+    st.n_prompt = 0xffffffffu;
+    WPCG_HIP(hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice));
+    WPCG_HIP(hipMemcpy(m->tokens + st.pos, &token, 4, hipMemcpyHostToDevice));
+    WPCG_HIP(hipGraphLaunch(m->exec, s));
+    WPCG_HIP(hipStreamSynchronize(s));
+    if (logits) WPCG_HIP(hipMemcpy(logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost));
+    if (argmax) {
+        WPCG_HIP(hipMemcpy(&st, m->st, sizeof st, hipMemcpyDeviceToHost));
+        *argmax = st.last;
+    }
+    return WPCG_OK;
+}
+
+int wpcg_model_debug_read(wpcg_model* m, int which, float* out, uint64_t n)
+{
+    if (!m || !out) return fail(WPCG_E_ARG, "null argument");
+    const wpcg_model_config& c = m->cfg;
+    const uint64_t qd = (uint64_t)c.n_heads * c.head_dim, kvd = (uint64_t)c.n_kv_heads * c.head_dim;
+    const float* src = nullptr;
+    uint64_t len = 0;
+    switch (which) {
+        case 0: src = m->residual; len = c.hidden; break;
+        case 1: src = m->normed; len = c.hidden; break;
+        case 2: src = m->q; len = qd; break;
+        case 3: src = m->k; len = kvd; break;
+        case 4: src = m->v; len = kvd; break;
+        case 5: src = m->attn; len = qd; break;
+        case 6: src = m->scores; len = (uint64_t)c.n_heads * c.max_pos; break;
+        case 7: src = m->logits; len = c.vocab; break;
+        case 8: src = m->mlp; len = c.hidden; break;
+        case 9: src = m->kc; len = (uint64_t)c.n_layers * kvd * c.max_pos; break;
+        case 10: src = m->vc; len = (uint64_t)c.n_layers * kvd * c.max_pos; break;
+        default: return fail(WPCG_E_ARG, "unknown buffer");
+    }
+    if (n > len) return fail(WPCG_E_ARG, "buffer holds " + std::to_string(len) + " floats");
+    if (int rc = check_ctx(m->ctx)) return rc;
+    WPCG_HIP(hipStreamSynchronize(m->ctx->stream));
+    WPCG_HIP(hipMemcpy(out, src, n * 4, hipMemcpyDeviceToHost));
+    return WPCG_OK;
+}
+
+int wpcg_model_generate(wpcg_model* m, const uint32_t* prompt, uint32_t n_prompt, uint32_t n_new,
+                        uint32_t* out, float* decode_ms)
+{
+    if (!m || !prompt || !out) return fail(WPCG_E_ARG, "null argument");
+    if (n_prompt == 0 || n_new == 0) return fail(WPCG_E_ARG, "need a prompt and at least one new token");
+    if ((uint64_t)n_prompt + n_new - 1 > m->cfg.max_pos) return fail(WPCG_E_ARG, "prompt + new tokens exceed max_pos");
+    for (uint32_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= m->cfg.vocab) return fail(WPCG_E_ARG, "prompt token id out of range");
+    if (int rc = ready(m)) return rc;
+    hipStream_t s = m->ctx->stream;
+    WPCG_HIP(hipStreamSynchronize(s));
+    DecodeState st{0, n_prompt, m->cfg.max_pos, 0};
+    WPCG_HIP(hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice));
+    WPCG_HIP(hipMemcpy(m->tokens, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice));
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    WPCG_HIP(hipEventCreate(&e0));
+    WPCG_HIP(hipEventCreate(&e1));
+    int rc = WPCG_OK;
+    // steps at positions 0..n_prompt-1 consume the prompt (the last one
+    // yields the first new token); the n_new-1 after it are pure decode
+    for (uint32_t i = 0; i < n_prompt + n_new - 1 && rc == WPCG_OK; i++) {
+        if (i == n_prompt) (void)hipEventRecord(e0, s);
+        const hipError_t e = hipGraphLaunch(m->exec, s);
+        if (e != hipSuccess) rc = hip_fail(e, "hipGraphLaunch");
+    }
+    (void)hipEventRecord(e1, s);
+    if (rc == WPCG_OK) {
+        const hipError_t e = hipEventSynchronize(e1);
+        if (e != hipSuccess) rc = hip_fail(e, "decode");
+    }
+    if (rc == WPCG_OK && decode_ms) {
+        float ms = 0.0f;
+        if (n_new > 1 && hipEventElapsedTime(&ms, e0, e1) != hipSuccess) ms = 0.0f;
+        *decode_ms = ms;
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (rc != WPCG_OK) return rc;
+    WPCG_HIP(hipMemcpy(out, m->tokens + n_prompt, (size_t)n_new * 4, hipMemcpyDeviceToHost));
+    return WPCG_OK;
+}
+
+}  // extern "C"

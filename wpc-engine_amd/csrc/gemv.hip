@@ -551,6 +551,24 @@ __global__ __launch_bounds__(256) void k_embed(const uint8_t* __restrict__ codes
     out[k] = __fadd_rn(h2f(p & 0xFFFFu), __fmul_rn((float)code, h2f(p >> 16)));
 }
 
+// The embedding row of the decode step's input token, tokens[st->pos].
+template <int SCHEME>
+__global__ __launch_bounds__(256) void k_embed_tok(const uint8_t* __restrict__ codes,
+                                                   const uint8_t* __restrict__ hp,
+                                                   const uint32_t* __restrict__ params,
+                                                   float* __restrict__ out,
+                                                   const uint32_t* __restrict__ tokens,
+                                                   const DecodeState* __restrict__ st, int nb,
+                                                   uint32_t rows)
+{
+    const int k = blockIdx.x * 256 + threadIdx.x;
+    if (k >= nb * 128) return;
+    const uint32_t row = min(tokens[st->pos], rows - 1);  // ids are checked on the host
+    const uint32_t code = code_at(codes, hp, row, (size_t)(k >> 7), nb, k & 127, SCHEME);
+    const uint32_t p = params[param_idx(row, nb, k >> 7)];
+    out[k] = __fadd_rn(h2f(p & 0xFFFFu), __fmul_rn((float)code, h2f(p >> 16)));
+}
+
 template <int SCHEME>
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ codes,
                                                  const uint8_t* __restrict__ hp,
@@ -648,6 +666,20 @@ hipError_t launch_embed(const DeviceMatrix& m, uint32_t row, float* out, hipStre
     else
         hipLaunchKernelGGL(k_embed<3>, grid, dim3(256), 0, s, m.codes, m.hp, m.params, out,
                            (size_t)row, (int)m.nb);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_tok(const DeviceMatrix& m, const uint32_t* tokens, const DecodeState* st,
+                            float* out, hipStream_t s)
+{
+    dim3 grid((unsigned)((m.cols + 255) / 256));
+    (void)hipGetLastError();  // report only this launch
+    if (m.scheme == 4)
+        hipLaunchKernelGGL(k_embed_tok<4>, grid, dim3(256), 0, s, m.codes, m.hp, m.params, out, tokens,
+                           st, (int)m.nb, (uint32_t)m.rows);
+    else
+        hipLaunchKernelGGL(k_embed_tok<3>, grid, dim3(256), 0, s, m.codes, m.hp, m.params, out, tokens,
+                           st, (int)m.nb, (uint32_t)m.rows);
     return hipGetLastError();
 }
 

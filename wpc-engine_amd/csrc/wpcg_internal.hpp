@@ -141,6 +141,28 @@ hipError_t launch_silu_mul(const float* g, const float* u, float* out, size_t n,
 hipError_t launch_combine(const float* ys, const int32_t* ids, const float* w, int top_k,
                           float* out, int h, hipStream_t s);
 
+// ---- decode step (decode.hip) ----------------------------------------------
+// Device-resident position and token bookkeeping of a decode: the step at
+// position `pos` reads tokens[pos]; its argmax is `last`, and is written to
+// tokens[pos+1] when pos+1 >= n_prompt (a generated token).
+struct DecodeState {
+    uint32_t pos, n_prompt, max_pos, last;
+};
+hipError_t launch_embed_tok(const DeviceMatrix& m, const uint32_t* tokens, const DecodeState* st,
+                            float* out, hipStream_t s);
+hipError_t launch_rms_norm(int mode, const float* x, const float* w, int n, float eps, float* out,
+                           hipStream_t s);
+hipError_t launch_head_norm_rope(int mode, float* q, const float* k, const float* v, const float* qn,
+                                 const float* kn, int nh, int nkv, int hd, float eps,
+                                 const float* cos_t, const float* sin_t, const DecodeState* st,
+                                 float* kc, float* vc, hipStream_t s);
+hipError_t launch_attention(int mode, const float* q, const float* kc, const float* vc, int nh,
+                            int nkv, int hd, int max_pos, float scale, const DecodeState* st,
+                            float* scores, float* out, hipStream_t s);
+hipError_t launch_add(float* x, const float* y, int n, hipStream_t s);
+hipError_t launch_argmax_next(const float* logits, int n, DecodeState* st, uint32_t* tokens,
+                              hipStream_t s);
+
 // ---- minimal JSON (for model_v{3,4}.meta) ---------------------------------
 struct MetaEntry {
     std::vector<uint64_t> shape;

@@ -89,6 +89,18 @@ _SIGS = {
     "wpcg_linear_dequant": (C.c_int, [_p, C.c_int, _p, _p]),
     "wpcg_linear_clone": (C.c_int, [_p, _pp]),
     "wpcg_linear_matvec_multi": (C.c_int, [C.c_int, _pp, _pp, _pp, _p]),
+    "wpcg_encode": (C.c_int, [C.c_int, _p, _u64, _p]),
+    "wpcg_model_create": (C.c_int, [_p, C.c_int, _p, _pp]),
+    "wpcg_model_destroy": (C.c_int, [_p]),
+    "wpcg_model_set_tensor": (C.c_int, [_p, C.c_char_p, _p, _u64]),
+    "wpcg_model_load_artifact": (C.c_int, [_p, _p]),
+    "wpcg_model_set_mode": (C.c_int, [_p, C.c_int]),
+    "wpcg_model_reset": (C.c_int, [_p]),
+    "wpcg_model_position": (C.c_int, [_p, C.POINTER(C.c_uint32)]),
+    "wpcg_model_forward_token": (C.c_int, [_p, C.c_uint32, _p, C.POINTER(C.c_uint32)]),
+    "wpcg_model_generate": (C.c_int, [_p, _p, C.c_uint32, C.c_uint32, _p, C.POINTER(C.c_float)]),
+    "wpcg_model_debug_read": (C.c_int, [_p, C.c_int, _p, _u64]),
+    "wpcg_rms_norm": (C.c_int, [_p, _p, _p, C.c_uint32, C.c_float, _p, C.c_int, _p]),
     "wpcg_dense_create": (C.c_int, [_p, _p, _u64, _u64, _p, _pp]),
     "wpcg_dense_destroy": (C.c_int, [_p]),
     "wpcg_dense_set_mode": (C.c_int, [_p, C.c_int]),
@@ -522,6 +534,16 @@ def softmax(ctx: Context, x) -> np.ndarray:
     return b.read(np.float32, x.size)
 
 
+def rms_norm(ctx: Context, x, w, eps: float, mode: int = MODE_EXACT) -> np.ndarray:
+    """rms_norm (norm.rs:4-13) on the GPU, returned to the host."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    xb, wb, ob = ctx.upload(x), ctx.upload(w), ctx.alloc(4 * x.size)
+    check(lib.wpcg_rms_norm(ctx.h, xb.ptr, wb.ptr, x.size, eps, ob.ptr, mode, None))
+    ctx.sync()
+    return ob.read(np.float32, x.size)
+
+
 def route(ctx: Context, probs, top_k: int, norm_topk: bool = True):
     """Qwen3MoeModel::route (qwen3_moe_model.rs:376-402) on the GPU:
     (ids int32[top_k], weights float32[top_k])."""
@@ -588,6 +610,95 @@ class MoeLayer:
     def close(self):
         if self.h:
             lib.wpcg_moe_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------------ encoder
+def encode(scheme: int, w) -> np.ndarray:
+    """encode_tensor_v{4,3} (quant_encoder.rs): fp32 values (a multiple of
+    128) to reference blocks, on the host."""
+    w = np.ascontiguousarray(w, np.float32).ravel()
+    out = np.empty(w.size // 128 * (68 if scheme == SCHEME_V4 else 100), np.uint8)
+    check(lib.wpcg_encode(scheme, _np_ptr(w), w.size, _np_ptr(out)))
+    return out
+
+
+# ------------------------------------------------------------------ decode
+class ModelConfig(C.Structure):
+    """wpcg_model_config (include/wpcg.h)."""
+    _fields_ = [("n_layers", C.c_uint32), ("hidden", C.c_uint32), ("n_heads", C.c_uint32),
+                ("n_kv_heads", C.c_uint32), ("head_dim", C.c_uint32), ("inter", C.c_uint32),
+                ("vocab", C.c_uint32), ("n_experts", C.c_uint32), ("top_k", C.c_uint32),
+                ("moe_inter", C.c_uint32), ("norm_topk", C.c_int32), ("tied", C.c_int32),
+                ("max_pos", C.c_uint32), ("eps", C.c_float), ("rope_theta", C.c_double)]
+
+    def as_dict(self):
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
+class Model:
+    """Dense Qwen3 / Qwen3-MoE decoder resident on the GPU
+    (Model::forward_token, model.rs:419-547; qwen3_moe_model.rs:406-542)."""
+
+    def __init__(self, ctx: Context, scheme: int, cfg: ModelConfig):
+        self.ctx, self.scheme, self.cfg = ctx, scheme, cfg
+        h = C.c_void_p()
+        check(lib.wpcg_model_create(ctx.h if ctx else None, scheme, C.byref(cfg), C.byref(h)))
+        self.h = h
+
+    def set_tensor(self, name: str, data: np.ndarray):
+        data = np.ascontiguousarray(data)
+        check(lib.wpcg_model_set_tensor(self.h, name.encode(), _np_ptr(data), data.nbytes))
+        return self
+
+    def load_artifact(self, data: "WpcModelData"):
+        check(lib.wpcg_model_load_artifact(self.h, data.h))
+        return self
+
+    def set_mode(self, mode: int):
+        check(lib.wpcg_model_set_mode(self.h, mode))
+        return self
+
+    def reset(self):
+        check(lib.wpcg_model_reset(self.h))
+        return self
+
+    def position(self) -> int:
+        p = C.c_uint32()
+        check(lib.wpcg_model_position(self.h, C.byref(p)))
+        return p.value
+
+    def forward_token(self, token: int, want_logits: bool = True):
+        """(logits float32[vocab] or None, argmax)"""
+        logits = np.empty(self.cfg.vocab, np.float32) if want_logits else None
+        a = C.c_uint32()
+        check(lib.wpcg_model_forward_token(self.h, token, None if logits is None else _np_ptr(logits),
+                                           C.byref(a)))
+        return logits, a.value
+
+    def generate(self, prompt, n_new: int):
+        """(new token ids uint32[n_new], ms of the n_new-1 steps after the prompt)"""
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.empty(n_new, np.uint32)
+        ms = C.c_float()
+        check(lib.wpcg_model_generate(self.h, _np_ptr(p), p.size, n_new, _np_ptr(out), C.byref(ms)))
+        return out, ms.value
+
+    def debug_read(self, which: int, n: int) -> np.ndarray:
+        """A device buffer of the last step (see wpcg_model_debug_read)."""
+        out = np.empty(n, np.float32)
+        check(lib.wpcg_model_debug_read(self.h, which, _np_ptr(out), n))
+        return out
+
+    def close(self):
+        if self.h:
+            lib.wpcg_model_destroy(self.h)
             self.h = None
 
     def __del__(self):

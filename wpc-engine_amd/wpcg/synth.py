@@ -111,3 +111,51 @@ def write_artifact(out_dir: str, scheme: int, tensors, sort: bool = True) -> dic
     with open(os.path.join(out_dir, f"model_v{scheme}.meta"), "w") as f:
         json.dump(meta, f, indent=2)
     return meta
+
+
+def model_tensors(cfg, scheme: int, seed: int, encode, std: float = 0.02, share_experts: bool = False):
+    """Seeded synthetic weights of a dense Qwen3 / Qwen3-MoE decoder, by the
+    reference's tensor names: every matrix ~N(0, std) then encoded with
+    `encode(scheme, w)` (the artifact compiler's encoder), norms 1.0, the
+    MoE router fp32 ~N(0, std). cfg: wpcg.ModelConfig or a dict of its fields.
+    With share_experts, every layer gets the same expert blocks (distinct
+    routers): one layer's worth of generation for a large model.
+    Yields (name, array)."""
+    c = cfg if isinstance(cfg, dict) else cfg.as_dict()
+    rng = np.random.default_rng(seed)
+    H, hd, V = c["hidden"], c["head_dim"], c["vocab"]
+    qd, kvd = c["n_heads"] * hd, c["n_kv_heads"] * hd
+
+    def mat(rows, cols):
+        return encode(scheme, (rng.standard_normal(rows * cols, dtype=np.float32) * np.float32(std)))
+
+    ones_h = np.ones(H, np.float32)
+    yield "model.embed_tokens.weight", mat(V, H)
+    if not c["tied"]:
+        yield "lm_head.weight", mat(V, H)
+    yield "model.norm.weight", ones_h
+    shared = None
+    for l in range(c["n_layers"]):
+        p = f"model.layers.{l}."
+        yield p + "input_layernorm.weight", ones_h
+        yield p + "post_attention_layernorm.weight", ones_h
+        yield p + "self_attn.q_norm.weight", np.ones(hd, np.float32)
+        yield p + "self_attn.k_norm.weight", np.ones(hd, np.float32)
+        yield p + "self_attn.q_proj.weight", mat(qd, H)
+        yield p + "self_attn.k_proj.weight", mat(kvd, H)
+        yield p + "self_attn.v_proj.weight", mat(kvd, H)
+        yield p + "self_attn.o_proj.weight", mat(H, qd)
+        if c["n_experts"] == 0:
+            I = c["inter"]
+            yield p + "mlp.gate_proj.weight", mat(I, H)
+            yield p + "mlp.up_proj.weight", mat(I, H)
+            yield p + "mlp.down_proj.weight", mat(H, I)
+        else:
+            I, E = c["moe_inter"], c["n_experts"]
+            yield p + "mlp.gate.weight", (rng.standard_normal((E, H), dtype=np.float32) * np.float32(std))
+            if shared is None or not share_experts:
+                shared = [(mat(I, H), mat(I, H), mat(H, I)) for _ in range(E)]
+            for e, (g, u, d) in enumerate(shared):
+                yield p + f"mlp.experts.{e}.gate_proj.weight", g
+                yield p + f"mlp.experts.{e}.up_proj.weight", u
+                yield p + f"mlp.experts.{e}.down_proj.weight", d
