@@ -278,6 +278,10 @@ int wpcg_model_set_tensor(wpcg_model* m, const char* name, const void* data, uin
  * which the reference reads from safetensors, go through set_tensor). */
 int wpcg_model_load_artifact(wpcg_model* m, wpcg_artifact* a);
 int wpcg_model_set_mode(wpcg_model* m, int mode);
+/* Steps as one replayed HIP graph (enabled, the default) or enqueued launch
+ * by launch (for tools that cannot trace graph replays). No reference
+ * counterpart. */
+int wpcg_model_set_graphs(wpcg_model* m, int enabled);
 /* Empty the KV cache (position 0). */
 int wpcg_model_reset(wpcg_model* m);
 int wpcg_model_position(wpcg_model* m, uint32_t* pos);
@@ -295,10 +299,9 @@ int wpcg_model_generate(wpcg_model* m, const uint32_t* prompt, uint32_t n_prompt
 
 /* Diagnostics, no reference counterpart: copies n floats of one of the
  * decode step's device buffers as the last step left them. which: 0
- * residual, 1 normed (after the final norm), 2 q (normed, rotated), 3 k and
- * 4 v (the last layer's projections), 5 attention output, 6 attention
- * weights [n_heads][max_pos], 7 logits, 8 MoE output, 9 K cache, 10 V cache
- * ([layer][kv_head][max_pos][head_dim]). */
+ * residual, 1 normed (after the final norm), 2 q (the projection), 3 k and
+ * 4 v (the last layer's projections), 5 attention output, 7 logits, 9 K
+ * cache, 10 V cache ([layer][kv_head][max_pos][head_dim]). */
 int wpcg_model_debug_read(wpcg_model* m, int which, float* out, uint64_t n);
 
 /* ---- HIP graphs over the context stream (no reference counterpart) ----

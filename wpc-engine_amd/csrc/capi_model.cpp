@@ -39,11 +39,12 @@ struct wpcg_model {
     DecodeState* st = nullptr;
     uint32_t* tokens = nullptr;                // [max_pos + 1]
     float *residual = nullptr, *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
-    float *attn = nullptr, *scores = nullptr, *mlp = nullptr, *g = nullptr, *u = nullptr,
+    float *attn = nullptr, *g = nullptr, *u = nullptr,
           *h = nullptr, *logits = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int graph_mode = -1;
+    bool use_graph = true;  // false: steps are enqueued launch by launch
     std::vector<void*> allocs;
 };
 
@@ -145,10 +146,8 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
         if (int rc = wpcg_linear_matvec_multi(3, qkv, xs, ys, s)) return rc;
         float* kc = m->kc + (size_t)l * nkv * c.max_pos * hd;
         float* vc = m->vc + (size_t)l * nkv * c.max_pos * hd;
-        WPCG_HIP(launch_head_norm_rope(mode, m->q, m->k, m->v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps,
-                                       m->cos_t, m->sin_t, m->st, kc, vc, s));
-        WPCG_HIP(launch_attention(mode, m->q, kc, vc, nh, nkv, hd, (int)c.max_pos, scale, m->st,
-                                  m->scores, m->attn, s));
+        WPCG_HIP(launch_attention(mode, m->q, m->k, m->v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale,
+                                  m->cos_t, m->sin_t, m->st, kc, vc, m->attn, s));
         // residual += o_proj(attn): the residual is the GEMV's bias and output
         {
             float* saved = L.o->bias;
@@ -159,8 +158,7 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
         }
         WPCG_HIP(launch_rms_norm(mode, m->residual, L.post_ln, H, c.eps, m->normed, s));
         if (c.n_experts) {
-            if (int rc = wpcg_moe_forward(L.moe, m->normed, m->mlp, nullptr, nullptr, s)) return rc;
-            WPCG_HIP(launch_add(m->residual, m->mlp, H, s));
+            if (int rc = moe_run(L.moe, m->normed, m->residual, m->residual, s)) return rc;
         } else {
             wpcg_linear* gu[2] = {L.gate, L.up};
             const float* x2[2] = {m->normed, m->normed};
@@ -185,6 +183,7 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
 
 int ensure_graph(wpcg_model* m)
 {
+    if (!m->use_graph) return WPCG_OK;
     if (m->exec && m->graph_mode == m->mode) return WPCG_OK;
     drop_graph(m);
     hipStream_t s = m->ctx->stream;
@@ -200,6 +199,15 @@ int ensure_graph(wpcg_model* m)
     m->graph = g;
     WPCG_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
     m->graph_mode = m->mode;
+    return WPCG_OK;
+}
+
+// One step on the context stream: the captured graph, or the launches.
+int run_step(wpcg_model* m)
+{
+    hipStream_t s = m->ctx->stream;
+    if (!m->use_graph) return enqueue_step(m, s);
+    WPCG_HIP(hipGraphLaunch(m->exec, s));
     return WPCG_OK;
 }
 
@@ -235,8 +243,10 @@ int wpcg_model_create(wpcg_ctx* ctx, int scheme, const wpcg_model_config* cfg, w
     const wpcg_model_config& c = *cfg;
     if (!c.n_layers || !c.hidden || !c.n_heads || !c.n_kv_heads || !c.head_dim || !c.vocab || !c.max_pos)
         return fail(WPCG_E_ARG, "every size in the config must be positive");
-    if (c.n_heads % c.n_kv_heads || c.head_dim % 2 || c.head_dim > 256)
-        return fail(WPCG_E_SHAPE, "n_heads must be a multiple of n_kv_heads; head_dim even, <= 256");
+    if (c.n_heads % c.n_kv_heads || c.head_dim % 32 || c.head_dim > 256)
+        return fail(WPCG_E_SHAPE, "n_heads must be a multiple of n_kv_heads; head_dim a multiple of 32, <= 256");
+    if (c.max_pos > (uint32_t)attention_max_pos())
+        return fail(WPCG_E_UNSUPPORTED, "max_pos above " + std::to_string(attention_max_pos()));
     if (c.hidden % 128 || (c.n_heads * c.head_dim) % 128 || (c.n_experts == 0 && c.inter % 128))
         return fail(WPCG_E_SHAPE, "matrix input sizes must be multiples of 128");
     if (c.n_experts == 0 && !c.inter) return fail(WPCG_E_ARG, "dense model needs intermediate_size");
@@ -277,8 +287,6 @@ int wpcg_model_create(wpcg_ctx* ctx, int scheme, const wpcg_model_config* cfg, w
     dev((void**)&m->k, kvd * 4);
     dev((void**)&m->v, kvd * 4);
     dev((void**)&m->attn, qd * 4);
-    dev((void**)&m->scores, (size_t)c.n_heads * c.max_pos * 4);
-    dev((void**)&m->mlp, c.hidden * 4u);
     dev((void**)&m->g, inter * 4);
     dev((void**)&m->u, inter * 4);
     dev((void**)&m->h, inter * 4);
@@ -435,6 +443,14 @@ int wpcg_model_set_mode(wpcg_model* m, int mode)
     return WPCG_OK;
 }
 
+int wpcg_model_set_graphs(wpcg_model* m, int enabled)
+{
+    if (!m) return fail(WPCG_E_ARG, "null model");
+    m->use_graph = enabled != 0;
+    drop_graph(m);
+    return WPCG_OK;
+}
+
 int wpcg_model_reset(wpcg_model* m)
 {
     if (!m) return fail(WPCG_E_ARG, "null model");
@@ -469,7 +485,7 @@ int wpcg_model_forward_token(wpcg_model* m, uint32_t token, float* logits, uint3
     st.n_prompt = 0xffffffffu;
     WPCG_HIP(hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice));
     WPCG_HIP(hipMemcpy(m->tokens + st.pos, &token, 4, hipMemcpyHostToDevice));
-    WPCG_HIP(hipGraphLaunch(m->exec, s));
+    if (int rc = run_step(m)) return rc;
     WPCG_HIP(hipStreamSynchronize(s));
     if (logits) WPCG_HIP(hipMemcpy(logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost));
     if (argmax) {
@@ -493,9 +509,7 @@ int wpcg_model_debug_read(wpcg_model* m, int which, float* out, uint64_t n)
         case 3: src = m->k; len = kvd; break;
         case 4: src = m->v; len = kvd; break;
         case 5: src = m->attn; len = qd; break;
-        case 6: src = m->scores; len = (uint64_t)c.n_heads * c.max_pos; break;
         case 7: src = m->logits; len = c.vocab; break;
-        case 8: src = m->mlp; len = c.hidden; break;
         case 9: src = m->kc; len = (uint64_t)c.n_layers * kvd * c.max_pos; break;
         case 10: src = m->vc; len = (uint64_t)c.n_layers * kvd * c.max_pos; break;
         default: return fail(WPCG_E_ARG, "unknown buffer");
@@ -529,8 +543,7 @@ int wpcg_model_generate(wpcg_model* m, const uint32_t* prompt, uint32_t n_prompt
     // yields the first new token); the n_new-1 after it are pure decode
     for (uint32_t i = 0; i < n_prompt + n_new - 1 && rc == WPCG_OK; i++) {
         if (i == n_prompt) (void)hipEventRecord(e0, s);
-        const hipError_t e = hipGraphLaunch(m->exec, s);
-        if (e != hipSuccess) rc = hip_fail(e, "hipGraphLaunch");
+        rc = run_step(m);
     }
     (void)hipEventRecord(e1, s);
     if (rc == WPCG_OK) {

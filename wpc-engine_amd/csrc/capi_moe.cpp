@@ -18,7 +18,7 @@ int valid_mode(int mode) { return mode == WPCG_MODE_EXACT || mode == WPCG_MODE_F
 
 void free_dense(wpcg_dense* d)
 {
-    if (d->wt) (void)hipFree(d->wt);
+    if (d->w) (void)hipFree(d->w);
     if (d->bias) (void)hipFree(d->bias);
 }
 
@@ -52,6 +52,42 @@ DeviceMatrix expert_view(int scheme, uint64_t rows, uint64_t cols)
 
 }  // namespace
 
+int wpcg::moe_run(wpcg_moe* m, const float* x_dev, float* out_dev, const float* add, hipStream_t s)
+{
+    const int K = (int)m->top_k, H = (int)m->hidden, I = (int)m->inter;
+    WPCG_HIP(launch_dense(m->router->w, (int)m->n_exp, H, m->mode, x_dev, nullptr, m->scores, s));
+    WPCG_HIP(launch_softmax_route(m->scores, (int)m->n_exp, K, m->norm_topk, m->ids, m->w, s));
+    // gate and up of the chosen experts, then SiLU(gate) * up
+    if (m->mode == WPCG_MODE_FAST) {
+        GemvJob jobs[MAX_JOBS];
+        for (int k = 0; k < K; k++) {
+            jobs[2 * k] = GemvJob{&m->gate, &m->plan, x_dev, nullptr, m->g + (size_t)k * I, m->ids, k};
+            jobs[2 * k + 1] = GemvJob{&m->up, &m->plan, x_dev, nullptr, m->u + (size_t)k * I, m->ids, k};
+        }
+        WPCG_HIP(launch_gemv_fast(jobs, 2 * K, s));
+    } else {
+        for (int k = 0; k < K; k++) {
+            WPCG_HIP(launch_gemv_exact(m->gate, x_dev, nullptr, m->g + (size_t)k * I, s, m->ids, k));
+            WPCG_HIP(launch_gemv_exact(m->up, x_dev, nullptr, m->u + (size_t)k * I, s, m->ids, k));
+        }
+    }
+    WPCG_HIP(launch_silu_mul(m->g, m->u, m->h, (size_t)K * I, s));
+    // down of the chosen experts, then the weighted sum in chosen order
+    if (m->mode == WPCG_MODE_FAST) {
+        GemvJob jobs[MAX_JOBS];
+        for (int k = 0; k < K; k++)
+            jobs[k] = GemvJob{&m->down, &m->plan, m->h + (size_t)k * I, nullptr, m->ys + (size_t)k * H,
+                              m->ids, k};
+        WPCG_HIP(launch_gemv_fast(jobs, K, s));
+    } else {
+        for (int k = 0; k < K; k++)
+            WPCG_HIP(launch_gemv_exact(m->down, m->h + (size_t)k * I, nullptr, m->ys + (size_t)k * H, s,
+                                       m->ids, k));
+    }
+    WPCG_HIP(launch_combine(m->ys, m->ids, m->w, K, out_dev, H, add, s));
+    return WPCG_OK;
+}
+
 extern "C" {
 
 // ------------------------------------------------------------ dense linear
@@ -68,11 +104,8 @@ int wpcg_dense_create(wpcg_ctx* ctx, const float* w, uint64_t out_f, uint64_t in
     d->ctx = ctx;
     d->out_f = out_f;
     d->in_f = in_f;
-    std::vector<float> wt(out_f * in_f);
-    for (uint64_t r = 0; r < out_f; r++)
-        for (uint64_t i = 0; i < in_f; i++) wt[i * out_f + r] = w[r * in_f + i];
-    hipError_t e = hipMalloc(&d->wt, wt.size() * sizeof(float));
-    if (e == hipSuccess) e = hipMemcpy(d->wt, wt.data(), wt.size() * sizeof(float), hipMemcpyHostToDevice);
+    hipError_t e = hipMalloc(&d->w, out_f * in_f * sizeof(float));
+    if (e == hipSuccess) e = hipMemcpy(d->w, w, out_f * in_f * sizeof(float), hipMemcpyHostToDevice);
     if (e == hipSuccess && bias) {
         e = hipMalloc(&d->bias, out_f * sizeof(float));
         if (e == hipSuccess) e = hipMemcpy(d->bias, bias, out_f * sizeof(float), hipMemcpyHostToDevice);
@@ -108,7 +141,7 @@ int wpcg_dense_matvec(wpcg_dense* d, const float* x_dev, float* y_dev, wpcg_stre
 {
     if (!d || !x_dev || !y_dev) return fail(WPCG_E_ARG, "null argument");
     if (int rc = check_ctx(d->ctx)) return rc;
-    WPCG_HIP(launch_dense(d->wt, (int)d->out_f, (int)d->in_f, d->mode, x_dev, d->bias, y_dev,
+    WPCG_HIP(launch_dense(d->w, (int)d->out_f, (int)d->in_f, d->mode, x_dev, d->bias, y_dev,
                           pick(d->ctx, stream)));
     return WPCG_OK;
 }
@@ -271,40 +304,10 @@ int wpcg_moe_forward(wpcg_moe* m, const float* x_dev, float* out_dev, int32_t* i
     if (!m->router) return fail(WPCG_E_ARG, "router not set");
     if (int rc = check_ctx(m->ctx)) return rc;
     hipStream_t s = pick(m->ctx, stream);
-    const int K = (int)m->top_k, H = (int)m->hidden, I = (int)m->inter;
-    WPCG_HIP(launch_dense(m->router->wt, (int)m->n_exp, H, m->mode, x_dev, nullptr, m->scores, s));
-    WPCG_HIP(launch_softmax(m->scores, (int)m->n_exp, s));
-    WPCG_HIP(launch_route(m->scores, (int)m->n_exp, K, m->norm_topk, m->ids, m->w, s));
-    // gate and up of the chosen experts, then SiLU(gate) * up
-    if (m->mode == WPCG_MODE_FAST) {
-        GemvJob jobs[MAX_JOBS];
-        for (int k = 0; k < K; k++) {
-            jobs[2 * k] = GemvJob{&m->gate, &m->plan, x_dev, nullptr, m->g + (size_t)k * I, m->ids, k};
-            jobs[2 * k + 1] = GemvJob{&m->up, &m->plan, x_dev, nullptr, m->u + (size_t)k * I, m->ids, k};
-        }
-        WPCG_HIP(launch_gemv_fast(jobs, 2 * K, s));
-    } else {
-        for (int k = 0; k < K; k++) {
-            WPCG_HIP(launch_gemv_exact(m->gate, x_dev, nullptr, m->g + (size_t)k * I, s, m->ids, k));
-            WPCG_HIP(launch_gemv_exact(m->up, x_dev, nullptr, m->u + (size_t)k * I, s, m->ids, k));
-        }
-    }
-    WPCG_HIP(launch_silu_mul(m->g, m->u, m->h, (size_t)K * I, s));
-    // down of the chosen experts, then the weighted sum in chosen order
-    if (m->mode == WPCG_MODE_FAST) {
-        GemvJob jobs[MAX_JOBS];
-        for (int k = 0; k < K; k++)
-            jobs[k] = GemvJob{&m->down, &m->plan, m->h + (size_t)k * I, nullptr, m->ys + (size_t)k * H,
-                              m->ids, k};
-        WPCG_HIP(launch_gemv_fast(jobs, K, s));
-    } else {
-        for (int k = 0; k < K; k++)
-            WPCG_HIP(launch_gemv_exact(m->down, m->h + (size_t)k * I, nullptr, m->ys + (size_t)k * H, s,
-                                       m->ids, k));
-    }
-    WPCG_HIP(launch_combine(m->ys, m->ids, m->w, K, out_dev, H, s));
-    if (ids_dev) WPCG_HIP(hipMemcpyAsync(ids_dev, m->ids, (size_t)K * 4, hipMemcpyDeviceToDevice, s));
-    if (weights_dev) WPCG_HIP(hipMemcpyAsync(weights_dev, m->w, (size_t)K * 4, hipMemcpyDeviceToDevice, s));
+    if (int rc = moe_run(m, x_dev, out_dev, nullptr, s)) return rc;
+    const size_t K = m->top_k;
+    if (ids_dev) WPCG_HIP(hipMemcpyAsync(ids_dev, m->ids, K * 4, hipMemcpyDeviceToDevice, s));
+    if (weights_dev) WPCG_HIP(hipMemcpyAsync(weights_dev, m->w, K * 4, hipMemcpyDeviceToDevice, s));
     return WPCG_OK;
 }
 

@@ -57,145 +57,191 @@ __device__ float sum_squares(const float* x, int n, float* red)
     return s_total;
 }
 
+// x is staged in LDS once (n <= RN_LDS; longer vectors are read from global
+// memory twice): EXACT's index-order sum of squares then runs from LDS in one
+// thread, FAST's from registers as a tree.
+constexpr int RN_LDS = 8192;
 template <int MODE>
 __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
                                                  const float* __restrict__ w, int n, float eps,
                                                  float* __restrict__ out)
 {
+    __shared__ float xs[RN_LDS];
     __shared__ float red[NW / 64];
-    const float s = sum_squares<MODE>(x, n, red);
-    const float mean_sq = __fdiv_rn(s, (float)n);
+    __shared__ float s_total;
+    const bool staged = n <= RN_LDS;
+    const float* src = staged ? xs : x;
+    float part = 0.0f;
+    for (int i = threadIdx.x; i < n; i += NW) {
+        const float v = x[i];
+        if (staged) xs[i] = v;
+        part = fmaf(v, v, part);
+    }
+    if (MODE == WPCG_MODE_EXACT) {
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float s = 0.0f;
+            for (int i = 0; i < n; i++) s = __fadd_rn(s, __fmul_rn(src[i], src[i]));
+            s_total = s;
+        }
+    } else {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = part;
+        __syncthreads();
+        if (threadIdx.x == 0) s_total = (red[0] + red[1]) + (red[2] + red[3]);
+    }
+    __syncthreads();
+    const float mean_sq = __fdiv_rn(s_total, (float)n);
     const float scale = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(mean_sq, eps)));
-    for (int i = threadIdx.x; i < n; i += NW) out[i] = __fmul_rn(__fmul_rn(x[i], scale), w[i]);
+    for (int i = threadIdx.x; i < n; i += NW) out[i] = __fmul_rn(__fmul_rn(src[i], scale), w[i]);
 }
 
-// ---- per-head q/k RMSNorm, RoPE, KV-cache append ---------------------------
-// Workgroup h < nh: query head h, normed with q_norm and rotated in place.
-// Workgroup nh + j: key head j, normed with k_norm, rotated and stored at the
-// current position of the layer's K cache; value head j copied to the V
-// cache. RoPE (rope.rs:24-39): out_i = x1*c - x2*s, out_{i+d/2} = x2*c + x1*s
-// with c, s the f32 casts of the host's f64 cos/sin (cos_t/sin_t, [pos][d/2]).
-// Caches are [layer][kv_head][max_pos][head_dim].
+// ---- attention step (model.rs:441-497) -------------------------------------
+// One workgroup per query head h (kv head j = h / (nh/nkv)), all in one
+// launch:
+//   q_h, k_j: RMSNorm with q_norm / k_norm, then RoPE at `pos`
+//     (rope.rs:24-39: out_i = x1*c - x2*s, out_{i+d/2} = x2*c + x1*s with c, s
+//     the f32 casts of the host's f64 cos/sin, cos_t/sin_t [pos][d/2]);
+//   the first query head of kv head j appends k_j and v_j to the caches;
+//   scores_t = (sum_d q_h[d] * k_t[d]) * scale for t <= pos (k_pos taken from
+//     LDS, earlier positions from the cache), softmax over them (norm.rs:28-43);
+//   out_h[d] = sum_t w_t * v_t[d] in position order.
+// Every workgroup recomputes k_j and v_j for `pos` itself, so no workgroup
+// waits for another's cache write. Caches are [kv_head][max_pos][head_dim]
+// of one layer. EXACT: index-order sums, separate roundings; FAST: fused
+// multiply-adds and tree sums. head_dim <= 256, pos < max_pos <= AT_MAXPOS.
+constexpr int AT_WG = 256;
+constexpr int AT_MAXPOS = 4096;
+
 template <int MODE>
-__global__ __launch_bounds__(128) void k_head_norm_rope(float* __restrict__ q,
-                                                        const float* __restrict__ k,
-                                                        const float* __restrict__ v,
-                                                        const float* __restrict__ qn,
-                                                        const float* __restrict__ kn, int nh,
-                                                        int hd, float eps,
-                                                        const float* __restrict__ cos_t,
-                                                        const float* __restrict__ sin_t,
-                                                        const DecodeState* __restrict__ st,
-                                                        float* __restrict__ kc,
-                                                        float* __restrict__ vc, int nkv)
+__device__ void head_rms_rope(const float* x, const float* w, float* y, float* red, int hd,
+                              float eps, const float* c, const float* sn)
 {
-    __shared__ float red[2];
-    __shared__ float y[256];  // head_dim <= 256
-    const int h = blockIdx.x;
-    const bool is_q = h < nh;
-    const float* x = is_q ? q + (size_t)h * hd : k + (size_t)(h - nh) * hd;
-    const float* w = is_q ? qn : kn;
+    __shared__ float s_tmp[256];
     const float s = sum_squares<MODE>(x, hd, red);
     const float mean_sq = __fdiv_rn(s, (float)hd);
     const float scale = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(mean_sq, eps)));
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) y[i] = __fmul_rn(__fmul_rn(x[i], scale), w[i]);
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) s_tmp[i] = __fmul_rn(__fmul_rn(x[i], scale), w[i]);
     __syncthreads();
-    const uint32_t pos = st->pos;
+    const int half = hd / 2;
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        const float x1 = s_tmp[i], x2 = s_tmp[i + half];
+        y[i] = __fsub_rn(__fmul_rn(x1, c[i]), __fmul_rn(x2, sn[i]));
+        y[i + half] = __fadd_rn(__fmul_rn(x2, c[i]), __fmul_rn(x1, sn[i]));
+    }
+    __syncthreads();
+}
+
+template <int MODE>
+__global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ qp,
+                                                     const float* __restrict__ kp,
+                                                     const float* __restrict__ vp,
+                                                     const float* __restrict__ qn,
+                                                     const float* __restrict__ kn, int nh, int nkv,
+                                                     int hd, float eps, float scale,
+                                                     const float* __restrict__ cos_t,
+                                                     const float* __restrict__ sin_t,
+                                                     const DecodeState* __restrict__ st,
+                                                     float* __restrict__ kc, float* __restrict__ vc,
+                                                     float* __restrict__ out)
+{
+    __shared__ __align__(16) float qs[256], ks[256], vs[256];
+    __shared__ float w[AT_MAXPOS];
+    __shared__ float red[AT_WG / 64];
+    __shared__ float s_sum;
+    const int h = blockIdx.x, n_rep = nh / nkv, j = h / n_rep;
+    const uint32_t pos = st->pos, max_pos = st->max_pos;
     const int half = hd / 2;
     const float* c = cos_t + (size_t)pos * half;
     const float* sn = sin_t + (size_t)pos * half;
-    float* dst = is_q ? q + (size_t)h * hd
-                      : kc + ((size_t)(h - nh) * st->max_pos + pos) * hd;
-    for (int i = threadIdx.x; i < half; i += blockDim.x) {
-        const float x1 = y[i], x2 = y[i + half];
-        dst[i] = __fsub_rn(__fmul_rn(x1, c[i]), __fmul_rn(x2, sn[i]));
-        dst[i + half] = __fadd_rn(__fmul_rn(x2, c[i]), __fmul_rn(x1, sn[i]));
-    }
-    if (!is_q) {
-        const int j = h - nh;
-        float* vd = vc + ((size_t)j * st->max_pos + pos) * hd;
-        for (int i = threadIdx.x; i < hd; i += blockDim.x) vd[i] = v[(size_t)j * hd + i];
-    }
-    (void)nkv;
-}
-
-// ---- attention over positions 0..pos (model.rs:466-490) --------------------
-// scores[h][t] = (sum_d q_h[d] * k_t[d]) * scale, index order; the head's
-// kv head is h / (nh / nkv). One thread per (head, position).
-template <int MODE>
-__global__ __launch_bounds__(64) void k_attn_scores(const float* __restrict__ q,
-                                                    const float* __restrict__ kc, int nh, int nkv,
-                                                    int hd, float scale,
-                                                    const DecodeState* __restrict__ st,
-                                                    float* __restrict__ scores)
-{
-    __shared__ float qs[256];
-    const int h = blockIdx.y;
-    const int t = blockIdx.x * 64 + threadIdx.x;
-    const uint32_t pos = st->pos, max_pos = st->max_pos;
-    if (blockIdx.x * 64 > pos) return;  // whole workgroup past the sequence
-    for (int i = threadIdx.x; i < hd; i += 64) qs[i] = q[(size_t)h * hd + i];
+    head_rms_rope<MODE>(qp + (size_t)h * hd, qn, qs, red, hd, eps, c, sn);
+    head_rms_rope<MODE>(kp + (size_t)j * hd, kn, ks, red, hd, eps, c, sn);
+    for (int i = threadIdx.x; i < hd; i += AT_WG) vs[i] = vp[(size_t)j * hd + i];
     __syncthreads();
-    if (t > (int)pos) return;
-    const int kvh = h / (nh / nkv);
-    const float* kt = kc + ((size_t)kvh * max_pos + t) * hd;
-    float dot = 0.0f;
-    if (MODE == WPCG_MODE_EXACT) {
-        for (int d = 0; d < hd; d++) dot = __fadd_rn(dot, __fmul_rn(qs[d], kt[d]));
-    } else {
-        for (int d = 0; d < hd; d++) dot = fmaf(qs[d], kt[d], dot);
+    const float* kb = kc + (size_t)j * max_pos * hd;
+    const float* vb = vc + (size_t)j * max_pos * hd;
+    if (h % n_rep == 0)
+        for (int i = threadIdx.x; i < hd; i += AT_WG) {
+            kc[((size_t)j * max_pos + pos) * hd + i] = ks[i];
+            vc[((size_t)j * max_pos + pos) * hd + i] = vs[i];
+        }
+    // scores: thread t, one position at a time; rows read as float4 chunks
+    const int n = (int)pos + 1;
+    for (int t = threadIdx.x; t < n; t += AT_WG) {
+        const float* kt = t == (int)pos ? ks : kb + (size_t)t * hd;
+        float dot = 0.0f;
+        for (int d0 = 0; d0 < hd; d0 += 32) {
+            float4 kv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) kv[u] = *reinterpret_cast<const float4*>(kt + d0 + 4 * u);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const float* q4 = qs + d0 + 4 * u;
+                if (MODE == WPCG_MODE_EXACT) {
+                    dot = __fadd_rn(dot, __fmul_rn(q4[0], kv[u].x));
+                    dot = __fadd_rn(dot, __fmul_rn(q4[1], kv[u].y));
+                    dot = __fadd_rn(dot, __fmul_rn(q4[2], kv[u].z));
+                    dot = __fadd_rn(dot, __fmul_rn(q4[3], kv[u].w));
+                } else {
+                    dot = fmaf(q4[0], kv[u].x, dot);
+                    dot = fmaf(q4[1], kv[u].y, dot);
+                    dot = fmaf(q4[2], kv[u].z, dot);
+                    dot = fmaf(q4[3], kv[u].w, dot);
+                }
+            }
+        }
+        w[t] = __fmul_rn(dot, scale);
     }
-    scores[(size_t)h * max_pos + t] = __fmul_rn(dot, scale);
-}
-
-// softmax_inplace over scores[h][0..pos] (norm.rs:28-43), one workgroup per head
-__global__ __launch_bounds__(NW) void k_attn_softmax(float* __restrict__ scores,
-                                                     const DecodeState* __restrict__ st)
-{
-    __shared__ float red[NW / 64];
-    __shared__ float s_sum;
-    const int n = (int)st->pos + 1;
-    float* x = scores + (size_t)blockIdx.x * st->max_pos;
+    __syncthreads();
+    // softmax over w[0..n)
     float m = -INFINITY;
-    for (int i = threadIdx.x; i < n; i += NW) m = fmaxf(m, x[i]);
+    for (int t = threadIdx.x; t < n; t += AT_WG) m = fmaxf(m, w[t]);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (int i = threadIdx.x; i < n; i += NW) x[i] = ref_expf(__fsub_rn(x[i], m));
+    for (int t = threadIdx.x; t < n; t += AT_WG) w[t] = ref_expf(__fsub_rn(w[t], m));
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (MODE == WPCG_MODE_EXACT) {
+        if (threadIdx.x == 0) {
+            float s = 0.0f;
+            for (int t = 0; t < n; t++) s = __fadd_rn(s, w[t]);
+            s_sum = s;
+        }
+    } else {
         float s = 0.0f;
-        for (int i = 0; i < n; i++) s = __fadd_rn(s, x[i]);
-        s_sum = s;
+        for (int t = threadIdx.x; t < n; t += AT_WG) s += w[t];
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+        __syncthreads();
+        if (threadIdx.x == 0) s_sum = (red[0] + red[1]) + (red[2] + red[3]);
     }
     __syncthreads();
-    const float s = s_sum;
-    if (s > 0.0f)
-        for (int i = threadIdx.x; i < n; i += NW) x[i] = __fdiv_rn(x[i], s);
-}
-
-// out[h][d] = sum_t scores[h][t] * v_t[d] in position order, from 0.
-// One thread per (head, d).
-template <int MODE>
-__global__ __launch_bounds__(128) void k_attn_out(const float* __restrict__ scores,
-                                                  const float* __restrict__ vc, int nh, int nkv,
-                                                  int hd, const DecodeState* __restrict__ st,
-                                                  float* __restrict__ out)
-{
-    const int h = blockIdx.x;
-    const uint32_t pos = st->pos, max_pos = st->max_pos;
-    const int kvh = h / (nh / nkv);
-    const float* w = scores + (size_t)h * max_pos;
-    const float* vb = vc + (size_t)kvh * max_pos * hd;
-    for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+    const float ssum = s_sum;
+    if (ssum > 0.0f)
+        for (int t = threadIdx.x; t < n; t += AT_WG) w[t] = __fdiv_rn(w[t], ssum);
+    __syncthreads();
+    // out[d] = sum_t w_t v_t[d], position order; thread d, loads 8 ahead
+    for (int d = threadIdx.x; d < hd; d += AT_WG) {
         float acc = 0.0f;
-        if (MODE == WPCG_MODE_EXACT) {
-            for (uint32_t t = 0; t <= pos; t++) acc = __fadd_rn(acc, __fmul_rn(w[t], vb[(size_t)t * hd + d]));
-        } else {
-            for (uint32_t t = 0; t <= pos; t++) acc = fmaf(w[t], vb[(size_t)t * hd + d], acc);
+        int t = 0;
+        for (; t + 8 <= (int)pos; t += 8) {
+            float vv[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) vv[u] = vb[(size_t)(t + u) * hd + d];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                acc = MODE == WPCG_MODE_EXACT ? __fadd_rn(acc, __fmul_rn(w[t + u], vv[u]))
+                                              : fmaf(w[t + u], vv[u], acc);
         }
+        for (; t < (int)pos; t++)
+            acc = MODE == WPCG_MODE_EXACT ? __fadd_rn(acc, __fmul_rn(w[t], vb[(size_t)t * hd + d]))
+                                          : fmaf(w[t], vb[(size_t)t * hd + d], acc);
+        acc = MODE == WPCG_MODE_EXACT ? __fadd_rn(acc, __fmul_rn(w[pos], vs[d])) : fmaf(w[pos], vs[d], acc);
         out[(size_t)h * hd + d] = acc;
     }
 }
@@ -255,40 +301,20 @@ hipError_t launch_rms_norm(int mode, const float* x, const float* w, int n, floa
     return hipGetLastError();
 }
 
-hipError_t launch_head_norm_rope(int mode, float* q, const float* k, const float* v, const float* qn,
-                                 const float* kn, int nh, int nkv, int hd, float eps,
-                                 const float* cos_t, const float* sin_t, const DecodeState* st,
-                                 float* kc, float* vc, hipStream_t s)
-{
-    (void)hipGetLastError();
-    if (mode == WPCG_MODE_EXACT)
-        hipLaunchKernelGGL(k_head_norm_rope<WPCG_MODE_EXACT>, dim3(nh + nkv), dim3(128), 0, s, q, k,
-                           v, qn, kn, nh, hd, eps, cos_t, sin_t, st, kc, vc, nkv);
-    else
-        hipLaunchKernelGGL(k_head_norm_rope<WPCG_MODE_FAST>, dim3(nh + nkv), dim3(128), 0, s, q, k,
-                           v, qn, kn, nh, hd, eps, cos_t, sin_t, st, kc, vc, nkv);
-    return hipGetLastError();
-}
+int attention_max_pos() { return AT_MAXPOS; }
 
-hipError_t launch_attention(int mode, const float* q, const float* kc, const float* vc, int nh,
-                            int nkv, int hd, int max_pos, float scale, const DecodeState* st,
-                            float* scores, float* out, hipStream_t s)
+hipError_t launch_attention(int mode, const float* q, const float* k, const float* v, const float* qn,
+                            const float* kn, int nh, int nkv, int hd, float eps, float scale,
+                            const float* cos_t, const float* sin_t, const DecodeState* st, float* kc,
+                            float* vc, float* out, hipStream_t s)
 {
     (void)hipGetLastError();
-    const dim3 g((max_pos + 63) / 64, nh);
     if (mode == WPCG_MODE_EXACT)
-        hipLaunchKernelGGL(k_attn_scores<WPCG_MODE_EXACT>, g, dim3(64), 0, s, q, kc, nh, nkv, hd, scale,
-                           st, scores);
+        hipLaunchKernelGGL(k_attention<WPCG_MODE_EXACT>, dim3(nh), dim3(AT_WG), 0, s, q, k, v, qn, kn,
+                           nh, nkv, hd, eps, scale, cos_t, sin_t, st, kc, vc, out);
     else
-        hipLaunchKernelGGL(k_attn_scores<WPCG_MODE_FAST>, g, dim3(64), 0, s, q, kc, nh, nkv, hd, scale,
-                           st, scores);
-    hipLaunchKernelGGL(k_attn_softmax, dim3(nh), dim3(NW), 0, s, scores, st);
-    if (mode == WPCG_MODE_EXACT)
-        hipLaunchKernelGGL(k_attn_out<WPCG_MODE_EXACT>, dim3(nh), dim3(128), 0, s, scores, vc, nh, nkv,
-                           hd, st, out);
-    else
-        hipLaunchKernelGGL(k_attn_out<WPCG_MODE_FAST>, dim3(nh), dim3(128), 0, s, scores, vc, nh, nkv,
-                           hd, st, out);
+        hipLaunchKernelGGL(k_attention<WPCG_MODE_FAST>, dim3(nh), dim3(AT_WG), 0, s, q, k, v, qn, kn,
+                           nh, nkv, hd, eps, scale, cos_t, sin_t, st, kc, vc, out);
     return hipGetLastError();
 }
 

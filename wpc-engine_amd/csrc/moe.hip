@@ -18,32 +18,54 @@ namespace wpcg {
 namespace {
 
 // ---- DenseLinear::matvec (wpc-runtime/src/weights.rs:59-78) -------------
-// y[r] = sum_i W[r][i] * x[i], index order. The device keeps W transposed,
-// wt[i*out_f + r], so step i of a wave's 64 rows is one coalesced load.
-__global__ __launch_bounds__(64) void k_dense_exact(const float* __restrict__ wt,
+// y[r] = sum_i W[r][i] * x[i], W row-major [out_f][in_f].
+// EXACT: one lane per row, index order, product and sum rounded separately;
+// each lane walks its own row (16-byte loads, reused from cache lines).
+__global__ __launch_bounds__(64) void k_dense_exact(const float* __restrict__ w,
                                                     const float* __restrict__ x,
                                                     const float* __restrict__ bias,
                                                     float* __restrict__ y, int out_f, int in_f)
 {
     const int r = blockIdx.x * 64 + threadIdx.x;
-    const float* col = wt + min(r, out_f - 1);
+    const float* row = w + (size_t)min(r, out_f - 1) * in_f;
     float acc = 0.0f;
-#pragma unroll 16
-    for (int i = 0; i < in_f; i++) acc = __fadd_rn(acc, __fmul_rn(col[(size_t)i * out_f], x[i]));
+    int i = 0;
+    if ((in_f & 3) == 0) {
+#pragma unroll 4
+        for (; i < in_f; i += 4) {
+            const float4 v = *reinterpret_cast<const float4*>(row + i);
+            acc = __fadd_rn(acc, __fmul_rn(v.x, x[i]));
+            acc = __fadd_rn(acc, __fmul_rn(v.y, x[i + 1]));
+            acc = __fadd_rn(acc, __fmul_rn(v.z, x[i + 2]));
+            acc = __fadd_rn(acc, __fmul_rn(v.w, x[i + 3]));
+        }
+    }
+    for (; i < in_f; i++) acc = __fadd_rn(acc, __fmul_rn(row[i], x[i]));
     if (r < out_f) y[r] = bias ? __fadd_rn(acc, bias[r]) : acc;
 }
 
-// FAST: one wave per row over the transposed layout's column, lanes strided
-// over i, fixed-order tree sum (deterministic, not the reference's order).
-__global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ wt,
+// FAST: one wave per row, 16-byte coalesced loads, fixed-order tree sum
+// (deterministic, not the reference's order).
+__global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ w,
                                                     const float* __restrict__ x,
                                                     const float* __restrict__ bias,
                                                     float* __restrict__ y, int out_f, int in_f)
 {
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int rr = min(r, out_f - 1);
+    const float* row = w + (size_t)min(r, out_f - 1) * in_f;
     float acc = 0.0f;
-    for (int i = lane; i < in_f; i += 64) acc = fmaf(wt[(size_t)i * out_f + rr], x[i], acc);
+    if ((in_f & 3) == 0) {
+        for (int i = 4 * lane; i < in_f; i += 256) {
+            const float4 v = *reinterpret_cast<const float4*>(row + i);
+            const float4 u = *reinterpret_cast<const float4*>(x + i);
+            acc = fmaf(v.x, u.x, acc);
+            acc = fmaf(v.y, u.y, acc);
+            acc = fmaf(v.z, u.z, acc);
+            acc = fmaf(v.w, u.w, acc);
+        }
+    } else {
+        for (int i = lane; i < in_f; i += 64) acc = fmaf(row[i], x[i], acc);
+    }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
     if (r < out_f && lane == 0) y[r] = bias ? acc + bias[r] : acc;
@@ -128,6 +150,82 @@ __global__ __launch_bounds__(64) void k_route(const float* __restrict__ p, int n
     }
 }
 
+// ---- softmax_inplace + route in one wave (the MoE router's tail) ----------
+// Same arithmetic as k_softmax then k_route: the exps go through LDS so
+// lane 0 can add them in index order; the top-k scan runs on the
+// probabilities in registers.
+__global__ __launch_bounds__(64) void k_softmax_route(const float* __restrict__ scores, int n,
+                                                      int top_k, int norm_topk,
+                                                      int32_t* __restrict__ ids,
+                                                      float* __restrict__ w)
+{
+    __shared__ float e[64 * RT_PER];
+    __shared__ float chosen[64];
+    __shared__ float s_sum;
+    const int lane = threadIdx.x;
+    float v[RT_PER];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < RT_PER; j++) {
+        const int i = lane + 64 * j;
+        v[j] = i < n ? scores[i] : -INFINITY;
+        m = fmaxf(m, v[j]);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+#pragma unroll
+    for (int j = 0; j < RT_PER; j++) {
+        const int i = lane + 64 * j;
+        if (i < n) {
+            v[j] = ref_expf(__fsub_rn(v[j], m));
+            e[i] = v[j];
+        }
+    }
+    __syncthreads();
+    if (lane == 0) {
+        float s = 0.0f;
+        for (int i = 0; i < n; i++) s = __fadd_rn(s, e[i]);
+        s_sum = s;
+    }
+    __syncthreads();
+    const float s = s_sum;
+#pragma unroll
+    for (int j = 0; j < RT_PER; j++) {
+        const int i = lane + 64 * j;
+        if (i < n) {
+            if (s > 0.0f) v[j] = __fdiv_rn(v[j], s);
+            if (!(v[j] > -INFINITY)) v[j] = -INFINITY;  // NaN is never chosen
+        }
+    }
+    int got = 0;
+    for (int k = 0; k < top_k; k++) {
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < RT_PER; j++)
+            if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int oi = __shfl_xor(bi, o);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if (!(bv > -INFINITY)) break;
+#pragma unroll
+        for (int j = 0; j < RT_PER; j++)
+            if (lane + 64 * j == bi) v[j] = -INFINITY;
+        if (lane == 0) { ids[k] = bi; chosen[k] = bv; }
+        got = k + 1;
+    }
+    if (lane == 0) {
+        float sw = 0.0f;
+        if (norm_topk)
+            for (int k = 0; k < got; k++) sw = __fadd_rn(sw, chosen[k]);
+        for (int k = 0; k < got; k++) w[k] = (norm_topk && sw > 0.0f) ? __fdiv_rn(chosen[k], sw) : chosen[k];
+        for (int k = got; k < top_k; k++) { ids[k] = -1; w[k] = 0.0f; }
+    }
+}
+
 // ---- SiLU(g) * u (qwen3_moe_model.rs:518-522, model.rs:527-531) ----------
 __global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ g,
                                                   const float* __restrict__ u,
@@ -142,30 +240,31 @@ __global__ __launch_bounds__(256) void k_silu_mul(const float* __restrict__ g,
 
 // ---- mlp_out = sum over chosen k of w_k * y_k (qwen3_moe_model.rs:526-528)
 // in chosen order from 0; slots with id < 0 were never run.
+// With `add`, out = add + that sum (residual[i] += mlp_out[i], :531-533).
 __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ ys,
                                                  const int32_t* __restrict__ ids,
                                                  const float* __restrict__ w, int top_k,
-                                                 float* __restrict__ out, int h)
+                                                 float* out, int h, const float* add)
 {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= h) return;
     float acc = 0.0f;
     for (int k = 0; k < top_k; k++)
         if (ids[k] >= 0) acc = __fadd_rn(acc, __fmul_rn(w[k], ys[(size_t)k * h + i]));
-    out[i] = acc;
+    out[i] = add ? __fadd_rn(add[i], acc) : acc;
 }
 
 }  // namespace
 
-hipError_t launch_dense(const float* wt, int out_f, int in_f, int mode, const float* x,
+hipError_t launch_dense(const float* w, int out_f, int in_f, int mode, const float* x,
                         const float* bias, float* y, hipStream_t s)
 {
     (void)hipGetLastError();
     if (mode == WPCG_MODE_EXACT)
-        hipLaunchKernelGGL(k_dense_exact, dim3((out_f + 63) / 64), dim3(64), 0, s, wt, x, bias, y,
+        hipLaunchKernelGGL(k_dense_exact, dim3((out_f + 63) / 64), dim3(64), 0, s, w, x, bias, y,
                            out_f, in_f);
     else
-        hipLaunchKernelGGL(k_dense_fast, dim3((out_f + 3) / 4), dim3(256), 0, s, wt, x, bias, y,
+        hipLaunchKernelGGL(k_dense_fast, dim3((out_f + 3) / 4), dim3(256), 0, s, w, x, bias, y,
                            out_f, in_f);
     return hipGetLastError();
 }
@@ -196,11 +295,19 @@ hipError_t launch_silu_mul(const float* g, const float* u, float* out, size_t n,
 }
 
 hipError_t launch_combine(const float* ys, const int32_t* ids, const float* w, int top_k,
-                          float* out, int h, hipStream_t s)
+                          float* out, int h, const float* add, hipStream_t s)
 {
     if (h == 0) return hipSuccess;
     (void)hipGetLastError();
-    hipLaunchKernelGGL(k_combine, dim3((h + 255) / 256), dim3(256), 0, s, ys, ids, w, top_k, out, h);
+    hipLaunchKernelGGL(k_combine, dim3((h + 255) / 256), dim3(256), 0, s, ys, ids, w, top_k, out, h, add);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax_route(const float* scores, int n, int top_k, int norm_topk, int32_t* ids,
+                                float* w, hipStream_t s)
+{
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k_softmax_route, dim3(1), dim3(64), 0, s, scores, n, top_k, norm_topk, ids, w);
     return hipGetLastError();
 }
 

@@ -131,7 +131,7 @@ int plan_kslices(uint64_t rows, uint64_t nb, int kg);
 int make_plan(const DeviceMatrix& m, FastPlan& plan, hipStream_t s, int kg = 0);
 
 // ---- MoE pieces (moe.hip) -------------------------------------------------
-hipError_t launch_dense(const float* wt, int out_f, int in_f, int mode, const float* x,
+hipError_t launch_dense(const float* w, int out_f, int in_f, int mode, const float* x,
                         const float* bias, float* y, hipStream_t s);
 hipError_t launch_softmax(float* x, int n, hipStream_t s);
 int route_max_n();
@@ -139,7 +139,11 @@ hipError_t launch_route(const float* p, int n, int top_k, int norm_topk, int32_t
                         hipStream_t s);
 hipError_t launch_silu_mul(const float* g, const float* u, float* out, size_t n, hipStream_t s);
 hipError_t launch_combine(const float* ys, const int32_t* ids, const float* w, int top_k,
-                          float* out, int h, hipStream_t s);
+                          float* out, int h, const float* add, hipStream_t s);
+hipError_t launch_softmax_route(const float* scores, int n, int top_k, int norm_topk, int32_t* ids,
+                                float* w, hipStream_t s);
+// The routed MLP of one layer: out = (add ? add + : ) sum_k w_k expert_k(x).
+int moe_run(wpcg_moe* m, const float* x, float* out, const float* add, hipStream_t s);
 
 // ---- decode step (decode.hip) ----------------------------------------------
 // Device-resident position and token bookkeeping of a decode: the step at
@@ -152,13 +156,13 @@ hipError_t launch_embed_tok(const DeviceMatrix& m, const uint32_t* tokens, const
                             float* out, hipStream_t s);
 hipError_t launch_rms_norm(int mode, const float* x, const float* w, int n, float eps, float* out,
                            hipStream_t s);
-hipError_t launch_head_norm_rope(int mode, float* q, const float* k, const float* v, const float* qn,
-                                 const float* kn, int nh, int nkv, int hd, float eps,
-                                 const float* cos_t, const float* sin_t, const DecodeState* st,
-                                 float* kc, float* vc, hipStream_t s);
-hipError_t launch_attention(int mode, const float* q, const float* kc, const float* vc, int nh,
-                            int nkv, int hd, int max_pos, float scale, const DecodeState* st,
-                            float* scores, float* out, hipStream_t s);
+// q/k RMSNorm + RoPE, KV append, scores, softmax and output of one layer's
+// attention at the state's position; max_pos <= attention_max_pos().
+int attention_max_pos();
+hipError_t launch_attention(int mode, const float* q, const float* k, const float* v, const float* qn,
+                            const float* kn, int nh, int nkv, int hd, float eps, float scale,
+                            const float* cos_t, const float* sin_t, const DecodeState* st, float* kc,
+                            float* vc, float* out, hipStream_t s);
 hipError_t launch_add(float* x, const float* y, int n, hipStream_t s);
 hipError_t launch_argmax_next(const float* logits, int n, DecodeState* st, uint32_t* tokens,
                               hipStream_t s);
@@ -212,7 +216,7 @@ struct wpcg_linear {
 struct wpcg_dense {
     wpcg_ctx* ctx = nullptr;
     uint64_t out_f = 0, in_f = 0;
-    float* wt = nullptr;    // device, transposed: wt[i*out_f + r] = W[r][i]
+    float* w = nullptr;     // device, row-major [out_f][in_f]
     float* bias = nullptr;  // device or null
     int mode = WPCG_MODE_EXACT;
 };

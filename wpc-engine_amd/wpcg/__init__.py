@@ -96,6 +96,7 @@ _SIGS = {
     "wpcg_model_load_artifact": (C.c_int, [_p, _p]),
     "wpcg_model_set_mode": (C.c_int, [_p, C.c_int]),
     "wpcg_model_reset": (C.c_int, [_p]),
+    "wpcg_model_set_graphs": (C.c_int, [_p, C.c_int]),
     "wpcg_model_position": (C.c_int, [_p, C.POINTER(C.c_uint32)]),
     "wpcg_model_forward_token": (C.c_int, [_p, C.c_uint32, _p, C.POINTER(C.c_uint32)]),
     "wpcg_model_generate": (C.c_int, [_p, _p, C.c_uint32, C.c_uint32, _p, C.POINTER(C.c_float)]),
@@ -667,6 +668,10 @@ class Model:
 
     def reset(self):
         check(lib.wpcg_model_reset(self.h))
+        return self
+
+    def set_graphs(self, enabled: bool):
+        check(lib.wpcg_model_set_graphs(self.h, int(bool(enabled))))
         return self
 
     def position(self) -> int:
