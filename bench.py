@@ -12,6 +12,12 @@ launches are replayed from a HIP graph so host launch cost is not timed.
 value = algorithmic bytes per step x steps / time, with
 bytes(GEMV) = rows*(cols/128)*BPB + 4*cols + 4*rows, BPB = 100 (v3) / 68 (v4).
 
+The metric's second half, decode tok/s of the Qwen3-30B-A3B-shaped v4 model
+is measured in the same run and reported under
+config.decode: greedy generation of 256 tokens after a 256-token prompt,
+every step on the device (one replayed HIP graph per token), with the
+oracle's CPU decode of the same model timed on a bounded sample.
+
 `--gpus N` with N > 1 is refused: this build measures one GPU.
 """
 import argparse
@@ -79,6 +85,87 @@ def cpu_baseline(scheme, shapes, blocks, xs, budget_s):
     }
 
 
+QWEN3_30B_A3B = dict(n_layers=48, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=128, inter=0,
+                     vocab=151936, n_experts=128, top_k=8, moe_inter=768, norm_topk=1, tied=0,
+                     max_pos=512, eps=1e-6, rope_theta=1e6)
+
+
+def decode_token_bytes(c, bpb=68):
+    """Weight bytes one decode token reads: attention, router (fp32), the
+    top-k experts, lm_head (SURVEY-style accounting; KV cache excluded)."""
+    H, hd = c["hidden"], c["head_dim"]
+    qd, kvd = c["n_heads"] * hd, c["n_kv_heads"] * hd
+    blocks = lambda r, k: r * (k // 128) * bpb  # noqa: E731
+    attn = blocks(qd, H) + 2 * blocks(kvd, H) + blocks(H, qd)
+    experts = c["top_k"] * (2 * blocks(c["moe_inter"], H) + blocks(H, c["moe_inter"]))
+    router = c["n_experts"] * H * 4
+    return c["n_layers"] * (attn + experts + router) + blocks(c["vocab"], H)
+
+
+def decode_bench(ctx, wpcg, synth, n_prompt, n_new, cpu_tokens):
+    """Greedy decode of the Qwen3-30B-A3B-shaped v4 model:
+    seeded weights ~N(0, 0.02) encoded as the artifact compiler does; one
+    layer's expert weights are generated and uploaded to every layer (48
+    distinct device copies, distinct routers), so every token reads
+    1.66 GB of distinct HBM. Returns the record's `decode` object."""
+    import numpy as np
+    cfg = QWEN3_30B_A3B
+    t0 = time.perf_counter()
+    model = wpcg.Model(ctx, wpcg.SCHEME_V4, wpcg.ModelConfig(**cfg))
+    keep = {} if cpu_tokens else None
+    resident = 0
+    for name, arr in synth.model_tensors(cfg, 4, 30, wpcg.encode, share_experts=True):
+        model.set_tensor(name, arr)
+        resident += arr.nbytes
+        if keep is not None:
+            keep[name] = arr
+    log(f"decode model built in {time.perf_counter() - t0:.1f} s ({resident / 1e9:.2f} GB resident)")
+    prompt = np.random.default_rng(31).integers(0, cfg["vocab"], n_prompt).astype(np.uint32)
+    out = {}
+    for mode, key, n in ((wpcg.MODE_FAST, "fast", n_new), (wpcg.MODE_EXACT, "exact", 16)):
+        model.set_mode(mode)
+        model.generate(prompt, n)            # warm-up (graph capture)
+        ids, ms = model.generate(prompt, n)
+        out[key] = ((n - 1) / (ms / 1e3), ms / (n - 1), ids)
+        log(f"decode {key}: {out[key][0]:.1f} tok/s ({out[key][1]:.3f} ms/token, {n - 1} steps)")
+    same = int(np.argmax(np.concatenate([out["fast"][2][:16] != out["exact"][2], [True]])))
+    tok_bytes = decode_token_bytes(cfg)
+    rec = {
+        "model": "Qwen3-30B-A3B-shaped, v4 (48 layers, hidden 2048, 32q/4kv x 128, 128 experts top-8, "
+                 "moe_inter 768, vocab 151936, fp32 router)",
+        "mode": "fast",
+        "prompt_tokens": int(n_prompt),
+        "new_tokens": int(n_new),
+        "tok_s": round(out["fast"][0], 2),
+        "ms_per_token": round(out["fast"][1], 4),
+        "exact_tok_s": round(out["exact"][0], 2),
+        "fast_ids_equal_exact_first16": same,
+        "weight_bytes_per_token": tok_bytes,
+        "roofline_tok_s": round(PEAK_GBPS * 1e9 / tok_bytes, 1),
+        "resident_gb": round(resident / 1e9, 2),
+        "data": "synthetic: weights N(0,0.02) then v4-encoded, norms 1.0; one layer's experts "
+                "replicated to all layers (distinct device copies)",
+    }
+    if cpu_tokens:
+        import oracle as O
+        kern = O.KERNEL_AVX2 if O.have_avx2() else O.KERNEL_FUSED
+        threads = max(1, min(16, os.cpu_count() or 1))
+        ref = O.Model(cfg, keep, cfg["max_pos"], kern, threads)
+        ref.forward_token(int(prompt[0]))    # warm-up
+        t1 = time.perf_counter()
+        for i in range(cpu_tokens):
+            ref.forward_token(int(prompt[1 + i]))
+        dt = time.perf_counter() - t1
+        ref.close()
+        rec["cpu_baseline"] = {"tok_s": round(cpu_tokens / dt, 3), "cores": threads, "kind": "port",
+                               "sample": f"{cpu_tokens} forward_token steps at positions 1..{cpu_tokens} "
+                                         f"of the same model on the host (oracle restatement, "
+                                         f"{'AVX2' if kern == O.KERNEL_AVX2 else 'scalar'} GEMV)"}
+        log(f"decode CPU baseline {rec['cpu_baseline']['tok_s']} tok/s on {threads} threads")
+    model.close()
+    return rec
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -94,6 +181,11 @@ def main():
                     help="leave through the runtime's exit path (profilers finalize there)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short run for rocprofv3 --pmc passes (no timing, no JSON)")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip the Qwen3-30B-A3B-shaped decode measurement")
+    ap.add_argument("--decode-prompt", type=int, default=256)
+    ap.add_argument("--decode-new", type=int, default=256)
+    ap.add_argument("--decode-cpu-tokens", type=int, default=4)
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -230,6 +322,14 @@ def main():
         cpu = cpu_baseline(scheme, QWEN3_4B, blocks, xs, args.cpu_seconds)
         log(f"CPU baseline {cpu['value']} GB/s on {cpu['cores']} threads")
 
+    decode = None
+    if not args.no_decode:
+        for lst in sets:  # free the rotated GEMV copies first
+            for l in lst:
+                l.close()
+        decode = decode_bench(ctx, wpcg, synth, args.decode_prompt, args.decode_new,
+                              0 if args.no_cpu_baseline else args.decode_cpu_tokens)
+
     kname = f"k_gemv_exact<{scheme}>" if mode == wpcg.MODE_EXACT else f"k_gemv_fast<{scheme}>"
     rec = {
         "metric": METRIC,
@@ -253,6 +353,7 @@ def main():
             "pct_of_peak": round(100 * value / PEAK_GBPS, 2),
             "launches_per_step": n_launch // steps,
             f"{other}_mode_gbps": round(o_val, 2),
+            "decode": decode,
         },
         "roofline": {
             "bound": "hbm",
