@@ -166,6 +166,86 @@ def decode_bench(ctx, wpcg, synth, n_prompt, n_new, cpu_tokens):
     return rec
 
 
+GEMMA_12B = [("gate/up_proj", 15360, 3840), ("down_proj", 3840, 15360)]
+MFMA_BF16_TFLOPS = 2500.0  # MI355X dense bf16
+
+
+def bf16_bits(x):
+    """fp32 -> bf16 bit patterns (round to nearest even, finite inputs)."""
+    import numpy as np
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def gemm_bench(ctx, wpcg, synth, cpu):
+    """batched v4 dequant-GEMM on the Gemma-12B-shaped
+    gate/up (15360x3840) and down (3840x15360) matrices, M in {1, 4, 16, 64}
+    activations (bf16 for M >= 4; M = 1 is the fp32 GEMV), HBM-cold over 34
+    rotated copies (1.07 GB), replayed from a HIP graph. The time of a call
+    includes every launch it makes (for M > 16 the X packing kernel too).
+    Bytes = W + M*K*2 (bf16 X; 4 for the fp32 GEMV) + M*N*4."""
+    import numpy as np
+    e0, e1 = ctx.event(), ctx.event()
+    out = {}
+    for name, rows, cols in GEMMA_12B:
+        base = wpcg.WpcLinear.from_blocks(ctx, 4, synth.random_v4_blocks(rows, cols, 41), rows, cols)
+        base.set_mode(wpcg.MODE_FAST)
+        wbytes = rows * (cols // 128) * 68
+        lins = [base] + [base.clone() for _ in range(-(-int(1.0e9) // wbytes) - 1)]
+        for M in (1, 4, 16, 64):
+            X = np.random.default_rng(M).standard_normal((M, cols)).astype(np.float32)
+            dt = wpcg.DTYPE_F32 if M == 1 else wpcg.DTYPE_BF16
+            xd = ctx.upload(X if M == 1 else bf16_bits(X))
+            yd = ctx.alloc(M * rows * 4)
+            body = lambda: [l.gemm_dev(xd, M, yd, dt) for l in lins]
+            body()
+            ctx.sync()
+            g = ctx.capture(body)
+            g.launch()
+            ctx.sync()
+            reps = 10
+            e0.record()
+            for _ in range(reps):
+                g.launch()
+            e1.record()
+            ctx.sync()
+            us = e0.elapsed_ms(e1) * 1e3 / (reps * len(lins))
+            alg = wbytes + M * cols * (4 if M == 1 else 2) + M * rows * 4
+            tflops = 2.0 * M * rows * cols / us / 1e6
+            out[f"{name} M={M}"] = {"us": round(us, 3), "gbps": round(alg / us / 1e3, 1),
+                                    "frac_hbm": round(alg / us / 1e3 / PEAK_GBPS, 4),
+                                    "tflops": round(tflops, 1),
+                                    "frac_mfma_bf16": round(tflops / MFMA_BF16_TFLOPS, 4)}
+            log(f"gemm {name} M={M}: {us:.2f} us, {alg / us / 1e3:.0f} GB/s, {tflops:.1f} TFLOP/s")
+            del g
+            xd.free()
+            yd.free()
+        for l in lins:
+            l.close()
+    rec = {"workload": "cfg4: batched v4 dequant-GEMM, Gemma-12B gate/up 15360x3840 and down 3840x15360, "
+                       "HBM-cold, bf16 X for M >= 4 (matrix cores), fp32 x GEMV for M = 1",
+           "results": out}
+    if cpu:
+        import oracle as O
+        rows, cols = GEMMA_12B[0][1], GEMMA_12B[0][2]
+        blocks = synth.random_v4_blocks(rows, cols, 41)
+        X = np.random.default_rng(4).standard_normal((4, cols)).astype(np.float32)
+        kern = O.KERNEL_AVX2 if O.have_avx2() else O.KERNEL_FUSED
+        threads = max(1, min(16, os.cpu_count() or 1))
+        O.linear_matmul_v4(blocks, rows, cols, X[:1], kern, threads)  # warm-up
+        t1 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t1 < 2.0 or n < 2:
+            O.linear_matmul_v4(blocks, rows, cols, X, kern, threads)
+            n += 1
+        us = (time.perf_counter() - t1) / n * 1e6
+        rec["cpu_baseline"] = {"us_gate_up_M4": round(us, 1), "cores": threads, "kind": "port",
+                               "sample": f"{n} calls of 4 per-token matvecs (the reference's path for a "
+                                         f"batch) on the gate/up matrix, oracle AVX2 restatement"}
+        log(f"gemm CPU baseline: gate/up M=4 {us:.0f} us on {threads} threads")
+    return rec
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -186,6 +266,7 @@ def main():
     ap.add_argument("--decode-prompt", type=int, default=256)
     ap.add_argument("--decode-new", type=int, default=256)
     ap.add_argument("--decode-cpu-tokens", type=int, default=4)
+    ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM (config 4) lines")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -322,11 +403,15 @@ def main():
         cpu = cpu_baseline(scheme, QWEN3_4B, blocks, xs, args.cpu_seconds)
         log(f"CPU baseline {cpu['value']} GB/s on {cpu['cores']} threads")
 
+    for lst in sets:  # free the rotated GEMV copies first
+        for l in lst:
+            l.close()
+    gemm = None
+    if not args.no_gemm:
+        gemm = gemm_bench(ctx, wpcg, synth, not args.no_cpu_baseline)
+
     decode = None
     if not args.no_decode:
-        for lst in sets:  # free the rotated GEMV copies first
-            for l in lst:
-                l.close()
         decode = decode_bench(ctx, wpcg, synth, args.decode_prompt, args.decode_new,
                               0 if args.no_cpu_baseline else args.decode_cpu_tokens)
 
@@ -354,6 +439,7 @@ def main():
             "launches_per_step": n_launch // steps,
             f"{other}_mode_gbps": round(o_val, 2),
             "decode": decode,
+            "gemm": gemm,
         },
         "roofline": {
             "bound": "hbm",

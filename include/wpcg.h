@@ -159,6 +159,31 @@ int wpcg_linear_matvec_host(wpcg_linear* lin, const float* x, float* y);
 int wpcg_linear_matvec_multi(int n, wpcg_linear* const* lins, const float* const* xs,
                              float* const* ys, wpcg_stream stream);
 
+/* Batched GEMM Y = X W^T (+ bias on every row of Y) for M activations.
+ * No reference counterpart: the reference runs one token at a time, and
+ * names batched prefill its principal missing piece (README.md:174-180).
+ * X: M rows of in_f values, contiguous, fp32 (x_dtype WPCG_DTYPE_F32) or
+ * bf16 bit patterns (WPCG_DTYPE_BF16); Y: M rows of out_f floats. With
+ * M == 1 and fp32 X this is wpcg_linear_matvec in the linear's mode. Else
+ * the matrix-core kernel runs (64 rows of X per launch pair): the codes
+ * are exact, X is rounded to bf16 (exact when given as bf16), each block's
+ * dots accumulate in fp32 and its scale and zero point are applied in fp32
+ * (the weights are never rounded). The first batched call on a linear
+ * allocates its workspace (about 16 KiB per 128 inputs plus the split-K
+ * partials); make it before capturing a graph that contains the call. */
+#define WPCG_DTYPE_F32  0
+#define WPCG_DTYPE_BF16 1
+int wpcg_linear_gemm(wpcg_linear* lin, const void* x_dev, int x_dtype, uint32_t M, float* y_dev,
+                     wpcg_stream stream);
+/* Host-pointer twin (synchronous). */
+int wpcg_linear_gemm_host(wpcg_linear* lin, const void* x, int x_dtype, uint32_t M, float* y);
+/* K-slices of the batched kernels (0 = the library's choice; a tuning knob,
+ * no reference counterpart), applied to both (M <= 16 and M > 16) within
+ * their limits. Frees the workspace; the next batched call makes it. The
+ * query returns the splits in use (or planned) for M <= 16 and M > 16. */
+int wpcg_linear_set_gemm_kslices(wpcg_linear* lin, int kslices);
+int wpcg_linear_gemm_kslices(wpcg_linear* lin, int* kslices_small, int* kslices);
+
 /* EmbeddingTable::embed (weights.rs:28; wpc_weights_v4.rs:241-249): decode
  * row `token` into out (in_f floats) as zp + code*scale with two roundings.
  * EmbeddingTable::logits (weights.rs:30) is wpcg_linear_matvec on the same

@@ -454,6 +454,7 @@ int wpcg_linear_destroy(wpcg_linear* L)
     (void)hipStreamSynchronize(L->ctx->stream);
     free_matrix(L->m);
     free_plan(L->plan);
+    free_gemm(L->gemm);
     if (L->bias) (void)hipFree(L->bias);
     if (L->x_stage) (void)hipFree(L->x_stage);
     if (L->y_stage) (void)hipFree(L->y_stage);
@@ -625,6 +626,7 @@ int wpcg_linear_clone(wpcg_linear* L, wpcg_linear** out)
     c->m.codes = c->m.hp = nullptr;
     c->m.params = nullptr;
     c->mode = L->mode;
+    c->gemm.kg_req = L->gemm.kg_req;  // the same batched split, made on first use
     const uint64_t nb = plane_blocks(L->m);
     hipStream_t s = L->ctx->stream;
     if (int rc = make_plan(c->m, c->plan, s, L->plan.kg)) {  // same split: same results

@@ -1,0 +1,733 @@
+// Batched dequant-GEMM Y = X W^T for M >= 2 activations (multi-sequence
+// decode, chunked prefill) on the bf16 matrix cores of gfx950.
+//
+// The weights are used as they sit in HBM (tile-major planes, see
+// wpcg_internal.hpp) and are never dequantized: the integer codes (0..15 or
+// 0..63) are exact in bf16, so v_mfma_f32_16x16x32_bf16 gives, per 16-row
+// tile and 128-value block b, the dots D = sum code * x over the block with
+// exact products and fp32 accumulation. Each block then adds
+//     scale * D + zp * S_b,   S_b = sum of the block's x (per column)
+// in fp32, which is the block's w = zp + code * scale without ever rounding
+// w. The only rounding of inputs is x to bf16 (none when X is given in
+// bf16). (The matrix cores are fed 128 + code, one byte permute per two
+// codes; see codes_bf16.)
+//
+// k-order. A lane of group g (lanes 16g..16g+15) of a tile's 16-byte code
+// word holds the codes of k = 8q + g + 4h (q < 8, h < 2; low nibbles) and
+// k + 64 (high nibbles), so for kstep i (0..3) lane group g feeds the
+// matrix core the eight values of
+//     k(i, g, s) = 8s + g + 4(i & 1) + 64(i >> 1),   s = 0..7
+// and X is packed once per call into that order (k_gemm_pack): fragment
+// (block b, column tile n, kstep i) is 64 lanes x 8 bf16, lane g*16 + c
+// holding column n*16 + c.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "wpcg_internal.hpp"
+
+namespace wpcg {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ int gk(int i, int g, int s) { return 8 * s + g + 4 * (i & 1) + 64 * (i >> 1); }
+
+__device__ __forceinline__ float h2f(uint32_t bits)
+{
+    _Float16 h;
+    uint16_t b = (uint16_t)bits;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+}
+
+// Two floats to packed bf16 (round to nearest even), low half first.
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b)
+{
+    const f32x2 f = {a, b};
+    const bf16x2 h = __builtin_convertvector(f, bf16x2);
+    uint32_t r;
+    __builtin_memcpy(&r, &h, 4);
+    return r;
+}
+__device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+constexpr int CPOL_NT = 2;   // streamed once
+constexpr int CPOL_SC1 = 16; // coherent across the device's L2s (agent scope)
+
+// ---- X -> bf16 fragments in k(i, g, s) order, plus per-block column sums
+// of the rounded values. One workgroup per (block, column tile): wave i is
+// kstep i, lane g*16 + c column c.
+template <bool BF16_IN>
+__global__ __launch_bounds__(256) void k_gemm_pack(const void* __restrict__ X, int M, int K, int NT,
+                                                   u32x4* __restrict__ xf, float* __restrict__ xsum)
+{
+    __shared__ float red[4][16];
+    const int b = blockIdx.x / NT, n = blockIdx.x % NT;
+    const int i = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    const int m = n * 16 + c;
+    float v[8];
+#pragma unroll
+    for (int s = 0; s < 8; s++) {
+        const size_t k = (size_t)b * 128 + gk(i, g, s);
+        if (m >= M)
+            v[s] = 0.0f;
+        else if constexpr (BF16_IN)
+            v[s] = __uint_as_float((uint32_t)static_cast<const uint16_t*>(X)[(size_t)m * K + k] << 16);
+        else
+            v[s] = static_cast<const float*>(X)[(size_t)m * K + k];
+    }
+    u32x4 o;
+    o.x = pk_bf16(v[0], v[1]);
+    o.y = pk_bf16(v[2], v[3]);
+    o.z = pk_bf16(v[4], v[5]);
+    o.w = pk_bf16(v[6], v[7]);
+    xf[((size_t)(b * NT + n) * 4 + i) * 64 + lane] = o;
+    float sum = ((bf16_lo(o.x) + bf16_hi(o.x)) + (bf16_lo(o.y) + bf16_hi(o.y))) +
+                ((bf16_lo(o.z) + bf16_hi(o.z)) + (bf16_lo(o.w) + bf16_hi(o.w)));
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    if (g == 0) red[i][c] = sum;
+    __syncthreads();
+    if (threadIdx.x < 16)
+        xsum[(size_t)b * NT * 16 + n * 16 + threadIdx.x] =
+            (red[0][threadIdx.x] + red[1][threadIdx.x]) + (red[2][threadIdx.x] + red[3][threadIdx.x]);
+}
+
+struct GemmArgs {
+    const uint8_t* codes;
+    const uint8_t* hp;
+    const uint32_t* params;
+    const u32x4* xf;     // packed X, [nb][NT][4][64] fragments
+    const float* xsum;   // [nb][NT*16]
+    float* y;            // [M][rows]
+    const float* bias;   // [rows] or null
+    float* part;         // [kg][NT*16][rows_pad] (kg > 1)
+    uint32_t* counters;  // one per row group (kg > 1), self-resetting
+    int rows, rows_pad, nb, M, kg;
+};
+
+constexpr int GM_WG = GEMM_WG_THREADS;  // 4 waves (row tiles per workgroup: 4 * GM_RT)
+constexpr int GM_WG8 = 2 * GM_WG;       // the M > 16 kernel: two waves per tile pair
+constexpr int GM_RT = GEMM_TILES_PER_WAVE;
+constexpr int GM_LA = 4;                // blocks of codes and of X in flight per wave
+
+// Eight codes (two dwords of one byte each, every code < 128) -> the eight
+// bf16 values 128 + code, exact: their bit patterns are 0x4300 | code, so
+// one byte permute makes two of them. The matrix cores then return
+// D' = sum (128 + code) x = D + 128 S, and a block adds
+// scale * D' + (zp - 128 scale) * S, which is scale * D + zp * S.
+__device__ __forceinline__ bf16x8 codes_bf16(uint32_t a, uint32_t b)
+{
+    u32x4 r;
+    r.x = __builtin_amdgcn_perm(0x43434343u, a, 0x04010400u);
+    r.y = __builtin_amdgcn_perm(0x43434343u, a, 0x04030402u);
+    r.z = __builtin_amdgcn_perm(0x43434343u, b, 0x04010400u);
+    r.w = __builtin_amdgcn_perm(0x43434343u, b, 0x04030402u);
+    bf16x8 o;
+    __builtin_memcpy(&o, &r, 16);
+    return o;
+}
+// zero point of the offset codes: zp - 128 * scale
+__device__ __forceinline__ float zp_off(uint32_t p) { return __builtin_fmaf(-128.0f, h2f(p >> 16), h2f(p & 0xFFFFu)); }
+
+// A workgroup of 8 waves computes 4 * GM_RT row tiles for all NT*16
+// columns over one K-slice: wave w takes tiles (rg*4 + (w&3))*GM_RT.. and
+// the column tiles of half w>>2, so the two waves of a tile pair read the
+// same codes (the second read is a cache hit) and each runs half the matrix
+// work. Per block: the slice's X fragments come through LDS (double
+// buffered, shared by all waves), fetched into registers GM_LA blocks
+// ahead; the codes come straight from HBM into registers, GM_LA blocks
+// ahead. Every buffer load has an exact range, so loads past the slice
+// return zeros (a zero block adds exactly 0).
+template <int SCHEME, int NT>
+__global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
+{
+    constexpr int NTH = (NT + 1) / 2;          // column tiles of the first half
+    constexpr int XV = (NT * 4096 + GM_WG8 * 16 - 1) / (GM_WG8 * 16);  // 16-byte X loads per thread per block
+    __shared__ __align__(16) u32x4 xb[2][NT * 4 * 64];
+    __shared__ float xsb[2][NT * 16];
+    __shared__ int s_last;
+
+    const int kg = P.kg, nb = P.nb;
+    const int kgi = blockIdx.x % kg, rg = blockIdx.x / kg;
+    const int nbk = (nb + kg - 1) / kg;
+    const int b0 = min(kgi * nbk, nb);
+    const int nbl = max(0, min(nb, b0 + nbk) - b0);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int g = lane >> 4, j = lane & 15;
+    const int ntiles = P.rows_pad / TILE_ROWS;
+    const int T0 = (rg * 4 + (wave & 3)) * GM_RT;
+    const int ch = wave >> 2;                   // column half
+    const int n0 = ch * NTH, n1 = ch ? NT : NTH;  // column tiles [n0, n1) (uniform)
+
+    __amdgpu_buffer_rsrc_t crs[GM_RT], hrs[GM_RT], prs[GM_RT];
+#pragma unroll
+    for (int rt = 0; rt < GM_RT; rt++) {
+        const int T = T0 + rt;
+        const bool ok = T < ntiles;
+        const size_t rec = (size_t)min(T, ntiles - 1) * nb + b0;
+        crs[rt] = buf_rsrc(P.codes + rec * CODE_REC, ok ? nbl * (int)CODE_REC : 0);
+        hrs[rt] = buf_rsrc((SCHEME == 3 ? P.hp : P.codes) + rec * HP_REC,
+                           ok && SCHEME == 3 ? nbl * (int)HP_REC : 0);
+        prs[rt] = buf_rsrc(P.params + rec * TILE_ROWS, ok ? nbl * TILE_ROWS * 4 : 0);
+    }
+    const auto xrs = buf_rsrc(P.xf + (size_t)b0 * NT * 256, nbl * NT * 4096);
+    const auto srs = buf_rsrc(P.xsum + (size_t)b0 * NT * 16, nbl * NT * 64);
+
+    u32x4 cr[GM_LA][GM_RT], pr[GM_LA][GM_RT];
+    u32x2 hr[GM_LA][GM_RT];
+    auto load_codes = [&](int u, int b) {
+#pragma unroll
+        for (int rt = 0; rt < GM_RT; rt++) {
+            cr[u][rt] = __builtin_amdgcn_raw_buffer_load_b128(crs[rt], b * (int)CODE_REC + lane * 16, 0, CPOL_NT);
+            if constexpr (SCHEME == 3)
+                hr[u][rt] = __builtin_amdgcn_raw_buffer_load_b64(hrs[rt], b * (int)HP_REC + lane * 8, 0, CPOL_NT);
+            pr[u][rt] = __builtin_amdgcn_raw_buffer_load_b128(prs[rt], b * 64 + g * 16, 0, CPOL_NT);
+        }
+    };
+    // X of block b: thread t holds 16-byte words t + v*GM_WG8 of the block's
+    // NT*256 words (a word past the block is never stored)
+    u32x4 xr[GM_LA][XV];
+    float sr[GM_LA];
+    auto load_x = [&](int u, int b) {
+#pragma unroll
+        for (int v = 0; v < XV; v++)
+            xr[u][v] = __builtin_amdgcn_raw_buffer_load_b128(
+                xrs, (b * NT * 256 + min((int)threadIdx.x + v * GM_WG8, NT * 256 - 1)) * 16, 0, 0);
+        sr[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            srs, (b * NT * 16 + min((int)threadIdx.x, NT * 16 - 1)) * 4, 0, 0));
+    };
+    auto store_x = [&](int u, int buf) {
+#pragma unroll
+        for (int v = 0; v < XV; v++) {
+            const int w = threadIdx.x + v * GM_WG8;
+            if (w < NT * 256) xb[buf][w] = xr[u][v];
+        }
+        if (threadIdx.x < NT * 16) xsb[buf][threadIdx.x] = sr[u];
+    };
+
+#pragma unroll
+    for (int u = 0; u < GM_LA; u++) load_x(u, u);
+#pragma unroll
+    for (int u = 0; u < GM_LA; u++) load_codes(u, u);
+    store_x(0, 0);
+    __syncthreads();
+
+    f32x4 acc[GM_RT][NTH];
+#pragma unroll
+    for (int rt = 0; rt < GM_RT; rt++)
+#pragma unroll
+        for (int n = 0; n < NTH; n++) acc[rt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Whole rounds of GM_LA unconditional steps (guarded steps would merge
+    // the wait-counter state at the loop edge and drain every load in
+    // flight once per round). Step b: fetch X(b + GM_LA) into the register
+    // slot X(b) left (it went to LDS a step ago), compute block b, refill
+    // the codes slot, move X(b+1) into the other LDS buffer, barrier.
+    const int steps = (nbl + GM_LA - 1) / GM_LA * GM_LA;
+    for (int bl = 0; bl < steps; bl += GM_LA) {
+#pragma unroll
+        for (int u = 0; u < GM_LA; u++) {
+            const int b = bl + u, buf = u & 1;
+            load_x(u, b + GM_LA);
+            bf16x8 A[GM_RT][4];
+            float sc[GM_RT][4], zp[GM_RT][4];
+#pragma unroll
+            for (int rt = 0; rt < GM_RT; rt++) {
+                const u32x4 U = cr[u][rt];
+                const uint32_t MK = 0x0F0F0F0Fu;
+                u32x4 lo = {U.x & MK, U.y & MK, U.z & MK, U.w & MK};
+                u32x4 hi = {(U.x >> 4) & MK, (U.y >> 4) & MK, (U.z >> 4) & MK, (U.w >> 4) & MK};
+                if constexpr (SCHEME == 3) {
+                    const uint32_t T6 = 0x30303030u, hx = hr[u][rt].x, hy = hr[u][rt].y;
+                    lo.x |= (hx << 4) & T6; lo.y |= (hx << 2) & T6;
+                    lo.z |= (hy << 4) & T6; lo.w |= (hy << 2) & T6;
+                    hi.x |= hx & T6;        hi.y |= (hx >> 2) & T6;
+                    hi.z |= hy & T6;        hi.w |= (hy >> 2) & T6;
+                }
+                A[rt][0] = codes_bf16(lo.x, lo.y);
+                A[rt][1] = codes_bf16(lo.z, lo.w);
+                A[rt][2] = codes_bf16(hi.x, hi.y);
+                A[rt][3] = codes_bf16(hi.z, hi.w);
+                const u32x4 p = pr[u][rt];
+                sc[rt][0] = h2f(p.x >> 16); zp[rt][0] = zp_off(p.x);
+                sc[rt][1] = h2f(p.y >> 16); zp[rt][1] = zp_off(p.y);
+                sc[rt][2] = h2f(p.z >> 16); zp[rt][2] = zp_off(p.z);
+                sc[rt][3] = h2f(p.w >> 16); zp[rt][3] = zp_off(p.w);
+            }
+            load_codes(u, b + GM_LA);
+#pragma unroll
+            for (int nn = 0; nn < NTH; nn++) {
+                const int n = n0 + nn;
+                if (n < n1) {  // uniform
+                    bf16x8 B[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const u32x4 w = xb[buf][(n * 4 + i) * 64 + lane];
+                        __builtin_memcpy(&B[i], &w, 16);
+                    }
+                    const float S = xsb[buf][n * 16 + j];
+                    f32x4 D[GM_RT];
+#pragma unroll
+                    for (int rt = 0; rt < GM_RT; rt++) D[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+#pragma unroll
+                        for (int rt = 0; rt < GM_RT; rt++)
+                            D[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[rt][i], B[i], D[rt], 0, 0, 0);
+#pragma unroll
+                    for (int rt = 0; rt < GM_RT; rt++)
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+                            acc[rt][nn][q] = __builtin_fmaf(zp[rt][q], S, __builtin_fmaf(sc[rt][q], D[rt][q], acc[rt][nn][q]));
+                }
+            }
+            store_x((u + 1) % GM_LA, buf ^ 1);  // X(b+1), fetched GM_LA-1 steps ago
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // lane (g, j) holds rows 4g..4g+3 of each tile for column n*16 + j
+    const int Mp = NT * 16;
+    if (kg == 1) {
+#pragma unroll
+        for (int rt = 0; rt < GM_RT; rt++)
+#pragma unroll
+            for (int nn = 0; nn < NTH; nn++) {
+                const int n = n0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
+                if (n >= n1 || m >= P.M) continue;
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (row + q < P.rows)
+                        P.y[(size_t)m * P.rows + row + q] = P.bias ? acc[rt][nn][q] + P.bias[row + q] : acc[rt][nn][q];
+            }
+        return;
+    }
+    // Split K: publish the slice's partials with coherent stores, then the
+    // last workgroup of the row group adds the kg slices in slice order
+    // (deterministic) and resets the counter. The stores are complete at
+    // the device's coherence point once vmcnt drains, before the barrier
+    // that precedes the counter increment; the last workgroup reads with
+    // coherent loads after it has seen the count.
+    const auto prt = buf_rsrc(P.part, kg * Mp * P.rows_pad * 4);
+#pragma unroll
+    for (int rt = 0; rt < GM_RT; rt++)
+#pragma unroll
+        for (int nn = 0; nn < NTH; nn++) {
+            const int n = n0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
+            if (n < n1 && T0 + rt < ntiles) {
+                u32x4 v;
+                __builtin_memcpy(&v, &acc[rt][nn], 16);
+                __builtin_amdgcn_raw_buffer_store_b128(v, prt, ((kgi * Mp + m) * P.rows_pad + row) * 4, 0, CPOL_SC1);
+            }
+        }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(P.counters + rg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == (uint32_t)(kg - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+#pragma unroll
+    for (int rt = 0; rt < GM_RT; rt++)
+#pragma unroll
+        for (int nn = 0; nn < NTH; nn++) {
+            const int n = n0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
+            if (n >= n1 || T0 + rt >= ntiles || m >= P.M) continue;
+            f32x4 s = {0.f, 0.f, 0.f, 0.f};
+            for (int k = 0; k < kg; k++) {
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(prt, ((k * Mp + m) * P.rows_pad + row) * 4, 0, CPOL_SC1);
+                f32x4 f;
+                __builtin_memcpy(&f, &v, 16);
+                s = k == 0 ? f : s + f;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (row + q < P.rows) P.y[(size_t)m * P.rows + row + q] = P.bias ? s[q] + P.bias[row + q] : s[q];
+        }
+    if (threadIdx.x == 0) __hip_atomic_store(P.counters + rg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- M <= 16: one kernel. The workgroup packs its whole K-slice of X
+// (row-major fp32 or bf16, straight from the caller's buffer) into bf16
+// fragments in LDS; its X loads are issued first, then its first blocks of
+// codes, so the pack waits for X alone. Two waves own each row tile, one
+// per half of the slice, so two waves share every SIMD; each runs its
+// blocks in pairs (two independent matrix-core chains) without barriers,
+// and the halves are added in a fixed order at the end.
+constexpr int GS_WG = 512;
+constexpr int GS_TILES = GS_WG / 128;  // row tiles per workgroup
+constexpr int GS_LA = 10;              // blocks of codes in flight per wave (even)
+
+struct GemmSmallArgs {
+    const uint8_t* codes;
+    const uint8_t* hp;
+    const uint32_t* params;
+    const void* x;       // [M][K] row-major
+    float* y;
+    const float* bias;
+    float* part;         // [kg][16][rows_pad] (kg > 1)
+    uint32_t* counters;
+    int rows, rows_pad, nb, M, kg;
+};
+
+// Eight bf16 of one fragment lane from two consecutive-k pieces: the low
+// (odd = 0) or high (odd = 1) halves of dwords a (slot 2q) and b (slot 2q+1).
+__device__ __forceinline__ uint32_t pick_halves(uint32_t a, uint32_t b, int odd)
+{
+    return odd ? (a >> 16) | (b & 0xFFFF0000u) : (a & 0xFFFFu) | (b << 16);
+}
+
+template <int SCHEME, bool BF16_IN>
+__global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
+{
+    __shared__ __align__(16) u32x4 xb[GEMM_SMALL_MAXBK][4][64];
+    __shared__ float psum[GEMM_SMALL_MAXBK][2][16];
+    __shared__ __align__(16) f32x4 red[GS_TILES][64];
+    __shared__ int s_last;
+
+    const int kg = P.kg, nb = P.nb, K = nb * 128, M = P.M;
+    const int kgi = blockIdx.x % kg, rg = blockIdx.x / kg;
+    const int nbk = (nb + kg - 1) / kg;
+    const int b0 = min(kgi * nbk, nb);
+    const int nbl = max(0, min(nb, b0 + nbk) - b0);  // <= GEMM_SMALL_MAXBK (the planner's rule)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int g = lane >> 4, j = lane & 15;
+    const int ntiles = P.rows_pad / TILE_ROWS;
+    const int T = rg * GS_TILES + (wave % GS_TILES);  // this wave's row tile
+    const bool tile_ok = T < ntiles;
+    const int part_k = wave / GS_TILES;                // half of the slice
+    const int hb = (nbl + 1) / 2;
+    const int kb0 = part_k ? hb : 0;                   // first block (within the slice)
+    const int kn = part_k ? nbl - hb : hb;             // blocks of this half
+
+    // ---- X loads first. Task (blk, c, h), c < M: the 64 values k in
+    // [64h, 64h+64) of row c of block blk, as eight 16-byte pieces of
+    // consecutive k; a thread takes tasks t and t + 512 (ntask <= 960).
+    constexpr int es = BF16_IN ? 2 : 4;
+    constexpr int PIECES = BF16_IN ? 8 : 16;  // 16-byte loads per task
+    const auto xrs = buf_rsrc(static_cast<const uint8_t*>(P.x) + (size_t)b0 * 128 * es,
+                              (int)(((size_t)(M - 1) * K + (size_t)nbl * 128) * es));
+    const int ntask = nbl * 2 * M;
+    u32x4 xv[2][PIECES];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int t = threadIdx.x + r * GS_WG;
+        const int blk = t / (2 * M), c = (t >> 1) % M, h = t & 1;
+        const int base = t < ntask ? (c * K + blk * 128 + 64 * h) * es : 0x7FFFFFF0;  // past the range: zeros
+#pragma unroll
+        for (int p = 0; p < PIECES; p++) xv[r][p] = __builtin_amdgcn_raw_buffer_load_b128(xrs, base + p * 16, 0, 0);
+    }
+
+    // ---- then the first GS_LA blocks of this wave's codes
+    const size_t rec = (size_t)min(T, ntiles - 1) * nb + b0 + kb0;
+    const auto crs = buf_rsrc(P.codes + rec * CODE_REC, tile_ok ? kn * (int)CODE_REC : 0);
+    const auto hrs = buf_rsrc((SCHEME == 3 ? P.hp : P.codes) + rec * HP_REC, tile_ok && SCHEME == 3 ? kn * (int)HP_REC : 0);
+    const auto prs = buf_rsrc(P.params + rec * TILE_ROWS, tile_ok ? kn * TILE_ROWS * 4 : 0);
+    u32x4 cr[GS_LA], pr[GS_LA];
+    u32x2 hr[GS_LA];
+    auto load_codes = [&](int u, int b) {
+        cr[u] = __builtin_amdgcn_raw_buffer_load_b128(crs, b * (int)CODE_REC + lane * 16, 0, CPOL_NT);
+        if constexpr (SCHEME == 3) hr[u] = __builtin_amdgcn_raw_buffer_load_b64(hrs, b * (int)HP_REC + lane * 8, 0, CPOL_NT);
+        pr[u] = __builtin_amdgcn_raw_buffer_load_b128(prs, b * 64 + g * 16, 0, CPOL_NT);
+    };
+#pragma unroll
+    for (int u = 0; u < GS_LA; u++) load_codes(u, u);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- pack: fragment (i = 2h + ii, lane group gg) slot s <- piece s,
+    // element gg + 4 ii. Columns c >= M are zeros.
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int t = threadIdx.x + r * GS_WG;
+        if (t < ntask) {
+            const int blk = t / (2 * M), c = (t >> 1) % M, h = t & 1;
+            uint32_t pc[8][4];
+#pragma unroll
+            for (int p = 0; p < 8; p++) {
+                if constexpr (BF16_IN) {
+                    pc[p][0] = xv[r][p].x; pc[p][1] = xv[r][p].y; pc[p][2] = xv[r][p].z; pc[p][3] = xv[r][p].w;
+                } else {
+                    const u32x4 a = xv[r][2 * p], b = xv[r][2 * p + 1];
+                    pc[p][0] = pk_bf16(__uint_as_float(a.x), __uint_as_float(a.y));
+                    pc[p][1] = pk_bf16(__uint_as_float(a.z), __uint_as_float(a.w));
+                    pc[p][2] = pk_bf16(__uint_as_float(b.x), __uint_as_float(b.y));
+                    pc[p][3] = pk_bf16(__uint_as_float(b.z), __uint_as_float(b.w));
+                }
+            }
+            float sum = 0.0f;
+#pragma unroll
+            for (int p = 0; p < 8; p++)
+#pragma unroll
+                for (int d = 0; d < 4; d++) sum += bf16_lo(pc[p][d]) + bf16_hi(pc[p][d]);
+            psum[blk][h][c] = sum;
+#pragma unroll
+            for (int ii = 0; ii < 2; ii++)
+#pragma unroll
+                for (int gg = 0; gg < 4; gg++) {
+                    const int d = (gg >> 1) + 2 * ii, odd = gg & 1;
+                    u32x4 o;
+                    o.x = pick_halves(pc[0][d], pc[1][d], odd);
+                    o.y = pick_halves(pc[2][d], pc[3][d], odd);
+                    o.z = pick_halves(pc[4][d], pc[5][d], odd);
+                    o.w = pick_halves(pc[6][d], pc[7][d], odd);
+                    xb[blk][2 * h + ii][gg * 16 + c] = o;
+                }
+        }
+    }
+    // zero columns M..15 of every fragment and their sums
+    for (int t = threadIdx.x; t < nbl * 2 * (16 - M); t += GS_WG) {
+        const int blk = t / (2 * (16 - M)), c = M + (t >> 1) % (16 - M), h = t & 1;
+        psum[blk][h][c] = 0.0f;
+#pragma unroll
+        for (int ii = 0; ii < 2; ii++)
+#pragma unroll
+            for (int gg = 0; gg < 4; gg++) xb[blk][2 * h + ii][gg * 16 + c] = u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+
+    // One block: the matrix-core chain (four ksteps) and the fp32 epilogue.
+    auto dots = [&](int u, int b) -> f32x4 {
+        bf16x8 B[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const u32x4 w = xb[kb0 + b][i][lane];
+            __builtin_memcpy(&B[i], &w, 16);
+        }
+        const u32x4 U = cr[u];
+        const uint32_t MK = 0x0F0F0F0Fu;
+        u32x4 lo = {U.x & MK, U.y & MK, U.z & MK, U.w & MK};
+        u32x4 hi = {(U.x >> 4) & MK, (U.y >> 4) & MK, (U.z >> 4) & MK, (U.w >> 4) & MK};
+        if constexpr (SCHEME == 3) {
+            const uint32_t T6 = 0x30303030u, hx = hr[u].x, hy = hr[u].y;
+            lo.x |= (hx << 4) & T6; lo.y |= (hx << 2) & T6;
+            lo.z |= (hy << 4) & T6; lo.w |= (hy << 2) & T6;
+            hi.x |= hx & T6;        hi.y |= (hx >> 2) & T6;
+            hi.z |= hy & T6;        hi.w |= (hy >> 2) & T6;
+        }
+        f32x4 D = {0.f, 0.f, 0.f, 0.f};
+        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(lo.x, lo.y), B[0], D, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(lo.z, lo.w), B[1], D, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(hi.x, hi.y), B[2], D, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(hi.z, hi.w), B[3], D, 0, 0, 0);
+        return D;
+    };
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    auto epilogue = [&](int u, int b, const f32x4& D) {
+        const float S = psum[kb0 + b][0][j] + psum[kb0 + b][1][j];
+        const u32x4 p = pr[u];
+        acc[0] = __builtin_fmaf(zp_off(p.x), S, __builtin_fmaf(h2f(p.x >> 16), D[0], acc[0]));
+        acc[1] = __builtin_fmaf(zp_off(p.y), S, __builtin_fmaf(h2f(p.y >> 16), D[1], acc[1]));
+        acc[2] = __builtin_fmaf(zp_off(p.z), S, __builtin_fmaf(h2f(p.z >> 16), D[2], acc[2]));
+        acc[3] = __builtin_fmaf(zp_off(p.w), S, __builtin_fmaf(h2f(p.w >> 16), D[3], acc[3]));
+    };
+    // Whole rounds of GS_LA unconditional steps, two blocks per step, each
+    // refilling its ring slots GS_LA blocks ahead (past the half: zeros,
+    // never used). Guarded steps inside the loop would merge the
+    // wait-counter state at the loop edge and make the compiler drain every
+    // load in flight once per round; the remainder runs after the loop.
+    const int full = kn / GS_LA * GS_LA;
+    for (int bl = 0; bl < full; bl += GS_LA) {
+#pragma unroll
+        for (int u = 0; u < GS_LA; u += 2) {
+            const f32x4 D0 = dots(u, bl + u), D1 = dots(u + 1, bl + u + 1);
+            epilogue(u, bl + u, D0);
+            epilogue(u + 1, bl + u + 1, D1);
+            load_codes(u, bl + u + GS_LA);
+            load_codes(u + 1, bl + u + 1 + GS_LA);
+            __builtin_amdgcn_sched_barrier(0);  // keep the refills here
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < GS_LA; u += 2) {
+        if (full + u + 1 < kn) {
+            const f32x4 D0 = dots(u, full + u), D1 = dots(u + 1, full + u + 1);
+            epilogue(u, full + u, D0);
+            epilogue(u + 1, full + u + 1, D1);
+        } else if (full + u < kn) {
+            epilogue(u, full + u, dots(u, full + u));
+        }
+    }
+
+    // the second half's sums join the first's (fixed order); from here on
+    // only the first four waves write, but all take part in every barrier
+    if (part_k) red[wave - GS_TILES][lane] = acc;
+    __syncthreads();
+    if (!part_k) acc = acc + red[wave][lane];
+    const bool writer = !part_k && tile_ok;
+
+    // lane (g, j) holds rows 4g..4g+3 of the tile for column j
+    const int row = T * TILE_ROWS + 4 * g;
+    if (kg == 1) {
+        if (writer && j < M)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (row + q < P.rows) P.y[(size_t)j * P.rows + row + q] = P.bias ? acc[q] + P.bias[row + q] : acc[q];
+        return;
+    }
+    // Split K: publish the slice's partials with coherent stores, then the
+    // last workgroup of the row group adds the kg slices in slice order
+    // (deterministic) and resets the counter. The stores are complete at
+    // the device's coherence point once vmcnt drains, before the barrier
+    // that precedes the counter increment; the last workgroup reads with
+    // coherent loads after it has seen the count.
+    const auto prt = buf_rsrc(P.part, kg * 16 * P.rows_pad * 4);
+    if (writer) {
+        u32x4 v;
+        __builtin_memcpy(&v, &acc, 16);
+        __builtin_amdgcn_raw_buffer_store_b128(v, prt, ((kgi * 16 + j) * P.rows_pad + row) * 4, 0, CPOL_SC1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(P.counters + rg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == (uint32_t)(kg - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (writer && j < M) {
+        f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < kg; k++) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(prt, ((k * 16 + j) * P.rows_pad + row) * 4, 0, CPOL_SC1);
+            f32x4 f;
+            __builtin_memcpy(&f, &v, 16);
+            sum = k == 0 ? f : sum + f;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            if (row + q < P.rows) P.y[(size_t)j * P.rows + row + q] = P.bias ? sum[q] + P.bias[row + q] : sum[q];
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(P.counters + rg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int SCHEME>
+hipError_t launch_nt(int nt, dim3 grid, hipStream_t s, const GemmArgs& a)
+{
+    switch (nt) {
+    case 2: hipLaunchKernelGGL((k_gemm<SCHEME, 2>), grid, dim3(GM_WG8), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((k_gemm<SCHEME, 3>), grid, dim3(GM_WG8), 0, s, a); break;
+    default: hipLaunchKernelGGL((k_gemm<SCHEME, 4>), grid, dim3(GM_WG8), 0, s, a); break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int gemm_row_groups(uint64_t rows)
+{
+    const uint64_t tiles = pad_rows(rows) / TILE_ROWS;
+    const uint64_t per = (uint64_t)GM_WG / 64 * GM_RT;
+    return (int)((tiles + per - 1) / per);
+}
+
+int gemm_small_row_groups(uint64_t rows)
+{
+    const uint64_t tiles = pad_rows(rows) / TILE_ROWS;
+    return (int)((tiles + GS_TILES - 1) / GS_TILES);
+}
+
+int gemm_kslices(uint64_t rows, uint64_t nb, int req)
+{
+    if (nb == 0) return 1;
+    if (req > 0) return fast_normalize_kslices(nb, (int)std::min<uint64_t>((uint64_t)req, nb));
+    // Enough workgroups for two per CU, but K-slices of at least 15 blocks:
+    // each slice's partial Y (64 x rows floats) costs a write and a read
+    // (measured on 3840 x 15360: 8 slices 38 us, 10 slices 50 us at M = 64).
+    const uint64_t rgs = (uint64_t)gemm_row_groups(rows);
+    uint64_t kg = (512 + rgs - 1) / rgs;
+    kg = std::min<uint64_t>(kg, std::max<uint64_t>(1, nb / 15));
+    return fast_normalize_kslices(nb, (int)std::max<uint64_t>(kg, 1));
+}
+
+int gemm_small_kslices(uint64_t rows, uint64_t nb, int req)
+{
+    if (nb == 0) return 1;
+    const int kmin = (int)((nb + GEMM_SMALL_MAXBK - 1) / GEMM_SMALL_MAXBK);
+    int kg = req;
+    if (kg <= 0) {  // about one workgroup per CU, slices of at least 4 blocks
+        const uint64_t rgs = (uint64_t)gemm_small_row_groups(rows);
+        kg = (int)std::min<uint64_t>((240 + rgs - 1) / rgs, std::max<uint64_t>(1, nb / 4));
+    }
+    kg = (int)std::min<uint64_t>((uint64_t)std::max(kg, kmin), nb);
+    // normalising can only lower the count, so recheck the slice length
+    int k = fast_normalize_kslices(nb, kg);
+    while ((nb + k - 1) / k > (uint64_t)GEMM_SMALL_MAXBK) k = fast_normalize_kslices(nb, ++kg);
+    return k;
+}
+
+hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, int x_bf16, int M,
+                       const float* bias, float* y, hipStream_t s)
+{
+    if (M < 1 || M > GEMM_MAX_M || m.nb == 0) return hipErrorInvalidValue;
+    const int NT = (M + 15) / 16;
+    const int nb = (int)m.nb;
+    (void)hipGetLastError();  // report only these launches
+    if (NT == 1) {
+        if ((nb + w.kg_small - 1) / w.kg_small > GEMM_SMALL_MAXBK)
+            return hipErrorInvalidValue;  // the planner never makes such a split
+        GemmSmallArgs a{};
+        a.codes = m.codes;
+        a.hp = m.hp;
+        a.params = m.params;
+        a.x = x;
+        a.y = y;
+        a.bias = bias;
+        a.part = w.part;
+        a.counters = w.counters;
+        a.rows = (int)m.rows;
+        a.rows_pad = (int)m.rows_pad;
+        a.nb = nb;
+        a.M = M;
+        a.kg = w.kg_small;
+        dim3 grid((unsigned)(gemm_small_row_groups(m.rows) * w.kg_small));
+        if (m.scheme == 4) {
+            if (x_bf16) hipLaunchKernelGGL((k_gemm_small<4, true>), grid, dim3(GS_WG), 0, s, a);
+            else hipLaunchKernelGGL((k_gemm_small<4, false>), grid, dim3(GS_WG), 0, s, a);
+        } else {
+            if (x_bf16) hipLaunchKernelGGL((k_gemm_small<3, true>), grid, dim3(GS_WG), 0, s, a);
+            else hipLaunchKernelGGL((k_gemm_small<3, false>), grid, dim3(GS_WG), 0, s, a);
+        }
+        return hipGetLastError();
+    }
+    dim3 pgrid((unsigned)(nb * NT));
+    if (x_bf16)
+        hipLaunchKernelGGL(k_gemm_pack<true>, pgrid, dim3(256), 0, s, x, M, (int)m.cols, NT,
+                           reinterpret_cast<u32x4*>(w.xf), w.xsum);
+    else
+        hipLaunchKernelGGL(k_gemm_pack<false>, pgrid, dim3(256), 0, s, x, M, (int)m.cols, NT,
+                           reinterpret_cast<u32x4*>(w.xf), w.xsum);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    GemmArgs a{};
+    a.codes = m.codes;
+    a.hp = m.hp;
+    a.params = m.params;
+    a.xf = reinterpret_cast<const u32x4*>(w.xf);
+    a.xsum = w.xsum;
+    a.y = y;
+    a.bias = bias;
+    a.part = w.part;
+    a.counters = w.counters;
+    a.rows = (int)m.rows;
+    a.rows_pad = (int)m.rows_pad;
+    a.nb = nb;
+    a.M = M;
+    a.kg = w.kg;
+    dim3 grid((unsigned)(gemm_row_groups(m.rows) * w.kg));
+    return m.scheme == 4 ? launch_nt<4>(NT, grid, s, a) : launch_nt<3>(NT, grid, s, a);
+}
+
+}  // namespace wpcg

@@ -112,6 +112,36 @@ inline int fast_normalize_kslices(uint64_t nb, int kg)
     return (int)((nb + nbk - 1) / nbk);
 }
 
+// ---- batched GEMM (gemm.hip) -------------------------------------------------
+// Y = X W^T for up to GEMM_MAX_M activations per launch. Up to 16 columns one
+// kernel packs X into LDS itself (a wave per row tile, K-slices of at most
+// GEMM_SMALL_MAXBK blocks); above that X is packed by a first kernel and a
+// workgroup of 4 waves covers 4 * GEMM_TILES_PER_WAVE row tiles.
+constexpr int GEMM_WG_THREADS = 256;
+constexpr int GEMM_TILES_PER_WAVE = 2;
+constexpr int GEMM_MAX_M = 64;
+constexpr int GEMM_SMALL_MAXBK = 30;
+// Workspace of one matrix, sized for GEMM_MAX_M columns; fixed once made so
+// captured graphs keep valid pointers.
+struct GemmWork {
+    int kg_req = 0;                 // requested K-slices (0 = the library's choice)
+    int kg = 1;                     // K-slices, more than 16 columns
+    int kg_small = 1;               // K-slices, up to 16 columns
+    void* xf = nullptr;             // packed X: nb * 4 column tiles * 4 KiB
+    float* xsum = nullptr;          // per-block column sums: nb * 64
+    float* part = nullptr;          // partial Y: [kg][64][rows_pad] or [kg_small][16][rows_pad]
+    uint32_t* counters = nullptr;   // one per row group, self-resetting
+};
+void free_gemm(GemmWork& w);  // keeps kg_req
+int gemm_row_groups(uint64_t rows);        // more than 16 columns
+int gemm_small_row_groups(uint64_t rows);  // up to 16 columns
+// Splits (requested kg, 0 = the library's choice), normalised to non-empty
+// slices (and, for the small kernel, slices of at most GEMM_SMALL_MAXBK).
+int gemm_kslices(uint64_t rows, uint64_t nb, int req);
+int gemm_small_kslices(uint64_t rows, uint64_t nb, int req);
+hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, int x_bf16, int M,
+                       const float* bias, float* y, hipStream_t s);
+
 // ---- host helpers shared by the C ABI files (capi*.cpp) -----------------
 hipStream_t pick(wpcg_ctx* ctx, wpcg_stream s);  // NULL = the context stream
 int check_ctx(wpcg_ctx* ctx);                     // non-null, device current
@@ -205,6 +235,7 @@ struct wpcg_linear {
     wpcg_ctx* ctx = nullptr;
     wpcg::DeviceMatrix m;
     wpcg::FastPlan plan;
+    wpcg::GemmWork gemm;    // made by the first batched call
     float* bias = nullptr;  // device, out_f floats, or null
     int mode = WPCG_MODE_EXACT;
     // staging for the synchronous *_host twins

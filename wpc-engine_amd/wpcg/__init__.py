@@ -28,6 +28,7 @@ OK, E_IO, E_FORMAT, E_SHAPE, E_NOTFOUND, E_DEVICE, E_ARG, E_NOMEM, E_UNSUPPORTED
 SCHEME_V3, SCHEME_V4 = 3, 4
 MODE_EXACT, MODE_FAST = 0, 1
 ROUND_FMA, ROUND_TWO = 0, 1
+DTYPE_F32, DTYPE_BF16 = 0, 1
 
 _ERR_NAMES = {0: "OK", 1: "E_IO", 2: "E_FORMAT", 3: "E_SHAPE", 4: "E_NOTFOUND", 5: "E_DEVICE",
               6: "E_ARG", 7: "E_NOMEM", 8: "E_UNSUPPORTED"}
@@ -84,6 +85,10 @@ _SIGS = {
     "wpcg_linear_device_bytes": (C.c_int, [_p, _u64p]),
     "wpcg_linear_matvec": (C.c_int, [_p, _p, _p, _p]),
     "wpcg_linear_matvec_host": (C.c_int, [_p, _p, _p]),
+    "wpcg_linear_gemm": (C.c_int, [_p, _p, C.c_int, C.c_uint32, _p, _p]),
+    "wpcg_linear_gemm_host": (C.c_int, [_p, _p, C.c_int, C.c_uint32, _p]),
+    "wpcg_linear_set_gemm_kslices": (C.c_int, [_p, C.c_int]),
+    "wpcg_linear_gemm_kslices": (C.c_int, [_p, _p, _p]),
     "wpcg_linear_embed": (C.c_int, [_p, C.c_uint32, _p, _p]),
     "wpcg_linear_embed_host": (C.c_int, [_p, C.c_uint32, _p]),
     "wpcg_linear_dequant": (C.c_int, [_p, C.c_int, _p, _p]),
@@ -428,6 +433,28 @@ class WpcLinear:
 
     def matvec_dev(self, x: DeviceBuffer, y: DeviceBuffer, stream=None):
         check(lib.wpcg_linear_matvec(self.h, x.ptr, y.ptr, stream))
+
+    def gemm(self, X, dtype: int = DTYPE_F32) -> np.ndarray:
+        """Y = X W^T (+ bias) for a batch X of shape (M, in_features): fp32
+        values, or bf16 bit patterns (uint16) with dtype DTYPE_BF16."""
+        X = np.ascontiguousarray(X, np.float32 if dtype == DTYPE_F32 else np.uint16)
+        assert X.ndim == 2 and X.shape[1] == self._in
+        Y = np.empty((X.shape[0], self._out), np.float32)
+        check(lib.wpcg_linear_gemm_host(self.h, _np_ptr(X), dtype, X.shape[0], _np_ptr(Y)))
+        return Y
+
+    def gemm_dev(self, X: DeviceBuffer, M: int, Y: DeviceBuffer, dtype: int = DTYPE_F32, stream=None):
+        check(lib.wpcg_linear_gemm(self.h, X.ptr, dtype, M, Y.ptr, stream))
+
+    def set_gemm_kslices(self, k: int):
+        check(lib.wpcg_linear_set_gemm_kslices(self.h, k))
+        return self
+
+    def gemm_kslices(self) -> tuple[int, int]:
+        """(K-slices for M <= 16, K-slices for M > 16)."""
+        a, b = C.c_int(), C.c_int()
+        check(lib.wpcg_linear_gemm_kslices(self.h, C.byref(a), C.byref(b)))
+        return a.value, b.value
 
     def embed(self, token: int) -> np.ndarray:
         out = np.empty(self._in, np.float32)
