@@ -166,10 +166,12 @@ def test_fast_split_plan_never_makes_an_empty_slice():
     # every slice must start inside the row (an empty trailing slice would
     # address blocks past the end of the matrix) and fit the LDS stage: 64
     # blocks with one 16-row tile per workgroup, 32 with two (matrices of
-    # 512 tiles or more). Checked for every block count and requested split.
+    # 512 tiles or more), 16 with four (2048 tiles or more, rows of at most
+    # 16 blocks). Checked for every block count and requested split.
     for nb in range(1, 161):
         for req in [0] + list(range(1, nb + 3)):
-            for rows, most in ((16, 64), (1024, 64), (8176, 64), (8177, 32), (9728, 32)):
+            for rows, most in ((16, 64), (1024, 64), (8176, 64), (8177, 32), (9728, 32),
+                               (32767, 32), (32769, 16 if nb <= 16 else 32), (151936, 16 if nb <= 16 else 32)):
                 k = wpcg.plan_kslices(rows, nb * 128, req)
                 nbk = -(-nb // k)
                 assert 1 <= k <= nb and nbk <= most, (nb, req, rows, k)

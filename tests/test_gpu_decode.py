@@ -96,6 +96,30 @@ def test_exact_decode_is_bit_identical(ctx, name, cfg, n_prompt, n_new, seed):
     ref.close()
 
 
+@pytest.mark.parametrize("name,cfg,n_steps,seed", [("dense", DENSE, 90, 111), ("moe", MOE, 90, 212),
+                                                    ("qwen3-moe-2L", QWEN3_MOE_2L, 78, 313)])
+def test_fast_decode_tracks_the_reference(ctx, name, cfg, n_steps, seed):
+    """FAST mode step by step on the oracle's greedy tokens: every step's
+    logits within 2e-3 of the logit range of the oracle's. The steps run
+    past several 32-position chunks of the FAST attention, so the chunk
+    merge and the key/value appends of every chunk are exercised."""
+    print(f"[gpu] fast decode {name}: building", flush=True)
+    m, ref = build(ctx, cfg, seed)
+    m.set_mode(wpcg.MODE_FAST)
+    tok = int(np.random.default_rng(5).integers(0, cfg["vocab"]))
+    worst = 0.0
+    for step in range(n_steps):
+        r = ref.forward_token(tok)
+        g, _ = m.forward_token(tok)
+        err = float(np.max(np.abs(g - r))) / float(r.max() - r.min())
+        worst = max(worst, err)
+        assert err <= 2e-3, f"{name}: step {step} logits off by {err:.2e} of the range"
+        tok = O.argmax(r)
+    print(f"[gpu] fast decode {name}: {n_steps} steps, worst logit error {worst:.2e} of the range", flush=True)
+    m.close()
+    ref.close()
+
+
 def test_decode_errors(ctx):
     cfg = dict(DENSE)
     m = wpcg.Model(ctx, 4, wpcg.ModelConfig(**cfg))

@@ -91,6 +91,9 @@ SHAPES = [
     (3, 37, 640),
     (4, 8200, 640),    # two tiles per workgroup, odd tile count (513)
     (3, 8195, 8320),   # two tiles per workgroup, 65 blocks: two K-slices
+    (4, 32784, 2048),  # four tiles per workgroup, 2049 tiles (one in the last workgroup)
+    (3, 33001, 1152),  # four tiles per workgroup, ragged last tile
+    (4, 32784, 2176),  # 2049 tiles but 17 blocks: two tiles per workgroup
 ]
 
 

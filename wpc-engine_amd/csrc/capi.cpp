@@ -123,7 +123,7 @@ int upload_rows(wpcg_ctx* ctx, const uint8_t* blocks, const DeviceMatrix& m, uin
 
 int plan_kslices(uint64_t rows, uint64_t nb, int kg)
 {
-    const uint64_t mb = fast_max_slice(rows);
+    const uint64_t mb = fast_max_slice(rows, nb);
     const int kmin = (int)std::max<uint64_t>(1, (nb + mb - 1) / mb);
     const int k = kg > 0 ? std::max(kmin, std::min(kg, (int)std::max<uint64_t>(1, nb)))
                          : fast_kslices(rows, nb);

@@ -41,6 +41,7 @@ struct wpcg_model {
     float *residual = nullptr, *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
     float *attn = nullptr, *g = nullptr, *u = nullptr,
           *h = nullptr, *logits = nullptr;
+    AttnWork attn_work;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int graph_mode = -1;
@@ -128,26 +129,52 @@ std::string missing(const wpcg_model* m)
     return "";
 }
 
+// A FAST job y = lin(RMSNorm(x; nw)) with the norm folded into the GEMV, or
+// without nw a plain FAST job; `ok` turns false when the linear cannot fold
+// the norm in (its row needs more than one K-slice).
+GemvJob fast_job(wpcg_linear* lin, const float* x, float* y, const float* nw, float eps, bool& ok)
+{
+    GemvJob J{&lin->m, &lin->plan, x, lin->bias, y};
+    if (nw) {
+        J.xform = XF_NORM;
+        J.nw = nw;
+        J.eps = eps;
+        ok = ok && lin->plan.kg == 1 && lin->m.nb > 0;
+    }
+    return J;
+}
+
 // One decode step on stream s: the token at tokens[pos] through every layer,
-// logits, argmax, position + 1.
+// logits, argmax, position + 1. FAST mode folds the RMSNorms into the
+// GEMVs that read them and runs the MoE layer as three launches (moe_run);
+// EXACT mode keeps every operation of the reference as its own launch.
 int enqueue_step(wpcg_model* m, hipStream_t s)
 {
     const wpcg_model_config& c = m->cfg;
     const int H = (int)c.hidden, hd = (int)c.head_dim, nh = (int)c.n_heads, nkv = (int)c.n_kv_heads;
-    const int qd = nh * hd, kvd = nkv * hd, mode = m->mode;
+    const int mode = m->mode;
+    const bool fast = mode == WPCG_MODE_FAST;
     const float scale = 1.0f / std::sqrt((float)hd);  // model.rs: 1/sqrt(head_dim) in f32
     WPCG_HIP(launch_embed_tok(m->embed->m, m->tokens, m->st, m->residual, s));
     for (uint32_t l = 0; l < c.n_layers; l++) {
         Layer& L = m->layers[l];
-        WPCG_HIP(launch_rms_norm(mode, m->residual, L.in_ln, H, c.eps, m->normed, s));
-        wpcg_linear* qkv[3] = {L.q, L.k, L.v};
-        const float* xs[3] = {m->normed, m->normed, m->normed};
-        float* ys[3] = {m->q, m->k, m->v};
-        if (int rc = wpcg_linear_matvec_multi(3, qkv, xs, ys, s)) return rc;
+        bool fused = fast;
+        GemvJob qkv_jobs[3] = {fast_job(L.q, m->residual, m->q, L.in_ln, c.eps, fused),
+                               fast_job(L.k, m->residual, m->k, L.in_ln, c.eps, fused),
+                               fast_job(L.v, m->residual, m->v, L.in_ln, c.eps, fused)};
+        if (fused) {
+            WPCG_HIP(launch_gemv_fast(qkv_jobs, 3, s));
+        } else {
+            WPCG_HIP(launch_rms_norm(mode, m->residual, L.in_ln, H, c.eps, m->normed, s));
+            wpcg_linear* qkv[3] = {L.q, L.k, L.v};
+            const float* xs[3] = {m->normed, m->normed, m->normed};
+            float* ys[3] = {m->q, m->k, m->v};
+            if (int rc = wpcg_linear_matvec_multi(3, qkv, xs, ys, s)) return rc;
+        }
         float* kc = m->kc + (size_t)l * nkv * c.max_pos * hd;
         float* vc = m->vc + (size_t)l * nkv * c.max_pos * hd;
         WPCG_HIP(launch_attention(mode, m->q, m->k, m->v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale,
-                                  m->cos_t, m->sin_t, m->st, kc, vc, m->attn, s));
+                                  m->cos_t, m->sin_t, m->st, kc, vc, m->attn, m->attn_work, s));
         // residual += o_proj(attn): the residual is the GEMV's bias and output
         {
             float* saved = L.o->bias;
@@ -155,6 +182,23 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
             const int rc = wpcg_linear_matvec(L.o, m->attn, m->residual, s);
             L.o->bias = saved;
             if (rc) return rc;
+        }
+        if (c.n_experts && fast) {
+            if (int rc = moe_run(L.moe, m->residual, m->residual, m->residual, s, L.post_ln, c.eps)) return rc;
+            continue;
+        }
+        if (!c.n_experts && fast) {  // dense SwiGLU: norm into gate/up, SiLU*up into down
+            fused = true;
+            GemvJob gu_jobs[2] = {fast_job(L.gate, m->residual, m->g, L.post_ln, c.eps, fused),
+                                  fast_job(L.up, m->residual, m->u, L.post_ln, c.eps, fused)};
+            if (fused) {
+                WPCG_HIP(launch_gemv_fast(gu_jobs, 2, s));
+                GemvJob down{&L.down->m, &L.down->plan, m->g, m->residual, m->residual};
+                down.xform = XF_SILU;
+                down.x2 = m->u;
+                WPCG_HIP(launch_gemv_fast(&down, 1, s));
+                continue;
+            }
         }
         WPCG_HIP(launch_rms_norm(mode, m->residual, L.post_ln, H, c.eps, m->normed, s));
         if (c.n_experts) {
@@ -171,12 +215,16 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
             L.down->bias = saved;
             if (rc) return rc;
         }
-        (void)qd;
-        (void)kvd;
     }
-    WPCG_HIP(launch_rms_norm(mode, m->residual, m->final_norm, H, c.eps, m->normed, s));
     wpcg_linear* head = c.tied ? m->embed : m->lm_head;
-    if (int rc = wpcg_linear_matvec(head, m->normed, m->logits, s)) return rc;
+    bool fused = fast;
+    GemvJob head_job = fast_job(head, m->residual, m->logits, m->final_norm, c.eps, fused);
+    if (fused) {
+        WPCG_HIP(launch_gemv_fast(&head_job, 1, s));
+    } else {
+        WPCG_HIP(launch_rms_norm(mode, m->residual, m->final_norm, H, c.eps, m->normed, s));
+        if (int rc = wpcg_linear_matvec(head, m->normed, m->logits, s)) return rc;
+    }
     WPCG_HIP(launch_argmax_next(m->logits, (int)c.vocab, m->st, m->tokens, s));
     return WPCG_OK;
 }
@@ -291,6 +339,15 @@ int wpcg_model_create(wpcg_ctx* ctx, int scheme, const wpcg_model_config* cfg, w
     dev((void**)&m->u, inter * 4);
     dev((void**)&m->h, inter * 4);
     dev((void**)&m->logits, (size_t)c.vocab * 4);
+    m->attn_work.nch = attention_fast_chunks((int)c.n_heads, (int)c.n_kv_heads, (int)hd);
+    if (m->attn_work.nch) {
+        dev((void**)&m->attn_work.part, kvd / hd * m->attn_work.nch * (c.n_heads / c.n_kv_heads) * (hd + 2) * 4);
+        dev((void**)&m->attn_work.counters, c.n_kv_heads * 4);
+        if (rc == WPCG_OK) {
+            const hipError_t e = hipMemset(m->attn_work.counters, 0, c.n_kv_heads * 4);
+            if (e != hipSuccess) rc = hip_fail(e, "attention workspace");
+        }
+    }
     if (rc == WPCG_OK) {
         // RoPE angles as rope.rs:29-33 computes them: f64 pow, sin, cos, cast to f32
         std::vector<float> cs((size_t)c.max_pos * half), sn((size_t)c.max_pos * half);

@@ -29,7 +29,7 @@ void free_moe(wpcg_moe* m)
     free_matrix(m->down);
     free_plan(m->plan);
     for (void* p : {(void*)m->scores, (void*)m->w, (void*)m->g, (void*)m->u, (void*)m->h,
-                    (void*)m->ys, (void*)m->ids})
+                    (void*)m->ys, (void*)m->ids, (void*)m->xn})
         if (p) (void)hipFree(p);
     if (m->router) {
         free_dense(m->router);
@@ -52,9 +52,42 @@ DeviceMatrix expert_view(int scheme, uint64_t rows, uint64_t cols)
 
 }  // namespace
 
-int wpcg::moe_run(wpcg_moe* m, const float* x_dev, float* out_dev, const float* add, hipStream_t s)
+int wpcg::moe_run(wpcg_moe* m, const float* x_dev, float* out_dev, const float* add, hipStream_t s,
+                  const float* nw, float eps)
 {
     const int K = (int)m->top_k, H = (int)m->hidden, I = (int)m->inter;
+    if (m->mode == WPCG_MODE_FAST && m->routed) {
+        WPCG_HIP(launch_dense(m->router->w, (int)m->n_exp, H, m->mode, x_dev, nullptr, m->scores, s, nw, eps));
+        GemvJob jobs[MAX_JOBS];
+        for (int k = 0; k < 2 * K; k++) {
+            GemvJob& J = jobs[k];
+            J = GemvJob{k % 2 ? &m->up : &m->gate, &m->plan, x_dev, nullptr,
+                        (k % 2 ? m->u : m->g) + (size_t)(k / 2) * I};
+            J.sel_k = k / 2;
+            J.xform = nw ? XF_NORM : XF_NONE;
+            J.nw = nw;
+            J.eps = eps;
+            J.scores = m->scores;
+            J.n_exp = (int)m->n_exp;
+            J.top_k = K;
+            J.norm_topk = m->norm_topk;
+            J.ids_out = m->ids;
+            J.w_out = m->w;
+        }
+        WPCG_HIP(launch_gemv_fast(jobs, 2 * K, s));
+        GemvJob down{&m->down, &m->plan, m->g, add, out_dev, m->ids};
+        down.xform = XF_SILU;
+        down.x2 = m->u;
+        down.routed = 1;
+        down.rw = m->w;
+        down.top_k = K;
+        WPCG_HIP(launch_gemv_fast(&down, 1, s));
+        return WPCG_OK;
+    }
+    if (nw) {  // the norm in a launch of its own
+        WPCG_HIP(launch_rms_norm(m->mode, x_dev, nw, H, eps, m->xn, s));
+        x_dev = m->xn;
+    }
     WPCG_HIP(launch_dense(m->router->w, (int)m->n_exp, H, m->mode, x_dev, nullptr, m->scores, s));
     WPCG_HIP(launch_softmax_route(m->scores, (int)m->n_exp, K, m->norm_topk, m->ids, m->w, s));
     // gate and up of the chosen experts, then SiLU(gate) * up
@@ -224,6 +257,10 @@ int wpcg_moe_create(wpcg_ctx* ctx, int scheme, uint32_t n_exp, uint32_t hidden, 
     dev((void**)&m->u, (size_t)top_k * inter * 4);
     dev((void**)&m->h, (size_t)top_k * inter * 4);
     dev((void**)&m->ys, (size_t)top_k * hidden * 4);
+    dev((void**)&m->xn, (size_t)hidden * 4);
+    // the FAST path's routed down projection: the chosen experts' rows side
+    // by side must fit one K-slice
+    m->routed = (uint64_t)top_k * (inter / 128) <= fast_max_slice(hidden, (uint64_t)top_k * (inter / 128));
     if (rc == WPCG_OK && e != hipSuccess) rc = hip_fail(e, "moe workspace");
     if (rc != WPCG_OK) {
         free_moe(m.get());

@@ -20,6 +20,8 @@
 namespace wpcg {
 namespace {
 
+constexpr int CPOL_SC1 = 16;  // device-coherent: read at the device's coherence point
+
 // Correctly rounded square root (IEEE, as f32::sqrt): the plain builtin
 // expands to the hardware estimate plus a rounding fixup; __fsqrt_rn, without
 // OCML's rounded-operation mode, is the bare estimate (up to 1 ulp off).
@@ -246,6 +248,276 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
     }
 }
 
+// ---- FAST attention step: positions split into chunks across workgroups ----
+// Workgroup (j, c) takes kv head j's query heads (n_rep = nh/nkv of them)
+// over chunk c of the n = pos + 1 positions: FA_NCH chunks of
+// ceil(n / FA_NCH) positions each, so the launch has a fixed shape (a HIP
+// graph replays it at every position) and the merge below reads at most
+// FA_NCH partial states. The chunk's keys and values pass through LDS in
+// blocks of FA_C positions, shared by all n_rep heads (the next block's
+// loads are in flight while the current one is used), with a running
+// (online) softmax: max m, sum l of exp(s - m), o = sum exp(s_t - m) v_t.
+// Each workgroup applies q_norm + RoPE to its heads itself; the chunk that
+// holds `pos` computes the current key (k_norm + RoPE) and value and
+// appends them to the caches. The last chunk to finish (a per-kv-head
+// counter, self-resetting) merges the states in chunk order:
+// out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, M = max_c m_c.
+// Sums are fixed-order trees and fused multiply-adds: deterministic, not
+// the reference's operation order. head_dim HD is 64 or 128, n_rep <=
+// FA_MAXREP.
+constexpr int FA_WG = 256;
+constexpr int FA_C = 32;
+constexpr int FA_NCH = 16;
+constexpr int FA_MAXREP = 16;
+
+// RMSNorm of one head row (w) then RoPE at the current position, by one
+// wave: lane l < HD/2 holds elements l and l + HD/2, which are exactly the
+// pair RoPE rotates. The result goes to y (LDS) and, if set, to g (global).
+template <int HD>
+__device__ __forceinline__ void fa_norm_rope(const float* x, const float* w, float eps, const float* c,
+                                             const float* sn, float* y, float* g)
+{
+    constexpr int half = HD / 2;
+    const int lane = threadIdx.x & 63;
+    const bool on = lane < half;
+    const float x1 = on ? x[lane] : 0.0f, x2 = on ? x[lane + half] : 0.0f;
+    float ss = fmaf(x1, x1, x2 * x2);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    const float scale = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)HD), eps)));
+    if (on) {
+        const float y1 = (x1 * scale) * w[lane], y2 = (x2 * scale) * w[lane + half];
+        const float o1 = fmaf(y1, c[lane], -(y2 * sn[lane])), o2 = fmaf(y2, c[lane], y1 * sn[lane]);
+        y[lane] = o1;
+        y[lane + half] = o2;
+        if (g) {
+            g[lane] = o1;
+            g[lane + half] = o2;
+        }
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(FA_WG) void k_attention_fast(const float* __restrict__ qp,
+                                                          const float* __restrict__ kp,
+                                                          const float* __restrict__ vp,
+                                                          const float* __restrict__ qn,
+                                                          const float* __restrict__ kn, int nh, int nkv,
+                                                          float eps, float scale,
+                                                          const float* __restrict__ cos_t,
+                                                          const float* __restrict__ sin_t,
+                                                          const DecodeState* __restrict__ st,
+                                                          float* __restrict__ kc, float* __restrict__ vc,
+                                                          float* __restrict__ out, float* __restrict__ part,
+                                                          uint32_t* __restrict__ counters)
+{
+    constexpr int HD4 = HD / 4, KS = HD + 4;  // KS: key rows 16-byte aligned, offset by 4 banks
+    constexpr int NOUT = FA_MAXREP * HD / FA_WG;   // outputs per thread
+    constexpr int NKV = FA_C * HD4 / FA_WG;        // 16-byte key (and value) loads per thread and block
+    __shared__ __align__(16) float qs[FA_MAXREP][HD];
+    __shared__ __align__(16) float ks[FA_C][KS];
+    __shared__ __align__(16) float vs[FA_C][HD];
+    __shared__ __align__(16) float kcur[HD], vcur[HD];
+    __shared__ float ps[FA_MAXREP][FA_C];
+    __shared__ float s_m[FA_MAXREP], s_l[FA_MAXREP], s_corr[FA_MAXREP];
+    __shared__ float mm[FA_NCH][FA_MAXREP], ml[FA_NCH][FA_MAXREP];
+    __shared__ int s_last;
+    const int j = blockIdx.x / FA_NCH, c = blockIdx.x % FA_NCH;
+    const uint32_t pos = st->pos, max_pos = st->max_pos;
+    const int n = (int)pos + 1, n_rep = nh / nkv;
+    const int len = (n + FA_NCH - 1) / FA_NCH, nact = (n + len - 1) / len;
+    const int tb = c * len;
+    if (tb >= n || pos >= max_pos) return;  // an empty chunk
+    const int te = min(tb + len, n);
+    const float* cs = cos_t + (size_t)pos * (HD / 2);
+    const float* sn = sin_t + (size_t)pos * (HD / 2);
+    float* kb = kc + (size_t)j * max_pos * HD;
+    float* vb = vc + (size_t)j * max_pos * HD;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+
+    // the block's cached keys and values: thread i, 16 bytes of row i / HD4
+    // (the current position's row comes from kcur / vcur)
+    float4 kr[NKV], vr[NKV];
+    auto load_block = [&](int t0) {
+#pragma unroll
+        for (int u = 0; u < NKV; u++) {
+            const int i = threadIdx.x + u * FA_WG, t = t0 + i / HD4, d = 4 * (i % HD4);
+            if (t < te && t != (int)pos) {
+                kr[u] = *reinterpret_cast<const float4*>(kb + (size_t)t * HD + d);
+                vr[u] = *reinterpret_cast<const float4*>(vb + (size_t)t * HD + d);
+            }
+        }
+    };
+    load_block(tb);
+    // q heads (and the current key and value, in the chunk that holds pos)
+    const bool has_pos = te == n;
+    for (int r = wave; r < n_rep + (has_pos ? 1 : 0); r += FA_WG / 64) {
+        if (r < n_rep) {
+            fa_norm_rope<HD>(qp + (size_t)(j * n_rep + r) * HD, qn, eps, cs, sn, qs[r], nullptr);
+        } else {
+            fa_norm_rope<HD>(kp + (size_t)j * HD, kn, eps, cs, sn, kcur, kb + (size_t)pos * HD);
+            for (int d = lane; d < HD; d += 64) {
+                const float vv = vp[(size_t)j * HD + d];
+                vcur[d] = vv;
+                vb[(size_t)pos * HD + d] = vv;
+            }
+        }
+    }
+    if (threadIdx.x < FA_MAXREP) {
+        s_m[threadIdx.x] = -INFINITY;
+        s_l[threadIdx.x] = 0.0f;
+    }
+    float o[NOUT];
+#pragma unroll
+    for (int u = 0; u < NOUT; u++) o[u] = 0.0f;
+    __syncthreads();  // qs, kcur, vcur, s_m, s_l written
+
+    for (int t0 = tb; t0 < te; t0 += FA_C) {
+        const int nt = min(FA_C, te - t0);
+#pragma unroll
+        for (int u = 0; u < NKV; u++) {
+            const int i = threadIdx.x + u * FA_WG, t = i / HD4, d = 4 * (i % HD4);
+            if (t < nt) {
+                const bool cur = t0 + t == (int)pos;
+                const float4 kv = cur ? *reinterpret_cast<const float4*>(kcur + d) : kr[u];
+                const float4 vv = cur ? *reinterpret_cast<const float4*>(vcur + d) : vr[u];
+                *reinterpret_cast<float4*>(&ks[t][d]) = kv;
+                *reinterpret_cast<float4*>(&vs[t][d]) = vv;
+            }
+        }
+        __syncthreads();
+        if (t0 + FA_C < te) load_block(t0 + FA_C);  // in flight during this block
+        // scores s[r][t] = (q_r . k_t) * scale
+        for (int i = threadIdx.x; i < n_rep * FA_C; i += FA_WG) {
+            const int r = i / FA_C, t = i % FA_C;
+            float dot = -INFINITY;
+            if (t < nt) {
+                float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+                for (int d = 0; d < HD; d += 4) {
+                    const float4 q4 = *reinterpret_cast<const float4*>(&qs[r][d]);
+                    const float4 k4 = *reinterpret_cast<const float4*>(&ks[t][d]);
+                    a0 = fmaf(q4.x, k4.x, a0);
+                    a1 = fmaf(q4.y, k4.y, a1);
+                    a2 = fmaf(q4.z, k4.z, a2);
+                    a3 = fmaf(q4.w, k4.w, a3);
+                }
+                dot = ((a0 + a1) + (a2 + a3)) * scale;
+            }
+            ps[r][t] = dot;
+        }
+        __syncthreads();
+        // running softmax per head (one wave per head, lanes = positions)
+        for (int r = wave; r < n_rep; r += FA_WG / 64) {
+            const float v = lane < FA_C ? ps[r][lane] : -INFINITY;
+            float m = v;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+            const float mo = s_m[r], mn = fmaxf(mo, m);
+            const float e = lane < nt ? __expf(v - mn) : 0.0f;
+            float l = e;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off);
+            const float corr = __expf(mo - mn);  // 0 on the first block (mo = -inf)
+            if (lane < FA_C) ps[r][lane] = e;
+            if (lane == 0) {
+                s_m[r] = mn;
+                s_l[r] = fmaf(s_l[r], corr, l);
+                s_corr[r] = corr;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < NOUT; u++) {
+            const int i = threadIdx.x + u * FA_WG, r = i / HD, d = i % HD;
+            if (r < n_rep) {
+                float acc = o[u] * s_corr[r];
+#pragma unroll
+                for (int t = 0; t < FA_C; t++)
+                    if (t < nt) acc = fmaf(ps[r][t], vs[t][d], acc);
+                o[u] = acc;
+            }
+        }
+        __syncthreads();  // before the next block overwrites ks, vs, ps
+    }
+
+    if (nact == 1) {
+#pragma unroll
+        for (int u = 0; u < NOUT; u++) {
+            const int i = threadIdx.x + u * FA_WG, r = i / HD, d = i % HD;
+            if (r < n_rep) out[(size_t)(j * n_rep + r) * HD + d] = __fdiv_rn(o[u], s_l[r]);
+        }
+        return;
+    }
+    // publish the chunk's state, [c][r][HD + 2] = o[0..HD), m, l: every
+    // exchange is issued, then their results are waited for together
+    constexpr int REC = HD + 2;
+    float* pw = part + ((size_t)j * FA_NCH + c) * n_rep * REC;
+    float prev[NOUT + 1];
+#pragma unroll
+    for (int u = 0; u < NOUT; u++) {
+        const int i = threadIdx.x + u * FA_WG, r = i / HD, d = i % HD;
+        prev[u] = r < n_rep ? __hip_atomic_exchange(pw + r * REC + d, o[u], __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT)
+                            : 0.0f;
+    }
+    prev[NOUT] = 0.0f;
+    if ((int)threadIdx.x < 2 * n_rep) {
+        const int r = threadIdx.x >> 1;
+        const float v = (threadIdx.x & 1) ? s_l[r] : s_m[r];
+        prev[NOUT] = __hip_atomic_exchange(pw + r * REC + HD + (threadIdx.x & 1), v, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int u = 0; u <= NOUT; u++) asm volatile("" ::"v"(prev[u]));
+    // the last chunk to finish merges (the handoff of the split-K GEMV: every
+    // state is performed at the coherence point before the count)
+    __syncthreads();
+    if (threadIdx.x == 0)
+        s_last = __hip_atomic_fetch_add(counters + j, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (uint32_t)(nact - 1);
+    __syncthreads();
+    if (!s_last) return;
+    // every state read at the coherence point, all loads issued together
+    const float* pj = part + (size_t)j * FA_NCH * n_rep * REC;
+    const auto prs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(pj), (short)0,
+                                                      nact * n_rep * REC * 4, 0x00020000);
+    float ov[NOUT][FA_NCH];
+#pragma unroll
+    for (int u = 0; u < NOUT; u++) {
+        const int i = threadIdx.x + u * FA_WG, r = min(i / HD, n_rep - 1), d = i % HD;
+#pragma unroll
+        for (int cc = 0; cc < FA_NCH; cc++)  // past nact: beyond the range, reads 0
+            ov[u][cc] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                prs, ((cc * n_rep + r) * REC + d) * 4, 0, CPOL_SC1));
+    }
+    for (int i = threadIdx.x; i < nact * n_rep * 2; i += FA_WG) {
+        const int cc = i / (2 * n_rep), r = (i >> 1) % n_rep;
+        const float v = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            prs, ((cc * n_rep + r) * REC + HD + (i & 1)) * 4, 0, CPOL_SC1));
+        if (i & 1) ml[cc][r] = v; else mm[cc][r] = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < NOUT; u++) {
+        const int i = threadIdx.x + u * FA_WG, r = i / HD, d = i % HD;
+        if (r < n_rep) {
+            float M = -INFINITY;
+            for (int cc = 0; cc < nact; cc++) M = fmaxf(M, mm[cc][r]);
+            float L = 0.0f, acc = 0.0f;
+#pragma unroll
+            for (int cc = 0; cc < FA_NCH; cc++)
+                if (cc < nact) {
+                    const float w = __expf(mm[cc][r] - M);
+                    L = fmaf(w, ml[cc][r], L);
+                    acc = fmaf(w, ov[u][cc], acc);
+                }
+            out[(size_t)(j * n_rep + r) * HD + d] = __fdiv_rn(acc, L);
+        }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(counters + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // x[i] += y[i] (residual updates the GEMV epilogues do not cover)
 __global__ __launch_bounds__(256) void k_add(float* __restrict__ x, const float* __restrict__ y, int n)
 {
@@ -266,7 +538,33 @@ __global__ __launch_bounds__(AM_WG) void k_argmax_next(const float* __restrict__
     __shared__ int si[AM_WG / 64];
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += AM_WG)
+    // thread t scans 16-byte chunks t, t+AM_WG, ... in increasing index
+    // order (strict >, so its first maximum stays), four chunks in flight
+    const int n4 = n >> 2;
+    const float4* l4 = reinterpret_cast<const float4*>(logits);
+    int c = threadIdx.x;
+    for (; c + 3 * AM_WG < n4; c += 4 * AM_WG) {
+        float4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = l4[c + u * AM_WG];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = 4 * (c + u * AM_WG);
+            if (v[u].x > bv) { bv = v[u].x; bi = i; }
+            if (v[u].y > bv) { bv = v[u].y; bi = i + 1; }
+            if (v[u].z > bv) { bv = v[u].z; bi = i + 2; }
+            if (v[u].w > bv) { bv = v[u].w; bi = i + 3; }
+        }
+    }
+    for (; c < n4; c += AM_WG) {
+        const float4 v = l4[c];
+        const int i = 4 * c;
+        if (v.x > bv) { bv = v.x; bi = i; }
+        if (v.y > bv) { bv = v.y; bi = i + 1; }
+        if (v.z > bv) { bv = v.z; bi = i + 2; }
+        if (v.w > bv) { bv = v.w; bi = i + 3; }
+    }
+    for (int i = 4 * n4 + threadIdx.x; i < n; i += AM_WG)
         if (logits[i] > bv) { bv = logits[i]; bi = i; }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
@@ -303,12 +601,27 @@ hipError_t launch_rms_norm(int mode, const float* x, const float* w, int n, floa
 
 int attention_max_pos() { return AT_MAXPOS; }
 
+int attention_fast_chunks(int nh, int nkv, int hd)
+{
+    if ((hd != 64 && hd != 128) || nh / nkv > FA_MAXREP) return 0;  // FAST uses the one-workgroup kernel
+    return FA_NCH;
+}
+
 hipError_t launch_attention(int mode, const float* q, const float* k, const float* v, const float* qn,
                             const float* kn, int nh, int nkv, int hd, float eps, float scale,
                             const float* cos_t, const float* sin_t, const DecodeState* st, float* kc,
-                            float* vc, float* out, hipStream_t s)
+                            float* vc, float* out, const AttnWork& w, hipStream_t s)
 {
     (void)hipGetLastError();
+    if (mode == WPCG_MODE_FAST && w.nch > 0) {
+        if (hd == 128)
+            hipLaunchKernelGGL(k_attention_fast<128>, dim3(nkv * w.nch), dim3(FA_WG), 0, s, q, k, v, qn, kn, nh,
+                               nkv, eps, scale, cos_t, sin_t, st, kc, vc, out, w.part, w.counters);
+        else
+            hipLaunchKernelGGL(k_attention_fast<64>, dim3(nkv * w.nch), dim3(FA_WG), 0, s, q, k, v, qn, kn, nh,
+                               nkv, eps, scale, cos_t, sin_t, st, kc, vc, out, w.part, w.counters);
+        return hipGetLastError();
+    }
     if (mode == WPCG_MODE_EXACT)
         hipLaunchKernelGGL(k_attention<WPCG_MODE_EXACT>, dim3(nh), dim3(AT_WG), 0, s, q, k, v, qn, kn,
                            nh, nkv, hd, eps, scale, cos_t, sin_t, st, kc, vc, out);

@@ -26,6 +26,8 @@
 // which keeps the small values of a block that holds an outlier accurate.
 #include <hip/hip_runtime.h>
 
+#define REF_EXPF_FN __device__ __forceinline__
+#include "ref_expf.h"
 #include "wpcg_internal.hpp"
 
 namespace wpcg {
@@ -194,17 +196,28 @@ struct FastProblem {
     const uint8_t* codes;
     const uint8_t* hp;
     const uint32_t* params;
-    const float* x;
+    const float* x;      // x; for XF_SILU the gate values g
+    const float* x2;     // XF_SILU: the up values u
+    const float* nw;     // XF_NORM: the RMSNorm weights
     float* y;
     const float* bias;
     float* part;
     uint32_t* counters;
     // Expert selection: with sel set, the matrix stacks experts of rows_pad
     // rows each and this problem is expert sel[sel_k] (its rows only; a
-    // negative id gives y = 0).
+    // negative id gives y = 0). With `scores` set instead, the workgroup
+    // routes itself (softmax and top_k of the n_exp router scores) and takes
+    // slot sel_k of the result; workgroup 0 of the launch also stores the
+    // ids and weights at ids_out / w_out.
     const int32_t* sel;
+    const float* rw;     // routed: the routing weight of each slot
+    const float* scores;
+    int32_t* ids_out;
+    float* w_out;
     int rows, rows_pad, nb, kg, wg_begin, tw;  // tw: 16-row tiles per workgroup
-    int sel_k, pad_;
+    int sel_k, xform, routed, n_exp, top_k, norm_topk;
+    float eps;
+    int enb;  // routed: blocks per row of one expert (nb = top_k * enb)
 };
 struct FastBatch {
     FastProblem p[MAX_JOBS];
@@ -267,6 +280,103 @@ __device__ __forceinline__ float lane_of(float v, int l)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// Softmax of n <= PER*64 router scores and the top-k selection of route()
+// (qwen3_moe_model.rs:376-402) by one wave, into LDS: ids[k], w[k] for
+// k < top_k. The softmax is softmax_inplace's (norm.rs:28-43) with the
+// libm-exact exp and a tree sum for the denominator (FAST mode: the scores
+// themselves come from the FAST router). The selection ranks each
+// probability by how many keys beat its key (bits(p) << 32 | ~index, p >= 0:
+// larger p first, then the lower index), which is the order of route()'s
+// repeated strict-`>` scans; NaN is never chosen; unfilled slots get id -1,
+// weight 0; with norm_topk the chosen weights are divided by their sum taken
+// in chosen order when it is positive. key: LDS scratch of PER*64 keys,
+// tab: LDS for the exp table (32 doubles), both filled here.
+__constant__ double k_exp_tab[32] = REF_EXPF_TABLE;
+
+template <int PER>
+__device__ __forceinline__ void route_wave(const float* __restrict__ scores, int n, int top_k, int norm_topk,
+                                           uint64_t* key, int32_t* ids, float* w, double* tab)
+{
+    const int lane = threadIdx.x & 63;
+    // the scores and the exp table are requested together (one round trip)
+    float v[PER];
+#pragma unroll
+    for (int q = 0; q < PER; q++) {
+        const int i = lane + 64 * q;
+        v[q] = scores[min(i, n - 1)];
+    }
+    const double t = k_exp_tab[lane & 31];
+    if (lane < 32) tab[lane] = t;
+    float m = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < PER; q++) {
+        const int i = lane + 64 * q;
+        if (i >= n) v[q] = -INFINITY;
+        m = fmaxf(m, v[q]);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    float sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < PER; q++) {
+        const int i = lane + 64 * q;
+        v[q] = i < n ? ref_expf_tab(__fsub_rn(v[q], m), tab) : 0.0f;
+        sum += v[q];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+    int selectable = 0;
+    uint64_t mine[PER];
+#pragma unroll
+    for (int q = 0; q < PER; q++) {
+        const int i = lane + 64 * q;
+        if (sum > 0.0f) v[q] = __fdiv_rn(v[q], sum);
+        const bool ok = i < n && v[q] > -INFINITY;  // NaN fails
+        selectable += ok ? 1 : 0;
+        mine[q] = ok ? ((uint64_t)__float_as_uint(v[q]) << 32) | (0xFFFFFFFFu - (uint32_t)i) : 0ull;
+        key[i] = mine[q];
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) selectable += __shfl_xor(selectable, o);
+    int rank[PER];
+#pragma unroll
+    for (int q = 0; q < PER; q++) rank[q] = 0;
+#pragma unroll 1
+    for (int t0 = 0; t0 < PER * 64; t0 += 8) {
+        uint64_t o[8];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const ulonglong2 pr = reinterpret_cast<const ulonglong2*>(key + t0)[u];
+            o[2 * u] = pr.x;
+            o[2 * u + 1] = pr.y;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+#pragma unroll
+            for (int q = 0; q < PER; q++) rank[q] += o[u] > mine[q] ? 1 : 0;
+    }
+#pragma unroll
+    for (int q = 0; q < PER; q++)
+        if (mine[q] && rank[q] < top_k) {
+            ids[rank[q]] = lane + 64 * q;
+            w[rank[q]] = v[q];
+        }
+    if (lane == 0) {
+        const int got = min(top_k, selectable);
+        float sw = 0.0f;
+        if (norm_topk)
+            for (int k = 0; k < got; k++) sw = __fadd_rn(sw, w[k]);
+        for (int k = 0; k < top_k; k++) {
+            if (k >= got) {
+                ids[k] = -1;
+                w[k] = 0.0f;
+            } else if (norm_topk && sw > 0.0f) {
+                w[k] = __fdiv_rn(w[k], sw);
+            }
+        }
+    }
+}
+
 // One row of the block epilogue, branch-free: the digit dot d (lanes of
 // columns 0..3) times scale*s_b, and the zero-point term zp*sum(x_b) (kept
 // by every lane, used from column 4). `p` is zp f16 | scale f16 << 16.
@@ -286,7 +396,23 @@ __device__ __forceinline__ void fast_step(float& acc, float& zacc, int d, uint32
 //          everywhere and adds exactly 0, and the groups' LDS reads, MFMAs
 //          and scaling overlap.
 //   sum:   the kw parts of a tile are added in part order (deterministic).
-template <int SCHEME>
+// Input transforms, applied to x in the prep (FAST mode only):
+//   XF_NORM  x' = x * nw, and the row's result is scaled by
+//            1 / sqrt(mean(x^2) + eps): RMSNorm (norm.rs:4-13) folded into
+//            the GEMV (a single K-slice holds the whole row);
+//   XF_SILU  x' = silu(g) * u (qwen3_moe_model.rs:518-522), times the
+//            slot's routing weight in a routed problem.
+// A routed problem (the MoE down projection of all chosen experts) has the
+// chosen experts' rows side by side: its K is top_k * enb blocks, block b
+// being block b % enb of expert sel[b / enb] with x from slot b / enb's g,
+// u and routing weight. One K-slice holds them all, so the row sum is the
+// weighted combine sum_k w_k W_k h_k of the chosen experts
+// (qwen3_moe_model.rs:526-533) with no cross-workgroup handoff.
+// KIND: FK_PLAIN (a stacked matrix's expert may still come from sel),
+// FK_ROUTE (the workgroup routes itself from router scores) or FK_ROUTED
+// (the routed down projection); all problems of a launch share it.
+constexpr int FK_PLAIN = 0, FK_ROUTE = 1, FK_ROUTED = 2;
+template <int SCHEME, int KIND>
 __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
 {
     // A wave's last group of four may reach up to 2 blocks past the slice:
@@ -296,7 +422,14 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
     __shared__ __align__(8) float2 xs[MAXBK + 4];              // {s_b, sum(x_b)}
     __shared__ __align__(16) uint32_t spar[8][QB * TILE_ROWS]; // parameters, per wave
     __shared__ float red[8][TILE_ROWS];
+    __shared__ float ssq[8];                                    // XF_NORM: sum of x^2 per wave
+    __shared__ int32_t route_ids[MAX_JOBS];                     // FK_ROUTE: the routing
+    __shared__ float route_w[MAX_JOBS];
     __shared__ int s_last;
+    // FK_ROUTE's keys and exp table live in xq, which routing finishes
+    // with before the barrier that precedes the x prep
+    uint64_t* const route_key = reinterpret_cast<uint64_t*>(xq);
+    double* const route_tab = reinterpret_cast<double*>(xq + ROUTE_MAXN * 8);
 
     const int wgid = blockIdx.x;
     // The problem this workgroup belongs to: the problems' first workgroups
@@ -310,25 +443,56 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
     const KargPtr kargs = (KargPtr)__builtin_amdgcn_kernarg_segment_ptr();
     const auto& P = kargs->p[pi];
     const int nb = P.nb, kg = P.kg, tw = P.tw;
+    const int xform = P.xform;
     const uint8_t* codes = P.codes;
     const uint8_t* hplane = SCHEME == 3 ? P.hp : P.codes;
     const uint32_t* params = P.params;
+    const int local = wgid - P.wg_begin;
+    const int kgi = local % kg, tg = local / kg;  // K-slice, tile group
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    // the slice: blocks [b0, b0 + nbl) of the matrix (of expert sel[kgi] in
+    // a routed problem), its x (g) and u at xp / x2p
+    int b0, nbl;
+    const float* xp;
+    const float* x2p = nullptr;
+    int e = 0;
     bool live = true;
-    if (P.sel) {  // the routed expert's rows of a stacked matrix
-        const int e = P.sel[P.sel_k];
+    if constexpr (KIND == FK_ROUTED) {
+        b0 = 0;
+        nbl = nb;
+        xp = P.x;
+        x2p = P.x2;
+    } else {
+        const int nbk = (nb + kg - 1) / kg;
+        b0 = kgi * nbk;
+        nbl = max(0, min(nb, b0 + nbk) - b0);
+        xp = P.x + (size_t)b0 * 128;
+        if (xform == XF_SILU) x2p = P.x2 + (size_t)b0 * 128;
+        if constexpr (KIND == FK_ROUTE) {  // this workgroup routes itself
+            if (wave == 0) {
+                if (P.n_exp <= 128)
+                    route_wave<2>(P.scores, P.n_exp, P.top_k, P.norm_topk, route_key, route_ids, route_w, route_tab);
+                else
+                    route_wave<4>(P.scores, P.n_exp, P.top_k, P.norm_topk, route_key, route_ids, route_w, route_tab);
+            }
+            __syncthreads();
+            e = route_ids[P.sel_k];
+            if (wgid == 0 && (int)threadIdx.x < P.top_k) {
+                P.ids_out[threadIdx.x] = route_ids[threadIdx.x];
+                P.w_out[threadIdx.x] = route_w[threadIdx.x];
+            }
+        } else if (P.sel) {
+            e = P.sel[P.sel_k];
+        }
+    }
+    if (KIND == FK_ROUTE || (KIND == FK_PLAIN && P.sel)) {  // the expert's rows of a stacked matrix
         live = e >= 0;
         const size_t t0 = (size_t)max(e, 0) * (P.rows_pad / TILE_ROWS) * nb;  // tile-block records
         codes += t0 * CODE_REC;
         hplane += t0 * HP_REC;
         params += t0 * TILE_ROWS;
     }
-    const int local = wgid - P.wg_begin;
-    const int kgi = local % kg, tg = local / kg;  // K-slice, tile group
-    const int nbk = (nb + kg - 1) / kg;
-    const int b0 = kgi * nbk;
-    const int nbl = max(0, min(nb, b0 + nbk) - b0);
     const int ntiles = P.rows_pad / TILE_ROWS;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int kw = 8 / tw;                           // waves per tile
     const int T = tg * tw + wave / kw, kq = wave % kw;
     const int q = (nbl + kw - 1) / kw;               // blocks per part (<= QB)
@@ -343,25 +507,77 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
     // x pair p = wave + 8*i: blocks 2p, 2p+1; lane l holds x[4(l&31) .. +3]
     // of block 2p + (l>>5).
     constexpr int XP = MAXBK / 16;  // pairs per wave
-    const auto xrs = buf_rsrc(P.x + (size_t)b0 * 128, nbl * 512);
-    u32x4 xv[XP];
+    const auto xrs = buf_rsrc(xp, nbl * 512);
+    u32x4 xv[XP], x2v[XP];
 #pragma unroll
     for (int i = 0; i < XP; i++)
         xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
-    const size_t rec = (size_t)min(T, ntiles - 1) * nb + wb;
-    // lane l: rows 4(l&3)..+3 of block l>>2 (blocks past QB are not kept)
-    const auto prs = buf_rsrc(params + rec * TILE_ROWS, qw * 64);
-    const u32x4 pv = __builtin_amdgcn_raw_buffer_load_b128(prs, lane * 16, 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    const auto crs = buf_rsrc(codes + rec * CODE_REC, qw * (int)CODE_REC);
-    const auto hrs = buf_rsrc(hplane + rec * HP_REC, SCHEME == 3 ? qw * (int)HP_REC : 0);
+    float wkv[XP];  // routed: the routing weight of each x pair's block
+    if (xform != XF_NONE) {  // the second operand of the transform: nw or u
+        const auto x2rs = buf_rsrc(xform == XF_NORM ? P.nw + (size_t)b0 * 128 : x2p, nbl * 512);
+#pragma unroll
+        for (int i = 0; i < XP; i++)
+            x2v[i] = __builtin_amdgcn_raw_buffer_load_b128(x2rs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
+    }
+    if constexpr (KIND == FK_ROUTED) {
+#pragma unroll
+        for (int i = 0; i < XP; i++) {
+            const int blk = 2 * (wave + 8 * i) + (lane >> 5);
+            wkv[i] = blk < nbl ? P.rw[blk / P.enb] : 0.0f;
+        }
+    }
+    u32x4 pv;
     u32x4 c[QB];
     u32x2 h[QB];
+    if constexpr (KIND != FK_ROUTED) {
+        const size_t rec = (size_t)min(T, ntiles - 1) * nb + wb;
+        // lane l: rows 4(l&3)..+3 of block l>>2 (blocks past QB are not kept)
+        const auto prs = buf_rsrc(params + rec * TILE_ROWS, qw * 64);
+        pv = __builtin_amdgcn_raw_buffer_load_b128(prs, lane * 16, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        const auto crs = buf_rsrc(codes + rec * CODE_REC, qw * (int)CODE_REC);
+        const auto hrs = buf_rsrc(hplane + rec * HP_REC, SCHEME == 3 ? qw * (int)HP_REC : 0);
 #pragma unroll
-    for (int i = 0; i < QB; i++) {
-        c[i] = __builtin_amdgcn_raw_buffer_load_b128(crs, i * (int)CODE_REC + lane * 16, 0, CPOL_NT);
-        if constexpr (SCHEME == 3)
-            h[i] = __builtin_amdgcn_raw_buffer_load_b64(hrs, i * (int)HP_REC + lane * 8, 0, CPOL_NT);
+        for (int i = 0; i < QB; i++) {
+            c[i] = __builtin_amdgcn_raw_buffer_load_b128(crs, i * (int)CODE_REC + lane * 16, 0, CPOL_NT);
+            if constexpr (SCHEME == 3)
+                h[i] = __builtin_amdgcn_raw_buffer_load_b64(hrs, i * (int)HP_REC + lane * 8, 0, CPOL_NT);
+        }
+    } else {
+        // block i of this wave's part is block (wb+i) % enb of expert
+        // sel[(wb+i) / enb]; a block past the part or of an unfilled slot
+        // (id < 0) reads zeros (a record range of 0 bytes)
+        const int enb = P.enb, tiles_e = ntiles;  // the stack's experts have rows_pad rows each
+        const int Tc = min(T, ntiles - 1);
+        size_t recs[QB];
+        int ok[QB];
+#pragma unroll
+        for (int i = 0; i < QB; i++) {
+            const int cb = wb + i, slot = cb / enb;
+            const int ei = i < qw ? P.sel[min(slot, P.top_k - 1)] : -1;
+            ok[i] = ei >= 0;
+            recs[i] = ((size_t)max(ei, 0) * tiles_e + Tc) * enb + cb % enb;
+        }
+        {
+            const int bi = lane >> 2;  // params: lane l, rows 4(l&3)..+3 of block l>>2
+            size_t rb = recs[0];
+            int okb = ok[0];
+#pragma unroll
+            for (int i = 1; i < QB; i++)
+                if (bi == i) { rb = recs[i]; okb = ok[i]; }
+            const auto prs = buf_rsrc(params + rb * TILE_ROWS, bi < QB && okb ? 64 : 0);
+            pv = __builtin_amdgcn_raw_buffer_load_b128(prs, (lane & 3) * 16, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < QB; i++) {
+            const auto crs = buf_rsrc(codes + recs[i] * CODE_REC, ok[i] ? (int)CODE_REC : 0);
+            c[i] = __builtin_amdgcn_raw_buffer_load_b128(crs, lane * 16, 0, CPOL_NT);
+            if constexpr (SCHEME == 3) {
+                const auto hrs = buf_rsrc(hplane + recs[i] * HP_REC, ok[i] ? (int)HP_REC : 0);
+                h[i] = __builtin_amdgcn_raw_buffer_load_b64(hrs, lane * 8, 0, CPOL_NT);
+            }
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -371,12 +587,24 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
     {
         const int hi = lane >> 5, k0 = 4 * (lane & 31);
         const int pos0 = frag_pos(k0), pos1 = frag_pos(k0 + 1), pos2 = frag_pos(k0 + 2), pos3 = frag_pos(k0 + 3);
+        float sq = 0.0f;
 #pragma unroll
         for (int i = 0; i < XP; i++) {
             const int p = wave + 8 * i;
             if (2 * p < nbl) {
-                const float v0 = __uint_as_float(xv[i].x), v1 = __uint_as_float(xv[i].y);
-                const float v2 = __uint_as_float(xv[i].z), v3 = __uint_as_float(xv[i].w);
+                float v0 = __uint_as_float(xv[i].x), v1 = __uint_as_float(xv[i].y);
+                float v2 = __uint_as_float(xv[i].z), v3 = __uint_as_float(xv[i].w);
+                if (xform == XF_NORM) {
+                    sq = fmaf(v0, v0, sq); sq = fmaf(v1, v1, sq); sq = fmaf(v2, v2, sq); sq = fmaf(v3, v3, sq);
+                    v0 *= __uint_as_float(x2v[i].x); v1 *= __uint_as_float(x2v[i].y);
+                    v2 *= __uint_as_float(x2v[i].z); v3 *= __uint_as_float(x2v[i].w);
+                } else if (xform == XF_SILU) {
+                    const float wk = KIND == FK_ROUTED ? wkv[i] : 1.0f;
+                    v0 = __fdividef(v0, 1.0f + __expf(-v0)) * __uint_as_float(x2v[i].x) * wk;
+                    v1 = __fdividef(v1, 1.0f + __expf(-v1)) * __uint_as_float(x2v[i].y) * wk;
+                    v2 = __fdividef(v2, 1.0f + __expf(-v2)) * __uint_as_float(x2v[i].z) * wk;
+                    v3 = __fdividef(v3, 1.0f + __expf(-v3)) * __uint_as_float(x2v[i].w) * wk;
+                }
                 float m = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
                 float s = (v0 + v1) + (v2 + v3);
                 m = fmaxf(m, dpp<DPP_XOR1>(m));
@@ -399,6 +627,11 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
                 put_digits(dst, pos3, v3, inv);
                 if ((lane & 31) == 0) xs[2 * p + hi] = make_float2(M * (1.0f / 127.0f), hi ? Sb : Sa);
             }
+        }
+        if (xform == XF_NORM) {
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+            if (lane == 0) ssq[wave] = sq;
         }
     }
     if (lane < QB * 4) *reinterpret_cast<u32x4*>(spar[wave] + lane * 4) = pv;
@@ -481,6 +714,10 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
     if (mine) {  // the tile's parts in order
         sum = red[tt * kw][rr];
         for (int k = 1; k < kw; k++) sum += red[tt * kw + k][rr];
+        if (xform == XF_NORM) {  // RMSNorm's scale of the row x
+            const float s2 = ((ssq[0] + ssq[1]) + (ssq[2] + ssq[3])) + ((ssq[4] + ssq[5]) + (ssq[6] + ssq[7]));
+            sum *= __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(s2, (float)(nb * 128)), P.eps)));
+        }
     }
     if (kg == 1) {
         if (mine && orow < (size_t)P.rows) P.y[orow] = P.bias ? sum + P.bias[orow] : sum;
@@ -596,7 +833,7 @@ int fast_kslices(uint64_t rows, uint64_t nb)
     // As few K-slices as fit: a split costs a cross-workgroup handoff. When
     // a split is needed anyway, slices of half the maximum leave each wave
     // one group of four blocks, which is faster than two groups.
-    const uint64_t mb = fast_max_slice(rows);
+    const uint64_t mb = fast_max_slice(rows, nb);
     uint64_t kg = (nb + mb - 1) / mb;
     if (kg > 1) kg = (nb + mb / 2 - 1) / (mb / 2);
     return fast_normalize_kslices(nb, (int)kg);
@@ -625,34 +862,71 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
     int wgs = 0;
     const int scheme = jobs[0].m->scheme;
     for (int i = 0; i < n; i++) {
-        const DeviceMatrix& m = *jobs[i].m;
+        const GemvJob& J = jobs[i];
+        const DeviceMatrix& m = *J.m;
         if (m.scheme != scheme) return hipErrorInvalidValue;
         FastProblem& P = B.p[i];
         P.codes = m.codes;
         P.hp = m.hp;
         P.params = m.params;
-        P.x = jobs[i].x;
-        P.y = jobs[i].y;
-        P.bias = jobs[i].bias;
-        P.part = jobs[i].plan->part;
-        P.counters = jobs[i].plan->counters;
+        P.x = J.x;
+        P.x2 = J.x2;
+        P.nw = J.nw;
+        P.y = J.y;
+        P.bias = J.bias;
+        P.part = J.plan->part;
+        P.counters = J.plan->counters;
         P.rows = (int)m.rows;
         P.rows_pad = (int)m.rows_pad;
         P.nb = (int)m.nb;
-        P.kg = jobs[i].plan->kg;
+        P.kg = J.plan->kg;
         P.wg_begin = wgs;
-        P.sel = jobs[i].sel;
-        P.sel_k = jobs[i].sel_k;
-        P.tw = fast_tiles_per_wg(m.rows);
+        P.sel = J.sel;
+        P.sel_k = J.sel_k;
+        P.tw = fast_tiles_per_wg(m.rows, J.routed ? (uint64_t)J.top_k * m.nb : m.nb);
+        P.xform = J.xform;
+        P.eps = J.eps;
+        P.routed = J.routed;
+        P.rw = J.rw;
+        P.scores = J.scores;
+        P.n_exp = J.n_exp;
+        P.top_k = J.top_k;
+        P.norm_topk = J.norm_topk;
+        P.ids_out = J.ids_out;
+        P.w_out = J.w_out;
+        if (J.routed) {  // the chosen experts' rows side by side
+            P.enb = (int)m.nb;
+            P.nb = J.top_k * (int)m.nb;
+        }
+        // shapes the kernel assumes: a normed row is one K-slice; a routed
+        // problem has one K-slice per slot, each an expert's whole row;
+        // routing reads at most ROUTE_MAXN scores into MAX_JOBS slots
+        if (J.xform == XF_NORM && (P.kg != 1 || !J.nw)) return hipErrorInvalidValue;
+        if (J.xform == XF_SILU && !J.x2) return hipErrorInvalidValue;
+        if (J.routed && (!J.sel || !J.rw || J.xform != XF_SILU || P.kg != 1 || J.top_k < 1 ||
+                         (uint64_t)J.top_k * m.nb > fast_max_slice(m.rows, (uint64_t)J.top_k * m.nb)))
+            return hipErrorInvalidValue;
+        if (J.scores && (J.n_exp < 1 || J.n_exp > ROUTE_MAXN || J.top_k < 1 || J.top_k > MAX_JOBS ||
+                         J.sel_k >= J.top_k || !J.ids_out || !J.w_out))
+            return hipErrorInvalidValue;
         const int tiles = (int)(m.rows_pad / TILE_ROWS);
         wgs += (tiles + P.tw - 1) / P.tw * P.kg;
     }
     if (wgs == 0) return hipSuccess;
+    const int kind = jobs[0].routed ? FK_ROUTED : jobs[0].scores ? FK_ROUTE : FK_PLAIN;
+    for (int i = 1; i < n; i++)
+        if ((jobs[i].routed ? FK_ROUTED : jobs[i].scores ? FK_ROUTE : FK_PLAIN) != kind) return hipErrorInvalidValue;
     (void)hipGetLastError();  // report only this launch
-    if (scheme == 4)
-        hipLaunchKernelGGL(k_gemv_fast<4>, dim3(wgs), dim3(FAST_WG), 0, s, B);
-    else
-        hipLaunchKernelGGL(k_gemv_fast<3>, dim3(wgs), dim3(FAST_WG), 0, s, B);
+    const dim3 grid(wgs), block(FAST_WG);
+    if (scheme == 4) {
+        if (kind == FK_PLAIN) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<4, FK_PLAIN>), grid, block, 0, s, B);
+        else if (kind == FK_ROUTE) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<4, FK_ROUTE>), grid, block, 0, s, B);
+        else hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<4, FK_ROUTED>), grid, block, 0, s, B);
+    } else {
+        if (kind == FK_PLAIN) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<3, FK_PLAIN>), grid, block, 0, s, B);
+        else if (kind == FK_ROUTE) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<3, FK_ROUTE>), grid, block, 0, s, B);
+        else hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<3, FK_ROUTED>), grid, block, 0, s, B);
+    }
     return hipGetLastError();
 }
 

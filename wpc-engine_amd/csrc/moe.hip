@@ -45,29 +45,49 @@ __global__ __launch_bounds__(64) void k_dense_exact(const float* __restrict__ w,
 }
 
 // FAST: one wave per row, 16-byte coalesced loads, fixed-order tree sum
-// (deterministic, not the reference's order).
+// (deterministic, not the reference's order). With nw set, x is RMSNorm'd
+// on the fly (norm.rs:4-13): y = W (x * nw) / sqrt(mean(x^2) + eps), the
+// sum of squares taken by each wave from the x it reads anyway.
 __global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ w,
                                                     const float* __restrict__ x,
                                                     const float* __restrict__ bias,
-                                                    float* __restrict__ y, int out_f, int in_f)
+                                                    float* __restrict__ y, int out_f, int in_f,
+                                                    const float* __restrict__ nw, float eps)
 {
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     const float* row = w + (size_t)min(r, out_f - 1) * in_f;
-    float acc = 0.0f;
+    float acc = 0.0f, sq = 0.0f;
     if ((in_f & 3) == 0) {
         for (int i = 4 * lane; i < in_f; i += 256) {
             const float4 v = *reinterpret_cast<const float4*>(row + i);
-            const float4 u = *reinterpret_cast<const float4*>(x + i);
+            float4 u = *reinterpret_cast<const float4*>(x + i);
+            if (nw) {
+                sq = fmaf(u.x, u.x, sq); sq = fmaf(u.y, u.y, sq); sq = fmaf(u.z, u.z, sq); sq = fmaf(u.w, u.w, sq);
+                const float4 n4 = *reinterpret_cast<const float4*>(nw + i);
+                u.x *= n4.x; u.y *= n4.y; u.z *= n4.z; u.w *= n4.w;
+            }
             acc = fmaf(v.x, u.x, acc);
             acc = fmaf(v.y, u.y, acc);
             acc = fmaf(v.z, u.z, acc);
             acc = fmaf(v.w, u.w, acc);
         }
     } else {
-        for (int i = lane; i < in_f; i += 64) acc = fmaf(row[i], x[i], acc);
+        for (int i = lane; i < in_f; i += 64) {
+            float u = x[i];
+            if (nw) {
+                sq = fmaf(u, u, sq);
+                u *= nw[i];
+            }
+            acc = fmaf(row[i], u, acc);
+        }
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+    if (nw) {
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+        acc *= __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(sq, (float)in_f), eps)));
+    }
     if (r < out_f && lane == 0) y[r] = bias ? acc + bias[r] : acc;
 }
 
@@ -150,6 +170,29 @@ __global__ __launch_bounds__(64) void k_route(const float* __restrict__ p, int n
     }
 }
 
+// ((e[0] + e[1]) + e[2]) + ... + e[n-1], each sum rounded: the index-order
+// sum of norm.rs:36-38. The LDS reads go out 16 bytes and 32 values at a
+// time so the chain of additions does not wait on each read.
+__device__ __forceinline__ float ordered_sum(const float* e, int n)
+{
+    float s = 0.0f;
+    int i = 0;
+    for (; i + 32 <= n; i += 32) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = reinterpret_cast<const float4*>(e + i)[u];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            s = __fadd_rn(s, v[u].x);
+            s = __fadd_rn(s, v[u].y);
+            s = __fadd_rn(s, v[u].z);
+            s = __fadd_rn(s, v[u].w);
+        }
+    }
+    for (; i < n; i++) s = __fadd_rn(s, e[i]);
+    return s;
+}
+
 // ---- softmax_inplace + route in one wave (the MoE router's tail) ----------
 // Same arithmetic as k_softmax then k_route: the exps go through LDS so
 // lane 0 can add them in index order; the top-k scan runs on the
@@ -159,7 +202,7 @@ __global__ __launch_bounds__(64) void k_softmax_route(const float* __restrict__ 
                                                       int32_t* __restrict__ ids,
                                                       float* __restrict__ w)
 {
-    __shared__ float e[64 * RT_PER];
+    __shared__ __align__(16) float e[64 * RT_PER];
     __shared__ float chosen[64];
     __shared__ float s_sum;
     const int lane = threadIdx.x;
@@ -182,11 +225,7 @@ __global__ __launch_bounds__(64) void k_softmax_route(const float* __restrict__ 
         }
     }
     __syncthreads();
-    if (lane == 0) {
-        float s = 0.0f;
-        for (int i = 0; i < n; i++) s = __fadd_rn(s, e[i]);
-        s_sum = s;
-    }
+    if (lane == 0) s_sum = ordered_sum(e, n);
     __syncthreads();
     const float s = s_sum;
 #pragma unroll
@@ -257,15 +296,17 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ ys,
 }  // namespace
 
 hipError_t launch_dense(const float* w, int out_f, int in_f, int mode, const float* x,
-                        const float* bias, float* y, hipStream_t s)
+                        const float* bias, float* y, hipStream_t s, const float* nw, float eps)
 {
     (void)hipGetLastError();
-    if (mode == WPCG_MODE_EXACT)
+    if (mode == WPCG_MODE_EXACT) {
+        if (nw) return hipErrorInvalidValue;  // EXACT normalises in its own launch
         hipLaunchKernelGGL(k_dense_exact, dim3((out_f + 63) / 64), dim3(64), 0, s, w, x, bias, y,
                            out_f, in_f);
-    else
+    } else {
         hipLaunchKernelGGL(k_dense_fast, dim3((out_f + 3) / 4), dim3(256), 0, s, w, x, bias, y,
-                           out_f, in_f);
+                           out_f, in_f, nw, eps);
+    }
     return hipGetLastError();
 }
 

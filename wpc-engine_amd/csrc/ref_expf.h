@@ -31,9 +31,10 @@
      0x1.ae89f995ad3adp+0, 0x1.b7f76f2fb5e47p+0, 0x1.c199bdd85529cp+0, 0x1.cb720dcef9069p+0, \
      0x1.d5818dcfba487p+0, 0x1.dfc97337b9b5fp+0, 0x1.ea4afa2a490dap+0, 0x1.f50765b6e4540p+0}
 
-REF_EXPF_FN float ref_expf(float x)
+// The same with the 32-entry table read from `tab` (e.g. a copy in GPU LDS,
+// where a lookup is cheaper than a read of the constant array).
+REF_EXPF_FN float ref_expf_tab(float x, const double* tab)
 {
-    const double tab[32] = REF_EXPF_TABLE;
     const double inv_ln2_32 = 0x1.71547652b82fep+0 * 32;
     const double shift = 0x1.8p+52;
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
@@ -61,4 +62,10 @@ REF_EXPF_FN float ref_expf(float x)
     memcpy(&s, &t, 8);
     const double p = fma(fma(c0, r, c1), r * r, fma(c2, r, 1.0));
     return (float)(p * s);
+}
+
+REF_EXPF_FN float ref_expf(float x)
+{
+    const double tab[32] = REF_EXPF_TABLE;
+    return ref_expf_tab(x, tab);
 }

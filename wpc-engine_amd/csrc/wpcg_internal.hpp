@@ -81,6 +81,13 @@ void transcode_rows(int scheme, const uint8_t* blocks, uint64_t r0, uint64_t nro
 // One GEMV y = W x (+ bias). With `sel` set, `m` describes one expert
 // (rows, rows_pad, nb) and its planes are the first of a stack of experts;
 // the job is expert sel[sel_k] of the stack (device-resident routing).
+// FAST-mode input transforms (the GEMV applies them to x as it reads it):
+//   XF_NORM  RMSNorm of x with weights nw and epsilon eps (norm.rs:4-13):
+//            y = W (x * nw) / sqrt(mean(x^2) + eps); needs kg = 1;
+//   XF_SILU  x = silu(x) * x2 (qwen3_moe_model.rs:518-522).
+constexpr int XF_NONE = 0, XF_NORM = 1, XF_SILU = 2;
+// Router scores routed inside a FAST launch: at most this many experts.
+constexpr int ROUTE_MAXN = 256;
 struct GemvJob {
     const DeviceMatrix* m;
     const FastPlan* plan;
@@ -89,12 +96,36 @@ struct GemvJob {
     float* y;
     const int32_t* sel = nullptr;
     int sel_k = 0;
+    // FAST mode only
+    int xform = XF_NONE;
+    const float* x2 = nullptr;
+    const float* nw = nullptr;
+    float eps = 0.0f;
+    // routed: the rows of experts sel[0..top_k) side by side as one K of
+    // top_k * cols (one K-slice: plan->kg = 1), x of slot k at x + k*cols
+    // (g) and x2 + k*cols (u), scaled by rw[k]; y = bias + the row sum
+    int routed = 0;
+    const float* rw = nullptr;
+    // route from router scores: softmax + top_k over n_exp scores in the
+    // kernel; the job is slot sel_k; ids and weights also go to ids_out / w_out
+    const float* scores = nullptr;
+    int n_exp = 0, top_k = 0, norm_topk = 0;
+    int32_t* ids_out = nullptr;
+    float* w_out = nullptr;
 };
 // FAST mode: a workgroup computes fast_tiles_per_wg 16-row tiles over a
 // K-slice of at most fast_max_slice blocks (the slice's x digits live in LDS).
 constexpr int FAST_MAXBK = 64;
-inline int fast_tiles_per_wg(uint64_t rows) { return pad_rows(rows) / TILE_ROWS >= 512 ? 2 : 1; }
-inline uint64_t fast_max_slice(uint64_t rows) { return FAST_MAXBK / fast_tiles_per_wg(rows); }
+// More tiles per workgroup for tall matrices: fewer workgroups each reading
+// x, and more weight bytes in flight per workgroup; 4 tiles only where a
+// whole row (nb <= 16 blocks) still fits the smaller slice.
+inline int fast_tiles_per_wg(uint64_t rows, uint64_t nb)
+{
+    const uint64_t tiles = pad_rows(rows) / TILE_ROWS;
+    if (tiles >= 2048 && nb <= FAST_MAXBK / 4) return 4;
+    return tiles >= 512 ? 2 : 1;
+}
+inline uint64_t fast_max_slice(uint64_t rows, uint64_t nb) { return FAST_MAXBK / fast_tiles_per_wg(rows, nb); }
 hipError_t launch_gemv_exact(const DeviceMatrix& m, const float* x, const float* bias, float* y,
                              hipStream_t s, const int32_t* sel = nullptr, int sel_k = 0);
 // All jobs must share the scheme. At most MAX_JOBS per launch.
@@ -161,8 +192,10 @@ int plan_kslices(uint64_t rows, uint64_t nb, int kg);
 int make_plan(const DeviceMatrix& m, FastPlan& plan, hipStream_t s, int kg = 0);
 
 // ---- MoE pieces (moe.hip) -------------------------------------------------
+// nw (FAST only): RMSNorm of x with weights nw and epsilon eps folded in.
 hipError_t launch_dense(const float* w, int out_f, int in_f, int mode, const float* x,
-                        const float* bias, float* y, hipStream_t s);
+                        const float* bias, float* y, hipStream_t s, const float* nw = nullptr,
+                        float eps = 0.0f);
 hipError_t launch_softmax(float* x, int n, hipStream_t s);
 int route_max_n();
 hipError_t launch_route(const float* p, int n, int top_k, int norm_topk, int32_t* ids, float* w,
@@ -172,8 +205,15 @@ hipError_t launch_combine(const float* ys, const int32_t* ids, const float* w, i
                           float* out, int h, const float* add, hipStream_t s);
 hipError_t launch_softmax_route(const float* scores, int n, int top_k, int norm_topk, int32_t* ids,
                                 float* w, hipStream_t s);
-// The routed MLP of one layer: out = (add ? add + : ) sum_k w_k expert_k(x).
-int moe_run(wpcg_moe* m, const float* x, float* out, const float* add, hipStream_t s);
+// The routed MLP of one layer: out = (add ? add + : ) sum_k w_k expert_k(xn),
+// xn = x, or with nw set RMSNorm(x) with weights nw and epsilon eps. FAST
+// mode runs it as three launches: the router (norm folded in), the chosen
+// experts' gate and up (each workgroup routes from the scores itself and
+// folds the norm in), and one routed down projection whose K-slices are
+// the chosen experts (SiLU*up and the routing weight folded into its x,
+// the combine and the residual into its ordered split-K sum).
+int moe_run(wpcg_moe* m, const float* x, float* out, const float* add, hipStream_t s,
+            const float* nw = nullptr, float eps = 0.0f);
 
 // ---- decode step (decode.hip) ----------------------------------------------
 // Device-resident position and token bookkeeping of a decode: the step at
@@ -189,10 +229,21 @@ hipError_t launch_rms_norm(int mode, const float* x, const float* w, int n, floa
 // q/k RMSNorm + RoPE, KV append, scores, softmax and output of one layer's
 // attention at the state's position; max_pos <= attention_max_pos().
 int attention_max_pos();
+// FAST mode splits the positions into nch chunks over workgroups; the
+// workspace holds each chunk's softmax state, nkv * nch * n_rep * (hd + 2)
+// floats, and nkv zeroed, self-resetting counters. nch = 0 (head_dim or
+// heads per kv head beyond the chunked kernel's limits) runs FAST on the
+// one-workgroup-per-head kernel.
+struct AttnWork {
+    int nch = 0;
+    float* part = nullptr;
+    uint32_t* counters = nullptr;
+};
+int attention_fast_chunks(int nh, int nkv, int hd);
 hipError_t launch_attention(int mode, const float* q, const float* k, const float* v, const float* qn,
                             const float* kn, int nh, int nkv, int hd, float eps, float scale,
                             const float* cos_t, const float* sin_t, const DecodeState* st, float* kc,
-                            float* vc, float* out, hipStream_t s);
+                            float* vc, float* out, const AttnWork& w, hipStream_t s);
 hipError_t launch_add(float* x, const float* y, int n, hipStream_t s);
 hipError_t launch_argmax_next(const float* logits, int n, DecodeState* st, uint32_t* tokens,
                               hipStream_t s);
@@ -263,7 +314,11 @@ struct wpcg_moe {
     wpcg_dense* router = nullptr;
     wpcg::DeviceMatrix gate, up, down;
     wpcg::FastPlan plan;  // kg = 1 for every expert shape (checked at creation)
+    // FAST: the chosen experts' down rows side by side fit one K-slice
+    // (false: the unfused path)
+    bool routed = false;
     float *scores = nullptr, *w = nullptr, *g = nullptr, *u = nullptr, *h = nullptr, *ys = nullptr;
+    float* xn = nullptr;  // the normed input when the norm is not folded in
     int32_t* ids = nullptr;
 };
 
