@@ -41,7 +41,9 @@ struct wpcg_model {
     float *residual = nullptr, *normed = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
     float *attn = nullptr, *g = nullptr, *u = nullptr,
           *h = nullptr, *logits = nullptr;
-    AttnWork attn_work;
+    // FAST attention's chunk states, merged by the o_proj GEMV (null: the
+    // head shape needs the one-workgroup-per-head kernel)
+    float *part_o = nullptr, *part_ml = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int graph_mode = -1;
@@ -173,10 +175,21 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
         }
         float* kc = m->kc + (size_t)l * nkv * c.max_pos * hd;
         float* vc = m->vc + (size_t)l * nkv * c.max_pos * hd;
-        WPCG_HIP(launch_attention(mode, m->q, m->k, m->v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale,
-                                  m->cos_t, m->sin_t, m->st, kc, vc, m->attn, m->attn_work, s));
-        // residual += o_proj(attn): the residual is the GEMV's bias and output
-        {
+        if (fast && m->part_o) {
+            // chunked attention; o_proj merges the chunks, residual += o_proj(attn)
+            WPCG_HIP(launch_attention_chunks(m->q, m->k, m->v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale,
+                                             m->cos_t, m->sin_t, m->st, kc, vc, m->part_o, m->part_ml, s));
+            GemvJob o{&L.o->m, &L.o->plan, m->part_o, m->residual, m->residual};
+            o.xform = XF_MERGE;
+            o.x2 = m->part_ml;
+            o.st = m->st;
+            o.head_dim = hd;
+            o.n_heads = nh;
+            WPCG_HIP(launch_gemv_fast(&o, 1, s));
+        } else {
+            WPCG_HIP(launch_attention(mode, m->q, m->k, m->v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale,
+                                      m->cos_t, m->sin_t, m->st, kc, vc, m->attn, s));
+            // residual += o_proj(attn): the residual is the GEMV's bias and output
             float* saved = L.o->bias;
             L.o->bias = m->residual;
             const int rc = wpcg_linear_matvec(L.o, m->attn, m->residual, s);
@@ -339,14 +352,9 @@ int wpcg_model_create(wpcg_ctx* ctx, int scheme, const wpcg_model_config* cfg, w
     dev((void**)&m->u, inter * 4);
     dev((void**)&m->h, inter * 4);
     dev((void**)&m->logits, (size_t)c.vocab * 4);
-    m->attn_work.nch = attention_fast_chunks((int)c.n_heads, (int)c.n_kv_heads, (int)hd);
-    if (m->attn_work.nch) {
-        dev((void**)&m->attn_work.part, kvd / hd * m->attn_work.nch * (c.n_heads / c.n_kv_heads) * (hd + 2) * 4);
-        dev((void**)&m->attn_work.counters, c.n_kv_heads * 4);
-        if (rc == WPCG_OK) {
-            const hipError_t e = hipMemset(m->attn_work.counters, 0, c.n_kv_heads * 4);
-            if (e != hipSuccess) rc = hip_fail(e, "attention workspace");
-        }
+    if (attention_fast_ok((int)c.n_heads, (int)c.n_kv_heads, (int)hd)) {
+        dev((void**)&m->part_o, (size_t)ATTN_CHUNKS * qd * 4);
+        dev((void**)&m->part_ml, (size_t)ATTN_CHUNKS * c.n_heads * 2 * 4);
     }
     if (rc == WPCG_OK) {
         // RoPE angles as rope.rs:29-33 computes them: f64 pow, sin, cos, cast to f32

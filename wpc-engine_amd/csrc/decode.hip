@@ -20,8 +20,6 @@
 namespace wpcg {
 namespace {
 
-constexpr int CPOL_SC1 = 16;  // device-coherent: read at the device's coherence point
-
 // Correctly rounded square root (IEEE, as f32::sqrt): the plain builtin
 // expands to the hardware estimate plus a rounding fixup; __fsqrt_rn, without
 // OCML's rounded-operation mode, is the bare estimate (up to 1 ulp off).
@@ -252,22 +250,21 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
 // Workgroup (j, c) takes kv head j's query heads (n_rep = nh/nkv of them)
 // over chunk c of the n = pos + 1 positions: FA_NCH chunks of
 // ceil(n / FA_NCH) positions each, so the launch has a fixed shape (a HIP
-// graph replays it at every position) and the merge below reads at most
-// FA_NCH partial states. The chunk's keys and values pass through LDS in
-// blocks of FA_C positions, shared by all n_rep heads (the next block's
-// loads are in flight while the current one is used), with a running
-// (online) softmax: max m, sum l of exp(s - m), o = sum exp(s_t - m) v_t.
-// Each workgroup applies q_norm + RoPE to its heads itself; the chunk that
-// holds `pos` computes the current key (k_norm + RoPE) and value and
-// appends them to the caches. The last chunk to finish (a per-kv-head
-// counter, self-resetting) merges the states in chunk order:
-// out = sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, M = max_c m_c.
-// Sums are fixed-order trees and fused multiply-adds: deterministic, not
-// the reference's operation order. head_dim HD is 64 or 128, n_rep <=
-// FA_MAXREP.
+// graph replays it at every position). The chunk's keys and values pass
+// through LDS in blocks of FA_C positions, shared by all n_rep heads (the
+// next block's loads are in flight while the current one is used), with a
+// running (online) softmax: max m, sum l of exp(s - m), o = sum exp(s_t - m)
+// v_t. Each workgroup applies q_norm + RoPE to its heads itself; the chunk
+// that holds `pos` computes the current key (k_norm + RoPE) and value and
+// appends them to the caches. Each chunk leaves its state for the o_proj
+// GEMV, which merges the chunks as it reads its input (attention_merge,
+// XF_MERGE): o at part_o[c][h][d], (m, l) at part_ml[c][h][0..1], h the
+// query head. Sums are fixed-order trees and fused multiply-adds:
+// deterministic, not the reference's operation order. head_dim HD is 64
+// or 128, n_rep <= FA_MAXREP.
 constexpr int FA_WG = 256;
 constexpr int FA_C = 32;
-constexpr int FA_NCH = 16;
+constexpr int FA_NCH = ATTN_CHUNKS;
 constexpr int FA_MAXREP = 16;
 
 // RMSNorm of one head row (w) then RoPE at the current position, by one
@@ -308,8 +305,7 @@ __global__ __launch_bounds__(FA_WG) void k_attention_fast(const float* __restric
                                                           const float* __restrict__ sin_t,
                                                           const DecodeState* __restrict__ st,
                                                           float* __restrict__ kc, float* __restrict__ vc,
-                                                          float* __restrict__ out, float* __restrict__ part,
-                                                          uint32_t* __restrict__ counters)
+                                                          float* __restrict__ part_o, float* __restrict__ part_ml)
 {
     constexpr int HD4 = HD / 4, KS = HD + 4;  // KS: key rows 16-byte aligned, offset by 4 banks
     constexpr int NOUT = FA_MAXREP * HD / FA_WG;   // outputs per thread
@@ -320,12 +316,10 @@ __global__ __launch_bounds__(FA_WG) void k_attention_fast(const float* __restric
     __shared__ __align__(16) float kcur[HD], vcur[HD];
     __shared__ float ps[FA_MAXREP][FA_C];
     __shared__ float s_m[FA_MAXREP], s_l[FA_MAXREP], s_corr[FA_MAXREP];
-    __shared__ float mm[FA_NCH][FA_MAXREP], ml[FA_NCH][FA_MAXREP];
-    __shared__ int s_last;
     const int j = blockIdx.x / FA_NCH, c = blockIdx.x % FA_NCH;
     const uint32_t pos = st->pos, max_pos = st->max_pos;
     const int n = (int)pos + 1, n_rep = nh / nkv;
-    const int len = (n + FA_NCH - 1) / FA_NCH, nact = (n + len - 1) / len;
+    const int len = (n + FA_NCH - 1) / FA_NCH;
     const int tb = c * len;
     if (tb >= n || pos >= max_pos) return;  // an empty chunk
     const int te = min(tb + len, n);
@@ -441,81 +435,16 @@ __global__ __launch_bounds__(FA_WG) void k_attention_fast(const float* __restric
         __syncthreads();  // before the next block overwrites ks, vs, ps
     }
 
-    if (nact == 1) {
-#pragma unroll
-        for (int u = 0; u < NOUT; u++) {
-            const int i = threadIdx.x + u * FA_WG, r = i / HD, d = i % HD;
-            if (r < n_rep) out[(size_t)(j * n_rep + r) * HD + d] = __fdiv_rn(o[u], s_l[r]);
-        }
-        return;
-    }
-    // publish the chunk's state, [c][r][HD + 2] = o[0..HD), m, l: every
-    // exchange is issued, then their results are waited for together
-    constexpr int REC = HD + 2;
-    float* pw = part + ((size_t)j * FA_NCH + c) * n_rep * REC;
-    float prev[NOUT + 1];
+    // the chunk's state (the next launch, o_proj, reads it)
 #pragma unroll
     for (int u = 0; u < NOUT; u++) {
         const int i = threadIdx.x + u * FA_WG, r = i / HD, d = i % HD;
-        prev[u] = r < n_rep ? __hip_atomic_exchange(pw + r * REC + d, o[u], __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT)
-                            : 0.0f;
+        if (r < n_rep) part_o[((size_t)c * nh + j * n_rep + r) * HD + d] = o[u];
     }
-    prev[NOUT] = 0.0f;
     if ((int)threadIdx.x < 2 * n_rep) {
         const int r = threadIdx.x >> 1;
-        const float v = (threadIdx.x & 1) ? s_l[r] : s_m[r];
-        prev[NOUT] = __hip_atomic_exchange(pw + r * REC + HD + (threadIdx.x & 1), v, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+        part_ml[((size_t)c * nh + j * n_rep + r) * 2 + (threadIdx.x & 1)] = (threadIdx.x & 1) ? s_l[r] : s_m[r];
     }
-#pragma unroll
-    for (int u = 0; u <= NOUT; u++) asm volatile("" ::"v"(prev[u]));
-    // the last chunk to finish merges (the handoff of the split-K GEMV: every
-    // state is performed at the coherence point before the count)
-    __syncthreads();
-    if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(counters + j, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 (uint32_t)(nact - 1);
-    __syncthreads();
-    if (!s_last) return;
-    // every state read at the coherence point, all loads issued together
-    const float* pj = part + (size_t)j * FA_NCH * n_rep * REC;
-    const auto prs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(pj), (short)0,
-                                                      nact * n_rep * REC * 4, 0x00020000);
-    float ov[NOUT][FA_NCH];
-#pragma unroll
-    for (int u = 0; u < NOUT; u++) {
-        const int i = threadIdx.x + u * FA_WG, r = min(i / HD, n_rep - 1), d = i % HD;
-#pragma unroll
-        for (int cc = 0; cc < FA_NCH; cc++)  // past nact: beyond the range, reads 0
-            ov[u][cc] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                prs, ((cc * n_rep + r) * REC + d) * 4, 0, CPOL_SC1));
-    }
-    for (int i = threadIdx.x; i < nact * n_rep * 2; i += FA_WG) {
-        const int cc = i / (2 * n_rep), r = (i >> 1) % n_rep;
-        const float v = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-            prs, ((cc * n_rep + r) * REC + HD + (i & 1)) * 4, 0, CPOL_SC1));
-        if (i & 1) ml[cc][r] = v; else mm[cc][r] = v;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < NOUT; u++) {
-        const int i = threadIdx.x + u * FA_WG, r = i / HD, d = i % HD;
-        if (r < n_rep) {
-            float M = -INFINITY;
-            for (int cc = 0; cc < nact; cc++) M = fmaxf(M, mm[cc][r]);
-            float L = 0.0f, acc = 0.0f;
-#pragma unroll
-            for (int cc = 0; cc < FA_NCH; cc++)
-                if (cc < nact) {
-                    const float w = __expf(mm[cc][r] - M);
-                    L = fmaf(w, ml[cc][r], L);
-                    acc = fmaf(w, ov[u][cc], acc);
-                }
-            out[(size_t)(j * n_rep + r) * HD + d] = __fdiv_rn(acc, L);
-        }
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(counters + j, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // x[i] += y[i] (residual updates the GEMV epilogues do not cover)
@@ -601,33 +530,36 @@ hipError_t launch_rms_norm(int mode, const float* x, const float* w, int n, floa
 
 int attention_max_pos() { return AT_MAXPOS; }
 
-int attention_fast_chunks(int nh, int nkv, int hd)
-{
-    if ((hd != 64 && hd != 128) || nh / nkv > FA_MAXREP) return 0;  // FAST uses the one-workgroup kernel
-    return FA_NCH;
-}
+bool attention_fast_ok(int nh, int nkv, int hd) { return (hd == 64 || hd == 128) && nh / nkv <= FA_MAXREP; }
 
 hipError_t launch_attention(int mode, const float* q, const float* k, const float* v, const float* qn,
                             const float* kn, int nh, int nkv, int hd, float eps, float scale,
                             const float* cos_t, const float* sin_t, const DecodeState* st, float* kc,
-                            float* vc, float* out, const AttnWork& w, hipStream_t s)
+                            float* vc, float* out, hipStream_t s)
 {
     (void)hipGetLastError();
-    if (mode == WPCG_MODE_FAST && w.nch > 0) {
-        if (hd == 128)
-            hipLaunchKernelGGL(k_attention_fast<128>, dim3(nkv * w.nch), dim3(FA_WG), 0, s, q, k, v, qn, kn, nh,
-                               nkv, eps, scale, cos_t, sin_t, st, kc, vc, out, w.part, w.counters);
-        else
-            hipLaunchKernelGGL(k_attention_fast<64>, dim3(nkv * w.nch), dim3(FA_WG), 0, s, q, k, v, qn, kn, nh,
-                               nkv, eps, scale, cos_t, sin_t, st, kc, vc, out, w.part, w.counters);
-        return hipGetLastError();
-    }
     if (mode == WPCG_MODE_EXACT)
         hipLaunchKernelGGL(k_attention<WPCG_MODE_EXACT>, dim3(nh), dim3(AT_WG), 0, s, q, k, v, qn, kn,
                            nh, nkv, hd, eps, scale, cos_t, sin_t, st, kc, vc, out);
     else
         hipLaunchKernelGGL(k_attention<WPCG_MODE_FAST>, dim3(nh), dim3(AT_WG), 0, s, q, k, v, qn, kn,
                            nh, nkv, hd, eps, scale, cos_t, sin_t, st, kc, vc, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_chunks(const float* q, const float* k, const float* v, const float* qn,
+                                   const float* kn, int nh, int nkv, int hd, float eps, float scale,
+                                   const float* cos_t, const float* sin_t, const DecodeState* st, float* kc,
+                                   float* vc, float* part_o, float* part_ml, hipStream_t s)
+{
+    if (!attention_fast_ok(nh, nkv, hd)) return hipErrorInvalidValue;
+    (void)hipGetLastError();
+    if (hd == 128)
+        hipLaunchKernelGGL(k_attention_fast<128>, dim3(nkv * FA_NCH), dim3(FA_WG), 0, s, q, k, v, qn, kn, nh,
+                           nkv, eps, scale, cos_t, sin_t, st, kc, vc, part_o, part_ml);
+    else
+        hipLaunchKernelGGL(k_attention_fast<64>, dim3(nkv * FA_NCH), dim3(FA_WG), 0, s, q, k, v, qn, kn, nh,
+                           nkv, eps, scale, cos_t, sin_t, st, kc, vc, part_o, part_ml);
     return hipGetLastError();
 }
 

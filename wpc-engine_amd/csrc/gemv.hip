@@ -215,14 +215,17 @@ struct FastProblem {
     int32_t* ids_out;
     float* w_out;
     int rows, rows_pad, nb, kg, wg_begin, tw;  // tw: 16-row tiles per workgroup
+    const DecodeState* st;  // XF_MERGE: the decode position
     int sel_k, xform, routed, n_exp, top_k, norm_topk;
     float eps;
     int enb;  // routed: blocks per row of one expert (nb = top_k * enb)
+    int head_dim, n_heads;  // XF_MERGE
 };
 struct FastBatch {
     FastProblem p[MAX_JOBS];
     int n;
 };
+static_assert(sizeof(FastBatch) <= 4096, "kernel arguments of a FAST launch");
 
 constexpr int FAST_WG = 512;        // 8 waves
 constexpr int QB = 8;               // most blocks one wave puts through the matrix cores
@@ -281,97 +284,108 @@ __device__ __forceinline__ float lane_of(float v, int l)
 }
 
 // Softmax of n <= PER*64 router scores and the top-k selection of route()
-// (qwen3_moe_model.rs:376-402) by one wave, into LDS: ids[k], w[k] for
-// k < top_k. The softmax is softmax_inplace's (norm.rs:28-43) with the
-// libm-exact exp and a tree sum for the denominator (FAST mode: the scores
-// themselves come from the FAST router). The selection ranks each
-// probability by how many keys beat its key (bits(p) << 32 | ~index, p >= 0:
-// larger p first, then the lower index), which is the order of route()'s
-// repeated strict-`>` scans; NaN is never chosen; unfilled slots get id -1,
-// weight 0; with norm_topk the chosen weights are divided by their sum taken
-// in chosen order when it is positive. key: LDS scratch of PER*64 keys,
-// tab: LDS for the exp table (32 doubles), both filled here.
+// (qwen3_moe_model.rs:376-402) by a workgroup, into LDS: ids[k], w[k] for
+// k < top_k. Every thread of the workgroup calls it. Wave 0 computes the
+// probabilities (softmax_inplace's arithmetic, norm.rs:28-43, with the
+// libm-exact exp and a tree sum for the denominator: FAST mode, whose
+// router scores are FAST themselves) and a key per expert,
+// bits(p) << 32 | ~index (p >= 0: larger p first, then the lower index);
+// the rank of a key is how many keys beat it, which is the order of
+// route()'s repeated strict-`>` scans. The eight waves count the
+// comparisons for one eighth of the keys each. NaN is never chosen;
+// unfilled slots get id -1, weight 0; with norm_topk the chosen weights are
+// divided by their sum taken in chosen order when it is positive.
+// LDS: key (PER*64 keys), rk (PER*64 counts), tab (the exp table).
 __constant__ double k_exp_tab[32] = REF_EXPF_TABLE;
 
 template <int PER>
-__device__ __forceinline__ void route_wave(const float* __restrict__ scores, int n, int top_k, int norm_topk,
-                                           uint64_t* key, int32_t* ids, float* w, double* tab)
+__device__ __forceinline__ void route_wg(const float* __restrict__ scores, int n, int top_k, int norm_topk,
+                                         uint64_t* key, int* rk, int32_t* ids, float* w, double* tab,
+                                         int* s_selectable)
 {
-    const int lane = threadIdx.x & 63;
-    // the scores and the exp table are requested together (one round trip)
+    constexpr int N = PER * 64;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float v[PER];
-#pragma unroll
-    for (int q = 0; q < PER; q++) {
-        const int i = lane + 64 * q;
-        v[q] = scores[min(i, n - 1)];
-    }
-    const double t = k_exp_tab[lane & 31];
-    if (lane < 32) tab[lane] = t;
-    float m = -INFINITY;
-#pragma unroll
-    for (int q = 0; q < PER; q++) {
-        const int i = lane + 64 * q;
-        if (i >= n) v[q] = -INFINITY;
-        m = fmaxf(m, v[q]);
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    float sum = 0.0f;
-#pragma unroll
-    for (int q = 0; q < PER; q++) {
-        const int i = lane + 64 * q;
-        v[q] = i < n ? ref_expf_tab(__fsub_rn(v[q], m), tab) : 0.0f;
-        sum += v[q];
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
-    int selectable = 0;
     uint64_t mine[PER];
+    if (wave == 0) {
+        // the scores and the exp table are requested together (one round trip)
 #pragma unroll
-    for (int q = 0; q < PER; q++) {
-        const int i = lane + 64 * q;
-        if (sum > 0.0f) v[q] = __fdiv_rn(v[q], sum);
-        const bool ok = i < n && v[q] > -INFINITY;  // NaN fails
-        selectable += ok ? 1 : 0;
-        mine[q] = ok ? ((uint64_t)__float_as_uint(v[q]) << 32) | (0xFFFFFFFFu - (uint32_t)i) : 0ull;
-        key[i] = mine[q];
-    }
+        for (int q = 0; q < PER; q++) v[q] = scores[min(lane + 64 * q, n - 1)];
+        const double t = k_exp_tab[lane & 31];
+        if (lane < 32) tab[lane] = t;
+        float m = -INFINITY;
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) selectable += __shfl_xor(selectable, o);
-    int rank[PER];
-#pragma unroll
-    for (int q = 0; q < PER; q++) rank[q] = 0;
-#pragma unroll 1
-    for (int t0 = 0; t0 < PER * 64; t0 += 8) {
-        uint64_t o[8];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const ulonglong2 pr = reinterpret_cast<const ulonglong2*>(key + t0)[u];
-            o[2 * u] = pr.x;
-            o[2 * u + 1] = pr.y;
+        for (int q = 0; q < PER; q++) {
+            if (lane + 64 * q >= n) v[q] = -INFINITY;
+            m = fmaxf(m, v[q]);
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++)
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        float sum = 0.0f;
 #pragma unroll
-            for (int q = 0; q < PER; q++) rank[q] += o[u] > mine[q] ? 1 : 0;
-    }
-#pragma unroll
-    for (int q = 0; q < PER; q++)
-        if (mine[q] && rank[q] < top_k) {
-            ids[rank[q]] = lane + 64 * q;
-            w[rank[q]] = v[q];
+        for (int q = 0; q < PER; q++) {
+            v[q] = lane + 64 * q < n ? ref_expf_tab(__fsub_rn(v[q], m), tab) : 0.0f;
+            sum += v[q];
         }
-    if (lane == 0) {
-        const int got = min(top_k, selectable);
-        float sw = 0.0f;
-        if (norm_topk)
-            for (int k = 0; k < got; k++) sw = __fadd_rn(sw, w[k]);
-        for (int k = 0; k < top_k; k++) {
-            if (k >= got) {
-                ids[k] = -1;
-                w[k] = 0.0f;
-            } else if (norm_topk && sw > 0.0f) {
-                w[k] = __fdiv_rn(w[k], sw);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+        int selectable = 0;
+#pragma unroll
+        for (int q = 0; q < PER; q++) {
+            const int i = lane + 64 * q;
+            if (sum > 0.0f) v[q] = __fdiv_rn(v[q], sum);
+            const bool ok = i < n && v[q] > -INFINITY;  // NaN fails
+            selectable += ok ? 1 : 0;
+            mine[q] = ok ? ((uint64_t)__float_as_uint(v[q]) << 32) | (0xFFFFFFFFu - (uint32_t)i) : 0ull;
+            key[i] = mine[q];
+            rk[i] = 0;
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) selectable += __shfl_xor(selectable, o);
+        if (lane == 0) *s_selectable = selectable;
+    }
+    __syncthreads();
+    // wave w counts, for every key, the keys [w*N/8, (w+1)*N/8) that beat it
+    {
+        uint64_t all[PER];
+#pragma unroll
+        for (int q = 0; q < PER; q++) all[q] = key[lane + 64 * q];
+        int part[PER];
+#pragma unroll
+        for (int q = 0; q < PER; q++) part[q] = 0;
+        const int t0 = wave * (N / 8);
+#pragma unroll
+        for (int u = 0; u < N / 8; u += 2) {
+            const ulonglong2 pr = *reinterpret_cast<const ulonglong2*>(key + t0 + u);
+#pragma unroll
+            for (int q = 0; q < PER; q++) part[q] += (pr.x > all[q] ? 1 : 0) + (pr.y > all[q] ? 1 : 0);
+        }
+#pragma unroll
+        for (int q = 0; q < PER; q++)
+            if (part[q]) atomicAdd(rk + lane + 64 * q, part[q]);
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int q = 0; q < PER; q++) {
+            const int r = rk[lane + 64 * q];
+            if (mine[q] && r < top_k) {
+                ids[r] = lane + 64 * q;
+                w[r] = v[q];
+            }
+        }
+        if (lane == 0) {  // this wave's own LDS writes are in place
+            const int got = min(top_k, *s_selectable);
+            float sw = 0.0f;
+            if (norm_topk)
+                for (int k = 0; k < got; k++) sw = __fadd_rn(sw, w[k]);
+            for (int k = 0; k < top_k; k++) {
+                if (k >= got) {
+                    ids[k] = -1;
+                    w[k] = 0.0f;
+                } else if (norm_topk && sw > 0.0f) {
+                    w[k] = __fdiv_rn(w[k], sw);
+                }
             }
         }
     }
@@ -401,7 +415,11 @@ __device__ __forceinline__ void fast_step(float& acc, float& zacc, int d, uint32
 //            1 / sqrt(mean(x^2) + eps): RMSNorm (norm.rs:4-13) folded into
 //            the GEMV (a single K-slice holds the whole row);
 //   XF_SILU  x' = silu(g) * u (qwen3_moe_model.rs:518-522), times the
-//            slot's routing weight in a routed problem.
+//            slot's routing weight in a routed problem;
+//   XF_MERGE x' = the attention output of head h = k / head_dim, merged
+//            from the chunk states the FAST attention left:
+//            sum_c e^(m_c - M) o_c[k] / sum_c e^(m_c - M) l_c, M = max_c m_c,
+//            over the chunks that held positions at this step.
 // A routed problem (the MoE down projection of all chosen experts) has the
 // chosen experts' rows side by side: its K is top_k * enb blocks, block b
 // being block b % enb of expert sel[b / enb] with x from slot b / enb's g,
@@ -411,8 +429,10 @@ __device__ __forceinline__ void fast_step(float& acc, float& zacc, int d, uint32
 // KIND: FK_PLAIN (a stacked matrix's expert may still come from sel),
 // FK_ROUTE (the workgroup routes itself from router scores) or FK_ROUTED
 // (the routed down projection); all problems of a launch share it.
+// XF: the input transform (XF_NONE, XF_NORM, XF_SILU), also shared by the
+// launch's problems.
 constexpr int FK_PLAIN = 0, FK_ROUTE = 1, FK_ROUTED = 2;
-template <int SCHEME, int KIND>
+template <int SCHEME, int KIND, int XF>
 __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
 {
     // A wave's last group of four may reach up to 2 blocks past the slice:
@@ -430,6 +450,7 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
     // with before the barrier that precedes the x prep
     uint64_t* const route_key = reinterpret_cast<uint64_t*>(xq);
     double* const route_tab = reinterpret_cast<double*>(xq + ROUTE_MAXN * 8);
+    int* const route_rk = reinterpret_cast<int*>(xq + ROUTE_MAXN * 8 + 32 * 8);
 
     const int wgid = blockIdx.x;
     // The problem this workgroup belongs to: the problems' first workgroups
@@ -443,7 +464,7 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
     const KargPtr kargs = (KargPtr)__builtin_amdgcn_kernarg_segment_ptr();
     const auto& P = kargs->p[pi];
     const int nb = P.nb, kg = P.kg, tw = P.tw;
-    const int xform = P.xform;
+    constexpr int xform = XF;
     const uint8_t* codes = P.codes;
     const uint8_t* hplane = SCHEME == 3 ? P.hp : P.codes;
     const uint32_t* params = P.params;
@@ -467,23 +488,56 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
         b0 = kgi * nbk;
         nbl = max(0, min(nb, b0 + nbk) - b0);
         xp = P.x + (size_t)b0 * 128;
-        if (xform == XF_SILU) x2p = P.x2 + (size_t)b0 * 128;
-        if constexpr (KIND == FK_ROUTE) {  // this workgroup routes itself
-            if (wave == 0) {
-                if (P.n_exp <= 128)
-                    route_wave<2>(P.scores, P.n_exp, P.top_k, P.norm_topk, route_key, route_ids, route_w, route_tab);
-                else
-                    route_wave<4>(P.scores, P.n_exp, P.top_k, P.norm_topk, route_key, route_ids, route_w, route_tab);
-            }
-            __syncthreads();
-            e = route_ids[P.sel_k];
-            if (wgid == 0 && (int)threadIdx.x < P.top_k) {
-                P.ids_out[threadIdx.x] = route_ids[threadIdx.x];
-                P.w_out[threadIdx.x] = route_w[threadIdx.x];
-            }
-        } else if (P.sel) {
-            e = P.sel[P.sel_k];
+        if constexpr (xform == XF_SILU) x2p = P.x2 + (size_t)b0 * 128;
+    }
+    // Loads, all issued before any use: x (L2-resident), then parameters,
+    // then weights (HBM): one memory round trip. Each is a buffer load over
+    // exactly the bytes it may touch, so a load past the end returns zeros
+    // without a memory access and every load can be unconditional. (With
+    // FK_ROUTE, routing runs between the x loads and the weight loads.)
+    // x pair p = wave + 8*i: blocks 2p, 2p+1; lane l holds x[4(l&31) .. +3]
+    // of block 2p + (l>>5).
+    constexpr int XP = MAXBK / 16;  // pairs per wave
+    const auto xrs = buf_rsrc(xp, nbl * 512);
+    u32x4 xv[XP], x2v[XP];
+    if constexpr (xform != XF_MERGE) {  // (XF_MERGE reads its chunk states in the prep)
+#pragma unroll
+        for (int i = 0; i < XP; i++)
+            xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
+    }
+    float wkv[XP];  // routed: the routing weight of each x pair's block
+    auto load_x2 = [&]() {  // the second operand of the transform: nw or u
+        const auto x2rs = buf_rsrc(xform == XF_NORM ? P.nw + (size_t)b0 * 128 : x2p, nbl * 512);
+#pragma unroll
+        for (int i = 0; i < XP; i++)
+            x2v[i] = __builtin_amdgcn_raw_buffer_load_b128(x2rs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
+    };
+    // (routing keeps x in flight; the norm weights, L2-resident, wait for it
+    // so that the routing workgroup stays within two per CU's registers)
+    if constexpr ((xform == XF_NORM || xform == XF_SILU) && KIND != FK_ROUTE) load_x2();
+    if constexpr (KIND == FK_ROUTED) {
+#pragma unroll
+        for (int i = 0; i < XP; i++) {
+            const int blk = 2 * (wave + 8 * i) + (lane >> 5);
+            wkv[i] = blk < nbl ? P.rw[blk / P.enb] : 0.0f;
         }
+    }
+    if constexpr (KIND == FK_ROUTE) {  // this workgroup routes itself
+        if (P.n_exp <= 128)
+            route_wg<2>(P.scores, P.n_exp, P.top_k, P.norm_topk, route_key, route_rk, route_ids, route_w,
+                        route_tab, &s_last);
+        else
+            route_wg<4>(P.scores, P.n_exp, P.top_k, P.norm_topk, route_key, route_rk, route_ids, route_w,
+                        route_tab, &s_last);
+        __syncthreads();
+        e = route_ids[P.sel_k];
+        if (wgid == 0 && (int)threadIdx.x < P.top_k) {
+            P.ids_out[threadIdx.x] = route_ids[threadIdx.x];
+            P.w_out[threadIdx.x] = route_w[threadIdx.x];
+        }
+        if constexpr (xform != XF_NONE) load_x2();
+    } else if constexpr (KIND == FK_PLAIN) {
+        if (P.sel) e = P.sel[P.sel_k];
     }
     if (KIND == FK_ROUTE || (KIND == FK_PLAIN && P.sel)) {  // the expert's rows of a stacked matrix
         live = e >= 0;
@@ -500,32 +554,6 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
     const int wb = b0 + kq * q;                      // its first block
     const int g = lane >> 4, j = lane & 15;
 
-    // Loads, all issued before any use: x (L2-resident), then parameters,
-    // then weights (HBM): one memory round trip. Each is a buffer load over
-    // exactly the bytes it may touch, so a load past the end returns zeros
-    // without a memory access and every load can be unconditional.
-    // x pair p = wave + 8*i: blocks 2p, 2p+1; lane l holds x[4(l&31) .. +3]
-    // of block 2p + (l>>5).
-    constexpr int XP = MAXBK / 16;  // pairs per wave
-    const auto xrs = buf_rsrc(xp, nbl * 512);
-    u32x4 xv[XP], x2v[XP];
-#pragma unroll
-    for (int i = 0; i < XP; i++)
-        xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
-    float wkv[XP];  // routed: the routing weight of each x pair's block
-    if (xform != XF_NONE) {  // the second operand of the transform: nw or u
-        const auto x2rs = buf_rsrc(xform == XF_NORM ? P.nw + (size_t)b0 * 128 : x2p, nbl * 512);
-#pragma unroll
-        for (int i = 0; i < XP; i++)
-            x2v[i] = __builtin_amdgcn_raw_buffer_load_b128(x2rs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
-    }
-    if constexpr (KIND == FK_ROUTED) {
-#pragma unroll
-        for (int i = 0; i < XP; i++) {
-            const int blk = 2 * (wave + 8 * i) + (lane >> 5);
-            wkv[i] = blk < nbl ? P.rw[blk / P.enb] : 0.0f;
-        }
-    }
     u32x4 pv;
     u32x4 c[QB];
     u32x2 h[QB];
@@ -588,17 +616,55 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
         const int hi = lane >> 5, k0 = 4 * (lane & 31);
         const int pos0 = frag_pos(k0), pos1 = frag_pos(k0 + 1), pos2 = frag_pos(k0 + 2), pos3 = frag_pos(k0 + 3);
         float sq = 0.0f;
+        int nact = 0;
+        if constexpr (xform == XF_MERGE) {  // the chunks that held positions at this step
+            const int n = (int)P.st->pos + 1, len = (n + ATTN_CHUNKS - 1) / ATTN_CHUNKS;
+            nact = (n + len - 1) / len;
+        }
 #pragma unroll
         for (int i = 0; i < XP; i++) {
             const int p = wave + 8 * i;
             if (2 * p < nbl) {
+                if constexpr (xform == XF_MERGE) {
+                    const int k = (b0 + 2 * p + hi) * 128 + k0, h = k / P.head_dim;
+                    const size_t stride = (size_t)P.n_heads * P.head_dim;
+                    float mv[ATTN_CHUNKS], lv[ATTN_CHUNKS];
+                    float4 ov[ATTN_CHUNKS];
+#pragma unroll
+                    for (int cc = 0; cc < ATTN_CHUNKS; cc++) {
+                        const bool on = cc < nact;
+                        const float2 ml = on ? *reinterpret_cast<const float2*>(P.x2 + ((size_t)cc * P.n_heads + h) * 2)
+                                             : make_float2(-INFINITY, 0.0f);
+                        mv[cc] = ml.x;
+                        lv[cc] = ml.y;
+                        ov[cc] = on ? *reinterpret_cast<const float4*>(P.x + cc * stride + k)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+                    }
+                    float M = -INFINITY;
+#pragma unroll
+                    for (int cc = 0; cc < ATTN_CHUNKS; cc++) M = fmaxf(M, mv[cc]);
+                    float L = 0.0f;
+                    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                    for (int cc = 0; cc < ATTN_CHUNKS; cc++) {
+                        const float w = cc < nact ? __expf(mv[cc] - M) : 0.0f;
+                        L = fmaf(w, lv[cc], L);
+                        a.x = fmaf(w, ov[cc].x, a.x);
+                        a.y = fmaf(w, ov[cc].y, a.y);
+                        a.z = fmaf(w, ov[cc].z, a.z);
+                        a.w = fmaf(w, ov[cc].w, a.w);
+                    }
+                    const float rl = __fdiv_rn(1.0f, L);
+                    xv[i] = u32x4{__float_as_uint(a.x * rl), __float_as_uint(a.y * rl),
+                                  __float_as_uint(a.z * rl), __float_as_uint(a.w * rl)};
+                }
                 float v0 = __uint_as_float(xv[i].x), v1 = __uint_as_float(xv[i].y);
                 float v2 = __uint_as_float(xv[i].z), v3 = __uint_as_float(xv[i].w);
-                if (xform == XF_NORM) {
+                if constexpr (xform == XF_NORM) {
                     sq = fmaf(v0, v0, sq); sq = fmaf(v1, v1, sq); sq = fmaf(v2, v2, sq); sq = fmaf(v3, v3, sq);
                     v0 *= __uint_as_float(x2v[i].x); v1 *= __uint_as_float(x2v[i].y);
                     v2 *= __uint_as_float(x2v[i].z); v3 *= __uint_as_float(x2v[i].w);
-                } else if (xform == XF_SILU) {
+                } else if constexpr (xform == XF_SILU) {
                     const float wk = KIND == FK_ROUTED ? wkv[i] : 1.0f;
                     v0 = __fdividef(v0, 1.0f + __expf(-v0)) * __uint_as_float(x2v[i].x) * wk;
                     v1 = __fdividef(v1, 1.0f + __expf(-v1)) * __uint_as_float(x2v[i].y) * wk;
@@ -628,7 +694,7 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
                 if ((lane & 31) == 0) xs[2 * p + hi] = make_float2(M * (1.0f / 127.0f), hi ? Sb : Sa);
             }
         }
-        if (xform == XF_NORM) {
+        if constexpr (xform == XF_NORM) {
 #pragma unroll
             for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
             if (lane == 0) ssq[wave] = sq;
@@ -714,7 +780,7 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
     if (mine) {  // the tile's parts in order
         sum = red[tt * kw][rr];
         for (int k = 1; k < kw; k++) sum += red[tt * kw + k][rr];
-        if (xform == XF_NORM) {  // RMSNorm's scale of the row x
+        if constexpr (xform == XF_NORM) {  // RMSNorm's scale of the row x
             const float s2 = ((ssq[0] + ssq[1]) + (ssq[2] + ssq[3])) + ((ssq[4] + ssq[5]) + (ssq[6] + ssq[7]));
             sum *= __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(s2, (float)(nb * 128)), P.eps)));
         }
@@ -894,6 +960,9 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         P.norm_topk = J.norm_topk;
         P.ids_out = J.ids_out;
         P.w_out = J.w_out;
+        P.st = J.st;
+        P.head_dim = J.head_dim;
+        P.n_heads = J.n_heads;
         if (J.routed) {  // the chosen experts' rows side by side
             P.enb = (int)m.nb;
             P.nb = J.top_k * (int)m.nb;
@@ -903,6 +972,9 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         // routing reads at most ROUTE_MAXN scores into MAX_JOBS slots
         if (J.xform == XF_NORM && (P.kg != 1 || !J.nw)) return hipErrorInvalidValue;
         if (J.xform == XF_SILU && !J.x2) return hipErrorInvalidValue;
+        if (J.xform == XF_MERGE && (!J.x2 || !J.st || (J.head_dim != 64 && J.head_dim != 128) ||
+                                    (uint64_t)J.n_heads * J.head_dim != m.cols))
+            return hipErrorInvalidValue;
         if (J.routed && (!J.sel || !J.rw || J.xform != XF_SILU || P.kg != 1 || J.top_k < 1 ||
                          (uint64_t)J.top_k * m.nb > fast_max_slice(m.rows, (uint64_t)J.top_k * m.nb)))
             return hipErrorInvalidValue;
@@ -914,19 +986,30 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
     }
     if (wgs == 0) return hipSuccess;
     const int kind = jobs[0].routed ? FK_ROUTED : jobs[0].scores ? FK_ROUTE : FK_PLAIN;
+    const int xf = jobs[0].xform;
     for (int i = 1; i < n; i++)
-        if ((jobs[i].routed ? FK_ROUTED : jobs[i].scores ? FK_ROUTE : FK_PLAIN) != kind) return hipErrorInvalidValue;
+        if ((jobs[i].routed ? FK_ROUTED : jobs[i].scores ? FK_ROUTE : FK_PLAIN) != kind || jobs[i].xform != xf)
+            return hipErrorInvalidValue;
     (void)hipGetLastError();  // report only this launch
     const dim3 grid(wgs), block(FAST_WG);
-    if (scheme == 4) {
-        if (kind == FK_PLAIN) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<4, FK_PLAIN>), grid, block, 0, s, B);
-        else if (kind == FK_ROUTE) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<4, FK_ROUTE>), grid, block, 0, s, B);
-        else hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<4, FK_ROUTED>), grid, block, 0, s, B);
-    } else {
-        if (kind == FK_PLAIN) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<3, FK_PLAIN>), grid, block, 0, s, B);
-        else if (kind == FK_ROUTE) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<3, FK_ROUTE>), grid, block, 0, s, B);
-        else hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<3, FK_ROUTED>), grid, block, 0, s, B);
-    }
+#define WPCG_FAST(S, K, X) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<S, K, X>), grid, block, 0, s, B)
+#define WPCG_FAST_S(S)                                                               \
+    do {                                                                             \
+        if (kind == FK_PLAIN && xf == XF_NONE) WPCG_FAST(S, FK_PLAIN, XF_NONE);      \
+        else if (kind == FK_PLAIN && xf == XF_NORM) WPCG_FAST(S, FK_PLAIN, XF_NORM); \
+        else if (kind == FK_PLAIN && xf == XF_SILU) WPCG_FAST(S, FK_PLAIN, XF_SILU); \
+        else if (kind == FK_PLAIN && xf == XF_MERGE) WPCG_FAST(S, FK_PLAIN, XF_MERGE); \
+        else if (kind == FK_ROUTE && xf == XF_NONE) WPCG_FAST(S, FK_ROUTE, XF_NONE); \
+        else if (kind == FK_ROUTE && xf == XF_NORM) WPCG_FAST(S, FK_ROUTE, XF_NORM); \
+        else if (kind == FK_ROUTED && xf == XF_SILU) WPCG_FAST(S, FK_ROUTED, XF_SILU); \
+        else return hipErrorInvalidValue;                                            \
+    } while (0)
+    if (scheme == 4)
+        WPCG_FAST_S(4);
+    else
+        WPCG_FAST_S(3);
+#undef WPCG_FAST_S
+#undef WPCG_FAST
     return hipGetLastError();
 }
 

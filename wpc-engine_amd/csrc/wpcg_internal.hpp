@@ -77,6 +77,13 @@ struct FastPlan {
 void transcode_rows(int scheme, const uint8_t* blocks, uint64_t r0, uint64_t nrows, uint64_t nb,
                     uint8_t* codes, uint8_t* hp, uint32_t* params_tile_major);
 
+// ---- decode state (decode.hip, gemv.hip) ------------------------------------
+// Device-resident position and token bookkeeping of a decode: the step at
+// position `pos` reads tokens[pos]; its argmax is `last`, and is written to
+// tokens[pos+1] when pos+1 >= n_prompt (a generated token).
+struct DecodeState {
+    uint32_t pos, n_prompt, max_pos, last;
+};
 // ---- kernel launchers (gemv.hip) ----------------------------------------
 // One GEMV y = W x (+ bias). With `sel` set, `m` describes one expert
 // (rows, rows_pad, nb) and its planes are the first of a stack of experts;
@@ -84,8 +91,11 @@ void transcode_rows(int scheme, const uint8_t* blocks, uint64_t r0, uint64_t nro
 // FAST-mode input transforms (the GEMV applies them to x as it reads it):
 //   XF_NORM  RMSNorm of x with weights nw and epsilon eps (norm.rs:4-13):
 //            y = W (x * nw) / sqrt(mean(x^2) + eps); needs kg = 1;
-//   XF_SILU  x = silu(x) * x2 (qwen3_moe_model.rs:518-522).
-constexpr int XF_NONE = 0, XF_NORM = 1, XF_SILU = 2;
+//   XF_SILU  x = silu(x) * x2 (qwen3_moe_model.rs:518-522);
+//   XF_MERGE x = the attention output merged from the chunk states of
+//            launch_attention_chunks: x = part_o, x2 = part_ml, with st,
+//            head_dim and the query head count in the job.
+constexpr int XF_NONE = 0, XF_NORM = 1, XF_SILU = 2, XF_MERGE = 3;
 // Router scores routed inside a FAST launch: at most this many experts.
 constexpr int ROUTE_MAXN = 256;
 struct GemvJob {
@@ -101,6 +111,8 @@ struct GemvJob {
     const float* x2 = nullptr;
     const float* nw = nullptr;
     float eps = 0.0f;
+    const DecodeState* st = nullptr;  // XF_MERGE: the position (the chunk count)
+    int head_dim = 0, n_heads = 0;    // XF_MERGE
     // routed: the rows of experts sel[0..top_k) side by side as one K of
     // top_k * cols (one K-slice: plan->kg = 1), x of slot k at x + k*cols
     // (g) and x2 + k*cols (u), scaled by rw[k]; y = bias + the row sum
@@ -216,12 +228,6 @@ int moe_run(wpcg_moe* m, const float* x, float* out, const float* add, hipStream
             const float* nw = nullptr, float eps = 0.0f);
 
 // ---- decode step (decode.hip) ----------------------------------------------
-// Device-resident position and token bookkeeping of a decode: the step at
-// position `pos` reads tokens[pos]; its argmax is `last`, and is written to
-// tokens[pos+1] when pos+1 >= n_prompt (a generated token).
-struct DecodeState {
-    uint32_t pos, n_prompt, max_pos, last;
-};
 hipError_t launch_embed_tok(const DeviceMatrix& m, const uint32_t* tokens, const DecodeState* st,
                             float* out, hipStream_t s);
 hipError_t launch_rms_norm(int mode, const float* x, const float* w, int n, float eps, float* out,
@@ -229,21 +235,20 @@ hipError_t launch_rms_norm(int mode, const float* x, const float* w, int n, floa
 // q/k RMSNorm + RoPE, KV append, scores, softmax and output of one layer's
 // attention at the state's position; max_pos <= attention_max_pos().
 int attention_max_pos();
-// FAST mode splits the positions into nch chunks over workgroups; the
-// workspace holds each chunk's softmax state, nkv * nch * n_rep * (hd + 2)
-// floats, and nkv zeroed, self-resetting counters. nch = 0 (head_dim or
-// heads per kv head beyond the chunked kernel's limits) runs FAST on the
-// one-workgroup-per-head kernel.
-struct AttnWork {
-    int nch = 0;
-    float* part = nullptr;
-    uint32_t* counters = nullptr;
-};
-int attention_fast_chunks(int nh, int nkv, int hd);
 hipError_t launch_attention(int mode, const float* q, const float* k, const float* v, const float* qn,
                             const float* kn, int nh, int nkv, int hd, float eps, float scale,
                             const float* cos_t, const float* sin_t, const DecodeState* st, float* kc,
-                            float* vc, float* out, const AttnWork& w, hipStream_t s);
+                            float* vc, float* out, hipStream_t s);
+// FAST attention over ATTN_CHUNKS chunks of the positions: each chunk's
+// softmax state goes to part_o [ATTN_CHUNKS][nh][hd] (unnormalised output)
+// and part_ml [ATTN_CHUNKS][nh][2] (max, sum of exps); the o_proj GEMV
+// merges them (XF_MERGE). Needs attention_fast_ok (head_dim 64 or 128).
+constexpr int ATTN_CHUNKS = 16;
+bool attention_fast_ok(int nh, int nkv, int hd);
+hipError_t launch_attention_chunks(const float* q, const float* k, const float* v, const float* qn,
+                                   const float* kn, int nh, int nkv, int hd, float eps, float scale,
+                                   const float* cos_t, const float* sin_t, const DecodeState* st, float* kc,
+                                   float* vc, float* part_o, float* part_ml, hipStream_t s);
 hipError_t launch_add(float* x, const float* y, int n, hipStream_t s);
 hipError_t launch_argmax_next(const float* logits, int n, DecodeState* st, uint32_t* tokens,
                               hipStream_t s);
