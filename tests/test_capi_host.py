@@ -165,13 +165,21 @@ def test_fast_split_plan_never_makes_an_empty_slice():
     # FAST mode splits each row's nb blocks into slices of ceil(nb/k) blocks;
     # every slice must start inside the row (an empty trailing slice would
     # address blocks past the end of the matrix) and fit the LDS stage: 64
-    # blocks with one 16-row tile per workgroup, 32 with two (matrices of
-    # 512 tiles or more), 16 with four (2048 tiles or more, rows of at most
-    # 16 blocks). Checked for every block count and requested split.
+    # blocks with one 16-row tile per workgroup, 32 with two, 16 with four.
+    # Matrices of 32 tiles or more take four tiles when a row has at most 16
+    # blocks, two when it has at most 32; matrices of 512 tiles or more take
+    # two tiles at least. Checked for every block count and requested split.
+    def most_of(rows, nb):
+        tiles = -(-rows // 16)
+        if tiles >= 32 and nb <= 16:
+            return 16
+        if tiles >= 32 and nb <= 32:
+            return 32
+        return 32 if tiles >= 512 else 64
     for nb in range(1, 161):
         for req in [0] + list(range(1, nb + 3)):
-            for rows, most in ((16, 64), (1024, 64), (8176, 64), (8177, 32), (9728, 32),
-                               (32767, 32), (32769, 16 if nb <= 16 else 32), (151936, 16 if nb <= 16 else 32)):
+            for rows in (16, 496, 497, 1024, 8176, 8177, 9728, 151936):
+                most = most_of(rows, nb)
                 k = wpcg.plan_kslices(rows, nb * 128, req)
                 nbk = -(-nb // k)
                 assert 1 <= k <= nb and nbk <= most, (nb, req, rows, k)

@@ -89,7 +89,9 @@ SHAPES = [
     (3, 9728, 2560),
     (3, 2560, 9728),
     (3, 37, 640),
-    (4, 8200, 640),    # two tiles per workgroup, odd tile count (513)
+    (4, 8200, 640),    # four tiles per workgroup, 513 tiles (one in the last workgroup)
+    (4, 488, 2560),    # 31 tiles: one tile per workgroup
+    (4, 520, 4096),    # 33 tiles, 32 blocks: two tiles per workgroup, odd tile count
     (3, 8195, 8320),   # two tiles per workgroup, 65 blocks: two K-slices
     (4, 32784, 2048),  # four tiles per workgroup, 2049 tiles (one in the last workgroup)
     (3, 33001, 1152),  # four tiles per workgroup, ragged last tile

@@ -950,6 +950,10 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         P.sel = J.sel;
         P.sel_k = J.sel_k;
         P.tw = fast_tiles_per_wg(m.rows, J.routed ? (uint64_t)J.top_k * m.nb : m.nb);
+        // the merge reads every chunk state of the whole row per workgroup:
+        // one tile each spreads that over twice the workgroups (the slice
+        // limit only grows, so the plan's K-split still fits)
+        if (J.xform == XF_MERGE) P.tw = 1;
         P.xform = J.xform;
         P.eps = J.eps;
         P.routed = J.routed;
