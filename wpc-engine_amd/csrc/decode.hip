@@ -16,6 +16,7 @@
 #define REF_EXPF_FN __device__ __forceinline__
 #include "ref_expf.h"
 #include "wpcg_internal.hpp"
+#include "wave.h"
 
 namespace wpcg {
 namespace {
@@ -43,8 +44,7 @@ __device__ float sum_squares(const float* x, int n, float* red)
     } else {
         float s = 0.0f;
         for (int i = threadIdx.x; i < n; i += blockDim.x) s = fmaf(x[i], x[i], s);
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+        s = wave_sum(s);
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
         __syncthreads();
         if (threadIdx.x == 0) {
@@ -85,8 +85,7 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
             s_total = s;
         }
     } else {
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o);
+        part = wave_sum(part);
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = part;
         __syncthreads();
         if (threadIdx.x == 0) s_total = (red[0] + red[1]) + (red[2] + red[3]);
@@ -197,8 +196,7 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
     // softmax over w[0..n)
     float m = -INFINITY;
     for (int t = threadIdx.x; t < n; t += AT_WG) m = fmaxf(m, w[t]);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = wave_max(m);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -213,8 +211,7 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
     } else {
         float s = 0.0f;
         for (int t = threadIdx.x; t < n; t += AT_WG) s += w[t];
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+        s = wave_sum(s);
         __syncthreads();
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
         __syncthreads();
@@ -278,9 +275,7 @@ __device__ __forceinline__ void fa_norm_rope(const float* x, const float* w, flo
     const int lane = threadIdx.x & 63;
     const bool on = lane < half;
     const float x1 = on ? x[lane] : 0.0f, x2 = on ? x[lane + half] : 0.0f;
-    float ss = fmaf(x1, x1, x2 * x2);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    const float ss = wave_sum(fmaf(x1, x1, x2 * x2));
     const float scale = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)HD), eps)));
     if (on) {
         const float y1 = (x1 * scale) * w[lane], y2 = (x2 * scale) * w[lane + half];
@@ -404,14 +399,10 @@ __global__ __launch_bounds__(FA_WG) void k_attention_fast(const float* __restric
         // running softmax per head (one wave per head, lanes = positions)
         for (int r = wave; r < n_rep; r += FA_WG / 64) {
             const float v = lane < FA_C ? ps[r][lane] : -INFINITY;
-            float m = v;
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+            const float m = wave_max(v);
             const float mo = s_m[r], mn = fmaxf(mo, m);
             const float e = lane < nt ? __expf(v - mn) : 0.0f;
-            float l = e;
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) l += __shfl_xor(l, off);
+            const float l = wave_sum(e);
             const float corr = __expf(mo - mn);  // 0 on the first block (mo = -inf)
             if (lane < FA_C) ps[r][lane] = e;
             if (lane == 0) {

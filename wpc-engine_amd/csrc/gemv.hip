@@ -29,6 +29,7 @@
 #define REF_EXPF_FN __device__ __forceinline__
 #include "ref_expf.h"
 #include "wpcg_internal.hpp"
+#include "wave.h"
 
 namespace wpcg {
 namespace {
@@ -319,16 +320,14 @@ __device__ __forceinline__ void route_wg(const float* __restrict__ scores, int n
             if (lane + 64 * q >= n) v[q] = -INFINITY;
             m = fmaxf(m, v[q]);
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        m = wave_max(m);
         float sum = 0.0f;
 #pragma unroll
         for (int q = 0; q < PER; q++) {
             v[q] = lane + 64 * q < n ? ref_expf_tab(__fsub_rn(v[q], m), tab) : 0.0f;
             sum += v[q];
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) sum += __shfl_xor(sum, o);
+        sum = wave_sum(sum);
         int selectable = 0;
 #pragma unroll
         for (int q = 0; q < PER; q++) {
@@ -340,8 +339,7 @@ __device__ __forceinline__ void route_wg(const float* __restrict__ scores, int n
             key[i] = mine[q];
             rk[i] = 0;
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) selectable += __shfl_xor(selectable, o);
+        selectable = wave_sum_i(selectable);
         if (lane == 0) *s_selectable = selectable;
     }
     __syncthreads();
@@ -695,8 +693,7 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
             }
         }
         if constexpr (xform == XF_NORM) {
-#pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+            sq = wave_sum(sq);
             if (lane == 0) ssq[wave] = sq;
         }
     }

@@ -13,6 +13,7 @@
 #define REF_EXPF_FN __device__ __forceinline__
 #include "ref_expf.h"
 #include "wpcg_internal.hpp"
+#include "wave.h"
 
 namespace wpcg {
 namespace {
@@ -81,11 +82,9 @@ __global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ w,
             acc = fmaf(row[i], u, acc);
         }
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o);
+    acc = wave_sum(acc);
     if (nw) {
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) sq += __shfl_xor(sq, o);
+        sq = wave_sum(sq);
         acc *= __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(sq, (float)in_f), eps)));
     }
     if (r < out_f && lane == 0) y[r] = bias ? acc + bias[r] : acc;
@@ -101,8 +100,7 @@ __global__ __launch_bounds__(SM_WG) void k_softmax(float* __restrict__ x, int n)
     __shared__ float s_sum;
     float m = -INFINITY;
     for (int i = threadIdx.x; i < n; i += SM_WG) m = fmaxf(m, x[i]);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = wave_max(m);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -214,8 +212,7 @@ __global__ __launch_bounds__(64) void k_softmax_route(const float* __restrict__ 
         v[j] = i < n ? scores[i] : -INFINITY;
         m = fmaxf(m, v[j]);
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    m = wave_max(m);
 #pragma unroll
     for (int j = 0; j < RT_PER; j++) {
         const int i = lane + 64 * j;
