@@ -276,8 +276,13 @@ int wpcg_rms_norm(wpcg_ctx* ctx, const float* x_dev, const float* w_dev, uint32_
  * One step is Model::forward_token (wpc-runtime/src/model.rs:419-547) or
  * Qwen3MoeModel::forward_token (qwen3_moe_model.rs:406-542) followed by
  * argmax (sampling.rs:3-14); it runs as one replayed HIP graph. EXACT mode
- * reproduces the reference's logits bit for bit; FAST mode uses the FAST
- * GEMV and router and tree sums for the long RMSNorm reductions. */
+ * reproduces the reference's logits bit for bit, one launch per operation.
+ * FAST mode computes the same step within a tolerance (FAST GEMVs and
+ * router, tree sums) in six launches per MoE layer (five dense): the
+ * RMSNorms are folded into the GEMVs that read them, attention is split
+ * over chunks of positions whose softmax states o_proj merges, routing runs
+ * inside the expert gate/up launch, and one routed down projection covers
+ * the chosen experts with SiLU*up, the routing weights and the residual. */
 typedef struct {
     uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim;
     uint32_t inter;                          /* dense MLP width (n_experts == 0)   */
@@ -324,9 +329,10 @@ int wpcg_model_generate(wpcg_model* m, const uint32_t* prompt, uint32_t n_prompt
 
 /* Diagnostics, no reference counterpart: copies n floats of one of the
  * decode step's device buffers as the last step left them. which: 0
- * residual, 1 normed (after the final norm), 2 q (the projection), 3 k and
- * 4 v (the last layer's projections), 5 attention output, 7 logits, 9 K
- * cache, 10 V cache ([layer][kv_head][max_pos][head_dim]). */
+ * residual, 1 normed (after the final norm; EXACT mode), 2 q (the
+ * projection), 3 k and 4 v (the last layer's projections), 5 attention
+ * output (EXACT mode; FAST merges it inside o_proj), 7 logits, 9 K cache,
+ * 10 V cache ([layer][kv_head][max_pos][head_dim]). */
 int wpcg_model_debug_read(wpcg_model* m, int which, float* out, uint64_t n);
 
 /* ---- HIP graphs over the context stream (no reference counterpart) ----

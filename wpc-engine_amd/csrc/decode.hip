@@ -304,12 +304,14 @@ __global__ __launch_bounds__(FA_WG) void k_attention_fast(const float* __restric
 {
     constexpr int HD4 = HD / 4, KS = HD + 4;  // KS: key rows 16-byte aligned, offset by 4 banks
     constexpr int NOUT = FA_MAXREP * HD / FA_WG;   // outputs per thread
+    constexpr int G = FA_WG / HD;                  // thread groups over head_dim
     constexpr int NKV = FA_C * HD4 / FA_WG;        // 16-byte key (and value) loads per thread and block
     __shared__ __align__(16) float qs[FA_MAXREP][HD];
     __shared__ __align__(16) float ks[FA_C][KS];
     __shared__ __align__(16) float vs[FA_C][HD];
     __shared__ __align__(16) float kcur[HD], vcur[HD];
-    __shared__ float ps[FA_MAXREP][FA_C];
+    __shared__ float ps[FA_MAXREP][FA_C];                     // scores, head-major
+    __shared__ __align__(16) float pt[FA_C][FA_MAXREP + 4];   // exp weights, position-major
     __shared__ float s_m[FA_MAXREP], s_l[FA_MAXREP], s_corr[FA_MAXREP];
     const int j = blockIdx.x / FA_NCH, c = blockIdx.x % FA_NCH;
     const uint32_t pos = st->pos, max_pos = st->max_pos;
@@ -356,6 +358,10 @@ __global__ __launch_bounds__(FA_WG) void k_attention_fast(const float* __restric
         s_m[threadIdx.x] = -INFINITY;
         s_l[threadIdx.x] = 0.0f;
     }
+    // output (r0 + k, d) of thread (g, d): consecutive heads per thread, so
+    // one 16-byte read of pt serves four of them
+    const int g = threadIdx.x / HD, d = threadIdx.x % HD;
+    const int nper = (n_rep + G - 1) / G, r0 = g * nper;
     float o[NOUT];
 #pragma unroll
     for (int u = 0; u < NOUT; u++) o[u] = 0.0f;
@@ -404,7 +410,7 @@ __global__ __launch_bounds__(FA_WG) void k_attention_fast(const float* __restric
             const float e = lane < nt ? __expf(v - mn) : 0.0f;
             const float l = wave_sum(e);
             const float corr = __expf(mo - mn);  // 0 on the first block (mo = -inf)
-            if (lane < FA_C) ps[r][lane] = e;
+            if (lane < FA_C) pt[lane][r] = e;
             if (lane == 0) {
                 s_m[r] = mn;
                 s_l[r] = fmaf(s_l[r], corr, l);
@@ -413,25 +419,37 @@ __global__ __launch_bounds__(FA_WG) void k_attention_fast(const float* __restric
         }
         __syncthreads();
 #pragma unroll
-        for (int u = 0; u < NOUT; u++) {
-            const int i = threadIdx.x + u * FA_WG, r = i / HD, d = i % HD;
-            if (r < n_rep) {
-                float acc = o[u] * s_corr[r];
+        for (int u = 0; u < NOUT; u++)
+            if (u < nper && r0 + u < n_rep) o[u] *= s_corr[r0 + u];
+        if ((nper & 3) == 0) {
+#pragma unroll 4
+            for (int t = 0; t < nt; t++) {
+                const float v = vs[t][d];
 #pragma unroll
-                for (int t = 0; t < FA_C; t++)
-                    if (t < nt) acc = fmaf(ps[r][t], vs[t][d], acc);
-                o[u] = acc;
+                for (int u = 0; u < NOUT; u += 4)
+                    if (u < nper) {
+                        const float4 w4 = *reinterpret_cast<const float4*>(&pt[t][r0 + u]);
+                        o[u] = fmaf(w4.x, v, o[u]);
+                        o[u + 1] = fmaf(w4.y, v, o[u + 1]);
+                        o[u + 2] = fmaf(w4.z, v, o[u + 2]);
+                        o[u + 3] = fmaf(w4.w, v, o[u + 3]);
+                    }
+            }
+        } else {
+            for (int t = 0; t < nt; t++) {
+                const float v = vs[t][d];
+#pragma unroll
+                for (int u = 0; u < NOUT; u++)
+                    if (u < nper) o[u] = fmaf(pt[t][r0 + u], v, o[u]);
             }
         }
-        __syncthreads();  // before the next block overwrites ks, vs, ps
+        __syncthreads();  // before the next block overwrites ks, vs, ps, pt
     }
 
     // the chunk's state (the next launch, o_proj, reads it)
 #pragma unroll
-    for (int u = 0; u < NOUT; u++) {
-        const int i = threadIdx.x + u * FA_WG, r = i / HD, d = i % HD;
-        if (r < n_rep) part_o[((size_t)c * nh + j * n_rep + r) * HD + d] = o[u];
-    }
+    for (int u = 0; u < NOUT; u++)
+        if (u < nper && r0 + u < n_rep) part_o[((size_t)c * nh + j * n_rep + r0 + u) * HD + d] = o[u];
     if ((int)threadIdx.x < 2 * n_rep) {
         const int r = threadIdx.x >> 1;
         part_ml[((size_t)c * nh + j * n_rep + r) * 2 + (threadIdx.x & 1)] = (threadIdx.x & 1) ? s_l[r] : s_m[r];
