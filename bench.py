@@ -42,7 +42,7 @@ BPB = {3: 100, 4: 68}
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (bench.py --pmc-pass) and scaled by
 # the same counters' reading for a copy kernel of known size; see
 # profiles/k_gemv_fast_cfg1_v3_traffic.txt. None where not measured.
-TRAFFIC = {(3, "fast"): 20023459}
+TRAFFIC = {(3, "fast"): 20093248}
 
 
 def log(msg):
@@ -102,7 +102,7 @@ def decode_token_bytes(c, bpb=68):
     return c["n_layers"] * (attn + experts + router) + blocks(c["vocab"], H)
 
 
-def decode_bench(ctx, wpcg, synth, n_prompt, n_new, cpu_tokens):
+def decode_bench(ctx, wpcg, synth, n_prompt, n_new, cpu_tokens, eager=False):
     """Greedy decode of the Qwen3-30B-A3B-shaped v4 model:
     seeded weights ~N(0, 0.02) encoded as the artifact compiler does; one
     layer's expert weights are generated and uploaded to every layer (48
@@ -121,6 +121,8 @@ def decode_bench(ctx, wpcg, synth, n_prompt, n_new, cpu_tokens):
             keep[name] = arr
     log(f"decode model built in {time.perf_counter() - t0:.1f} s ({resident / 1e9:.2f} GB resident)")
     prompt = np.random.default_rng(31).integers(0, cfg["vocab"], n_prompt).astype(np.uint32)
+    if eager:  # launch by launch, for kernel traces (a trace cannot see inside graph replays)
+        model.set_graphs(False)
     out = {}
     for mode, key, n in ((wpcg.MODE_FAST, "fast", n_new), (wpcg.MODE_EXACT, "exact", 16)):
         model.set_mode(mode)
@@ -266,6 +268,8 @@ def main():
     ap.add_argument("--decode-prompt", type=int, default=256)
     ap.add_argument("--decode-new", type=int, default=256)
     ap.add_argument("--decode-cpu-tokens", type=int, default=4)
+    ap.add_argument("--decode-eager", action="store_true",
+                    help="decode steps launch by launch instead of graph replays (for kernel traces)")
     ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM (config 4) lines")
     args = ap.parse_args()
 
@@ -413,9 +417,9 @@ def main():
     decode = None
     if not args.no_decode:
         decode = decode_bench(ctx, wpcg, synth, args.decode_prompt, args.decode_new,
-                              0 if args.no_cpu_baseline else args.decode_cpu_tokens)
+                              0 if args.no_cpu_baseline else args.decode_cpu_tokens, args.decode_eager)
 
-    kname = f"k_gemv_exact<{scheme}>" if mode == wpcg.MODE_EXACT else f"k_gemv_fast<{scheme}>"
+    kname = f"k_gemv_exact<{scheme}>" if mode == wpcg.MODE_EXACT else f"k_gemv_fast<{scheme}, 0, 0>"
     rec = {
         "metric": METRIC,
         "value": round(value, 2),
