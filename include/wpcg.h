@@ -270,6 +270,51 @@ int wpcg_moe_forward(wpcg_moe* m, const float* x_dev, float* out_dev, int32_t* i
 int wpcg_rms_norm(wpcg_ctx* ctx, const float* x_dev, const float* w_dev, uint32_t n, float eps,
                   float* out_dev, int mode, wpcg_stream stream);
 
+/* ---- checkpoint I/O: safetensors and config.json ----
+ * The dense checkpoint the reference reads the fp32 tensors from (norms and
+ * routers; WPC only compresses 2-D matrices), as one model.safetensors or
+ * as shards named by model.safetensors.index.json. Every file is mapped and
+ * validated as the `safetensors` crate 0.4.5 validates it (header length,
+ * '{' start, offsets tiling the data in order, sizes matching shape and
+ * dtype); where the reference panics (invalid file, missing tensor,
+ * unsupported dtype) these return E_FORMAT, E_NOTFOUND, E_UNSUPPORTED. */
+typedef struct wpcg_safetensors wpcg_safetensors;
+/* ShardedSafetensors::open (wpc-runtime/src/weights.rs:197-244): the
+ * directory's model.safetensors when present, else the shards of its
+ * model.safetensors.index.json `weight_map` (E_IO when neither exists). */
+int wpcg_safetensors_open(const char* model_dir, wpcg_safetensors** out);
+/* SafetensorsFile::open (weights.rs:130-138), one file. */
+int wpcg_safetensors_open_file(const char* path, wpcg_safetensors** out);
+int wpcg_safetensors_close(wpcg_safetensors* st);
+/* SafetensorsFile::names (weights.rs:140-142): every tensor, header order,
+ * shard after shard. The name stays valid until close. */
+int wpcg_safetensors_tensor_count(wpcg_safetensors* st, uint64_t* n);
+int wpcg_safetensors_name(wpcg_safetensors* st, uint64_t i, const char** name);
+/* ShardedSafetensors::shape (weights.rs:256-263): *ndim always set; E_ARG
+ * when it exceeds max_dims. */
+int wpcg_safetensors_shape(wpcg_safetensors* st, const char* name, uint32_t* ndim, uint64_t* dims,
+                           uint32_t max_dims);
+/* The header's dtype string ("F32", "BF16", ...). No reference counterpart. */
+int wpcg_safetensors_dtype(wpcg_safetensors* st, const char* name, const char** dtype);
+/* ShardedSafetensors::read_f32 / SafetensorsFile::read_f32
+ * (weights.rs:149-178, 246-254): F32 as stored, F16 exactly (a NaN gains
+ * the quiet bit, as half 2.x converts it), BF16 as its bits << 16; n must
+ * equal the element count (E_SHAPE). */
+int wpcg_safetensors_read_f32(wpcg_safetensors* st, const char* name, float* out, uint64_t n);
+/* Config::load / Config::from_json_str (wpc-runtime/src/config.rs:85-95)
+ * into a model config: required vocab_size, hidden_size,
+ * num_hidden_layers, num_attention_heads, num_key_value_heads,
+ * intermediate_size, rope_theta, rms_norm_eps; tie_word_embeddings
+ * defaults to true; head_dim falls back to hidden_size /
+ * num_attention_heads (Config::head_dim, config.rs:59-62). model_type
+ * "qwen3_moe" selects the MoE decoder, as wpc-runtime/src/main.rs:73-77
+ * does, with the fields of moe_dims (qwen3_moe_model.rs:121-135: each
+ * required, top_k in 1..=num_experts, norm_topk_prob defaulting to true);
+ * any other config is a dense decoder (n_experts = 0). max_pos, the
+ * KV-cache length, is the caller's. E_FORMAT names the offending field. */
+int wpcg_config_parse(const char* json_text, uint32_t max_pos, struct wpcg_model_config_s* out);
+int wpcg_config_load(const char* path, uint32_t max_pos, struct wpcg_model_config_s* out);
+
 /* ---- device-resident decode step ----
  * A dense Qwen3 (n_experts == 0, SwiGLU MLP) or Qwen3-MoE decoder whose
  * weights, fp32 KV cache, activations, position and tokens stay on the GPU.
@@ -283,7 +328,7 @@ int wpcg_rms_norm(wpcg_ctx* ctx, const float* x_dev, const float* w_dev, uint32_
  * over chunks of positions whose softmax states o_proj merges, routing runs
  * inside the expert gate/up launch, and one routed down projection covers
  * the chosen experts with SiLU*up, the routing weights and the residual. */
-typedef struct {
+typedef struct wpcg_model_config_s {
     uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim;
     uint32_t inter;                          /* dense MLP width (n_experts == 0)   */
     uint32_t vocab;
@@ -307,6 +352,12 @@ int wpcg_model_set_tensor(wpcg_model* m, const char* name, const void* data, uin
 /* Every quantized matrix of the config from an artifact (the fp32 tensors,
  * which the reference reads from safetensors, go through set_tensor). */
 int wpcg_model_load_artifact(wpcg_model* m, wpcg_artifact* a);
+/* The fp32 tensors from a checkpoint by the reference's names, as
+ * build_layers and the loaders read them (qwen3_moe_model.rs:140-196,
+ * 327-365; qwen3_model.rs:40-90, 187-206): model.norm.weight and per
+ * layer {input,post_attention}_layernorm, self_attn.{q,k}_norm and, for
+ * MoE, the router mlp.gate.weight (F32/F16/BF16 widened to fp32). */
+int wpcg_model_load_safetensors(wpcg_model* m, wpcg_safetensors* st);
 int wpcg_model_set_mode(wpcg_model* m, int mode);
 /* Steps as one replayed HIP graph (enabled, the default) or enqueued launch
  * by launch (for tools that cannot trace graph replays). No reference

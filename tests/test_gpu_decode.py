@@ -133,3 +133,29 @@ def test_decode_errors(ctx):
         m.set_tensor("model.norm.weight", np.ones(3, np.float32))
     assert e.value.code == wpcg.E_SHAPE
     m.close()
+
+
+@pytest.mark.parametrize("name,cfg,scheme,dtype,shards,seed", [("dense-v3-bf16", DENSE, 3, "BF16", 1, 121),
+                                                               ("moe-v4-f16-sharded", MOE, 4, "F16", 3, 222)])
+def test_model_loads_from_checkpoint(ctx, tmp_path, name, cfg, scheme, dtype, shards, seed):
+    """load_wpc_v{3,4} end to end: config.json, the norms and routers from
+    safetensors (non-unit norms stored in `dtype`), the matrices from the
+    artifact; EXACT logits bit-identical to the oracle's on the tensors as
+    the checkpoint holds them."""
+    print(f"[gpu] checkpoint load {name}", flush=True)
+    tensors = synth.write_checkpoint(str(tmp_path / "model"), str(tmp_path / "wpc"), cfg, scheme, seed,
+                                     wpcg.encode, dtype, shards)
+    m = wpcg.Model.load_wpc(ctx, scheme, tmp_path / "model", tmp_path / "wpc", cfg["max_pos"])
+    assert m.cfg.as_dict()["n_experts"] == cfg["n_experts"]
+    kern = O.KERNEL_AVX2 if O.have_avx2() else O.KERNEL_FUSED
+    ref = O.Model(cfg, tensors, cfg["max_pos"], kern, 16)
+    tok = 5
+    for step in range(12):
+        r = ref.forward_token(tok)
+        g, a = m.forward_token(tok)
+        assert np.array_equal(bits(g), bits(r)), f"{name}: logits differ at step {step}"
+        tok = O.argmax(r)
+        assert a == tok
+    print(f"[gpu] checkpoint load {name}: 12 steps bit-identical", flush=True)
+    m.close()
+    ref.close()

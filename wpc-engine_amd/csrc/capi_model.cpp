@@ -494,6 +494,28 @@ int wpcg_model_load_artifact(wpcg_model* m, wpcg_artifact* a)
     return WPCG_OK;
 }
 
+int wpcg_model_load_safetensors(wpcg_model* m, wpcg_safetensors* st)
+{
+    if (!m || !st) return fail(WPCG_E_ARG, "null argument");
+    const wpcg_model_config& c = m->cfg;
+    std::vector<std::pair<std::string, uint64_t>> names = {{"model.norm.weight", c.hidden}};
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        names.push_back({p + "input_layernorm.weight", c.hidden});
+        names.push_back({p + "post_attention_layernorm.weight", c.hidden});
+        names.push_back({p + "self_attn.q_norm.weight", c.head_dim});
+        names.push_back({p + "self_attn.k_norm.weight", c.head_dim});
+        if (c.n_experts) names.push_back({p + "mlp.gate.weight", (uint64_t)c.n_experts * c.hidden});
+    }
+    std::vector<float> buf;
+    for (const auto& [n, count] : names) {
+        buf.resize(count);
+        if (int rc = wpcg_safetensors_read_f32(st, n.c_str(), buf.data(), count)) return rc;
+        if (int rc = wpcg_model_set_tensor(m, n.c_str(), buf.data(), count * sizeof(float))) return rc;
+    }
+    return WPCG_OK;
+}
+
 int wpcg_model_set_mode(wpcg_model* m, int mode)
 {
     if (!m || (mode != WPCG_MODE_EXACT && mode != WPCG_MODE_FAST)) return fail(WPCG_E_ARG, "null model or bad mode");

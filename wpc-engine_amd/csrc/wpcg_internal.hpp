@@ -257,6 +257,20 @@ hipError_t launch_add(float* x, const float* y, int n, hipStream_t s);
 hipError_t launch_argmax_next(const float* logits, int n, DecodeState* st, uint32_t* tokens,
                               hipStream_t s);
 
+// ---- JSON DOM (json.cpp): safetensors headers, their index, config.json ----
+struct JsonValue {
+    enum Kind { NUL, BOOL, NUM, STR, ARR, OBJ } kind = NUL;
+    bool b = false;
+    double num = 0.0;
+    bool is_uint = false;  // an integer literal that fits uint64 (u holds it)
+    uint64_t u = 0;
+    std::string str;
+    std::vector<JsonValue> arr;
+    std::vector<std::pair<std::string, JsonValue>> obj;
+    const JsonValue* get(const std::string& key) const;  // null if absent or not an object
+};
+bool json_parse(const char* text, size_t n, JsonValue& out, std::string& err);
+
 // ---- minimal JSON (for model_v{3,4}.meta) ---------------------------------
 struct MetaEntry {
     std::vector<uint64_t> shape;

@@ -99,6 +99,17 @@ _SIGS = {
     "wpcg_model_destroy": (C.c_int, [_p]),
     "wpcg_model_set_tensor": (C.c_int, [_p, C.c_char_p, _p, _u64]),
     "wpcg_model_load_artifact": (C.c_int, [_p, _p]),
+    "wpcg_model_load_safetensors": (C.c_int, [_p, _p]),
+    "wpcg_safetensors_open": (C.c_int, [C.c_char_p, _pp]),
+    "wpcg_safetensors_open_file": (C.c_int, [C.c_char_p, _pp]),
+    "wpcg_safetensors_close": (C.c_int, [_p]),
+    "wpcg_safetensors_tensor_count": (C.c_int, [_p, _u64p]),
+    "wpcg_safetensors_name": (C.c_int, [_p, _u64, C.POINTER(C.c_char_p)]),
+    "wpcg_safetensors_shape": (C.c_int, [_p, C.c_char_p, C.POINTER(C.c_uint32), _u64p, C.c_uint32]),
+    "wpcg_safetensors_dtype": (C.c_int, [_p, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "wpcg_safetensors_read_f32": (C.c_int, [_p, C.c_char_p, _p, _u64]),
+    "wpcg_config_parse": (C.c_int, [C.c_char_p, C.c_uint32, _p]),
+    "wpcg_config_load": (C.c_int, [C.c_char_p, C.c_uint32, _p]),
     "wpcg_model_set_mode": (C.c_int, [_p, C.c_int]),
     "wpcg_model_reset": (C.c_int, [_p]),
     "wpcg_model_set_graphs": (C.c_int, [_p, C.c_int]),
@@ -670,6 +681,86 @@ class ModelConfig(C.Structure):
         return {f: getattr(self, f) for f, _ in self._fields_}
 
 
+def config_from_json_str(text: str, max_pos: int) -> ModelConfig:
+    """Config::from_json_str (wpc-runtime/src/config.rs:85-88) with head_dim
+    (config.rs:59-62) and, for Qwen3-MoE, moe_dims
+    (qwen3_moe_model.rs:121-135) resolved; max_pos is the KV-cache length."""
+    cfg = ModelConfig()
+    check(lib.wpcg_config_parse(text.encode(), max_pos, C.byref(cfg)))
+    return cfg
+
+
+def config_load(path, max_pos: int) -> ModelConfig:
+    """Config::load (config.rs:90-93)."""
+    cfg = ModelConfig()
+    check(lib.wpcg_config_load(os.fsencode(path), max_pos, C.byref(cfg)))
+    return cfg
+
+
+class ShardedSafetensors:
+    """A checkpoint directory: model.safetensors, or the shards its
+    model.safetensors.index.json names (ShardedSafetensors,
+    wpc-runtime/src/weights.rs:180-264). Host memory only."""
+
+    def __init__(self, handle):
+        self.h = handle
+
+    @classmethod
+    def open(cls, model_dir) -> "ShardedSafetensors":
+        h = C.c_void_p()
+        check(lib.wpcg_safetensors_open(os.fsencode(model_dir), C.byref(h)))
+        return cls(h)
+
+    def names(self) -> list[str]:
+        n = C.c_uint64()
+        check(lib.wpcg_safetensors_tensor_count(self.h, C.byref(n)))
+        out = []
+        for i in range(n.value):
+            p = C.c_char_p()
+            check(lib.wpcg_safetensors_name(self.h, i, C.byref(p)))
+            out.append(p.value.decode())
+        return out
+
+    def shape(self, name: str) -> list[int]:
+        nd = C.c_uint32()
+        dims = (C.c_uint64 * 16)()
+        check(lib.wpcg_safetensors_shape(self.h, name.encode(), C.byref(nd), dims, 16))
+        return [dims[i] for i in range(nd.value)]
+
+    def dtype(self, name: str) -> str:
+        p = C.c_char_p()
+        check(lib.wpcg_safetensors_dtype(self.h, name.encode(), C.byref(p)))
+        return p.value.decode()
+
+    def read_f32(self, name: str) -> np.ndarray:
+        """The tensor widened to float32, flat row-major."""
+        n = int(np.prod(self.shape(name), dtype=np.uint64))
+        out = np.empty(n, np.float32)
+        check(lib.wpcg_safetensors_read_f32(self.h, name.encode(), _np_ptr(out), n))
+        return out
+
+    def close(self):
+        if self.h:
+            lib.wpcg_safetensors_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class SafetensorsFile(ShardedSafetensors):
+    """One .safetensors file (SafetensorsFile, weights.rs:125-178)."""
+
+    @classmethod
+    def open(cls, path) -> "SafetensorsFile":
+        h = C.c_void_p()
+        check(lib.wpcg_safetensors_open_file(os.fsencode(path), C.byref(h)))
+        return cls(h)
+
+
 class Model:
     """Dense Qwen3 / Qwen3-MoE decoder resident on the GPU
     (Model::forward_token, model.rs:419-547; qwen3_moe_model.rs:406-542)."""
@@ -688,6 +779,31 @@ class Model:
     def load_artifact(self, data: "WpcModelData"):
         check(lib.wpcg_model_load_artifact(self.h, data.h))
         return self
+
+    def load_safetensors(self, st: ShardedSafetensors):
+        """Norms and routers from the dense checkpoint, as load_wpc_v4 reads
+        them (qwen3_moe_model.rs:140-196, 327-365; qwen3_model.rs:40-90)."""
+        check(lib.wpcg_model_load_safetensors(self.h, st.h))
+        return self
+
+    @classmethod
+    def load_wpc(cls, ctx: Context, scheme: int, model_dir, wpc_dir, max_pos: int) -> "Model":
+        """load_wpc_v4 / load_wpc_v3 (qwen3_moe_model.rs:327-365,
+        qwen3_model.rs:187-206): config.json and the fp32 tensors from
+        model_dir, every quantized matrix from the artifact in wpc_dir."""
+        cfg = config_load(os.path.join(os.fsdecode(model_dir), "config.json"), max_pos)
+        m = cls(ctx, scheme, cfg)
+        st = ShardedSafetensors.open(model_dir)
+        try:
+            m.load_safetensors(st)
+        finally:
+            st.close()
+        data = WpcModelData.open(wpc_dir, scheme)
+        try:
+            m.load_artifact(data)
+        finally:
+            data.close()
+        return m
 
     def set_mode(self, mode: int):
         check(lib.wpcg_model_set_mode(self.h, mode))

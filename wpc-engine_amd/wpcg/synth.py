@@ -11,6 +11,12 @@ reference's compiler lays them out (wpc-compiler/src/main.rs:644-696): blocks
 appended tensor after tensor, meta {"layers":[{name, shape, offset_bytes,
 size_bytes}], "block_size":128}, with tensors in the compiler's locality
 order (tensor_sort_key, wpc-compiler/src/main.rs:93-128).
+
+safetensors_bytes writes the dense checkpoint format the reference reads
+its fp32 tensors from (an 8-byte little-endian header length, the JSON
+header, the data); write_checkpoint lays out a whole model directory
+(config.json, one or several safetensors files with an index) beside its
+artifact.
 """
 from __future__ import annotations
 
@@ -159,3 +165,137 @@ def model_tensors(cfg, scheme: int, seed: int, encode, std: float = 0.02, share_
                 yield p + f"mlp.experts.{e}.gate_proj.weight", g
                 yield p + f"mlp.experts.{e}.up_proj.weight", u
                 yield p + f"mlp.experts.{e}.down_proj.weight", d
+
+
+# dtype name -> (numpy dtype of the stored element, bytes per element); BF16
+# is stored as the upper 16 bits of a float32.
+ST_DTYPES = {"F32": ("<f4", 4), "F16": ("<f2", 2), "BF16": ("<u2", 2), "F64": ("<f8", 8),
+             "I32": ("<i4", 4), "I64": ("<i8", 8), "U8": ("u1", 1), "I8": ("i1", 1),
+             "BOOL": ("u1", 1), "I16": ("<i2", 2), "U16": ("<u2", 2), "U32": ("<u4", 4),
+             "U64": ("<u8", 8), "F8_E5M2": ("u1", 1), "F8_E4M3": ("u1", 1)}
+
+
+def to_bf16_bits(a) -> np.ndarray:
+    """float32 -> bfloat16 bit patterns, round to nearest even (NaN kept a NaN)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    nan = np.isnan(np.ascontiguousarray(a, np.float32))
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def safetensors_bytes(tensors, metadata=None) -> bytes:
+    """A .safetensors file: tensors is an iterable of (name, dtype, shape,
+    raw bytes) laid out in that order; metadata an optional str->str map."""
+    header, chunks, off = {}, [], 0
+    if metadata is not None:
+        header["__metadata__"] = metadata
+    for name, dtype, shape, raw in tensors:
+        raw = bytes(raw)
+        header[name] = {"dtype": dtype, "shape": list(shape), "data_offsets": [off, off + len(raw)]}
+        chunks.append(raw)
+        off += len(raw)
+    h = json.dumps(header, separators=(",", ":")).encode()
+    h += b" " * (-len(h) % 8)  # the writer's alignment padding
+    return len(h).to_bytes(8, "little") + h + b"".join(chunks)
+
+
+def encode_st(name: str, dtype: str, a) -> tuple:
+    """(name, dtype, shape, raw) for a float array stored as F32/F16/BF16."""
+    a = np.asarray(a, np.float32)
+    if dtype == "F32":
+        raw = a.astype("<f4").tobytes()
+    elif dtype == "F16":
+        raw = a.astype("<f2").tobytes()
+    elif dtype == "BF16":
+        raw = to_bf16_bits(a).astype("<u2").tobytes()
+    else:
+        raise ValueError(dtype)
+    return name, dtype, a.shape, raw
+
+
+def widened(dtype: str, a) -> np.ndarray:
+    """The float32 values a reader of `dtype` storage sees."""
+    a = np.asarray(a, np.float32)
+    if dtype == "F16":
+        return a.astype(np.float16).astype(np.float32)
+    if dtype == "BF16":
+        return (to_bf16_bits(a).astype(np.uint32) << 16).view(np.float32).reshape(a.shape)
+    return a.copy()
+
+
+def config_json(cfg) -> dict:
+    """config.json fields of a wpcg.ModelConfig (or dict of its fields), in
+    the Hugging Face names the reference's Config reads."""
+    c = cfg if isinstance(cfg, dict) else cfg.as_dict()
+    j = {"model_type": "qwen3_moe" if c["n_experts"] else "qwen3",
+         "vocab_size": c["vocab"], "hidden_size": c["hidden"], "num_hidden_layers": c["n_layers"],
+         "num_attention_heads": c["n_heads"], "num_key_value_heads": c["n_kv_heads"],
+         "intermediate_size": c["inter"] or 6144, "head_dim": c["head_dim"],
+         "rope_theta": float(c["rope_theta"]), "rms_norm_eps": float(c["eps"]),
+         "tie_word_embeddings": bool(c["tied"])}
+    if c["n_experts"]:
+        j.update(num_experts=c["n_experts"], num_experts_per_tok=c["top_k"],
+                 moe_intermediate_size=c["moe_inter"], norm_topk_prob=bool(c["norm_topk"]))
+    return j
+
+
+def write_checkpoint(model_dir: str, wpc_dir: str, cfg, scheme: int, seed: int, encode,
+                     dtype: str = "BF16", shards: int = 1) -> dict:
+    """A model directory as the reference loads it: config.json plus the fp32
+    tensors (norms ~1 + N(0, 0.1), routers ~N(0, 0.02)) in safetensors of
+    `dtype`, one model.safetensors or `shards` files with an index; and the
+    quantized matrices in a WPC artifact under wpc_dir. Returns every tensor
+    as the decoder sees it (fp32 tensors widened from their storage)."""
+    os.makedirs(model_dir, exist_ok=True)
+    with open(os.path.join(model_dir, "config.json"), "w") as f:
+        json.dump(config_json(cfg), f, indent=2)
+    rng = np.random.default_rng(seed + 7)
+    tensors, dense, quant = {}, [], []
+    for name, arr in model_tensors(cfg, scheme, seed, encode):
+        if arr.dtype == np.uint8:
+            quant.append((name, None, arr))
+            tensors[name] = arr
+            continue
+        if name.endswith("mlp.gate.weight"):
+            v = arr
+        else:
+            v = (1.0 + 0.1 * rng.standard_normal(arr.shape)).astype(np.float32)
+        dense.append(encode_st(name, dtype, v))
+        tensors[name] = widened(dtype, v).reshape(-1)
+    c = cfg if isinstance(cfg, dict) else cfg.as_dict()
+    write_artifact(wpc_dir, scheme, [(n, _quant_shape(n, c), b) for n, _, b in quant])
+    if shards <= 1:
+        with open(os.path.join(model_dir, "model.safetensors"), "wb") as f:
+            f.write(safetensors_bytes(dense, {"format": "pt"}))
+    else:
+        weight_map = {}
+        for s in range(shards):
+            fname = f"model-{s + 1:05d}-of-{shards:05d}.safetensors"
+            part = dense[s::shards]
+            with open(os.path.join(model_dir, fname), "wb") as f:
+                f.write(safetensors_bytes(part, {"format": "pt"}))
+            for t in part:
+                weight_map[t[0]] = fname
+        with open(os.path.join(model_dir, "model.safetensors.index.json"), "w") as f:
+            json.dump({"metadata": {"total_size": sum(len(t[3]) for t in dense)},
+                       "weight_map": weight_map}, f, indent=2)
+    return tensors
+
+
+def _quant_shape(name: str, c) -> list:
+    """[out, in] of a quantized matrix by its name."""
+    H, hd = c["hidden"], c["head_dim"]
+    qd, kvd = c["n_heads"] * hd, c["n_kv_heads"] * hd
+    I = c["moe_inter"] if c["n_experts"] else c["inter"]
+    if "embed_tokens" in name or name.startswith("lm_head"):
+        return [c["vocab"], H]
+    if "q_proj" in name:
+        return [qd, H]
+    if "k_proj" in name or "v_proj" in name:
+        return [kvd, H]
+    if "o_proj" in name:
+        return [H, qd]
+    if "down_proj" in name:
+        return [H, I]
+    return [I, H]
