@@ -170,9 +170,13 @@ int wpcg_linear_matvec_multi(int n, wpcg_linear* const* lins, const float* const
  * dots accumulate in fp32 and its scale and zero point are applied in fp32
  * (the weights are never rounded). The first batched call on a linear
  * allocates its workspace (about 16 KiB per 128 inputs plus the split-K
- * partials); make it before capturing a graph that contains the call. */
+ * partials); make it before capturing a graph that contains the call.
+ * WPCG_DTYPE_F32_SPLIT: fp32 X fed to the matrix cores as two bf16 terms
+ * hi = bf16(x), lo = bf16(x - hi), so X is carried to a relative 2^-18
+ * (32 rows of X per launch; twice the matrix-core work). */
 #define WPCG_DTYPE_F32  0
 #define WPCG_DTYPE_BF16 1
+#define WPCG_DTYPE_F32_SPLIT 2
 int wpcg_linear_gemm(wpcg_linear* lin, const void* x_dev, int x_dtype, uint32_t M, float* y_dev,
                      wpcg_stream stream);
 /* Host-pointer twin (synchronous). */

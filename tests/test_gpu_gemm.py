@@ -11,6 +11,11 @@ in float64 as the truth:
   * X given in fp32: X is rounded to bf16 (relative 2^-9 per value), so
         |y - y_true| <= (2^-9 + 3e-5) * sum_k (|zp_k| + code_k*scale_k) * |x_k|
     with y_true computed from the unrounded X.
+  * X given in fp32 with DTYPE_F32_SPLIT: hi = bf16(x) and lo = bf16(x - hi)
+    both go through the matrix cores (|x - hi - lo| <= 2^-18 |x|), so the
+    bf16-input bound holds with 2^-17 added; and, against a plain rounding
+    to bf16, the largest error stays under 2e-5 of the largest |y|, which
+    rounding X to bf16 exceeds by ~50x on these inputs.
 
 A wrong k-order, lane, column or block index moves outputs by ~1% of the
 same sum, 300x above the first bound; the bf16-input cases catch that.
@@ -26,6 +31,8 @@ pytestmark = pytest.mark.gpu
 
 TOL_ACC = 3e-5
 TOL_BF16 = 2.0 ** -9 + TOL_ACC
+TOL_SPLIT = 2.0 ** -17 + TOL_ACC
+SPLIT_REL = 2e-5  # max |y - y_true| / max |y_true|, split X
 
 
 @pytest.fixture(scope="module")
@@ -180,4 +187,46 @@ def test_gemm_config4_shapes(ctx, rows, cols):
                   f"M={M} bf16")
         print(f"[gpu]   M={M}: worst bf16-input error {w:.2e} of the term sum", flush=True)
         check(lin.gemm(X), X, 4, blocks, rows, cols, TOL_BF16, None, f"M={M} fp32")
+    lin.close()
+
+
+def rel_to_max(Y, X, scheme, blocks, rows, cols, bias=None):
+    zp, cs = parts64(scheme, blocks, rows, cols)
+    truth = X.astype(np.float64) @ (zp + cs).T
+    if bias is not None:
+        truth = truth + bias.astype(np.float64)
+    return float(np.max(np.abs(Y - truth)) / np.max(np.abs(truth)))
+
+
+@pytest.mark.parametrize("scheme", [4, 3])
+@pytest.mark.parametrize("rows,cols", [(70, 256), (300, 1280), (1000, 2560)])
+@pytest.mark.parametrize("M", [1, 3, 8, 9, 16, 17, 32, 45, 70])
+def test_gemm_split_fp32(ctx, scheme, rows, cols, M):
+    """DTYPE_F32_SPLIT: the small kernel (M <= 8 per launch), the packed
+    kernel with hi and lo tiles (9..32), several launches (> 32)."""
+    print(f"[gpu] gemm split v{scheme} {rows}x{cols} M={M}", flush=True)
+    rng = np.random.default_rng(rows * 7 + cols + M + scheme)
+    bias = rng.standard_normal(rows).astype(np.float32)
+    lin, blocks = make(ctx, scheme, rows, cols, seed=rows + 3 * cols + M, bias=bias)
+    X = rng.standard_normal((M, cols)).astype(np.float32)
+    Y = lin.gemm(X, wpcg.DTYPE_F32_SPLIT)
+    check(Y, X, scheme, blocks, rows, cols, TOL_SPLIT, bias, "split X")
+    r = rel_to_max(Y, X, scheme, blocks, rows, cols, bias)
+    assert r <= SPLIT_REL, f"split X: {r:.2e} of max |y|"
+    if M > 1 and cols >= 1280:  # the bf16-rounded path really is coarser
+        assert rel_to_max(lin.gemm(X), X, scheme, blocks, rows, cols, bias) > 5 * r
+    assert np.array_equal(lin.gemm(X, wpcg.DTYPE_F32_SPLIT), Y), "not deterministic"
+    lin.close()
+
+
+@pytest.mark.parametrize("M", [4, 24])
+def test_gemm_split_every_ksplit(ctx, M):
+    rows, cols = 200, 128 * 70
+    lin, blocks = make(ctx, 4, rows, cols, seed=19)
+    X = np.random.default_rng(6).standard_normal((M, cols)).astype(np.float32)
+    for kg in (1, 3, 7, 0):
+        lin.set_gemm_kslices(kg)
+        Y = lin.gemm(X, wpcg.DTYPE_F32_SPLIT)
+        check(Y, X, 4, blocks, rows, cols, TOL_SPLIT, None, f"split kg={kg}")
+        assert rel_to_max(Y, X, 4, blocks, rows, cols) <= SPLIT_REL
     lin.close()

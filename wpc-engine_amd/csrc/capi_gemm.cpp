@@ -64,11 +64,12 @@ int run_gemm(wpcg_linear* L, const void* x, int x_dtype, uint32_t M, float* y, h
                                     "make it before capturing a graph");
         if (int rc = make_gemm(L, s)) return rc;
     }
-    const uint64_t es = x_dtype == WPCG_DTYPE_F32 ? 4 : 2;
-    for (uint32_t c = 0; c < M; c += GEMM_MAX_M) {
-        const int mc = (int)std::min<uint32_t>(GEMM_MAX_M, M - c);
-        WPCG_HIP(launch_gemm(m, L->gemm, static_cast<const uint8_t*>(x) + (uint64_t)c * m.cols * es,
-                             x_dtype == WPCG_DTYPE_BF16, mc, L->bias, y + (uint64_t)c * m.rows, s));
+    const uint64_t es = x_dtype == WPCG_DTYPE_BF16 ? 2 : 4;
+    const uint32_t step = x_dtype == WPCG_DTYPE_F32_SPLIT ? GEMM_MAX_M_SPLIT : GEMM_MAX_M;
+    for (uint32_t c = 0; c < M; c += step) {
+        const int mc = (int)std::min<uint32_t>(step, M - c);
+        WPCG_HIP(launch_gemm(m, L->gemm, static_cast<const uint8_t*>(x) + (uint64_t)c * m.cols * es, x_dtype, mc,
+                             L->bias, nullptr, y + (uint64_t)c * m.rows, s));
     }
     return WPCG_OK;
 }
@@ -76,7 +77,8 @@ int run_gemm(wpcg_linear* L, const void* x, int x_dtype, uint32_t M, float* y, h
 int check_gemm_args(wpcg_linear* L, const void* x, int x_dtype, uint32_t M, const float* y)
 {
     if (!L) return fail(WPCG_E_ARG, "null linear");
-    if (x_dtype != WPCG_DTYPE_F32 && x_dtype != WPCG_DTYPE_BF16) return fail(WPCG_E_ARG, "unknown x dtype");
+    if (x_dtype != WPCG_DTYPE_F32 && x_dtype != WPCG_DTYPE_BF16 && x_dtype != WPCG_DTYPE_F32_SPLIT)
+        return fail(WPCG_E_ARG, "unknown x dtype");
     if (M && L->m.rows && (!y || (!x && L->m.cols))) return fail(WPCG_E_ARG, "null x or y");
     if ((uint64_t)M * L->m.cols > (1ull << 40)) return fail(WPCG_E_SHAPE, "batch too large");
     return check_ctx(L->ctx);
@@ -99,7 +101,7 @@ int wpcg_linear_gemm_host(wpcg_linear* L, const void* x, int x_dtype, uint32_t M
 {
     if (int rc = check_gemm_args(L, x, x_dtype, M, y)) return rc;
     if (M == 0 || L->m.rows == 0) return WPCG_OK;
-    const uint64_t xb = (uint64_t)M * L->m.cols * (x_dtype == WPCG_DTYPE_F32 ? 4 : 2);
+    const uint64_t xb = (uint64_t)M * L->m.cols * (x_dtype == WPCG_DTYPE_BF16 ? 2 : 4);
     const uint64_t yb = (uint64_t)M * L->m.rows * sizeof(float);
     std::lock_guard<std::mutex> g(L->host_mu);
     hipStream_t s = L->ctx->stream;

@@ -65,17 +65,24 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int
 constexpr int CPOL_NT = 2;   // streamed once
 constexpr int CPOL_SC1 = 16; // coherent across the device's L2s (agent scope)
 
+// x rounded to bf16 (nearest even), as a float
+__device__ __forceinline__ float bf16_round(float v) { return bf16_lo(pk_bf16(v, 0.0f)); }
+
 // ---- X -> bf16 fragments in k(i, g, s) order, plus per-block column sums
 // of the rounded values. One workgroup per (block, column tile): wave i is
-// kstep i, lane g*16 + c column c.
-template <bool BF16_IN>
+// kstep i, lane g*16 + c column c. SPLIT (fp32 X): column tiles
+// [0, NT/2) hold hi = bf16(x) and tiles [NT/2, NT) lo = bf16(x - hi) of the
+// same columns, so hi + lo carries x to a relative 2^-18.
+template <bool BF16_IN, bool SPLIT>
 __global__ __launch_bounds__(256) void k_gemm_pack(const void* __restrict__ X, int M, int K, int NT,
                                                    u32x4* __restrict__ xf, float* __restrict__ xsum)
 {
     __shared__ float red[4][16];
     const int b = blockIdx.x / NT, n = blockIdx.x % NT;
     const int i = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
-    const int m = n * 16 + c;
+    const int nh = SPLIT ? NT / 2 : NT;
+    const bool lo_part = SPLIT && n >= nh;
+    const int m = (lo_part ? n - nh : n) * 16 + c;
     float v[8];
 #pragma unroll
     for (int s = 0; s < 8; s++) {
@@ -86,6 +93,7 @@ __global__ __launch_bounds__(256) void k_gemm_pack(const void* __restrict__ X, i
             v[s] = __uint_as_float((uint32_t)static_cast<const uint16_t*>(X)[(size_t)m * K + k] << 16);
         else
             v[s] = static_cast<const float*>(X)[(size_t)m * K + k];
+        if (lo_part) v[s] = v[s] - bf16_round(v[s]);  // exact in fp32
     }
     u32x4 o;
     o.x = pk_bf16(v[0], v[1]);
@@ -112,10 +120,19 @@ struct GemmArgs {
     const float* xsum;   // [nb][NT*16]
     float* y;            // [M][rows]
     const float* bias;   // [rows] or null
+    const float* res;    // [M][rows] added to Y (may be y itself) or null
     float* part;         // [kg][NT*16][rows_pad] (kg > 1)
     uint32_t* counters;  // one per row group (kg > 1), self-resetting
     int rows, rows_pad, nb, M, kg;
 };
+
+// The value written for output (m, row): the sum, the bias, the residual.
+__device__ __forceinline__ float out_val(float v, const float* bias, const float* res, int rows, int m, int row)
+{
+    if (bias) v += bias[row];
+    if (res) v += res[(size_t)m * rows + row];
+    return v;
+}
 
 constexpr int GM_WG = GEMM_WG_THREADS;  // 4 waves (row tiles per workgroup: 4 * GM_RT)
 constexpr int GM_WG8 = 2 * GM_WG;       // the M > 16 kernel: two waves per tile pair
@@ -150,9 +167,15 @@ __device__ __forceinline__ float zp_off(uint32_t p) { return __builtin_fmaf(-128
 // ahead; the codes come straight from HBM into registers, GM_LA blocks
 // ahead. Every buffer load has an exact range, so loads past the slice
 // return zeros (a zero block adds exactly 0).
-template <int SCHEME, int NT>
+//
+// SPLIT: column tiles [0, NT/2) are the hi parts and [NT/2, NT) the lo parts
+// of the same NT/2 column tiles (k_gemm_pack<*, true>), so wave half 0 runs
+// hi and half 1 lo over the same codes; after the loop half 1 hands its sums
+// to half 0 through LDS, which adds hi + lo and alone writes.
+template <int SCHEME, int NT, bool SPLIT>
 __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
 {
+    static_assert(!SPLIT || NT % 2 == 0, "split needs hi and lo tiles");
     constexpr int NTH = (NT + 1) / 2;          // column tiles of the first half
     constexpr int XV = (NT * 4096 + GM_WG8 * 16 - 1) / (GM_WG8 * 16);  // 16-byte X loads per thread per block
     __shared__ __align__(16) u32x4 xb[2][NT * 4 * 64];
@@ -299,6 +322,26 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
         }
     }
 
+    if constexpr (SPLIT) {
+        // every wave is past its last LDS read of X (the loop ends on a barrier)
+        f32x4* ex = reinterpret_cast<f32x4*>(&xb[0][0]);
+        static_assert(sizeof(xb) >= 4 * GM_RT * NTH * 64 * sizeof(f32x4), "hand-over space");
+        if (ch == 1)
+#pragma unroll
+            for (int rt = 0; rt < GM_RT; rt++)
+#pragma unroll
+                for (int nn = 0; nn < NTH; nn++) ex[(((wave & 3) * GM_RT + rt) * NTH + nn) * 64 + lane] = acc[rt][nn];
+        __syncthreads();
+        if (ch == 0)
+#pragma unroll
+            for (int rt = 0; rt < GM_RT; rt++)
+#pragma unroll
+                for (int nn = 0; nn < NTH; nn++)
+                    acc[rt][nn] = acc[rt][nn] + ex[(((wave & 3) * GM_RT + rt) * NTH + nn) * 64 + lane];
+    }
+    // the column tiles this wave writes: [c0, c1) (SPLIT: half 0, the hi tiles)
+    const int c0 = SPLIT ? 0 : n0, c1 = SPLIT ? (ch ? 0 : NTH) : n1;
+
     // lane (g, j) holds rows 4g..4g+3 of each tile for column n*16 + j
     const int Mp = NT * 16;
     if (kg == 1) {
@@ -306,12 +349,12 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
         for (int rt = 0; rt < GM_RT; rt++)
 #pragma unroll
             for (int nn = 0; nn < NTH; nn++) {
-                const int n = n0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
-                if (n >= n1 || m >= P.M) continue;
+                const int n = c0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
+                if (n >= c1 || m >= P.M) continue;
 #pragma unroll
                 for (int q = 0; q < 4; q++)
                     if (row + q < P.rows)
-                        P.y[(size_t)m * P.rows + row + q] = P.bias ? acc[rt][nn][q] + P.bias[row + q] : acc[rt][nn][q];
+                        P.y[(size_t)m * P.rows + row + q] = out_val(acc[rt][nn][q], P.bias, P.res, P.rows, m, row + q);
             }
         return;
     }
@@ -326,8 +369,8 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
     for (int rt = 0; rt < GM_RT; rt++)
 #pragma unroll
         for (int nn = 0; nn < NTH; nn++) {
-            const int n = n0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
-            if (n < n1 && T0 + rt < ntiles) {
+            const int n = c0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
+            if (n < c1 && T0 + rt < ntiles) {
                 u32x4 v;
                 __builtin_memcpy(&v, &acc[rt][nn], 16);
                 __builtin_amdgcn_raw_buffer_store_b128(v, prt, ((kgi * Mp + m) * P.rows_pad + row) * 4, 0, CPOL_SC1);
@@ -345,8 +388,8 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
     for (int rt = 0; rt < GM_RT; rt++)
 #pragma unroll
         for (int nn = 0; nn < NTH; nn++) {
-            const int n = n0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
-            if (n >= n1 || T0 + rt >= ntiles || m >= P.M) continue;
+            const int n = c0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
+            if (n >= c1 || T0 + rt >= ntiles || m >= P.M) continue;
             f32x4 s = {0.f, 0.f, 0.f, 0.f};
             for (int k = 0; k < kg; k++) {
                 const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(prt, ((k * Mp + m) * P.rows_pad + row) * 4, 0, CPOL_SC1);
@@ -356,7 +399,7 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
             }
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                if (row + q < P.rows) P.y[(size_t)m * P.rows + row + q] = P.bias ? s[q] + P.bias[row + q] : s[q];
+                if (row + q < P.rows) P.y[(size_t)m * P.rows + row + q] = out_val(s[q], P.bias, P.res, P.rows, m, row + q);
         }
     if (threadIdx.x == 0) __hip_atomic_store(P.counters + rg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -376,12 +419,22 @@ struct GemmSmallArgs {
     const uint8_t* codes;
     const uint8_t* hp;
     const uint32_t* params;
-    const void* x;       // [M][K] row-major
+    const void* x;       // [M][K] row-major (GROUPED: [xrows][K])
     float* y;
     const float* bias;
+    const float* res;    // [M][rows] added to Y (may be y itself) or null
     float* part;         // [kg][16][rows_pad] (kg > 1)
     uint32_t* counters;
     int rows, rows_pad, nb, M, kg;
+    // GROUPED: workgroup item * rgs + rg takes items[item] = {expert, first
+    // pair p0, count}; its column c is X row rowidx[p0 + c] (rowidx null:
+    // row p0 + c) and Y row p0 + c; the expert's planes sit e * e{codes,
+    // hp, params} further on. kg = 1.
+    const int* rowidx;
+    const int* items;
+    const int* nitems;
+    size_t ecodes, ehp, eparams;  // bytes, bytes, 32-bit words
+    int xrows, rgs;
 };
 
 // Eight bf16 of one fragment lane from two consecutive-k pieces: the low
@@ -391,16 +444,48 @@ __device__ __forceinline__ uint32_t pick_halves(uint32_t a, uint32_t b, int odd)
     return odd ? (a >> 16) | (b & 0xFFFF0000u) : (a & 0xFFFFu) | (b << 16);
 }
 
-template <int SCHEME, bool BF16_IN>
+// The fp32 value held in a dword minus its bf16 rounding (exact), i.e. the
+// lo part of a SPLIT column.
+__device__ __forceinline__ float lo_of(uint32_t bits)
+{
+    const float v = __uint_as_float(bits);
+    return v - bf16_round(v);
+}
+
+// SPLIT (fp32 X, M <= 8): fragment columns [0, M) carry hi = bf16(x) and
+// [M, 2M) lo = bf16(x - hi) of the same rows; after the dots lane j adds
+// lane j + M (hi + lo) and writes column j.
+template <int SCHEME, bool BF16_IN, bool SPLIT, bool GROUPED>
 __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
 {
+    static_assert(!(SPLIT && BF16_IN), "bf16 X has no lo part");
     __shared__ __align__(16) u32x4 xb[GEMM_SMALL_MAXBK][4][64];
     __shared__ float psum[GEMM_SMALL_MAXBK][2][16];
     __shared__ __align__(16) f32x4 red[GS_TILES][64];
     __shared__ int s_last;
 
-    const int kg = P.kg, nb = P.nb, K = nb * 128, M = P.M;
-    const int kgi = blockIdx.x % kg, rg = blockIdx.x / kg;
+    const int kg = GROUPED ? 1 : P.kg, nb = P.nb, K = nb * 128;
+    int M = P.M, p0 = 0;
+    const uint8_t* codes = P.codes;
+    const uint8_t* hpl = P.hp;
+    const uint32_t* params = P.params;
+    int kgi, rg;
+    if constexpr (GROUPED) {
+        const int item = blockIdx.x / P.rgs;
+        rg = blockIdx.x % P.rgs;
+        kgi = 0;
+        if (item >= *P.nitems) return;  // uniform over the workgroup
+        const int e = P.items[3 * item];
+        p0 = P.items[3 * item + 1];
+        M = P.items[3 * item + 2];
+        codes += (size_t)e * P.ecodes;
+        hpl += (size_t)e * P.ehp;
+        params += (size_t)e * P.eparams;
+    } else {
+        kgi = blockIdx.x % kg;
+        rg = blockIdx.x / kg;
+    }
+    const int Mx = SPLIT ? 2 * M : M;  // fragment columns in use
     const int nbk = (nb + kg - 1) / kg;
     const int b0 = min(kgi * nbk, nb);
     const int nbl = max(0, min(nb, b0 + nbk) - b0);  // <= GEMM_SMALL_MAXBK (the planner's rule)
@@ -419,24 +504,27 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
     // consecutive k; a thread takes tasks t and t + 512 (ntask <= 960).
     constexpr int es = BF16_IN ? 2 : 4;
     constexpr int PIECES = BF16_IN ? 8 : 16;  // 16-byte loads per task
+    const int xrows = GROUPED ? P.xrows : M;
     const auto xrs = buf_rsrc(static_cast<const uint8_t*>(P.x) + (size_t)b0 * 128 * es,
-                              (int)(((size_t)(M - 1) * K + (size_t)nbl * 128) * es));
-    const int ntask = nbl * 2 * M;
+                              (int)(((size_t)(xrows - 1) * K + (size_t)nbl * 128) * es));
+    const int ntask = nbl * 2 * Mx;
     u32x4 xv[2][PIECES];
 #pragma unroll
     for (int r = 0; r < 2; r++) {
         const int t = threadIdx.x + r * GS_WG;
-        const int blk = t / (2 * M), c = (t >> 1) % M, h = t & 1;
-        const int base = t < ntask ? (c * K + blk * 128 + 64 * h) * es : 0x7FFFFFF0;  // past the range: zeros
+        const int blk = t / (2 * Mx), c = (t >> 1) % Mx, h = t & 1;
+        int xr = SPLIT && c >= M ? c - M : c;  // the X row of fragment column c
+        if constexpr (GROUPED) xr = t < ntask ? (P.rowidx ? P.rowidx[p0 + xr] : p0 + xr) : 0;
+        const int base = t < ntask ? (xr * K + blk * 128 + 64 * h) * es : 0x7FFFFFF0;  // past the range: zeros
 #pragma unroll
         for (int p = 0; p < PIECES; p++) xv[r][p] = __builtin_amdgcn_raw_buffer_load_b128(xrs, base + p * 16, 0, 0);
     }
 
     // ---- then the first GS_LA blocks of this wave's codes
     const size_t rec = (size_t)min(T, ntiles - 1) * nb + b0 + kb0;
-    const auto crs = buf_rsrc(P.codes + rec * CODE_REC, tile_ok ? kn * (int)CODE_REC : 0);
-    const auto hrs = buf_rsrc((SCHEME == 3 ? P.hp : P.codes) + rec * HP_REC, tile_ok && SCHEME == 3 ? kn * (int)HP_REC : 0);
-    const auto prs = buf_rsrc(P.params + rec * TILE_ROWS, tile_ok ? kn * TILE_ROWS * 4 : 0);
+    const auto crs = buf_rsrc(codes + rec * CODE_REC, tile_ok ? kn * (int)CODE_REC : 0);
+    const auto hrs = buf_rsrc((SCHEME == 3 ? hpl : codes) + rec * HP_REC, tile_ok && SCHEME == 3 ? kn * (int)HP_REC : 0);
+    const auto prs = buf_rsrc(params + rec * TILE_ROWS, tile_ok ? kn * TILE_ROWS * 4 : 0);
     u32x4 cr[GS_LA], pr[GS_LA];
     u32x2 hr[GS_LA];
     auto load_codes = [&](int u, int b) {
@@ -449,17 +537,23 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- pack: fragment (i = 2h + ii, lane group gg) slot s <- piece s,
-    // element gg + 4 ii. Columns c >= M are zeros.
+    // element gg + 4 ii. Columns c >= Mx are zeros.
 #pragma unroll
     for (int r = 0; r < 2; r++) {
         const int t = threadIdx.x + r * GS_WG;
         if (t < ntask) {
-            const int blk = t / (2 * M), c = (t >> 1) % M, h = t & 1;
+            const int blk = t / (2 * Mx), c = (t >> 1) % Mx, h = t & 1;
             uint32_t pc[8][4];
 #pragma unroll
             for (int p = 0; p < 8; p++) {
                 if constexpr (BF16_IN) {
                     pc[p][0] = xv[r][p].x; pc[p][1] = xv[r][p].y; pc[p][2] = xv[r][p].z; pc[p][3] = xv[r][p].w;
+                } else if (SPLIT && c >= M) {
+                    const u32x4 a = xv[r][2 * p], b = xv[r][2 * p + 1];
+                    pc[p][0] = pk_bf16(lo_of(a.x), lo_of(a.y));
+                    pc[p][1] = pk_bf16(lo_of(a.z), lo_of(a.w));
+                    pc[p][2] = pk_bf16(lo_of(b.x), lo_of(b.y));
+                    pc[p][3] = pk_bf16(lo_of(b.z), lo_of(b.w));
                 } else {
                     const u32x4 a = xv[r][2 * p], b = xv[r][2 * p + 1];
                     pc[p][0] = pk_bf16(__uint_as_float(a.x), __uint_as_float(a.y));
@@ -488,9 +582,9 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
                 }
         }
     }
-    // zero columns M..15 of every fragment and their sums
-    for (int t = threadIdx.x; t < nbl * 2 * (16 - M); t += GS_WG) {
-        const int blk = t / (2 * (16 - M)), c = M + (t >> 1) % (16 - M), h = t & 1;
+    // zero columns Mx..15 of every fragment and their sums
+    for (int t = threadIdx.x; t < nbl * 2 * (16 - Mx); t += GS_WG) {
+        const int blk = t / (2 * (16 - Mx)), c = Mx + (t >> 1) % (16 - Mx), h = t & 1;
         psum[blk][h][c] = 0.0f;
 #pragma unroll
         for (int ii = 0; ii < 2; ii++)
@@ -567,15 +661,20 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
     if (part_k) red[wave - GS_TILES][lane] = acc;
     __syncthreads();
     if (!part_k) acc = acc + red[wave][lane];
+    if constexpr (SPLIT) {  // lane j += lane j + M (lanes j >= M are not written)
+#pragma unroll
+        for (int q = 0; q < 4; q++) acc[q] += __shfl(acc[q], lane + M);
+    }
     const bool writer = !part_k && tile_ok;
 
-    // lane (g, j) holds rows 4g..4g+3 of the tile for column j
+    // lane (g, j) holds rows 4g..4g+3 of the tile for column j (Y row p0 + j)
     const int row = T * TILE_ROWS + 4 * g;
     if (kg == 1) {
         if (writer && j < M)
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                if (row + q < P.rows) P.y[(size_t)j * P.rows + row + q] = P.bias ? acc[q] + P.bias[row + q] : acc[q];
+                if (row + q < P.rows)
+                    P.y[(size_t)(p0 + j) * P.rows + row + q] = out_val(acc[q], P.bias, P.res, P.rows, p0 + j, row + q);
         return;
     }
     // Split K: publish the slice's partials with coherent stores, then the
@@ -608,20 +707,33 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
         }
 #pragma unroll
         for (int q = 0; q < 4; q++)
-            if (row + q < P.rows) P.y[(size_t)j * P.rows + row + q] = P.bias ? sum[q] + P.bias[row + q] : sum[q];
+            if (row + q < P.rows) P.y[(size_t)j * P.rows + row + q] = out_val(sum[q], P.bias, P.res, P.rows, j, row + q);
     }
     if (threadIdx.x == 0) __hip_atomic_store(P.counters + rg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int SCHEME>
+template <int SCHEME, bool SPLIT>
 hipError_t launch_nt(int nt, dim3 grid, hipStream_t s, const GemmArgs& a)
 {
-    switch (nt) {
-    case 2: hipLaunchKernelGGL((k_gemm<SCHEME, 2>), grid, dim3(GM_WG8), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((k_gemm<SCHEME, 3>), grid, dim3(GM_WG8), 0, s, a); break;
-    default: hipLaunchKernelGGL((k_gemm<SCHEME, 4>), grid, dim3(GM_WG8), 0, s, a); break;
+    if constexpr (SPLIT) {
+        if (nt == 2) hipLaunchKernelGGL((k_gemm<SCHEME, 2, true>), grid, dim3(GM_WG8), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm<SCHEME, 4, true>), grid, dim3(GM_WG8), 0, s, a);
+    } else {
+        switch (nt) {
+        case 2: hipLaunchKernelGGL((k_gemm<SCHEME, 2, false>), grid, dim3(GM_WG8), 0, s, a); break;
+        case 3: hipLaunchKernelGGL((k_gemm<SCHEME, 3, false>), grid, dim3(GM_WG8), 0, s, a); break;
+        default: hipLaunchKernelGGL((k_gemm<SCHEME, 4, false>), grid, dim3(GM_WG8), 0, s, a); break;
+        }
     }
     return hipGetLastError();
+}
+
+template <int SCHEME>
+void launch_small(int x_mode, dim3 grid, hipStream_t s, const GemmSmallArgs& a)
+{
+    if (x_mode == GX_BF16) hipLaunchKernelGGL((k_gemm_small<SCHEME, true, false, false>), grid, dim3(GS_WG), 0, s, a);
+    else if (x_mode == GX_SPLIT) hipLaunchKernelGGL((k_gemm_small<SCHEME, false, true, false>), grid, dim3(GS_WG), 0, s, a);
+    else hipLaunchKernelGGL((k_gemm_small<SCHEME, false, false, false>), grid, dim3(GS_WG), 0, s, a);
 }
 
 }  // namespace
@@ -668,14 +780,16 @@ int gemm_small_kslices(uint64_t rows, uint64_t nb, int req)
     return k;
 }
 
-hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, int x_bf16, int M,
-                       const float* bias, float* y, hipStream_t s)
+hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, int x_mode, int M,
+                       const float* bias, const float* res, float* y, hipStream_t s)
 {
-    if (M < 1 || M > GEMM_MAX_M || m.nb == 0) return hipErrorInvalidValue;
-    const int NT = (M + 15) / 16;
+    const bool split = x_mode == GX_SPLIT;
+    if (M < 1 || M > (split ? GEMM_MAX_M_SPLIT : GEMM_MAX_M) || m.nb == 0) return hipErrorInvalidValue;
+    const int cols = split ? 2 * M : M;  // fragment columns
+    const int NT = (cols + 15) / 16;
     const int nb = (int)m.nb;
     (void)hipGetLastError();  // report only these launches
-    if (NT == 1) {
+    if (cols <= 16) {
         if ((nb + w.kg_small - 1) / w.kg_small > GEMM_SMALL_MAXBK)
             return hipErrorInvalidValue;  // the planner never makes such a split
         GemmSmallArgs a{};
@@ -685,6 +799,7 @@ hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, 
         a.x = x;
         a.y = y;
         a.bias = bias;
+        a.res = res;
         a.part = w.part;
         a.counters = w.counters;
         a.rows = (int)m.rows;
@@ -693,21 +808,21 @@ hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, 
         a.M = M;
         a.kg = w.kg_small;
         dim3 grid((unsigned)(gemm_small_row_groups(m.rows) * w.kg_small));
-        if (m.scheme == 4) {
-            if (x_bf16) hipLaunchKernelGGL((k_gemm_small<4, true>), grid, dim3(GS_WG), 0, s, a);
-            else hipLaunchKernelGGL((k_gemm_small<4, false>), grid, dim3(GS_WG), 0, s, a);
-        } else {
-            if (x_bf16) hipLaunchKernelGGL((k_gemm_small<3, true>), grid, dim3(GS_WG), 0, s, a);
-            else hipLaunchKernelGGL((k_gemm_small<3, false>), grid, dim3(GS_WG), 0, s, a);
-        }
+        if (m.scheme == 4) launch_small<4>(x_mode, grid, s, a);
+        else launch_small<3>(x_mode, grid, s, a);
         return hipGetLastError();
     }
-    dim3 pgrid((unsigned)(nb * NT));
-    if (x_bf16)
-        hipLaunchKernelGGL(k_gemm_pack<true>, pgrid, dim3(256), 0, s, x, M, (int)m.cols, NT,
+    // SPLIT: hi tiles then as many lo tiles (NT even)
+    const int ntiles = split ? 2 * ((M + 15) / 16) : NT;
+    dim3 pgrid((unsigned)(nb * ntiles));
+    if (x_mode == GX_BF16)
+        hipLaunchKernelGGL((k_gemm_pack<true, false>), pgrid, dim3(256), 0, s, x, M, (int)m.cols, ntiles,
+                           reinterpret_cast<u32x4*>(w.xf), w.xsum);
+    else if (split)
+        hipLaunchKernelGGL((k_gemm_pack<false, true>), pgrid, dim3(256), 0, s, x, M, (int)m.cols, ntiles,
                            reinterpret_cast<u32x4*>(w.xf), w.xsum);
     else
-        hipLaunchKernelGGL(k_gemm_pack<false>, pgrid, dim3(256), 0, s, x, M, (int)m.cols, NT,
+        hipLaunchKernelGGL((k_gemm_pack<false, false>), pgrid, dim3(256), 0, s, x, M, (int)m.cols, ntiles,
                            reinterpret_cast<u32x4*>(w.xf), w.xsum);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -719,6 +834,7 @@ hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, 
     a.xsum = w.xsum;
     a.y = y;
     a.bias = bias;
+    a.res = res;
     a.part = w.part;
     a.counters = w.counters;
     a.rows = (int)m.rows;
@@ -727,7 +843,38 @@ hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, 
     a.M = M;
     a.kg = w.kg;
     dim3 grid((unsigned)(gemm_row_groups(m.rows) * w.kg));
-    return m.scheme == 4 ? launch_nt<4>(NT, grid, s, a) : launch_nt<3>(NT, grid, s, a);
+    if (split) return m.scheme == 4 ? launch_nt<4, true>(ntiles, grid, s, a) : launch_nt<3, true>(ntiles, grid, s, a);
+    return m.scheme == 4 ? launch_nt<4, false>(ntiles, grid, s, a) : launch_nt<3, false>(ntiles, grid, s, a);
+}
+
+hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, int xrows, const int* rowidx, const int* items,
+                               const int* nitems, int max_items, float* y, hipStream_t s)
+{
+    if (m.nb == 0 || m.nb > (uint64_t)GEMM_SMALL_MAXBK || xrows < 1 || max_items < 1) return hipErrorInvalidValue;
+    (void)hipGetLastError();
+    GemmSmallArgs a{};
+    a.codes = m.codes;
+    a.hp = m.hp;
+    a.params = m.params;
+    a.x = x;
+    a.y = y;
+    a.rows = (int)m.rows;
+    a.rows_pad = (int)m.rows_pad;
+    a.nb = (int)m.nb;
+    a.kg = 1;
+    a.rowidx = rowidx;
+    a.items = items;
+    a.nitems = nitems;
+    const size_t tiles = m.rows_pad / TILE_ROWS;
+    a.ecodes = tiles * m.nb * CODE_REC;
+    a.ehp = m.scheme == 3 ? tiles * m.nb * HP_REC : 0;
+    a.eparams = tiles * m.nb * TILE_ROWS;
+    a.xrows = xrows;
+    a.rgs = gemm_small_row_groups(m.rows);
+    dim3 grid((unsigned)(a.rgs * max_items));
+    if (m.scheme == 4) hipLaunchKernelGGL((k_gemm_small<4, false, true, true>), grid, dim3(GS_WG), 0, s, a);
+    else hipLaunchKernelGGL((k_gemm_small<3, false, true, true>), grid, dim3(GS_WG), 0, s, a);
+    return hipGetLastError();
 }
 
 }  // namespace wpcg

@@ -186,8 +186,23 @@ int gemm_small_row_groups(uint64_t rows);  // up to 16 columns
 // slices (and, for the small kernel, slices of at most GEMM_SMALL_MAXBK).
 int gemm_kslices(uint64_t rows, uint64_t nb, int req);
 int gemm_small_kslices(uint64_t rows, uint64_t nb, int req);
-hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, int x_bf16, int M,
-                       const float* bias, float* y, hipStream_t s);
+// x_mode: GX_F32 (x rounded to bf16), GX_BF16, GX_SPLIT (fp32 x as hi + lo
+// bf16 terms, relative 2^-18; at most GEMM_MAX_M_SPLIT columns). res: [M][rows]
+// added to Y (may alias y) or null.
+constexpr int GX_F32 = 0, GX_BF16 = 1, GX_SPLIT = 2;
+constexpr int GEMM_MAX_M_SPLIT = 32;
+hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, int x_mode, int M,
+                       const float* bias, const float* res, float* y, hipStream_t s);
+// Expert-grouped GEMM in the SPLIT mode, one launch for every expert of a
+// stack: m is one expert's shape, its planes the first of the stack
+// (expert e at e * its plane sizes). Work item i = items[3i..3i+2] =
+// {expert, first pair p0, count <= GEMM_GROUP_COLS}; its column c reads X
+// row rowidx[p0 + c] (null: row p0 + c, X has xrows rows) and writes Y row
+// p0 + c. *nitems (device) items are live; max_items bounds the grid.
+// Needs m.nb <= GEMM_SMALL_MAXBK (one K-slice).
+constexpr int GEMM_GROUP_COLS = 8;
+hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, int xrows, const int* rowidx, const int* items,
+                               const int* nitems, int max_items, float* y, hipStream_t s);
 
 // ---- host helpers shared by the C ABI files (capi*.cpp) -----------------
 hipStream_t pick(wpcg_ctx* ctx, wpcg_stream s);  // NULL = the context stream

@@ -28,7 +28,7 @@ OK, E_IO, E_FORMAT, E_SHAPE, E_NOTFOUND, E_DEVICE, E_ARG, E_NOMEM, E_UNSUPPORTED
 SCHEME_V3, SCHEME_V4 = 3, 4
 MODE_EXACT, MODE_FAST = 0, 1
 ROUND_FMA, ROUND_TWO = 0, 1
-DTYPE_F32, DTYPE_BF16 = 0, 1
+DTYPE_F32, DTYPE_BF16, DTYPE_F32_SPLIT = 0, 1, 2
 
 _ERR_NAMES = {0: "OK", 1: "E_IO", 2: "E_FORMAT", 3: "E_SHAPE", 4: "E_NOTFOUND", 5: "E_DEVICE",
               6: "E_ARG", 7: "E_NOMEM", 8: "E_UNSUPPORTED"}
@@ -447,8 +447,9 @@ class WpcLinear:
 
     def gemm(self, X, dtype: int = DTYPE_F32) -> np.ndarray:
         """Y = X W^T (+ bias) for a batch X of shape (M, in_features): fp32
-        values, or bf16 bit patterns (uint16) with dtype DTYPE_BF16."""
-        X = np.ascontiguousarray(X, np.float32 if dtype == DTYPE_F32 else np.uint16)
+        values (DTYPE_F32 rounds them to bf16, DTYPE_F32_SPLIT carries them
+        as two bf16 terms), or bf16 bit patterns (uint16) with DTYPE_BF16."""
+        X = np.ascontiguousarray(X, np.uint16 if dtype == DTYPE_BF16 else np.float32)
         assert X.ndim == 2 and X.shape[1] == self._in
         Y = np.empty((X.shape[0], self._out), np.float32)
         check(lib.wpcg_linear_gemm_host(self.h, _np_ptr(X), dtype, X.shape[0], _np_ptr(Y)))
