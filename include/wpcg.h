@@ -374,9 +374,27 @@ int wpcg_model_position(wpcg_model* m, uint32_t* pos);
  * floats) and/or their argmax, either may be NULL. E_ARG when the cache is
  * full. */
 int wpcg_model_forward_token(wpcg_model* m, uint32_t token, float* logits, uint32_t* argmax);
+/* The prompt loop of wpc-runtime/src/main.rs:259-262 (forward_token per
+ * prompt token, keeping the last logits) for n tokens at the next n
+ * positions: the same result as n forward_token calls, logits and argmax of
+ * the last. EXACT mode runs exactly those steps (bit-identical). FAST mode
+ * runs the tokens as batches of up to 256 rows (the reference's missing
+ * batched prefill, README.md:174-180): every layer reads each weight once
+ * per batch; the dense projections run on the matrix cores with X carried
+ * as two bf16 terms (WPCG_DTYPE_F32_SPLIT), attention is causal over the
+ * cache, and the experts run grouped: the (token, slot) pairs are sorted by
+ * expert and one launch per projection covers every expert's tokens. Its
+ * results match the step-by-step FAST ones within FAST's tolerance. E_ARG
+ * when the cache cannot hold n more positions. */
+int wpcg_model_prefill(wpcg_model* m, const uint32_t* tokens, uint32_t n, float* logits, uint32_t* argmax);
+/* FAST mode: prompts of wpcg_model_prefill and wpcg_model_generate go
+ * through the batched prefill (enabled, the default) or step by step. No
+ * reference counterpart. */
+int wpcg_model_set_prefill(wpcg_model* m, int enabled);
 /* Greedy generation from position 0: the prompt, then n_new tokens, each
  * the argmax of the previous step's logits, written to out (n_new ids).
- * Steps run back to back on the device with no host round trip.
+ * Steps run back to back on the device with no host round trip; in FAST
+ * mode the prompt goes through the batched prefill (wpcg_model_prefill).
  * decode_ms (may be NULL) receives the time of the n_new-1 steps after the
  * prompt. */
 int wpcg_model_generate(wpcg_model* m, const uint32_t* prompt, uint32_t n_prompt, uint32_t n_new,

@@ -1,0 +1,153 @@
+"""GPU tests of the batched prefill (wpcg_model_prefill) against the same
+model run token by token (forward_token; the reference's prompt loop,
+wpc-runtime/src/main.rs:259-262), on seeded synthetic v4 models.
+
+The reference has no batched forward pass, so its semantics are those n
+steps. EXACT mode runs exactly them: bit-identical. FAST mode batches the
+tokens (matrix-core GEMMs with X carried as two bf16 terms, causal attention
+over the cache, experts grouped by the pairs routed to them), so it is held
+to a tolerance against the step-by-step FAST run:
+  * logits of the last token within 1e-4 of their range;
+  * every key and value written to the cache within 1e-4 of the cache's
+    largest magnitude;
+  * greedy decoding continued from both states gives the same ids (printed;
+    asserted for the first 16 steps).
+Cases cover one pass, several passes (more tokens than a pass holds), a
+prefill after decode steps (a non-zero start position), dense and MoE.
+"""
+import numpy as np
+import pytest
+
+import wpcg
+from wpcg import synth
+
+pytestmark = pytest.mark.gpu
+
+DENSE = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, inter=512, vocab=1000,
+             n_experts=0, top_k=0, moe_inter=0, norm_topk=1, tied=1, max_pos=352, eps=1e-6,
+             rope_theta=1e6)
+MOE = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, inter=0, vocab=1000,
+           n_experts=16, top_k=4, moe_inter=128, norm_topk=1, tied=0, max_pos=352, eps=1e-6,
+           rope_theta=1e6)
+# Qwen3-30B-A3B shapes (config 3) with two of the 48 layers
+QWEN3_MOE_2L = dict(n_layers=2, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=128, inter=0,
+                    vocab=151936, n_experts=128, top_k=8, moe_inter=768, norm_topk=1, tied=0,
+                    max_pos=320, eps=1e-6, rope_theta=1e6)
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = wpcg.Context(0)
+    yield c
+    c.close()
+
+
+def build(ctx, cfg, seed, mode):
+    m = wpcg.Model(ctx, 4, wpcg.ModelConfig(**cfg))
+    for name, arr in synth.model_tensors(cfg, 4, seed, wpcg.encode):
+        m.set_tensor(name, arr)
+    return m.set_mode(mode)
+
+
+def cache(m, cfg, n):
+    """Keys and values of positions < n, [layer][kv_head][n][head_dim]."""
+    L, kv, mp, hd = cfg["n_layers"], cfg["n_kv_heads"], cfg["max_pos"], cfg["head_dim"]
+    size = L * kv * mp * hd
+    k = m.debug_read(9, size).reshape(L, kv, mp, hd)[:, :, :n]
+    v = m.debug_read(10, size).reshape(L, kv, mp, hd)[:, :, :n]
+    return k, v
+
+
+def greedy(m, first, steps):
+    ids, tok = [], first
+    for _ in range(steps):
+        _, tok = m.forward_token(tok, want_logits=False)
+        ids.append(tok)
+    return ids
+
+
+@pytest.mark.parametrize("name,cfg,n_pre,n,seed", [
+    ("dense-one-pass", DENSE, 0, 100, 11),
+    ("dense-two-passes", DENSE, 0, 300, 12),
+    ("dense-after-steps", DENSE, 7, 90, 13),
+    ("moe-one-pass", MOE, 0, 200, 21),
+    ("moe-two-passes", MOE, 3, 290, 22),
+    ("qwen3-moe-2L", QWEN3_MOE_2L, 0, 256, 31),
+])
+def test_fast_prefill_matches_steps(ctx, name, cfg, n_pre, n, seed):
+    print(f"[gpu] prefill {name}: {n_pre} steps then {n} tokens", flush=True)
+    m = build(ctx, cfg, seed, wpcg.MODE_FAST)
+    rng = np.random.default_rng(seed)
+    toks = rng.integers(0, cfg["vocab"], n_pre + n).astype(np.uint32)
+    # token by token
+    for t in toks:
+        ref, ref_id = m.forward_token(int(t))
+    kr, vr = cache(m, cfg, n_pre + n)
+    ref_ids = greedy(m, ref_id, 24)
+    # the same tokens, the last n batched
+    m.reset()
+    for t in toks[:n_pre]:
+        m.forward_token(int(t), want_logits=False)
+    got, got_id = m.prefill(toks[n_pre:])
+    assert m.position() == n_pre + n
+    kg, vg = cache(m, cfg, n_pre + n)
+    ids = greedy(m, got_id, 24)
+    span = float(ref.max() - ref.min())
+    err = float(np.max(np.abs(got - ref))) / span
+    kerr = max(float(np.max(np.abs(kg - kr))) / float(np.max(np.abs(kr))),
+               float(np.max(np.abs(vg - vr))) / float(np.max(np.abs(vr))))
+    same = int(np.argmax(np.concatenate([np.array(ids) != np.array(ref_ids), [True]])))
+    print(f"[gpu] prefill {name}: logits {err:.2e} of range, cache {kerr:.2e}, "
+          f"argmax {got_id} vs {ref_id}, greedy ids equal for {same} of 24", flush=True)
+    assert err <= TOL, f"{name}: last logits {err:.2e} of the range"
+    assert kerr <= TOL, f"{name}: cache {kerr:.2e}"
+    assert got_id == ref_id
+    assert ids[:16] == ref_ids[:16]
+    m.close()
+
+
+def test_exact_prefill_is_the_steps(ctx):
+    cfg = MOE
+    m = build(ctx, cfg, 41, wpcg.MODE_EXACT)
+    toks = np.random.default_rng(4).integers(0, cfg["vocab"], 20).astype(np.uint32)
+    for t in toks:
+        ref, ref_id = m.forward_token(int(t))
+    kr, vr = cache(m, cfg, 20)
+    m.reset()
+    got, got_id = m.prefill(toks)
+    kg, vg = cache(m, cfg, 20)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)) and got_id == ref_id
+    assert np.array_equal(kg, kr) and np.array_equal(vg, vr)
+    m.close()
+
+
+@pytest.mark.parametrize("name,cfg,seed", [("dense", DENSE, 51), ("moe", MOE, 52)])
+def test_generate_with_prefill(ctx, name, cfg, seed):
+    """FAST generate: batched prompt vs step-by-step prompt, same ids."""
+    m = build(ctx, cfg, seed, wpcg.MODE_FAST)
+    prompt = np.random.default_rng(seed).integers(0, cfg["vocab"], 64).astype(np.uint32)
+    a, _ = m.generate(prompt, 32)
+    m.set_prefill(False)
+    b, _ = m.generate(prompt, 32)
+    same = int(np.argmax(np.concatenate([a != b, [True]])))
+    print(f"[gpu] generate {name}: ids equal for {same} of 32", flush=True)
+    assert same >= 16
+    m.close()
+
+
+def test_prefill_errors(ctx):
+    cfg = dict(DENSE, max_pos=40)
+    m = build(ctx, cfg, 61, wpcg.MODE_FAST)
+    with pytest.raises(wpcg.WpcgError) as e:
+        m.prefill(np.zeros(41, np.uint32))
+    assert e.value.code == wpcg.E_ARG
+    with pytest.raises(wpcg.WpcgError) as e:
+        m.prefill(np.array([5, cfg["vocab"]], np.uint32))
+    assert e.value.code == wpcg.E_ARG
+    m.prefill(np.arange(30, dtype=np.uint32))
+    with pytest.raises(wpcg.WpcgError):  # 30 + 11 > 40
+        m.prefill(np.arange(11, dtype=np.uint32))
+    m.prefill(np.arange(10, dtype=np.uint32))  # exactly full
+    assert m.position() == 40
+    m.close()

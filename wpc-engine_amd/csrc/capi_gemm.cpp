@@ -74,6 +74,32 @@ int run_gemm(wpcg_linear* L, const void* x, int x_dtype, uint32_t M, float* y, h
     return WPCG_OK;
 }
 
+}  // namespace
+
+int linear_gemm(wpcg_linear* L, const float* x, int x_mode, uint32_t M, const float* res, float* y, hipStream_t s)
+{
+    const DeviceMatrix& m = L->m;
+    if (M == 0 || m.rows == 0) return WPCG_OK;
+    if (m.nb == 0) return fail(WPCG_E_SHAPE, "batched GEMM of a matrix without inputs");
+    if (!L->gemm.xf) {
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        WPCG_HIP(hipStreamIsCapturing(s, &st));
+        if (st != hipStreamCaptureStatusNone)
+            return fail(WPCG_E_ARG, "the first batched call on a linear allocates its workspace: "
+                                    "make it before capturing a graph");
+        if (int rc = make_gemm(L, s)) return rc;
+    }
+    const uint32_t step = x_mode == GX_SPLIT ? GEMM_MAX_M_SPLIT : GEMM_MAX_M;
+    for (uint32_t c = 0; c < M; c += step) {
+        const int mc = (int)std::min<uint32_t>(step, M - c);
+        WPCG_HIP(launch_gemm(m, L->gemm, x + (uint64_t)c * m.cols, x_mode, mc, L->bias,
+                             res ? res + (uint64_t)c * m.rows : nullptr, y + (uint64_t)c * m.rows, s));
+    }
+    return WPCG_OK;
+}
+
+namespace {
+
 int check_gemm_args(wpcg_linear* L, const void* x, int x_dtype, uint32_t M, const float* y)
 {
     if (!L) return fail(WPCG_E_ARG, "null linear");

@@ -4,6 +4,7 @@
 // model.rs:419-547; Qwen3MoeModel::forward_token, qwen3_moe_model.rs:406-542)
 // plus the greedy argmax (sampling.rs:3-14) is a fixed sequence of launches
 // that is captured once as a HIP graph and replayed per token.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <memory>
@@ -23,6 +24,18 @@ struct Layer {
     wpcg_linear *gate = nullptr, *up = nullptr, *down = nullptr;  // dense MLP
     wpcg_moe* moe = nullptr;                                       // sparse MLP
     std::vector<uint8_t> experts_set;                              // 3 bits per expert
+};
+
+// Batch buffers of the FAST prefill, made by the first prefill call: rows
+// are the chunk's tokens (at most cap of them).
+struct Prefill {
+    uint32_t cap = 0;
+    float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr;
+    float *g = nullptr, *u = nullptr;           // dense MLP [cap][inter]
+    float *r = nullptr, *w = nullptr;           // router logits [cap][E], weights [cap][top_k]
+    int32_t* ids = nullptr;                     // [cap][top_k]
+    int *pair_tok = nullptr, *pair_pos = nullptr, *items = nullptr, *nitems = nullptr;
+    float *ge = nullptr, *ue = nullptr, *de = nullptr;  // per sorted pair: [P][moe_inter] x2, [P][hidden]
 };
 
 }  // namespace
@@ -48,6 +61,8 @@ struct wpcg_model {
     hipGraphExec_t exec = nullptr;
     int graph_mode = -1;
     bool use_graph = true;  // false: steps are enqueued launch by launch
+    bool use_prefill = true;  // FAST: prompts go through the batched prefill
+    Prefill pf;
     std::vector<void*> allocs;
 };
 
@@ -238,6 +253,145 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
         WPCG_HIP(launch_rms_norm(mode, m->residual, m->final_norm, H, c.eps, m->normed, s));
         if (int rc = wpcg_linear_matvec(head, m->normed, m->logits, s)) return rc;
     }
+    WPCG_HIP(launch_argmax_next(m->logits, (int)c.vocab, m->st, m->tokens, s));
+    return WPCG_OK;
+}
+
+// ---- batched prefill (FAST) --------------------------------------------------
+// Rows of tokens per prefill pass; longer prompts run pass after pass.
+constexpr uint32_t PF_CAP = 256;
+
+// Whether the batched path covers this model: FAST attention's head shapes,
+// and for MoE the router width, the pair count and one-slice expert GEMMs.
+bool prefill_ok(const wpcg_model* m)
+{
+    const wpcg_model_config& c = m->cfg;
+    if (!attention_fast_ok((int)c.n_heads, (int)c.n_kv_heads, (int)c.head_dim)) return false;
+    if (!c.n_experts) return true;
+    const uint32_t cap = std::min(PF_CAP, c.max_pos);
+    return c.n_experts <= (uint32_t)ROUTE_MAXN && cap * c.top_k <= (uint32_t)PF_MAX_PAIRS &&
+           c.hidden / 128 <= (uint32_t)GEMM_SMALL_MAXBK && c.moe_inter / 128 <= (uint32_t)GEMM_SMALL_MAXBK &&
+           c.moe_inter % 128 == 0;
+}
+
+int make_prefill(wpcg_model* m)
+{
+    Prefill& P = m->pf;
+    if (P.cap) return WPCG_OK;
+    const wpcg_model_config& c = m->cfg;
+    const size_t cap = std::min(PF_CAP, c.max_pos), H = c.hidden, qd = (size_t)c.n_heads * c.head_dim,
+                 kvd = (size_t)c.n_kv_heads * c.head_dim;
+    int rc = WPCG_OK;
+    auto dev = [&](void** p, size_t bytes) {
+        if (rc != WPCG_OK) return;
+        const hipError_t e = hipMalloc(p, std::max<size_t>(bytes, 4));
+        if (e != hipSuccess) {
+            rc = hip_fail(e, "prefill buffers");
+            return;
+        }
+        m->allocs.push_back(*p);
+    };
+    dev((void**)&P.x, cap * H * 4);
+    dev((void**)&P.xn, cap * H * 4);
+    dev((void**)&P.q, cap * qd * 4);
+    dev((void**)&P.k, cap * kvd * 4);
+    dev((void**)&P.v, cap * kvd * 4);
+    dev((void**)&P.attn, cap * qd * 4);
+    if (c.n_experts) {
+        const size_t pairs = cap * c.top_k, E = c.n_experts, I = c.moe_inter;
+        dev((void**)&P.r, cap * E * 4);
+        dev((void**)&P.w, pairs * 4);
+        dev((void**)&P.ids, pairs * 4);
+        dev((void**)&P.pair_tok, pairs * 4);
+        dev((void**)&P.pair_pos, pairs * 4);
+        dev((void**)&P.items, 3 * (pairs / GEMM_GROUP_COLS + E + 1) * 4);
+        dev((void**)&P.nitems, 4);
+        dev((void**)&P.ge, pairs * I * 4);
+        dev((void**)&P.ue, pairs * I * 4);
+        dev((void**)&P.de, pairs * H * 4);
+    } else {
+        dev((void**)&P.g, cap * c.inter * 4);
+        dev((void**)&P.u, cap * c.inter * 4);
+    }
+    if (rc == WPCG_OK) P.cap = (uint32_t)cap;
+    return rc;
+}
+
+// Tokens tokens[pos0 .. pos0+n-1] (already on the device) through every
+// layer as one batch, n <= cap: keys and values of those positions land in
+// the caches; the last row's final hidden state is left in pf.x[n-1].
+int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
+{
+    const wpcg_model_config& c = m->cfg;
+    Prefill& P = m->pf;
+    const int H = (int)c.hidden, hd = (int)c.head_dim, nh = (int)c.n_heads, nkv = (int)c.n_kv_heads;
+    const float scale = 1.0f / std::sqrt((float)hd);
+    const int F = WPCG_MODE_FAST;
+    WPCG_HIP(launch_embed_rows(m->embed->m, m->tokens + pos0, (int)n, P.x, s));
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        Layer& L = m->layers[l];
+        WPCG_HIP(launch_rms_norm_rows(F, P.x, L.in_ln, H, (int)n, c.eps, P.xn, s));
+        if (int rc = linear_gemm(L.q, P.xn, GX_SPLIT, n, nullptr, P.q, s)) return rc;
+        if (int rc = linear_gemm(L.k, P.xn, GX_SPLIT, n, nullptr, P.k, s)) return rc;
+        if (int rc = linear_gemm(L.v, P.xn, GX_SPLIT, n, nullptr, P.v, s)) return rc;
+        float* kc = m->kc + (size_t)l * nkv * c.max_pos * hd;
+        float* vc = m->vc + (size_t)l * nkv * c.max_pos * hd;
+        WPCG_HIP(launch_prefill_attention(P.q, P.k, P.v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale, m->cos_t,
+                                          m->sin_t, (int)pos0, (int)n, (int)c.max_pos, kc, vc, P.attn, s));
+        if (int rc = linear_gemm(L.o, P.attn, GX_SPLIT, n, P.x, P.x, s)) return rc;  // residual += o_proj
+        WPCG_HIP(launch_rms_norm_rows(F, P.x, L.post_ln, H, (int)n, c.eps, P.xn, s));
+        if (!c.n_experts) {
+            if (int rc = linear_gemm(L.gate, P.xn, GX_SPLIT, n, nullptr, P.g, s)) return rc;
+            if (int rc = linear_gemm(L.up, P.xn, GX_SPLIT, n, nullptr, P.u, s)) return rc;
+            WPCG_HIP(launch_silu_mul(P.g, P.u, P.g, (size_t)n * c.inter, s));
+            if (int rc = linear_gemm(L.down, P.g, GX_SPLIT, n, P.x, P.x, s)) return rc;
+            continue;
+        }
+        // experts: route every row, sort the (row, slot) pairs by expert, one
+        // grouped launch per projection, then the ordered combine
+        wpcg_moe* E = L.moe;
+        const int ne = (int)c.n_experts, K = (int)c.top_k, pairs = (int)n * K;
+        const int max_items = pairs / GEMM_GROUP_COLS + ne + 1;
+        WPCG_HIP(launch_pf_router(P.xn, E->router->w, (int)n, ne, H, P.r, s));
+        WPCG_HIP(launch_softmax_route_rows(P.r, ne, (int)n, K, (int)c.norm_topk, P.ids, P.w, s));
+        WPCG_HIP(launch_pf_group(P.ids, pairs, ne, K, P.pair_tok, P.pair_pos, P.items, P.nitems, s));
+        WPCG_HIP(launch_gemm_grouped(E->gate, P.xn, (int)n, P.pair_tok, P.items, P.nitems, max_items, P.ge, s));
+        WPCG_HIP(launch_gemm_grouped(E->up, P.xn, (int)n, P.pair_tok, P.items, P.nitems, max_items, P.ue, s));
+        WPCG_HIP(launch_silu_mul(P.ge, P.ue, P.ge, (size_t)pairs * c.moe_inter, s));
+        WPCG_HIP(launch_gemm_grouped(E->down, P.ge, pairs, nullptr, P.items, P.nitems, max_items, P.de, s));
+        WPCG_HIP(launch_pf_combine(P.x, P.de, P.w, P.pair_pos, (int)n, K, H, s));
+    }
+    return WPCG_OK;
+}
+
+// FAST prefill of tokens[pos0 .. pos0+n-1] in passes of at most cap rows,
+// then the last row's logits and the argmax step (st holds pos0 + n - 1 and
+// the caller's n_prompt, so the argmax lands in tokens[] as a step's would).
+int prefill_run(wpcg_model* m, uint32_t pos0, uint32_t n, uint32_t n_prompt)
+{
+    if (int rc = make_prefill(m)) return rc;
+    hipStream_t s = m->ctx->stream;
+    const wpcg_model_config& c = m->cfg;
+    uint32_t last = 0;
+    for (uint32_t done = 0; done < n;) {
+        const uint32_t len = std::min(m->pf.cap, n - done);
+        if (int rc = prefill_pass(m, pos0 + done, len, s)) return rc;
+        last = len - 1;
+        done += len;
+    }
+    const float* xl = m->pf.x + (size_t)last * c.hidden;
+    wpcg_linear* head = c.tied ? m->embed : m->lm_head;
+    bool fused = true;
+    GemvJob head_job = fast_job(head, xl, m->logits, m->final_norm, c.eps, fused);
+    if (fused) {
+        WPCG_HIP(launch_gemv_fast(&head_job, 1, s));
+    } else {
+        WPCG_HIP(launch_rms_norm(WPCG_MODE_FAST, xl, m->final_norm, (int)c.hidden, c.eps, m->normed, s));
+        if (int rc = wpcg_linear_matvec(head, m->normed, m->logits, s)) return rc;
+    }
+    WPCG_HIP(hipStreamSynchronize(s));
+    DecodeState st{pos0 + n - 1, n_prompt, c.max_pos, 0};
+    WPCG_HIP(hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice));
     WPCG_HIP(launch_argmax_next(m->logits, (int)c.vocab, m->st, m->tokens, s));
     return WPCG_OK;
 }
@@ -626,11 +780,19 @@ int wpcg_model_generate(wpcg_model* m, const uint32_t* prompt, uint32_t n_prompt
     WPCG_HIP(hipEventCreate(&e0));
     WPCG_HIP(hipEventCreate(&e1));
     int rc = WPCG_OK;
-    // steps at positions 0..n_prompt-1 consume the prompt (the last one
-    // yields the first new token); the n_new-1 after it are pure decode
-    for (uint32_t i = 0; i < n_prompt + n_new - 1 && rc == WPCG_OK; i++) {
-        if (i == n_prompt) (void)hipEventRecord(e0, s);
-        rc = run_step(m);
+    if (m->mode == WPCG_MODE_FAST && m->use_prefill && prefill_ok(m)) {
+        // the prompt as batches (yielding the first new token), then n_new-1
+        // decode steps
+        rc = prefill_run(m, 0, n_prompt, n_prompt);
+        (void)hipEventRecord(e0, s);
+        for (uint32_t i = 1; i < n_new && rc == WPCG_OK; i++) rc = run_step(m);
+    } else {
+        // steps at positions 0..n_prompt-1 consume the prompt (the last one
+        // yields the first new token); the n_new-1 after it are pure decode
+        for (uint32_t i = 0; i < n_prompt + n_new - 1 && rc == WPCG_OK; i++) {
+            if (i == n_prompt) (void)hipEventRecord(e0, s);
+            rc = run_step(m);
+        }
     }
     (void)hipEventRecord(e1, s);
     if (rc == WPCG_OK) {
@@ -646,6 +808,45 @@ int wpcg_model_generate(wpcg_model* m, const uint32_t* prompt, uint32_t n_prompt
     (void)hipEventDestroy(e1);
     if (rc != WPCG_OK) return rc;
     WPCG_HIP(hipMemcpy(out, m->tokens + n_prompt, (size_t)n_new * 4, hipMemcpyDeviceToHost));
+    return WPCG_OK;
+}
+
+int wpcg_model_set_prefill(wpcg_model* m, int enabled)
+{
+    if (!m) return fail(WPCG_E_ARG, "null model");
+    m->use_prefill = enabled != 0;
+    return WPCG_OK;
+}
+
+int wpcg_model_prefill(wpcg_model* m, const uint32_t* tokens, uint32_t n, float* logits, uint32_t* argmax)
+{
+    if (!m || !tokens) return fail(WPCG_E_ARG, "null argument");
+    if (n == 0) return fail(WPCG_E_ARG, "no tokens");
+    for (uint32_t i = 0; i < n; i++)
+        if (tokens[i] >= m->cfg.vocab) return fail(WPCG_E_ARG, "token id out of range");
+    if (int rc = ready(m)) return rc;
+    hipStream_t s = m->ctx->stream;
+    DecodeState st;
+    WPCG_HIP(hipStreamSynchronize(s));
+    WPCG_HIP(hipMemcpy(&st, m->st, sizeof st, hipMemcpyDeviceToHost));
+    if ((uint64_t)st.pos + n > m->cfg.max_pos) return fail(WPCG_E_ARG, "KV cache full (max_pos reached)");
+    WPCG_HIP(hipMemcpy(m->tokens + st.pos, tokens, (size_t)n * 4, hipMemcpyHostToDevice));
+    // every token comes from the host: keep the argmax out of tokens[]
+    const uint32_t pos0 = st.pos;
+    st.n_prompt = 0xffffffffu;
+    if (m->mode == WPCG_MODE_FAST && m->use_prefill && prefill_ok(m)) {
+        if (int rc = prefill_run(m, pos0, n, st.n_prompt)) return rc;
+    } else {
+        WPCG_HIP(hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice));
+        for (uint32_t i = 0; i < n; i++)
+            if (int rc = run_step(m)) return rc;
+    }
+    WPCG_HIP(hipStreamSynchronize(s));
+    if (logits) WPCG_HIP(hipMemcpy(logits, m->logits, (size_t)m->cfg.vocab * 4, hipMemcpyDeviceToHost));
+    if (argmax) {
+        WPCG_HIP(hipMemcpy(&st, m->st, sizeof st, hipMemcpyDeviceToHost));
+        *argmax = st.last;
+    }
     return WPCG_OK;
 }
 

@@ -66,6 +66,8 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
                                                  const float* __restrict__ w, int n, float eps,
                                                  float* __restrict__ out)
 {
+    x += (size_t)blockIdx.x * n;  // row blockIdx.x of a batch (one row: 0)
+    out += (size_t)blockIdx.x * n;
     __shared__ float xs[RN_LDS];
     __shared__ float red[NW / 64];
     __shared__ float s_total;
@@ -456,6 +458,153 @@ __global__ __launch_bounds__(FA_WG) void k_attention_fast(const float* __restric
     }
 }
 
+// ---- batched prefill: the n tokens at positions pos0 .. pos0+n-1 ----------
+// Row t of Q [n][nh*HD], K and V [n][nkv*HD] is position pos0 + t. Workgroup
+// t: q_norm + RoPE on every query head in place, k_norm + RoPE on every key
+// head into the key cache, every value head into the value cache (one wave
+// per head row, as fa_norm_rope does it for one position).
+template <int HD>
+__global__ __launch_bounds__(256) void k_pf_qk_rope(float* __restrict__ Q, const float* __restrict__ Kx,
+                                                    const float* __restrict__ Vx, const float* __restrict__ qn,
+                                                    const float* __restrict__ kn, int nh, int nkv, float eps,
+                                                    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+                                                    int pos0, int max_pos, float* __restrict__ kc,
+                                                    float* __restrict__ vc)
+{
+    const int t = blockIdx.x, pos = pos0 + t;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const float* cs = cos_t + (size_t)pos * (HD / 2);
+    const float* sn = sin_t + (size_t)pos * (HD / 2);
+    for (int r = wave; r < nh + 2 * nkv; r += 4) {
+        if (r < nh) {
+            float* q = Q + ((size_t)t * nh + r) * HD;
+            fa_norm_rope<HD>(q, qn, eps, cs, sn, q, nullptr);
+        } else if (r < nh + nkv) {
+            const int j = r - nh;
+            fa_norm_rope<HD>(Kx + ((size_t)t * nkv + j) * HD, kn, eps, cs, sn,
+                             kc + ((size_t)j * max_pos + pos) * HD, nullptr);
+        } else {
+            const int j = r - nh - nkv;
+            for (int d = lane; d < HD; d += 64)
+                vc[((size_t)j * max_pos + pos) * HD + d] = Vx[((size_t)t * nkv + j) * HD + d];
+        }
+    }
+}
+
+// Causal attention of query token t (position p = pos0 + t) over positions
+// 0..p of the caches, for the n_rep query heads of kv head j: workgroup
+// (j, t). Keys and values pass through LDS in blocks of FA_C positions
+// (the next block's loads in flight), with a running softmax per head as
+// in k_attention_fast; the output is o / l, written to O [n][nh*HD].
+template <int HD>
+__global__ __launch_bounds__(FA_WG) void k_pf_attention(const float* __restrict__ Q, int nh, int nkv, float scale,
+                                                        int pos0, int max_pos, const float* __restrict__ kc,
+                                                        const float* __restrict__ vc, float* __restrict__ O)
+{
+    constexpr int HD4 = HD / 4, KS = HD + 4;
+    constexpr int NOUT = FA_MAXREP * HD / FA_WG;
+    constexpr int G = FA_WG / HD;
+    constexpr int NKV = FA_C * HD4 / FA_WG;
+    __shared__ __align__(16) float qs[FA_MAXREP][HD];
+    __shared__ __align__(16) float ks[FA_C][KS];
+    __shared__ __align__(16) float vs[FA_C][HD];
+    __shared__ float ps[FA_MAXREP][FA_C];
+    __shared__ __align__(16) float pt[FA_C][FA_MAXREP + 4];
+    __shared__ float s_m[FA_MAXREP], s_l[FA_MAXREP], s_corr[FA_MAXREP];
+    const int j = blockIdx.x, t = blockIdx.y;
+    const int n = pos0 + t + 1, n_rep = nh / nkv;
+    const float* kb = kc + (size_t)j * max_pos * HD;
+    const float* vb = vc + (size_t)j * max_pos * HD;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+
+    float4 kr[NKV], vr[NKV];
+    auto load_block = [&](int t0) {
+#pragma unroll
+        for (int u = 0; u < NKV; u++) {
+            const int i = threadIdx.x + u * FA_WG, tt = t0 + i / HD4, d = 4 * (i % HD4);
+            if (tt < n) {
+                kr[u] = *reinterpret_cast<const float4*>(kb + (size_t)tt * HD + d);
+                vr[u] = *reinterpret_cast<const float4*>(vb + (size_t)tt * HD + d);
+            }
+        }
+    };
+    load_block(0);
+    for (int i = threadIdx.x; i < n_rep * HD; i += FA_WG)
+        qs[i / HD][i % HD] = Q[((size_t)t * nh + j * n_rep) * HD + i];
+    if (threadIdx.x < FA_MAXREP) {
+        s_m[threadIdx.x] = -INFINITY;
+        s_l[threadIdx.x] = 0.0f;
+    }
+    const int g = threadIdx.x / HD, d = threadIdx.x % HD;
+    const int nper = (n_rep + G - 1) / G, r0 = g * nper;
+    float o[NOUT];
+#pragma unroll
+    for (int u = 0; u < NOUT; u++) o[u] = 0.0f;
+    __syncthreads();
+
+    for (int t0 = 0; t0 < n; t0 += FA_C) {
+        const int nt = min(FA_C, n - t0);
+#pragma unroll
+        for (int u = 0; u < NKV; u++) {
+            const int i = threadIdx.x + u * FA_WG, tt = i / HD4, dd = 4 * (i % HD4);
+            if (tt < nt) {
+                *reinterpret_cast<float4*>(&ks[tt][dd]) = kr[u];
+                *reinterpret_cast<float4*>(&vs[tt][dd]) = vr[u];
+            }
+        }
+        __syncthreads();
+        if (t0 + FA_C < n) load_block(t0 + FA_C);
+        for (int i = threadIdx.x; i < n_rep * FA_C; i += FA_WG) {
+            const int r = i / FA_C, tt = i % FA_C;
+            float dot = -INFINITY;
+            if (tt < nt) {
+                float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+                for (int dd = 0; dd < HD; dd += 4) {
+                    const float4 q4 = *reinterpret_cast<const float4*>(&qs[r][dd]);
+                    const float4 k4 = *reinterpret_cast<const float4*>(&ks[tt][dd]);
+                    a0 = fmaf(q4.x, k4.x, a0);
+                    a1 = fmaf(q4.y, k4.y, a1);
+                    a2 = fmaf(q4.z, k4.z, a2);
+                    a3 = fmaf(q4.w, k4.w, a3);
+                }
+                dot = ((a0 + a1) + (a2 + a3)) * scale;
+            }
+            ps[r][tt] = dot;
+        }
+        __syncthreads();
+        for (int r = wave; r < n_rep; r += FA_WG / 64) {
+            const float v = lane < FA_C ? ps[r][lane] : -INFINITY;
+            const float m = wave_max(v);
+            const float mo = s_m[r], mn = fmaxf(mo, m);
+            const float e = lane < nt ? __expf(v - mn) : 0.0f;
+            const float l = wave_sum(e);
+            const float corr = __expf(mo - mn);
+            if (lane < FA_C) pt[lane][r] = e;
+            if (lane == 0) {
+                s_m[r] = mn;
+                s_l[r] = fmaf(s_l[r], corr, l);
+                s_corr[r] = corr;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < NOUT; u++)
+            if (u < nper && r0 + u < n_rep) o[u] *= s_corr[r0 + u];
+        for (int tt = 0; tt < nt; tt++) {
+            const float v = vs[tt][d];
+#pragma unroll
+            for (int u = 0; u < NOUT; u++)
+                if (u < nper) o[u] = fmaf(pt[tt][r0 + u], v, o[u]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < NOUT; u++)
+        if (u < nper && r0 + u < n_rep)
+            O[((size_t)t * nh + j * n_rep + r0 + u) * HD + d] = __fdiv_rn(o[u], s_l[r0 + u]);
+}
+
 // x[i] += y[i] (residual updates the GEMV epilogues do not cover)
 __global__ __launch_bounds__(256) void k_add(float* __restrict__ x, const float* __restrict__ y, int n)
 {
@@ -537,6 +686,17 @@ hipError_t launch_rms_norm(int mode, const float* x, const float* w, int n, floa
     return hipGetLastError();
 }
 
+hipError_t launch_rms_norm_rows(int mode, const float* x, const float* w, int n, int rows, float eps, float* out,
+                                hipStream_t s)
+{
+    (void)hipGetLastError();
+    if (mode == WPCG_MODE_EXACT)
+        hipLaunchKernelGGL(k_rms_norm<WPCG_MODE_EXACT>, dim3(rows), dim3(NW), 0, s, x, w, n, eps, out);
+    else
+        hipLaunchKernelGGL(k_rms_norm<WPCG_MODE_FAST>, dim3(rows), dim3(NW), 0, s, x, w, n, eps, out);
+    return hipGetLastError();
+}
+
 int attention_max_pos() { return AT_MAXPOS; }
 
 bool attention_fast_ok(int nh, int nkv, int hd) { return (hd == 64 || hd == 128) && nh / nkv <= FA_MAXREP; }
@@ -569,6 +729,27 @@ hipError_t launch_attention_chunks(const float* q, const float* k, const float* 
     else
         hipLaunchKernelGGL(k_attention_fast<64>, dim3(nkv * FA_NCH), dim3(FA_WG), 0, s, q, k, v, qn, kn, nh,
                            nkv, eps, scale, cos_t, sin_t, st, kc, vc, part_o, part_ml);
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_attention(float* Q, const float* Kx, const float* Vx, const float* qn, const float* kn,
+                                    int nh, int nkv, int hd, float eps, float scale, const float* cos_t,
+                                    const float* sin_t, int pos0, int n, int max_pos, float* kc, float* vc,
+                                    float* out, hipStream_t s)
+{
+    if (!attention_fast_ok(nh, nkv, hd) || n < 1 || pos0 + n > max_pos) return hipErrorInvalidValue;
+    (void)hipGetLastError();
+    if (hd == 128) {
+        hipLaunchKernelGGL(k_pf_qk_rope<128>, dim3(n), dim3(256), 0, s, Q, Kx, Vx, qn, kn, nh, nkv, eps, cos_t,
+                           sin_t, pos0, max_pos, kc, vc);
+        hipLaunchKernelGGL(k_pf_attention<128>, dim3(nkv, n), dim3(FA_WG), 0, s, Q, nh, nkv, scale, pos0, max_pos,
+                           kc, vc, out);
+    } else {
+        hipLaunchKernelGGL(k_pf_qk_rope<64>, dim3(n), dim3(256), 0, s, Q, Kx, Vx, qn, kn, nh, nkv, eps, cos_t,
+                           sin_t, pos0, max_pos, kc, vc);
+        hipLaunchKernelGGL(k_pf_attention<64>, dim3(nkv, n), dim3(FA_WG), 0, s, Q, nh, nkv, scale, pos0, max_pos,
+                           kc, vc, out);
+    }
     return hipGetLastError();
 }
 

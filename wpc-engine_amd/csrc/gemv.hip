@@ -869,6 +869,22 @@ __global__ __launch_bounds__(256) void k_embed_tok(const uint8_t* __restrict__ c
     out[k] = __fadd_rn(h2f(p & 0xFFFFu), __fmul_rn((float)code, h2f(p >> 16)));
 }
 
+// Embedding rows of a batch of tokens: out[t] = row tokens[t] (blockIdx.y = t).
+template <int SCHEME>
+__global__ __launch_bounds__(256) void k_embed_rows(const uint8_t* __restrict__ codes,
+                                                    const uint8_t* __restrict__ hp,
+                                                    const uint32_t* __restrict__ params,
+                                                    float* __restrict__ out,
+                                                    const uint32_t* __restrict__ tokens, int nb, uint32_t rows)
+{
+    const int k = blockIdx.x * 256 + threadIdx.x;
+    if (k >= nb * 128) return;
+    const uint32_t row = min(tokens[blockIdx.y], rows - 1);  // ids are checked on the host
+    const uint32_t code = code_at(codes, hp, row, (size_t)(k >> 7), nb, k & 127, SCHEME);
+    const uint32_t p = params[param_idx(row, nb, k >> 7)];
+    out[(size_t)blockIdx.y * nb * 128 + k] = __fadd_rn(h2f(p & 0xFFFFu), __fmul_rn((float)code, h2f(p >> 16)));
+}
+
 template <int SCHEME>
 __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ codes,
                                                  const uint8_t* __restrict__ hp,
@@ -1038,6 +1054,19 @@ hipError_t launch_embed_tok(const DeviceMatrix& m, const uint32_t* tokens, const
     else
         hipLaunchKernelGGL(k_embed_tok<3>, grid, dim3(256), 0, s, m.codes, m.hp, m.params, out, tokens,
                            st, (int)m.nb, (uint32_t)m.rows);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(const DeviceMatrix& m, const uint32_t* tokens, int n, float* out, hipStream_t s)
+{
+    dim3 grid((unsigned)((m.cols + 255) / 256), (unsigned)n);
+    (void)hipGetLastError();
+    if (m.scheme == 4)
+        hipLaunchKernelGGL(k_embed_rows<4>, grid, dim3(256), 0, s, m.codes, m.hp, m.params, out, tokens, (int)m.nb,
+                           (uint32_t)m.rows);
+    else
+        hipLaunchKernelGGL(k_embed_rows<3>, grid, dim3(256), 0, s, m.codes, m.hp, m.params, out, tokens, (int)m.nb,
+                           (uint32_t)m.rows);
     return hipGetLastError();
 }
 

@@ -200,6 +200,9 @@ __global__ __launch_bounds__(64) void k_softmax_route(const float* __restrict__ 
                                                       int32_t* __restrict__ ids,
                                                       float* __restrict__ w)
 {
+    scores += (size_t)blockIdx.x * n;  // row blockIdx.x of a batch (one row: 0)
+    ids += (size_t)blockIdx.x * top_k;
+    w += (size_t)blockIdx.x * top_k;
     __shared__ __align__(16) float e[64 * RT_PER];
     __shared__ float chosen[64];
     __shared__ float s_sum;
@@ -346,6 +349,14 @@ hipError_t launch_softmax_route(const float* scores, int n, int top_k, int norm_
 {
     (void)hipGetLastError();
     hipLaunchKernelGGL(k_softmax_route, dim3(1), dim3(64), 0, s, scores, n, top_k, norm_topk, ids, w);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax_route_rows(const float* scores, int n, int rows, int top_k, int norm_topk, int32_t* ids,
+                                     float* w, hipStream_t s)
+{
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k_softmax_route, dim3(rows), dim3(64), 0, s, scores, n, top_k, norm_topk, ids, w);
     return hipGetLastError();
 }
 

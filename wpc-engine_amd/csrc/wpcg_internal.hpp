@@ -269,6 +269,33 @@ hipError_t launch_attention_chunks(const float* q, const float* k, const float* 
                                    const float* cos_t, const float* sin_t, const DecodeState* st, float* kc,
                                    float* vc, float* part_o, float* part_ml, hipStream_t s);
 hipError_t launch_add(float* x, const float* y, int n, hipStream_t s);
+// ---- batched prefill (decode.hip, gemv.hip, moe.hip, prefill.hip) ---------
+// n tokens at positions pos0 .. pos0+n-1, row t of every batch buffer being
+// position pos0 + t.
+hipError_t launch_embed_rows(const DeviceMatrix& m, const uint32_t* tokens, int n, float* out, hipStream_t s);
+hipError_t launch_rms_norm_rows(int mode, const float* x, const float* w, int n, int rows, float eps, float* out,
+                                hipStream_t s);
+// q_norm/k_norm + RoPE (Q in place, keys into kc), values into vc, then
+// causal attention of every row over positions 0..pos0+t into out [n][nh*hd].
+// Needs attention_fast_ok.
+hipError_t launch_prefill_attention(float* Q, const float* Kx, const float* Vx, const float* qn, const float* kn,
+                                    int nh, int nkv, int hd, float eps, float scale, const float* cos_t,
+                                    const float* sin_t, int pos0, int n, int max_pos, float* kc, float* vc,
+                                    float* out, hipStream_t s);
+hipError_t launch_softmax_route_rows(const float* scores, int n, int rows, int top_k, int norm_topk, int32_t* ids,
+                                     float* w, hipStream_t s);
+// R[t][e] = X[t] . W[e] (fp32 router rows), R is [T][E].
+hipError_t launch_pf_router(const float* X, const float* W, int T, int E, int K, float* R, hipStream_t s);
+// (token, slot) pairs sorted by expert for launch_gemm_grouped: pair_tok
+// [P], pair_pos [P], items [3 * (P / GEMM_GROUP_COLS + E)], nitems [1].
+constexpr int PF_MAX_PAIRS = 8192;
+hipError_t launch_pf_group(const int32_t* ids, int P, int E, int top_k, int* pair_tok, int* pair_pos, int* items,
+                           int* nitems, hipStream_t s);
+hipError_t launch_pf_combine(float* X, const float* D, const float* w, const int* pair_pos, int T, int top_k, int H,
+                             hipStream_t s);
+// Y = X W^T (+ res) for M rows of fp32 X with the linear's batched kernels
+// (x_mode GX_*), its workspace made on first use (not under capture).
+int linear_gemm(wpcg_linear* L, const float* x, int x_mode, uint32_t M, const float* res, float* y, hipStream_t s);
 hipError_t launch_argmax_next(const float* logits, int n, DecodeState* st, uint32_t* tokens,
                               hipStream_t s);
 

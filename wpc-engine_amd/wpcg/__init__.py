@@ -116,6 +116,8 @@ _SIGS = {
     "wpcg_model_position": (C.c_int, [_p, C.POINTER(C.c_uint32)]),
     "wpcg_model_forward_token": (C.c_int, [_p, C.c_uint32, _p, C.POINTER(C.c_uint32)]),
     "wpcg_model_generate": (C.c_int, [_p, _p, C.c_uint32, C.c_uint32, _p, C.POINTER(C.c_float)]),
+    "wpcg_model_prefill": (C.c_int, [_p, _p, C.c_uint32, _p, C.POINTER(C.c_uint32)]),
+    "wpcg_model_set_prefill": (C.c_int, [_p, C.c_int]),
     "wpcg_model_debug_read": (C.c_int, [_p, C.c_int, _p, _u64]),
     "wpcg_rms_norm": (C.c_int, [_p, _p, _p, C.c_uint32, C.c_float, _p, C.c_int, _p]),
     "wpcg_dense_create": (C.c_int, [_p, _p, _u64, _u64, _p, _pp]),
@@ -830,6 +832,20 @@ class Model:
         check(lib.wpcg_model_forward_token(self.h, token, None if logits is None else _np_ptr(logits),
                                            C.byref(a)))
         return logits, a.value
+
+    def prefill(self, tokens, want_logits: bool = True):
+        """The tokens at the next positions as forward_token would run them
+        one by one (FAST: batched): (logits of the last or None, argmax)."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.empty(self.cfg.vocab, np.float32) if want_logits else None
+        a = C.c_uint32()
+        check(lib.wpcg_model_prefill(self.h, _np_ptr(t), t.size, None if logits is None else _np_ptr(logits),
+                                     C.byref(a)))
+        return logits, a.value
+
+    def set_prefill(self, enabled: bool):
+        check(lib.wpcg_model_set_prefill(self.h, int(bool(enabled))))
+        return self
 
     def generate(self, prompt, n_new: int):
         """(new token ids uint32[n_new], ms of the n_new-1 steps after the prompt)"""
