@@ -36,6 +36,8 @@ struct Prefill {
     int32_t* ids = nullptr;                     // [cap][top_k]
     int *pair_tok = nullptr, *pair_pos = nullptr, *items = nullptr, *nitems = nullptr;
     float *ge = nullptr, *ue = nullptr, *de = nullptr;  // per sorted pair: [P][moe_inter] x2, [P][hidden]
+    void* xf = nullptr;       // packed X of the batched GEMMs (launch_gemm_pack_rows)
+    float* xsum = nullptr;
 };
 
 }  // namespace
@@ -270,7 +272,8 @@ bool prefill_ok(const wpcg_model* m)
     if (!c.n_experts) return true;
     const uint32_t cap = std::min(PF_CAP, c.max_pos);
     return c.n_experts <= (uint32_t)ROUTE_MAXN && cap * c.top_k <= (uint32_t)PF_MAX_PAIRS &&
-           c.hidden / 128 <= (uint32_t)GEMM_SMALL_MAXBK && c.moe_inter / 128 <= (uint32_t)GEMM_SMALL_MAXBK &&
+           c.hidden / 128 <= (uint32_t)GEMM_GROUP_MAXBK && c.moe_inter / 128 <= (uint32_t)GEMM_GROUP_MAXBK &&
+           pad_rows(c.hidden) <= (uint64_t)GEMM_GROUP_MAXROWS && pad_rows(c.moe_inter) <= (uint64_t)GEMM_GROUP_MAXROWS &&
            c.moe_inter % 128 == 0;
 }
 
@@ -297,6 +300,9 @@ int make_prefill(wpcg_model* m)
     dev((void**)&P.k, cap * kvd * 4);
     dev((void**)&P.v, cap * kvd * 4);
     dev((void**)&P.attn, cap * qd * 4);
+    const size_t kmax = std::max<size_t>({H, qd, c.n_experts ? 0 : (size_t)c.inter});
+    dev((void**)&P.xf, kmax / 128 * gemm_rows_tiles((int)cap) * 4096);
+    dev((void**)&P.xsum, kmax / 128 * gemm_rows_tiles((int)cap) * 16 * 4);
     if (c.n_experts) {
         const size_t pairs = cap * c.top_k, E = c.n_experts, I = c.moe_inter;
         dev((void**)&P.r, cap * E * 4);
@@ -331,20 +337,25 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
     for (uint32_t l = 0; l < c.n_layers; l++) {
         Layer& L = m->layers[l];
         WPCG_HIP(launch_rms_norm_rows(F, P.x, L.in_ln, H, (int)n, c.eps, P.xn, s));
-        if (int rc = linear_gemm(L.q, P.xn, GX_SPLIT, n, nullptr, P.q, s)) return rc;
-        if (int rc = linear_gemm(L.k, P.xn, GX_SPLIT, n, nullptr, P.k, s)) return rc;
-        if (int rc = linear_gemm(L.v, P.xn, GX_SPLIT, n, nullptr, P.v, s)) return rc;
+        WPCG_HIP(launch_gemm_pack_rows(P.xn, (int)n, H, P.xf, P.xsum, s));
+        WPCG_HIP(launch_gemm_packed_rows(L.q->m, P.xf, P.xsum, (int)n, L.q->bias, nullptr, P.q, s));
+        WPCG_HIP(launch_gemm_packed_rows(L.k->m, P.xf, P.xsum, (int)n, L.k->bias, nullptr, P.k, s));
+        WPCG_HIP(launch_gemm_packed_rows(L.v->m, P.xf, P.xsum, (int)n, L.v->bias, nullptr, P.v, s));
         float* kc = m->kc + (size_t)l * nkv * c.max_pos * hd;
         float* vc = m->vc + (size_t)l * nkv * c.max_pos * hd;
         WPCG_HIP(launch_prefill_attention(P.q, P.k, P.v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale, m->cos_t,
                                           m->sin_t, (int)pos0, (int)n, (int)c.max_pos, kc, vc, P.attn, s));
-        if (int rc = linear_gemm(L.o, P.attn, GX_SPLIT, n, P.x, P.x, s)) return rc;  // residual += o_proj
+        // residual += o_proj(attn)
+        WPCG_HIP(launch_gemm_pack_rows(P.attn, (int)n, nh * hd, P.xf, P.xsum, s));
+        WPCG_HIP(launch_gemm_packed_rows(L.o->m, P.xf, P.xsum, (int)n, L.o->bias, P.x, P.x, s));
         WPCG_HIP(launch_rms_norm_rows(F, P.x, L.post_ln, H, (int)n, c.eps, P.xn, s));
         if (!c.n_experts) {
-            if (int rc = linear_gemm(L.gate, P.xn, GX_SPLIT, n, nullptr, P.g, s)) return rc;
-            if (int rc = linear_gemm(L.up, P.xn, GX_SPLIT, n, nullptr, P.u, s)) return rc;
+            WPCG_HIP(launch_gemm_pack_rows(P.xn, (int)n, H, P.xf, P.xsum, s));
+            WPCG_HIP(launch_gemm_packed_rows(L.gate->m, P.xf, P.xsum, (int)n, L.gate->bias, nullptr, P.g, s));
+            WPCG_HIP(launch_gemm_packed_rows(L.up->m, P.xf, P.xsum, (int)n, L.up->bias, nullptr, P.u, s));
             WPCG_HIP(launch_silu_mul(P.g, P.u, P.g, (size_t)n * c.inter, s));
-            if (int rc = linear_gemm(L.down, P.g, GX_SPLIT, n, P.x, P.x, s)) return rc;
+            WPCG_HIP(launch_gemm_pack_rows(P.g, (int)n, (int)c.inter, P.xf, P.xsum, s));
+            WPCG_HIP(launch_gemm_packed_rows(L.down->m, P.xf, P.xsum, (int)n, L.down->bias, P.x, P.x, s));
             continue;
         }
         // experts: route every row, sort the (row, slot) pairs by expert, one

@@ -591,11 +591,27 @@ __global__ __launch_bounds__(FA_WG) void k_pf_attention(const float* __restrict_
 #pragma unroll
         for (int u = 0; u < NOUT; u++)
             if (u < nper && r0 + u < n_rep) o[u] *= s_corr[r0 + u];
-        for (int tt = 0; tt < nt; tt++) {
-            const float v = vs[tt][d];
+        if ((nper & 3) == 0) {  // four heads' weights per 16-byte read
+#pragma unroll 4
+            for (int tt = 0; tt < nt; tt++) {
+                const float v = vs[tt][d];
 #pragma unroll
-            for (int u = 0; u < NOUT; u++)
-                if (u < nper) o[u] = fmaf(pt[tt][r0 + u], v, o[u]);
+                for (int u = 0; u < NOUT; u += 4)
+                    if (u < nper) {
+                        const float4 w4 = *reinterpret_cast<const float4*>(&pt[tt][r0 + u]);
+                        o[u] = fmaf(w4.x, v, o[u]);
+                        o[u + 1] = fmaf(w4.y, v, o[u + 1]);
+                        o[u + 2] = fmaf(w4.z, v, o[u + 2]);
+                        o[u + 3] = fmaf(w4.w, v, o[u + 3]);
+                    }
+            }
+        } else {
+            for (int tt = 0; tt < nt; tt++) {
+                const float v = vs[tt][d];
+#pragma unroll
+                for (int u = 0; u < NOUT; u++)
+                    if (u < nper) o[u] = fmaf(pt[tt][r0 + u], v, o[u]);
+            }
         }
         __syncthreads();
     }

@@ -73,16 +73,21 @@ __device__ __forceinline__ float bf16_round(float v) { return bf16_lo(pk_bf16(v,
 // kstep i, lane g*16 + c column c. SPLIT (fp32 X): column tiles
 // [0, NT/2) hold hi = bf16(x) and tiles [NT/2, NT) lo = bf16(x - hi) of the
 // same columns, so hi + lo carries x to a relative 2^-18.
+//
+// The XT column tiles of a block form groups of NT (the tiles one k_gemm
+// workgroup reads); with SPLIT each group holds NT/2 hi tiles then the NT/2
+// lo tiles of the same columns.
 template <bool BF16_IN, bool SPLIT>
-__global__ __launch_bounds__(256) void k_gemm_pack(const void* __restrict__ X, int M, int K, int NT,
+__global__ __launch_bounds__(256) void k_gemm_pack(const void* __restrict__ X, int M, int K, int XT, int NT,
                                                    u32x4* __restrict__ xf, float* __restrict__ xsum)
 {
     __shared__ float red[4][16];
-    const int b = blockIdx.x / NT, n = blockIdx.x % NT;
+    const int b = blockIdx.x / XT, n = blockIdx.x % XT;
     const int i = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, c = lane & 15;
+    const int cg = n / NT, w = n % NT;  // group, tile within it
     const int nh = SPLIT ? NT / 2 : NT;
-    const bool lo_part = SPLIT && n >= nh;
-    const int m = (lo_part ? n - nh : n) * 16 + c;
+    const bool lo_part = SPLIT && w >= nh;
+    const int m = (cg * nh + (lo_part ? w - nh : w)) * 16 + c;
     float v[8];
 #pragma unroll
     for (int s = 0; s < 8; s++) {
@@ -100,7 +105,7 @@ __global__ __launch_bounds__(256) void k_gemm_pack(const void* __restrict__ X, i
     o.y = pk_bf16(v[2], v[3]);
     o.z = pk_bf16(v[4], v[5]);
     o.w = pk_bf16(v[6], v[7]);
-    xf[((size_t)(b * NT + n) * 4 + i) * 64 + lane] = o;
+    xf[((size_t)(b * XT + n) * 4 + i) * 64 + lane] = o;
     float sum = ((bf16_lo(o.x) + bf16_hi(o.x)) + (bf16_lo(o.y) + bf16_hi(o.y))) +
                 ((bf16_lo(o.z) + bf16_hi(o.z)) + (bf16_lo(o.w) + bf16_hi(o.w)));
     sum += __shfl_xor(sum, 16);
@@ -108,7 +113,7 @@ __global__ __launch_bounds__(256) void k_gemm_pack(const void* __restrict__ X, i
     if (g == 0) red[i][c] = sum;
     __syncthreads();
     if (threadIdx.x < 16)
-        xsum[(size_t)b * NT * 16 + n * 16 + threadIdx.x] =
+        xsum[(size_t)b * XT * 16 + n * 16 + threadIdx.x] =
             (red[0][threadIdx.x] + red[1][threadIdx.x]) + (red[2][threadIdx.x] + red[3][threadIdx.x]);
 }
 
@@ -124,6 +129,10 @@ struct GemmArgs {
     float* part;         // [kg][NT*16][rows_pad] (kg > 1)
     uint32_t* counters;  // one per row group (kg > 1), self-resetting
     int rows, rows_pad, nb, M, kg;
+    // column groups: the packed X holds xt tiles per block (groups of NT);
+    // with rgs8 > 0 workgroup cg * rgs8 + rg takes row group rg (< rgs) of
+    // column group cg, kg = 1 (the groups of one row group share an XCD's L2)
+    int xt, rgs, rgs8;
 };
 
 // The value written for output (m, row): the sum, the bias, the residual.
@@ -182,8 +191,19 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
     __shared__ float xsb[2][NT * 16];
     __shared__ int s_last;
 
-    const int kg = P.kg, nb = P.nb;
-    const int kgi = blockIdx.x % kg, rg = blockIdx.x / kg;
+    const int kg = P.kg, nb = P.nb, XT = P.xt;
+    int kgi, rg, cg;
+    if (P.rgs8) {
+        rg = blockIdx.x % P.rgs8;
+        cg = blockIdx.x / P.rgs8;
+        kgi = 0;
+        if (rg >= P.rgs) return;  // padding of the row groups, uniform
+    } else {
+        kgi = blockIdx.x % kg;
+        rg = blockIdx.x / kg;
+        cg = 0;
+    }
+    const int mcol0 = cg * (SPLIT ? NT / 2 : NT) * 16;  // the group's first output column
     const int nbk = (nb + kg - 1) / kg;
     const int b0 = min(kgi * nbk, nb);
     const int nbl = max(0, min(nb, b0 + nbk) - b0);
@@ -205,8 +225,8 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
                            ok && SCHEME == 3 ? nbl * (int)HP_REC : 0);
         prs[rt] = buf_rsrc(P.params + rec * TILE_ROWS, ok ? nbl * TILE_ROWS * 4 : 0);
     }
-    const auto xrs = buf_rsrc(P.xf + (size_t)b0 * NT * 256, nbl * NT * 4096);
-    const auto srs = buf_rsrc(P.xsum + (size_t)b0 * NT * 16, nbl * NT * 64);
+    const auto xrs = buf_rsrc(P.xf + ((size_t)b0 * XT + cg * NT) * 256, (nbl * XT - cg * NT) * 4096);
+    const auto srs = buf_rsrc(P.xsum + (size_t)b0 * XT * 16 + cg * NT * 16, (nbl * XT - cg * NT) * 64);
 
     u32x4 cr[GM_LA][GM_RT], pr[GM_LA][GM_RT];
     u32x2 hr[GM_LA][GM_RT];
@@ -227,9 +247,9 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
 #pragma unroll
         for (int v = 0; v < XV; v++)
             xr[u][v] = __builtin_amdgcn_raw_buffer_load_b128(
-                xrs, (b * NT * 256 + min((int)threadIdx.x + v * GM_WG8, NT * 256 - 1)) * 16, 0, 0);
+                xrs, (b * XT * 256 + min((int)threadIdx.x + v * GM_WG8, NT * 256 - 1)) * 16, 0, 0);
         sr[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-            srs, (b * NT * 16 + min((int)threadIdx.x, NT * 16 - 1)) * 4, 0, 0));
+            srs, (b * XT * 16 + min((int)threadIdx.x, NT * 16 - 1)) * 4, 0, 0));
     };
     auto store_x = [&](int u, int buf) {
 #pragma unroll
@@ -349,7 +369,7 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
         for (int rt = 0; rt < GM_RT; rt++)
 #pragma unroll
             for (int nn = 0; nn < NTH; nn++) {
-                const int n = c0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
+                const int n = c0 + nn, m = mcol0 + n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
                 if (n >= c1 || m >= P.M) continue;
 #pragma unroll
                 for (int q = 0; q < 4; q++)
@@ -419,22 +439,13 @@ struct GemmSmallArgs {
     const uint8_t* codes;
     const uint8_t* hp;
     const uint32_t* params;
-    const void* x;       // [M][K] row-major (GROUPED: [xrows][K])
+    const void* x;       // [M][K] row-major
     float* y;
     const float* bias;
     const float* res;    // [M][rows] added to Y (may be y itself) or null
     float* part;         // [kg][16][rows_pad] (kg > 1)
     uint32_t* counters;
     int rows, rows_pad, nb, M, kg;
-    // GROUPED: workgroup item * rgs + rg takes items[item] = {expert, first
-    // pair p0, count}; its column c is X row rowidx[p0 + c] (rowidx null:
-    // row p0 + c) and Y row p0 + c; the expert's planes sit e * e{codes,
-    // hp, params} further on. kg = 1.
-    const int* rowidx;
-    const int* items;
-    const int* nitems;
-    size_t ecodes, ehp, eparams;  // bytes, bytes, 32-bit words
-    int xrows, rgs;
 };
 
 // Eight bf16 of one fragment lane from two consecutive-k pieces: the low
@@ -455,7 +466,7 @@ __device__ __forceinline__ float lo_of(uint32_t bits)
 // SPLIT (fp32 X, M <= 8): fragment columns [0, M) carry hi = bf16(x) and
 // [M, 2M) lo = bf16(x - hi) of the same rows; after the dots lane j adds
 // lane j + M (hi + lo) and writes column j.
-template <int SCHEME, bool BF16_IN, bool SPLIT, bool GROUPED>
+template <int SCHEME, bool BF16_IN, bool SPLIT>
 __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
 {
     static_assert(!(SPLIT && BF16_IN), "bf16 X has no lo part");
@@ -464,27 +475,8 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
     __shared__ __align__(16) f32x4 red[GS_TILES][64];
     __shared__ int s_last;
 
-    const int kg = GROUPED ? 1 : P.kg, nb = P.nb, K = nb * 128;
-    int M = P.M, p0 = 0;
-    const uint8_t* codes = P.codes;
-    const uint8_t* hpl = P.hp;
-    const uint32_t* params = P.params;
-    int kgi, rg;
-    if constexpr (GROUPED) {
-        const int item = blockIdx.x / P.rgs;
-        rg = blockIdx.x % P.rgs;
-        kgi = 0;
-        if (item >= *P.nitems) return;  // uniform over the workgroup
-        const int e = P.items[3 * item];
-        p0 = P.items[3 * item + 1];
-        M = P.items[3 * item + 2];
-        codes += (size_t)e * P.ecodes;
-        hpl += (size_t)e * P.ehp;
-        params += (size_t)e * P.eparams;
-    } else {
-        kgi = blockIdx.x % kg;
-        rg = blockIdx.x / kg;
-    }
+    const int kg = P.kg, nb = P.nb, K = nb * 128, M = P.M;
+    const int kgi = blockIdx.x % kg, rg = blockIdx.x / kg;
     const int Mx = SPLIT ? 2 * M : M;  // fragment columns in use
     const int nbk = (nb + kg - 1) / kg;
     const int b0 = min(kgi * nbk, nb);
@@ -504,17 +496,15 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
     // consecutive k; a thread takes tasks t and t + 512 (ntask <= 960).
     constexpr int es = BF16_IN ? 2 : 4;
     constexpr int PIECES = BF16_IN ? 8 : 16;  // 16-byte loads per task
-    const int xrows = GROUPED ? P.xrows : M;
     const auto xrs = buf_rsrc(static_cast<const uint8_t*>(P.x) + (size_t)b0 * 128 * es,
-                              (int)(((size_t)(xrows - 1) * K + (size_t)nbl * 128) * es));
+                              (int)(((size_t)(M - 1) * K + (size_t)nbl * 128) * es));
     const int ntask = nbl * 2 * Mx;
     u32x4 xv[2][PIECES];
 #pragma unroll
     for (int r = 0; r < 2; r++) {
         const int t = threadIdx.x + r * GS_WG;
         const int blk = t / (2 * Mx), c = (t >> 1) % Mx, h = t & 1;
-        int xr = SPLIT && c >= M ? c - M : c;  // the X row of fragment column c
-        if constexpr (GROUPED) xr = t < ntask ? (P.rowidx ? P.rowidx[p0 + xr] : p0 + xr) : 0;
+        const int xr = SPLIT && c >= M ? c - M : c;  // the X row of fragment column c
         const int base = t < ntask ? (xr * K + blk * 128 + 64 * h) * es : 0x7FFFFFF0;  // past the range: zeros
 #pragma unroll
         for (int p = 0; p < PIECES; p++) xv[r][p] = __builtin_amdgcn_raw_buffer_load_b128(xrs, base + p * 16, 0, 0);
@@ -522,9 +512,9 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
 
     // ---- then the first GS_LA blocks of this wave's codes
     const size_t rec = (size_t)min(T, ntiles - 1) * nb + b0 + kb0;
-    const auto crs = buf_rsrc(codes + rec * CODE_REC, tile_ok ? kn * (int)CODE_REC : 0);
-    const auto hrs = buf_rsrc((SCHEME == 3 ? hpl : codes) + rec * HP_REC, tile_ok && SCHEME == 3 ? kn * (int)HP_REC : 0);
-    const auto prs = buf_rsrc(params + rec * TILE_ROWS, tile_ok ? kn * TILE_ROWS * 4 : 0);
+    const auto crs = buf_rsrc(P.codes + rec * CODE_REC, tile_ok ? kn * (int)CODE_REC : 0);
+    const auto hrs = buf_rsrc((SCHEME == 3 ? P.hp : P.codes) + rec * HP_REC, tile_ok && SCHEME == 3 ? kn * (int)HP_REC : 0);
+    const auto prs = buf_rsrc(P.params + rec * TILE_ROWS, tile_ok ? kn * TILE_ROWS * 4 : 0);
     u32x4 cr[GS_LA], pr[GS_LA];
     u32x2 hr[GS_LA];
     auto load_codes = [&](int u, int b) {
@@ -667,14 +657,13 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
     }
     const bool writer = !part_k && tile_ok;
 
-    // lane (g, j) holds rows 4g..4g+3 of the tile for column j (Y row p0 + j)
+    // lane (g, j) holds rows 4g..4g+3 of the tile for column j
     const int row = T * TILE_ROWS + 4 * g;
     if (kg == 1) {
         if (writer && j < M)
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                if (row + q < P.rows)
-                    P.y[(size_t)(p0 + j) * P.rows + row + q] = out_val(acc[q], P.bias, P.res, P.rows, p0 + j, row + q);
+                if (row + q < P.rows) P.y[(size_t)j * P.rows + row + q] = out_val(acc[q], P.bias, P.res, P.rows, j, row + q);
         return;
     }
     // Split K: publish the slice's partials with coherent stores, then the
@@ -712,6 +701,199 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
     if (threadIdx.x == 0) __hip_atomic_store(P.counters + rg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---- expert-grouped GEMM (prefill): one workgroup per work item = one
+// expert's run of at most GEMM_GROUP_COLS (X row, Y row) pairs. The item's X
+// rows are loaded once and packed into LDS as hi and lo bf16 fragments
+// (fragment columns [0, M) and [M, 2M)); then each wave streams whole row
+// tiles of the expert (tiles w, w + 8, ...) through the full K, GG_LA
+// blocks of codes in flight across tile boundaries, in whole unguarded
+// rounds (units past the wave's last read zeros and are dropped), and puts
+// each tile's 16 rows x M columns (hi + lo added) into LDS; the workgroup
+// writes Y once at the end, so no global store sits inside the stream to
+// hold up its loads. Items are spread so
+// that consecutive items (one expert's runs) share an XCD and its L2:
+// workgroup b takes item (b % 8) * S + b / 8 with S = ceil(nitems / 8).
+constexpr int GG_WG = 512;
+constexpr int GG_LA = 8;
+struct GemmGroupArgs {
+    const uint8_t* codes;
+    const uint8_t* hp;
+    const uint32_t* params;
+    const float* x;      // [xrows][K]
+    float* y;            // [pairs][rows]
+    const int* rowidx;   // X row of pair p (null: row p)
+    const int* items;    // [3 * n]: expert, first pair, count
+    const int* nitems;
+    size_t ecodes, ehp, eparams;
+    int rows, rows_pad, nb, xrows;
+};
+
+template <int SCHEME>
+__global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
+{
+    __shared__ __align__(16) u32x4 xb[GEMM_GROUP_MAXBK][4][64];
+    __shared__ float psum[GEMM_GROUP_MAXBK][2][16];
+    __shared__ float ys[GEMM_GROUP_COLS][GEMM_GROUP_MAXROWS];
+    const int nitems = *P.nitems;
+    const int S = (nitems + 7) / 8;
+    const int item = (int)(blockIdx.x % 8) * S + (int)(blockIdx.x / 8);
+    if ((int)(blockIdx.x / 8) >= S || item >= nitems) return;  // uniform
+    const int e = P.items[3 * item], p0 = P.items[3 * item + 1], M = P.items[3 * item + 2];
+    const int nb = P.nb, K = nb * 128, Mx = 2 * M;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int g = lane >> 4, j = lane & 15;
+    const int ntiles = P.rows_pad / TILE_ROWS;
+
+    // this wave's units: (tile wave + 8 * (u / nb), block u % nb)
+    const int my_tiles = ntiles > wave ? (ntiles - wave + 7) / 8 : 0;
+    const int nunits = my_tiles * nb;
+    const uint8_t* codes = P.codes + (size_t)e * P.ecodes;
+    const uint8_t* hpl = P.hp + (size_t)e * P.ehp;
+    const uint32_t* params = P.params + (size_t)e * P.eparams;
+    const int nrec = ntiles * nb;
+    const auto crs = buf_rsrc(codes, nrec * (int)CODE_REC);
+    const auto hrs = buf_rsrc(SCHEME == 3 ? hpl : codes, SCHEME == 3 ? nrec * (int)HP_REC : 0);
+    const auto prs = buf_rsrc(params, nrec * TILE_ROWS * 4);
+    u32x4 cr[GG_LA], pr[GG_LA];
+    u32x2 hr[GG_LA];
+    // unit u -> record (tile, block); past the wave's units: an offset past
+    // the range (zeros, never used)
+    auto load_unit = [&](int slot, int u) {
+        const int t = wave + 8 * (u / nb), b = u % nb;
+        const int rec = u < nunits ? t * nb + b : nrec;
+        cr[slot] = __builtin_amdgcn_raw_buffer_load_b128(crs, rec * (int)CODE_REC + lane * 16, 0, CPOL_NT);
+        if constexpr (SCHEME == 3) hr[slot] = __builtin_amdgcn_raw_buffer_load_b64(hrs, rec * (int)HP_REC + lane * 8, 0, CPOL_NT);
+        pr[slot] = __builtin_amdgcn_raw_buffer_load_b128(prs, rec * 64 + g * 16, 0, CPOL_NT);
+    };
+
+    // ---- X: task (row c < M, block blk, half h) loads 64 consecutive k of
+    // X row rowidx[p0 + c] as 16 pieces of 16 bytes (one task per thread)
+    const int ntask = M * nb * 2;
+    const int t = threadIdx.x;
+    const int c = t % M, blk = (t / M) >> 1, h = (t / M) & 1;
+    const int xr = t < ntask ? (P.rowidx ? P.rowidx[p0 + c] : p0 + c) : 0;
+    const auto xrs = buf_rsrc(P.x, P.xrows * K * 4);
+    u32x4 xv[16];
+    const int base = t < ntask ? (xr * K + blk * 128 + 64 * h) * 4 : 0x7FFFFFF0;
+#pragma unroll
+    for (int q = 0; q < 16; q++) xv[q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, base + q * 16, 0, 0);
+#pragma unroll
+    for (int u = 0; u < GG_LA; u++) load_unit(u, u);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- pack: hi into fragment column c, lo into column M + c; fragment
+    // (i = 2h + ii, lane group gg) slot s <- piece s, element gg + 4 ii
+    if (t < ntask) {
+        uint32_t ph[8][4], pl[8][4];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const u32x4 a = xv[2 * q], b = xv[2 * q + 1];
+            ph[q][0] = pk_bf16(__uint_as_float(a.x), __uint_as_float(a.y));
+            ph[q][1] = pk_bf16(__uint_as_float(a.z), __uint_as_float(a.w));
+            ph[q][2] = pk_bf16(__uint_as_float(b.x), __uint_as_float(b.y));
+            ph[q][3] = pk_bf16(__uint_as_float(b.z), __uint_as_float(b.w));
+            pl[q][0] = pk_bf16(lo_of(a.x), lo_of(a.y));
+            pl[q][1] = pk_bf16(lo_of(a.z), lo_of(a.w));
+            pl[q][2] = pk_bf16(lo_of(b.x), lo_of(b.y));
+            pl[q][3] = pk_bf16(lo_of(b.z), lo_of(b.w));
+        }
+        float sh = 0.0f, sl = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                sh += bf16_lo(ph[q][d]) + bf16_hi(ph[q][d]);
+                sl += bf16_lo(pl[q][d]) + bf16_hi(pl[q][d]);
+            }
+        psum[blk][h][c] = sh;
+        psum[blk][h][M + c] = sl;
+#pragma unroll
+        for (int ii = 0; ii < 2; ii++)
+#pragma unroll
+            for (int gg = 0; gg < 4; gg++) {
+                const int d = (gg >> 1) + 2 * ii, odd = gg & 1;
+                u32x4 o;
+                o.x = pick_halves(ph[0][d], ph[1][d], odd);
+                o.y = pick_halves(ph[2][d], ph[3][d], odd);
+                o.z = pick_halves(ph[4][d], ph[5][d], odd);
+                o.w = pick_halves(ph[6][d], ph[7][d], odd);
+                xb[blk][2 * h + ii][gg * 16 + c] = o;
+                o.x = pick_halves(pl[0][d], pl[1][d], odd);
+                o.y = pick_halves(pl[2][d], pl[3][d], odd);
+                o.z = pick_halves(pl[4][d], pl[5][d], odd);
+                o.w = pick_halves(pl[6][d], pl[7][d], odd);
+                xb[blk][2 * h + ii][gg * 16 + M + c] = o;
+            }
+    }
+    // zero fragment columns Mx..15 and their sums
+    for (int z = threadIdx.x; z < nb * 2 * (16 - Mx); z += GG_WG) {
+        const int zb = z / (2 * (16 - Mx)), zc = Mx + (z >> 1) % (16 - Mx), zh = z & 1;
+        psum[zb][zh][zc] = 0.0f;
+#pragma unroll
+        for (int ii = 0; ii < 2; ii++)
+#pragma unroll
+            for (int gg = 0; gg < 4; gg++) xb[zb][2 * zh + ii][gg * 16 + zc] = u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+
+    // ---- the unit stream, whole rounds of GG_LA
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    int ub = 0, ut = wave;  // block and tile of the unit being computed
+    const int rounds = (nunits + GG_LA - 1) / GG_LA * GG_LA;
+    for (int u0 = 0; u0 < rounds; u0 += GG_LA) {
+#pragma unroll
+        for (int k = 0; k < GG_LA; k++) {
+            const int u = u0 + k;
+            {
+                bf16x8 B[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const u32x4 w = xb[ub][i][lane];
+                    __builtin_memcpy(&B[i], &w, 16);
+                }
+                const u32x4 U = cr[k];
+                const uint32_t MK = 0x0F0F0F0Fu;
+                u32x4 lo = {U.x & MK, U.y & MK, U.z & MK, U.w & MK};
+                u32x4 hi = {(U.x >> 4) & MK, (U.y >> 4) & MK, (U.z >> 4) & MK, (U.w >> 4) & MK};
+                if constexpr (SCHEME == 3) {
+                    const uint32_t T6 = 0x30303030u, hx = hr[k].x, hy = hr[k].y;
+                    lo.x |= (hx << 4) & T6; lo.y |= (hx << 2) & T6;
+                    lo.z |= (hy << 4) & T6; lo.w |= (hy << 2) & T6;
+                    hi.x |= hx & T6;        hi.y |= (hx >> 2) & T6;
+                    hi.z |= hy & T6;        hi.w |= (hy >> 2) & T6;
+                }
+                f32x4 D = {0.f, 0.f, 0.f, 0.f};
+                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(lo.x, lo.y), B[0], D, 0, 0, 0);
+                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(lo.z, lo.w), B[1], D, 0, 0, 0);
+                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(hi.x, hi.y), B[2], D, 0, 0, 0);
+                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(hi.z, hi.w), B[3], D, 0, 0, 0);
+                const float Sx = psum[ub][0][j] + psum[ub][1][j];
+                const u32x4 pp = pr[k];
+                acc[0] = __builtin_fmaf(zp_off(pp.x), Sx, __builtin_fmaf(h2f(pp.x >> 16), D[0], acc[0]));
+                acc[1] = __builtin_fmaf(zp_off(pp.y), Sx, __builtin_fmaf(h2f(pp.y >> 16), D[1], acc[1]));
+                acc[2] = __builtin_fmaf(zp_off(pp.z), Sx, __builtin_fmaf(h2f(pp.z >> 16), D[2], acc[2]));
+                acc[3] = __builtin_fmaf(zp_off(pp.w), Sx, __builtin_fmaf(h2f(pp.w >> 16), D[3], acc[3]));
+                load_unit(k, u + GG_LA);
+                if (++ub == nb) {  // the tile is complete: hi + lo into LDS, next tile
+#pragma unroll
+                    for (int q = 0; q < 4; q++) acc[q] += __shfl(acc[q], lane + M);
+                    if (ut < ntiles && j < M)
+#pragma unroll
+                        for (int q = 0; q < 4; q++) ys[j][ut * TILE_ROWS + 4 * g + q] = acc[q];
+                    acc = f32x4{0.f, 0.f, 0.f, 0.f};
+                    ub = 0;
+                    ut += 8;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < M * P.rows; i += GG_WG) {
+        const int jj = i / P.rows, r = i % P.rows;
+        P.y[(size_t)(p0 + jj) * P.rows + r] = ys[jj][r];
+    }
+}
+
 template <int SCHEME, bool SPLIT>
 hipError_t launch_nt(int nt, dim3 grid, hipStream_t s, const GemmArgs& a)
 {
@@ -731,9 +913,9 @@ hipError_t launch_nt(int nt, dim3 grid, hipStream_t s, const GemmArgs& a)
 template <int SCHEME>
 void launch_small(int x_mode, dim3 grid, hipStream_t s, const GemmSmallArgs& a)
 {
-    if (x_mode == GX_BF16) hipLaunchKernelGGL((k_gemm_small<SCHEME, true, false, false>), grid, dim3(GS_WG), 0, s, a);
-    else if (x_mode == GX_SPLIT) hipLaunchKernelGGL((k_gemm_small<SCHEME, false, true, false>), grid, dim3(GS_WG), 0, s, a);
-    else hipLaunchKernelGGL((k_gemm_small<SCHEME, false, false, false>), grid, dim3(GS_WG), 0, s, a);
+    if (x_mode == GX_BF16) hipLaunchKernelGGL((k_gemm_small<SCHEME, true, false>), grid, dim3(GS_WG), 0, s, a);
+    else if (x_mode == GX_SPLIT) hipLaunchKernelGGL((k_gemm_small<SCHEME, false, true>), grid, dim3(GS_WG), 0, s, a);
+    else hipLaunchKernelGGL((k_gemm_small<SCHEME, false, false>), grid, dim3(GS_WG), 0, s, a);
 }
 
 }  // namespace
@@ -816,13 +998,13 @@ hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, 
     const int ntiles = split ? 2 * ((M + 15) / 16) : NT;
     dim3 pgrid((unsigned)(nb * ntiles));
     if (x_mode == GX_BF16)
-        hipLaunchKernelGGL((k_gemm_pack<true, false>), pgrid, dim3(256), 0, s, x, M, (int)m.cols, ntiles,
+        hipLaunchKernelGGL((k_gemm_pack<true, false>), pgrid, dim3(256), 0, s, x, M, (int)m.cols, ntiles, ntiles,
                            reinterpret_cast<u32x4*>(w.xf), w.xsum);
     else if (split)
-        hipLaunchKernelGGL((k_gemm_pack<false, true>), pgrid, dim3(256), 0, s, x, M, (int)m.cols, ntiles,
+        hipLaunchKernelGGL((k_gemm_pack<false, true>), pgrid, dim3(256), 0, s, x, M, (int)m.cols, ntiles, ntiles,
                            reinterpret_cast<u32x4*>(w.xf), w.xsum);
     else
-        hipLaunchKernelGGL((k_gemm_pack<false, false>), pgrid, dim3(256), 0, s, x, M, (int)m.cols, ntiles,
+        hipLaunchKernelGGL((k_gemm_pack<false, false>), pgrid, dim3(256), 0, s, x, M, (int)m.cols, ntiles, ntiles,
                            reinterpret_cast<u32x4*>(w.xf), w.xsum);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -842,26 +1024,61 @@ hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, 
     a.nb = nb;
     a.M = M;
     a.kg = w.kg;
+    a.xt = ntiles;
     dim3 grid((unsigned)(gemm_row_groups(m.rows) * w.kg));
     if (split) return m.scheme == 4 ? launch_nt<4, true>(ntiles, grid, s, a) : launch_nt<3, true>(ntiles, grid, s, a);
     return m.scheme == 4 ? launch_nt<4, false>(ntiles, grid, s, a) : launch_nt<3, false>(ntiles, grid, s, a);
 }
 
+hipError_t launch_gemm_pack_rows(const float* x, int M, int K, void* xf, float* xsum, hipStream_t s)
+{
+    if (M < 1 || K % 128) return hipErrorInvalidValue;
+    const int xt = gemm_rows_tiles(M);
+    (void)hipGetLastError();
+    hipLaunchKernelGGL((k_gemm_pack<false, true>), dim3((unsigned)(K / 128 * xt)), dim3(256), 0, s, x, M, K, xt, 4,
+                       reinterpret_cast<u32x4*>(xf), xsum);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const float* xsum, int M, const float* bias,
+                                   const float* res, float* y, hipStream_t s)
+{
+    if (M < 1 || m.nb == 0) return hipErrorInvalidValue;
+    (void)hipGetLastError();
+    GemmArgs a{};
+    a.codes = m.codes;
+    a.hp = m.hp;
+    a.params = m.params;
+    a.xf = static_cast<const u32x4*>(xf);
+    a.xsum = xsum;
+    a.y = y;
+    a.bias = bias;
+    a.res = res;
+    a.rows = (int)m.rows;
+    a.rows_pad = (int)m.rows_pad;
+    a.nb = (int)m.nb;
+    a.M = M;
+    a.kg = 1;
+    a.xt = gemm_rows_tiles(M);
+    a.rgs = gemm_row_groups(m.rows);
+    a.rgs8 = (a.rgs + 7) / 8 * 8;
+    dim3 grid((unsigned)(a.rgs8 * (a.xt / 4)));
+    return m.scheme == 4 ? launch_nt<4, true>(4, grid, s, a) : launch_nt<3, true>(4, grid, s, a);
+}
+
 hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, int xrows, const int* rowidx, const int* items,
                                const int* nitems, int max_items, float* y, hipStream_t s)
 {
-    if (m.nb == 0 || m.nb > (uint64_t)GEMM_SMALL_MAXBK || xrows < 1 || max_items < 1) return hipErrorInvalidValue;
+    if (m.nb == 0 || m.nb > (uint64_t)GEMM_GROUP_MAXBK || m.rows_pad > (uint64_t)GEMM_GROUP_MAXROWS || xrows < 1 ||
+        max_items < 1)
+        return hipErrorInvalidValue;
     (void)hipGetLastError();
-    GemmSmallArgs a{};
+    GemmGroupArgs a{};
     a.codes = m.codes;
     a.hp = m.hp;
     a.params = m.params;
     a.x = x;
     a.y = y;
-    a.rows = (int)m.rows;
-    a.rows_pad = (int)m.rows_pad;
-    a.nb = (int)m.nb;
-    a.kg = 1;
     a.rowidx = rowidx;
     a.items = items;
     a.nitems = nitems;
@@ -869,11 +1086,13 @@ hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, int xrows,
     a.ecodes = tiles * m.nb * CODE_REC;
     a.ehp = m.scheme == 3 ? tiles * m.nb * HP_REC : 0;
     a.eparams = tiles * m.nb * TILE_ROWS;
+    a.rows = (int)m.rows;
+    a.rows_pad = (int)m.rows_pad;
+    a.nb = (int)m.nb;
     a.xrows = xrows;
-    a.rgs = gemm_small_row_groups(m.rows);
-    dim3 grid((unsigned)(a.rgs * max_items));
-    if (m.scheme == 4) hipLaunchKernelGGL((k_gemm_small<4, false, true, true>), grid, dim3(GS_WG), 0, s, a);
-    else hipLaunchKernelGGL((k_gemm_small<3, false, true, true>), grid, dim3(GS_WG), 0, s, a);
+    dim3 grid((unsigned)((max_items + 7) / 8 * 8));
+    if (m.scheme == 4) hipLaunchKernelGGL(k_gemm_grouped<4>, grid, dim3(GG_WG), 0, s, a);
+    else hipLaunchKernelGGL(k_gemm_grouped<3>, grid, dim3(GG_WG), 0, s, a);
     return hipGetLastError();
 }
 

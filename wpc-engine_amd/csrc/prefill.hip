@@ -12,32 +12,53 @@
 namespace wpcg {
 namespace {
 
-// R[t][e] = sum_k X[t][k] * W[e][k] for a tile of 16 experts x 16 rows per
-// workgroup: thread (e, t) runs its dot in index order with fused
-// multiply-adds over K chunks of 128 staged in LDS (rows padded by one
-// float, so the 16 rows of a chunk fall in 16 banks).
-constexpr int RT_K = 128;
+// R[t][e] = sum_k X[t][k] * W[e][k] on the fp32 matrix cores: workgroup
+// (16 experts, 16 rows), each of its 4 waves one quarter of K, then the
+// quarters added in order through LDS. Lane (q, r) of a wave reads 16 bytes
+// of X row t0 + r and of W row e0 + r at k0 + 4q; with component i of
+// both, v_mfma_f32_16x16x4_f32 adds X[r][k0 + 4kk + i] * W[c][k0 + 4kk + i]
+// over kk, so four instructions cover k0 .. k0 + 15. Rows past T or E read
+// row 0 and are never written. K % 64 == 0.
+typedef float f32x4v __attribute__((ext_vector_type(4)));
 __global__ __launch_bounds__(256) void k_pf_router(const float* __restrict__ X, const float* __restrict__ W,
                                                    int T, int E, int K, float* __restrict__ R)
 {
-    __shared__ float xs[16][RT_K + 1];
-    __shared__ float ws[16][RT_K + 1];
+    __shared__ f32x4v red[4][64];
     const int e0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
-    const int te = threadIdx.x >> 4, tt = threadIdx.x & 15;
-    float acc = 0.0f;
-    for (int k0 = 0; k0 < K; k0 += RT_K) {
-        for (int i = threadIdx.x; i < 16 * RT_K; i += 256) {
-            const int r = i / RT_K, k = i % RT_K;
-            const bool in = k0 + k < K;
-            xs[r][k] = in && t0 + r < T ? X[(size_t)(t0 + r) * K + k0 + k] : 0.0f;
-            ws[r][k] = in && e0 + r < E ? W[(size_t)(e0 + r) * K + k0 + k] : 0.0f;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
+    const int kq = K / 4, kb = wave * kq;
+    const float4* xp = reinterpret_cast<const float4*>(X + (size_t)(t0 + r < T ? t0 + r : 0) * K + kb + 4 * q);
+    const float4* wp = reinterpret_cast<const float4*>(W + (size_t)(e0 + r < E ? e0 + r : 0) * K + kb + 4 * q);
+    f32x4v d = {0.f, 0.f, 0.f, 0.f};
+    constexpr int U = 4;  // 16-byte loads in flight per operand
+    for (int k = 0; k < kq; k += 16 * U) {
+        float4 a[U], b[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const bool in = k + 16 * u < kq;
+            a[u] = in ? xp[(k + 16 * u) / 4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            b[u] = in ? wp[(k + 16 * u) / 4] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        __syncthreads();
-#pragma unroll 8
-        for (int k = 0; k < RT_K; k++) acc = fmaf(xs[tt][k], ws[te][k], acc);
-        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x, b[u].x, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].y, b[u].y, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].z, b[u].z, d, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w, b[u].w, d, 0, 0, 0);
+        }
     }
-    if (t0 + tt < T && e0 + te < E) R[(size_t)(t0 + tt) * E + e0 + te] = acc;
+    red[wave][lane] = d;
+    __syncthreads();
+    if (wave == 0) {
+        // lane (g, j) holds rows (tokens) 4g..4g+3 of column (expert) j
+        const f32x4v s4 = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+        const int g = lane >> 4, j = lane & 15;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = t0 + 4 * g + i, e = e0 + j;
+            if (t < T && e < E) R[(size_t)t * E + e] = s4[i];
+        }
+    }
 }
 
 // The P = T * top_k pairs q = t * top_k + k, sorted by expert, ties in pair
@@ -62,32 +83,56 @@ __global__ __launch_bounds__(GR_WG) void k_pf_group(const int32_t* __restrict__ 
         else pair_pos[q] = -1;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int o = 0, io = 0;
-        for (int e = 0; e < E; e++) {
-            off[e] = o;
-            ioff[e] = io;
-            o += cnt[e];
-            io += (cnt[e] + GEMM_GROUP_COLS - 1) / GEMM_GROUP_COLS;
-        }
-        *nitems = io;
+    // exclusive prefix sums of the counts and of the item counts (E <= 256:
+    // a Hillis-Steele scan over LDS)
+    const int e_me = threadIdx.x;
+    int c_me = e_me < E ? cnt[e_me] : 0, i_me = (c_me + GEMM_GROUP_COLS - 1) / GEMM_GROUP_COLS;
+    if (e_me < ROUTE_MAXN) {
+        off[e_me] = c_me;
+        ioff[e_me] = i_me;
     }
     __syncthreads();
-    // stable placement: wave w takes experts w, w + 16, ...; a ballot per
-    // 64 pairs gives each match its rank among the earlier matches
+    for (int d = 1; d < ROUTE_MAXN; d <<= 1) {
+        int a = 0, b = 0;
+        if (e_me < ROUTE_MAXN && e_me >= d) {
+            a = off[e_me - d];
+            b = ioff[e_me - d];
+        }
+        __syncthreads();
+        if (e_me < ROUTE_MAXN && e_me >= d) {
+            off[e_me] += a;
+            ioff[e_me] += b;
+        }
+        __syncthreads();
+    }
+    if (e_me < ROUTE_MAXN) {  // inclusive -> exclusive
+        off[e_me] -= c_me;
+        ioff[e_me] -= i_me;
+    }
+    if (e_me == ROUTE_MAXN - 1) *nitems = ioff[e_me] + i_me;
+    __syncthreads();
+    // stable placement: wave w takes experts w, w + 16, ... (at most
+    // ROUTE_MAXN / 16 of them) and walks the pairs 64 at a time; a ballot
+    // per expert gives each match its rank among the earlier matches
+    constexpr int EPW = ROUTE_MAXN / (GR_WG / 64);
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int e = wave; e < E; e += GR_WG / 64) {
-        int run = off[e];
-        for (int q0 = 0; q0 < P; q0 += 64) {
-            const int q = q0 + lane;
-            const bool hit = q < P && sid[q] == e;
+    int run[EPW];
+#pragma unroll
+    for (int u = 0; u < EPW; u++) run[u] = wave + 16 * u < E ? off[wave + 16 * u] : 0;
+    for (int q0 = 0; q0 < P; q0 += 64) {
+        const int q = q0 + lane;
+        const int myid = q < P ? sid[q] : -1;
+#pragma unroll
+        for (int u = 0; u < EPW; u++) {
+            const int e = wave + 16 * u;
+            const bool hit = myid == e;
             const uint64_t mask = __ballot(hit);
             if (hit) {
-                const int at = run + __popcll(mask & ((1ull << lane) - 1));
+                const int at = run[u] + __popcll(mask & ((1ull << lane) - 1));
                 pair_tok[at] = q / top_k;
                 pair_pos[q] = at;
             }
-            run += __popcll(mask);
+            run[u] += __popcll(mask);
         }
     }
     for (int e = threadIdx.x; e < E; e += GR_WG)
@@ -120,6 +165,7 @@ __global__ __launch_bounds__(256) void k_pf_combine(float* __restrict__ X, const
 hipError_t launch_pf_router(const float* X, const float* W, int T, int E, int K, float* R, hipStream_t s)
 {
     (void)hipGetLastError();
+    if (K % 64) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_pf_router, dim3((E + 15) / 16, (T + 15) / 16), dim3(256), 0, s, X, W, T, E, K, R);
     return hipGetLastError();
 }

@@ -199,8 +199,20 @@ hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, 
 // {expert, first pair p0, count <= GEMM_GROUP_COLS}; its column c reads X
 // row rowidx[p0 + c] (null: row p0 + c, X has xrows rows) and writes Y row
 // p0 + c. *nitems (device) items are live; max_items bounds the grid.
-// Needs m.nb <= GEMM_SMALL_MAXBK (one K-slice).
+// Needs m.nb <= GEMM_GROUP_MAXBK (the item's X sits in LDS whole) and
+// m.rows_pad <= GEMM_GROUP_MAXROWS (so does its Y).
 constexpr int GEMM_GROUP_COLS = 8;
+constexpr int GEMM_GROUP_MAXBK = 16;
+constexpr int GEMM_GROUP_MAXROWS = 2048;
+// Many rows of fp32 X in the SPLIT mode as one launch per matrix: X packed
+// once (launch_gemm_pack_rows; the pack serves every matrix with K inputs),
+// then workgroups over (row group, group of 32 rows of X); xf holds
+// K/128 * gemm_rows_tiles(M) * 4 KiB, xsum K/128 * gemm_rows_tiles(M) * 16
+// floats.
+inline int gemm_rows_tiles(int M) { return (M + 31) / 32 * 4; }
+hipError_t launch_gemm_pack_rows(const float* x, int M, int K, void* xf, float* xsum, hipStream_t s);
+hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const float* xsum, int M, const float* bias,
+                                   const float* res, float* y, hipStream_t s);
 hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, int xrows, const int* rowidx, const int* items,
                                const int* nitems, int max_items, float* y, hipStream_t s);
 
