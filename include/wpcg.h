@@ -391,6 +391,22 @@ int wpcg_model_prefill(wpcg_model* m, const uint32_t* tokens, uint32_t n, float*
  * through the batched prefill (enabled, the default) or step by step. No
  * reference counterpart. */
 int wpcg_model_set_prefill(wpcg_model* m, int enabled);
+/* Speculative verification, the hook the reference names as blocked on a
+ * batched pass (WHITEPAPER.md:576-586, 662-693): the n tokens (the last
+ * accepted token, then the drafts) at the next n positions in one batch,
+ * and argmax[i] = the greedy next token after tokens[0..i], which is what
+ * forward_token(tokens[i]) would return at that point. A draft d_{i+1} is
+ * accepted while it equals argmax[i]; wpcg_model_set_position then drops
+ * the rejected positions. logits (may be NULL) receives n rows of vocab
+ * floats. FAST mode: one prefill pass plus the final norm and head as one
+ * batched GEMM over the n rows (within FAST's tolerance of the steps);
+ * EXACT mode: the n steps (bit-identical). 1 <= n <= WPCG_VERIFY_MAX. No
+ * reference counterpart. */
+#define WPCG_VERIFY_MAX 64
+int wpcg_model_verify(wpcg_model* m, const uint32_t* tokens, uint32_t n, uint32_t* argmax, float* logits);
+/* Move the position back to pos (<= the current one): later cache entries
+ * are ignored and overwritten by the next steps. No reference counterpart. */
+int wpcg_model_set_position(wpcg_model* m, uint32_t pos);
 /* Greedy generation from position 0: the prompt, then n_new tokens, each
  * the argmax of the previous step's logits, written to out (n_new ids).
  * Steps run back to back on the device with no host round trip; in FAST

@@ -151,3 +151,47 @@ def test_prefill_errors(ctx):
     m.prefill(np.arange(10, dtype=np.uint32))  # exactly full
     assert m.position() == 40
     m.close()
+
+
+@pytest.mark.parametrize("name,cfg,mode,seed", [("moe-fast", MOE, wpcg.MODE_FAST, 71),
+                                                ("qwen3-moe-2L-fast", QWEN3_MOE_2L, wpcg.MODE_FAST, 72),
+                                                ("dense-exact", DENSE, wpcg.MODE_EXACT, 73)])
+def test_speculative_verify(ctx, name, cfg, mode, seed):
+    """verify([a0, g1 .. g7]) against the greedy steps a0 -> g1 -> ... -> g8:
+    argmax[i] == g[i+1]; a wrong draft changes only what follows it; a
+    rewind to an accepted prefix continues exactly as the steps did."""
+    print(f"[gpu] verify {name}", flush=True)
+    m = build(ctx, cfg, seed, mode)
+    prompt = np.random.default_rng(seed).integers(0, cfg["vocab"], 40).astype(np.uint32)
+    _, a0 = m.prefill(prompt)
+    n = len(prompt)
+    g, step_logits, tok = [], [], a0
+    for _ in range(8):
+        lg, tok = m.forward_token(tok)
+        g.append(tok)
+        step_logits.append(lg)
+    m.set_position(n)
+    drafts = np.array([a0] + g[:7], np.uint32)
+    ids, lg = m.verify(drafts, want_logits=True)
+    assert m.position() == n + 8
+    assert list(ids) == g, f"{name}: {list(ids)} vs {g}"
+    span = float(np.max(step_logits) - np.min(step_logits))
+    err = float(np.max(np.abs(lg - np.array(step_logits)))) / span
+    print(f"[gpu] verify {name}: 8 argmaxes equal the steps, logits {err:.2e} of range", flush=True)
+    if mode == wpcg.MODE_EXACT:
+        assert np.array_equal(lg.view(np.uint32), np.array(step_logits).view(np.uint32))
+    else:
+        assert err <= TOL
+    # a wrong third draft: the first two verdicts stand
+    m.set_position(n)
+    bad = drafts.copy()
+    bad[2] = (int(g[1]) + 1) % cfg["vocab"]
+    ids2, _ = m.verify(bad)
+    assert list(ids2[:2]) == g[:2]
+    # keep a0, g1 (positions n, n+1), drop the rest; g2 goes to n + 2
+    m.set_position(n + 2)
+    _, nxt = m.forward_token(int(g[2]))
+    assert nxt == g[3]
+    with pytest.raises(wpcg.WpcgError):
+        m.set_position(n + 10)  # only backwards
+    m.close()

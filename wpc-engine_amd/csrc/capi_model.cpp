@@ -38,6 +38,8 @@ struct Prefill {
     float *ge = nullptr, *ue = nullptr, *de = nullptr;  // per sorted pair: [P][moe_inter] x2, [P][hidden]
     void* xf = nullptr;       // packed X of the batched GEMMs (launch_gemm_pack_rows)
     float* xsum = nullptr;
+    float* vlogits = nullptr;  // verification: [WPCG_VERIFY_MAX][vocab], made on first use
+    uint32_t* vids = nullptr;  // [WPCG_VERIFY_MAX]
 };
 
 }  // namespace
@@ -404,6 +406,35 @@ int prefill_run(wpcg_model* m, uint32_t pos0, uint32_t n, uint32_t n_prompt)
     DecodeState st{pos0 + n - 1, n_prompt, c.max_pos, 0};
     WPCG_HIP(hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice));
     WPCG_HIP(launch_argmax_next(m->logits, (int)c.vocab, m->st, m->tokens, s));
+    return WPCG_OK;
+}
+
+// FAST verification of tokens[pos0 .. pos0+n-1] (n <= WPCG_VERIFY_MAX <= cap,
+// one pass): every row's logits (final norm, head as one batched GEMM) and
+// argmax; the position ends at pos0 + n with the last argmax as st.last.
+int verify_run(wpcg_model* m, uint32_t pos0, uint32_t n)
+{
+    if (int rc = make_prefill(m)) return rc;
+    const wpcg_model_config& c = m->cfg;
+    Prefill& P = m->pf;
+    hipStream_t s = m->ctx->stream;
+    if (!P.vlogits) {
+        WPCG_HIP(hipMalloc(&P.vlogits, (size_t)WPCG_VERIFY_MAX * c.vocab * 4));
+        m->allocs.push_back(P.vlogits);
+        WPCG_HIP(hipMalloc(&P.vids, WPCG_VERIFY_MAX * 4));
+        m->allocs.push_back(P.vids);
+    }
+    if (int rc = prefill_pass(m, pos0, n, s)) return rc;
+    wpcg_linear* head = c.tied ? m->embed : m->lm_head;
+    WPCG_HIP(launch_rms_norm_rows(WPCG_MODE_FAST, P.x, m->final_norm, (int)c.hidden, (int)n, c.eps, P.xn, s));
+    WPCG_HIP(launch_gemm_pack_rows(P.xn, (int)n, (int)c.hidden, P.xf, P.xsum, s));
+    WPCG_HIP(launch_gemm_packed_rows(head->m, P.xf, P.xsum, (int)n, head->bias, nullptr, P.vlogits, s));
+    WPCG_HIP(launch_argmax_rows(P.vlogits, (int)c.vocab, (int)n, P.vids, s));
+    WPCG_HIP(hipStreamSynchronize(s));
+    uint32_t last = 0;
+    WPCG_HIP(hipMemcpy(&last, P.vids + (n - 1), 4, hipMemcpyDeviceToHost));
+    DecodeState st{pos0 + n, 0xffffffffu, c.max_pos, last};
+    WPCG_HIP(hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice));
     return WPCG_OK;
 }
 
@@ -858,6 +889,53 @@ int wpcg_model_prefill(wpcg_model* m, const uint32_t* tokens, uint32_t n, float*
         WPCG_HIP(hipMemcpy(&st, m->st, sizeof st, hipMemcpyDeviceToHost));
         *argmax = st.last;
     }
+    return WPCG_OK;
+}
+
+int wpcg_model_verify(wpcg_model* m, const uint32_t* tokens, uint32_t n, uint32_t* argmax, float* logits)
+{
+    if (!m || !tokens || !argmax) return fail(WPCG_E_ARG, "null argument");
+    if (n == 0 || n > WPCG_VERIFY_MAX) return fail(WPCG_E_ARG, "verify takes 1.." + std::to_string(WPCG_VERIFY_MAX) + " tokens");
+    for (uint32_t i = 0; i < n; i++)
+        if (tokens[i] >= m->cfg.vocab) return fail(WPCG_E_ARG, "token id out of range");
+    if (int rc = ready(m)) return rc;
+    hipStream_t s = m->ctx->stream;
+    const size_t V = m->cfg.vocab;
+    DecodeState st;
+    WPCG_HIP(hipStreamSynchronize(s));
+    WPCG_HIP(hipMemcpy(&st, m->st, sizeof st, hipMemcpyDeviceToHost));
+    if ((uint64_t)st.pos + n > m->cfg.max_pos) return fail(WPCG_E_ARG, "KV cache full (max_pos reached)");
+    WPCG_HIP(hipMemcpy(m->tokens + st.pos, tokens, (size_t)n * 4, hipMemcpyHostToDevice));
+    const uint32_t pos0 = st.pos;
+    if (m->mode == WPCG_MODE_FAST && m->use_prefill && prefill_ok(m)) {
+        if (int rc = verify_run(m, pos0, n)) return rc;
+        WPCG_HIP(hipMemcpy(argmax, m->pf.vids, (size_t)n * 4, hipMemcpyDeviceToHost));
+        if (logits) WPCG_HIP(hipMemcpy(logits, m->pf.vlogits, (size_t)n * V * 4, hipMemcpyDeviceToHost));
+        return WPCG_OK;
+    }
+    // step by step (EXACT: the reference's steps exactly)
+    st.n_prompt = 0xffffffffu;
+    WPCG_HIP(hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice));
+    for (uint32_t i = 0; i < n; i++) {
+        if (int rc = run_step(m)) return rc;
+        WPCG_HIP(hipStreamSynchronize(s));
+        if (logits) WPCG_HIP(hipMemcpy(logits + i * V, m->logits, V * 4, hipMemcpyDeviceToHost));
+        WPCG_HIP(hipMemcpy(&st, m->st, sizeof st, hipMemcpyDeviceToHost));
+        argmax[i] = st.last;
+    }
+    return WPCG_OK;
+}
+
+int wpcg_model_set_position(wpcg_model* m, uint32_t pos)
+{
+    if (!m) return fail(WPCG_E_ARG, "null model");
+    if (int rc = check_ctx(m->ctx)) return rc;
+    DecodeState st;
+    WPCG_HIP(hipStreamSynchronize(m->ctx->stream));
+    WPCG_HIP(hipMemcpy(&st, m->st, sizeof st, hipMemcpyDeviceToHost));
+    if (pos > st.pos) return fail(WPCG_E_ARG, "set_position only moves back (to drop rejected tokens)");
+    st.pos = pos;
+    WPCG_HIP(hipMemcpy(m->st, &st, sizeof st, hipMemcpyHostToDevice));
     return WPCG_OK;
 }
 

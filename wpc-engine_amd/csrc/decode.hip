@@ -630,12 +630,11 @@ __global__ __launch_bounds__(256) void k_add(float* __restrict__ x, const float*
 
 // ---- argmax (sampling.rs:3-14) and the next step's input -------------------
 // First index of the largest logit (strict >, so NaN never wins; 0 when no
-// logit beats -inf). Then the position advances; a position at or past the
-// prompt gets the argmax as its token.
+// logit beats -inf).
 constexpr int AM_WG = 1024;
-__global__ __launch_bounds__(AM_WG) void k_argmax_next(const float* __restrict__ logits, int n,
-                                                       DecodeState* __restrict__ st,
-                                                       uint32_t* __restrict__ tokens)
+// The first index of the largest of logits[0..n) by the whole workgroup
+// (AM_WG threads), valid in thread 0; -1 when no value beats -inf.
+__device__ int block_argmax(const float* __restrict__ logits, int n)
 {
     __shared__ float sv[AM_WG / 64];
     __shared__ int si[AM_WG / 64];
@@ -677,15 +676,34 @@ __global__ __launch_bounds__(AM_WG) void k_argmax_next(const float* __restrict__
     }
     if ((threadIdx.x & 63) == 0) { sv[threadIdx.x >> 6] = bv; si[threadIdx.x >> 6] = bi; }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x == 0)
         for (int w = 1; w < AM_WG / 64; w++)  // wave 0's result is already in bv, bi
             if (sv[w] > bv || (sv[w] == bv && si[w] < bi)) { bv = sv[w]; bi = si[w]; }
-        const uint32_t next = bv > -INFINITY ? (uint32_t)bi : 0u;
+    return bv > -INFINITY ? bi : -1;
+}
+
+// Then the position advances; a position at or past the prompt gets the
+// argmax (0 when no logit beats -inf) as its token.
+__global__ __launch_bounds__(AM_WG) void k_argmax_next(const float* __restrict__ logits, int n,
+                                                       DecodeState* __restrict__ st,
+                                                       uint32_t* __restrict__ tokens)
+{
+    const int bi = block_argmax(logits, n);
+    if (threadIdx.x == 0) {
+        const uint32_t next = bi >= 0 ? (uint32_t)bi : 0u;
         const uint32_t p = st->pos + 1;
         st->last = next;
         if (p >= st->n_prompt && p <= st->max_pos) tokens[p] = next;
         st->pos = p;
     }
+}
+
+// out[r] = argmax of row r of logits [rows][n] (0 when none beats -inf).
+__global__ __launch_bounds__(AM_WG) void k_argmax_rows(const float* __restrict__ logits, int n,
+                                                       uint32_t* __restrict__ out)
+{
+    const int bi = block_argmax(logits + (size_t)blockIdx.x * n, n);
+    if (threadIdx.x == 0) out[blockIdx.x] = bi >= 0 ? (uint32_t)bi : 0u;
 }
 
 }  // namespace
@@ -773,6 +791,13 @@ hipError_t launch_add(float* x, const float* y, int n, hipStream_t s)
 {
     (void)hipGetLastError();
     hipLaunchKernelGGL(k_add, dim3((n + 255) / 256), dim3(256), 0, s, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_rows(const float* logits, int n, int rows, uint32_t* out, hipStream_t s)
+{
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k_argmax_rows, dim3(rows), dim3(AM_WG), 0, s, logits, n, out);
     return hipGetLastError();
 }
 

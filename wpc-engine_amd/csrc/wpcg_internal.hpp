@@ -310,6 +310,8 @@ hipError_t launch_pf_combine(float* X, const float* D, const float* w, const int
 int linear_gemm(wpcg_linear* L, const float* x, int x_mode, uint32_t M, const float* res, float* y, hipStream_t s);
 hipError_t launch_argmax_next(const float* logits, int n, DecodeState* st, uint32_t* tokens,
                               hipStream_t s);
+// out[r] = the first index of the largest logit of row r (logits [rows][n]).
+hipError_t launch_argmax_rows(const float* logits, int n, int rows, uint32_t* out, hipStream_t s);
 
 // ---- JSON DOM (json.cpp): safetensors headers, their index, config.json ----
 struct JsonValue {

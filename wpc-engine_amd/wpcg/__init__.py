@@ -118,6 +118,8 @@ _SIGS = {
     "wpcg_model_generate": (C.c_int, [_p, _p, C.c_uint32, C.c_uint32, _p, C.POINTER(C.c_float)]),
     "wpcg_model_prefill": (C.c_int, [_p, _p, C.c_uint32, _p, C.POINTER(C.c_uint32)]),
     "wpcg_model_set_prefill": (C.c_int, [_p, C.c_int]),
+    "wpcg_model_verify": (C.c_int, [_p, _p, C.c_uint32, _p, _p]),
+    "wpcg_model_set_position": (C.c_int, [_p, C.c_uint32]),
     "wpcg_model_debug_read": (C.c_int, [_p, C.c_int, _p, _u64]),
     "wpcg_rms_norm": (C.c_int, [_p, _p, _p, C.c_uint32, C.c_float, _p, C.c_int, _p]),
     "wpcg_dense_create": (C.c_int, [_p, _p, _u64, _u64, _p, _pp]),
@@ -842,6 +844,19 @@ class Model:
         check(lib.wpcg_model_prefill(self.h, _np_ptr(t), t.size, None if logits is None else _np_ptr(logits),
                                      C.byref(a)))
         return logits, a.value
+
+    def verify(self, tokens, want_logits: bool = False):
+        """(argmax after each token uint32[n], logits [n][vocab] or None)."""
+        t = np.ascontiguousarray(tokens, np.uint32)
+        ids = np.empty(t.size, np.uint32)
+        logits = np.empty((t.size, self.cfg.vocab), np.float32) if want_logits else None
+        check(lib.wpcg_model_verify(self.h, _np_ptr(t), t.size, _np_ptr(ids),
+                                    None if logits is None else _np_ptr(logits)))
+        return ids, logits
+
+    def set_position(self, pos: int):
+        check(lib.wpcg_model_set_position(self.h, pos))
+        return self
 
     def set_prefill(self, enabled: bool):
         check(lib.wpcg_model_set_prefill(self.h, int(bool(enabled))))
