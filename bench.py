@@ -131,6 +131,21 @@ def decode_bench(ctx, wpcg, synth, n_prompt, n_new, cpu_tokens, eager=False):
         out[key] = ((n - 1) / (ms / 1e3), ms / (n - 1), ids)
         log(f"decode {key}: {out[key][0]:.1f} tok/s ({out[key][1]:.3f} ms/token, {n - 1} steps)")
     same = int(np.argmax(np.concatenate([out["fast"][2][:16] != out["exact"][2], [True]])))
+    # the prompt alone: batched prefill (FAST) against the same tokens step
+    # by step, each timed from an empty cache to the last token's logits
+    model.set_mode(wpcg.MODE_FAST)
+    pre = {}
+    for key, batched in (("batched", True), ("steps", False)):
+        model.set_prefill(batched)
+        model.reset()
+        model.prefill(prompt, want_logits=False)  # warm-up
+        model.reset()
+        t1 = time.perf_counter()
+        _, first = model.prefill(prompt, want_logits=False)
+        pre[key] = (time.perf_counter() - t1, first)
+    model.set_prefill(True)
+    log(f"prefill of {n_prompt} tokens: batched {pre['batched'][0] * 1e3:.1f} ms, "
+        f"step by step {pre['steps'][0] * 1e3:.1f} ms")
     tok_bytes = decode_token_bytes(cfg)
     rec = {
         "model": "Qwen3-30B-A3B-shaped, v4 (48 layers, hidden 2048, 32q/4kv x 128, 128 experts top-8, "
@@ -141,6 +156,10 @@ def decode_bench(ctx, wpcg, synth, n_prompt, n_new, cpu_tokens, eager=False):
         "tok_s": round(out["fast"][0], 2),
         "ms_per_token": round(out["fast"][1], 4),
         "exact_tok_s": round(out["exact"][0], 2),
+        "prefill": {"tokens": int(n_prompt), "ms": round(pre["batched"][0] * 1e3, 2),
+                    "tok_s": round(n_prompt / pre["batched"][0], 1),
+                    "stepwise_ms": round(pre["steps"][0] * 1e3, 2),
+                    "first_token_equal_stepwise": bool(pre["batched"][1] == pre["steps"][1])},
         "fast_ids_equal_exact_first16": same,
         "weight_bytes_per_token": tok_bytes,
         "roofline_tok_s": round(PEAK_GBPS * 1e9 / tok_bytes, 1),
