@@ -517,18 +517,32 @@ __global__ __launch_bounds__(FA_WG) void k_pf_attention(const float* __restrict_
     const float* vb = vc + (size_t)j * max_pos * HD;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 
-    float4 kr[NKV], vr[NKV];
-    auto load_block = [&](int t0) {
-#pragma unroll
-        for (int u = 0; u < NKV; u++) {
-            const int i = threadIdx.x + u * FA_WG, tt = t0 + i / HD4, d = 4 * (i % HD4);
-            if (tt < n) {
-                kr[u] = *reinterpret_cast<const float4*>(kb + (size_t)tt * HD + d);
-                vr[u] = *reinterpret_cast<const float4*>(vb + (size_t)tt * HD + d);
-            }
-        }
-    };
-    load_block(0);
+    // rows past the last position read row n - 1 (never stored to LDS), so
+    // every load is unconditional
+    // (named registers rather than an array, which the compiler kept in
+    // scratch memory here)
+    static_assert(NKV <= 4, "at most four 16-byte loads per thread and block");
+    float4 kr0, kr1, kr2, kr3, vr0, vr1, vr2, vr3;
+#define PF_LOAD_U(U, T0, KR, VR)                                                                    \
+    if constexpr (U < NKV) {                                                                        \
+        const int i = threadIdx.x + U * FA_WG, tt = min((T0) + i / HD4, n - 1), d = 4 * (i % HD4); \
+        KR = *reinterpret_cast<const float4*>(kb + (size_t)tt * HD + d);                           \
+        VR = *reinterpret_cast<const float4*>(vb + (size_t)tt * HD + d);                           \
+    }
+#define PF_LOAD_BLOCK(T0)             \
+    PF_LOAD_U(0, T0, kr0, vr0)         \
+    PF_LOAD_U(1, T0, kr1, vr1)         \
+    PF_LOAD_U(2, T0, kr2, vr2)         \
+    PF_LOAD_U(3, T0, kr3, vr3)
+#define PF_STORE_U(U, KR, VR)                                                \
+    if constexpr (U < NKV) {                                                 \
+        const int i = threadIdx.x + U * FA_WG, tt = i / HD4, dd = 4 * (i % HD4); \
+        if (tt < nt) {                                                       \
+            *reinterpret_cast<float4*>(&ks[tt][dd]) = KR;                    \
+            *reinterpret_cast<float4*>(&vs[tt][dd]) = VR;                    \
+        }                                                                    \
+    }
+    PF_LOAD_BLOCK(0)
     for (int i = threadIdx.x; i < n_rep * HD; i += FA_WG)
         qs[i / HD][i % HD] = Q[((size_t)t * nh + j * n_rep) * HD + i];
     if (threadIdx.x < FA_MAXREP) {
@@ -544,16 +558,14 @@ __global__ __launch_bounds__(FA_WG) void k_pf_attention(const float* __restrict_
 
     for (int t0 = 0; t0 < n; t0 += FA_C) {
         const int nt = min(FA_C, n - t0);
-#pragma unroll
-        for (int u = 0; u < NKV; u++) {
-            const int i = threadIdx.x + u * FA_WG, tt = i / HD4, dd = 4 * (i % HD4);
-            if (tt < nt) {
-                *reinterpret_cast<float4*>(&ks[tt][dd]) = kr[u];
-                *reinterpret_cast<float4*>(&vs[tt][dd]) = vr[u];
-            }
-        }
+        PF_STORE_U(0, kr0, vr0)
+        PF_STORE_U(1, kr1, vr1)
+        PF_STORE_U(2, kr2, vr2)
+        PF_STORE_U(3, kr3, vr3)
         __syncthreads();
-        if (t0 + FA_C < n) load_block(t0 + FA_C);
+        if (t0 + FA_C < n) {
+            PF_LOAD_BLOCK(t0 + FA_C)
+        }
         for (int i = threadIdx.x; i < n_rep * FA_C; i += FA_WG) {
             const int r = i / FA_C, tt = i % FA_C;
             float dot = -INFINITY;
@@ -620,6 +632,9 @@ __global__ __launch_bounds__(FA_WG) void k_pf_attention(const float* __restrict_
         if (u < nper && r0 + u < n_rep)
             O[((size_t)t * nh + j * n_rep + r0 + u) * HD + d] = __fdiv_rn(o[u], s_l[r0 + u]);
 }
+#undef PF_LOAD_BLOCK
+#undef PF_LOAD_U
+#undef PF_STORE_U
 
 // x[i] += y[i] (residual updates the GEMV epilogues do not cover)
 __global__ __launch_bounds__(256) void k_add(float* __restrict__ x, const float* __restrict__ y, int n)

@@ -756,14 +756,19 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
     const auto prs = buf_rsrc(params, nrec * TILE_ROWS * 4);
     u32x4 cr[GG_LA], pr[GG_LA];
     u32x2 hr[GG_LA];
-    // unit u -> record (tile, block); past the wave's units: an offset past
-    // the range (zeros, never used)
-    auto load_unit = [&](int slot, int u) {
-        const int t = wave + 8 * (u / nb), b = u % nb;
-        const int rec = u < nunits ? t * nb + b : nrec;
+    // units are requested in order: the next one's record is (lt, lb), its
+    // tile and block; past the wave's units the record index runs past the
+    // range (zeros, never used)
+    int lt = wave, lb = 0;
+    auto load_next = [&](int slot) {
+        const int rec = lt < ntiles ? lt * nb + lb : nrec;
         cr[slot] = __builtin_amdgcn_raw_buffer_load_b128(crs, rec * (int)CODE_REC + lane * 16, 0, CPOL_NT);
         if constexpr (SCHEME == 3) hr[slot] = __builtin_amdgcn_raw_buffer_load_b64(hrs, rec * (int)HP_REC + lane * 8, 0, CPOL_NT);
         pr[slot] = __builtin_amdgcn_raw_buffer_load_b128(prs, rec * 64 + g * 16, 0, CPOL_NT);
+        if (++lb == nb) {
+            lb = 0;
+            lt += 8;
+        }
     };
 
     // ---- X: task (row c < M, block blk, half h) loads 64 consecutive k of
@@ -778,7 +783,7 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
 #pragma unroll
     for (int q = 0; q < 16; q++) xv[q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, base + q * 16, 0, 0);
 #pragma unroll
-    for (int u = 0; u < GG_LA; u++) load_unit(u, u);
+    for (int u = 0; u < GG_LA; u++) load_next(u);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- pack: hi into fragment column c, lo into column M + c; fragment
@@ -836,55 +841,64 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
     }
     __syncthreads();
 
-    // ---- the unit stream, whole rounds of GG_LA
+    // ---- the unit stream, whole rounds of GG_LA, two units at a time (two
+    // independent matrix-core chains, then their epilogues in unit order)
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    int ub = 0, ut = wave;  // block and tile of the unit being computed
+    int ub = 0, ut = wave;  // block and tile of the next unit to finish
+    auto dots = [&](int slot, int blk) -> f32x4 {
+        bf16x8 B[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const u32x4 w = xb[blk][i][lane];
+            __builtin_memcpy(&B[i], &w, 16);
+        }
+        const u32x4 U = cr[slot];
+        const uint32_t MK = 0x0F0F0F0Fu;
+        u32x4 lo = {U.x & MK, U.y & MK, U.z & MK, U.w & MK};
+        u32x4 hi = {(U.x >> 4) & MK, (U.y >> 4) & MK, (U.z >> 4) & MK, (U.w >> 4) & MK};
+        if constexpr (SCHEME == 3) {
+            const uint32_t T6 = 0x30303030u, hx = hr[slot].x, hy = hr[slot].y;
+            lo.x |= (hx << 4) & T6; lo.y |= (hx << 2) & T6;
+            lo.z |= (hy << 4) & T6; lo.w |= (hy << 2) & T6;
+            hi.x |= hx & T6;        hi.y |= (hx >> 2) & T6;
+            hi.z |= hy & T6;        hi.w |= (hy >> 2) & T6;
+        }
+        f32x4 D = {0.f, 0.f, 0.f, 0.f};
+        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(lo.x, lo.y), B[0], D, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(lo.z, lo.w), B[1], D, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(hi.x, hi.y), B[2], D, 0, 0, 0);
+        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(hi.z, hi.w), B[3], D, 0, 0, 0);
+        return D;
+    };
+    auto finish = [&](int slot, const f32x4& D) {
+        const float Sx = psum[ub][0][j] + psum[ub][1][j];
+        const u32x4 pp = pr[slot];
+        acc[0] = __builtin_fmaf(zp_off(pp.x), Sx, __builtin_fmaf(h2f(pp.x >> 16), D[0], acc[0]));
+        acc[1] = __builtin_fmaf(zp_off(pp.y), Sx, __builtin_fmaf(h2f(pp.y >> 16), D[1], acc[1]));
+        acc[2] = __builtin_fmaf(zp_off(pp.z), Sx, __builtin_fmaf(h2f(pp.z >> 16), D[2], acc[2]));
+        acc[3] = __builtin_fmaf(zp_off(pp.w), Sx, __builtin_fmaf(h2f(pp.w >> 16), D[3], acc[3]));
+        if (++ub == nb) {  // the tile is complete: hi + lo into LDS, next tile
+#pragma unroll
+            for (int q = 0; q < 4; q++) acc[q] += __shfl(acc[q], lane + M);
+            if (ut < ntiles && j < M)
+#pragma unroll
+                for (int q = 0; q < 4; q++) ys[j][ut * TILE_ROWS + 4 * g + q] = acc[q];
+            acc = f32x4{0.f, 0.f, 0.f, 0.f};
+            ub = 0;
+            ut += 8;
+        }
+    };
+    static_assert(GG_LA % 2 == 0, "units go in pairs");
     const int rounds = (nunits + GG_LA - 1) / GG_LA * GG_LA;
     for (int u0 = 0; u0 < rounds; u0 += GG_LA) {
 #pragma unroll
-        for (int k = 0; k < GG_LA; k++) {
-            const int u = u0 + k;
-            {
-                bf16x8 B[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const u32x4 w = xb[ub][i][lane];
-                    __builtin_memcpy(&B[i], &w, 16);
-                }
-                const u32x4 U = cr[k];
-                const uint32_t MK = 0x0F0F0F0Fu;
-                u32x4 lo = {U.x & MK, U.y & MK, U.z & MK, U.w & MK};
-                u32x4 hi = {(U.x >> 4) & MK, (U.y >> 4) & MK, (U.z >> 4) & MK, (U.w >> 4) & MK};
-                if constexpr (SCHEME == 3) {
-                    const uint32_t T6 = 0x30303030u, hx = hr[k].x, hy = hr[k].y;
-                    lo.x |= (hx << 4) & T6; lo.y |= (hx << 2) & T6;
-                    lo.z |= (hy << 4) & T6; lo.w |= (hy << 2) & T6;
-                    hi.x |= hx & T6;        hi.y |= (hx >> 2) & T6;
-                    hi.z |= hy & T6;        hi.w |= (hy >> 2) & T6;
-                }
-                f32x4 D = {0.f, 0.f, 0.f, 0.f};
-                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(lo.x, lo.y), B[0], D, 0, 0, 0);
-                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(lo.z, lo.w), B[1], D, 0, 0, 0);
-                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(hi.x, hi.y), B[2], D, 0, 0, 0);
-                D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(hi.z, hi.w), B[3], D, 0, 0, 0);
-                const float Sx = psum[ub][0][j] + psum[ub][1][j];
-                const u32x4 pp = pr[k];
-                acc[0] = __builtin_fmaf(zp_off(pp.x), Sx, __builtin_fmaf(h2f(pp.x >> 16), D[0], acc[0]));
-                acc[1] = __builtin_fmaf(zp_off(pp.y), Sx, __builtin_fmaf(h2f(pp.y >> 16), D[1], acc[1]));
-                acc[2] = __builtin_fmaf(zp_off(pp.z), Sx, __builtin_fmaf(h2f(pp.z >> 16), D[2], acc[2]));
-                acc[3] = __builtin_fmaf(zp_off(pp.w), Sx, __builtin_fmaf(h2f(pp.w >> 16), D[3], acc[3]));
-                load_unit(k, u + GG_LA);
-                if (++ub == nb) {  // the tile is complete: hi + lo into LDS, next tile
-#pragma unroll
-                    for (int q = 0; q < 4; q++) acc[q] += __shfl(acc[q], lane + M);
-                    if (ut < ntiles && j < M)
-#pragma unroll
-                        for (int q = 0; q < 4; q++) ys[j][ut * TILE_ROWS + 4 * g + q] = acc[q];
-                    acc = f32x4{0.f, 0.f, 0.f, 0.f};
-                    ub = 0;
-                    ut += 8;
-                }
-            }
+        for (int k = 0; k < GG_LA; k += 2) {
+            const int b1 = ub + 1 == nb ? 0 : ub + 1;  // the second unit's block
+            const f32x4 D0 = dots(k, ub), D1 = dots(k + 1, b1);
+            finish(k, D0);
+            finish(k + 1, D1);
+            load_next(k);
+            load_next(k + 1);
         }
     }
     __syncthreads();
