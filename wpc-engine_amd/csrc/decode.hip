@@ -31,16 +31,46 @@ __device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
 // out_i = x_i * scale * w_i. One workgroup of NW threads.
 constexpr int NW = 256;
 
+// ((0 + v0^2) + v1^2) + ... in index order with separate roundings, by one
+// thread. Sixteen values are requested ahead of the sixteen being added, so
+// the load latency hides behind the chain of additions; the padding past n
+// adds +0.0, which leaves a sum of squares unchanged.
+__device__ float ordered_sumsq(const float* v, int n)
+{
+    float s = 0.0f;
+    if (((uintptr_t)v & 15) != 0) {
+        for (int i = 0; i < n; i++) s = __fadd_rn(s, __fmul_rn(v[i], v[i]));
+        return s;
+    }
+    const float4* v4 = reinterpret_cast<const float4*>(v);
+    const int n4 = n >> 2;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 cur[4], nxt[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) cur[u] = u < n4 ? v4[u] : z;
+    for (int c = 0; c < n4; c += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) nxt[u] = c + 4 + u < n4 ? v4[c + 4 + u] : z;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            s = __fadd_rn(s, __fmul_rn(cur[u].x, cur[u].x));
+            s = __fadd_rn(s, __fmul_rn(cur[u].y, cur[u].y));
+            s = __fadd_rn(s, __fmul_rn(cur[u].z, cur[u].z));
+            s = __fadd_rn(s, __fmul_rn(cur[u].w, cur[u].w));
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) cur[u] = nxt[u];
+    }
+    for (int i = n4 * 4; i < n; i++) s = __fadd_rn(s, __fmul_rn(v[i], v[i]));
+    return s;
+}
+
 template <int MODE>
 __device__ float sum_squares(const float* x, int n, float* red)
 {
     __shared__ float s_total;
     if (MODE == WPCG_MODE_EXACT) {
-        if (threadIdx.x == 0) {
-            float s = 0.0f;
-            for (int i = 0; i < n; i++) s = __fadd_rn(s, __fmul_rn(x[i], x[i]));
-            s_total = s;
-        }
+        if (threadIdx.x == 0) s_total = ordered_sumsq(x, n);
     } else {
         float s = 0.0f;
         for (int i = threadIdx.x; i < n; i += blockDim.x) s = fmaf(x[i], x[i], s);
@@ -68,7 +98,7 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
 {
     x += (size_t)blockIdx.x * n;  // row blockIdx.x of a batch (one row: 0)
     out += (size_t)blockIdx.x * n;
-    __shared__ float xs[RN_LDS];
+    __shared__ __align__(16) float xs[RN_LDS];
     __shared__ float red[NW / 64];
     __shared__ float s_total;
     const bool staged = n <= RN_LDS;
@@ -81,11 +111,7 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
     }
     if (MODE == WPCG_MODE_EXACT) {
         __syncthreads();
-        if (threadIdx.x == 0) {
-            float s = 0.0f;
-            for (int i = 0; i < n; i++) s = __fadd_rn(s, __fmul_rn(src[i], src[i]));
-            s_total = s;
-        }
+        if (threadIdx.x == 0) s_total = ordered_sumsq(src, n);
     } else {
         part = wave_sum(part);
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = part;

@@ -45,6 +45,69 @@ __global__ __launch_bounds__(64) void k_dense_exact(const float* __restrict__ w,
     if (r < out_f) y[r] = bias ? __fadd_rn(acc, bias[r]) : acc;
 }
 
+// The same sums for in_f % 4 == 0, sixteen rows per workgroup: the whole
+// workgroup stages K chunks of the rows (and of x) into LDS, double
+// buffered, while lanes 0..15 of wave 0 run their rows' index-order chains
+// from LDS (rows padded by four floats: the sixteen rows' 16-byte reads hit
+// distinct banks).
+constexpr int DE_ROWS = 16, DE_K = 512;
+__global__ __launch_bounds__(256) void k_dense_exact_lds(const float* __restrict__ w,
+                                                        const float* __restrict__ x,
+                                                        const float* __restrict__ bias,
+                                                        float* __restrict__ y, int out_f, int in_f)
+{
+    __shared__ __align__(16) float ws[2][DE_ROWS][DE_K + 4];
+    __shared__ __align__(16) float xs[2][DE_K];
+    const int r0 = blockIdx.x * DE_ROWS, t = threadIdx.x;
+    const int nch = (in_f + DE_K - 1) / DE_K;
+    constexpr int PER = DE_ROWS * DE_K / 4 / 256;  // 16-byte loads of W per thread and chunk
+    float4 st[PER];
+    float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
+    auto load = [&](int c) {
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int idx = t + 256 * u, rr = idx / (DE_K / 4), k = c * DE_K + 4 * (idx % (DE_K / 4));
+            const int row = min(r0 + rr, out_f - 1);
+            st[u] = k < in_f ? *reinterpret_cast<const float4*>(w + (size_t)row * in_f + k)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (t < DE_K / 4) {
+            const int k = c * DE_K + 4 * t;
+            xv = k < in_f ? *reinterpret_cast<const float4*>(x + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto store = [&](int b) {
+#pragma unroll
+        for (int u = 0; u < PER; u++) {
+            const int idx = t + 256 * u;
+            *reinterpret_cast<float4*>(&ws[b][idx / (DE_K / 4)][4 * (idx % (DE_K / 4))]) = st[u];
+        }
+        if (t < DE_K / 4) *reinterpret_cast<float4*>(&xs[b][4 * t]) = xv;
+    };
+    load(0);
+    store(0);
+    __syncthreads();
+    float acc = 0.0f;
+    for (int c = 0; c < nch; c++) {
+        const int b = c & 1;
+        if (c + 1 < nch) load(c + 1);
+        if (t < DE_ROWS) {
+            const int len = min(DE_K, in_f - c * DE_K);
+            for (int k = 0; k < len; k += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(&ws[b][t][k]);
+                const float4 xx = *reinterpret_cast<const float4*>(&xs[b][k]);
+                acc = __fadd_rn(acc, __fmul_rn(v.x, xx.x));
+                acc = __fadd_rn(acc, __fmul_rn(v.y, xx.y));
+                acc = __fadd_rn(acc, __fmul_rn(v.z, xx.z));
+                acc = __fadd_rn(acc, __fmul_rn(v.w, xx.w));
+            }
+        }
+        if (c + 1 < nch) store(b ^ 1);
+        __syncthreads();
+    }
+    if (t < DE_ROWS && r0 + t < out_f) y[r0 + t] = bias ? __fadd_rn(acc, bias[r0 + t]) : acc;
+}
+
 // FAST: one wave per row, 16-byte coalesced loads, fixed-order tree sum
 // (deterministic, not the reference's order). With nw set, x is RMSNorm'd
 // on the fly (norm.rs:4-13): y = W (x * nw) / sqrt(mean(x^2) + eps), the
@@ -301,8 +364,12 @@ hipError_t launch_dense(const float* w, int out_f, int in_f, int mode, const flo
     (void)hipGetLastError();
     if (mode == WPCG_MODE_EXACT) {
         if (nw) return hipErrorInvalidValue;  // EXACT normalises in its own launch
-        hipLaunchKernelGGL(k_dense_exact, dim3((out_f + 63) / 64), dim3(64), 0, s, w, x, bias, y,
-                           out_f, in_f);
+        if (in_f % 4 == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0)
+            hipLaunchKernelGGL(k_dense_exact_lds, dim3((out_f + DE_ROWS - 1) / DE_ROWS), dim3(256), 0, s, w, x,
+                               bias, y, out_f, in_f);
+        else
+            hipLaunchKernelGGL(k_dense_exact, dim3((out_f + 63) / 64), dim3(64), 0, s, w, x, bias, y,
+                               out_f, in_f);
     } else {
         hipLaunchKernelGGL(k_dense_fast, dim3((out_f + 3) / 4), dim3(256), 0, s, w, x, bias, y,
                            out_f, in_f, nw, eps);
