@@ -32,10 +32,10 @@ __device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
 constexpr int NW = 256;
 
 // ((0 + v0^2) + v1^2) + ... in index order with separate roundings, by one
-// thread. Sixteen values are requested ahead of the sixteen being added, so
-// the load latency hides behind the chain of additions; the padding past n
-// adds +0.0, which leaves a sum of squares unchanged.
-__device__ float ordered_sumsq(const float* v, int n)
+// thread. The next sixteen values are requested (clamped in bounds, no
+// branch) before the current sixteen are added, so the load latency hides
+// behind the chain of additions.
+__device__ __forceinline__ float ordered_sumsq(const float* v, int n)
 {
     float s = 0.0f;
     if (((uintptr_t)v & 15) != 0) {
@@ -43,25 +43,27 @@ __device__ float ordered_sumsq(const float* v, int n)
         return s;
     }
     const float4* v4 = reinterpret_cast<const float4*>(v);
-    const int n4 = n >> 2;
-    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 cur[4], nxt[4];
+    const int n4 = n >> 2, nfull = n4 & ~3;  // float4s in whole groups of four
+    if (nfull) {
+        float4 cur[4];
 #pragma unroll
-    for (int u = 0; u < 4; u++) cur[u] = u < n4 ? v4[u] : z;
-    for (int c = 0; c < n4; c += 4) {
+        for (int u = 0; u < 4; u++) cur[u] = v4[u];
+        for (int c = 0; c < nfull; c += 4) {
+            float4 nxt[4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) nxt[u] = c + 4 + u < n4 ? v4[c + 4 + u] : z;
+            for (int u = 0; u < 4; u++) nxt[u] = v4[min(c + 4 + u, n4 - 1)];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-            s = __fadd_rn(s, __fmul_rn(cur[u].x, cur[u].x));
-            s = __fadd_rn(s, __fmul_rn(cur[u].y, cur[u].y));
-            s = __fadd_rn(s, __fmul_rn(cur[u].z, cur[u].z));
-            s = __fadd_rn(s, __fmul_rn(cur[u].w, cur[u].w));
+            for (int u = 0; u < 4; u++) {
+                s = __fadd_rn(s, __fmul_rn(cur[u].x, cur[u].x));
+                s = __fadd_rn(s, __fmul_rn(cur[u].y, cur[u].y));
+                s = __fadd_rn(s, __fmul_rn(cur[u].z, cur[u].z));
+                s = __fadd_rn(s, __fmul_rn(cur[u].w, cur[u].w));
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) cur[u] = nxt[u];
         }
-#pragma unroll
-        for (int u = 0; u < 4; u++) cur[u] = nxt[u];
     }
-    for (int i = n4 * 4; i < n; i++) s = __fadd_rn(s, __fmul_rn(v[i], v[i]));
+    for (int i = nfull * 4; i < n; i++) s = __fadd_rn(s, __fmul_rn(v[i], v[i]));
     return s;
 }
 
@@ -111,7 +113,7 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
     }
     if (MODE == WPCG_MODE_EXACT) {
         __syncthreads();
-        if (threadIdx.x == 0) s_total = ordered_sumsq(src, n);
+        if (threadIdx.x == 0) s_total = staged ? ordered_sumsq(xs, n) : ordered_sumsq(x, n);
     } else {
         part = wave_sum(part);
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = part;
