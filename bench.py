@@ -267,6 +267,27 @@ def gemm_bench(ctx, wpcg, synth, cpu):
     return rec
 
 
+def prefill_trace(wpcg, synth, layers, n_prompt):
+    """Four FAST prefills of the config-3 model cut to `layers` layers, each
+    timed; for rocprofv3 kernel traces of the batched prefill."""
+    import numpy as np
+    cfg = dict(QWEN3_30B_A3B, n_layers=layers)
+    ctx = wpcg.Context(0)
+    model = wpcg.Model(ctx, wpcg.SCHEME_V4, wpcg.ModelConfig(**cfg))
+    for name, arr in synth.model_tensors(cfg, 4, 30, wpcg.encode, share_experts=True):
+        model.set_tensor(name, arr)
+    model.set_mode(wpcg.MODE_FAST)
+    prompt = np.random.default_rng(31).integers(0, cfg["vocab"], n_prompt).astype(np.uint32)
+    for _ in range(4):
+        model.reset()
+        t0 = time.perf_counter()
+        model.prefill(prompt, want_logits=False)
+        log(f"prefill of {n_prompt} tokens, {layers} layers: {(time.perf_counter() - t0) * 1e3:.2f} ms")
+    model.close()
+    ctx.close()
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -290,6 +311,9 @@ def main():
     ap.add_argument("--decode-eager", action="store_true",
                     help="decode steps launch by launch instead of graph replays (for kernel traces)")
     ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM (config 4) lines")
+    ap.add_argument("--prefill-trace", type=int, default=0, metavar="LAYERS",
+                    help="only: build the config-3 model with LAYERS layers and run four FAST prefills "
+                         "of --decode-prompt tokens (for kernel traces), then exit")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -302,6 +326,9 @@ def main():
 
     import wpcg
     from wpcg import synth
+
+    if args.prefill_trace:
+        return prefill_trace(wpcg, synth, args.prefill_trace, args.decode_prompt)
 
     scheme = args.scheme
     mode = wpcg.MODE_EXACT if args.mode == "exact" else wpcg.MODE_FAST

@@ -185,7 +185,10 @@ template <int SCHEME, int NT, bool SPLIT>
 __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
 {
     static_assert(!SPLIT || NT % 2 == 0, "split needs hi and lo tiles");
-    constexpr int NTH = (NT + 1) / 2;          // column tiles of the first half
+    // each wave takes one row tile and every column tile, so a tile's codes
+    // are unpacked once per block
+    constexpr int RT = 1, NTH = NT;
+    static_assert(GM_WG8 / 64 * RT == 4 * GM_RT, "a row group is 8 tiles");
     constexpr int XV = (NT * 4096 + GM_WG8 * 16 - 1) / (GM_WG8 * 16);  // 16-byte X loads per thread per block
     __shared__ __align__(16) u32x4 xb[2][NT * 4 * 64];
     __shared__ float xsb[2][NT * 16];
@@ -210,13 +213,12 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int g = lane >> 4, j = lane & 15;
     const int ntiles = P.rows_pad / TILE_ROWS;
-    const int T0 = (rg * 4 + (wave & 3)) * GM_RT;
-    const int ch = wave >> 2;                   // column half
-    const int n0 = ch * NTH, n1 = ch ? NT : NTH;  // column tiles [n0, n1) (uniform)
+    const int T0 = rg * 8 + wave;
+    const int n0 = 0, n1 = NT;  // column tiles [n0, n1)
 
-    __amdgpu_buffer_rsrc_t crs[GM_RT], hrs[GM_RT], prs[GM_RT];
+    __amdgpu_buffer_rsrc_t crs[RT], hrs[RT], prs[RT];
 #pragma unroll
-    for (int rt = 0; rt < GM_RT; rt++) {
+    for (int rt = 0; rt < RT; rt++) {
         const int T = T0 + rt;
         const bool ok = T < ntiles;
         const size_t rec = (size_t)min(T, ntiles - 1) * nb + b0;
@@ -228,11 +230,11 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
     const auto xrs = buf_rsrc(P.xf + ((size_t)b0 * XT + cg * NT) * 256, (nbl * XT - cg * NT) * 4096);
     const auto srs = buf_rsrc(P.xsum + (size_t)b0 * XT * 16 + cg * NT * 16, (nbl * XT - cg * NT) * 64);
 
-    u32x4 cr[GM_LA][GM_RT], pr[GM_LA][GM_RT];
-    u32x2 hr[GM_LA][GM_RT];
+    u32x4 cr[GM_LA][RT], pr[GM_LA][RT];
+    u32x2 hr[GM_LA][RT];
     auto load_codes = [&](int u, int b) {
 #pragma unroll
-        for (int rt = 0; rt < GM_RT; rt++) {
+        for (int rt = 0; rt < RT; rt++) {
             cr[u][rt] = __builtin_amdgcn_raw_buffer_load_b128(crs[rt], b * (int)CODE_REC + lane * 16, 0, CPOL_NT);
             if constexpr (SCHEME == 3)
                 hr[u][rt] = __builtin_amdgcn_raw_buffer_load_b64(hrs[rt], b * (int)HP_REC + lane * 8, 0, CPOL_NT);
@@ -267,9 +269,9 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
     store_x(0, 0);
     __syncthreads();
 
-    f32x4 acc[GM_RT][NTH];
+    f32x4 acc[RT][NTH];
 #pragma unroll
-    for (int rt = 0; rt < GM_RT; rt++)
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int n = 0; n < NTH; n++) acc[rt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -284,10 +286,10 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
         for (int u = 0; u < GM_LA; u++) {
             const int b = bl + u, buf = u & 1;
             load_x(u, b + GM_LA);
-            bf16x8 A[GM_RT][4];
-            float sc[GM_RT][4], zp[GM_RT][4];
+            bf16x8 A[RT][4];
+            float sc[RT][4], zp[RT][4];
 #pragma unroll
-            for (int rt = 0; rt < GM_RT; rt++) {
+            for (int rt = 0; rt < RT; rt++) {
                 const u32x4 U = cr[u][rt];
                 const uint32_t MK = 0x0F0F0F0Fu;
                 u32x4 lo = {U.x & MK, U.y & MK, U.z & MK, U.w & MK};
@@ -321,16 +323,16 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
                         __builtin_memcpy(&B[i], &w, 16);
                     }
                     const float S = xsb[buf][n * 16 + j];
-                    f32x4 D[GM_RT];
+                    f32x4 D[RT];
 #pragma unroll
-                    for (int rt = 0; rt < GM_RT; rt++) D[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int rt = 0; rt < RT; rt++) D[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int i = 0; i < 4; i++)
 #pragma unroll
-                        for (int rt = 0; rt < GM_RT; rt++)
+                        for (int rt = 0; rt < RT; rt++)
                             D[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[rt][i], B[i], D[rt], 0, 0, 0);
 #pragma unroll
-                    for (int rt = 0; rt < GM_RT; rt++)
+                    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
                         for (int q = 0; q < 4; q++)
                             acc[rt][nn][q] = __builtin_fmaf(zp[rt][q], S, __builtin_fmaf(sc[rt][q], D[rt][q], acc[rt][nn][q]));
@@ -342,31 +344,20 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
         }
     }
 
-    if constexpr (SPLIT) {
-        // every wave is past its last LDS read of X (the loop ends on a barrier)
-        f32x4* ex = reinterpret_cast<f32x4*>(&xb[0][0]);
-        static_assert(sizeof(xb) >= 4 * GM_RT * NTH * 64 * sizeof(f32x4), "hand-over space");
-        if (ch == 1)
+    if constexpr (SPLIT) {  // lo tiles [NT/2, NT) join their hi tiles
 #pragma unroll
-            for (int rt = 0; rt < GM_RT; rt++)
+        for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-                for (int nn = 0; nn < NTH; nn++) ex[(((wave & 3) * GM_RT + rt) * NTH + nn) * 64 + lane] = acc[rt][nn];
-        __syncthreads();
-        if (ch == 0)
-#pragma unroll
-            for (int rt = 0; rt < GM_RT; rt++)
-#pragma unroll
-                for (int nn = 0; nn < NTH; nn++)
-                    acc[rt][nn] = acc[rt][nn] + ex[(((wave & 3) * GM_RT + rt) * NTH + nn) * 64 + lane];
+            for (int n = 0; n < NT / 2; n++) acc[rt][n] = acc[rt][n] + acc[rt][n + NT / 2];
     }
     // the column tiles this wave writes: [c0, c1) (SPLIT: half 0, the hi tiles)
-    const int c0 = SPLIT ? 0 : n0, c1 = SPLIT ? (ch ? 0 : NTH) : n1;
+    const int c0 = 0, c1 = SPLIT ? NT / 2 : NT;
 
     // lane (g, j) holds rows 4g..4g+3 of each tile for column n*16 + j
     const int Mp = NT * 16;
     if (kg == 1) {
 #pragma unroll
-        for (int rt = 0; rt < GM_RT; rt++)
+        for (int rt = 0; rt < RT; rt++)
 #pragma unroll
             for (int nn = 0; nn < NTH; nn++) {
                 const int n = c0 + nn, m = mcol0 + n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
@@ -386,7 +377,7 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
     // coherent loads after it has seen the count.
     const auto prt = buf_rsrc(P.part, kg * Mp * P.rows_pad * 4);
 #pragma unroll
-    for (int rt = 0; rt < GM_RT; rt++)
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int nn = 0; nn < NTH; nn++) {
             const int n = c0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
@@ -405,7 +396,7 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
     __syncthreads();
     if (!s_last) return;
 #pragma unroll
-    for (int rt = 0; rt < GM_RT; rt++)
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int nn = 0; nn < NTH; nn++) {
             const int n = c0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
