@@ -544,16 +544,23 @@ int wpcg_linear_matvec_multi(int n, wpcg_linear* const* lins, const float* const
     }
     if (int rc = check_ctx(ctx)) return rc;
     hipStream_t s = pick(ctx, stream);
-    // FAST members of one scheme share launches of up to MAX_JOBS; EXACT
-    // members run one launch each.
+    // members of one scheme and mode share launches of up to MAX_JOBS
     for (int scheme : {3, 4}) {
-        GemvJob jobs[MAX_JOBS];
-        int nj = 0;
+        GemvJob jobs[MAX_JOBS], ejobs[MAX_JOBS];
+        int nj = 0, ne = 0;
         for (int i = 0; i < n; i++) {
             wpcg_linear* L = lins[i];
             if (L->m.scheme != scheme || L->m.rows == 0) continue;
-            if (L->mode == WPCG_MODE_EXACT || L->m.nb == 0) {
+            if (L->m.nb == 0) {
                 WPCG_HIP(launch_gemv_exact(L->m, xs[i], L->bias, ys[i], s));
+                continue;
+            }
+            if (L->mode == WPCG_MODE_EXACT) {
+                ejobs[ne++] = GemvJob{&L->m, &L->plan, xs[i], L->bias, ys[i]};
+                if (ne == MAX_JOBS) {
+                    WPCG_HIP(launch_gemv_exact_multi(ejobs, ne, s));
+                    ne = 0;
+                }
                 continue;
             }
             jobs[nj++] = GemvJob{&L->m, &L->plan, xs[i], L->bias, ys[i]};
@@ -563,6 +570,7 @@ int wpcg_linear_matvec_multi(int n, wpcg_linear* const* lins, const float* const
             }
         }
         if (nj) WPCG_HIP(launch_gemv_fast(jobs, nj, s));
+        if (ne) WPCG_HIP(launch_gemv_exact_multi(ejobs, ne, s));
     }
     return WPCG_OK;
 }

@@ -98,11 +98,14 @@ int wpcg::moe_run(wpcg_moe* m, const float* x_dev, float* out_dev, const float* 
             jobs[2 * k + 1] = GemvJob{&m->up, &m->plan, x_dev, nullptr, m->u + (size_t)k * I, m->ids, k};
         }
         WPCG_HIP(launch_gemv_fast(jobs, 2 * K, s));
-    } else {
+    } else {  // the chosen experts' gate and up, MAX_JOBS GEMVs per launch
+        GemvJob jobs[2 * MAX_JOBS];
         for (int k = 0; k < K; k++) {
-            WPCG_HIP(launch_gemv_exact(m->gate, x_dev, nullptr, m->g + (size_t)k * I, s, m->ids, k));
-            WPCG_HIP(launch_gemv_exact(m->up, x_dev, nullptr, m->u + (size_t)k * I, s, m->ids, k));
+            jobs[2 * k] = GemvJob{&m->gate, &m->plan, x_dev, nullptr, m->g + (size_t)k * I, m->ids, k};
+            jobs[2 * k + 1] = GemvJob{&m->up, &m->plan, x_dev, nullptr, m->u + (size_t)k * I, m->ids, k};
         }
+        for (int j0 = 0; j0 < 2 * K; j0 += MAX_JOBS)
+            WPCG_HIP(launch_gemv_exact_multi(jobs + j0, std::min(MAX_JOBS, 2 * K - j0), s));
     }
     WPCG_HIP(launch_silu_mul(m->g, m->u, m->h, (size_t)K * I, s));
     // down of the chosen experts, then the weighted sum in chosen order
@@ -113,9 +116,10 @@ int wpcg::moe_run(wpcg_moe* m, const float* x_dev, float* out_dev, const float* 
                               m->ids, k};
         WPCG_HIP(launch_gemv_fast(jobs, K, s));
     } else {
+        GemvJob jobs[MAX_JOBS];
         for (int k = 0; k < K; k++)
-            WPCG_HIP(launch_gemv_exact(m->down, m->h + (size_t)k * I, nullptr, m->ys + (size_t)k * H, s,
-                                       m->ids, k));
+            jobs[k] = GemvJob{&m->down, &m->plan, m->h + (size_t)k * I, nullptr, m->ys + (size_t)k * H, m->ids, k};
+        WPCG_HIP(launch_gemv_exact_multi(jobs, K, s));
     }
     WPCG_HIP(launch_combine(m->ys, m->ids, m->w, K, out_dev, H, add, s));
     return WPCG_OK;

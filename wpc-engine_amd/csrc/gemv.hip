@@ -120,23 +120,20 @@ __device__ __forceinline__ float v3_exact_block(uint2 c, uint32_t h, uint32_t p,
     return acc;
 }
 
-// With `sel` set, the planes stack experts of rows_pad rows each and the
-// GEMV is expert sel[sel_k]'s (a negative id writes y = 0).
+// One 16-row tile (workgroup-local index `tile`) of an EXACT GEMV. With
+// `sel` set, the planes stack experts of rows_pad rows each and the GEMV is
+// expert sel[sel_k]'s (a negative id writes y = 0).
 template <int SCHEME>
-__global__ __launch_bounds__(EX_WG) void k_gemv_exact(const uint8_t* __restrict__ codes,
-                                                      const uint8_t* __restrict__ hp,
-                                                      const uint32_t* __restrict__ params,
-                                                      const float* __restrict__ x,
-                                                      const float* __restrict__ bias,
-                                                      float* __restrict__ y, int rows, int nb,
-                                                      const int32_t* __restrict__ sel, int sel_k,
-                                                      int rows_pad)
+__device__ __forceinline__ void gemv_exact_tile(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ hp,
+                                                const uint32_t* __restrict__ params, const float* __restrict__ x,
+                                                const float* __restrict__ bias, float* __restrict__ y, int rows,
+                                                int nb, const int32_t* __restrict__ sel, int sel_k, int rows_pad,
+                                                int tile, float* xs)
 {
-    __shared__ __align__(16) float xs[EX_SEG * XS_BLK];
     if (sel) {
         const int e = sel[sel_k];
         if (e < 0) {
-            const int r = blockIdx.x * (EX_WG / 8) + (threadIdx.x >> 3);
+            const int r = tile * (EX_WG / 8) + (threadIdx.x >> 3);
             if (r < rows && (threadIdx.x & 7) == 0) y[r] = 0.0f;
             return;
         }
@@ -146,10 +143,10 @@ __global__ __launch_bounds__(EX_WG) void k_gemv_exact(const uint8_t* __restrict_
         params += t0 * TILE_ROWS;
     }
     const int L = threadIdx.x & 7;
-    const int row = blockIdx.x * (EX_WG / 8) + (threadIdx.x >> 3);
+    const int row = tile * (EX_WG / 8) + (threadIdx.x >> 3);
     const bool active = row < rows;
-    const size_t tb = (size_t)blockIdx.x * (size_t)nb;  // this tile's first block record
-    const uint32_t* pp = params + (size_t)blockIdx.x * nb * TILE_ROWS + (row & (TILE_ROWS - 1));
+    const size_t tb = (size_t)tile * (size_t)nb;  // this tile's first block record
+    const uint32_t* pp = params + (size_t)tile * nb * TILE_ROWS + (row & (TILE_ROWS - 1));
     float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += EX_SEG) {
         const int nbs = min(EX_SEG, nb - b0);
@@ -182,6 +179,54 @@ __global__ __launch_bounds__(EX_WG) void k_gemv_exact(const uint8_t* __restrict_
     const float s1 = s4 + __shfl_xor(s4, 1);
     const float r = s1 + __shfl_xor(s1, 2);
     if (active && L == 0) y[row] = bias ? r + bias[row] : r;
+}
+
+template <int SCHEME>
+__global__ __launch_bounds__(EX_WG) void k_gemv_exact(const uint8_t* __restrict__ codes,
+                                                      const uint8_t* __restrict__ hp,
+                                                      const uint32_t* __restrict__ params,
+                                                      const float* __restrict__ x,
+                                                      const float* __restrict__ bias,
+                                                      float* __restrict__ y, int rows, int nb,
+                                                      const int32_t* __restrict__ sel, int sel_k,
+                                                      int rows_pad)
+{
+    __shared__ __align__(16) float xs[EX_SEG * XS_BLK];
+    gemv_exact_tile<SCHEME>(codes, hp, params, x, bias, y, rows, nb, sel, sel_k, rows_pad, blockIdx.x, xs);
+}
+
+// Several EXACT GEMVs (same scheme) in one launch: workgroup w belongs to
+// the problem whose range [wg_begin, next wg_begin) holds it, and runs that
+// problem's tile w - wg_begin exactly as k_gemv_exact would.
+struct ExactProblem {
+    const uint8_t* codes;
+    const uint8_t* hp;
+    const uint32_t* params;
+    const float* x;
+    const float* bias;
+    float* y;
+    const int32_t* sel;
+    int rows, nb, sel_k, rows_pad, wg_begin;
+};
+struct ExactBatch {
+    ExactProblem p[MAX_JOBS];
+    int n;
+};
+static_assert(sizeof(ExactBatch) <= 4096, "kernel arguments of a batched EXACT launch");
+
+template <int SCHEME>
+__global__ __launch_bounds__(EX_WG) void k_gemv_exact_multi(const ExactBatch B)
+{
+    __shared__ __align__(16) float xs[EX_SEG * XS_BLK];
+    const int wgid = blockIdx.x;
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < MAX_JOBS; i++) pi += (i < B.n && wgid >= B.p[i].wg_begin) ? 1 : 0;
+    typedef const __attribute__((address_space(4))) ExactBatch* KargPtr;
+    const KargPtr kargs = (KargPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    const auto& P = kargs->p[pi];
+    gemv_exact_tile<SCHEME>(P.codes, P.hp, P.params, P.x, P.bias, P.y, P.rows, P.nb, P.sel, P.sel_k, P.rows_pad,
+                            wgid - P.wg_begin, xs);
 }
 
 // ============================================================ FAST mode
@@ -930,6 +975,40 @@ hipError_t launch_gemv_exact(const DeviceMatrix& m, const float* x, const float*
     else
         hipLaunchKernelGGL(k_gemv_exact<3>, grid, dim3(EX_WG), 0, s, m.codes, m.hp, m.params, x,
                            bias, y, rows, nb, sel, sel_k, (int)m.rows_pad);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_exact_multi(const GemvJob* jobs, int n, hipStream_t s)
+{
+    if (n <= 0 || n > MAX_JOBS) return hipErrorInvalidValue;
+    ExactBatch B{};
+    B.n = n;
+    int wgs = 0;
+    const int scheme = jobs[0].m->scheme;
+    for (int i = 0; i < n; i++) {
+        const DeviceMatrix& m = *jobs[i].m;
+        if (m.scheme != scheme || m.nb == 0) return hipErrorInvalidValue;
+        ExactProblem& P = B.p[i];
+        P.codes = m.codes;
+        P.hp = m.hp;
+        P.params = m.params;
+        P.x = jobs[i].x;
+        P.bias = jobs[i].bias;
+        P.y = jobs[i].y;
+        P.sel = jobs[i].sel;
+        P.sel_k = jobs[i].sel_k;
+        P.rows = (int)m.rows;
+        P.nb = (int)m.nb;
+        P.rows_pad = (int)m.rows_pad;
+        P.wg_begin = wgs;
+        wgs += (int)(m.rows_pad / (EX_WG / 8));
+    }
+    if (wgs == 0) return hipSuccess;
+    (void)hipGetLastError();  // report only this launch
+    if (scheme == 4)
+        hipLaunchKernelGGL(k_gemv_exact_multi<4>, dim3(wgs), dim3(EX_WG), 0, s, B);
+    else
+        hipLaunchKernelGGL(k_gemv_exact_multi<3>, dim3(wgs), dim3(EX_WG), 0, s, B);
     return hipGetLastError();
 }
 

@@ -147,6 +147,9 @@ hipError_t launch_gemv_exact(const DeviceMatrix& m, const float* x, const float*
 // All jobs must share the scheme. At most MAX_JOBS per launch.
 constexpr int MAX_JOBS = 16;
 hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s);
+// Up to MAX_JOBS EXACT GEMVs of one scheme in one launch (m, x, bias, y,
+// sel, sel_k of each job), each bit-identical to launch_gemv_exact's.
+hipError_t launch_gemv_exact_multi(const GemvJob* jobs, int n, hipStream_t s);
 hipError_t launch_embed(const DeviceMatrix& m, uint32_t row, float* out, hipStream_t s);
 hipError_t launch_dequant(const DeviceMatrix& m, int rounding, float* w, hipStream_t s);
 int fast_kslices(uint64_t rows, uint64_t nb);
