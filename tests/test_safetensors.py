@@ -381,3 +381,29 @@ def test_checkpoint_writer_round_trip(tmp_path):
         art = wpcg.WpcModelDataV4.open(str(d / "wpc"))
         assert art.tensor_count() == len(tensors) - len(fp)
         art.close()
+
+
+def test_json_edge_cases():
+    """The JSON reader behind both formats: escapes, unicode, nesting limit,
+    trailing garbage, duplicate keys (the last one wins, as serde_json's map)."""
+    base = json.loads(QWEN3_JSON)
+    txt = json.dumps(base)
+    # duplicate key: the later value is the one used
+    dup = txt[:-1] + ', "hidden_size": 4096}'
+    assert wpcg.config_from_json_str(dup, 8).hidden == 4096
+    # escapes and non-ASCII text are read, whitespace anywhere
+    odd = json.dumps(dict(base, model_type="qwen3", note="tab\\t \\u00e9 \\ud83d\\ude00 \"q\""), indent=3)
+    assert wpcg.config_from_json_str(odd, 8).hidden == 2560
+    for bad in (txt + " x", txt[:-1], '{"a": [1, 2,]}', '{"a": "\\q"}', '{"a": 01}', "[" * 200 + "]" * 200,
+                '{"vocab_size": 1e400}'):
+        with pytest.raises(wpcg.WpcgError) as e:
+            wpcg.config_from_json_str(bad, 8)
+        assert e.value.code == wpcg.E_FORMAT, bad[:30]
+
+
+def test_deeply_nested_header_is_rejected(tmp_path):
+    h = ('{"a": {"dtype": "F32", "shape": [1], "data_offsets": [0, 4]}, "__metadata__": '
+         + '{"x": ' * 300 + '"y"' + "}" * 300 + "}").encode()
+    p = tmp_path / "deep.safetensors"
+    p.write_bytes(len(h).to_bytes(8, "little") + h + bytes(4))
+    assert rc_of(wpcg.SafetensorsFile.open, p) == wpcg.E_FORMAT
