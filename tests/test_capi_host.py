@@ -167,18 +167,22 @@ def test_fast_split_plan_never_makes_an_empty_slice():
     # address blocks past the end of the matrix) and fit the LDS stage: 64
     # blocks with one 16-row tile per workgroup, 32 with two, 16 with four.
     # Matrices of 32 tiles or more take four tiles when a row has at most 16
-    # blocks, two when it has at most 32; matrices of 512 tiles or more take
-    # two tiles at least. Checked for every block count and requested split.
+    # blocks; of 192 tiles or more, two when it has at most 32; of 128 tiles
+    # or more, two when a row is longer than 64 blocks; of 512 tiles or
+    # more, two tiles at least. Checked for every block count and requested
+    # split.
     def most_of(rows, nb):
         tiles = -(-rows // 16)
         if tiles >= 32 and nb <= 16:
             return 16
-        if tiles >= 32 and nb <= 32:
+        if tiles >= 192 and nb <= 32:
+            return 32
+        if tiles >= 128 and nb > 64:
             return 32
         return 32 if tiles >= 512 else 64
     for nb in range(1, 161):
         for req in [0] + list(range(1, nb + 3)):
-            for rows in (16, 496, 497, 1024, 8176, 8177, 9728, 151936):
+            for rows in (16, 496, 497, 1024, 2032, 2048, 2560, 3056, 3072, 8176, 8177, 9728, 151936):
                 most = most_of(rows, nb)
                 k = wpcg.plan_kslices(rows, nb * 128, req)
                 nbk = -(-nb // k)
@@ -186,10 +190,10 @@ def test_fast_split_plan_never_makes_an_empty_slice():
                 assert (k - 1) * nbk < nb <= k * nbk, (nb, req, k, nbk)
                 if req == 0:
                     # the default: the fewest slices that fit, or, when that
-                    # is more than one, slices of at most half the maximum
+                    # is more than one, slices of at most 32 blocks
                     raw = -(-nb // most)
                     if raw > 1:
-                        raw = -(-nb // (most // 2))
+                        raw = -(-nb // min(most, 32))
                     nbk_raw = -(-nb // raw)
                     assert k == -(-nb // nbk_raw), (nb, rows, k)
     with pytest.raises(wpcg.WpcgError) as e:

@@ -17,10 +17,11 @@
 //   x ~= s_b * Q / 2^21,  s_b = max|x_b| / 127,  Q = rint(x * 127*2^21 / max|x_b|)
 // and Q = d0*2^21 + d1*2^14 + d2*2^7 + d3 with int8 digits d0 = Q >> 21 in
 // [-128,127], d1..d3 in [0,127]. v_mfma_i32_16x16x64_i8 then gives the exact integer
-// dots D_j = sum(code * d_j) for the four digit columns of a 16-row tile,
-// and each block adds
+// dots D_j = sum(code * d_j) of the four digits with each row of a 16-row
+// tile (the digits are the first operand, so one lane receives all four
+// of its row), and each block adds
 //   scale * s_b * (D0 + D1*2^-7 + D2*2^-14 + D3*2^-21) + zp * sum(x_b)
-// to fp32 accumulators (the zp term rides on the idle fifth column). The
+// to the row's fp32 accumulators (the digit sum by Horner's rule). The
 // only approximation is x's representation: the fp32 product x*127*2^21/m
 // (relative 6e-8, as fp32 itself) plus 0.5*s_b*2^-21 = 1.9e-9 * max|x_b|,
 // which keeps the small values of a block that holds an outlier accurate.
@@ -275,6 +276,7 @@ static_assert(sizeof(FastBatch) <= 4096, "kernel arguments of a FAST launch");
 
 constexpr int FAST_WG = 512;        // 8 waves
 constexpr int QB = 8;               // most blocks one wave puts through the matrix cores
+constexpr int MG = 2;               // blocks per branch-free group of the matrix-core loop
 constexpr int NDIG = 4;             // int8 digits per x value
 constexpr int HALF = 4 * NDIG * 16; // fragment bytes per MFMA half: 4 groups x digits x 16
 constexpr int FRAG = 2 * HALF;      // per block
@@ -434,24 +436,16 @@ __device__ __forceinline__ void route_wg(const float* __restrict__ scores, int n
     }
 }
 
-// One row of the block epilogue, branch-free: the digit dot d (lanes of
-// columns 0..3) times scale*s_b, and the zero-point term zp*sum(x_b) (kept
-// by every lane, used from column 4). `p` is zp f16 | scale f16 << 16.
-__device__ __forceinline__ void fast_step(float& acc, float& zacc, int d, uint32_t p, float sb, float Sb)
-{
-    acc = __builtin_fmaf((float)d * sb, h2f(p >> 16), acc);
-    zacc = __builtin_fmaf(h2f(p & 0xFFFFu), Sb, zacc);
-}
-
 // A workgroup of 8 waves computes tw (1 or 2) 16-row tiles over one K-slice
 // of nbl <= 8*QB/tw blocks.
 //   prep:  the slice's x becomes int8 digit fragments in LDS, shared by all
 //          waves; a wave takes two blocks at a time (32 lanes, 4 values each).
 //   dots:  wave w works on tile w / kw (kw = 8/tw waves per tile) over the
 //          contiguous kq-th part of the slice (kq = w % kw), in branch-free
-//          groups of four blocks: a block past the part's end reads zeros
+//          groups of MG blocks: a block past the part's end reads zeros
 //          everywhere and adds exactly 0, and the groups' LDS reads, MFMAs
-//          and scaling overlap.
+//          and scaling overlap (groups of two waste fewer slots on a part
+//          of 5 or 7 blocks than groups of four and measured faster).
 //   sum:   the kw parts of a tile are added in part order (deterministic).
 // Input transforms, applied to x in the prep (FAST mode only):
 //   XF_NORM  x' = x * nw, and the row's result is scaled by
@@ -478,7 +472,7 @@ constexpr int FK_PLAIN = 0, FK_ROUTE = 1, FK_ROUTED = 2;
 template <int SCHEME, int KIND, int XF>
 __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
 {
-    // A wave's last group of four may reach up to 2 blocks past the slice:
+    // A wave's last group of MG may reach up to MG-1 blocks past the slice:
     // those blocks' codes are zero, their digits are never written (any
     // int8 is harmless) and their scales are zeroed below (a stale NaN is not).
     __shared__ __align__(16) int8_t xq[(MAXBK + 4) * FRAG];     // digits of the slice
@@ -747,31 +741,31 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
     __syncthreads();
 
     // ---- matrix-core phase
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    float z0 = 0.f, z1 = 0.f, z2 = 0.f, z3 = 0.f;
+    float acc = 0.f, zacc = 0.f;
     {
         const int lb = kq * q;  // the part's first block within the slice
-        // lanes of columns >= 4 read digit column j&3 (finite, weighted 0 below)
+        // lane (g, j) supplies digit row j&3 of the x operand, so its rows
+        // 4..15 repeat digits 0..3 and every lane group of the result alike
         const int8_t* xf = xq + lb * FRAG + g * (NDIG * 16) + (j & 3) * 16;
         const float2* xsp = xs + lb;
-        const uint32_t* sp = spar[wave] + 4 * g;
+        const uint32_t* sp = spar[wave] + j;
         const uint32_t M = 0x0F0F0F0Fu;
 #pragma unroll
-        for (int i0 = 0; i0 < QB; i0 += 4) {
+        for (int i0 = 0; i0 < QB; i0 += MG) {
             if (i0 < qw) {
                 // this group's LDS operands first, so their latencies overlap
-                v4i B0[4], B1[4];
-                u32x4 pr[4];
-                float2 sc[4];
+                v4i B0[MG], B1[MG];
+                uint32_t pr[MG];
+                float2 sc[MG];
 #pragma unroll
-                for (int u = 0; u < 4; u++) {
+                for (int u = 0; u < MG; u++) {
                     B0[u] = *reinterpret_cast<const v4i*>(xf + (i0 + u) * FRAG);
                     B1[u] = *reinterpret_cast<const v4i*>(xf + (i0 + u) * FRAG + HALF);
-                    pr[u] = *reinterpret_cast<const u32x4*>(sp + (i0 + u) * TILE_ROWS);
+                    pr[u] = sp[(i0 + u) * TILE_ROWS];
                     sc[u] = xsp[i0 + u];
                 }
 #pragma unroll
-                for (int i = i0; i < i0 + 4; i++) {
+                for (int i = i0; i < i0 + MG; i++) {
                     const int u = i - i0;
                     v4i A0, A1;
                     A0.x = c[i].x & M; A0.y = c[i].y & M; A0.z = c[i].z & M; A0.w = c[i].w & M;
@@ -785,33 +779,22 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
                         A1.x |= hx & T6;        A1.y |= (hx >> 2) & T6;
                         A1.z |= hy & T6;        A1.w |= (hy >> 2) & T6;
                     }
+                    // x digits as the first operand: lane (g, j) gets digits
+                    // 0..3 of row j's dot (every lane group alike)
                     v4i d = {0, 0, 0, 0};
-                    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0, B0[u], d, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1, B1[u], d, 0, 0, 0);
-                    fast_step(a0, z0, d.x, pr[u].x, sc[u].x, sc[u].y);
-                    fast_step(a1, z1, d.y, pr[u].y, sc[u].x, sc[u].y);
-                    fast_step(a2, z2, d.z, pr[u].z, sc[u].x, sc[u].y);
-                    fast_step(a3, z3, d.w, pr[u].w, sc[u].x, sc[u].y);
+                    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(B0[u], A0, d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(B1[u], A1, d, 0, 0, 0);
+                    float cd = fmaf((float)d.w, 0x1p-7f, (float)d.z);
+                    cd = fmaf(cd, 0x1p-7f, (float)d.y);
+                    cd = fmaf(cd, 0x1p-7f, (float)d.x);
+                    acc = __builtin_fmaf(cd * sc[u].x, h2f(pr[u] >> 16), acc);
+                    zacc = __builtin_fmaf(h2f(pr[u] & 0xFFFFu), sc[u].y, zacc);
                 }
             }
         }
     }
-    // digit weights 2^(-7j) on columns 0..3, the zero-point sum on column 4,
-    // 0 elsewhere; then the sum over columns 0..7 (rows 4g..4g+3 in lanes
-    // 16g..16g+7)
-    const float wj = j < NDIG ? __builtin_ldexpf(1.0f, -7 * j) : 0.0f;
-    const bool zcol = j == NDIG;
-    a0 = zcol ? z0 : a0 * wj;
-    a1 = zcol ? z1 : a1 * wj;
-    a2 = zcol ? z2 : a2 * wj;
-    a3 = zcol ? z3 : a3 * wj;
-    a0 = sum8(a0); a1 = sum8(a1); a2 = sum8(a2); a3 = sum8(a3);
-    if (j == 0) {
-        red[wave][4 * g + 0] = a0;
-        red[wave][4 * g + 1] = a1;
-        red[wave][4 * g + 2] = a2;
-        red[wave][4 * g + 3] = a3;
-    }
+    // lane (g, j) holds row j's sum over its blocks
+    if (g == 0) red[wave][j] = acc + zacc;
     __syncthreads();
 
     const int t = threadIdx.x;
@@ -955,11 +938,15 @@ int fast_kslices(uint64_t rows, uint64_t nb)
 {
     if (nb == 0) return 1;
     // As few K-slices as fit: a split costs a cross-workgroup handoff. When
-    // a split is needed anyway, slices of half the maximum leave each wave
-    // one group of four blocks, which is faster than two groups.
+    // a split is needed anyway, slices of at most half the largest slice
+    // (measured on 2560x9728: 3 slices of 26 blocks beat 2 of 38 at one
+    // tile per workgroup, and at two tiles 3 slices beat 5).
     const uint64_t mb = fast_max_slice(rows, nb);
     uint64_t kg = (nb + mb - 1) / mb;
-    if (kg > 1) kg = (nb + mb / 2 - 1) / (mb / 2);
+    if (kg > 1) {
+        const uint64_t cap = std::min<uint64_t>(mb, FAST_MAXBK / 2);
+        kg = (nb + cap - 1) / cap;
+    }
     return fast_normalize_kslices(nb, (int)kg);
 }
 

@@ -128,17 +128,20 @@ struct GemvJob {
 // FAST mode: a workgroup computes fast_tiles_per_wg 16-row tiles over a
 // K-slice of at most fast_max_slice blocks (the slice's x digits live in LDS).
 constexpr int FAST_MAXBK = 64;
-// Tiles per workgroup: as many as keep a whole row in one slice (4 tiles
-// for rows of at most 16 blocks, 2 for at most 32) once the matrix has 32
-// tiles, so that each wave streams its full QB blocks and a launch needs
-// fewer workgroups (measured: 11% faster Qwen3-30B-A3B-shaped decode than
-// one tile per workgroup); matrices of 512 tiles or more take 2 tiles
-// even when their rows need a split.
+// Tiles per workgroup: as many as keep a whole row in one slice, so that
+// each wave streams more blocks and a launch needs fewer workgroups: 4 tiles
+// for rows of at most 16 blocks once the matrix has 32 tiles (measured: 11%
+// faster Qwen3-30B-A3B-shaped decode than one tile per workgroup), 2 for
+// rows of at most 32 blocks once it has 192 (a 160-tile matrix of 32-block
+// rows ran 10% faster on 160 workgroups than on 80). Rows longer than one
+// slice take 2 tiles from 128 tiles on (2560x9728: 240 workgroups beat
+// 480), and matrices of 512 tiles or more take 2 in any case.
 inline int fast_tiles_per_wg(uint64_t rows, uint64_t nb)
 {
     const uint64_t tiles = pad_rows(rows) / TILE_ROWS;
     if (tiles >= 32 && nb <= FAST_MAXBK / 4) return 4;
-    if (tiles >= 32 && nb <= FAST_MAXBK / 2) return 2;
+    if (tiles >= 192 && nb <= FAST_MAXBK / 2) return 2;
+    if (tiles >= 128 && nb > FAST_MAXBK) return 2;
     return tiles >= 512 ? 2 : 1;
 }
 inline uint64_t fast_max_slice(uint64_t rows, uint64_t nb) { return FAST_MAXBK / fast_tiles_per_wg(rows, nb); }
