@@ -470,7 +470,10 @@ __device__ __forceinline__ void route_wg(const float* __restrict__ scores, int n
 // launch's problems.
 constexpr int FK_PLAIN = 0, FK_ROUTE = 1, FK_ROUTED = 2;
 template <int SCHEME, int KIND, int XF>
-__global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
+// The plain GEMV asks for 6 waves per SIMD (at most 80 VGPRs): three
+// workgroups per CU instead of two, so a launch of up to 768 workgroups
+// runs in one round (2x9728x2560 v3: 12.5 -> 11.1 us).
+__global__ __launch_bounds__(FAST_WG, XF == XF_NONE ? 6 : 1) void k_gemv_fast(const FastBatch B)
 {
     // A wave's last group of MG may reach up to MG-1 blocks past the slice:
     // those blocks' codes are zero, their digits are never written (any
@@ -535,12 +538,17 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
     // x pair p = wave + 8*i: blocks 2p, 2p+1; lane l holds x[4(l&31) .. +3]
     // of block 2p + (l>>5).
     constexpr int XP = MAXBK / 16;  // pairs per wave
+    // The plain GEMV loads XP0 pairs up front and the rest only when its
+    // slice has them (slices of more than 32 blocks): fewer registers held
+    // across the memory round trip.
+    constexpr int XP0 = 2;
     const auto xrs = buf_rsrc(xp, nbl * 512);
     u32x4 xv[XP], x2v[XP];
     if constexpr (xform != XF_MERGE) {  // (XF_MERGE reads its chunk states in the prep)
 #pragma unroll
         for (int i = 0; i < XP; i++)
-            xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
+            if (XF != XF_NONE || i < XP0)
+                xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
     }
     float wkv[XP];  // routed: the routing weight of each x pair's block
     auto load_x2 = [&]() {  // the second operand of the transform: nw or u
@@ -662,6 +670,8 @@ __global__ __launch_bounds__(FAST_WG) void k_gemv_fast(const FastBatch B)
         for (int i = 0; i < XP; i++) {
             const int p = wave + 8 * i;
             if (2 * p < nbl) {
+                if constexpr (XF == XF_NONE)
+                    if (i >= XP0) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, p * 1024 + lane * 16, 0, 0);
                 if constexpr (xform == XF_MERGE) {
                     const int k = (b0 + 2 * p + hi) * 128 + k0, h = k / P.head_dim;
                     const size_t stride = (size_t)P.n_heads * P.head_dim;
