@@ -42,7 +42,7 @@ BPB = {3: 100, 4: 68}
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (bench.py --pmc-pass) and scaled by
 # the same counters' reading for a copy kernel of known size; see
 # profiles/k_gemv_fast_cfg1_v3_traffic.txt. None where not measured.
-TRAFFIC = {(3, "fast"): 20093248}
+TRAFFIC = {(3, "fast"): 20061794}
 
 
 def log(msg):
@@ -267,6 +267,46 @@ def gemm_bench(ctx, wpcg, synth, cpu):
     return rec
 
 
+def large_gemv_bench(ctx, wpcg, synth):
+    """The largest GEMV of the config-3 decode, its lm_head shape (151936 x
+    2048, v4, 165 MB) as a plain FAST GEMV with an fp32 x, HBM-cold over 7
+    rotated copies (1.16 GB), replayed from a HIP graph: the kernel's
+    bandwidth once a launch is large enough to stream (the config-1 launches
+    are 8-39 MB each and bound by their memory round trip)."""
+    import numpy as np
+    rows, cols = 151936, 2048
+    base = wpcg.WpcLinear.from_blocks(ctx, 4, synth.random_v4_blocks(rows, cols, 77), rows, cols)
+    base.set_mode(wpcg.MODE_FAST)
+    lins = [base] + [base.clone() for _ in range(6)]
+    xd = ctx.upload(synth.random_x(cols, seed=5))
+    yd = ctx.alloc(4 * rows)
+    body = lambda: [l.matvec_dev(xd, yd) for l in lins]
+    body()
+    ctx.sync()
+    g = ctx.capture(body)
+    g.launch()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    reps = 10
+    e0.record()
+    for _ in range(reps):
+        g.launch()
+    e1.record()
+    ctx.sync()
+    us = e0.elapsed_ms(e1) * 1e3 / (reps * len(lins))
+    alg = gemv_bytes(rows, cols, 4)
+    del g
+    for l in lins:
+        l.close()
+    xd.free()
+    yd.free()
+    gbps = alg / us / 1e3
+    log(f"large GEMV v4 {rows}x{cols}: {us:.2f} us, {gbps:.0f} GB/s ({100 * gbps / PEAK_GBPS:.1f}% of peak)")
+    return {"shape": f"v4 {rows}x{cols} (config-3 lm_head), FAST, fp32 x, HBM-cold over 7 copies",
+            "us": round(us, 3), "gbps": round(gbps, 1), "frac_hbm": round(gbps / PEAK_GBPS, 4),
+            "algorithmic_bytes": alg}
+
+
 def prefill_trace(wpcg, synth, layers, n_prompt):
     """Four FAST prefills of the config-3 model cut to `layers` layers, each
     timed; for rocprofv3 kernel traces of the batched prefill."""
@@ -311,6 +351,8 @@ def main():
     ap.add_argument("--decode-eager", action="store_true",
                     help="decode steps launch by launch instead of graph replays (for kernel traces)")
     ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM (config 4) lines")
+    ap.add_argument("--no-large-gemv", action="store_true",
+                    help="skip the lm_head-shaped v4 GEMV line (165 MB per launch)")
     ap.add_argument("--prefill-trace", type=int, default=0, metavar="LAYERS",
                     help="only: build the config-3 model with LAYERS layers and run four FAST prefills "
                          "of --decode-prompt tokens (for kernel traces), then exit")
@@ -456,6 +498,7 @@ def main():
     for lst in sets:  # free the rotated GEMV copies first
         for l in lst:
             l.close()
+    large = None if args.no_large_gemv else large_gemv_bench(ctx, wpcg, synth)
     gemm = None
     if not args.no_gemm:
         gemm = gemm_bench(ctx, wpcg, synth, not args.no_cpu_baseline)
@@ -490,6 +533,7 @@ def main():
             f"{other}_mode_gbps": round(o_val, 2),
             "decode": decode,
             "gemm": gemm,
+            "large_gemv": large,
         },
         "roofline": {
             "bound": "hbm",
