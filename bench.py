@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the dequant-GEMV hot path on one MI355X.
 
-Workload: batch-1 dequant-GEMV over the seven
+Workload (benchmark config 1): batch-1 dequant-GEMV over the seven
 Qwen3-4B layer shapes (q 4096x2560, k/v 1024x2560, o 2560x4096, gate/up
 9728x2560, down 2560x9728) in the v3 scheme (6-bit codes, two-plane device
 layout), seeded synthetic blocks, x ~ N(0,1) fp32. One step = one pass of
@@ -13,7 +13,7 @@ value = algorithmic bytes per step x steps / time, with
 bytes(GEMV) = rows*(cols/128)*BPB + 4*cols + 4*rows, BPB = 100 (v3) / 68 (v4).
 
 The metric's second half, decode tok/s of the Qwen3-30B-A3B-shaped v4 model
-is measured in the same run and reported under
+(benchmark config 3), is measured in the same run and reported under
 config.decode: greedy generation of 256 tokens after a 256-token prompt,
 every step on the device (one replayed HIP graph per token), with the
 oracle's CPU decode of the same model timed on a bounded sample.
@@ -92,7 +92,7 @@ QWEN3_30B_A3B = dict(n_layers=48, hidden=2048, n_heads=32, n_kv_heads=4, head_di
 
 def decode_token_bytes(c, bpb=68):
     """Weight bytes one decode token reads: attention, router (fp32), the
-    top-k experts, lm_head (SURVEY-style accounting; KV cache excluded)."""
+    top-k experts, lm_head (KV cache excluded)."""
     H, hd = c["hidden"], c["head_dim"]
     qd, kvd = c["n_heads"] * hd, c["n_kv_heads"] * hd
     blocks = lambda r, k: r * (k // 128) * bpb  # noqa: E731
@@ -103,7 +103,7 @@ def decode_token_bytes(c, bpb=68):
 
 
 def decode_bench(ctx, wpcg, synth, n_prompt, n_new, cpu_tokens, eager=False):
-    """Greedy decode of the Qwen3-30B-A3B-shaped v4 model:
+    """Greedy decode of the Qwen3-30B-A3B-shaped v4 model (benchmark config 3):
     seeded weights ~N(0, 0.02) encoded as the artifact compiler does; one
     layer's expert weights are generated and uploaded to every layer (48
     distinct device copies, distinct routers), so every token reads
@@ -199,7 +199,7 @@ def bf16_bits(x):
 
 
 def gemm_bench(ctx, wpcg, synth, cpu):
-    """batched v4 dequant-GEMM on the Gemma-12B-shaped
+    """Benchmark config 4: batched v4 dequant-GEMM on the Gemma-12B-shaped
     gate/up (15360x3840) and down (3840x15360) matrices, M in {1, 4, 16, 64}
     activations (bf16 for M >= 4; M = 1 is the fp32 GEMV), HBM-cold over 34
     rotated copies (1.07 GB), replayed from a HIP graph. The time of a call
