@@ -472,8 +472,9 @@ constexpr int FK_PLAIN = 0, FK_ROUTE = 1, FK_ROUTED = 2;
 template <int SCHEME, int KIND, int XF>
 // The plain GEMV asks for 6 waves per SIMD (at most 80 VGPRs): three
 // workgroups per CU instead of two, so a launch of up to 768 workgroups
-// runs in one round (2x9728x2560 v3: 12.5 -> 11.1 us).
-__global__ __launch_bounds__(FAST_WG, XF == XF_NONE ? 6 : 1) void k_gemv_fast(const FastBatch B)
+// runs in one round (2x9728x2560 v3: 12.5 -> 11.1 us). The routing kinds
+// keep their registers (their routing state would spill).
+__global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1) void k_gemv_fast(const FastBatch B)
 {
     // A wave's last group of MG may reach up to MG-1 blocks past the slice:
     // those blocks' codes are zero, their digits are never written (any
