@@ -91,7 +91,11 @@ SHAPES = [
     (3, 37, 640),
     (4, 8200, 640),    # four tiles per workgroup, 513 tiles (one in the last workgroup)
     (4, 488, 2560),    # 31 tiles: one tile per workgroup
-    (4, 520, 4096),    # 33 tiles, 32 blocks: two tiles per workgroup, odd tile count
+    (4, 520, 4096),    # 33 tiles, 32 blocks: one tile per workgroup (two from 192 tiles)
+    (3, 3056, 4096),   # 191 tiles, 32 blocks: one tile per workgroup
+    (3, 3080, 4096),   # 193 tiles, 32 blocks: two tiles per workgroup, odd tile count
+    (4, 2032, 9728),   # 127 tiles, 76 blocks: one tile per workgroup, 3 K-slices
+    (4, 2056, 9728),   # 129 tiles, 76 blocks: two tiles per workgroup, 3 K-slices
     (3, 8195, 8320),   # two tiles per workgroup, 65 blocks: two K-slices
     (4, 32784, 2048),  # four tiles per workgroup, 2049 tiles (one in the last workgroup)
     (3, 33001, 1152),  # four tiles per workgroup, ragged last tile
