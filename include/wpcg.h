@@ -129,10 +129,12 @@ int wpcg_linear_destroy(wpcg_linear* lin);
 int wpcg_linear_shape(wpcg_linear* lin, uint64_t* out_f, uint64_t* in_f);
 int wpcg_linear_set_mode(wpcg_linear* lin, int mode);
 /* FAST mode splits K over `kslices` workgroups per group of output rows
- * (0 = the library's choice for the shape). A workgroup covers 16 rows, or
- * 32 for matrices of 8192 rows or more, and a slice at most 64 blocks (32
- * with 32 rows); requests are raised to that minimum and capped at one
- * block per slice. Replaces the matrix's split-K workspace: graphs captured
+ * (0 = the library's choice for the shape). A workgroup covers 16, 32 or
+ * 64 rows (one, two or four 16-row tiles, chosen from the matrix's shape)
+ * and a slice at most 64, 32 or 16 blocks respectively; requests are
+ * raised to that minimum and capped at one block per slice. When the
+ * library must split, it uses slices of at most 32 blocks. Replaces the
+ * matrix's split-K workspace: graphs captured
  * earlier with this linear must be destroyed first. No reference
  * counterpart (a tuning knob). */
 int wpcg_linear_set_kslices(wpcg_linear* lin, int kslices);
