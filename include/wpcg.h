@@ -68,6 +68,7 @@ typedef struct wpcg_ctx wpcg_ctx;
 typedef struct wpcg_artifact wpcg_artifact;
 typedef struct wpcg_linear wpcg_linear;
 typedef struct wpcg_event wpcg_event;
+typedef struct wpcg_model_config_s wpcg_model_config; /* defined with the decode step below */
 typedef void* wpcg_stream;
 
 /* ---- library ---- */
@@ -318,8 +319,8 @@ int wpcg_safetensors_read_f32(wpcg_safetensors* st, const char* name, float* out
  * required, top_k in 1..=num_experts, norm_topk_prob defaulting to true);
  * any other config is a dense decoder (n_experts = 0). max_pos, the
  * KV-cache length, is the caller's. E_FORMAT names the offending field. */
-int wpcg_config_parse(const char* json_text, uint32_t max_pos, struct wpcg_model_config_s* out);
-int wpcg_config_load(const char* path, uint32_t max_pos, struct wpcg_model_config_s* out);
+int wpcg_config_parse(const char* json_text, uint32_t max_pos, wpcg_model_config* out);
+int wpcg_config_load(const char* path, uint32_t max_pos, wpcg_model_config* out);
 
 /* ---- device-resident decode step ----
  * A dense Qwen3 (n_experts == 0, SwiGLU MLP) or Qwen3-MoE decoder whose
@@ -334,7 +335,7 @@ int wpcg_config_load(const char* path, uint32_t max_pos, struct wpcg_model_confi
  * over chunks of positions whose softmax states o_proj merges, routing runs
  * inside the expert gate/up launch, and one routed down projection covers
  * the chosen experts with SiLU*up, the routing weights and the residual. */
-typedef struct wpcg_model_config_s {
+struct wpcg_model_config_s {
     uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim;
     uint32_t inter;                          /* dense MLP width (n_experts == 0)   */
     uint32_t vocab;
@@ -344,7 +345,7 @@ typedef struct wpcg_model_config_s {
     uint32_t max_pos;                        /* KV-cache length                    */
     float eps;                               /* RMSNorm epsilon                    */
     double rope_theta;
-} wpcg_model_config;
+};
 typedef struct wpcg_model wpcg_model;
 int wpcg_model_create(wpcg_ctx* ctx, int scheme, const wpcg_model_config* cfg, wpcg_model** out);
 int wpcg_model_destroy(wpcg_model* m);
