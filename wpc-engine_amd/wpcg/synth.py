@@ -22,7 +22,6 @@ from __future__ import annotations
 
 import json
 import os
-import re
 
 import numpy as np
 
@@ -77,12 +76,36 @@ def random_x(n: int, seed: int) -> np.ndarray:
     return np.random.default_rng(seed).standard_normal(n).astype(np.float32)
 
 
+def _rust_usize(s: str):
+    """`s.parse::<usize>().ok()`: an optional '+', then one or more ASCII
+    digits, at most 2^64 - 1; anything else is None."""
+    if s.startswith("+"):
+        s = s[1:]
+    if not s or not all("0" <= ch <= "9" for ch in s):
+        return None
+    v = int(s)
+    return v if v < 2 ** 64 else None
+
+
+def _field_after(name: str, marker: str):
+    """`name.split(marker).nth(1).and_then(|r| r.split('.').next())` parsed as
+    usize: the text between the first and second occurrence of `marker` (or
+    the end), cut at its first '.'."""
+    parts = name.split(marker)
+    if len(parts) < 2:
+        return None
+    return _rust_usize(parts[1].split(".")[0])
+
+
 def tensor_sort_key(name: str):
-    """(layer, section, expert, projection), wpc-compiler/src/main.rs:93-128."""
-    m = re.search(r"layers\.(\d+)\.", name)
-    layer = int(m.group(1)) + 1 if m else 0
-    m = re.search(r"experts\.(\d+)\.", name)
-    expert = int(m.group(1)) if m else None
+    """(layer, section, expert, projection), wpc-compiler/src/main.rs:93-128:
+    layer is 0 for non-layer tensors, else the layer index + 1; section 0
+    for the layer's other matrices, 1 for the router (`mlp.gate.weight`), 2
+    for experts, which sort by numeric index, each one's gate/up/down
+    adjacent. Sorting by it is stable (Rust's sort_by_key)."""
+    layer = _field_after(name, "layers.")
+    layer = layer + 1 if layer is not None else 0
+    expert = _field_after(name, "experts.")
     if "gate_proj" in name:
         proj = 0
     elif "up_proj" in name:
