@@ -21,7 +21,9 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 PKG_ROOT = os.path.dirname(_HERE)
-LIB_PATH = os.path.join(PKG_ROOT, "lib", "libwpcg.so")
+# WPCG_LIB names another build of the same library (the host-sanitizer build
+# _build/asan/libwpcg_asan.so in tests/test_sanitize.py); by default lib/libwpcg.so.
+LIB_PATH = os.environ.get("WPCG_LIB") or os.path.join(PKG_ROOT, "lib", "libwpcg.so")
 HEADER = os.path.join(os.path.dirname(PKG_ROOT), "include", "wpcg.h")
 
 OK, E_IO, E_FORMAT, E_SHAPE, E_NOTFOUND, E_DEVICE, E_ARG, E_NOMEM, E_UNSUPPORTED = range(9)
