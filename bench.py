@@ -1,22 +1,31 @@
 #!/usr/bin/env python3
 """Benchmark of the dequant-GEMV hot path on one MI355X.
 
-Workload (benchmark config 1): batch-1 dequant-GEMV over the seven
-Qwen3-4B layer shapes (q 4096x2560, k/v 1024x2560, o 2560x4096, gate/up
-9728x2560, down 2560x9728) in the v3 scheme (6-bit codes, two-plane device
-layout), seeded synthetic blocks, x ~ N(0,1) fp32. One step = one pass of
-the seven GEMVs. Weights are HBM-cold: the step rotates over enough device
-copies of the layer to exceed the 256 MB Infinity Cache (>= 1 GiB), and the
-launches are replayed from a HIP graph so host launch cost is not timed.
+Workload (benchmark config 1, the record's `value`): batch-1 dequant-GEMV over
+the seven Qwen3-4B layer shapes (q 4096x2560, k/v 1024x2560, o 2560x4096,
+gate/up 9728x2560, down 2560x9728) in the v3 scheme (6-bit codes, two-plane
+device layout), seeded synthetic blocks, x ~ N(0,1) fp32. One step = one pass
+of the seven GEMVs in four launches (q/k/v share their input and a launch, as
+do gate/up; o and down run alone, as in a decode layer where their inputs come
+from other operations). Weights are HBM-cold: the steps rotate over enough
+device copies of the layer to exceed the 256 MB Infinity Cache (>= 1 GB), and
+the launches are replayed from HIP graphs so host launch cost is not timed.
+Exactly --warmup untimed steps, then exactly --steps timed steps.
 
 value = algorithmic bytes per step x steps / time, with
 bytes(GEMV) = rows*(cols/128)*BPB + 4*cols + 4*rows, BPB = 100 (v3) / 68 (v4).
 
-The metric's second half, decode tok/s of the Qwen3-30B-A3B-shaped v4 model
-(benchmark config 3), is measured in the same run and reported under
-config.decode: greedy generation of 256 tokens after a 256-token prompt,
-every step on the device (one replayed HIP graph per token), with the
-oracle's CPU decode of the same model timed on a bounded sample.
+Also measured in the same run (under `config`):
+  per_shape   each config-1 GEMV alone, HBM-cold, GB/s and % of peak;
+  cfg0        the config-0 v4 GEMV 4864x896, HBM-cold (rotated over >= 1 GB)
+              and cache-hot (one copy), launch after launch;
+  decode      greedy decode of the Qwen3-30B-A3B-shaped v4 model (config 3);
+  decode_dense greedy decode of the dense Qwen3-4B-shaped v4 model (config 2);
+  gemm        the batched v4 GEMM at Gemma-12B shapes (config 4);
+  large_gemv  the FAST kernel on the config-3 lm_head shape (165 MB).
+CPU baselines run the oracle's AVX2 restatement of the reference kernels on
+the host, with the box's CPU share (at most 16 threads) and with 1 thread,
+recording nproc and the CPU model.
 
 `--gpus N` with N > 1 is refused: this build measures one GPU.
 """
@@ -43,6 +52,8 @@ BPB = {3: 100, 4: 68}
 # the same counters' reading for a copy kernel of known size; see
 # profiles/k_gemv_fast_cfg1_v3_traffic.txt. None where not measured.
 TRAFFIC = {(3, "fast"): 20061794}
+TRAFFIC_SOURCE = ("profiles/k_gemv_fast_cfg1_v3_traffic.txt: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
+                  "passes over bench.py --pmc-pass, scaled by a 256 MiB device copy's readings")
 
 
 def log(msg):
@@ -53,136 +64,208 @@ def gemv_bytes(rows, cols, scheme):
     return rows * (cols // 128) * BPB[scheme] + 4 * cols + 4 * rows
 
 
-def cpu_baseline(scheme, shapes, blocks, xs, budget_s):
-    """The oracle's AVX2 restatement of the reference row kernel on the host
-    cores, rows split over threads as WpcLinear*::matvec does with rayon."""
-    import oracle as O
-    threads = max(1, min(16, os.cpu_count() or 1))
-    kern = O.KERNEL_AVX2 if O.have_avx2() else O.KERNEL_FUSED
-    step_bytes = sum(gemv_bytes(r, c, scheme) for _, r, c in shapes)
+def host_info():
+    """nproc, the threads this process may use, the CPU model, and the
+    thread count of the all-cores baseline: the CPUs this process may run on,
+    capped at OMP_NUM_THREADS and at 16 (the host-CPU share of one GPU on
+    the benchmark machines)."""
+    nproc = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = nproc
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    cap = int(omp) if omp.isdigit() and int(omp) > 0 else affinity
+    return {"nproc": nproc, "affinity": affinity, "cpu_model": model,
+            "threads_all": max(1, min(affinity, cap, 16))}
 
-    def one_pass():
-        for (name, r, c), b in zip(shapes, blocks):
-            O.linear_matvec(scheme, b, r, c, xs[c], None, kern, threads)
 
-    one_pass()  # warm-up
+def timed_median(fn, budget_s, min_reps=20):
+    """Median wall time of fn() after one warm-up call: at least min_reps
+    calls, more while budget_s lasts."""
+    fn()
     times = []
     t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(times) < 3:
+    while len(times) < min_reps or time.perf_counter() < t_end:
         t0 = time.perf_counter()
-        one_pass()
+        fn()
         times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
+    return statistics.median(times), len(times)
+
+
+def cpu_gemv_baseline(scheme, shapes, blocks, xs, budget_s, what):
+    """The oracle's AVX2 restatement of the reference row kernel
+    (matvec_v{3,4}_fused) on the host cores, rows split over threads as
+    WpcLinear*::matvec does with rayon (wpc_weights_v4.rs:165-193), on the
+    given matrices: all cores and 1 core, median of >= 20 passes each."""
+    import oracle as O
+    hi = host_info()
+    kern = O.KERNEL_AVX2 if O.have_avx2() else O.KERNEL_FUSED
+    step_bytes = sum(gemv_bytes(r, c, scheme) for _, r, c in shapes)
+    res = {}
+    for key, threads, budget in (("all", hi["threads_all"], budget_s), ("one", 1, budget_s / 2)):
+        def one_pass(threads=threads):
+            for (name, r, c), b in zip(shapes, blocks):
+                O.linear_matvec(scheme, b, r, c, xs[c], None, kern, threads)
+        med, n = timed_median(one_pass, budget)
+        res[key] = (step_bytes / med / 1e9, med, n, threads)
+    kname = "AVX2 intrinsics" if kern == O.KERNEL_AVX2 else "scalar fmaf"
     return {
-        "value": round(step_bytes / med / 1e9, 3),
+        "value": round(res["all"][0], 3),
         "unit": "GB/s",
-        "cores": threads,
+        "cores": res["all"][3],
         "kind": "port",
-        "sample": (f"{len(times)} passes over the seven Qwen3-4B v{scheme} matrices "
-                   f"({step_bytes / 1e6:.1f} MB each), median; "
-                   f"{'AVX2 intrinsics' if kern == O.KERNEL_AVX2 else 'scalar fmaf'} "
-                   f"restatement of matvec_v{scheme}_fused, {threads} threads"),
+        "one_core_value": round(res["one"][0], 3),
+        "nproc": hi["nproc"],
+        "cpu_model": hi["cpu_model"],
+        "sample": (f"{what} ({step_bytes / 1e6:.2f} MB per pass): median of {res['all'][2]} passes on "
+                   f"{res['all'][3]} threads (all of this process's CPUs, at most 16) and of "
+                   f"{res['one'][2]} on 1 thread; {kname} restatement of matvec_v{scheme}_fused, rows "
+                   f"split over threads as rayon does; nproc {hi['nproc']}, {hi['cpu_model']}"),
     }
 
 
 QWEN3_30B_A3B = dict(n_layers=48, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=128, inter=0,
                      vocab=151936, n_experts=128, top_k=8, moe_inter=768, norm_topk=1, tied=0,
                      max_pos=512, eps=1e-6, rope_theta=1e6)
+QWEN3_4B_DENSE = dict(n_layers=36, hidden=2560, n_heads=32, n_kv_heads=8, head_dim=128, inter=9728,
+                      vocab=151936, n_experts=0, top_k=0, moe_inter=0, norm_topk=1, tied=1,
+                      max_pos=512, eps=1e-6, rope_theta=1e6)
+DECODE_MODELS = {
+    "decode": (QWEN3_30B_A3B, "Qwen3-30B-A3B-shaped, v4 (48 layers, hidden 2048, 32q/4kv x 128, 128 experts "
+                              "top-8, moe_inter 768, vocab 151936 untied, fp32 router)"),
+    "decode_dense": (QWEN3_4B_DENSE, "Qwen3-4B-shaped dense, v4 (36 layers, hidden 2560, 32q/8kv x 128, "
+                               "intermediate 9728 SwiGLU, vocab 151936 tied)"),
+}
 
 
 def decode_token_bytes(c, bpb=68):
-    """Weight bytes one decode token reads: attention, router (fp32), the
-    top-k experts, lm_head (KV cache excluded)."""
+    """Weight bytes one decode token reads: attention, the MLP (or the router,
+    fp32, and the top-k experts), the output head (KV cache excluded)."""
     H, hd = c["hidden"], c["head_dim"]
     qd, kvd = c["n_heads"] * hd, c["n_kv_heads"] * hd
     blocks = lambda r, k: r * (k // 128) * bpb  # noqa: E731
     attn = blocks(qd, H) + 2 * blocks(kvd, H) + blocks(H, qd)
-    experts = c["top_k"] * (2 * blocks(c["moe_inter"], H) + blocks(H, c["moe_inter"]))
-    router = c["n_experts"] * H * 4
-    return c["n_layers"] * (attn + experts + router) + blocks(c["vocab"], H)
+    if c["n_experts"]:
+        mlp = c["top_k"] * (2 * blocks(c["moe_inter"], H) + blocks(H, c["moe_inter"])) + c["n_experts"] * H * 4
+    else:
+        mlp = 2 * blocks(c["inter"], H) + blocks(H, c["inter"])
+    return c["n_layers"] * (attn + mlp) + blocks(c["vocab"], H)
 
 
-def decode_bench(ctx, wpcg, synth, n_prompt, n_new, cpu_tokens, eager=False):
-    """Greedy decode of the Qwen3-30B-A3B-shaped v4 model (benchmark config 3):
-    seeded weights ~N(0, 0.02) encoded as the artifact compiler does; one
-    layer's expert weights are generated and uploaded to every layer (48
-    distinct device copies, distinct routers), so every token reads
-    1.66 GB of distinct HBM. Returns the record's `decode` object."""
+def kv_bytes_per_token(c, n_prompt, n_new):
+    """fp32 K and V bytes read per decode step, averaged over the timed steps
+    (positions n_prompt .. n_prompt + n_new - 2): every layer reads
+    2 * n_kv_heads * head_dim * 4 bytes per cached position."""
+    per_pos = c["n_layers"] * 2 * c["n_kv_heads"] * c["head_dim"] * 4
+    mean_len = n_prompt + 1 + (n_new - 2) / 2.0
+    return per_pos * mean_len
+
+
+def decode_bench(ctx, wpcg, synth, key, n_prompt, n_new, cpu_tokens, eager=False, n_exact=64):
+    """Greedy decode of a config-2/3 model: seeded weights ~N(0, 0.02)
+    encoded as the artifact compiler does (layer 0 from fresh draws, later
+    layers seeded row permutations of it: distinct weights, every token
+    reads all its bytes from HBM), FAST generation of n_new tokens after an
+    n_prompt-token prompt timed with HIP events around the replayed steps,
+    EXACT generation of n_exact tokens and the number of leading ids the two
+    share, the batched prefill of the prompt, and the oracle's CPU decode of
+    the same model on a bounded sample. Returns the record's object."""
     import numpy as np
-    cfg = QWEN3_30B_A3B
+    cfg, desc = DECODE_MODELS[key]
     t0 = time.perf_counter()
     model = wpcg.Model(ctx, wpcg.SCHEME_V4, wpcg.ModelConfig(**cfg))
     keep = {} if cpu_tokens else None
     resident = 0
-    for name, arr in synth.model_tensors(cfg, 4, 30, wpcg.encode, share_experts=True):
+    for name, arr in synth.model_tensors(cfg, 4, 30, wpcg.encode, derive_layers=True):
         model.set_tensor(name, arr)
         resident += arr.nbytes
         if keep is not None:
             keep[name] = arr
-    log(f"decode model built in {time.perf_counter() - t0:.1f} s ({resident / 1e9:.2f} GB resident)")
+    log(f"{key} model built in {time.perf_counter() - t0:.1f} s ({resident / 1e9:.2f} GB resident)")
     prompt = np.random.default_rng(31).integers(0, cfg["vocab"], n_prompt).astype(np.uint32)
     if eager:  # launch by launch, for kernel traces (a trace cannot see inside graph replays)
         model.set_graphs(False)
     out = {}
-    for mode, key, n in ((wpcg.MODE_FAST, "fast", n_new), (wpcg.MODE_EXACT, "exact", 16)):
+    for mode, mk, n in ((wpcg.MODE_FAST, "fast", n_new), (wpcg.MODE_EXACT, "exact", n_exact)):
         model.set_mode(mode)
         model.generate(prompt, n)            # warm-up (graph capture)
         ids, ms = model.generate(prompt, n)
-        out[key] = ((n - 1) / (ms / 1e3), ms / (n - 1), ids)
-        log(f"decode {key}: {out[key][0]:.1f} tok/s ({out[key][1]:.3f} ms/token, {n - 1} steps)")
-    same = int(np.argmax(np.concatenate([out["fast"][2][:16] != out["exact"][2], [True]])))
+        out[mk] = ((n - 1) / (ms / 1e3), ms / (n - 1), ids)
+        log(f"{key} {mk}: {out[mk][0]:.1f} tok/s ({out[mk][1]:.3f} ms/token, {n - 1} steps)")
+    m = min(n_new, n_exact)
+    same = int(np.argmax(np.concatenate([out["fast"][2][:m] != out["exact"][2][:m], [True]])))
+    log(f"{key}: FAST greedy ids equal EXACT's for {same} of {m}")
     # the prompt alone: batched prefill (FAST) against the same tokens step
     # by step, each timed from an empty cache to the last token's logits
     model.set_mode(wpcg.MODE_FAST)
     pre = {}
-    for key, batched in (("batched", True), ("steps", False)):
+    for pk, batched in (("batched", True), ("steps", False)):
         model.set_prefill(batched)
         model.reset()
         model.prefill(prompt, want_logits=False)  # warm-up
         model.reset()
         t1 = time.perf_counter()
         _, first = model.prefill(prompt, want_logits=False)
-        pre[key] = (time.perf_counter() - t1, first)
+        pre[pk] = (time.perf_counter() - t1, first)
     model.set_prefill(True)
-    log(f"prefill of {n_prompt} tokens: batched {pre['batched'][0] * 1e3:.1f} ms, "
+    log(f"{key} prefill of {n_prompt} tokens: batched {pre['batched'][0] * 1e3:.1f} ms, "
         f"step by step {pre['steps'][0] * 1e3:.1f} ms")
     tok_bytes = decode_token_bytes(cfg)
+    kv = kv_bytes_per_token(cfg, n_prompt, n_new)
     rec = {
-        "model": "Qwen3-30B-A3B-shaped, v4 (48 layers, hidden 2048, 32q/4kv x 128, 128 experts top-8, "
-                 "moe_inter 768, vocab 151936, fp32 router)",
+        "model": desc,
         "mode": "fast",
         "prompt_tokens": int(n_prompt),
         "new_tokens": int(n_new),
         "tok_s": round(out["fast"][0], 2),
         "ms_per_token": round(out["fast"][1], 4),
         "exact_tok_s": round(out["exact"][0], 2),
+        "fast_ids_equal_exact": f"{same} of {m}",
         "prefill": {"tokens": int(n_prompt), "ms": round(pre["batched"][0] * 1e3, 2),
                     "tok_s": round(n_prompt / pre["batched"][0], 1),
                     "stepwise_ms": round(pre["steps"][0] * 1e3, 2),
                     "first_token_equal_stepwise": bool(pre["batched"][1] == pre["steps"][1])},
-        "fast_ids_equal_exact_first16": same,
         "weight_bytes_per_token": tok_bytes,
-        "roofline_tok_s": round(PEAK_GBPS * 1e9 / tok_bytes, 1),
+        "kv_bytes_per_token_mean": round(kv),
+        "achieved_gbps": round((tok_bytes + kv) * out["fast"][0] / 1e9, 1),
+        "roofline_tok_s": round(PEAK_GBPS * 1e9 / (tok_bytes + kv), 1),
+        "frac_of_roofline": round(out["fast"][0] * (tok_bytes + kv) / (PEAK_GBPS * 1e9), 4),
         "resident_gb": round(resident / 1e9, 2),
-        "data": "synthetic: weights N(0,0.02) then v4-encoded, norms 1.0; one layer's experts "
-                "replicated to all layers (distinct device copies)",
+        "data": "synthetic: weights N(0,0.02) then v4-encoded (layer 0 drawn, later layers seeded row "
+                "permutations of it), norms 1.0, prompt of random ids",
     }
     if cpu_tokens:
         import oracle as O
         kern = O.KERNEL_AVX2 if O.have_avx2() else O.KERNEL_FUSED
-        threads = max(1, min(16, os.cpu_count() or 1))
-        ref = O.Model(cfg, keep, cfg["max_pos"], kern, threads)
-        ref.forward_token(int(prompt[0]))    # warm-up
-        t1 = time.perf_counter()
-        for i in range(cpu_tokens):
-            ref.forward_token(int(prompt[1 + i]))
-        dt = time.perf_counter() - t1
-        ref.close()
-        rec["cpu_baseline"] = {"tok_s": round(cpu_tokens / dt, 3), "cores": threads, "kind": "port",
-                               "sample": f"{cpu_tokens} forward_token steps at positions 1..{cpu_tokens} "
-                                         f"of the same model on the host (oracle restatement, "
-                                         f"{'AVX2' if kern == O.KERNEL_AVX2 else 'scalar'} GEMV)"}
-        log(f"decode CPU baseline {rec['cpu_baseline']['tok_s']} tok/s on {threads} threads")
+        hi = host_info()
+        res = {}
+        for tk, threads, n in (("all", hi["threads_all"], cpu_tokens), ("one", 1, max(1, cpu_tokens // 4))):
+            ref = O.Model(cfg, keep, cfg["max_pos"], kern, threads)
+            ref.forward_token(int(prompt[0]))    # warm-up
+            t1 = time.perf_counter()
+            for i in range(n):
+                ref.forward_token(int(prompt[1 + i]))
+            res[tk] = (n / (time.perf_counter() - t1), n, threads)
+            ref.close()
+        rec["cpu_baseline"] = {
+            "tok_s": round(res["all"][0], 3), "cores": res["all"][2], "kind": "port",
+            "one_core_tok_s": round(res["one"][0], 3), "nproc": hi["nproc"], "cpu_model": hi["cpu_model"],
+            "sample": (f"{res['all'][1]} forward_token steps at positions 1..{res['all'][1]} on "
+                       f"{res['all'][2]} threads and {res['one'][1]} on 1 thread, the same model on the "
+                       f"host (oracle restatement, {'AVX2' if kern == O.KERNEL_AVX2 else 'scalar'} GEMV, "
+                       f"rows split over threads as rayon does)")}
+        log(f"{key} CPU baseline {res['all'][0]:.3f} tok/s on {res['all'][2]} threads, "
+            f"{res['one'][0]:.3f} on 1")
     model.close()
     return rec
 
@@ -252,7 +335,7 @@ def gemm_bench(ctx, wpcg, synth, cpu):
         blocks = synth.random_v4_blocks(rows, cols, 41)
         X = np.random.default_rng(4).standard_normal((4, cols)).astype(np.float32)
         kern = O.KERNEL_AVX2 if O.have_avx2() else O.KERNEL_FUSED
-        threads = max(1, min(16, os.cpu_count() or 1))
+        threads = host_info()["threads_all"]
         O.linear_matmul_v4(blocks, rows, cols, X[:1], kern, threads)  # warm-up
         t1 = time.perf_counter()
         n = 0
@@ -314,7 +397,7 @@ def prefill_trace(wpcg, synth, layers, n_prompt):
     cfg = dict(QWEN3_30B_A3B, n_layers=layers)
     ctx = wpcg.Context(0)
     model = wpcg.Model(ctx, wpcg.SCHEME_V4, wpcg.ModelConfig(**cfg))
-    for name, arr in synth.model_tensors(cfg, 4, 30, wpcg.encode, share_experts=True):
+    for name, arr in synth.model_tensors(cfg, 4, 30, wpcg.encode, derive_layers=True):
         model.set_tensor(name, arr)
     model.set_mode(wpcg.MODE_FAST)
     prompt = np.random.default_rng(31).integers(0, cfg["vocab"], n_prompt).astype(np.uint32)
@@ -328,6 +411,108 @@ def prefill_trace(wpcg, synth, layers, n_prompt):
     return 0
 
 
+def rotation_runner(ctx, copies, step_for_copy):
+    """run(n): exactly n steps, step i on copy i % copies, replayed from HIP
+    graphs: one graph per full rotation and one per remainder length."""
+    graphs = {}
+
+    def graph(k):
+        if k not in graphs:
+            graphs[k] = ctx.capture(lambda: [step_for_copy(i) for i in range(k)])
+        return graphs[k]
+
+    def run(n):
+        q, r = divmod(n, copies)
+        for _ in range(q):
+            graph(copies).launch()
+        if r:
+            graph(r).launch()
+
+    def warm():
+        graph(copies)  # capture before any timed region
+        return graphs
+    return run, warm, graphs
+
+
+def gemv_series_us(ctx, wpcg, lins, xd, yd, reps=8):
+    """Device time of one launch of lins[i].matvec(x), launched one after the
+    other (each waits for the previous on the stream) over every member of
+    lins, from a replayed graph: the mean over reps replays."""
+    body = lambda: [l.matvec_dev(xd, yd) for l in lins]  # noqa: E731
+    g = ctx.capture(body)
+    g.launch()
+    ctx.sync()
+    e0, e1 = ctx.event(), ctx.event()
+    e0.record()
+    for _ in range(reps):
+        g.launch()
+    e1.record()
+    ctx.sync()
+    us = e0.elapsed_ms(e1) * 1e3 / (reps * len(lins))
+    del g
+    return us
+
+
+def per_shape_bench(ctx, wpcg, synth, scheme, shapes, min_bytes):
+    """Each config-1 GEMV alone: FAST, HBM-cold (rotated over >= min_bytes of
+    device copies of that matrix), launch after launch."""
+    out = {}
+    for i, (name, r, c) in enumerate(shapes):
+        gen = synth.random_v3_blocks if scheme == 3 else synth.random_v4_blocks
+        base = wpcg.WpcLinear.from_blocks(ctx, scheme, gen(r, c, seed=1000 + i), r, c)
+        base.set_mode(wpcg.MODE_FAST)
+        n = max(1, -(-int(min_bytes) // base.device_bytes()))
+        lins = [base] + [base.clone() for _ in range(n - 1)]
+        xd = ctx.upload(synth.random_x(c, seed=c))
+        yd = ctx.alloc(4 * r)
+        us = gemv_series_us(ctx, wpcg, lins, xd, yd)
+        alg = gemv_bytes(r, c, scheme)
+        out[name] = {"shape": f"{r}x{c}", "us": round(us, 3), "gbps": round(alg / us / 1e3, 1),
+                     "frac_hbm": round(alg / us / 1e3 / PEAK_GBPS, 4), "bytes": alg, "copies": n}
+        log(f"per-shape {name} {r}x{c}: {us:.2f} us, {alg / us / 1e3:.0f} GB/s over {n} copies")
+        for l in lins:
+            l.close()
+        xd.free()
+        yd.free()
+    return out
+
+
+def cfg0_bench(ctx, wpcg, synth, min_bytes, cpu_budget):
+    """Benchmark config 0: the v4 GEMV 4864x896 (Qwen2.5-0.5B MLP up-proj),
+    FAST, fp32 x. HBM-cold: launch after launch over >= min_bytes of device
+    copies (each launch's weights come from HBM); cache-hot: the same launches
+    on one copy (resident in the Infinity Cache after the first)."""
+    rows, cols = 4864, 896
+    blocks = synth.random_v4_blocks(rows, cols, seed=0x12345678 & 0xFFFF)
+    x = synth.random_x(cols, seed=0x5678)
+    base = wpcg.WpcLinear.from_blocks(ctx, 4, blocks, rows, cols).set_mode(wpcg.MODE_FAST)
+    n = max(1, -(-int(min_bytes) // base.device_bytes()))
+    lins = [base] + [base.clone() for _ in range(n - 1)]
+    xd = ctx.upload(x)
+    yd = ctx.alloc(4 * rows)
+    cold = gemv_series_us(ctx, wpcg, lins, xd, yd)
+    hot = gemv_series_us(ctx, wpcg, [base] * n, xd, yd)
+    alg = gemv_bytes(rows, cols, 4)
+    for l in lins:
+        l.close()
+    xd.free()
+    yd.free()
+    log(f"cfg0 v4 {rows}x{cols}: HBM-cold {cold:.3f} us ({alg / cold / 1e3:.0f} GB/s), "
+        f"cache-hot {hot:.3f} us ({alg / hot / 1e3:.0f} GB/s)")
+    rec = {"shape": f"v4 {rows}x{cols}", "bytes": alg, "copies": n,
+           "hbm_cold": {"us": round(cold, 3), "gbps": round(alg / cold / 1e3, 1),
+                        "frac_hbm": round(alg / cold / 1e3 / PEAK_GBPS, 4)},
+           "cache_hot": {"us": round(hot, 3), "gbps": round(alg / hot / 1e3, 1),
+                         "frac_hbm": round(alg / hot / 1e3 / PEAK_GBPS, 4)},
+           "north_star_us_at_70pct": round(alg / (0.7 * PEAK_GBPS) / 1e3, 3)}
+    if cpu_budget:
+        rec["cpu_baseline"] = cpu_gemv_baseline(4, [("up_proj", rows, cols)], [blocks], {cols: x},
+                                                cpu_budget, "the config-0 v4 GEMV 4864x896")
+        log(f"cfg0 CPU baseline {rec['cpu_baseline']['value']} GB/s on {rec['cpu_baseline']['cores']} "
+            f"threads, {rec['cpu_baseline']['one_core_value']} on 1")
+    return rec
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -337,17 +522,20 @@ def main():
     ap.add_argument("--mode", default="fast", choices=("exact", "fast"))
     ap.add_argument("--min-bytes", type=float, default=1.0e9,
                     help="rotated working set, bytes (>= 1 GB defeats the 256 MB MALL)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--normal-exit", action="store_true",
                     help="leave through the runtime's exit path (profilers finalize there)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short run for rocprofv3 --pmc passes (no timing, no JSON)")
-    ap.add_argument("--no-decode", action="store_true",
-                    help="skip the Qwen3-30B-A3B-shaped decode measurement")
+    ap.add_argument("--only", default="",
+                    help="comma list of extra sections to run (per_shape,cfg0,large_gemv,gemm,decode,"
+                         "decode_dense); default: all")
+    ap.add_argument("--no-decode", action="store_true", help="skip both decode measurements")
     ap.add_argument("--decode-prompt", type=int, default=256)
     ap.add_argument("--decode-new", type=int, default=256)
-    ap.add_argument("--decode-cpu-tokens", type=int, default=4)
+    ap.add_argument("--dense-prompt", type=int, default=128)
+    ap.add_argument("--decode-cpu-tokens", type=int, default=8)
     ap.add_argument("--decode-eager", action="store_true",
                     help="decode steps launch by launch instead of graph replays (for kernel traces)")
     ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM (config 4) lines")
@@ -363,6 +551,23 @@ def main():
               "(the single-GPU kernel is the unit of work; see the sharding design notes).",
               file=sys.stderr)
         return 2
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
+    sections = {"per_shape", "cfg0", "large_gemv", "gemm", "decode", "decode_dense"}
+    if args.only:
+        want = {w.strip() for w in args.only.split(",") if w.strip()}
+        bad = want - sections
+        if bad:
+            print(f"--only: unknown sections {sorted(bad)}", file=sys.stderr)
+            return 2
+        sections = want
+    if args.no_decode:
+        sections -= {"decode", "decode_dense"}
+    if args.no_gemm:
+        sections.discard("gemm")
+    if args.no_large_gemv:
+        sections.discard("large_gemv")
 
     import numpy as np
 
@@ -405,10 +610,9 @@ def main():
             lambda: L["down_proj"].matvec_dev(xb[9728], yb["down_proj"]),
         ]
 
-    def one_round():
-        for s in sets:  # one step per copy
-            for fn in step_launches(s):
-                fn()
+    def one_step(i):
+        for fn in step_launches(sets[i % copies]):
+            fn()
 
     def launch_durations(rounds):
         """Average device duration of one launch, from an event pair recorded
@@ -430,27 +634,26 @@ def main():
                 n += 1
         return total / n * 1e3, n
 
-    def measure(mode):
+    def measure(mode, steps, warmup):
+        """Exactly `warmup` untimed steps, then exactly `steps` timed ones."""
         for s in sets:
             for l in s:
                 l.set_mode(mode)
-        graph = ctx.capture(one_round)  # `copies` steps per replay
-        launches = max(1, -(-args.warmup // copies))
-        reps = max(1, -(-args.steps // copies))
-        for _ in range(launches):
-            graph.launch()
+        run, warm, graphs = rotation_runner(ctx, copies, one_step)
+        warm()
+        run(warmup)
+        if steps % copies:
+            run(steps % copies)  # capture the remainder graph outside the timed region
         ctx.sync()
         e0, e1 = ctx.event(), ctx.event()
         e0.record()
-        for _ in range(reps):
-            graph.launch()
+        run(steps)
         e1.record()
-        ms = e0.elapsed_ms(e1)
         ctx.sync()
-        steps = reps * copies
+        ms = e0.elapsed_ms(e1)
+        graphs.clear()
         n_launch = steps * (4 if mode == wpcg.MODE_FAST else len(QWEN3_4B))
-        return (step_bytes * steps / (ms / 1e3) / 1e9, ms, steps, launches * copies,
-                ms * 1e3 / n_launch, n_launch)
+        return step_bytes * steps / (ms / 1e3) / 1e9, ms, ms * 1e3 / n_launch, n_launch
 
     if args.pmc_pass:
         # short run for hardware-counter passes: a few rotations of the FAST
@@ -460,7 +663,8 @@ def main():
             for l in s:
                 l.set_mode(mode)
         for _ in range(4):
-            one_round()
+            for i in range(copies):
+                one_step(i)
         ctx.sync()
         n = 256 << 20  # bytes read and bytes written by the copy kernel
         src, dst = ctx.alloc(n), ctx.alloc(n)
@@ -471,14 +675,15 @@ def main():
         return 0
 
     other = "exact" if args.mode == "fast" else "fast"
-    log(f"timing {other} mode")
-    o_val = measure(wpcg.MODE_EXACT if other == "exact" else wpcg.MODE_FAST)[0]
+    log(f"timing {other} mode ({copies} steps)")
+    o_val = measure(wpcg.MODE_EXACT if other == "exact" else wpcg.MODE_FAST, copies, copies)[0]
     log(f"{other}: {o_val:.1f} GB/s ({100 * o_val / PEAK_GBPS:.1f}% of peak)")
-    log(f"timing {args.mode} mode, {args.steps} steps")
-    value, ms, steps, warm, avg_launch_us, n_launch = measure(mode)
+    log(f"timing {args.mode} mode: {args.warmup} warm-up steps, {args.steps} timed steps")
+    value, ms, avg_launch_us, n_launch = measure(mode, args.steps, args.warmup)
+    steps = args.steps
     log(f"{args.mode}: {value:.1f} GB/s ({100 * value / PEAK_GBPS:.1f}% of peak), "
         f"{ms / steps * 1e3:.2f} us/step, {n_launch} launches, avg {avg_launch_us:.2f} us")
-    # The graph replays the launches back to back on one stream, so the
+    # The graphs replay the launches back to back on one stream, so the
     # event-timed region divided by the launches is the kernel's average
     # launch duration (inter-kernel gaps included; rocprofv3's kernel trace
     # of the same command gives the same average within a few percent).
@@ -491,22 +696,25 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        log(f"CPU baseline (~{args.cpu_seconds:.0f} s)")
-        cpu = cpu_baseline(scheme, QWEN3_4B, blocks, xs, args.cpu_seconds)
-        log(f"CPU baseline {cpu['value']} GB/s on {cpu['cores']} threads")
+        log(f"CPU baseline (~{1.5 * args.cpu_seconds:.0f} s)")
+        cpu = cpu_gemv_baseline(scheme, QWEN3_4B, blocks, xs, args.cpu_seconds,
+                                f"passes over the seven Qwen3-4B v{scheme} matrices")
+        log(f"CPU baseline {cpu['value']} GB/s on {cpu['cores']} threads, {cpu['one_core_value']} on 1")
 
     for lst in sets:  # free the rotated GEMV copies first
         for l in lst:
             l.close()
-    large = None if args.no_large_gemv else large_gemv_bench(ctx, wpcg, synth)
-    gemm = None
-    if not args.no_gemm:
-        gemm = gemm_bench(ctx, wpcg, synth, not args.no_cpu_baseline)
-
-    decode = None
-    if not args.no_decode:
-        decode = decode_bench(ctx, wpcg, synth, args.decode_prompt, args.decode_new,
-                              0 if args.no_cpu_baseline else args.decode_cpu_tokens, args.decode_eager)
+    cpu_budget = 0 if args.no_cpu_baseline else args.cpu_seconds / 2
+    per_shape = per_shape_bench(ctx, wpcg, synth, scheme, QWEN3_4B, args.min_bytes) \
+        if "per_shape" in sections else None
+    cfg0 = cfg0_bench(ctx, wpcg, synth, args.min_bytes, cpu_budget) if "cfg0" in sections else None
+    large = large_gemv_bench(ctx, wpcg, synth) if "large_gemv" in sections else None
+    gemm = gemm_bench(ctx, wpcg, synth, not args.no_cpu_baseline) if "gemm" in sections else None
+    cpu_tokens = 0 if args.no_cpu_baseline else args.decode_cpu_tokens
+    decode = decode_bench(ctx, wpcg, synth, "decode", args.decode_prompt, args.decode_new, cpu_tokens,
+                          args.decode_eager) if "decode" in sections else None
+    decode_dense = decode_bench(ctx, wpcg, synth, "decode_dense", args.dense_prompt, args.decode_new,
+                                cpu_tokens, args.decode_eager) if "decode_dense" in sections else None
 
     kname = f"k_gemv_exact<{scheme}>" if mode == wpcg.MODE_EXACT else f"k_gemv_fast<{scheme}, 0, 0>"
     rec = {
@@ -515,7 +723,7 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": warm,
+        "warmup": args.warmup,
         "ms_per_step": round(ms / steps, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -524,14 +732,18 @@ def main():
         "data": "synthetic (seeded: codes uniform, zp f16(N(-0.03,0.005)), scale f16(U(0.002,0.006)), x N(0,1))",
         "config": {
             "workload": (f"cfg1: v{scheme} dequant-GEMV batch 1 over the seven Qwen3-4B layer shapes "
-                         f"(q/k/v/o/gate/up/down), HBM-cold over {copies} rotated copies"),
+                         f"(q/k/v/o/gate/up/down) in 4 launches per step, HBM-cold over {copies} rotated "
+                         f"copies"),
             "scheme": f"v{scheme}",
             "mode": args.mode,
             "bytes_per_step": step_bytes,
             "pct_of_peak": round(100 * value / PEAK_GBPS, 2),
             "launches_per_step": n_launch // steps,
             f"{other}_mode_gbps": round(o_val, 2),
+            "per_shape": per_shape,
+            "cfg0": cfg0,
             "decode": decode,
+            "decode_dense": decode_dense,
             "gemm": gemm,
             "large_gemv": large,
         },
@@ -546,6 +758,7 @@ def main():
             "eager_launch_us": round(eager_us, 3),
             "algorithmic_bytes_per_launch": round(launch_bytes),
             "traffic": TRAFFIC.get((scheme, args.mode)),
+            "traffic_source": TRAFFIC_SOURCE if (scheme, args.mode) in TRAFFIC else None,
         },
         "cpu_baseline": cpu,
     }

@@ -5,9 +5,22 @@ argmax (sampling.rs:3-14), on seeded synthetic v4 models (weights
 ~N(0, 0.02) encoded as the artifact compiler does, norms 1.0).
 
 EXACT mode: the logits of every step are bit-identical to the oracle's, and
-greedy generation gives the same token ids for 64 steps. FAST mode: the
-step's logits stay within 1e-3 of the logit range of the EXACT ones, and its
-greedy ids are reported against EXACT's (they may part after a near tie)."""
+greedy generation gives the same token ids for 64 steps. FAST mode (the mode
+the throughput figures use): every step's logits within FAST_TOL of the
+oracle's logit range, and its 64 greedy ids identical to EXACT's (and so to
+the oracle's).
+
+Shapes: small dense and MoE models; two layers of the Qwen3-30B-A3B shape
+(config 3) and of the dense Qwen3-4B shape (config 2: hidden 2560, 32q/8kv
+heads of 128, intermediate 9728, tied vocabulary of 151936); and a model whose
+o_proj input is an odd number of blocks (6 heads of 64 = 3 blocks), which
+exercises the FAST attention merge on a half-filled pair of blocks."""
+
+# FAST logits: |fast - oracle| <= FAST_TOL * (max - min of the oracle's
+# logits) at every step. FAST carries x to 28 bits per 128-block with exact
+# integer dot products and sums in a fixed order other than the reference's;
+# the measured worst is about 1.1e-6 of the range.
+FAST_TOL = 1e-5
 import numpy as np
 import pytest
 
@@ -27,6 +40,14 @@ MOE = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, inter=0
 QWEN3_MOE_2L = dict(n_layers=2, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=128, inter=0,
                     vocab=151936, n_experts=128, top_k=8, moe_inter=768, norm_topk=1, tied=0,
                     max_pos=80, eps=1e-6, rope_theta=1e6)
+# Qwen3-4B shapes (config 2) with two of the 36 layers
+QWEN3_4B_2L = dict(n_layers=2, hidden=2560, n_heads=32, n_kv_heads=8, head_dim=128, inter=9728,
+                   vocab=151936, n_experts=0, top_k=0, moe_inter=0, norm_topk=1, tied=1,
+                   max_pos=96, eps=1e-6, rope_theta=1e6)
+# o_proj reads 6 x 64 = 384 values: 3 blocks, an odd count
+ODD_OPROJ = dict(n_layers=2, hidden=256, n_heads=6, n_kv_heads=2, head_dim=64, inter=384, vocab=1000,
+                 n_experts=0, top_k=0, moe_inter=0, norm_topk=1, tied=1, max_pos=96, eps=1e-6,
+                 rope_theta=1e6)
 
 
 @pytest.fixture(scope="module")
@@ -52,7 +73,9 @@ def bits(a):
 
 @pytest.mark.parametrize("name,cfg,n_prompt,n_new,seed", [("dense", DENSE, 8, 64, 101),
                                                           ("moe", MOE, 8, 64, 202),
-                                                          ("qwen3-moe-2L", QWEN3_MOE_2L, 12, 64, 303)])
+                                                          ("qwen3-moe-2L", QWEN3_MOE_2L, 12, 64, 303),
+                                                          ("qwen3-4b-2L", QWEN3_4B_2L, 12, 64, 404),
+                                                          ("odd-oproj", ODD_OPROJ, 8, 64, 505)])
 def test_exact_decode_is_bit_identical(ctx, name, cfg, n_prompt, n_new, seed):
     print(f"[gpu] decode {name}: building", flush=True)
     m, ref = build(ctx, cfg, seed)
@@ -80,29 +103,38 @@ def test_exact_decode_is_bit_identical(ctx, name, cfg, n_prompt, n_new, seed):
     assert list(out[: len(ids)]) == ids, f"{name}: generate() diverges from the stepwise run"
     print(f"[gpu] decode {name}: {n_new} greedy ids identical, e.g. {ids[:8]}", flush=True)
 
-    # FAST mode: logits of the first prompt step close to EXACT's, greedy run reported
+    # FAST mode: the first prompt step's logits close to EXACT's, and the same
+    # 64 greedy ids from the same prompt (generate: batched prompt in FAST)
     m.set_mode(wpcg.MODE_FAST).reset()
     g, _ = m.forward_token(int(prompt[0]))
     m.reset()
     m.set_mode(wpcg.MODE_EXACT)
     e, _ = m.forward_token(int(prompt[0]))
     span = float(e.max() - e.min())
-    assert np.max(np.abs(g - e)) <= 1e-3 * span, f"{name}: FAST logits far from EXACT"
+    err = float(np.max(np.abs(g - e))) / span
+    assert err <= FAST_TOL, f"{name}: FAST logits {err:.2e} of the range from EXACT"
     m.set_mode(wpcg.MODE_FAST)
-    fout, _ = m.generate(prompt, n_new)
-    same = int(np.argmax(np.concatenate([fout != out, [True]])))
-    print(f"[gpu] decode {name}: FAST greedy ids match EXACT for {same} of {n_new} steps", flush=True)
+    for prefill in (True, False):
+        m.set_prefill(prefill)
+        fout, _ = m.generate(prompt, n_new)
+        same = int(np.argmax(np.concatenate([fout != out, [True]])))
+        print(f"[gpu] decode {name}: FAST ({'batched' if prefill else 'stepwise'} prompt) greedy ids "
+              f"match EXACT for {same} of {n_new} steps", flush=True)
+        assert list(fout) == list(out), f"{name}: FAST greedy ids part from EXACT at step {same}"
     m.close()
     ref.close()
 
 
 @pytest.mark.parametrize("name,cfg,n_steps,seed", [("dense", DENSE, 90, 111), ("moe", MOE, 90, 212),
-                                                    ("qwen3-moe-2L", QWEN3_MOE_2L, 78, 313)])
+                                                    ("qwen3-moe-2L", QWEN3_MOE_2L, 78, 313),
+                                                    ("qwen3-4b-2L", QWEN3_4B_2L, 90, 414),
+                                                    ("odd-oproj", ODD_OPROJ, 90, 515)])
 def test_fast_decode_tracks_the_reference(ctx, name, cfg, n_steps, seed):
     """FAST mode step by step on the oracle's greedy tokens: every step's
-    logits within 2e-3 of the logit range of the oracle's. The steps run
-    past several 32-position chunks of the FAST attention, so the chunk
-    merge and the key/value appends of every chunk are exercised."""
+    logits within FAST_TOL of the logit range of the oracle's, and the same
+    argmax. The steps run past many chunk boundaries of the FAST attention
+    (16 chunks of ceil((pos+1)/16) positions), so the chunk merge and the
+    key/value appends of every chunk are exercised."""
     print(f"[gpu] fast decode {name}: building", flush=True)
     m, ref = build(ctx, cfg, seed)
     m.set_mode(wpcg.MODE_FAST)
@@ -110,11 +142,12 @@ def test_fast_decode_tracks_the_reference(ctx, name, cfg, n_steps, seed):
     worst = 0.0
     for step in range(n_steps):
         r = ref.forward_token(tok)
-        g, _ = m.forward_token(tok)
+        g, a = m.forward_token(tok)
         err = float(np.max(np.abs(g - r))) / float(r.max() - r.min())
         worst = max(worst, err)
-        assert err <= 2e-3, f"{name}: step {step} logits off by {err:.2e} of the range"
+        assert err <= FAST_TOL, f"{name}: step {step} logits off by {err:.2e} of the range"
         tok = O.argmax(r)
+        assert a == tok, f"{name}: step {step} argmax {a} vs the oracle's {tok}"
     print(f"[gpu] fast decode {name}: {n_steps} steps, worst logit error {worst:.2e} of the range", flush=True)
     m.close()
     ref.close()

@@ -10,12 +10,20 @@ oracle's restatement of matvec_v{3,4}_fused) and the float64 truth y_true:
     all exactly 0 still carries the fp32 rounding of 0.25*sum(x) twice). The
     reference's own v4 test normalises by term magnitude with 0.02
     (wpc-eval/src/fused_kernel.rs:676-682).
-  * |y - y_ref| / |y_ref| < 1e-4 on every row with |y_ref| >= 0.1 * rms(y_ref)
-    (the north star's 1e-4 relative bound, away from near-zero outputs whose
-    relative error is dominated by fp32 summation order alone).
+  * max over EVERY row of |y - y_true| / max(|y_true|, floor) < 1e-4, the
+    reference's own test form (|got - exp| / max(|exp|, 1e-6) < 1e-4,
+    wpc-eval/src/fused_kernel.rs:589-625) with the floor stated as 1% of the
+    rms output. A floor scaled to the outputs is needed: below it a relative
+    error measures fp32 summation order alone, and the reference kernel
+    itself (the oracle's AVX2 restatement) is 1.45e-3 from float64 on the v3
+    q_proj shape with the literal 1e-6 floor, 6.2e-4 with a floor of 0.1% of
+    the rms output. The same figure against the reference kernel's result,
+    and the reference kernel's own, are printed beside it.
 A wrong code, lane or block index moves a row by ~1% of its term magnitude,
 four orders of magnitude above the first bound.
 """
+REL_TOL = 1e-4
+FLOOR_OF_RMS = 1e-2
 import numpy as np
 import pytest
 
@@ -70,10 +78,15 @@ def check_fast(y, scheme, blocks, rows, cols, x, what, bias=None):
     worst = int(np.argmax(err / mag))
     assert np.all(err <= 1e-6 * mag), (
         f"{what}: row {worst} |y-y_true|={err[worst]:.3e} > 1e-6*{mag[worst]:.3e}")
-    big = np.abs(y_ref) >= 0.1 * np.sqrt(np.mean(y_ref ** 2))
-    rel = np.abs(y.astype(np.float64) - y_ref)[big] / np.abs(y_ref[big])
-    assert rel.max() < 1e-4, f"{what}: max relative error {rel.max():.3e} vs the reference kernel"
-    return float(rel.max()), float((err / mag).max())
+    floor = FLOOR_OF_RMS * np.sqrt(np.mean(y_true ** 2))
+    yd = y.astype(np.float64)
+    rel = float(np.max(err / np.maximum(np.abs(y_true), floor)))
+    rel_ref = float(np.max(np.abs(yd - y_ref) / np.maximum(np.abs(y_ref), floor)))
+    ref_own = float(np.max(np.abs(y_ref - y_true) / np.maximum(np.abs(y_true), floor)))
+    print(f"[gpu] {what}: max rel error over all {rows} rows (floor {floor:.2e}): {rel:.2e} vs float64, "
+          f"{rel_ref:.2e} vs the reference kernel (whose own is {ref_own:.2e})", flush=True)
+    assert rel < REL_TOL, f"{what}: max relative error {rel:.3e} vs float64 (floor {floor:.2e})"
+    return rel, float((err / mag).max())
 
 
 SHAPES = [

@@ -674,13 +674,19 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
                 if constexpr (XF == XF_NONE)
                     if (i >= XP0) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, p * 1024 + lane * 16, 0, 0);
                 if constexpr (xform == XF_MERGE) {
+                    // The half-wave of block 2p+1 when the slice ends at 2p+1
+                    // (odd nbl) takes zeros without a load, as the buffer
+                    // loads of the other transforms give it: its head index
+                    // may lie past n_heads, and its chunk states may not
+                    // exist.
+                    const bool blk_ok = 2 * p + hi < nbl;
                     const int k = (b0 + 2 * p + hi) * 128 + k0, h = k / P.head_dim;
                     const size_t stride = (size_t)P.n_heads * P.head_dim;
                     float mv[ATTN_CHUNKS], lv[ATTN_CHUNKS];
                     float4 ov[ATTN_CHUNKS];
 #pragma unroll
                     for (int cc = 0; cc < ATTN_CHUNKS; cc++) {
-                        const bool on = cc < nact;
+                        const bool on = blk_ok && cc < nact;
                         const float2 ml = on ? *reinterpret_cast<const float2*>(P.x2 + ((size_t)cc * P.n_heads + h) * 2)
                                              : make_float2(-INFINITY, 0.0f);
                         mv[cc] = ml.x;
@@ -703,8 +709,9 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
                         a.w = fmaf(w, ov[cc].w, a.w);
                     }
                     const float rl = __fdiv_rn(1.0f, L);
-                    xv[i] = u32x4{__float_as_uint(a.x * rl), __float_as_uint(a.y * rl),
-                                  __float_as_uint(a.z * rl), __float_as_uint(a.w * rl)};
+                    xv[i] = blk_ok ? u32x4{__float_as_uint(a.x * rl), __float_as_uint(a.y * rl),
+                                           __float_as_uint(a.z * rl), __float_as_uint(a.w * rl)}
+                                   : u32x4{0u, 0u, 0u, 0u};
                 }
                 float v0 = __uint_as_float(xv[i].x), v1 = __uint_as_float(xv[i].y);
                 float v2 = __uint_as_float(xv[i].z), v3 = __uint_as_float(xv[i].w);

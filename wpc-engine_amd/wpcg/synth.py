@@ -142,13 +142,24 @@ def write_artifact(out_dir: str, scheme: int, tensors, sort: bool = True) -> dic
     return meta
 
 
-def model_tensors(cfg, scheme: int, seed: int, encode, std: float = 0.02, share_experts: bool = False):
+def permute_rows(blocks, rows: int, cols: int, scheme: int, perm) -> np.ndarray:
+    """The block rows of a [rows, cols] matrix (reference layout, one row =
+    cols/128 consecutive blocks) in the order `perm`."""
+    row_bytes = (cols // 128) * BPB[scheme]
+    return np.ascontiguousarray(np.asarray(blocks, np.uint8).reshape(rows, row_bytes)[perm]).ravel()
+
+
+def model_tensors(cfg, scheme: int, seed: int, encode, std: float = 0.02, derive_layers: bool = False):
     """Seeded synthetic weights of a dense Qwen3 / Qwen3-MoE decoder, by the
     reference's tensor names: every matrix ~N(0, std) then encoded with
     `encode(scheme, w)` (the artifact compiler's encoder), norms 1.0, the
     MoE router fp32 ~N(0, std). cfg: wpcg.ModelConfig or a dict of its fields.
-    With share_experts, every layer gets the same expert blocks (distinct
-    routers): one layer's worth of generation for a large model.
+    With derive_layers, only layer 0's matrices are encoded from fresh draws;
+    every later layer's quantized matrices are seeded random row permutations
+    of layer 0's (one permutation per layer and matrix), so each layer holds
+    distinct weights of the same distribution without encoding every layer
+    on the host (15 GB of experts for the Qwen3-30B-A3B shape). Routers are
+    drawn fresh for every layer.
     Yields (name, array)."""
     c = cfg if isinstance(cfg, dict) else cfg.as_dict()
     rng = np.random.default_rng(seed)
@@ -163,31 +174,35 @@ def model_tensors(cfg, scheme: int, seed: int, encode, std: float = 0.02, share_
     if not c["tied"]:
         yield "lm_head.weight", mat(V, H)
     yield "model.norm.weight", ones_h
-    shared = None
+    E = c["n_experts"]
+    I = c["moe_inter"] if E else c["inter"]
+    # (suffix, rows, cols) of every quantized matrix of a layer
+    shapes = [("self_attn.q_proj.weight", qd, H), ("self_attn.k_proj.weight", kvd, H),
+              ("self_attn.v_proj.weight", kvd, H), ("self_attn.o_proj.weight", H, qd)]
+    if E == 0:
+        shapes += [("mlp.gate_proj.weight", I, H), ("mlp.up_proj.weight", I, H), ("mlp.down_proj.weight", H, I)]
+    else:
+        for e in range(E):
+            shapes += [(f"mlp.experts.{e}.gate_proj.weight", I, H), (f"mlp.experts.{e}.up_proj.weight", I, H),
+                       (f"mlp.experts.{e}.down_proj.weight", H, I)]
+    first = None
     for l in range(c["n_layers"]):
         p = f"model.layers.{l}."
         yield p + "input_layernorm.weight", ones_h
         yield p + "post_attention_layernorm.weight", ones_h
         yield p + "self_attn.q_norm.weight", np.ones(hd, np.float32)
         yield p + "self_attn.k_norm.weight", np.ones(hd, np.float32)
-        yield p + "self_attn.q_proj.weight", mat(qd, H)
-        yield p + "self_attn.k_proj.weight", mat(kvd, H)
-        yield p + "self_attn.v_proj.weight", mat(kvd, H)
-        yield p + "self_attn.o_proj.weight", mat(H, qd)
-        if c["n_experts"] == 0:
-            I = c["inter"]
-            yield p + "mlp.gate_proj.weight", mat(I, H)
-            yield p + "mlp.up_proj.weight", mat(I, H)
-            yield p + "mlp.down_proj.weight", mat(H, I)
-        else:
-            I, E = c["moe_inter"], c["n_experts"]
+        if E:
             yield p + "mlp.gate.weight", (rng.standard_normal((E, H), dtype=np.float32) * np.float32(std))
-            if shared is None or not share_experts:
-                shared = [(mat(I, H), mat(I, H), mat(H, I)) for _ in range(E)]
-            for e, (g, u, d) in enumerate(shared):
-                yield p + f"mlp.experts.{e}.gate_proj.weight", g
-                yield p + f"mlp.experts.{e}.up_proj.weight", u
-                yield p + f"mlp.experts.{e}.down_proj.weight", d
+        if first is None or not derive_layers:
+            mats = [mat(r, k) for _, r, k in shapes]
+            if derive_layers:
+                first = mats
+        else:
+            prng = np.random.default_rng((seed, l))
+            mats = [permute_rows(b, r, k, scheme, prng.permutation(r)) for b, (_, r, k) in zip(first, shapes)]
+        for (suffix, _, _), b in zip(shapes, mats):
+            yield p + suffix, b
 
 
 # dtype name -> (numpy dtype of the stored element, bytes per element); BF16
