@@ -525,7 +525,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--normal-exit", action="store_true",
-                    help="leave through the runtime's exit path (profilers finalize there)")
+                    help="leave through the runtime's exit path even with WPCG_HARD_EXIT=1 "
+                         "(profilers finalize there)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="short run for rocprofv3 --pmc passes (no timing, no JSON)")
     ap.add_argument("--only", default="",
@@ -774,6 +775,8 @@ if __name__ == "__main__":
         traceback.print_exc()
         rc = 1
     _w = sys.modules.get("wpcg")
-    if _w is not None and _w.gpu_used() and "--normal-exit" not in sys.argv:
-        _w.hard_exit(rc)  # see wpcg.hard_exit
+    if _w is not None and _w.gpu_used():
+        if "--normal-exit" in sys.argv:
+            _w.NORMAL_EXIT = True
+        rc = _w.finish(rc)  # see wpcg.NORMAL_EXIT
     sys.exit(rc)

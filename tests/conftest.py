@@ -5,9 +5,10 @@ rest run on any CPU. Nothing here imports torch: the HIP library owns its
 device memory and streams, and keeping a second HIP runtime out of the
 process avoids two copies of libamdhip64 side by side.
 
-A session that touched the GPU ends through wpcg.hard_exit (orderly
-shutdown, then os._exit with pytest's exit status), after pytest has
-written its report; see wpcg.hard_exit for why.
+A session that touched the GPU ends through wpcg.finish after pytest has
+written its report: every native handle is released (newest first), then
+the process leaves normally, or through os._exit with pytest's exit status
+when WPCG_HARD_EXIT=1; see wpcg.NORMAL_EXIT.
 """
 import os
 import sys
@@ -34,4 +35,4 @@ def pytest_sessionfinish(session, exitstatus):
 def pytest_unconfigure(config):
     wpcg = sys.modules.get("wpcg")
     if wpcg is not None and wpcg.gpu_used():
-        wpcg.hard_exit(_exit_status["code"])
+        wpcg.finish(_exit_status["code"])

@@ -11,6 +11,7 @@ fallback: if the library is missing, importing this module raises.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import os
 import re
@@ -190,32 +191,73 @@ def device_count() -> int:
     return n.value if rc == OK else 0
 
 
-# Processes that used the GPU end through hard_exit(): every live context is
-# synchronized and destroyed, output is flushed, and the process leaves with
-# os._exit, skipping the ROCm runtime's own exit-time teardown. On the
-# MI355X boxes that teardown aborted (std::bad_variant_access thrown from a
-# runtime library) after all work had completed and all handles were freed.
-_live = weakref.WeakSet()
+# Every wrapper of a native handle registers itself here, in creation order.
+# release_all() releases the live ones newest first, so each handle goes
+# before anything it was made from (a linear before its context, a graph
+# before the buffers it was captured over); an atexit hook runs it, so a
+# process that leaves normally has destroyed every stream, graph, event and
+# device buffer of this library before the ROCm runtime's own exit-time
+# teardown begins.
+_tracked = []
 _gpu_used = False
+# Processes that used the GPU leave through the interpreter's normal exit
+# after release_all() (NORMAL_EXIT). WPCG_HARD_EXIT=1 ends them with os._exit
+# after release_all() instead, skipping the runtime's exit-time teardown:
+# that teardown once aborted (std::bad_variant_access thrown from a runtime
+# library) when handles were left to Python's finalizers at shutdown.
+NORMAL_EXIT = os.environ.get("WPCG_HARD_EXIT", "") != "1"
+
+
+def _track(obj):
+    _tracked.append(weakref.ref(obj))
+    if len(_tracked) > 4096 and len(_tracked) % 4096 == 0:  # drop dead references now and then
+        _tracked[:] = [r for r in _tracked if r() is not None]
 
 
 def gpu_used() -> bool:
     return _gpu_used
 
 
-def hard_exit(code: int = 0):
-    for ctx in list(_live):
-        if not ctx.h:
+def release_all() -> int:
+    """Releases every native handle still alive, newest first; contexts are
+    synchronized before they are destroyed. Returns the number of errors."""
+    errors = 0
+    for r in reversed(_tracked):
+        o = r()
+        if o is None:
             continue
         try:
-            ctx.sync()
-            ctx.close()
-        except Exception as e:  # report, but still leave
-            print(f"wpcg: shutdown error: {e}", file=sys.stderr)
-            code = code or 1
+            if isinstance(o, Context) and o.h:
+                o.sync()
+            o._release()
+        except Exception as e:  # report, and keep releasing
+            print(f"wpcg: release error: {e}", file=sys.stderr)
+            errors += 1
+    _tracked.clear()
+    return errors
+
+
+atexit.register(release_all)
+
+
+def hard_exit(code: int = 0):
+    """release_all(), flush, then os._exit(code)."""
+    if release_all():
+        code = code or 1
     sys.stdout.flush()
     sys.stderr.flush()
     os._exit(code)
+
+
+def finish(code: int = 0) -> int:
+    """The end of a process that used the GPU: release_all(), then either
+    return `code` for a normal exit (NORMAL_EXIT) or leave through
+    hard_exit."""
+    if not NORMAL_EXIT:
+        hard_exit(code)
+    if release_all():
+        code = code or 1
+    return code
 
 
 # ------------------------------------------------------------------ device
@@ -228,7 +270,7 @@ class Context:
         check(lib.wpcg_ctx_create(device, C.byref(h)))
         _gpu_used = True
         self.h = h
-        _live.add(self)
+        _track(self)
         s = C.c_void_p()
         check(lib.wpcg_ctx_stream(self.h, C.byref(s)))
         self.stream = s
@@ -264,6 +306,8 @@ class Context:
             lib.wpcg_ctx_destroy(self.h)
             self.h = None
 
+    _release = close
+
     def __del__(self):
         try:
             self.close()
@@ -277,6 +321,7 @@ class DeviceBuffer:
         p = C.c_void_p()
         check(lib.wpcg_dev_alloc(ctx.h, self.nbytes, C.byref(p)))
         self.ptr = p
+        _track(self)
 
     def write(self, arr: np.ndarray):
         arr = np.ascontiguousarray(arr)
@@ -294,6 +339,10 @@ class DeviceBuffer:
             lib.wpcg_dev_free(self.ctx.h, self.ptr)
             self.ptr = None
 
+    def _release(self):
+        if self.ctx.h:
+            self.free()
+
     def __del__(self):
         try:
             if self.ctx.h:
@@ -308,6 +357,7 @@ class Event:
         h = C.c_void_p()
         check(lib.wpcg_event_create(ctx.h, C.byref(h)))
         self.h = h
+        _track(self)
 
     def record(self, stream=None):
         check(lib.wpcg_event_record(self.h, stream))
@@ -317,9 +367,14 @@ class Event:
         check(lib.wpcg_event_elapsed_ms(self.h, end.h, C.byref(ms)))
         return ms.value
 
+    def _release(self):
+        if self.h:
+            lib.wpcg_event_destroy(self.h)
+            self.h = None
+
     def __del__(self):
         try:
-            lib.wpcg_event_destroy(self.h)
+            self._release()
         except Exception:
             pass
 
@@ -327,13 +382,19 @@ class Event:
 class Graph:
     def __init__(self, ctx: Context, h):
         self.ctx, self.h = ctx, h
+        _track(self)
 
     def launch(self, stream=None):
         check(lib.wpcg_graph_launch(self.h, stream))
 
+    def _release(self):
+        if self.h:
+            lib.wpcg_graph_destroy(self.h)
+            self.h = None
+
     def __del__(self):
         try:
-            lib.wpcg_graph_destroy(self.h)
+            self._release()
         except Exception:
             pass
 
@@ -346,6 +407,7 @@ class WpcModelData:
 
     def __init__(self, h, scheme):
         self.h, self.scheme = h, scheme
+        _track(self)
 
     @classmethod
     def open(cls, wpc_dir: str, scheme: int | None = None):
@@ -371,6 +433,8 @@ class WpcModelData:
             lib.wpcg_artifact_close(self.h)
             self.h = None
 
+    _release = close
+
     def __del__(self):
         try:
             self.close()
@@ -392,6 +456,7 @@ class WpcLinear:
 
     def __init__(self, ctx: Context, h):
         self.ctx, self.h = ctx, h
+        _track(self)
         o, i = C.c_uint64(), C.c_uint64()
         check(lib.wpcg_linear_shape(h, C.byref(o), C.byref(i)))
         self._out, self._in = o.value, i.value
@@ -500,6 +565,8 @@ class WpcLinear:
             lib.wpcg_linear_destroy(self.h)
             self.h = None
 
+    _release = close
+
     def __del__(self):
         try:
             self.close()
@@ -538,6 +605,7 @@ class DenseLinear:
         check(lib.wpcg_dense_create(ctx.h if ctx else None, _np_ptr(w), self._out, self._in,
                                     None if b is None else _np_ptr(b), C.byref(h)))
         self.h = h
+        _track(self)
 
     def in_features(self) -> int:
         return self._in
@@ -563,6 +631,8 @@ class DenseLinear:
         if self.h:
             lib.wpcg_dense_destroy(self.h)
             self.h = None
+
+    _release = close
 
     def __del__(self):
         try:
@@ -621,6 +691,7 @@ class MoeLayer:
         check(lib.wpcg_moe_create(ctx.h if ctx else None, scheme, n_exp, hidden, inter, top_k,
                                   int(bool(norm_topk)), C.byref(h)))
         self.h = h
+        _track(self)
 
     def set_router(self, w):
         w = np.ascontiguousarray(w, np.float32)
@@ -657,6 +728,8 @@ class MoeLayer:
         if self.h:
             lib.wpcg_moe_destroy(self.h)
             self.h = None
+
+    _release = close
 
     def __del__(self):
         try:
@@ -711,6 +784,7 @@ class ShardedSafetensors:
 
     def __init__(self, handle):
         self.h = handle
+        _track(self)
 
     @classmethod
     def open(cls, model_dir) -> "ShardedSafetensors":
@@ -751,6 +825,8 @@ class ShardedSafetensors:
             lib.wpcg_safetensors_close(self.h)
             self.h = None
 
+    _release = close
+
     def __del__(self):
         try:
             self.close()
@@ -777,6 +853,7 @@ class Model:
         h = C.c_void_p()
         check(lib.wpcg_model_create(ctx.h if ctx else None, scheme, C.byref(cfg), C.byref(h)))
         self.h = h
+        _track(self)
 
     def set_tensor(self, name: str, data: np.ndarray):
         data = np.ascontiguousarray(data)
@@ -882,6 +959,8 @@ class Model:
         if self.h:
             lib.wpcg_model_destroy(self.h)
             self.h = None
+
+    _release = close
 
     def __del__(self):
         try:
