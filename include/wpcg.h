@@ -184,6 +184,23 @@ int wpcg_linear_gemm(wpcg_linear* lin, const void* x_dev, int x_dtype, uint32_t 
                      wpcg_stream stream);
 /* Host-pointer twin (synchronous). */
 int wpcg_linear_gemm_host(wpcg_linear* lin, const void* x, int x_dtype, uint32_t M, float* y);
+/* wpcg_linear_gemm that allocates nothing: the same kernels, splits and
+ * results (bit for bit), with the workspace (packed X, per-block column
+ * sums, split-K partials, counters) carved from a fixed device array of
+ * WPCG_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on
+ * until the process ends, instead of the linear's own workspace. No
+ * reference counterpart: for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc); the first batched call on a linear may be this one even
+ * while a graph is being captured. Every call on one GPU uses that GPU's
+ * one array: calls that overlap on a GPU (other streams, other threads)
+ * race and must be serialized by the caller. E_UNSUPPORTED (naming the
+ * bytes needed) when the call's workspace exceeds the array; with M == 1
+ * and fp32 X it runs wpcg_linear_matvec, whose workspace the linear made
+ * when it was created. */
+#define WPCG_NOALLOC_SCRATCH_BYTES (16u << 20)
+int wpcg_linear_gemm_noalloc(wpcg_linear* lin, const void* x_dev, int x_dtype, uint32_t M, float* y_dev,
+                             wpcg_stream stream);
 /* K-slices of the batched kernels (0 = the library's choice; a tuning knob,
  * no reference counterpart), applied to both (M <= 16 and M > 16) within
  * their limits. Frees the workspace; the next batched call makes it. The

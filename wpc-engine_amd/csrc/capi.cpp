@@ -205,6 +205,7 @@ int wpcg_ctx_create(int device, wpcg_ctx** out)
     std::unique_ptr<wpcg_ctx> c(new (std::nothrow) wpcg_ctx);
     if (!c) return fail(WPCG_E_NOMEM, "context allocation");
     c->device = device;
+    if (int rc = scratch_setup(device)) return rc;  // the no-allocation workspace's address
     WPCG_HIP(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
     *out = c.release();
     return WPCG_OK;

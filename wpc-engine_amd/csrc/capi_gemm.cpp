@@ -123,6 +123,53 @@ int wpcg_linear_gemm(wpcg_linear* L, const void* x, int x_dtype, uint32_t M, flo
     return run_gemm(L, x, x_dtype, M, y, pick(L->ctx, stream));
 }
 
+int wpcg_linear_gemm_noalloc(wpcg_linear* L, const void* x, int x_dtype, uint32_t M, float* y,
+                             wpcg_stream stream)
+{
+    if (int rc = check_gemm_args(L, x, x_dtype, M, y)) return rc;
+    const DeviceMatrix& m = L->m;
+    hipStream_t s = pick(L->ctx, stream);
+    if (M == 0 || m.rows == 0) return WPCG_OK;
+    // the cases the matvec serves use no batched workspace
+    if (m.nb == 0 || (x_dtype == WPCG_DTYPE_F32 && M == 1)) return run_gemm(L, x, x_dtype, M, y, s);
+    // the workspace make_gemm would allocate, at 256-byte aligned offsets
+    GemmWork w{};
+    w.kg_req = L->gemm.kg_req;
+    w.kg = gemm_kslices(m.rows, m.nb, w.kg_req);
+    w.kg_small = gemm_small_kslices(m.rows, m.nb, w.kg_req);
+    const uint64_t ncnt = std::max<uint64_t>(
+        1, (uint64_t)std::max(gemm_row_groups(m.rows), gemm_small_row_groups(m.rows)));
+    const uint64_t part = (w.kg > 1 || w.kg_small > 1)
+                              ? std::max<uint64_t>((uint64_t)w.kg * GEMM_MAX_M, (uint64_t)w.kg_small * 16) *
+                                    m.rows_pad * sizeof(float)
+                              : 0;
+    auto up = [](uint64_t b) { return (b + 255) / 256 * 256; };
+    const uint64_t o_xsum = up(ncnt * sizeof(uint32_t));
+    const uint64_t o_xf = o_xsum + up(m.nb * GEMM_MAX_M * sizeof(float));
+    const uint64_t o_part = o_xf + up(m.nb * 4 * 4096);
+    const uint64_t need = o_part + up(part);
+    if (need > WPCG_NOALLOC_SCRATCH_BYTES)
+        return fail(WPCG_E_UNSUPPORTED, "batched GEMM without allocation: this matrix needs " + std::to_string(need) +
+                                            " bytes of workspace, the fixed array holds " +
+                                            std::to_string(WPCG_NOALLOC_SCRATCH_BYTES));
+    uint8_t* base = static_cast<uint8_t*>(scratch_ptr(L->ctx->device));
+    if (!base) return fail(WPCG_E_DEVICE, "the no-allocation workspace is not set up on this device");
+    w.counters = reinterpret_cast<uint32_t*>(base);
+    w.xsum = reinterpret_cast<float*>(base + o_xsum);
+    w.xf = base + o_xf;
+    w.part = part ? reinterpret_cast<float*>(base + o_part) : nullptr;
+    // the array keeps the last call's contents: the counters must start at 0
+    WPCG_HIP(launch_fill_u32(w.counters, (int)ncnt, 0u, s));
+    const uint64_t es = x_dtype == WPCG_DTYPE_BF16 ? 2 : 4;
+    const uint32_t step = x_dtype == WPCG_DTYPE_F32_SPLIT ? GEMM_MAX_M_SPLIT : GEMM_MAX_M;
+    for (uint32_t c = 0; c < M; c += step) {
+        const int mc = (int)std::min<uint32_t>(step, M - c);
+        WPCG_HIP(launch_gemm(m, w, static_cast<const uint8_t*>(x) + (uint64_t)c * m.cols * es, x_dtype, mc,
+                             L->bias, nullptr, y + (uint64_t)c * m.rows, s));
+    }
+    return WPCG_OK;
+}
+
 int wpcg_linear_gemm_host(wpcg_linear* L, const void* x, int x_dtype, uint32_t M, float* y)
 {
     if (int rc = check_gemm_args(L, x, x_dtype, M, y)) return rc;

@@ -222,6 +222,16 @@ hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const 
 hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, int xrows, const int* rowidx, const int* items,
                                const int* nitems, int max_items, float* y, hipStream_t s);
 
+// ---- the no-allocation workspace (scratch.hip) --------------------------------
+// scratch_setup(device) looks up the device address of the library's fixed
+// workspace array on `device` (which must be current) and keeps it;
+// wpcg_ctx_create runs it. scratch_ptr(device) returns that address (null
+// before set-up). launch_fill_u32 writes v to p[0..n) with a kernel (no
+// memset node, so a captured graph replays it correctly).
+int scratch_setup(int device);
+void* scratch_ptr(int device);
+hipError_t launch_fill_u32(uint32_t* p, int n, uint32_t v, hipStream_t s);
+
 // ---- host helpers shared by the C ABI files (capi*.cpp) -----------------
 hipStream_t pick(wpcg_ctx* ctx, wpcg_stream s);  // NULL = the context stream
 int check_ctx(wpcg_ctx* ctx);                     // non-null, device current

@@ -90,6 +90,7 @@ _SIGS = {
     "wpcg_linear_matvec_host": (C.c_int, [_p, _p, _p]),
     "wpcg_linear_gemm": (C.c_int, [_p, _p, C.c_int, C.c_uint32, _p, _p]),
     "wpcg_linear_gemm_host": (C.c_int, [_p, _p, C.c_int, C.c_uint32, _p]),
+    "wpcg_linear_gemm_noalloc": (C.c_int, [_p, _p, C.c_int, C.c_uint32, _p, _p]),
     "wpcg_linear_set_gemm_kslices": (C.c_int, [_p, C.c_int]),
     "wpcg_linear_gemm_kslices": (C.c_int, [_p, _p, _p]),
     "wpcg_linear_embed": (C.c_int, [_p, C.c_uint32, _p, _p]),
