@@ -370,17 +370,57 @@ __global__ __launch_bounds__(FA_WG) void k_attention_fast(const float* __restric
         }
     };
     load_block(tb);
-    // q heads (and the current key and value, in the chunk that holds pos)
+    // q heads (and the current key and value, in the chunk that holds pos):
+    // wave w takes rows r = w, w + 4, ... (row n_rep is the key). Every load
+    // of the wave's rows, the norm weights and this position's RoPE table is
+    // issued before any is used (one memory round trip), then each row is
+    // RMS-normalised and rotated as fa_norm_rope does it.
     const bool has_pos = te == n;
-    for (int r = wave; r < n_rep + (has_pos ? 1 : 0); r += FA_WG / 64) {
-        if (r < n_rep) {
-            fa_norm_rope<HD>(qp + (size_t)(j * n_rep + r) * HD, qn, eps, cs, sn, qs[r], nullptr);
-        } else {
-            fa_norm_rope<HD>(kp + (size_t)j * HD, kn, eps, cs, sn, kcur, kb + (size_t)pos * HD);
-            for (int d = lane; d < HD; d += 64) {
-                const float vv = vp[(size_t)j * HD + d];
-                vcur[d] = vv;
-                vb[(size_t)pos * HD + d] = vv;
+    {
+        constexpr int half = HD / 2, NWV = FA_WG / 64;
+        constexpr int RW = (FA_MAXREP + NWV) / NWV;  // rows per wave at most
+        const int nrows = n_rep + (has_pos ? 1 : 0);
+        const bool on = lane < half;
+        const int li = on ? lane : 0;  // every address in bounds; off lanes' values are discarded
+        float x1[RW], x2[RW];
+#pragma unroll
+        for (int i = 0; i < RW; i++) {
+            const int r = wave + i * NWV;
+            const float* src = r < n_rep ? qp + (size_t)(j * n_rep + r) * HD : kp + (size_t)j * HD;
+            x1[i] = src[li];
+            x2[i] = src[li + half];
+        }
+        const float c1 = cs[li], s1 = sn[li];
+        const float qw1 = qn[li], qw2 = qn[li + half], kw1 = kn[li], kw2 = kn[li + half];
+        float vv[HD / 64];
+#pragma unroll
+        for (int u = 0; u < HD / 64; u++) vv[u] = vp[(size_t)j * HD + lane + 64 * u];
+#pragma unroll
+        for (int i = 0; i < RW; i++) {
+            const int r = wave + i * NWV;
+            if (r < nrows) {
+                const float a1 = on ? x1[i] : 0.0f, a2 = on ? x2[i] : 0.0f;
+                const float ss = wave_sum(fmaf(a1, a1, a2 * a2));
+                const float sc = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(ss, (float)HD), eps)));
+                const bool isq = r < n_rep;
+                const float y1 = (a1 * sc) * (isq ? qw1 : kw1), y2 = (a2 * sc) * (isq ? qw2 : kw2);
+                const float o1 = fmaf(y1, c1, -(y2 * s1)), o2 = fmaf(y2, c1, y1 * s1);
+                if (on) {
+                    float* y = isq ? qs[r] : kcur;
+                    y[lane] = o1;
+                    y[lane + half] = o2;
+                    if (!isq) {
+                        kb[(size_t)pos * HD + lane] = o1;
+                        kb[(size_t)pos * HD + lane + half] = o2;
+                    }
+                }
+                if (!isq) {
+#pragma unroll
+                    for (int u = 0; u < HD / 64; u++) {
+                        vcur[lane + 64 * u] = vv[u];
+                        vb[(size_t)pos * HD + lane + 64 * u] = vv[u];
+                    }
+                }
             }
         }
     }

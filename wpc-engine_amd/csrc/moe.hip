@@ -122,18 +122,37 @@ __global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ w,
     const float* row = w + (size_t)min(r, out_f - 1) * in_f;
     float acc = 0.0f, sq = 0.0f;
     if ((in_f & 3) == 0) {
-        for (int i = 4 * lane; i < in_f; i += 256) {
-            const float4 v = *reinterpret_cast<const float4*>(row + i);
-            float4 u = *reinterpret_cast<const float4*>(x + i);
-            if (nw) {
-                sq = fmaf(u.x, u.x, sq); sq = fmaf(u.y, u.y, sq); sq = fmaf(u.z, u.z, sq); sq = fmaf(u.w, u.w, sq);
-                const float4 n4 = *reinterpret_cast<const float4*>(nw + i);
-                u.x *= n4.x; u.y *= n4.y; u.z *= n4.z; u.w *= n4.w;
+        // DF_U float4s per lane per pass, every load of a pass issued before
+        // any is used: one memory round trip per 64 * 4 * DF_U inputs
+        // (buffer loads over exactly the row, x and nw: past the end they
+        // return zeros without touching memory, so no load needs a branch)
+        constexpr int DF_U = 8;
+        const auto wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(row), (short)0, in_f * 4, 0x00020000);
+        const auto xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), (short)0, in_f * 4, 0x00020000);
+        const auto nr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(nw ? nw : x), (short)0,
+                                                          nw ? in_f * 4 : 0, 0x00020000);
+        for (int base = 0; base < in_f; base += 256 * DF_U) {
+            float4 v[DF_U], u[DF_U], n4[DF_U];
+#pragma unroll
+            for (int q = 0; q < DF_U; q++) {
+                const int off = (base + 256 * q + 4 * lane) * 4;
+                v[q] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
+                u[q] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+                if (nw) n4[q] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(nr, off, 0, 0));
             }
-            acc = fmaf(v.x, u.x, acc);
-            acc = fmaf(v.y, u.y, acc);
-            acc = fmaf(v.z, u.z, acc);
-            acc = fmaf(v.w, u.w, acc);
+#pragma unroll
+            for (int q = 0; q < DF_U; q++) {
+                float4 uq = u[q];
+                if (nw) {
+                    sq = fmaf(uq.x, uq.x, sq); sq = fmaf(uq.y, uq.y, sq);
+                    sq = fmaf(uq.z, uq.z, sq); sq = fmaf(uq.w, uq.w, sq);
+                    uq.x *= n4[q].x; uq.y *= n4[q].y; uq.z *= n4[q].z; uq.w *= n4[q].w;
+                }
+                acc = fmaf(v[q].x, uq.x, acc);
+                acc = fmaf(v[q].y, uq.y, acc);
+                acc = fmaf(v[q].z, uq.z, acc);
+                acc = fmaf(v[q].w, uq.w, acc);
+            }
         }
     } else {
         for (int i = lane; i < in_f; i += 64) {
