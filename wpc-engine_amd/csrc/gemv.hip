@@ -196,9 +196,10 @@ __global__ __launch_bounds__(EX_WG) void k_gemv_exact(const uint8_t* __restrict_
     gemv_exact_tile<SCHEME>(codes, hp, params, x, bias, y, rows, nb, sel, sel_k, rows_pad, blockIdx.x, xs);
 }
 
-// Several EXACT GEMVs (same scheme) in one launch: workgroup w belongs to
-// the problem whose range [wg_begin, next wg_begin) holds it, and runs that
-// problem's tile w - wg_begin exactly as k_gemv_exact would.
+// Several EXACT GEMVs (same scheme) in one launch: workgroup (x, y) runs
+// tile x of problem y exactly as k_gemv_exact would (x < the problem's nwg;
+// the grid is as wide as the largest problem). The problem index comes from
+// the grid, so a workgroup reads its problem's fields in one round trip.
 struct ExactProblem {
     const uint8_t* codes;
     const uint8_t* hp;
@@ -207,7 +208,7 @@ struct ExactProblem {
     const float* bias;
     float* y;
     const int32_t* sel;
-    int rows, nb, sel_k, rows_pad, wg_begin;
+    int rows, nb, sel_k, rows_pad, nwg;
 };
 struct ExactBatch {
     ExactProblem p[MAX_JOBS];
@@ -219,15 +220,20 @@ template <int SCHEME>
 __global__ __launch_bounds__(EX_WG) void k_gemv_exact_multi(const ExactBatch B)
 {
     __shared__ __align__(16) float xs[EX_SEG * XS_BLK];
-    const int wgid = blockIdx.x;
-    int pi = 0;
-#pragma unroll
-    for (int i = 1; i < MAX_JOBS; i++) pi += (i < B.n && wgid >= B.p[i].wg_begin) ? 1 : 0;
+    // (the problem is read through the kernel-argument segment: indexing the
+    // by-value argument with a variable would copy it to scratch memory)
     typedef const __attribute__((address_space(4))) ExactBatch* KargPtr;
     const KargPtr kargs = (KargPtr)__builtin_amdgcn_kernarg_segment_ptr();
-    const auto& P = kargs->p[pi];
-    gemv_exact_tile<SCHEME>(P.codes, P.hp, P.params, P.x, P.bias, P.y, P.rows, P.nb, P.sel, P.sel_k, P.rows_pad,
-                            wgid - P.wg_begin, xs);
+    const auto& P = kargs->p[blockIdx.y];
+    const uint8_t* const codes = P.codes;
+    const uint32_t* const params = P.params;
+    const float* const x = P.x;
+    const int nb = P.nb, rows_pad = P.rows_pad, nwg = P.nwg;
+    // these loads go out together, before the exit test below needs nwg
+    asm volatile("" ::"s"(codes), "s"(params), "s"(x), "s"(nb), "s"(rows_pad), "s"(nwg));
+    if ((int)blockIdx.x >= nwg) return;  // past this problem's tiles
+    gemv_exact_tile<SCHEME>(codes, P.hp, params, x, P.bias, P.y, P.rows, nb, P.sel, P.sel_k, rows_pad, blockIdx.x,
+                            xs);
 }
 
 // ============================================================ FAST mode
@@ -261,7 +267,7 @@ struct FastProblem {
     const float* scores;
     int32_t* ids_out;
     float* w_out;
-    int rows, rows_pad, nb, kg, wg_begin, tw;  // tw: 16-row tiles per workgroup
+    int rows, rows_pad, nb, kg, nwg, tw;  // nwg: workgroups; tw: 16-row tiles per workgroup
     const DecodeState* st;  // XF_MERGE: the decode position
     int sel_k, xform, routed, n_exp, top_k, norm_topk;
     float eps;
@@ -493,23 +499,26 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     double* const route_tab = reinterpret_cast<double*>(xq + ROUTE_MAXN * 8);
     int* const route_rk = reinterpret_cast<int*>(xq + ROUTE_MAXN * 8 + 32 * 8);
 
-    const int wgid = blockIdx.x;
-    // The problem this workgroup belongs to: the problems' first workgroups
-    // are read together, then the problem itself is read through the
-    // kernel-argument segment (indexing the by-value argument with a
-    // variable would copy it to scratch memory).
-    int pi = 0;
-#pragma unroll
-    for (int i = 1; i < MAX_JOBS; i++) pi += (i < B.n && wgid >= B.p[i].wg_begin) ? 1 : 0;
+    // Workgroup (x, y) is workgroup x of problem y: the problem index comes
+    // from the grid, so the problem's fields are read in one round trip (a
+    // search over the problems' workgroup ranges cost two more, ~0.85 us per
+    // launch). The problem is read through the kernel-argument segment
+    // (indexing the by-value argument with a variable would copy it to
+    // scratch memory). The grid is as wide as the largest problem.
     typedef const __attribute__((address_space(4))) FastBatch* KargPtr;
     const KargPtr kargs = (KargPtr)__builtin_amdgcn_kernarg_segment_ptr();
-    const auto& P = kargs->p[pi];
-    const int nb = P.nb, kg = P.kg, tw = P.tw;
+    const auto& P = kargs->p[blockIdx.y];
+    const int local = blockIdx.x;
+    const int nb = P.nb, kg = P.kg, tw = P.tw, nwg = P.nwg, rows_pad = P.rows_pad;
     constexpr int xform = XF;
     const uint8_t* codes = P.codes;
     const uint8_t* hplane = SCHEME == 3 ? P.hp : P.codes;
     const uint32_t* params = P.params;
-    const int local = wgid - P.wg_begin;
+    const float* const x0 = P.x;
+    // these loads go out together, before the exit test below needs nwg
+    asm volatile("" ::"s"(nb), "s"(kg), "s"(tw), "s"(nwg), "s"(rows_pad), "s"(codes), "s"(hplane),
+                 "s"(params), "s"(x0));
+    if (local >= nwg) return;  // past this problem's workgroups
     const int kgi = local % kg, tg = local / kg;  // K-slice, tile group
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     // the slice: blocks [b0, b0 + nbl) of the matrix (of expert sel[kgi] in
@@ -522,13 +531,13 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     if constexpr (KIND == FK_ROUTED) {
         b0 = 0;
         nbl = nb;
-        xp = P.x;
+        xp = x0;
         x2p = P.x2;
     } else {
         const int nbk = (nb + kg - 1) / kg;
         b0 = kgi * nbk;
         nbl = max(0, min(nb, b0 + nbk) - b0);
-        xp = P.x + (size_t)b0 * 128;
+        xp = x0 + (size_t)b0 * 128;
         if constexpr (xform == XF_SILU) x2p = P.x2 + (size_t)b0 * 128;
     }
     // Loads, all issued before any use: x (L2-resident), then parameters,
@@ -577,7 +586,7 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
                         route_tab, &s_last);
         __syncthreads();
         e = route_ids[P.sel_k];
-        if (wgid == 0 && (int)threadIdx.x < P.top_k) {
+        if (local == 0 && blockIdx.y == 0 && (int)threadIdx.x < P.top_k) {
             P.ids_out[threadIdx.x] = route_ids[threadIdx.x];
             P.w_out[threadIdx.x] = route_w[threadIdx.x];
         }
@@ -587,12 +596,12 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     }
     if (KIND == FK_ROUTE || (KIND == FK_PLAIN && P.sel)) {  // the expert's rows of a stacked matrix
         live = e >= 0;
-        const size_t t0 = (size_t)max(e, 0) * (P.rows_pad / TILE_ROWS) * nb;  // tile-block records
+        const size_t t0 = (size_t)max(e, 0) * (rows_pad / TILE_ROWS) * nb;  // tile-block records
         codes += t0 * CODE_REC;
         hplane += t0 * HP_REC;
         params += t0 * TILE_ROWS;
     }
-    const int ntiles = P.rows_pad / TILE_ROWS;
+    const int ntiles = rows_pad / TILE_ROWS;
     const int kw = 8 / tw;                           // waves per tile
     const int T = tg * tw + wave / kw, kq = wave % kw;
     const int q = (nbl + kw - 1) / kw;               // blocks per part (<= QB)
@@ -622,13 +631,16 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
         // sel[(wb+i) / enb]; a block past the part or of an unfilled slot
         // (id < 0) reads zeros (a record range of 0 bytes)
         const int enb = P.enb, tiles_e = ntiles;  // the stack's experts have rows_pad rows each
-        const int Tc = min(T, ntiles - 1);
+        const int Tc = min(T, ntiles - 1), top_k = P.top_k;
+        // the chosen experts' ids, slot l in lane l (one load for every
+        // block; reading them block by block cost a round trip each)
+        const int selv = (int)__builtin_amdgcn_raw_buffer_load_b32(buf_rsrc(P.sel, top_k * 4), (lane & 15) * 4, 0, 0);
         size_t recs[QB];
         int ok[QB];
 #pragma unroll
         for (int i = 0; i < QB; i++) {
             const int cb = wb + i, slot = cb / enb;
-            const int ei = i < qw ? P.sel[min(slot, P.top_k - 1)] : -1;
+            const int ei = i < qw ? __builtin_amdgcn_readlane(selv, min(slot, top_k - 1)) : -1;
             ok[i] = ei >= 0;
             recs[i] = ((size_t)max(ei, 0) * tiles_e + Tc) * enb + cb % enb;
         }
@@ -1005,15 +1017,15 @@ hipError_t launch_gemv_exact_multi(const GemvJob* jobs, int n, hipStream_t s)
         P.rows = (int)m.rows;
         P.nb = (int)m.nb;
         P.rows_pad = (int)m.rows_pad;
-        P.wg_begin = wgs;
-        wgs += (int)(m.rows_pad / (EX_WG / 8));
+        P.nwg = (int)(m.rows_pad / (EX_WG / 8));
+        wgs = std::max(wgs, P.nwg);
     }
     if (wgs == 0) return hipSuccess;
     (void)hipGetLastError();  // report only this launch
     if (scheme == 4)
-        hipLaunchKernelGGL(k_gemv_exact_multi<4>, dim3(wgs), dim3(EX_WG), 0, s, B);
+        hipLaunchKernelGGL(k_gemv_exact_multi<4>, dim3(wgs, n), dim3(EX_WG), 0, s, B);
     else
-        hipLaunchKernelGGL(k_gemv_exact_multi<3>, dim3(wgs), dim3(EX_WG), 0, s, B);
+        hipLaunchKernelGGL(k_gemv_exact_multi<3>, dim3(wgs, n), dim3(EX_WG), 0, s, B);
     return hipGetLastError();
 }
 
@@ -1043,7 +1055,6 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         P.rows_pad = (int)m.rows_pad;
         P.nb = (int)m.nb;
         P.kg = J.plan->kg;
-        P.wg_begin = wgs;
         P.sel = J.sel;
         P.sel_k = J.sel_k;
         P.tw = fast_tiles_per_wg(m.rows, J.routed ? (uint64_t)J.top_k * m.nb : m.nb);
@@ -1083,7 +1094,8 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
                          J.sel_k >= J.top_k || !J.ids_out || !J.w_out))
             return hipErrorInvalidValue;
         const int tiles = (int)(m.rows_pad / TILE_ROWS);
-        wgs += (tiles + P.tw - 1) / P.tw * P.kg;
+        P.nwg = (tiles + P.tw - 1) / P.tw * P.kg;
+        wgs = std::max(wgs, P.nwg);
     }
     if (wgs == 0) return hipSuccess;
     const int kind = jobs[0].routed ? FK_ROUTED : jobs[0].scores ? FK_ROUTE : FK_PLAIN;
@@ -1092,7 +1104,7 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         if ((jobs[i].routed ? FK_ROUTED : jobs[i].scores ? FK_ROUTE : FK_PLAIN) != kind || jobs[i].xform != xf)
             return hipErrorInvalidValue;
     (void)hipGetLastError();  // report only this launch
-    const dim3 grid(wgs), block(FAST_WG);
+    const dim3 grid(wgs, n), block(FAST_WG);
 #define WPCG_FAST(S, K, X) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<S, K, X>), grid, block, 0, s, B)
 #define WPCG_FAST_S(S)                                                               \
     do {                                                                             \
