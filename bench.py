@@ -51,9 +51,10 @@ BPB = {3: 100, 4: 68}
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (bench.py --pmc-pass) and scaled by
 # the same counters' reading for a copy kernel of known size; see
 # profiles/k_gemv_fast_cfg1_v3_traffic.txt. None where not measured.
-TRAFFIC = {(3, "fast"): 20061794}
+TRAFFIC = {(3, "fast"): 20033022}
 TRAFFIC_SOURCE = ("profiles/k_gemv_fast_cfg1_v3_traffic.txt: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
-                  "passes over bench.py --pmc-pass, scaled by a 256 MiB device copy's readings")
+                  "passes over bench.py --pmc-pass (the workload rotated over >= 1 GB, HBM-cold), scaled by "
+                  "a 256 MiB device copy's readings")
 
 
 def log(msg):
@@ -513,7 +514,71 @@ def cfg0_bench(ctx, wpcg, synth, min_bytes, cpu_budget):
     return rec
 
 
+def summarize_profile(out_dir, match=""):
+    """Print rocprofv3 CSV output (run on the CPU, after a traced run) grouped by
+    kernel and launch shape: kernel traces as launches, mean and median
+    duration (end - start), counter collections as the mean value of each
+    counter per dispatch. `match` keeps the kernels whose name contains it."""
+    import csv
+    import glob
+    import collections
+
+    def grid_of(row, axis):
+        g = int(row.get(f"Grid_Size_{axis}") or 1)
+        w = int(row.get(f"Workgroup_Size_{axis}") or 1)
+        return g // max(w, 1)
+
+    def short(name):
+        return name.replace("wpcg::(anonymous namespace)::", "").split("(")[0].replace("void ", "")
+
+    found = False
+    for path in sorted(glob.glob(os.path.join(out_dir, "**", "*kernel_trace.csv"), recursive=True)):
+        found = True
+        groups = collections.defaultdict(list)
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                if match and match not in row["Kernel_Name"]:
+                    continue
+                key = (short(row["Kernel_Name"]), grid_of(row, "X"), grid_of(row, "Y"))
+                groups[key].append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+        print(f"# {os.path.relpath(path, out_dir)}: kernel, workgroups x by y, launches, mean us, median us")
+        for (name, gx, gy), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+            print(f"{name:44s} {gx:6d} x {gy:<3d} {len(v):7d} {statistics.mean(v):9.2f} "
+                  f"{statistics.median(v):9.2f}")
+    for path in sorted(glob.glob(os.path.join(out_dir, "**", "*counter_collection.csv"), recursive=True)):
+        found = True
+        groups = collections.defaultdict(lambda: collections.defaultdict(float))
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                if match and match not in row["Kernel_Name"]:
+                    continue
+                wg = int(row.get("Workgroup_Size") or 1)
+                key = (short(row["Kernel_Name"]), int(row.get("Grid_Size") or 0) // max(wg, 1))
+                # one row per dispatch and counter (dimensions already summed)
+                did = int(row.get("Dispatch_Id") or row.get("Correlation_Id") or 0)
+                groups[key][(row["Counter_Name"], did)] += float(row["Counter_Value"])
+        print(f"# {os.path.relpath(path, out_dir)}: kernel, workgroups, counter, dispatches, "
+              "mean per dispatch, last dispatch")
+        for (name, wgs), vals in sorted(groups.items()):
+            per = collections.defaultdict(list)
+            for (cn, did), v in sorted(vals.items(), key=lambda kv: kv[0][1]):
+                per[cn].append(v)
+            for cn, v in sorted(per.items()):
+                print(f"{name:44s} {wgs:7d} {cn:28s} {len(v):6d} {statistics.mean(v):16.1f} {v[-1]:16.1f}")
+    if not found:
+        print(f"no rocprofv3 CSV output under {out_dir}", file=sys.stderr)
+        return 1
+    return 0
+
+
 def main():
+    if "--summarize" in sys.argv:
+        ap = argparse.ArgumentParser()
+        ap.add_argument("--summarize", required=True, metavar="DIR",
+                        help="print a rocprofv3 --output-format csv directory grouped by kernel and shape")
+        ap.add_argument("--match", default="", help="only kernels whose name contains this")
+        a = ap.parse_args()
+        return summarize_profile(a.summarize, a.match)
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
@@ -531,7 +596,7 @@ def main():
                     help="short run for rocprofv3 --pmc passes (no timing, no JSON)")
     ap.add_argument("--only", default="",
                     help="comma list of extra sections to run (per_shape,cfg0,large_gemv,gemm,decode,"
-                         "decode_dense); default: all")
+                         "decode_dense, or none for the config-1 line alone); default: all")
     ap.add_argument("--no-decode", action="store_true", help="skip both decode measurements")
     ap.add_argument("--decode-prompt", type=int, default=256)
     ap.add_argument("--decode-new", type=int, default=256)
@@ -557,7 +622,7 @@ def main():
         return 2
     sections = {"per_shape", "cfg0", "large_gemv", "gemm", "decode", "decode_dense"}
     if args.only:
-        want = {w.strip() for w in args.only.split(",") if w.strip()}
+        want = {w.strip() for w in args.only.split(",") if w.strip()} - {"none"}
         bad = want - sections
         if bad:
             print(f"--only: unknown sections {sorted(bad)}", file=sys.stderr)

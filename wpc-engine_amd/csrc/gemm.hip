@@ -143,10 +143,10 @@ __device__ __forceinline__ float out_val(float v, const float* bias, const float
     return v;
 }
 
-constexpr int GM_WG = GEMM_WG_THREADS;  // 4 waves (row tiles per workgroup: 4 * GM_RT)
-constexpr int GM_WG8 = 2 * GM_WG;       // the M > 16 kernel: two waves per tile pair
-constexpr int GM_RT = GEMM_TILES_PER_WAVE;
-constexpr int GM_LA = 4;                // blocks of codes and of X in flight per wave
+constexpr int GM_WG = GEMM_WG_THREADS;   // 8 waves, two per SIMD
+constexpr int GM_RT = GEMM_TILES_PER_WAVE;  // row tiles per wave: a row group is GM_WG / 64 * GM_RT = 8 tiles
+constexpr int GM_R = 4;                  // blocks of X per LDS round (one barrier per round)
+constexpr int GM_LA = GM_R;              // blocks of codes in flight per wave (one ring slot per block of a round)
 
 // Eight codes (two dwords of one byte each, every code < 128) -> the eight
 // bf16 values 128 + code, exact: their bit patterns are 0x4300 | code, so
@@ -167,31 +167,40 @@ __device__ __forceinline__ bf16x8 codes_bf16(uint32_t a, uint32_t b)
 // zero point of the offset codes: zp - 128 * scale
 __device__ __forceinline__ float zp_off(uint32_t p) { return __builtin_fmaf(-128.0f, h2f(p >> 16), h2f(p & 0xFFFFu)); }
 
-// A workgroup of 8 waves computes 4 * GM_RT row tiles for all NT*16
-// columns over one K-slice: wave w takes tiles (rg*4 + (w&3))*GM_RT.. and
-// the column tiles of half w>>2, so the two waves of a tile pair read the
-// same codes (the second read is a cache hit) and each runs half the matrix
-// work. Per block: the slice's X fragments come through LDS (double
-// buffered, shared by all waves), fetched into registers GM_LA blocks
-// ahead; the codes come straight from HBM into registers, GM_LA blocks
-// ahead. Every buffer load has an exact range, so loads past the slice
-// return zeros (a zero block adds exactly 0).
+// A workgroup of 8 waves (two per SIMD, so one wave's waits are filled by the
+// other's work) computes one row group (8 row tiles) for all NT*16 columns
+// over one K-slice. Wave w takes GM_RT tiles from rg*8 + w*GM_RT and every
+// column tile, so each tile's codes are unpacked once per block. The codes
+// come straight from HBM into registers, GM_LA blocks ahead.
+//
+// X goes through LDS in rounds of GM_R blocks, double buffered, with one
+// barrier per round: round r+1's fragments are fetched into registers at
+// the start of round r-1, stored into the free buffer at the start of round
+// r (after the barrier that ended round r-1, which every read of that
+// buffer preceded) and published by the barrier that ends round r. Each wave
+// reads a column tile's fragments from LDS one tile ahead of its matrix
+// work, so LDS reads overlap the dots; the barrier that ends a round sits
+// before the round's last tile, whose fragments are already in registers,
+// and is followed by the read of the next round's first tile.
+//
+// Every buffer load has an exact range: loads past the slice return zeros,
+// and a zero block adds exactly 0.
 //
 // SPLIT: column tiles [0, NT/2) are the hi parts and [NT/2, NT) the lo parts
-// of the same NT/2 column tiles (k_gemm_pack<*, true>), so wave half 0 runs
-// hi and half 1 lo over the same codes; after the loop half 1 hands its sums
-// to half 0 through LDS, which adds hi + lo and alone writes.
+// of the same NT/2 column tiles (k_gemm_pack<*, true>); after the loop the
+// wave adds each lo tile's sums to its hi tile's and writes the hi tiles.
 template <int SCHEME, int NT, bool SPLIT>
-__global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
+__global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P)
 {
     static_assert(!SPLIT || NT % 2 == 0, "split needs hi and lo tiles");
-    // each wave takes one row tile and every column tile, so a tile's codes
-    // are unpacked once per block
-    constexpr int RT = 1, NTH = NT;
-    static_assert(GM_WG8 / 64 * RT == 4 * GM_RT, "a row group is 8 tiles");
-    constexpr int XV = (NT * 4096 + GM_WG8 * 16 - 1) / (GM_WG8 * 16);  // 16-byte X loads per thread per block
-    __shared__ __align__(16) u32x4 xb[2][NT * 4 * 64];
-    __shared__ float xsb[2][NT * 16];
+    constexpr int RT = GM_RT;
+    static_assert(GM_WG / 64 * RT == 8, "a row group is 8 tiles");
+    constexpr int FW = NT * 256;                              // 16-byte X words per block
+    constexpr int XV = (GM_R * FW + GM_WG - 1) / GM_WG;       // X words per thread per round
+    constexpr int SN = GM_R * NT * 16;                        // X sums per round
+    constexpr int SV = (SN + GM_WG - 1) / GM_WG;
+    __shared__ __align__(16) u32x4 xb[2][GM_R * FW];
+    __shared__ float xsb[2][SN];
     __shared__ int s_last;
 
     const int kg = P.kg, nb = P.nb, XT = P.xt;
@@ -213,8 +222,7 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int g = lane >> 4, j = lane & 15;
     const int ntiles = P.rows_pad / TILE_ROWS;
-    const int T0 = rg * 8 + wave;
-    const int n0 = 0, n1 = NT;  // column tiles [n0, n1)
+    const int T0 = rg * 8 + wave * RT;
 
     __amdgpu_buffer_rsrc_t crs[RT], hrs[RT], prs[RT];
 #pragma unroll
@@ -241,51 +249,80 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
             pr[u][rt] = __builtin_amdgcn_raw_buffer_load_b128(prs[rt], b * 64 + g * 16, 0, CPOL_NT);
         }
     };
-    // X of block b: thread t holds 16-byte words t + v*GM_WG8 of the block's
-    // NT*256 words (a word past the block is never stored)
-    u32x4 xr[GM_LA][XV];
-    float sr[GM_LA];
-    auto load_x = [&](int u, int b) {
-#pragma unroll
-        for (int v = 0; v < XV; v++)
-            xr[u][v] = __builtin_amdgcn_raw_buffer_load_b128(
-                xrs, (b * XT * 256 + min((int)threadIdx.x + v * GM_WG8, NT * 256 - 1)) * 16, 0, 0);
-        sr[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-            srs, (b * XT * 16 + min((int)threadIdx.x, NT * 16 - 1)) * 4, 0, 0));
-    };
-    auto store_x = [&](int u, int buf) {
+    // X of round r: thread t holds the round's 16-byte words t + v*GM_WG
+    // (block r*GM_R + word / FW, word % FW of it) and sums t + v*GM_WG
+    // (block r*GM_R + i / (NT*16), column i % (NT*16)).
+    u32x4 xr[XV];
+    float sr[SV];
+    auto load_round = [&](int r) {
 #pragma unroll
         for (int v = 0; v < XV; v++) {
-            const int w = threadIdx.x + v * GM_WG8;
-            if (w < NT * 256) xb[buf][w] = xr[u][v];
+            const int i = min((int)threadIdx.x + v * GM_WG, GM_R * FW - 1);
+            xr[v] = __builtin_amdgcn_raw_buffer_load_b128(xrs, ((r * GM_R + i / FW) * XT * 256 + i % FW) * 16, 0, 0);
         }
-        if (threadIdx.x < NT * 16) xsb[buf][threadIdx.x] = sr[u];
+#pragma unroll
+        for (int v = 0; v < SV; v++) {
+            const int i = min((int)threadIdx.x + v * GM_WG, SN - 1);
+            sr[v] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                srs, ((r * GM_R + i / (NT * 16)) * XT * 16 + i % (NT * 16)) * 4, 0, 0));
+        }
+    };
+    auto store_round = [&](int buf) {
+#pragma unroll
+        for (int v = 0; v < XV; v++) {
+            const int i = threadIdx.x + v * GM_WG;
+            if (i < GM_R * FW) xb[buf][i] = xr[v];
+        }
+#pragma unroll
+        for (int v = 0; v < SV; v++) {
+            const int i = threadIdx.x + v * GM_WG;
+            if (i < SN) xsb[buf][i] = sr[v];
+        }
+    };
+    // the fragments of column tile n of block u of a round buffer, and the
+    // tile's column sum for this lane's column
+    auto read_tile = [&](bf16x8 (&B)[4], float& S, int buf, int u, int n) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const u32x4 w = xb[buf][u * FW + (n * 4 + i) * 64 + lane];
+            __builtin_memcpy(&B[i], &w, 16);
+        }
+        S = xsb[buf][u * NT * 16 + n * 16 + j];
     };
 
+    // prologue: round 0 and the first GM_LA blocks of codes, then round 1,
+    // in the order the loop keeps (so the wait counts at its head match)
+    load_round(0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < GM_LA; u++) load_x(u, u);
-#pragma unroll
-    for (int u = 0; u < GM_LA; u++) load_codes(u, u);
-    store_x(0, 0);
+    for (int u = 0; u < GM_LA; u++) {
+        load_codes(u, u);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    store_round(0);
+    load_round(1);
     __syncthreads();
 
-    f32x4 acc[RT][NTH];
+    f32x4 acc[RT][NT];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-        for (int n = 0; n < NTH; n++) acc[rt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int n = 0; n < NT; n++) acc[rt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Whole rounds of GM_LA unconditional steps (guarded steps would merge
-    // the wait-counter state at the loop edge and drain every load in
-    // flight once per round). Step b: fetch X(b + GM_LA) into the register
-    // slot X(b) left (it went to LDS a step ago), compute block b, refill
-    // the codes slot, move X(b+1) into the other LDS buffer, barrier.
-    const int steps = (nbl + GM_LA - 1) / GM_LA * GM_LA;
-    for (int bl = 0; bl < steps; bl += GM_LA) {
+    bf16x8 Bc[4];
+    float Sc;
+    read_tile(Bc, Sc, 0, 0, 0);
+
+    // Whole rounds of unconditional steps (guarded steps would merge the
+    // wait-counter state at the loop edge and drain every load in flight).
+    const int nrounds = (nbl + GM_R - 1) / GM_R;
+    for (int r = 0; r < nrounds; r++) {
+        const int buf = r & 1;
+        store_round(buf ^ 1);  // round r+1 into the buffer round r-1 left
+        load_round(r + 2);
 #pragma unroll
-        for (int u = 0; u < GM_LA; u++) {
-            const int b = bl + u, buf = u & 1;
-            load_x(u, b + GM_LA);
+        for (int u = 0; u < GM_R; u++) {
+            const int b = r * GM_R + u;
             bf16x8 A[RT][4];
             float sc[RT][4], zp[RT][4];
 #pragma unroll
@@ -313,34 +350,36 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
             }
             load_codes(u, b + GM_LA);
 #pragma unroll
-            for (int nn = 0; nn < NTH; nn++) {
-                const int n = n0 + nn;
-                if (n < n1) {  // uniform
-                    bf16x8 B[4];
+            for (int n = 0; n < NT; n++) {
+                // the next tile's fragments: this round's buffer, or (before
+                // the round's last tile, after the barrier) the next round's
+                bf16x8 Bn[4];
+                float Sn;
+                if (n + 1 < NT) {
+                    read_tile(Bn, Sn, buf, u, n + 1);
+                } else if (u + 1 < GM_R) {
+                    read_tile(Bn, Sn, buf, u + 1, 0);
+                } else {
+                    __syncthreads();
+                    read_tile(Bn, Sn, buf ^ 1, 0, 0);
+                }
+                f32x4 D[RT];
 #pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const u32x4 w = xb[buf][(n * 4 + i) * 64 + lane];
-                        __builtin_memcpy(&B[i], &w, 16);
-                    }
-                    const float S = xsb[buf][n * 16 + j];
-                    f32x4 D[RT];
+                for (int rt = 0; rt < RT; rt++) D[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                    for (int rt = 0; rt < RT; rt++) D[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int i = 0; i < 4; i++)
-#pragma unroll
-                        for (int rt = 0; rt < RT; rt++)
-                            D[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[rt][i], B[i], D[rt], 0, 0, 0);
+                for (int i = 0; i < 4; i++)
 #pragma unroll
                     for (int rt = 0; rt < RT; rt++)
+                        D[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[rt][i], Bc[i], D[rt], 0, 0, 0);
 #pragma unroll
-                        for (int q = 0; q < 4; q++)
-                            acc[rt][nn][q] = __builtin_fmaf(zp[rt][q], S, __builtin_fmaf(sc[rt][q], D[rt][q], acc[rt][nn][q]));
-                }
+                for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        acc[rt][n][q] = __builtin_fmaf(zp[rt][q], Sc, __builtin_fmaf(sc[rt][q], D[rt][q], acc[rt][n][q]));
+#pragma unroll
+                for (int i = 0; i < 4; i++) Bc[i] = Bn[i];
+                Sc = Sn;
             }
-            store_x((u + 1) % GM_LA, buf ^ 1);  // X(b+1), fetched GM_LA-1 steps ago
-            __syncthreads();
-            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
@@ -350,8 +389,8 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
 #pragma unroll
             for (int n = 0; n < NT / 2; n++) acc[rt][n] = acc[rt][n] + acc[rt][n + NT / 2];
     }
-    // the column tiles this wave writes: [c0, c1) (SPLIT: half 0, the hi tiles)
-    const int c0 = 0, c1 = SPLIT ? NT / 2 : NT;
+    // the column tiles this wave writes: [0, NW) (SPLIT: the hi tiles)
+    constexpr int NW = SPLIT ? NT / 2 : NT;
 
     // lane (g, j) holds rows 4g..4g+3 of each tile for column n*16 + j
     const int Mp = NT * 16;
@@ -359,13 +398,13 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
 #pragma unroll
         for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-            for (int nn = 0; nn < NTH; nn++) {
-                const int n = c0 + nn, m = mcol0 + n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
-                if (n >= c1 || m >= P.M) continue;
+            for (int n = 0; n < NW; n++) {
+                const int m = mcol0 + n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
+                if (m >= P.M) continue;
 #pragma unroll
                 for (int q = 0; q < 4; q++)
                     if (row + q < P.rows)
-                        P.y[(size_t)m * P.rows + row + q] = out_val(acc[rt][nn][q], P.bias, P.res, P.rows, m, row + q);
+                        P.y[(size_t)m * P.rows + row + q] = out_val(acc[rt][n][q], P.bias, P.res, P.rows, m, row + q);
             }
         return;
     }
@@ -379,11 +418,11 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-        for (int nn = 0; nn < NTH; nn++) {
-            const int n = c0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
-            if (n < c1 && T0 + rt < ntiles) {
+        for (int n = 0; n < NW; n++) {
+            const int m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
+            if (T0 + rt < ntiles) {
                 u32x4 v;
-                __builtin_memcpy(&v, &acc[rt][nn], 16);
+                __builtin_memcpy(&v, &acc[rt][n], 16);
                 __builtin_amdgcn_raw_buffer_store_b128(v, prt, ((kgi * Mp + m) * P.rows_pad + row) * 4, 0, CPOL_SC1);
             }
         }
@@ -395,23 +434,45 @@ __global__ __launch_bounds__(GM_WG8) void k_gemm(const GemmArgs P)
     }
     __syncthreads();
     if (!s_last) return;
+    // The slices in slice order. Every load of GM_KC slices (all written
+    // column tiles) is issued before the first add, so a chunk costs one
+    // round trip to the coherence point; slices past kg read as zeros (past
+    // the buffer's range) and are not added.
+    constexpr int GM_KC = 8;
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++)
+    for (int rt = 0; rt < RT; rt++) {
+        const int row = (T0 + rt) * TILE_ROWS + 4 * g;
+        f32x4 s[NW];
+        for (int k0 = 0; k0 < kg; k0 += GM_KC) {
+            u32x4 v[GM_KC][NW];
 #pragma unroll
-        for (int nn = 0; nn < NTH; nn++) {
-            const int n = c0 + nn, m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
-            if (n >= c1 || T0 + rt >= ntiles || m >= P.M) continue;
-            f32x4 s = {0.f, 0.f, 0.f, 0.f};
-            for (int k = 0; k < kg; k++) {
-                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(prt, ((k * Mp + m) * P.rows_pad + row) * 4, 0, CPOL_SC1);
-                f32x4 f;
-                __builtin_memcpy(&f, &v, 16);
-                s = k == 0 ? f : s + f;
-            }
+            for (int kk = 0; kk < GM_KC; kk++)
+#pragma unroll
+                for (int n = 0; n < NW; n++) {
+                    const int m = n * 16 + j, k = k0 + kk;
+                    v[kk][n] = __builtin_amdgcn_raw_buffer_load_b128(
+                        prt, k < kg ? ((k * Mp + m) * P.rows_pad + row) * 4 : 0x7FFFFFF0, 0, CPOL_SC1);
+                }
+#pragma unroll
+            for (int kk = 0; kk < GM_KC; kk++)
+                if (k0 + kk < kg)
+#pragma unroll
+                    for (int n = 0; n < NW; n++) {
+                        f32x4 f;
+                        __builtin_memcpy(&f, &v[kk][n], 16);
+                        s[n] = k0 + kk == 0 ? f : s[n] + f;
+                    }
+        }
+        if (T0 + rt >= ntiles) continue;
+#pragma unroll
+        for (int n = 0; n < NW; n++) {
+            const int m = mcol0 + n * 16 + j;
+            if (m >= P.M) continue;
 #pragma unroll
             for (int q = 0; q < 4; q++)
-                if (row + q < P.rows) P.y[(size_t)m * P.rows + row + q] = out_val(s[q], P.bias, P.res, P.rows, m, row + q);
+                if (row + q < P.rows) P.y[(size_t)m * P.rows + row + q] = out_val(s[n][q], P.bias, P.res, P.rows, m, row + q);
         }
+    }
     if (threadIdx.x == 0) __hip_atomic_store(P.counters + rg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -678,12 +739,22 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
     __syncthreads();
     if (!s_last) return;
     if (writer && j < M) {
+        // the slices in slice order, GS_KC loads in flight before the adds
+        constexpr int GS_KC = 16;
         f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-        for (int k = 0; k < kg; k++) {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(prt, ((k * 16 + j) * P.rows_pad + row) * 4, 0, CPOL_SC1);
-            f32x4 f;
-            __builtin_memcpy(&f, &v, 16);
-            sum = k == 0 ? f : sum + f;
+        for (int k0 = 0; k0 < kg; k0 += GS_KC) {
+            u32x4 v[GS_KC];
+#pragma unroll
+            for (int kk = 0; kk < GS_KC; kk++)
+                v[kk] = __builtin_amdgcn_raw_buffer_load_b128(
+                    prt, k0 + kk < kg ? (((k0 + kk) * 16 + j) * P.rows_pad + row) * 4 : 0x7FFFFFF0, 0, CPOL_SC1);
+#pragma unroll
+            for (int kk = 0; kk < GS_KC; kk++)
+                if (k0 + kk < kg) {
+                    f32x4 f;
+                    __builtin_memcpy(&f, &v[kk], 16);
+                    sum = k0 + kk == 0 ? f : sum + f;
+                }
         }
 #pragma unroll
         for (int q = 0; q < 4; q++)
@@ -903,13 +974,13 @@ template <int SCHEME, bool SPLIT>
 hipError_t launch_nt(int nt, dim3 grid, hipStream_t s, const GemmArgs& a)
 {
     if constexpr (SPLIT) {
-        if (nt == 2) hipLaunchKernelGGL((k_gemm<SCHEME, 2, true>), grid, dim3(GM_WG8), 0, s, a);
-        else hipLaunchKernelGGL((k_gemm<SCHEME, 4, true>), grid, dim3(GM_WG8), 0, s, a);
+        if (nt == 2) hipLaunchKernelGGL((k_gemm<SCHEME, 2, true>), grid, dim3(GM_WG), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm<SCHEME, 4, true>), grid, dim3(GM_WG), 0, s, a);
     } else {
         switch (nt) {
-        case 2: hipLaunchKernelGGL((k_gemm<SCHEME, 2, false>), grid, dim3(GM_WG8), 0, s, a); break;
-        case 3: hipLaunchKernelGGL((k_gemm<SCHEME, 3, false>), grid, dim3(GM_WG8), 0, s, a); break;
-        default: hipLaunchKernelGGL((k_gemm<SCHEME, 4, false>), grid, dim3(GM_WG8), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((k_gemm<SCHEME, 2, false>), grid, dim3(GM_WG), 0, s, a); break;
+        case 3: hipLaunchKernelGGL((k_gemm<SCHEME, 3, false>), grid, dim3(GM_WG), 0, s, a); break;
+        default: hipLaunchKernelGGL((k_gemm<SCHEME, 4, false>), grid, dim3(GM_WG), 0, s, a); break;
         }
     }
     return hipGetLastError();

@@ -169,9 +169,10 @@ inline int fast_normalize_kslices(uint64_t nb, int kg)
 // Y = X W^T for up to GEMM_MAX_M activations per launch. Up to 16 columns one
 // kernel packs X into LDS itself (a wave per row tile, K-slices of at most
 // GEMM_SMALL_MAXBK blocks); above that X is packed by a first kernel and a
-// workgroup of 4 waves covers 4 * GEMM_TILES_PER_WAVE row tiles.
-constexpr int GEMM_WG_THREADS = 256;
-constexpr int GEMM_TILES_PER_WAVE = 2;
+// workgroup of GEMM_WG_THREADS / 64 waves covers a row group of 8 row tiles,
+// GEMM_TILES_PER_WAVE per wave.
+constexpr int GEMM_WG_THREADS = 512;
+constexpr int GEMM_TILES_PER_WAVE = 1;
 constexpr int GEMM_MAX_M = 64;
 constexpr int GEMM_SMALL_MAXBK = 30;
 // Workspace of one matrix, sized for GEMM_MAX_M columns; fixed once made so
