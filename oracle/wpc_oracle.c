@@ -19,6 +19,7 @@
 #include <math.h>
 #include <pthread.h>
 #include <stdatomic.h>
+#include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -445,21 +446,116 @@ static void* par_worker(void* arg)
     return NULL;
 }
 
+/* A persistent worker pool, as rayon's global pool in the reference: worker
+ * threads are started on first need; between jobs each spins briefly on the
+ * job generation and then sleeps on a condition variable, so a call costs a
+ * wake-up (or nothing, when calls follow closely) rather than thread
+ * creation, which made a decode step slower on 16 threads than on one. One
+ * job runs at a time; the caller takes part and returns when every worker it
+ * woke is done. After fork() the child starts with an empty pool. */
+#define POOL_MAX 255
+#define POOL_SPIN 1024 /* pause iterations before sleeping (tens of us) */
+static struct {
+    pthread_mutex_t mu;
+    pthread_cond_t cv_job, cv_done;
+    int nworkers;          /* started, excluding callers */
+    atomic_ulong gen;      /* job generation */
+    _Atomic(par_job*) job;
+    atomic_int want;       /* workers with id < want take part in the job */
+    atomic_int pending;    /* of those, not yet done */
+} g_pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER, PTHREAD_COND_INITIALIZER, 0, 0, NULL, 0, 0};
+static pthread_mutex_t g_pool_call = PTHREAD_MUTEX_INITIALIZER;
+static pthread_once_t g_pool_once = PTHREAD_ONCE_INIT;
+/* the job generation when worker i was started: it first runs the next one
+ * (the job it was started for, published before it can take the lock) */
+static unsigned long g_pool_gen0[POOL_MAX];
+
+static inline void cpu_pause(void)
+{
+#if defined(__x86_64__)
+    _mm_pause();
+#endif
+}
+
+static void pool_reset_in_child(void)
+{
+    pthread_mutex_init(&g_pool.mu, NULL);
+    pthread_cond_init(&g_pool.cv_job, NULL);
+    pthread_cond_init(&g_pool.cv_done, NULL);
+    pthread_mutex_init(&g_pool_call, NULL);
+    g_pool.nworkers = 0;
+    atomic_store(&g_pool.gen, 0);
+    atomic_store(&g_pool.job, NULL);
+    atomic_store(&g_pool.want, 0);
+    atomic_store(&g_pool.pending, 0);
+}
+static void pool_init_once(void) { pthread_atfork(NULL, NULL, pool_reset_in_child); }
+
+static void* pool_worker(void* arg)
+{
+    const int id = (int)(intptr_t)arg;  /* 0-based among the workers */
+    pthread_mutex_lock(&g_pool.mu);
+    unsigned long seen = g_pool_gen0[id];
+    pthread_mutex_unlock(&g_pool.mu);
+    for (;;) {
+        for (int i = 0; i < POOL_SPIN && atomic_load(&g_pool.gen) == seen; i++) cpu_pause();
+        if (atomic_load(&g_pool.gen) == seen) {
+            pthread_mutex_lock(&g_pool.mu);
+            while (atomic_load(&g_pool.gen) == seen) pthread_cond_wait(&g_pool.cv_job, &g_pool.mu);
+            pthread_mutex_unlock(&g_pool.mu);
+        }
+        /* job and want are stored before the generation's increment, and no
+         * new job starts before this one's pending count reaches zero */
+        seen = atomic_load(&g_pool.gen);
+        const int take = id < atomic_load(&g_pool.want);
+        par_job* j = atomic_load(&g_pool.job);
+        if (!take) continue;
+        par_worker(j);
+        if (atomic_fetch_sub(&g_pool.pending, 1) == 1) {
+            pthread_mutex_lock(&g_pool.mu);
+            pthread_cond_signal(&g_pool.cv_done);
+            pthread_mutex_unlock(&g_pool.mu);
+        }
+    }
+    return NULL;
+}
+
 static void parallel_rows(size_t n, int threads, row_fn fn, void* ctx)
 {
     if (threads <= 1 || n < 64) { fn(ctx, 0, n); return; }
-    if (threads > 256) threads = 256;
+    if (threads > POOL_MAX + 1) threads = POOL_MAX + 1;
+    pthread_once(&g_pool_once, pool_init_once);
     par_job j;
     j.fn = fn; j.ctx = ctx; j.n = n;
     j.chunk = n / ((size_t)threads * 8);
     if (j.chunk < 16) j.chunk = 16;
     atomic_init(&j.next, 0);
-    pthread_t tid[256];
-    int started = 0;
-    for (int t = 1; t < threads; t++)
-        if (pthread_create(&tid[started], NULL, par_worker, &j) == 0) started++;
+    pthread_mutex_lock(&g_pool_call);
+    pthread_mutex_lock(&g_pool.mu);
+    while (g_pool.nworkers < threads - 1) {
+        pthread_t t;
+        pthread_attr_t at;
+        pthread_attr_init(&at);
+        pthread_attr_setdetachstate(&at, PTHREAD_CREATE_DETACHED);
+        g_pool_gen0[g_pool.nworkers] = atomic_load(&g_pool.gen);
+        const int ok = pthread_create(&t, &at, pool_worker, (void*)(intptr_t)g_pool.nworkers) == 0;
+        pthread_attr_destroy(&at);
+        if (!ok) break;
+        g_pool.nworkers++;
+    }
+    const int w = g_pool.nworkers < threads - 1 ? g_pool.nworkers : threads - 1;
+    atomic_store(&g_pool.job, &j);
+    atomic_store(&g_pool.want, w);
+    atomic_store(&g_pool.pending, w);
+    atomic_fetch_add(&g_pool.gen, 1);
+    pthread_cond_broadcast(&g_pool.cv_job);
+    pthread_mutex_unlock(&g_pool.mu);
     par_worker(&j);
-    for (int t = 0; t < started; t++) pthread_join(tid[t], NULL);
+    for (int i = 0; i < POOL_SPIN && atomic_load(&g_pool.pending) > 0; i++) cpu_pause();
+    pthread_mutex_lock(&g_pool.mu);
+    while (atomic_load(&g_pool.pending) > 0) pthread_cond_wait(&g_pool.cv_done, &g_pool.mu);
+    pthread_mutex_unlock(&g_pool.mu);
+    pthread_mutex_unlock(&g_pool_call);
 }
 
 typedef struct {
