@@ -67,6 +67,45 @@ __device__ __forceinline__ float ordered_sumsq(const float* v, int n)
     return s;
 }
 
+// ((0 + q0) + q1) + ... in index order, by one thread, from 16-byte aligned
+// LDS (q = the squares, rounded, already computed by the whole workgroup): the
+// chain is one addition per value, with eight 16-byte reads in flight ahead
+// of it (clamped in bounds, no branch in the loop).
+__device__ __forceinline__ float ordered_sum_lds(const float* q, int n)
+{
+    const float4* q4 = reinterpret_cast<const float4*>(q);
+    const int n4 = n >> 2;
+    float s = 0.0f;
+    if (n4 > 0) {
+        constexpr int D = 8;
+        float4 buf[D];
+#pragma unroll
+        for (int u = 0; u < D; u++) buf[u] = q4[min(u, n4 - 1)];
+        int c = 0;
+        for (; c + D <= n4; c += D) {
+#pragma unroll
+            for (int u = 0; u < D; u++) {
+                const float4 v = buf[u];
+                buf[u] = q4[min(c + D + u, n4 - 1)];  // the next group's
+                s = __fadd_rn(s, v.x);
+                s = __fadd_rn(s, v.y);
+                s = __fadd_rn(s, v.z);
+                s = __fadd_rn(s, v.w);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < D; u++)  // buf[u] holds float4 c + u
+            if (c + u < n4) {
+                s = __fadd_rn(s, buf[u].x);
+                s = __fadd_rn(s, buf[u].y);
+                s = __fadd_rn(s, buf[u].z);
+                s = __fadd_rn(s, buf[u].w);
+            }
+    }
+    for (int i = n4 * 4; i < n; i++) s = __fadd_rn(s, q[i]);
+    return s;
+}
+
 template <int MODE>
 __device__ float sum_squares(const float* x, int n, float* red)
 {
@@ -90,8 +129,8 @@ __device__ float sum_squares(const float* x, int n, float* red)
 }
 
 // x is staged in LDS once (n <= RN_LDS; longer vectors are read from global
-// memory twice): EXACT's index-order sum of squares then runs from LDS in one
-// thread, FAST's from registers as a tree.
+// memory twice). EXACT: the workgroup also stores every square (rounded) in
+// LDS, and one thread adds them in index order; FAST: a tree from registers.
 constexpr int RN_LDS = 8192;
 template <int MODE>
 __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
@@ -101,6 +140,7 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
     x += (size_t)blockIdx.x * n;  // row blockIdx.x of a batch (one row: 0)
     out += (size_t)blockIdx.x * n;
     __shared__ __align__(16) float xs[RN_LDS];
+    __shared__ __align__(16) float sq[MODE == WPCG_MODE_EXACT ? RN_LDS : 4];
     __shared__ float red[NW / 64];
     __shared__ float s_total;
     const bool staged = n <= RN_LDS;
@@ -108,12 +148,15 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
     float part = 0.0f;
     for (int i = threadIdx.x; i < n; i += NW) {
         const float v = x[i];
-        if (staged) xs[i] = v;
+        if (staged) {
+            xs[i] = v;
+            if (MODE == WPCG_MODE_EXACT) sq[i] = __fmul_rn(v, v);
+        }
         part = fmaf(v, v, part);
     }
     if (MODE == WPCG_MODE_EXACT) {
         __syncthreads();
-        if (threadIdx.x == 0) s_total = staged ? ordered_sumsq(xs, n) : ordered_sumsq(x, n);
+        if (threadIdx.x == 0) s_total = staged ? ordered_sum_lds(sq, n) : ordered_sumsq(x, n);
     } else {
         part = wave_sum(part);
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = part;

@@ -92,15 +92,37 @@ __global__ __launch_bounds__(256) void k_dense_exact_lds(const float* __restrict
         const int b = c & 1;
         if (c + 1 < nch) load(c + 1);
         if (t < DE_ROWS) {
-            const int len = min(DE_K, in_f - c * DE_K);
-            for (int k = 0; k < len; k += 4) {
-                const float4 v = *reinterpret_cast<const float4*>(&ws[b][t][k]);
-                const float4 xx = *reinterpret_cast<const float4*>(&xs[b][k]);
+            // the chunk's chain, eight 16-byte reads of W and of x in flight
+            // ahead of it (clamped in bounds, no branch in the loop)
+            const int l4 = min(DE_K, in_f - c * DE_K) >> 2;  // in_f % 4 == 0
+            const float4* wr = reinterpret_cast<const float4*>(&ws[b][t][0]);
+            const float4* xr = reinterpret_cast<const float4*>(&xs[b][0]);
+            constexpr int D = 8;
+            float4 wb[D], xb[D];
+#pragma unroll
+            for (int u = 0; u < D; u++) {
+                wb[u] = wr[min(u, l4 - 1)];
+                xb[u] = xr[min(u, l4 - 1)];
+            }
+            auto step = [&](const float4& v, const float4& xx) {
                 acc = __fadd_rn(acc, __fmul_rn(v.x, xx.x));
                 acc = __fadd_rn(acc, __fmul_rn(v.y, xx.y));
                 acc = __fadd_rn(acc, __fmul_rn(v.z, xx.z));
                 acc = __fadd_rn(acc, __fmul_rn(v.w, xx.w));
+            };
+            int k = 0;
+            for (; k + D <= l4; k += D) {
+#pragma unroll
+                for (int u = 0; u < D; u++) {
+                    const float4 v = wb[u], xx = xb[u];
+                    wb[u] = wr[min(k + D + u, l4 - 1)];
+                    xb[u] = xr[min(k + D + u, l4 - 1)];
+                    step(v, xx);
+                }
             }
+#pragma unroll
+            for (int u = 0; u < D; u++)  // wb[u], xb[u] hold float4 k + u
+                if (k + u < l4) step(wb[u], xb[u]);
         }
         if (c + 1 < nch) store(b ^ 1);
         __syncthreads();
