@@ -68,41 +68,43 @@ __device__ __forceinline__ float ordered_sumsq(const float* v, int n)
 }
 
 // ((0 + q0) + q1) + ... in index order, by one thread, from 16-byte aligned
-// LDS (q = the squares, rounded, already computed by the whole workgroup): the
-// chain is one addition per value, with eight 16-byte reads in flight ahead
-// of it (clamped in bounds, no branch in the loop).
+// LDS (q = the squares, rounded, already computed by the whole workgroup and
+// padded with +0.0 to a multiple of 64 values: adding +0.0 to the sum, which
+// starts at +0.0 and never becomes -0.0, changes nothing). The chain is one
+// addition per value; each group of 32 values is read from LDS a whole group
+// ahead of its additions (two register sets, the reads pinned in place).
+constexpr int OS_GROUP = 8;  // float4s per group
 __device__ __forceinline__ float ordered_sum_lds(const float* q, int n)
 {
     const float4* q4 = reinterpret_cast<const float4*>(q);
-    const int n4 = n >> 2;
+    const int ng = (n + 4 * OS_GROUP - 1) / (4 * OS_GROUP);  // groups of 32 values
     float s = 0.0f;
-    if (n4 > 0) {
-        constexpr int D = 8;
-        float4 buf[D];
+    float4 A[OS_GROUP], B[OS_GROUP];
+    auto add = [&](const float4 (&v)[OS_GROUP]) {
 #pragma unroll
-        for (int u = 0; u < D; u++) buf[u] = q4[min(u, n4 - 1)];
-        int c = 0;
-        for (; c + D <= n4; c += D) {
-#pragma unroll
-            for (int u = 0; u < D; u++) {
-                const float4 v = buf[u];
-                buf[u] = q4[min(c + D + u, n4 - 1)];  // the next group's
-                s = __fadd_rn(s, v.x);
-                s = __fadd_rn(s, v.y);
-                s = __fadd_rn(s, v.z);
-                s = __fadd_rn(s, v.w);
-            }
+        for (int u = 0; u < OS_GROUP; u++) {
+            s = __fadd_rn(s, v[u].x);
+            s = __fadd_rn(s, v[u].y);
+            s = __fadd_rn(s, v[u].z);
+            s = __fadd_rn(s, v[u].w);
         }
+    };
 #pragma unroll
-        for (int u = 0; u < D; u++)  // buf[u] holds float4 c + u
-            if (c + u < n4) {
-                s = __fadd_rn(s, buf[u].x);
-                s = __fadd_rn(s, buf[u].y);
-                s = __fadd_rn(s, buf[u].z);
-                s = __fadd_rn(s, buf[u].w);
-            }
+    for (int u = 0; u < OS_GROUP; u++) A[u] = q4[u];
+    int g = 0;
+    for (; g + 2 <= ng; g += 2) {
+#pragma unroll
+        for (int u = 0; u < OS_GROUP; u++) B[u] = q4[(g + 1) * OS_GROUP + u];
+        __builtin_amdgcn_sched_barrier(0);
+        add(A);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < OS_GROUP; u++) A[u] = q4[(g + 2) * OS_GROUP + u];
+        __builtin_amdgcn_sched_barrier(0);
+        add(B);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    for (int i = n4 * 4; i < n; i++) s = __fadd_rn(s, q[i]);
+    if (g < ng) add(A);  // an odd last group
     return s;
 }
 
@@ -140,7 +142,9 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
     x += (size_t)blockIdx.x * n;  // row blockIdx.x of a batch (one row: 0)
     out += (size_t)blockIdx.x * n;
     __shared__ __align__(16) float xs[RN_LDS];
-    __shared__ __align__(16) float sq[MODE == WPCG_MODE_EXACT ? RN_LDS : 4];
+    // the squares, padded with zeros to a multiple of 64 and one group past
+    // that (the chain reads one group ahead)
+    __shared__ __align__(16) float sq[MODE == WPCG_MODE_EXACT ? RN_LDS + 96 : 4];
     __shared__ float red[NW / 64];
     __shared__ float s_total;
     const bool staged = n <= RN_LDS;
@@ -155,6 +159,8 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
         part = fmaf(v, v, part);
     }
     if (MODE == WPCG_MODE_EXACT) {
+        if (staged)
+            for (int i = n + threadIdx.x; i < (n + 63) / 64 * 64 + 32; i += NW) sq[i] = 0.0f;
         __syncthreads();
         if (threadIdx.x == 0) s_total = staged ? ordered_sum_lds(sq, n) : ordered_sumsq(x, n);
     } else {

@@ -48,16 +48,20 @@ __global__ __launch_bounds__(64) void k_dense_exact(const float* __restrict__ w,
 // The same sums for in_f % 4 == 0, sixteen rows per workgroup: the whole
 // workgroup stages K chunks of the rows (and of x) into LDS, double
 // buffered, while lanes 0..15 of wave 0 run their rows' index-order chains
-// from LDS (rows padded by four floats: the sixteen rows' 16-byte reads hit
-// distinct banks).
-constexpr int DE_ROWS = 16, DE_K = 512;
+// from LDS (a row's stride is 4 floats past a multiple of 32, so the sixteen
+// rows' 16-byte reads hit distinct banks). Each lane reads a group of 32
+// values a whole group ahead of its chain (two register sets); a chunk's
+// values past in_f are zeros (adding w*x = +-0 to the sum changes nothing:
+// it starts at +0.0 and never becomes -0.0), and each row and x keep one
+// group of slack past the chunk for the read ahead, never added.
+constexpr int DE_ROWS = 16, DE_K = 512, DE_G = 8;  // DE_G float4s per group
 __global__ __launch_bounds__(256) void k_dense_exact_lds(const float* __restrict__ w,
                                                         const float* __restrict__ x,
                                                         const float* __restrict__ bias,
                                                         float* __restrict__ y, int out_f, int in_f)
 {
-    __shared__ __align__(16) float ws[2][DE_ROWS][DE_K + 4];
-    __shared__ __align__(16) float xs[2][DE_K];
+    __shared__ __align__(16) float ws[2][DE_ROWS][DE_K + 4 + 4 * DE_G];
+    __shared__ __align__(16) float xs[2][DE_K + 4 * DE_G];
     const int r0 = blockIdx.x * DE_ROWS, t = threadIdx.x;
     const int nch = (in_f + DE_K - 1) / DE_K;
     constexpr int PER = DE_ROWS * DE_K / 4 / 256;  // 16-byte loads of W per thread and chunk
@@ -92,37 +96,40 @@ __global__ __launch_bounds__(256) void k_dense_exact_lds(const float* __restrict
         const int b = c & 1;
         if (c + 1 < nch) load(c + 1);
         if (t < DE_ROWS) {
-            // the chunk's chain, eight 16-byte reads of W and of x in flight
-            // ahead of it (clamped in bounds, no branch in the loop)
-            const int l4 = min(DE_K, in_f - c * DE_K) >> 2;  // in_f % 4 == 0
+            const int len = min(DE_K, in_f - c * DE_K);
+            const int ng = (len + 4 * DE_G - 1) / (4 * DE_G);  // groups of 32 values
             const float4* wr = reinterpret_cast<const float4*>(&ws[b][t][0]);
             const float4* xr = reinterpret_cast<const float4*>(&xs[b][0]);
-            constexpr int D = 8;
-            float4 wb[D], xb[D];
+            float4 WA[DE_G], XA[DE_G], WB[DE_G], XB[DE_G];
+            auto read = [&](float4 (&W)[DE_G], float4 (&X)[DE_G], int g) {
 #pragma unroll
-            for (int u = 0; u < D; u++) {
-                wb[u] = wr[min(u, l4 - 1)];
-                xb[u] = xr[min(u, l4 - 1)];
-            }
-            auto step = [&](const float4& v, const float4& xx) {
-                acc = __fadd_rn(acc, __fmul_rn(v.x, xx.x));
-                acc = __fadd_rn(acc, __fmul_rn(v.y, xx.y));
-                acc = __fadd_rn(acc, __fmul_rn(v.z, xx.z));
-                acc = __fadd_rn(acc, __fmul_rn(v.w, xx.w));
-            };
-            int k = 0;
-            for (; k + D <= l4; k += D) {
-#pragma unroll
-                for (int u = 0; u < D; u++) {
-                    const float4 v = wb[u], xx = xb[u];
-                    wb[u] = wr[min(k + D + u, l4 - 1)];
-                    xb[u] = xr[min(k + D + u, l4 - 1)];
-                    step(v, xx);
+                for (int u = 0; u < DE_G; u++) {
+                    W[u] = wr[g * DE_G + u];
+                    X[u] = xr[g * DE_G + u];
                 }
-            }
+            };
+            auto add = [&](const float4 (&W)[DE_G], const float4 (&X)[DE_G]) {
 #pragma unroll
-            for (int u = 0; u < D; u++)  // wb[u], xb[u] hold float4 k + u
-                if (k + u < l4) step(wb[u], xb[u]);
+                for (int u = 0; u < DE_G; u++) {
+                    acc = __fadd_rn(acc, __fmul_rn(W[u].x, X[u].x));
+                    acc = __fadd_rn(acc, __fmul_rn(W[u].y, X[u].y));
+                    acc = __fadd_rn(acc, __fmul_rn(W[u].z, X[u].z));
+                    acc = __fadd_rn(acc, __fmul_rn(W[u].w, X[u].w));
+                }
+            };
+            read(WA, XA, 0);
+            int g = 0;
+            for (; g + 2 <= ng; g += 2) {
+                read(WB, XB, g + 1);
+                __builtin_amdgcn_sched_barrier(0);
+                add(WA, XA);
+                __builtin_amdgcn_sched_barrier(0);
+                if (g + 2 < ng) read(WA, XA, g + 2);  // (the last pair reads no slack)
+                __builtin_amdgcn_sched_barrier(0);
+                add(WB, XB);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (g < ng) add(WA, XA);  // an odd last group
         }
         if (c + 1 < nch) store(b ^ 1);
         __syncthreads();
