@@ -56,6 +56,14 @@ __device__ __forceinline__ float h2f(uint32_t bits)
     return (float)h;
 }
 
+// Buffer resource over [base, base + bytes): raw buffer loads at offsets
+// past `bytes` return zeros and access no memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+constexpr int CPOL_NT = 2;  // non-temporal: streamed weights are read once
+
 // ============================================================ EXACT mode
 constexpr int XS_LANE = 20;  // floats per AVX lane in LDS (bank spread)
 constexpr int XS_BLK = 8 * XS_LANE;
@@ -144,32 +152,44 @@ __device__ __forceinline__ void gemv_exact_tile(const uint8_t* __restrict__ code
         params += t0 * TILE_ROWS;
     }
     const int L = threadIdx.x & 7;
-    const int row = tile * (EX_WG / 8) + (threadIdx.x >> 3);
+    const int r16 = threadIdx.x >> 3;  // row within the tile
+    const int row = tile * (EX_WG / 8) + r16;
     const bool active = row < rows;
     const size_t tb = (size_t)tile * (size_t)nb;  // this tile's first block record
-    const uint32_t* pp = params + (size_t)tile * nb * TILE_ROWS + (row & (TILE_ROWS - 1));
+    // the tile's records: per block, the workgroup reads one contiguous 1 KiB
+    // code record (v3: and a 512 B high-plane record) and 64 B of parameters
+    const auto crs = buf_rsrc(codes + tb * CODE_REC, nb * (int)CODE_REC);
+    const auto hrs = buf_rsrc((SCHEME == 3 ? hp : codes) + tb * HP_REC, SCHEME == 3 ? nb * (int)HP_REC : 0);
+    const auto prs = buf_rsrc(params + tb * TILE_ROWS, nb * TILE_ROWS * 4);
+    const int coff = dcode_pos(r16, L), hoff = dhp_pos(r16, L), poff = r16 * 4;
     float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += EX_SEG) {
         const int nbs = min(EX_SEG, nb - b0);
+        // every load of the segment first (range-checked: none past the
+        // row), so their latency overlaps the staging of x and each other
+        uint2 c[EX_SEG];
+        uint32_t h[EX_SEG], p[EX_SEG];
+#pragma unroll
+        for (int s = 0; s < EX_SEG; s++) {
+            if (s < nbs) {  // uniform
+                const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(crs, (b0 + s) * (int)CODE_REC + coff, 0, CPOL_NT);
+                c[s] = make_uint2(v.x, v.y);
+                if constexpr (SCHEME == 3)
+                    h[s] = __builtin_amdgcn_raw_buffer_load_b32(hrs, (b0 + s) * (int)HP_REC + hoff, 0, CPOL_NT);
+                p[s] = __builtin_amdgcn_raw_buffer_load_b32(prs, (b0 + s) * TILE_ROWS * 4 + poff, 0, CPOL_NT);
+            }
+        }
         __syncthreads();
         stage_x(xs, x, b0, nbs);
         __syncthreads();
-        // per block, the workgroup reads one contiguous 1 KiB code record
-        const uint8_t* cp = codes + (tb + b0) * CODE_REC + dcode_pos(threadIdx.x >> 3, L);
         const float* xl = xs + L * XS_LANE;
-        if constexpr (SCHEME == 4) {
-#pragma unroll 4
-            for (int s = 0; s < nbs; s++) {
-                const uint2 c = *reinterpret_cast<const uint2*>(cp + (size_t)s * CODE_REC);
-                acc = v4_exact_block(c, pp[(size_t)(b0 + s) * TILE_ROWS], xl + s * XS_BLK, acc);
-            }
-        } else {
-            const uint8_t* hq = hp + (tb + b0) * HP_REC + dhp_pos(threadIdx.x >> 3, L);
-#pragma unroll 4
-            for (int s = 0; s < nbs; s++) {
-                const uint2 c = *reinterpret_cast<const uint2*>(cp + (size_t)s * CODE_REC);
-                const uint32_t h = *reinterpret_cast<const uint32_t*>(hq + (size_t)s * HP_REC);
-                acc = v3_exact_block(c, h, pp[(size_t)(b0 + s) * TILE_ROWS], xl + s * XS_BLK, acc);
+#pragma unroll
+        for (int s = 0; s < EX_SEG; s++) {
+            if (s < nbs) {  // uniform
+                if constexpr (SCHEME == 4)
+                    acc = v4_exact_block(c[s], p[s], xl + s * XS_BLK, acc);
+                else
+                    acc = v3_exact_block(c[s], h[s], p[s], xl + s * XS_BLK, acc);
             }
         }
     }
@@ -237,13 +257,6 @@ __global__ __launch_bounds__(EX_WG) void k_gemv_exact_multi(const ExactBatch B)
 }
 
 // ============================================================ FAST mode
-// Buffer resource over [base, base + bytes): raw buffer loads at offsets
-// past `bytes` return zeros and access no memory.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes)
-{
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
-}
-constexpr int CPOL_NT = 2;  // non-temporal: streamed weights are read once
 
 struct FastProblem {
     const uint8_t* codes;
