@@ -45,48 +45,44 @@ __global__ __launch_bounds__(64) void k_dense_exact(const float* __restrict__ w,
     if (r < out_f) y[r] = bias ? __fadd_rn(acc, bias[r]) : acc;
 }
 
-// The same sums for in_f % 4 == 0, sixteen rows per workgroup: the whole
-// workgroup stages K chunks of the rows (and of x) into LDS, double
-// buffered, while lanes 0..15 of wave 0 run their rows' index-order chains
-// from LDS (a row's stride is 4 floats past a multiple of 32, so the sixteen
-// rows' 16-byte reads hit distinct banks). Each lane reads a group of 32
-// values a whole group ahead of its chain (two register sets); a chunk's
-// values past in_f are zeros (adding w*x = +-0 to the sum changes nothing:
-// it starts at +0.0 and never becomes -0.0), and each row and x keep one
-// group of slack past the chunk for the read ahead, never added.
+// The same sums for in_f % 4 == 0, sixteen rows per workgroup. The whole
+// workgroup stages K chunks of the rows' products w*x (each rounded, as the
+// reference rounds it before adding) into LDS, double buffered, while lanes
+// 0..15 of wave 0 add their rows' products in index order: one addition per
+// value. A row's stride is 4 floats past a multiple of 32, so the sixteen
+// rows' 16-byte reads hit distinct banks. Each lane reads a group of 32
+// products a whole group ahead of its chain (two register sets); a chunk's
+// products past in_f are zeros (adding them changes nothing: the sum starts
+// at +0.0 and never becomes -0.0).
 constexpr int DE_ROWS = 16, DE_K = 512, DE_G = 8;  // DE_G float4s per group
 __global__ __launch_bounds__(256) void k_dense_exact_lds(const float* __restrict__ w,
                                                         const float* __restrict__ x,
                                                         const float* __restrict__ bias,
                                                         float* __restrict__ y, int out_f, int in_f)
 {
-    __shared__ __align__(16) float ws[2][DE_ROWS][DE_K + 4 + 4 * DE_G];
-    __shared__ __align__(16) float xs[2][DE_K + 4 * DE_G];
+    __shared__ __align__(16) float ws[2][DE_ROWS][DE_K + 4];
     const int r0 = blockIdx.x * DE_ROWS, t = threadIdx.x;
     const int nch = (in_f + DE_K - 1) / DE_K;
     constexpr int PER = DE_ROWS * DE_K / 4 / 256;  // 16-byte loads of W per thread and chunk
-    float4 st[PER];
-    float4 xv = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 st[PER], xq[PER];
     auto load = [&](int c) {
 #pragma unroll
         for (int u = 0; u < PER; u++) {
             const int idx = t + 256 * u, rr = idx / (DE_K / 4), k = c * DE_K + 4 * (idx % (DE_K / 4));
             const int row = min(r0 + rr, out_f - 1);
-            st[u] = k < in_f ? *reinterpret_cast<const float4*>(w + (size_t)row * in_f + k)
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        if (t < DE_K / 4) {
-            const int k = c * DE_K + 4 * t;
-            xv = k < in_f ? *reinterpret_cast<const float4*>(x + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const bool in = k < in_f;
+            st[u] = in ? *reinterpret_cast<const float4*>(w + (size_t)row * in_f + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+            xq[u] = in ? *reinterpret_cast<const float4*>(x + k) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
     };
     auto store = [&](int b) {
 #pragma unroll
         for (int u = 0; u < PER; u++) {
             const int idx = t + 256 * u;
-            *reinterpret_cast<float4*>(&ws[b][idx / (DE_K / 4)][4 * (idx % (DE_K / 4))]) = st[u];
+            const float4 p = make_float4(__fmul_rn(st[u].x, xq[u].x), __fmul_rn(st[u].y, xq[u].y),
+                                         __fmul_rn(st[u].z, xq[u].z), __fmul_rn(st[u].w, xq[u].w));
+            *reinterpret_cast<float4*>(&ws[b][idx / (DE_K / 4)][4 * (idx % (DE_K / 4))]) = p;
         }
-        if (t < DE_K / 4) *reinterpret_cast<float4*>(&xs[b][4 * t]) = xv;
     };
     load(0);
     store(0);
@@ -98,38 +94,34 @@ __global__ __launch_bounds__(256) void k_dense_exact_lds(const float* __restrict
         if (t < DE_ROWS) {
             const int len = min(DE_K, in_f - c * DE_K);
             const int ng = (len + 4 * DE_G - 1) / (4 * DE_G);  // groups of 32 values
-            const float4* wr = reinterpret_cast<const float4*>(&ws[b][t][0]);
-            const float4* xr = reinterpret_cast<const float4*>(&xs[b][0]);
-            float4 WA[DE_G], XA[DE_G], WB[DE_G], XB[DE_G];
-            auto read = [&](float4 (&W)[DE_G], float4 (&X)[DE_G], int g) {
+            const float4* pr = reinterpret_cast<const float4*>(&ws[b][t][0]);
+            float4 A[DE_G], B[DE_G];
+            auto read = [&](float4 (&V)[DE_G], int g) {
+#pragma unroll
+                for (int u = 0; u < DE_G; u++) V[u] = pr[g * DE_G + u];
+            };
+            auto add = [&](const float4 (&V)[DE_G]) {
 #pragma unroll
                 for (int u = 0; u < DE_G; u++) {
-                    W[u] = wr[g * DE_G + u];
-                    X[u] = xr[g * DE_G + u];
+                    acc = __fadd_rn(acc, V[u].x);
+                    acc = __fadd_rn(acc, V[u].y);
+                    acc = __fadd_rn(acc, V[u].z);
+                    acc = __fadd_rn(acc, V[u].w);
                 }
             };
-            auto add = [&](const float4 (&W)[DE_G], const float4 (&X)[DE_G]) {
-#pragma unroll
-                for (int u = 0; u < DE_G; u++) {
-                    acc = __fadd_rn(acc, __fmul_rn(W[u].x, X[u].x));
-                    acc = __fadd_rn(acc, __fmul_rn(W[u].y, X[u].y));
-                    acc = __fadd_rn(acc, __fmul_rn(W[u].z, X[u].z));
-                    acc = __fadd_rn(acc, __fmul_rn(W[u].w, X[u].w));
-                }
-            };
-            read(WA, XA, 0);
+            read(A, 0);
             int g = 0;
             for (; g + 2 <= ng; g += 2) {
-                read(WB, XB, g + 1);
+                read(B, g + 1);
                 __builtin_amdgcn_sched_barrier(0);
-                add(WA, XA);
+                add(A);
                 __builtin_amdgcn_sched_barrier(0);
-                if (g + 2 < ng) read(WA, XA, g + 2);  // (the last pair reads no slack)
+                if (g + 2 < ng) read(A, g + 2);
                 __builtin_amdgcn_sched_barrier(0);
-                add(WB, XB);
+                add(B);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if (g < ng) add(WA, XA);  // an odd last group
+            if (g < ng) add(A);  // an odd last group
         }
         if (c + 1 < nch) store(b ^ 1);
         __syncthreads();
