@@ -71,12 +71,27 @@ constexpr int EX_SEG = 32;   // blocks of x per LDS pass (20 KiB)
 constexpr int EX_WG = 128;   // 16 rows x 8 lanes
 
 // x staged as xs[s*XS_BLK + L*XS_LANE + G] = x[(b0+s)*128 + G*8 + L]: the 16
-// activations AVX lane L uses, in the order it uses them.
+// activations AVX lane L uses, in the order it uses them. Every 16-byte load
+// of the segment is issued before the first store (range-checked: none past
+// the segment's nbs blocks).
 __device__ __forceinline__ void stage_x(float* xs, const float* __restrict__ x, int b0, int nbs)
 {
-    for (int i = threadIdx.x; i < nbs * 128; i += EX_WG) {
-        int s = i >> 7, r = i & 127;
-        xs[s * XS_BLK + (r & 7) * XS_LANE + (r >> 3)] = x[(size_t)b0 * 128 + i];
+    constexpr int PER = EX_SEG * 128 / 4 / EX_WG;  // float4s per thread
+    const auto xr = buf_rsrc(x + (size_t)b0 * 128, nbs * 512);
+    u32x4 v[PER];
+#pragma unroll
+    for (int u = 0; u < PER; u++) v[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, (threadIdx.x + u * EX_WG) * 16, 0, 0);
+#pragma unroll
+    for (int u = 0; u < PER; u++) {
+        const int i = 4 * (threadIdx.x + u * EX_WG);  // first of four consecutive values
+        if (i < nbs * 128) {
+            const int s = i >> 7, r = i & 127;
+            float* d = xs + s * XS_BLK + (r >> 3);
+            d[((r + 0) & 7) * XS_LANE] = __uint_as_float(v[u].x);
+            d[((r + 1) & 7) * XS_LANE] = __uint_as_float(v[u].y);
+            d[((r + 2) & 7) * XS_LANE] = __uint_as_float(v[u].z);
+            d[((r + 3) & 7) * XS_LANE] = __uint_as_float(v[u].w);
+        }
     }
 }
 
