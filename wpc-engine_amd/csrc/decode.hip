@@ -108,12 +108,18 @@ __device__ __forceinline__ float ordered_sum_lds(const float* q, int n)
     return s;
 }
 
+// EXACT: the workgroup stores every square (rounded) into LDS, zero padded,
+// and one thread adds them in index order (n <= 256).
 template <int MODE>
 __device__ float sum_squares(const float* x, int n, float* red)
 {
     __shared__ float s_total;
+    __shared__ __align__(16) float s_sq[MODE == WPCG_MODE_EXACT ? 256 + 96 : 4];
     if (MODE == WPCG_MODE_EXACT) {
-        if (threadIdx.x == 0) s_total = ordered_sumsq(x, n);
+        for (int i = threadIdx.x; i < (n + 63) / 64 * 64 + 32; i += blockDim.x)
+            s_sq[i] = i < n ? __fmul_rn(x[i], x[i]) : 0.0f;
+        __syncthreads();
+        if (threadIdx.x == 0) s_total = ordered_sum_lds(s_sq, n);
     } else {
         float s = 0.0f;
         for (int i = threadIdx.x; i < n; i += blockDim.x) s = fmaf(x[i], x[i], s);
@@ -191,6 +197,7 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
 // multiply-adds and tree sums. head_dim <= 256, pos < max_pos <= AT_MAXPOS.
 constexpr int AT_WG = 256;
 constexpr int AT_MAXPOS = 4096;
+constexpr int AT_VB = 32;  // value rows per LDS block of the output step
 
 template <int MODE>
 __device__ void head_rms_rope(const float* x, const float* w, float* y, float* red, int hd,
@@ -225,7 +232,8 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
                                                      float* __restrict__ out)
 {
     __shared__ __align__(16) float qs[256], ks[256], vs[256];
-    __shared__ float w[AT_MAXPOS];
+    __shared__ __align__(16) float w[AT_MAXPOS + 96];  // zero padded for the ordered sum
+    __shared__ __align__(16) float vsh[2][AT_VB * 256];
     __shared__ float red[AT_WG / 64];
     __shared__ float s_sum;
     const int h = blockIdx.x, n_rep = nh / nkv, j = h / n_rep;
@@ -244,17 +252,21 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
             kc[((size_t)j * max_pos + pos) * hd + i] = ks[i];
             vc[((size_t)j * max_pos + pos) * hd + i] = vs[i];
         }
-    // scores: thread t, one position at a time; rows read as float4 chunks
+    // scores: thread t, one position at a time; a row's 128-value halves
+    // read with all their 16-byte loads issued before the dot's chain
     const int n = (int)pos + 1;
     for (int t = threadIdx.x; t < n; t += AT_WG) {
         const float* kt = t == (int)pos ? ks : kb + (size_t)t * hd;
         float dot = 0.0f;
-        for (int d0 = 0; d0 < hd; d0 += 32) {
-            float4 kv[8];
+        for (int d0 = 0; d0 < hd; d0 += 128) {
+            float4 kv[32];
 #pragma unroll
-            for (int u = 0; u < 8; u++) kv[u] = *reinterpret_cast<const float4*>(kt + d0 + 4 * u);
+            for (int u = 0; u < 32; u++)
+                kv[u] = d0 + 4 * u < hd ? *reinterpret_cast<const float4*>(kt + d0 + 4 * u)
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int u = 0; u < 8; u++) {
+            for (int u = 0; u < 32; u++) {
+                if (d0 + 4 * u >= hd) break;  // uniform
                 const float* q4 = qs + d0 + 4 * u;
                 if (MODE == WPCG_MODE_EXACT) {
                     dot = __fadd_rn(dot, __fmul_rn(q4[0], kv[u].x));
@@ -282,11 +294,9 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
     for (int t = threadIdx.x; t < n; t += AT_WG) w[t] = ref_expf(__fsub_rn(w[t], m));
     __syncthreads();
     if (MODE == WPCG_MODE_EXACT) {
-        if (threadIdx.x == 0) {
-            float s = 0.0f;
-            for (int t = 0; t < n; t++) s = __fadd_rn(s, w[t]);
-            s_sum = s;
-        }
+        for (int t = n + threadIdx.x; t < (n + 63) / 64 * 64 + 32; t += AT_WG) w[t] = 0.0f;
+        __syncthreads();
+        if (threadIdx.x == 0) s_sum = ordered_sum_lds(w, n);
     } else {
         float s = 0.0f;
         for (int t = threadIdx.x; t < n; t += AT_WG) s += w[t];
@@ -301,23 +311,55 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
     if (ssum > 0.0f)
         for (int t = threadIdx.x; t < n; t += AT_WG) w[t] = __fdiv_rn(w[t], ssum);
     __syncthreads();
-    // out[d] = sum_t w_t v_t[d], position order; thread d, loads 8 ahead
-    for (int d = threadIdx.x; d < hd; d += AT_WG) {
-        float acc = 0.0f;
-        int t = 0;
-        for (; t + 8 <= (int)pos; t += 8) {
-            float vv[8];
+    // out[d] = sum_t w_t v_t[d], position order; thread d. The cached value
+    // rows (t < pos) pass through LDS in blocks of AT_VB positions, double
+    // buffered: the whole workgroup issues the next block's 16-byte loads
+    // before the current block's chains; t = pos comes from vs.
+    const int nv = (int)pos, nblk = (nv + AT_VB - 1) / AT_VB, f4 = AT_VB * hd / 4;
+    constexpr int VPER = AT_VB * 256 / 4 / AT_WG;  // float4s per thread per block (hd <= 256)
+    float4 vr[VPER];
+    auto vload = [&](int bk) {
 #pragma unroll
-            for (int u = 0; u < 8; u++) vv[u] = vb[(size_t)(t + u) * hd + d];
-#pragma unroll
-            for (int u = 0; u < 8; u++)
-                acc = MODE == WPCG_MODE_EXACT ? __fadd_rn(acc, __fmul_rn(w[t + u], vv[u]))
-                                              : fmaf(w[t + u], vv[u], acc);
+        for (int u = 0; u < VPER; u++) {
+            const int i = threadIdx.x + u * AT_WG;  // float4 of the block
+            const int t = bk * AT_VB + 4 * i / hd;
+            vr[u] = i < f4 && t < nv ? *reinterpret_cast<const float4*>(vb + (size_t)bk * AT_VB * hd + 4 * i)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        for (; t < (int)pos; t++)
-            acc = MODE == WPCG_MODE_EXACT ? __fadd_rn(acc, __fmul_rn(w[t], vb[(size_t)t * hd + d]))
-                                          : fmaf(w[t], vb[(size_t)t * hd + d], acc);
-        acc = MODE == WPCG_MODE_EXACT ? __fadd_rn(acc, __fmul_rn(w[pos], vs[d])) : fmaf(w[pos], vs[d], acc);
+    };
+    auto vstore = [&](int b) {
+#pragma unroll
+        for (int u = 0; u < VPER; u++) {
+            const int i = threadIdx.x + u * AT_WG;
+            if (i < f4) *reinterpret_cast<float4*>(&vsh[b][4 * i]) = vr[u];
+        }
+    };
+    const int d = threadIdx.x;
+    float acc = 0.0f;
+    auto step = [&](float wt, float v) {
+        acc = MODE == WPCG_MODE_EXACT ? __fadd_rn(acc, __fmul_rn(wt, v)) : fmaf(wt, v, acc);
+    };
+    if (nblk > 0) {
+        vload(0);
+        vstore(0);
+    }
+    __syncthreads();
+    for (int bk = 0; bk < nblk; bk++) {
+        const int b = bk & 1, t0 = bk * AT_VB;
+        if (bk + 1 < nblk) vload(bk + 1);
+        if (d < hd) {
+            if (t0 + AT_VB <= nv) {
+#pragma unroll
+                for (int u = 0; u < AT_VB; u++) step(w[t0 + u], vsh[b][u * hd + d]);
+            } else {
+                for (int u = 0; u < nv - t0; u++) step(w[t0 + u], vsh[b][u * hd + d]);
+            }
+        }
+        if (bk + 1 < nblk) vstore(b ^ 1);
+        __syncthreads();
+    }
+    if (d < hd) {
+        step(w[pos], vs[d]);
         out[(size_t)h * hd + d] = acc;
     }
 }
