@@ -4,7 +4,9 @@
 Workload (benchmark config 1, the record's `value`): batch-1 dequant-GEMV over
 the seven Qwen3-4B layer shapes (q 4096x2560, k/v 1024x2560, o 2560x4096,
 gate/up 9728x2560, down 2560x9728) in the v3 scheme (6-bit codes, two-plane
-device layout), seeded synthetic blocks, x ~ N(0,1) fp32. One step = one pass
+device layout), synthetic blocks and x ~ N(0,1) fp32 drawn with the configs'
+PRNG (xoshiro256++ seeded 0x12345678, Box-Muller in f32, as the reference's
+evaluator draws x; wpcg.synth.wpc_blocks / wpc_x). One step = one pass
 of the seven GEMVs in four launches (q/k/v share their input and a launch, as
 do gate/up; o and down run alone, as in a decode layer where their inputs come
 from other operations). Weights are HBM-cold: the steps rotate over enough
@@ -454,17 +456,17 @@ def gemv_series_us(ctx, wpcg, lins, xd, yd, reps=8):
     return us
 
 
-def per_shape_bench(ctx, wpcg, synth, scheme, shapes, min_bytes):
-    """Each config-1 GEMV alone: FAST, HBM-cold (rotated over >= min_bytes of
-    device copies of that matrix), launch after launch."""
+def per_shape_bench(ctx, wpcg, scheme, shapes, blocks, xs, min_bytes):
+    """Each config-1 GEMV alone (the step's own matrices and x): FAST,
+    HBM-cold (rotated over >= min_bytes of device copies of that matrix),
+    launch after launch."""
     out = {}
     for i, (name, r, c) in enumerate(shapes):
-        gen = synth.random_v3_blocks if scheme == 3 else synth.random_v4_blocks
-        base = wpcg.WpcLinear.from_blocks(ctx, scheme, gen(r, c, seed=1000 + i), r, c)
+        base = wpcg.WpcLinear.from_blocks(ctx, scheme, blocks[i], r, c)
         base.set_mode(wpcg.MODE_FAST)
         n = max(1, -(-int(min_bytes) // base.device_bytes()))
         lins = [base] + [base.clone() for _ in range(n - 1)]
-        xd = ctx.upload(synth.random_x(c, seed=c))
+        xd = ctx.upload(xs[c])
         yd = ctx.alloc(4 * r)
         us = gemv_series_us(ctx, wpcg, lins, xd, yd)
         alg = gemv_bytes(r, c, scheme)
@@ -484,8 +486,8 @@ def cfg0_bench(ctx, wpcg, synth, min_bytes, cpu_budget):
     copies (each launch's weights come from HBM); cache-hot: the same launches
     on one copy (resident in the Infinity Cache after the first)."""
     rows, cols = 4864, 896
-    blocks = synth.random_v4_blocks(rows, cols, seed=0x12345678 & 0xFFFF)
-    x = synth.random_x(cols, seed=0x5678)
+    blocks = synth.wpc_blocks(4, rows, cols, matrix_id=0)  # the configs' PRNG (synth.WPC_SEED)
+    x = synth.wpc_x(cols)
     base = wpcg.WpcLinear.from_blocks(ctx, 4, blocks, rows, cols).set_mode(wpcg.MODE_FAST)
     n = max(1, -(-int(min_bytes) // base.device_bytes()))
     lins = [base] + [base.clone() for _ in range(n - 1)]
@@ -645,10 +647,10 @@ def main():
 
     scheme = args.scheme
     mode = wpcg.MODE_EXACT if args.mode == "exact" else wpcg.MODE_FAST
-    gen = synth.random_v3_blocks if scheme == 3 else synth.random_v4_blocks
-    log(f"generating seeded v{scheme} blocks for the seven Qwen3-4B shapes")
-    blocks = [gen(r, c, seed=1000 + i) for i, (_, r, c) in enumerate(QWEN3_4B)]
-    xs = {c: synth.random_x(c, seed=c) for c in sorted({c for _, _, c in QWEN3_4B})}
+    log(f"generating v{scheme} blocks for the seven Qwen3-4B shapes (xoshiro256++, seed "
+        f"{synth.WPC_SEED:#x}, the configs' PRNG)")
+    blocks = [synth.wpc_blocks(scheme, r, c, matrix_id=1 + i) for i, (_, r, c) in enumerate(QWEN3_4B)]
+    xs = {c: synth.wpc_x(c) for c in sorted({c for _, _, c in QWEN3_4B})}
 
     ctx = wpcg.Context(0)
     base = [wpcg.WpcLinear.from_blocks(ctx, scheme, b, r, c)
@@ -771,7 +773,7 @@ def main():
         for l in lst:
             l.close()
     cpu_budget = 0 if args.no_cpu_baseline else args.cpu_seconds / 2
-    per_shape = per_shape_bench(ctx, wpcg, synth, scheme, QWEN3_4B, args.min_bytes) \
+    per_shape = per_shape_bench(ctx, wpcg, scheme, QWEN3_4B, blocks, xs, args.min_bytes) \
         if "per_shape" in sections else None
     cfg0 = cfg0_bench(ctx, wpcg, synth, args.min_bytes, cpu_budget) if "cfg0" in sections else None
     large = large_gemv_bench(ctx, wpcg, synth) if "large_gemv" in sections else None
@@ -795,7 +797,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded: codes uniform, zp f16(N(-0.03,0.005)), scale f16(U(0.002,0.006)), x N(0,1))",
+        "data": ("synthetic, the configs' PRNG (xoshiro256++ seeded 0x12345678 as wpc-eval/src/main.rs:77-82, "
+                 "Box-Muller in f32; one stream per matrix row): codes uniform, zp f16(N(-0.03,0.005)), "
+                 "scale f16(U(0.002,0.006)), x N(0,1)"),
         "config": {
             "workload": (f"cfg1: v{scheme} dequant-GEMV batch 1 over the seven Qwen3-4B layer shapes "
                          f"(q/k/v/o/gate/up/down) in 4 launches per step, HBM-cold over {copies} rotated "

@@ -5,6 +5,9 @@ configurations specify: codes uniform over the scheme's range, zero_point
 f16(N(-0.03, 0.005)), scale f16(U(0.002, 0.006)), f16 by round-to-nearest-
 even (numpy's float16 conversion, the same rounding as the reference's
 half::f16::from_f32). numpy's PCG64 generator is used with the given seed.
+wpc_blocks / wpc_x draw the same parameters with the benchmark
+configurations' own PRNG (xoshiro256++ seeded as the reference's evaluator
+seeds it; see below), so a Rust caller can regenerate them.
 
 write_artifact emits model_v{3,4}.meta + model_v{3,4}.wpc exactly as the
 reference's compiler lays them out (wpc-compiler/src/main.rs:644-696): blocks
@@ -74,6 +77,144 @@ def random_v3_blocks(rows: int, cols: int, seed: int) -> np.ndarray:
 
 def random_x(n: int, seed: int) -> np.ndarray:
     return np.random.default_rng(seed).standard_normal(n).astype(np.float32)
+
+
+# ---- the benchmark configurations' PRNG -------------------------------------
+# Configs 0 and 1 draw their inputs with xoshiro256++ and Box-Muller as the
+# reference's evaluator does (wpc-eval/src/main.rs:77-82: seed 0x1234_5678,
+# `rng.gen::<f32>()` twice per value, `(-2 ln u1).sqrt() * (2 pi u2).cos()` in
+# f32), with crates pinned in the reference's Cargo.lock (rand 0.8.7,
+# rand_xoshiro 0.6.0). Restated from their published algorithms:
+# - xoshiro256++ 1.0 (Blackman and Vigna): result = rotl(s0 + s3, 23) + s0,
+#   then t = s1 << 17, s2 ^= s0, s3 ^= s1, s1 ^= s2, s0 ^= s3, s2 ^= t,
+#   s3 = rotl(s3, 45);
+# - `seed_from_u64(seed)`: the four state words are the first four outputs of
+#   SplitMix64 started at `seed` (x += 0x9e3779b97f4a7c15; z = x;
+#   z = (z ^ z>>30) * 0xbf58476d1ce4e5b9; z = (z ^ z>>27) * 0x94d049bb133111eb;
+#   z ^ z>>31);
+# - `next_u32` is the upper half of `next_u64`; `gen::<f32>()` is
+#   (next_u32 >> 8) * 2^-24;
+# - ln and cos are the host libm's logf and cosf (what Rust's f32::ln/cos call
+#   on Linux), sqrt is correctly rounded, every other step one f32 rounding.
+# The weights of a matrix use one stream per row r, seeded
+# WPC_SEED + ((matrix_id + 1) << 32) + r, and per block in order: u1, u2 (a
+# normal n by the same Box-Muller), u, then 128 codes `next_u32 >> (32 - bits)`;
+# zp = f16(-0.03 + 0.005 n), scale = f16(0.002 + 0.004 u) (round to nearest
+# even, as half::f16::from_f32). x of length n is the first n values of the
+# stream seeded WPC_SEED.
+WPC_SEED = 0x12345678
+_M64 = (1 << 64) - 1
+
+
+def _rotl_np(x, k):
+    return (x << np.uint64(k)) | (x >> np.uint64(64 - k))
+
+
+def splitmix64_np(state):
+    """One SplitMix64 step over a uint64 array: (new state, output)."""
+    state = state + np.uint64(0x9E3779B97F4A7C15)
+    z = (state ^ (state >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return state, z ^ (z >> np.uint64(31))
+
+
+class Xoshiro256pp:
+    """Independent xoshiro256++ streams, one per seed, advanced together
+    (numpy uint64 arithmetic wraps modulo 2^64). `state` may be given
+    instead of seeds: a (4, S) array of the four state words."""
+
+    def __init__(self, seeds=None, state=None):
+        if state is not None:
+            self.s = [np.asarray(w, np.uint64).copy() for w in state]
+            return
+        st = np.atleast_1d(np.asarray(seeds, dtype=np.uint64)).copy()
+        self.s = []
+        for _ in range(4):
+            st, z = splitmix64_np(st)
+            self.s.append(z)
+
+    def next_u64(self) -> np.ndarray:
+        s0, s1, s2, s3 = self.s
+        result = _rotl_np(s0 + s3, 23) + s0
+        t = s1 << np.uint64(17)
+        s2 = s2 ^ s0
+        s3 = s3 ^ s1
+        s1 = s1 ^ s2
+        s0 = s0 ^ s3
+        s2 = s2 ^ t
+        s3 = _rotl_np(s3, 45)
+        self.s = [s0, s1, s2, s3]
+        return result
+
+    def next_u32(self) -> np.ndarray:
+        return (self.next_u64() >> np.uint64(32)).astype(np.uint32)
+
+    def gen_f32(self) -> np.ndarray:
+        return (self.next_u32() >> np.uint32(8)).astype(np.float32) * np.float32(2.0 ** -24)
+
+
+_libm = None
+
+
+def _box_muller_f32(u1: np.ndarray, u2: np.ndarray) -> np.ndarray:
+    """sqrt(-2 ln u1) * cos(2 pi u2), in f32 with the host libm's logf and cosf."""
+    global _libm
+    import ctypes
+    if _libm is None:
+        _libm = ctypes.CDLL("libm.so.6")
+        for fn in (_libm.logf, _libm.cosf):
+            fn.restype = ctypes.c_float
+            fn.argtypes = [ctypes.c_float]
+    two_pi = np.float32(2.0) * np.float32(np.pi)  # Rust's 2.0f32 * f32::consts::PI
+    lg = np.array([_libm.logf(float(v)) for v in u1], np.float32)
+    ang = (two_pi * u2.astype(np.float32)).astype(np.float32)
+    cs = np.array([_libm.cosf(float(v)) for v in ang], np.float32)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        return (np.sqrt(np.float32(-2.0) * lg) * cs).astype(np.float32)
+
+
+def wpc_x(n: int, seed: int = WPC_SEED) -> np.ndarray:
+    """x of length n drawn as the reference's evaluator draws it (one stream,
+    two uniforms per value, Box-Muller in f32)."""
+    rng = Xoshiro256pp([seed])
+    u = np.empty(2 * n, np.float32)
+    for i in range(2 * n):
+        u[i] = rng.gen_f32()[0]
+    return _box_muller_f32(u[0::2], u[1::2])
+
+
+def wpc_blocks(scheme: int, rows: int, cols: int, matrix_id: int, seed: int = WPC_SEED) -> np.ndarray:
+    """rows*(cols/128) v4 or v3 blocks with the configs' parameters, drawn
+    per row as described above."""
+    assert cols % 128 == 0 and scheme in (3, 4)
+    nb, bits = cols // 128, (4 if scheme == 4 else 6)
+    seeds = np.uint64(seed) + (np.uint64(matrix_id + 1) << np.uint64(32)) + np.arange(rows, dtype=np.uint64)
+    rng = Xoshiro256pp(seeds)
+    u1 = np.empty((nb, rows), np.float32)
+    u2 = np.empty((nb, rows), np.float32)
+    uu = np.empty((nb, rows), np.float32)
+    codes = np.empty((nb, 128, rows), np.uint8)
+    shift = np.uint32(32 - bits)
+    for b in range(nb):
+        u1[b] = rng.gen_f32()
+        u2[b] = rng.gen_f32()
+        uu[b] = rng.gen_f32()
+        for k in range(128):
+            codes[b, k] = (rng.next_u32() >> shift).astype(np.uint8)
+    n = _box_muller_f32(u1.ravel(), u2.ravel()).reshape(nb, rows)
+    zp = (np.float32(-0.03) + (np.float32(0.005) * n).astype(np.float32)).astype(np.float32)
+    sc = (np.float32(0.002) + (np.float32(0.004) * uu).astype(np.float32)).astype(np.float32)
+    zp16 = zp.T.reshape(-1).astype(np.float16)  # [row][block] order
+    sc16 = sc.T.reshape(-1).astype(np.float16)
+    c = codes.transpose(2, 0, 1).reshape(rows * nb, 128)  # [row][block][k]
+    out = np.empty((rows * nb, BPB[scheme]), np.uint8)
+    out[:, 0:2] = zp16.view(np.uint8).reshape(-1, 2)
+    out[:, 2:4] = sc16.view(np.uint8).reshape(-1, 2)
+    if scheme == 4:
+        out[:, 4:] = (c[:, :64] & 15) | ((c[:, 64:] & 15) << 4)
+    else:
+        out[:, 4:] = pack_v3_codes(c)
+    return out.ravel()
 
 
 def _rust_usize(s: str):
