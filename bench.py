@@ -437,11 +437,28 @@ def rotation_runner(ctx, copies, step_for_copy):
     return run, warm, graphs
 
 
+# --series-eager: the per-shape and config-0 series launch one by one instead
+# of replaying a graph (for kernel traces: rocprofv3 ended the process on a
+# graph of several hundred launches); their times then include host launch
+# cost, so such a run's JSON is not a measurement of record.
+SERIES_EAGER = False
+
+
 def gemv_series_us(ctx, wpcg, lins, xd, yd, reps=8):
     """Device time of one launch of lins[i].matvec(x), launched one after the
     other (each waits for the previous on the stream) over every member of
     lins, from a replayed graph: the mean over reps replays."""
     body = lambda: [l.matvec_dev(xd, yd) for l in lins]  # noqa: E731
+    if SERIES_EAGER:
+        body()
+        ctx.sync()
+        e0, e1 = ctx.event(), ctx.event()
+        e0.record()
+        for _ in range(reps):
+            body()
+        e1.record()
+        ctx.sync()
+        return e0.elapsed_ms(e1) * 1e3 / (reps * len(lins))
     g = ctx.capture(body)
     g.launch()
     ctx.sync()
@@ -607,6 +624,8 @@ def main():
     ap.add_argument("--decode-eager", action="store_true",
                     help="decode steps launch by launch instead of graph replays (for kernel traces)")
     ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM (config 4) lines")
+    ap.add_argument("--series-eager", action="store_true",
+                    help="per-shape and config-0 series launched one by one (kernel traces only)")
     ap.add_argument("--no-large-gemv", action="store_true",
                     help="skip the lm_head-shaped v4 GEMV line (165 MB per launch)")
     ap.add_argument("--prefill-trace", type=int, default=0, metavar="LAYERS",
@@ -614,6 +633,8 @@ def main():
                          "of --decode-prompt tokens (for kernel traces), then exit")
     args = ap.parse_args()
 
+    global SERIES_EAGER
+    SERIES_EAGER = args.series_eager
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
               "(the single-GPU kernel is the unit of work; see the sharding design notes).",

@@ -102,7 +102,9 @@ SHAPES = [
     (3, 9728, 2560),
     (3, 2560, 9728),
     (3, 37, 640),
-    (4, 8200, 640),    # four tiles per workgroup, 513 tiles (one in the last workgroup)
+    (4, 8200, 640),    # 513 tiles of 5 blocks: two tiles per workgroup (one in the last)
+    (4, 4864, 896),    # config 0: 304 tiles of 7 blocks, two tiles per workgroup
+    (4, 4080, 896),    # 255 tiles of 7 blocks: four tiles per workgroup, three in the last
     (4, 488, 2560),    # 31 tiles: one tile per workgroup
     (4, 520, 4096),    # 33 tiles, 32 blocks: one tile per workgroup (two from 192 tiles)
     (3, 3056, 4096),   # 191 tiles, 32 blocks: one tile per workgroup

@@ -135,10 +135,14 @@ constexpr int FAST_MAXBK = 64;
 // rows of at most 32 blocks once it has 192 (a 160-tile matrix of 32-block
 // rows ran 10% faster on 160 workgroups than on 80). Rows longer than one
 // slice take 2 tiles from 128 tiles on (2560x9728: 240 workgroups beat
-// 480), and matrices of 512 tiles or more take 2 in any case.
+// 480), and matrices of 512 tiles or more take 2 in any case. Short rows
+// (at most 8 blocks) of a matrix of 256 tiles or more take 2, not 4: the
+// config-0 GEMV (4864x896, 304 tiles of 7 blocks) ran 3.69 us on 152
+// workgroups against 3.87 on 76 and 4.53 on 304.
 inline int fast_tiles_per_wg(uint64_t rows, uint64_t nb)
 {
     const uint64_t tiles = pad_rows(rows) / TILE_ROWS;
+    if (tiles >= 256 && nb <= 8) return 2;
     if (tiles >= 32 && nb <= FAST_MAXBK / 4) return 4;
     if (tiles >= 192 && nb <= FAST_MAXBK / 2) return 2;
     if (tiles >= 128 && nb > FAST_MAXBK) return 2;
