@@ -155,6 +155,47 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
     __shared__ float s_total;
     const bool staged = n <= RN_LDS;
     const float* src = staged ? xs : x;
+    if (MODE == WPCG_MODE_EXACT && staged && (n & 3) == 0) {
+        // every 16-byte load of x and of the weights first (range-checked,
+        // none past n), the squares into LDS, x kept in registers for the
+        // output: one memory round trip before the ordered chain
+        constexpr int V = RN_LDS / 4 / NW;
+        typedef float f4 __attribute__((ext_vector_type(4)));
+        const auto xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), (short)0, n * 4, 0x00020000);
+        const auto wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(w), (short)0, n * 4, 0x00020000);
+        f4 xv[V], wv[V];
+#pragma unroll
+        for (int u = 0; u < V; u++) {
+            xv[u] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(xr, (threadIdx.x + u * NW) * 16, 0, 0));
+            wv[u] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(wr, (threadIdx.x + u * NW) * 16, 0, 0));
+        }
+#pragma unroll
+        for (int u = 0; u < V; u++) {
+            const int i = 4 * (threadIdx.x + u * NW);
+            if (i < n) {
+                const f4 v = xv[u];
+                *reinterpret_cast<f4*>(&sq[i]) = f4{__fmul_rn(v.x, v.x), __fmul_rn(v.y, v.y),
+                                                    __fmul_rn(v.z, v.z), __fmul_rn(v.w, v.w)};
+            }
+        }
+        for (int i = n + threadIdx.x; i < (n + 63) / 64 * 64 + 32; i += NW) sq[i] = 0.0f;
+        __syncthreads();
+        if (threadIdx.x == 0) s_total = ordered_sum_lds(sq, n);
+        __syncthreads();
+        const float mean_sq = __fdiv_rn(s_total, (float)n);
+        const float scale = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(mean_sq, eps)));
+#pragma unroll
+        for (int u = 0; u < V; u++) {
+            const int i = 4 * (threadIdx.x + u * NW);
+            if (i < n) {
+                out[i] = __fmul_rn(__fmul_rn(xv[u].x, scale), wv[u].x);
+                out[i + 1] = __fmul_rn(__fmul_rn(xv[u].y, scale), wv[u].y);
+                out[i + 2] = __fmul_rn(__fmul_rn(xv[u].z, scale), wv[u].z);
+                out[i + 3] = __fmul_rn(__fmul_rn(xv[u].w, scale), wv[u].w);
+            }
+        }
+        return;
+    }
     float part = 0.0f;
     for (int i = threadIdx.x; i < n; i += NW) {
         const float v = x[i];
