@@ -480,7 +480,20 @@ __global__ __launch_bounds__(FA_WG) void k_attention_fast(const float* __restric
     const int n = (int)pos + 1, n_rep = nh / nkv;
     const int len = (n + FA_NCH - 1) / FA_NCH;
     const int tb = c * len;
-    if (tb >= n || pos >= max_pos) return;  // an empty chunk
+    if (tb >= n || pos >= max_pos) {
+        // An empty chunk leaves the neutral state (m = -inf, l = 0, o = 0),
+        // so the merge in o_proj takes every chunk without knowing the
+        // position: an empty chunk's weight exp(-inf - M) is 0. (Past the
+        // cache, pos >= max_pos, every chunk is empty and chunk 0 leaves
+        // m = 0, l = 1: the merged output is 0 rather than 0/0.)
+        const bool unit = c == 0;
+        for (int i = threadIdx.x; i < n_rep * HD; i += FA_WG)
+            part_o[((size_t)c * nh + j * n_rep) * HD + i] = 0.0f;
+        if ((int)threadIdx.x < 2 * n_rep)
+            part_ml[((size_t)c * nh + j * n_rep) * 2 + threadIdx.x] =
+                (threadIdx.x & 1) ? (unit ? 1.0f : 0.0f) : (unit ? 0.0f : -INFINITY);
+        return;
+    }
     const int te = min(tb + len, n);
     const float* cs = cos_t + (size_t)pos * (HD / 2);
     const float* sn = sin_t + (size_t)pos * (HD / 2);

@@ -582,12 +582,44 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     constexpr int XP0 = 2;
     const auto xrs = buf_rsrc(xp, nbl * 512);
     u32x4 xv[XP], x2v[XP];
-    if constexpr (xform != XF_MERGE) {  // (XF_MERGE reads its chunk states in the prep)
+    if constexpr (xform != XF_MERGE) {
 #pragma unroll
         for (int i = 0; i < XP; i++)
             if (XF != XF_NONE || i < XP0)
                 xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
     }
+    // XF_MERGE: the chunk states of x pair p = wave + 8i: for every chunk
+    // c, (m, l) of the head of this lane's four values and their four
+    // unnormalised outputs. Chunks that held no position carry the neutral
+    // state (m = -inf, l = 0, o = 0), so every chunk is read and the position
+    // is not needed. Lanes of a block past the slice (blocks 2p+1 = nbl of an
+    // odd slice, or a whole pair past it) load nothing (an out-of-range
+    // offset: their head index may lie past n_heads) and their values are
+    // replaced by zeros after the merge. Pair 0's loads go out
+    // here, with the kernel's first loads and before the weights (its inputs
+    // are the attention's outputs, an L2 or memory round trip away).
+    struct MergeIn { float m[ATTN_CHUNKS], l[ATTN_CHUNKS]; float4 o[ATTN_CHUNKS]; };
+    auto merge_load = [&](int i, MergeIn& in) {
+        const int p = wave + 8 * i, hi = lane >> 5, k0 = 4 * (lane & 31);
+        const bool blk_ok = 2 * p + hi < nbl;
+        const int k = (b0 + 2 * p + hi) * 128 + k0, h = k / P.head_dim;
+        const int stride = P.n_heads * P.head_dim;
+        // buffer loads: the chunk's offset is a scalar, the lane's a vector
+        // offset; a lane past the slice reads out of range (zeros, no access)
+        const auto ors = buf_rsrc(P.x, ATTN_CHUNKS * stride * 4);
+        const auto mrs = buf_rsrc(P.x2, ATTN_CHUNKS * P.n_heads * 8);
+        const int vo = blk_ok ? k * 4 : 0x40000000, vm = blk_ok ? h * 8 : 0x40000000;
+#pragma unroll
+        for (int cc = 0; cc < ATTN_CHUNKS; cc++) {
+            const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(mrs, vm, cc * P.n_heads * 8, 0);
+            const u32x4 o = __builtin_amdgcn_raw_buffer_load_b128(ors, vo, cc * stride * 4, 0);
+            in.m[cc] = __uint_as_float(ml.x);
+            in.l[cc] = __uint_as_float(ml.y);
+            in.o[cc] = make_float4(__uint_as_float(o.x), __uint_as_float(o.y), __uint_as_float(o.z), __uint_as_float(o.w));
+        }
+    };
+    MergeIn mg0;
+    if constexpr (xform == XF_MERGE) merge_load(0, mg0);
     float wkv[XP];  // routed: the routing weight of each x pair's block
     auto load_x2 = [&]() {  // the second operand of the transform: nw or u
         const auto x2rs = buf_rsrc(xform == XF_NORM ? P.nw + (size_t)b0 * 128 : x2p, nbl * 512);
@@ -697,96 +729,137 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
 
     // ---- x -> int8 digits. x ~= s_b * Q / 2^21 with s_b = M/127; the scale
     // and its inverse need only agree to fp32 rounding, so both come from one
-    // reciprocal.
+    // reciprocal. A wave digitises its pairs two at a time in one straight
+    // run of code, so the two pairs' dependent chains (reductions, reciprocal,
+    // rounding) overlap; the prep is latency-bound, one wave per SIMD at a
+    // time. A pair past the slice computes on zeros (its buffer loads
+    // returned zeros) and writes nothing.
     {
         const int hi = lane >> 5, k0 = 4 * (lane & 31);
         const int pos0 = frag_pos(k0), pos1 = frag_pos(k0 + 1), pos2 = frag_pos(k0 + 2), pos3 = frag_pos(k0 + 3);
         float sq = 0.0f;
-        int nact = 0;
-        if constexpr (xform == XF_MERGE) {  // the chunks that held positions at this step
-            const int n = (int)P.st->pos + 1, len = (n + ATTN_CHUNKS - 1) / ATTN_CHUNKS;
-            nact = (n + len - 1) / len;
-        }
-#pragma unroll
-        for (int i = 0; i < XP; i++) {
+        // x' of pair i (after the transform) as four values per lane
+        auto pair_values = [&](int i, float (&v)[4]) {
             const int p = wave + 8 * i;
-            if (2 * p < nbl) {
+            if constexpr (xform == XF_MERGE) {
+                // sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, M = max_c m_c
+                MergeIn later;
+                if (i > 0) merge_load(i, later);
+                const MergeIn& in = i == 0 ? mg0 : later;
+                float M = -INFINITY;
+#pragma unroll
+                for (int cc = 0; cc < ATTN_CHUNKS; cc++) M = fmaxf(M, in.m[cc]);
+                float L = 0.0f;
+                float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int cc = 0; cc < ATTN_CHUNKS; cc++) {
+                    const float w = __expf(in.m[cc] - M);  // 0 for a neutral chunk
+                    L = fmaf(w, in.l[cc], L);
+                    a.x = fmaf(w, in.o[cc].x, a.x);
+                    a.y = fmaf(w, in.o[cc].y, a.y);
+                    a.z = fmaf(w, in.o[cc].z, a.z);
+                    a.w = fmaf(w, in.o[cc].w, a.w);
+                }
+                // a block past the slice read zeros (L = 0): its values are zeros
+                const bool blk_ok = 2 * (wave + 8 * i) + hi < nbl;
+                const float rl = __fdiv_rn(1.0f, L);
+                xv[i] = blk_ok ? u32x4{__float_as_uint(a.x * rl), __float_as_uint(a.y * rl),
+                                       __float_as_uint(a.z * rl), __float_as_uint(a.w * rl)}
+                               : u32x4{0u, 0u, 0u, 0u};
+            }
+            v[0] = __uint_as_float(xv[i].x); v[1] = __uint_as_float(xv[i].y);
+            v[2] = __uint_as_float(xv[i].z); v[3] = __uint_as_float(xv[i].w);
+            if constexpr (xform == XF_NORM) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) sq = fmaf(v[e], v[e], sq);
+                v[0] *= __uint_as_float(x2v[i].x); v[1] *= __uint_as_float(x2v[i].y);
+                v[2] *= __uint_as_float(x2v[i].z); v[3] *= __uint_as_float(x2v[i].w);
+            } else if constexpr (xform == XF_SILU) {
+                const float wk = KIND == FK_ROUTED ? wkv[i] : 1.0f;
+                const uint32_t u[4] = {x2v[i].x, x2v[i].y, x2v[i].z, x2v[i].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = __fdividef(v[e], 1.0f + __expf(-v[e])) * __uint_as_float(u[e]) * wk;
+            }
+        };
+        // block max |x| and sum of two pairs' values, step by step for both
+        // so that the two dependent chains interleave: lane-local, the 16
+        // lanes of a row by DPP exchanges (max on the bits of non-negative
+        // floats), then the two rows of a block by a row swap; every lane of a
+        // block ends with the same values, the sums added in one fixed order.
+        // Then the 28-bit Q of each value.
+        struct Dig { int Q[4]; float M, S; };
+        auto digitize2 = [&](const float (&v)[2][4], Dig (&d)[2]) {
+            uint32_t mb[2];
+            float sm[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                mb[u] = __float_as_uint(fmaxf(fmaxf(fabsf(v[u][0]), fabsf(v[u][1])), fmaxf(fabsf(v[u][2]), fabsf(v[u][3]))));
+                sm[u] = (v[u][0] + v[u][1]) + (v[u][2] + v[u][3]);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++) mb[u] = max(mb[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb[u], DPP_XOR1, 0xF, 0xF, false));
+#pragma unroll
+            for (int u = 0; u < 2; u++) sm[u] += dpp<DPP_XOR1>(sm[u]);
+#pragma unroll
+            for (int u = 0; u < 2; u++) mb[u] = max(mb[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb[u], DPP_XOR2, 0xF, 0xF, false));
+#pragma unroll
+            for (int u = 0; u < 2; u++) sm[u] += dpp<DPP_XOR2>(sm[u]);
+#pragma unroll
+            for (int u = 0; u < 2; u++) mb[u] = max(mb[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb[u], DPP_HALF_MIRROR, 0xF, 0xF, false));
+#pragma unroll
+            for (int u = 0; u < 2; u++) sm[u] += dpp<DPP_HALF_MIRROR>(sm[u]);
+#pragma unroll
+            for (int u = 0; u < 2; u++) mb[u] = max(mb[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb[u], DPP_MIRROR, 0xF, 0xF, false));
+#pragma unroll
+            for (int u = 0; u < 2; u++) sm[u] += dpp<DPP_MIRROR>(sm[u]);
+            float inv[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const auto mr = __builtin_amdgcn_permlane16_swap(mb[u], mb[u], false, false);
+                d[u].M = __uint_as_float(max((uint32_t)mr[0], (uint32_t)mr[1]));
+                inv[u] = d[u].M > 0.0f ? (127.0f * 2097152.0f) * __builtin_amdgcn_rcpf(d[u].M) : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const auto sr = __builtin_amdgcn_permlane16_swap(__float_as_uint(sm[u]), __float_as_uint(sm[u]), false, false);
+                d[u].S = __uint_as_float(sr[0]) + __uint_as_float(sr[1]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+#pragma unroll
+                for (int u = 0; u < 2; u++) d[u].Q[e] = (int)rintf(v[u][e] * inv[u]);
+        };
+        // pair i's digit bytes and {s_b, sum} into LDS (pairs inside the slice)
+        auto put_pair = [&](int i, const Dig& d) {
+            const int p = wave + 8 * i;
+            if (2 * p >= nbl) return;
+            int8_t* dst = xq + (2 * p + hi) * FRAG;
+            const int pos[4] = {pos0, pos1, pos2, pos3};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                int8_t* b = dst + pos[e];
+                b[0] = (int8_t)(d.Q[e] >> 21);
+                b[16] = (int8_t)((d.Q[e] >> 14) & 127);
+                b[32] = (int8_t)((d.Q[e] >> 7) & 127);
+                b[48] = (int8_t)(d.Q[e] & 127);
+            }
+            if ((lane & 31) == 0) xs[2 * p + hi] = make_float2(d.M * (1.0f / 127.0f), d.S);
+        };
+#pragma unroll
+        for (int i = 0; i < XP; i += 2) {
+            if (2 * (wave + 8 * i) < nbl) {
                 if constexpr (XF == XF_NONE)
-                    if (i >= XP0) xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, p * 1024 + lane * 16, 0, 0);
-                if constexpr (xform == XF_MERGE) {
-                    // The half-wave of block 2p+1 when the slice ends at 2p+1
-                    // (odd nbl) takes zeros without a load, as the buffer
-                    // loads of the other transforms give it: its head index
-                    // may lie past n_heads, and its chunk states may not
-                    // exist.
-                    const bool blk_ok = 2 * p + hi < nbl;
-                    const int k = (b0 + 2 * p + hi) * 128 + k0, h = k / P.head_dim;
-                    const size_t stride = (size_t)P.n_heads * P.head_dim;
-                    float mv[ATTN_CHUNKS], lv[ATTN_CHUNKS];
-                    float4 ov[ATTN_CHUNKS];
-#pragma unroll
-                    for (int cc = 0; cc < ATTN_CHUNKS; cc++) {
-                        const bool on = blk_ok && cc < nact;
-                        const float2 ml = on ? *reinterpret_cast<const float2*>(P.x2 + ((size_t)cc * P.n_heads + h) * 2)
-                                             : make_float2(-INFINITY, 0.0f);
-                        mv[cc] = ml.x;
-                        lv[cc] = ml.y;
-                        ov[cc] = on ? *reinterpret_cast<const float4*>(P.x + cc * stride + k)
-                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (i >= XP0) {
+                        xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
+                        xv[i + 1] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (wave + 8 * (i + 1)) * 1024 + lane * 16, 0, 0);
                     }
-                    float M = -INFINITY;
-#pragma unroll
-                    for (int cc = 0; cc < ATTN_CHUNKS; cc++) M = fmaxf(M, mv[cc]);
-                    float L = 0.0f;
-                    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-                    for (int cc = 0; cc < ATTN_CHUNKS; cc++) {
-                        const float w = cc < nact ? __expf(mv[cc] - M) : 0.0f;
-                        L = fmaf(w, lv[cc], L);
-                        a.x = fmaf(w, ov[cc].x, a.x);
-                        a.y = fmaf(w, ov[cc].y, a.y);
-                        a.z = fmaf(w, ov[cc].z, a.z);
-                        a.w = fmaf(w, ov[cc].w, a.w);
-                    }
-                    const float rl = __fdiv_rn(1.0f, L);
-                    xv[i] = blk_ok ? u32x4{__float_as_uint(a.x * rl), __float_as_uint(a.y * rl),
-                                           __float_as_uint(a.z * rl), __float_as_uint(a.w * rl)}
-                                   : u32x4{0u, 0u, 0u, 0u};
-                }
-                float v0 = __uint_as_float(xv[i].x), v1 = __uint_as_float(xv[i].y);
-                float v2 = __uint_as_float(xv[i].z), v3 = __uint_as_float(xv[i].w);
-                if constexpr (xform == XF_NORM) {
-                    sq = fmaf(v0, v0, sq); sq = fmaf(v1, v1, sq); sq = fmaf(v2, v2, sq); sq = fmaf(v3, v3, sq);
-                    v0 *= __uint_as_float(x2v[i].x); v1 *= __uint_as_float(x2v[i].y);
-                    v2 *= __uint_as_float(x2v[i].z); v3 *= __uint_as_float(x2v[i].w);
-                } else if constexpr (xform == XF_SILU) {
-                    const float wk = KIND == FK_ROUTED ? wkv[i] : 1.0f;
-                    v0 = __fdividef(v0, 1.0f + __expf(-v0)) * __uint_as_float(x2v[i].x) * wk;
-                    v1 = __fdividef(v1, 1.0f + __expf(-v1)) * __uint_as_float(x2v[i].y) * wk;
-                    v2 = __fdividef(v2, 1.0f + __expf(-v2)) * __uint_as_float(x2v[i].z) * wk;
-                    v3 = __fdividef(v3, 1.0f + __expf(-v3)) * __uint_as_float(x2v[i].w) * wk;
-                }
-                float m = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
-                float s = (v0 + v1) + (v2 + v3);
-                m = fmaxf(m, dpp<DPP_XOR1>(m));
-                m = fmaxf(m, dpp<DPP_XOR2>(m));
-                m = fmaxf(m, dpp<DPP_HALF_MIRROR>(m));
-                m = fmaxf(m, dpp<DPP_MIRROR>(m));
-                s = sum8(s);
-                s += dpp<DPP_MIRROR>(s);
-                // rows of 16 -> the two blocks (lanes 0..31 and 32..63)
-                const float Ma = fmaxf(lane_of(m, 0), lane_of(m, 16));
-                const float Mb = fmaxf(lane_of(m, 32), lane_of(m, 48));
-                const float Sa = lane_of(s, 0) + lane_of(s, 16);
-                const float Sb = lane_of(s, 32) + lane_of(s, 48);
-                const float M = hi ? Mb : Ma;
-                const float inv = M > 0.0f ? (127.0f * 2097152.0f) * __builtin_amdgcn_rcpf(M) : 0.0f;
-                int8_t* dst = xq + (2 * p + hi) * FRAG;
-                put_digits(dst, pos0, v0, inv);
-                put_digits(dst, pos1, v1, inv);
-                put_digits(dst, pos2, v2, inv);
-                put_digits(dst, pos3, v3, inv);
-                if ((lane & 31) == 0) xs[2 * p + hi] = make_float2(M * (1.0f / 127.0f), hi ? Sb : Sa);
+                float v2[2][4];
+                pair_values(i, v2[0]);
+                pair_values(i + 1, v2[1]);
+                Dig d2[2];
+                digitize2(v2, d2);
+                put_pair(i, d2[0]);
+                put_pair(i + 1, d2[1]);
             }
         }
         if constexpr (xform == XF_NORM) {
@@ -1120,6 +1193,9 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
             return hipErrorInvalidValue;
         if (J.scores && (J.n_exp < 1 || J.n_exp > ROUTE_MAXN || J.top_k < 1 || J.top_k > MAX_JOBS ||
                          J.sel_k >= J.top_k || !J.ids_out || !J.w_out))
+            return hipErrorInvalidValue;
+        // a K-slice's blocks must fit the workgroup (FAST_MAXBK / tw)
+        if (!J.routed && ((uint64_t)P.nb + P.kg - 1) / P.kg > (uint64_t)(FAST_MAXBK / P.tw))
             return hipErrorInvalidValue;
         const int tiles = (int)(m.rows_pad / TILE_ROWS);
         P.nwg = (tiles + P.tw - 1) / P.tw * P.kg;
