@@ -27,6 +27,8 @@
 // which keeps the small values of a block that holds an outlier accurate.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #define REF_EXPF_FN __device__ __forceinline__
 #include "ref_expf.h"
 #include "wpcg_internal.hpp"
@@ -301,6 +303,11 @@ struct FastProblem {
     float eps;
     int enb;  // routed: blocks per row of one expert (nb = top_k * enb)
     int head_dim, n_heads;  // XF_MERGE
+    // set by the host so that the kernel divides nothing: blocks per K-slice
+    // ceil(nb / kg), log2 of tw, and ceil(2^32 / kg) (0 when kg = 1) for
+    // workgroup / kg as a multiply-high (exact for workgroups < 2^16)
+    int nbk, ltw;
+    uint32_t kg_inv;
 };
 struct FastBatch {
     FastProblem p[MAX_JOBS];
@@ -453,24 +460,25 @@ __device__ __forceinline__ void route_wg(const float* __restrict__ scores, int n
                 w[r] = v[q];
             }
         }
-        if (lane == 0) {  // this wave's own LDS writes are in place
-            const int got = min(top_k, *s_selectable);
+        // Lane k < top_k finishes slot k (this wave's own LDS writes above
+        // are in place for its reads): one read per lane, the chosen
+        // weights' sum in chosen order through lane reads, the divisions in
+        // parallel (one lane doing all of it serially through LDS took 1.2 us)
+        const int got = __builtin_amdgcn_readfirstlane(min(top_k, *s_selectable));
+        float wk = lane < got ? w[lane] : 0.0f;
+        if (norm_topk) {
             float sw = 0.0f;
-            if (norm_topk)
-                for (int k = 0; k < got; k++) sw = __fadd_rn(sw, w[k]);
-            for (int k = 0; k < top_k; k++) {
-                if (k >= got) {
-                    ids[k] = -1;
-                    w[k] = 0.0f;
-                } else if (norm_topk && sw > 0.0f) {
-                    w[k] = __fdiv_rn(w[k], sw);
-                }
-            }
+            for (int k = 0; k < got; k++) sw = __fadd_rn(sw, lane_of(wk, k));
+            if (sw > 0.0f) wk = __fdiv_rn(wk, sw);
+        }
+        if (lane < top_k) {
+            if (lane >= got) ids[lane] = -1;
+            w[lane] = lane < got ? wk : 0.0f;
         }
     }
 }
 
-// A workgroup of 8 waves computes tw (1 or 2) 16-row tiles over one K-slice
+// A workgroup of 8 waves computes tw (1, 2 or 4) 16-row tiles over one K-slice
 // of nbl <= 8*QB/tw blocks.
 //   prep:  the slice's x becomes int8 digit fragments in LDS, shared by all
 //          waves; a wave takes two blocks at a time (32 lanes, 4 values each).
@@ -544,10 +552,12 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     const uint32_t* params = P.params;
     const float* const x0 = P.x;
     // these loads go out together, before the exit test below needs nwg
+    const int nbk_ = P.nbk, ltw_ = P.ltw;
+    const uint32_t kg_inv_ = P.kg_inv;
     asm volatile("" ::"s"(nb), "s"(kg), "s"(tw), "s"(nwg), "s"(rows_pad), "s"(codes), "s"(hplane),
-                 "s"(params), "s"(x0));
+                 "s"(params), "s"(x0), "s"(nbk_), "s"(ltw_), "s"(kg_inv_));
     if (local >= nwg) return;  // past this problem's workgroups
-    const int kgi = local % kg, tg = local / kg;  // K-slice, tile group
+    const int tg = kg == 1 ? local : (int)__umulhi((uint32_t)local, kg_inv_), kgi = local - tg * kg;  // tile group, K-slice
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     // the slice: blocks [b0, b0 + nbl) of the matrix (of expert sel[kgi] in
     // a routed problem), its x (g) and u at xp / x2p
@@ -562,7 +572,7 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
         xp = x0;
         x2p = P.x2;
     } else {
-        const int nbk = (nb + kg - 1) / kg;
+        const int nbk = nbk_;
         b0 = kgi * nbk;
         nbl = max(0, min(nb, b0 + nbk) - b0);
         xp = x0 + (size_t)b0 * 128;
@@ -618,8 +628,14 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
             in.o[cc] = make_float4(__uint_as_float(o.x), __uint_as_float(o.y), __uint_as_float(o.z), __uint_as_float(o.w));
         }
     };
-    MergeIn mg0;
-    if constexpr (xform == XF_MERGE) merge_load(0, mg0);
+    // Pair 1 too when the slice has it (an unsplit o_proj: dense Qwen3-4B
+    // decode 685 -> 699 tok/s); v3's extra weight registers leave no room
+    // for its states, which it loads in the prep.
+    MergeIn mg0, mg1;
+    if constexpr (xform == XF_MERGE) {
+        merge_load(0, mg0);
+        if (SCHEME == 4 && 2 * (wave + 8) < nbl) merge_load(1, mg1);
+    }
     float wkv[XP];  // routed: the routing weight of each x pair's block
     auto load_x2 = [&]() {  // the second operand of the transform: nw or u
         const auto x2rs = buf_rsrc(xform == XF_NORM ? P.nw + (size_t)b0 * 128 : x2p, nbl * 512);
@@ -631,10 +647,13 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     // so that the routing workgroup stays within two per CU's registers)
     if constexpr ((xform == XF_NORM || xform == XF_SILU) && KIND != FK_ROUTE) load_x2();
     if constexpr (KIND == FK_ROUTED) {
+        // blk / enb as (blk * minv) >> 20: exact for blk < 2^20 / enb, and
+        // blk < FAST_MAXBK here
+        const uint32_t minv = (1u << 20) / (uint32_t)P.enb + 1;
 #pragma unroll
         for (int i = 0; i < XP; i++) {
             const int blk = 2 * (wave + 8 * i) + (lane >> 5);
-            wkv[i] = blk < nbl ? P.rw[blk / P.enb] : 0.0f;
+            wkv[i] = blk < nbl ? P.rw[((uint32_t)blk * minv) >> 20] : 0.0f;
         }
     }
     if constexpr (KIND == FK_ROUTE) {  // this workgroup routes itself
@@ -662,9 +681,9 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
         params += t0 * TILE_ROWS;
     }
     const int ntiles = rows_pad / TILE_ROWS;
-    const int kw = 8 / tw;                           // waves per tile
-    const int T = tg * tw + wave / kw, kq = wave % kw;
-    const int q = (nbl + kw - 1) / kw;               // blocks per part (<= QB)
+    const int ltw = ltw_, lkw = 3 - ltw, kw = 1 << lkw;  // kw = 8 / tw waves per tile
+    const int T = (tg << ltw) + (wave >> lkw), kq = wave & (kw - 1);
+    const int q = (nbl + kw - 1) >> lkw;             // blocks per part (<= QB)
     const int qw = live && T < ntiles ? max(0, min(q, nbl - kq * q)) : 0;  // this wave's blocks
     const int wb = b0 + kq * q;                      // its first block
     const int g = lane >> 4, j = lane & 15;
@@ -697,12 +716,17 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
         const int selv = (int)__builtin_amdgcn_raw_buffer_load_b32(buf_rsrc(P.sel, top_k * 4), (lane & 15) * 4, 0, 0);
         size_t recs[QB];
         int ok[QB];
+        // block wb + i is block r of slot `slot`, stepped without a division
+        int slot = wb / enb, r = wb - slot * enb;
 #pragma unroll
         for (int i = 0; i < QB; i++) {
-            const int cb = wb + i, slot = cb / enb;
             const int ei = i < qw ? __builtin_amdgcn_readlane(selv, min(slot, top_k - 1)) : -1;
             ok[i] = ei >= 0;
-            recs[i] = ((size_t)max(ei, 0) * tiles_e + Tc) * enb + cb % enb;
+            recs[i] = ((size_t)max(ei, 0) * tiles_e + Tc) * enb + r;
+            if (++r == enb) {
+                r = 0;
+                slot++;
+            }
         }
         {
             const int bi = lane >> 2;  // params: lane l, rows 4(l&3)..+3 of block l>>2
@@ -732,8 +756,7 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     // reciprocal. A wave digitises its pairs two at a time in one straight
     // run of code, so the two pairs' dependent chains (reductions, reciprocal,
     // rounding) overlap; the prep is latency-bound, one wave per SIMD at a
-    // time. A pair past the slice computes on zeros (its buffer loads
-    // returned zeros) and writes nothing.
+    // time. A wave's last pair, when it has an odd number, goes alone.
     {
         const int hi = lane >> 5, k0 = 4 * (lane & 31);
         const int pos0 = frag_pos(k0), pos1 = frag_pos(k0 + 1), pos2 = frag_pos(k0 + 2), pos3 = frag_pos(k0 + 3);
@@ -744,8 +767,9 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
             if constexpr (xform == XF_MERGE) {
                 // sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, M = max_c m_c
                 MergeIn later;
-                if (i > 0) merge_load(i, later);
-                const MergeIn& in = i == 0 ? mg0 : later;
+                constexpr int early = SCHEME == 4 ? 2 : 1;  // pairs loaded at entry
+                if (i >= early) merge_load(i, later);
+                const MergeIn& in = i == 0 ? mg0 : i < early ? mg1 : later;
                 float M = -INFINITY;
 #pragma unroll
                 for (int cc = 0; cc < ATTN_CHUNKS; cc++) M = fmaxf(M, in.m[cc]);
@@ -788,46 +812,47 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
         // block ends with the same values, the sums added in one fixed order.
         // Then the 28-bit Q of each value.
         struct Dig { int Q[4]; float M, S; };
-        auto digitize2 = [&](const float (&v)[2][4], Dig (&d)[2]) {
+        auto digitize = [&](auto npairs, const float (&v)[2][4], Dig (&d)[2]) {
+            constexpr int NP = decltype(npairs)::value;
             uint32_t mb[2];
             float sm[2];
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
+            for (int u = 0; u < NP; u++) {
                 mb[u] = __float_as_uint(fmaxf(fmaxf(fabsf(v[u][0]), fabsf(v[u][1])), fmaxf(fabsf(v[u][2]), fabsf(v[u][3]))));
                 sm[u] = (v[u][0] + v[u][1]) + (v[u][2] + v[u][3]);
             }
 #pragma unroll
-            for (int u = 0; u < 2; u++) mb[u] = max(mb[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb[u], DPP_XOR1, 0xF, 0xF, false));
+            for (int u = 0; u < NP; u++) mb[u] = max(mb[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb[u], DPP_XOR1, 0xF, 0xF, false));
 #pragma unroll
-            for (int u = 0; u < 2; u++) sm[u] += dpp<DPP_XOR1>(sm[u]);
+            for (int u = 0; u < NP; u++) sm[u] += dpp<DPP_XOR1>(sm[u]);
 #pragma unroll
-            for (int u = 0; u < 2; u++) mb[u] = max(mb[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb[u], DPP_XOR2, 0xF, 0xF, false));
+            for (int u = 0; u < NP; u++) mb[u] = max(mb[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb[u], DPP_XOR2, 0xF, 0xF, false));
 #pragma unroll
-            for (int u = 0; u < 2; u++) sm[u] += dpp<DPP_XOR2>(sm[u]);
+            for (int u = 0; u < NP; u++) sm[u] += dpp<DPP_XOR2>(sm[u]);
 #pragma unroll
-            for (int u = 0; u < 2; u++) mb[u] = max(mb[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb[u], DPP_HALF_MIRROR, 0xF, 0xF, false));
+            for (int u = 0; u < NP; u++) mb[u] = max(mb[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb[u], DPP_HALF_MIRROR, 0xF, 0xF, false));
 #pragma unroll
-            for (int u = 0; u < 2; u++) sm[u] += dpp<DPP_HALF_MIRROR>(sm[u]);
+            for (int u = 0; u < NP; u++) sm[u] += dpp<DPP_HALF_MIRROR>(sm[u]);
 #pragma unroll
-            for (int u = 0; u < 2; u++) mb[u] = max(mb[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb[u], DPP_MIRROR, 0xF, 0xF, false));
+            for (int u = 0; u < NP; u++) mb[u] = max(mb[u], (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb[u], DPP_MIRROR, 0xF, 0xF, false));
 #pragma unroll
-            for (int u = 0; u < 2; u++) sm[u] += dpp<DPP_MIRROR>(sm[u]);
+            for (int u = 0; u < NP; u++) sm[u] += dpp<DPP_MIRROR>(sm[u]);
             float inv[2];
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
+            for (int u = 0; u < NP; u++) {
                 const auto mr = __builtin_amdgcn_permlane16_swap(mb[u], mb[u], false, false);
                 d[u].M = __uint_as_float(max((uint32_t)mr[0], (uint32_t)mr[1]));
                 inv[u] = d[u].M > 0.0f ? (127.0f * 2097152.0f) * __builtin_amdgcn_rcpf(d[u].M) : 0.0f;
             }
 #pragma unroll
-            for (int u = 0; u < 2; u++) {
+            for (int u = 0; u < NP; u++) {
                 const auto sr = __builtin_amdgcn_permlane16_swap(__float_as_uint(sm[u]), __float_as_uint(sm[u]), false, false);
                 d[u].S = __uint_as_float(sr[0]) + __uint_as_float(sr[1]);
             }
 #pragma unroll
             for (int e = 0; e < 4; e++)
 #pragma unroll
-                for (int u = 0; u < 2; u++) d[u].Q[e] = (int)rintf(v[u][e] * inv[u]);
+                for (int u = 0; u < NP; u++) d[u].Q[e] = (int)rintf(v[u][e] * inv[u]);
         };
         // pair i's digit bytes and {s_b, sum} into LDS (pairs inside the slice)
         auto put_pair = [&](int i, const Dig& d) {
@@ -854,12 +879,17 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
                         xv[i + 1] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (wave + 8 * (i + 1)) * 1024 + lane * 16, 0, 0);
                     }
                 float v2[2][4];
-                pair_values(i, v2[0]);
-                pair_values(i + 1, v2[1]);
                 Dig d2[2];
-                digitize2(v2, d2);
-                put_pair(i, d2[0]);
-                put_pair(i + 1, d2[1]);
+                pair_values(i, v2[0]);
+                if (2 * (wave + 8 * (i + 1)) < nbl) {
+                    pair_values(i + 1, v2[1]);
+                    digitize(std::integral_constant<int, 2>(), v2, d2);
+                    put_pair(i, d2[0]);
+                    put_pair(i + 1, d2[1]);
+                } else {  // the wave's last pair
+                    digitize(std::integral_constant<int, 1>(), v2, d2);
+                    put_pair(i, d2[0]);
+                }
             }
         }
         if constexpr (xform == XF_NORM) {
@@ -1199,6 +1229,10 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
             return hipErrorInvalidValue;
         const int tiles = (int)(m.rows_pad / TILE_ROWS);
         P.nwg = (tiles + P.tw - 1) / P.tw * P.kg;
+        if (P.nwg >= 65536) return hipErrorInvalidValue;
+        P.nbk = (P.nb + P.kg - 1) / P.kg;
+        P.ltw = P.tw == 4 ? 2 : P.tw == 2 ? 1 : 0;
+        P.kg_inv = P.kg > 1 ? (uint32_t)((0x100000000ull + P.kg - 1) / P.kg) : 0u;
         wgs = std::max(wgs, P.nwg);
     }
     if (wgs == 0) return hipSuccess;
