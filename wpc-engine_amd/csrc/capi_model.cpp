@@ -61,6 +61,9 @@ struct wpcg_model {
     // FAST attention's chunk states, merged by the o_proj GEMV (null: the
     // head shape needs the one-workgroup-per-head kernel)
     float *part_o = nullptr, *part_ml = nullptr;
+    // o_proj's second K-slice when its two slices are left to the readers
+    // of the residual (the router, gate/up and down add it as they read)
+    float* o2 = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int graph_mode = -1;
@@ -180,6 +183,7 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
     for (uint32_t l = 0; l < c.n_layers; l++) {
         Layer& L = m->layers[l];
         bool fused = fast;
+        const float* o2 = nullptr;  // o_proj's deferred second slice, if any
         GemvJob qkv_jobs[3] = {fast_job(L.q, m->residual, m->q, L.in_ln, c.eps, fused),
                                fast_job(L.k, m->residual, m->k, L.in_ln, c.eps, fused),
                                fast_job(L.v, m->residual, m->v, L.in_ln, c.eps, fused)};
@@ -204,7 +208,13 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
             o.st = m->st;
             o.head_dim = hd;
             o.n_heads = nh;
+            // Two K-slices: no handoff between them. Slice 0 adds its sum to
+            // the residual in place, slice 1 writes o2, and the next ops read
+            // residual + o2 (a handoff of three device-scope round trips
+            // cost ~1-2 us at the end of the launch).
+            if (L.o->plan.kg == 2) o.y2 = m->o2;
             WPCG_HIP(launch_gemv_fast(&o, 1, s));
+            o2 = o.y2;
         } else {
             WPCG_HIP(launch_attention(mode, m->q, m->k, m->v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale,
                                       m->cos_t, m->sin_t, m->st, kc, vc, m->attn, s));
@@ -216,7 +226,7 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
             if (rc) return rc;
         }
         if (c.n_experts && fast) {
-            if (int rc = moe_run(L.moe, m->residual, m->residual, m->residual, s, L.post_ln, c.eps)) return rc;
+            if (int rc = moe_run(L.moe, m->residual, m->residual, m->residual, s, L.post_ln, c.eps, o2)) return rc;
             continue;
         }
         if (!c.n_experts && fast) {  // dense SwiGLU: norm into gate/up, SiLU*up into down
@@ -224,14 +234,17 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
             GemvJob gu_jobs[2] = {fast_job(L.gate, m->residual, m->g, L.post_ln, c.eps, fused),
                                   fast_job(L.up, m->residual, m->u, L.post_ln, c.eps, fused)};
             if (fused) {
+                gu_jobs[0].x_add = gu_jobs[1].x_add = o2;
                 WPCG_HIP(launch_gemv_fast(gu_jobs, 2, s));
                 GemvJob down{&L.down->m, &L.down->plan, m->g, m->residual, m->residual};
                 down.xform = XF_SILU;
                 down.x2 = m->u;
+                down.bias2 = o2;
                 WPCG_HIP(launch_gemv_fast(&down, 1, s));
                 continue;
             }
         }
+        if (o2) return fail(WPCG_E_UNSUPPORTED, "deferred o_proj slice without a FAST reader");
         WPCG_HIP(launch_rms_norm(mode, m->residual, L.post_ln, H, c.eps, m->normed, s));
         if (c.n_experts) {
             if (int rc = moe_run(L.moe, m->normed, m->residual, m->residual, s)) return rc;
@@ -551,6 +564,7 @@ int wpcg_model_create(wpcg_ctx* ctx, int scheme, const wpcg_model_config* cfg, w
     if (attention_fast_ok((int)c.n_heads, (int)c.n_kv_heads, (int)hd)) {
         dev((void**)&m->part_o, (size_t)ATTN_CHUNKS * qd * 4);
         dev((void**)&m->part_ml, (size_t)ATTN_CHUNKS * c.n_heads * 2 * 4);
+        dev((void**)&m->o2, (size_t)c.hidden * 4);
     }
     if (rc == WPCG_OK) {
         // RoPE angles as rope.rs:29-33 computes them: f64 pow, sin, cos, cast to f32

@@ -52,12 +52,18 @@ DeviceMatrix expert_view(int scheme, uint64_t rows, uint64_t cols)
 
 }  // namespace
 
+// x_add (FAST, routed, with nw): the layer input is x + x_add, a deferred
+// K-slice of the GEMV that wrote x; the router and gate/up add it as they
+// read x, and the down projection adds it to `add`.
 int wpcg::moe_run(wpcg_moe* m, const float* x_dev, float* out_dev, const float* add, hipStream_t s,
-                  const float* nw, float eps)
+                  const float* nw, float eps, const float* x_add)
 {
     const int K = (int)m->top_k, H = (int)m->hidden, I = (int)m->inter;
+    if (x_add && !(m->mode == WPCG_MODE_FAST && m->routed && nw && add))
+        return fail(WPCG_E_UNSUPPORTED, "a deferred input slice needs the FAST routed path");
     if (m->mode == WPCG_MODE_FAST && m->routed) {
-        WPCG_HIP(launch_dense(m->router->w, (int)m->n_exp, H, m->mode, x_dev, nullptr, m->scores, s, nw, eps));
+        WPCG_HIP(launch_dense(m->router->w, (int)m->n_exp, H, m->mode, x_dev, nullptr, m->scores, s, nw, eps,
+                              x_add));
         GemvJob jobs[MAX_JOBS];
         for (int k = 0; k < 2 * K; k++) {
             GemvJob& J = jobs[k];
@@ -73,6 +79,7 @@ int wpcg::moe_run(wpcg_moe* m, const float* x_dev, float* out_dev, const float* 
             J.norm_topk = m->norm_topk;
             J.ids_out = m->ids;
             J.w_out = m->w;
+            J.x_add = x_add;
         }
         WPCG_HIP(launch_gemv_fast(jobs, 2 * K, s));
         GemvJob down{&m->down, &m->plan, m->g, add, out_dev, m->ids};
@@ -81,6 +88,7 @@ int wpcg::moe_run(wpcg_moe* m, const float* x_dev, float* out_dev, const float* 
         down.routed = 1;
         down.rw = m->w;
         down.top_k = K;
+        down.bias2 = x_add;
         WPCG_HIP(launch_gemv_fast(&down, 1, s));
         return WPCG_OK;
     }

@@ -308,6 +308,11 @@ struct FastProblem {
     // workgroup / kg as a multiply-high (exact for workgroups < 2^16)
     int nbk, ltw;
     uint32_t kg_inv;
+    // deferred K-split (kg = 2): slice 1 writes its sum to y2; XF_NORM adds
+    // x_add to x; the bias is bias + bias2
+    float* y2;
+    const float* x_add;
+    const float* bias2;
 };
 struct FastBatch {
     FastProblem p[MAX_JOBS];
@@ -334,18 +339,6 @@ __device__ __forceinline__ int frag_pos(int k)
     return (k >> 6) * HALF + (k & 3) * (NDIG * 16) + ((k >> 3) & 7) + 8 * ((k >> 2) & 1);
 }
 
-// Q = d0*2^21 + d1*2^14 + d2*2^7 + d3 with |Q| <= 127*2^21 (+ rounding):
-// d0 = Q >> 21 (arithmetic) in [-128, 127] and d1, d2, d3 the three 7-bit
-// fields of Q mod 2^21, in [0, 127]. `pos` is frag_pos(k).
-__device__ __forceinline__ void put_digits(int8_t* blk, int pos, float v, float inv)
-{
-    const int Q = (int)rintf(v * inv);
-    int8_t* p = blk + pos;
-    p[0] = (int8_t)(Q >> 21);
-    p[16] = (int8_t)((Q >> 14) & 127);
-    p[32] = (int8_t)((Q >> 7) & 127);
-    p[48] = (int8_t)(Q & 127);
-}
 
 // DPP lane exchange inside rows of 16 lanes (full row and bank masks).
 template <int CTRL>
@@ -358,14 +351,6 @@ constexpr int DPP_XOR2 = 0x4E;         // quad_perm [2,3,0,1]
 constexpr int DPP_HALF_MIRROR = 0x141; // lane i <-> 7-i within each 8
 constexpr int DPP_MIRROR = 0x140;      // lane i <-> 15-i within each 16
 
-// Sum over the 8 lanes of each half-row; every lane of the 8 ends with the
-// same value (each step adds a lane and its partner, which commute).
-__device__ __forceinline__ float sum8(float v)
-{
-    v += dpp<DPP_XOR1>(v);
-    v += dpp<DPP_XOR2>(v);
-    return v + dpp<DPP_HALF_MIRROR>(v);
-}
 
 __device__ __forceinline__ float lane_of(float v, int l)
 {
@@ -591,12 +576,21 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     // across the memory round trip.
     constexpr int XP0 = 2;
     const auto xrs = buf_rsrc(xp, nbl * 512);
-    u32x4 xv[XP], x2v[XP];
+    u32x4 xv[XP], x2v[XP], xav[XP];
     if constexpr (xform != XF_MERGE) {
 #pragma unroll
         for (int i = 0; i < XP; i++)
             if (XF != XF_NONE || i < XP0)
                 xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
+    }
+    const bool has_xa = XF == XF_NORM && P.x_add;  // the deferred slice, with x's loads
+    if constexpr (XF == XF_NORM) {
+        if (has_xa) {
+            const auto ars = buf_rsrc(P.x_add + (size_t)b0 * 128, nbl * 512);
+#pragma unroll
+            for (int i = 0; i < XP; i++)
+                xav[i] = __builtin_amdgcn_raw_buffer_load_b128(ars, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
+        }
     }
     // XF_MERGE: the chunk states of x pair p = wave + 8i: for every chunk
     // c, (m, l) of the head of this lane's four values and their four
@@ -763,7 +757,6 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
         float sq = 0.0f;
         // x' of pair i (after the transform) as four values per lane
         auto pair_values = [&](int i, float (&v)[4]) {
-            const int p = wave + 8 * i;
             if constexpr (xform == XF_MERGE) {
                 // sum_c e^(m_c - M) o_c / sum_c e^(m_c - M) l_c, M = max_c m_c
                 MergeIn later;
@@ -794,6 +787,10 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
             v[0] = __uint_as_float(xv[i].x); v[1] = __uint_as_float(xv[i].y);
             v[2] = __uint_as_float(xv[i].z); v[3] = __uint_as_float(xv[i].w);
             if constexpr (xform == XF_NORM) {
+                if (has_xa) {
+                    v[0] += __uint_as_float(xav[i].x); v[1] += __uint_as_float(xav[i].y);
+                    v[2] += __uint_as_float(xav[i].z); v[3] += __uint_as_float(xav[i].w);
+                }
 #pragma unroll
                 for (int e = 0; e < 4; e++) sq = fmaf(v[e], v[e], sq);
                 v[0] *= __uint_as_float(x2v[i].x); v[1] *= __uint_as_float(x2v[i].y);
@@ -854,7 +851,11 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
 #pragma unroll
                 for (int u = 0; u < NP; u++) d[u].Q[e] = (int)rintf(v[u][e] * inv[u]);
         };
-        // pair i's digit bytes and {s_b, sum} into LDS (pairs inside the slice)
+        // pair i's digit bytes and {s_b, sum} into LDS (pairs inside the
+        // slice): Q = d0*2^21 + d1*2^14 + d2*2^7 + d3 with |Q| <= 127*2^21 (+
+        // rounding), d0 = Q >> 21 (arithmetic) in [-128, 127] and d1, d2, d3
+        // the three 7-bit fields of Q mod 2^21; digit j of index k at
+        // frag_pos(k) + 16*j
         auto put_pair = [&](int i, const Dig& d) {
             const int p = wave + 8 * i;
             if (2 * p >= nbl) return;
@@ -971,8 +972,13 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
             sum *= __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(s2, (float)(nb * 128)), P.eps)));
         }
     }
-    if (kg == 1) {
-        if (mine && orow < (size_t)P.rows) P.y[orow] = P.bias ? sum + P.bias[orow] : sum;
+    if (kg == 1 || P.y2) {  // one slice, or the deferred split: slice 1 to y2
+        if (mine && orow < (size_t)P.rows) {
+            if (kgi == 0)
+                P.y[orow] = P.bias ? sum + (P.bias2 ? P.bias[orow] + P.bias2[orow] : P.bias[orow]) : sum;
+            else
+                P.y2[orow] = sum;
+        }
         return;
     }
     // Split K: publish this slice's partials; the last workgroup of the tile
@@ -1204,6 +1210,9 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         P.ids_out = J.ids_out;
         P.w_out = J.w_out;
         P.st = J.st;
+        P.y2 = J.y2;
+        P.x_add = J.x_add;
+        P.bias2 = J.bias2;
         P.head_dim = J.head_dim;
         P.n_heads = J.n_heads;
         if (J.routed) {  // the chosen experts' rows side by side
@@ -1215,6 +1224,9 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         // routing reads at most ROUTE_MAXN scores into MAX_JOBS slots
         if (J.xform == XF_NORM && (P.kg != 1 || !J.nw)) return hipErrorInvalidValue;
         if (J.xform == XF_SILU && !J.x2) return hipErrorInvalidValue;
+        // the deferred split: two slices and no routing; x_add with the norm; bias2 with a bias
+        if (J.y2 && (P.kg != 2 || J.routed)) return hipErrorInvalidValue;
+        if ((J.x_add && J.xform != XF_NORM) || (J.bias2 && !J.bias)) return hipErrorInvalidValue;
         if (J.xform == XF_MERGE && (!J.x2 || !J.st || (J.head_dim != 64 && J.head_dim != 128) ||
                                     (uint64_t)J.n_heads * J.head_dim != m.cols))
             return hipErrorInvalidValue;

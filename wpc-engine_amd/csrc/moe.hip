@@ -132,12 +132,14 @@ __global__ __launch_bounds__(256) void k_dense_exact_lds(const float* __restrict
 // FAST: one wave per row, 16-byte coalesced loads, fixed-order tree sum
 // (deterministic, not the reference's order). With nw set, x is RMSNorm'd
 // on the fly (norm.rs:4-13): y = W (x * nw) / sqrt(mean(x^2) + eps), the
-// sum of squares taken by each wave from the x it reads anyway.
+// sum of squares taken by each wave from the x it reads anyway. With x_add
+// set, the input is x + x_add (a deferred K-slice of the GEMV that made x).
 __global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ w,
                                                     const float* __restrict__ x,
                                                     const float* __restrict__ bias,
                                                     float* __restrict__ y, int out_f, int in_f,
-                                                    const float* __restrict__ nw, float eps)
+                                                    const float* __restrict__ nw, float eps,
+                                                    const float* __restrict__ x_add)
 {
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     const float* row = w + (size_t)min(r, out_f - 1) * in_f;
@@ -152,18 +154,24 @@ __global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ w,
         const auto xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), (short)0, in_f * 4, 0x00020000);
         const auto nr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(nw ? nw : x), (short)0,
                                                           nw ? in_f * 4 : 0, 0x00020000);
+        const auto ar = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x_add ? x_add : x), (short)0,
+                                                          x_add ? in_f * 4 : 0, 0x00020000);
         for (int base = 0; base < in_f; base += 256 * DF_U) {
-            float4 v[DF_U], u[DF_U], n4[DF_U];
+            float4 v[DF_U], u[DF_U], n4[DF_U], a4[DF_U];
 #pragma unroll
             for (int q = 0; q < DF_U; q++) {
                 const int off = (base + 256 * q + 4 * lane) * 4;
                 v[q] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
                 u[q] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
                 if (nw) n4[q] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(nr, off, 0, 0));
+                if (x_add) a4[q] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ar, off, 0, 0));
             }
 #pragma unroll
             for (int q = 0; q < DF_U; q++) {
                 float4 uq = u[q];
+                if (x_add) {
+                    uq.x += a4[q].x; uq.y += a4[q].y; uq.z += a4[q].z; uq.w += a4[q].w;
+                }
                 if (nw) {
                     sq = fmaf(uq.x, uq.x, sq); sq = fmaf(uq.y, uq.y, sq);
                     sq = fmaf(uq.z, uq.z, sq); sq = fmaf(uq.w, uq.w, sq);
@@ -178,6 +186,7 @@ __global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ w,
     } else {
         for (int i = lane; i < in_f; i += 64) {
             float u = x[i];
+            if (x_add) u += x_add[i];
             if (nw) {
                 sq = fmaf(u, u, sq);
                 u *= nw[i];
@@ -399,11 +408,12 @@ __global__ __launch_bounds__(256) void k_combine(const float* __restrict__ ys,
 }  // namespace
 
 hipError_t launch_dense(const float* w, int out_f, int in_f, int mode, const float* x,
-                        const float* bias, float* y, hipStream_t s, const float* nw, float eps)
+                        const float* bias, float* y, hipStream_t s, const float* nw, float eps,
+                        const float* x_add)
 {
     (void)hipGetLastError();
     if (mode == WPCG_MODE_EXACT) {
-        if (nw) return hipErrorInvalidValue;  // EXACT normalises in its own launch
+        if (nw || x_add) return hipErrorInvalidValue;  // EXACT normalises in its own launch
         if (in_f % 4 == 0 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)x & 15) == 0)
             hipLaunchKernelGGL(k_dense_exact_lds, dim3((out_f + DE_ROWS - 1) / DE_ROWS), dim3(256), 0, s, w, x,
                                bias, y, out_f, in_f);
@@ -412,7 +422,7 @@ hipError_t launch_dense(const float* w, int out_f, int in_f, int mode, const flo
                                out_f, in_f);
     } else {
         hipLaunchKernelGGL(k_dense_fast, dim3((out_f + 3) / 4), dim3(256), 0, s, w, x, bias, y,
-                           out_f, in_f, nw, eps);
+                           out_f, in_f, nw, eps, x_add);
     }
     return hipGetLastError();
 }

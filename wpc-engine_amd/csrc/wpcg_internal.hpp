@@ -111,8 +111,16 @@ struct GemvJob {
     const float* x2 = nullptr;
     const float* nw = nullptr;
     float eps = 0.0f;
-    const DecodeState* st = nullptr;  // XF_MERGE: the position (the chunk count)
+    const DecodeState* st = nullptr;  // XF_MERGE: checked present (the merge reads every chunk)
     int head_dim = 0, n_heads = 0;    // XF_MERGE
+    // Deferred K-split (plan->kg == 2, not routed): slice 0 writes its sum
+    // (+ bias) to y and slice 1 its sum to y2, with no handoff between the
+    // slices; the consumer adds y2 (x_add, bias2 below).
+    float* y2 = nullptr;
+    // XF_NORM: x + x_add is the vector normalised (the deferred slice)
+    const float* x_add = nullptr;
+    // with bias: y = sum + (bias + bias2)
+    const float* bias2 = nullptr;
     // routed: the rows of experts sel[0..top_k) side by side as one K of
     // top_k * cols (one K-slice: plan->kg = 1), x of slot k at x + k*cols
     // (g) and x2 + k*cols (u), scaled by rw[k]; y = bias + the row sum
@@ -257,9 +265,10 @@ int make_plan(const DeviceMatrix& m, FastPlan& plan, hipStream_t s, int kg = 0);
 
 // ---- MoE pieces (moe.hip) -------------------------------------------------
 // nw (FAST only): RMSNorm of x with weights nw and epsilon eps folded in.
+// FAST: x_add, if set, is added to x as it is read (a deferred K-slice).
 hipError_t launch_dense(const float* w, int out_f, int in_f, int mode, const float* x,
                         const float* bias, float* y, hipStream_t s, const float* nw = nullptr,
-                        float eps = 0.0f);
+                        float eps = 0.0f, const float* x_add = nullptr);
 hipError_t launch_softmax(float* x, int n, hipStream_t s);
 int route_max_n();
 hipError_t launch_route(const float* p, int n, int top_k, int norm_topk, int32_t* ids, float* w,
@@ -277,7 +286,7 @@ hipError_t launch_softmax_route(const float* scores, int n, int top_k, int norm_
 // the chosen experts (SiLU*up and the routing weight folded into its x,
 // the combine and the residual into its ordered split-K sum).
 int moe_run(wpcg_moe* m, const float* x, float* out, const float* add, hipStream_t s,
-            const float* nw = nullptr, float eps = 0.0f);
+            const float* nw = nullptr, float eps = 0.0f, const float* x_add = nullptr);
 
 // ---- decode step (decode.hip) ----------------------------------------------
 hipError_t launch_embed_tok(const DeviceMatrix& m, const uint32_t* tokens, const DecodeState* st,
