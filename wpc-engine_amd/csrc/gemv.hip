@@ -539,8 +539,20 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     // these loads go out together, before the exit test below needs nwg
     const int nbk_ = P.nbk, ltw_ = P.ltw;
     const uint32_t kg_inv_ = P.kg_inv;
-    asm volatile("" ::"s"(nb), "s"(kg), "s"(tw), "s"(nwg), "s"(rows_pad), "s"(codes), "s"(hplane),
-                 "s"(params), "s"(x0), "s"(nbk_), "s"(ltw_), "s"(kg_inv_));
+    // With them, the fields each kind reads before its weight loads (read
+    // where they are used, each was a further dependent round trip): one
+    // statement, so that one wait covers them all.
+    {
+        const float* f0 = XF == XF_NORM ? P.x_add : XF == XF_SILU || XF == XF_MERGE ? P.x2 : nullptr;
+        const float* f1 = XF == XF_NORM ? P.nw : KIND == FK_ROUTE ? P.scores : KIND == FK_ROUTED ? P.rw : nullptr;
+        const int32_t* f2 = KIND != FK_ROUTE ? P.sel : nullptr;
+        const int i0 = XF == XF_MERGE ? P.head_dim : KIND == FK_ROUTE ? P.n_exp : KIND == FK_ROUTED ? P.enb : 0;
+        const int i1 = XF == XF_MERGE ? P.n_heads : KIND != FK_PLAIN ? P.top_k : 0;
+        const int i2 = KIND == FK_ROUTE ? P.norm_topk : 0, i3 = KIND == FK_ROUTE ? P.sel_k : 0;
+        asm volatile("" ::"s"(nb), "s"(kg), "s"(tw), "s"(nwg), "s"(rows_pad), "s"(codes), "s"(hplane),
+                     "s"(params), "s"(x0), "s"(nbk_), "s"(ltw_), "s"(kg_inv_), "s"(f0), "s"(f1), "s"(f2), "s"(i0),
+                     "s"(i1), "s"(i2), "s"(i3));
+    }
     if (local >= nwg) return;  // past this problem's workgroups
     const int tg = kg == 1 ? local : (int)__umulhi((uint32_t)local, kg_inv_), kgi = local - tg * kg;  // tile group, K-slice
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -637,9 +649,11 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
         for (int i = 0; i < XP; i++)
             x2v[i] = __builtin_amdgcn_raw_buffer_load_b128(x2rs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
     };
-    // (routing keeps x in flight; the norm weights, L2-resident, wait for it
-    // so that the routing workgroup stays within two per CU's registers)
-    if constexpr ((xform == XF_NORM || xform == XF_SILU) && KIND != FK_ROUTE) load_x2();
+    // (with routing too: requested after routing, the norm weights were a
+    // memory round trip on the critical path, ~1 us; the registers this holds
+    // across routing leave one routing workgroup per CU, which is what a
+    // top-8 gate/up launch of 192 workgroups uses)
+    if constexpr (xform == XF_NORM || xform == XF_SILU) load_x2();
     if constexpr (KIND == FK_ROUTED) {
         // blk / enb as (blk * minv) >> 20: exact for blk < 2^20 / enb, and
         // blk < FAST_MAXBK here
@@ -663,7 +677,6 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
             P.ids_out[threadIdx.x] = route_ids[threadIdx.x];
             P.w_out[threadIdx.x] = route_w[threadIdx.x];
         }
-        if constexpr (xform != XF_NONE) load_x2();
     } else if constexpr (KIND == FK_PLAIN) {
         if (P.sel) e = P.sel[P.sel_k];
     }
