@@ -129,11 +129,15 @@ __global__ __launch_bounds__(256) void k_dense_exact_lds(const float* __restrict
     if (t < DE_ROWS && r0 + t < out_f) y[r0 + t] = bias ? __fadd_rn(acc, bias[r0 + t]) : acc;
 }
 
-// FAST: one wave per row, 16-byte coalesced loads, fixed-order tree sum
-// (deterministic, not the reference's order). With nw set, x is RMSNorm'd
-// on the fly (norm.rs:4-13): y = W (x * nw) / sqrt(mean(x^2) + eps), the
-// sum of squares taken by each wave from the x it reads anyway. With x_add
-// set, the input is x + x_add (a deferred K-slice of the GEMV that made x).
+// FAST: one workgroup of 4 waves per row, wave q taking the q-th quarter of
+// it, 16-byte loads with every load of a pass issued before any is used,
+// fixed-order tree sums (deterministic, not the reference's order). With nw
+// set, x is RMSNorm'd on the fly (norm.rs:4-13): y = W (x * nw) /
+// sqrt(mean(x^2) + eps), the sum of squares taken from the x the workgroup
+// reads anyway. With x_add set, the input is x + x_add (a deferred K-slice
+// of the GEMV that made x). (A wave per row and 4 rows per workgroup made
+// each CU read 4 copies of x, nw and x_add besides its rows: 3.45 us for the
+// 128 x 2048 router with x_add.)
 __global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ w,
                                                     const float* __restrict__ x,
                                                     const float* __restrict__ bias,
@@ -141,26 +145,26 @@ __global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ w,
                                                     const float* __restrict__ nw, float eps,
                                                     const float* __restrict__ x_add)
 {
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const float* row = w + (size_t)min(r, out_f - 1) * in_f;
+    __shared__ float red[2][4];
+    const int r = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const float* row = w + (size_t)r * in_f;
     float acc = 0.0f, sq = 0.0f;
     if ((in_f & 3) == 0) {
-        // DF_U float4s per lane per pass, every load of a pass issued before
-        // any is used: one memory round trip per 64 * 4 * DF_U inputs
-        // (buffer loads over exactly the row, x and nw: past the end they
-        // return zeros without touching memory, so no load needs a branch)
-        constexpr int DF_U = 8;
-        const auto wr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(row), (short)0, in_f * 4, 0x00020000);
-        const auto xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), (short)0, in_f * 4, 0x00020000);
-        const auto nr = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(nw ? nw : x), (short)0,
-                                                          nw ? in_f * 4 : 0, 0x00020000);
-        const auto ar = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x_add ? x_add : x), (short)0,
-                                                          x_add ? in_f * 4 : 0, 0x00020000);
-        for (int base = 0; base < in_f; base += 256 * DF_U) {
+        // the wave's float4s [f0, f1) of the row; buffer loads over exactly
+        // those bytes of the row, x, nw and x_add (past them zeros, no access)
+        constexpr int DF_U = 2;  // float4s per lane per pass
+        const int q4 = in_f / 4, per = (q4 + 3) / 4;
+        const int f0 = min(q4, wave * per), nb = (min(q4, f0 + per) - f0) * 16;
+        auto rs = [&](const float* p, int bytes) {
+            return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p), (short)0, bytes, 0x00020000);
+        };
+        const auto wr = rs(row + 4 * f0, nb), xr = rs(x + 4 * f0, nb);
+        const auto nr = rs(nw ? nw + 4 * f0 : x, nw ? nb : 0), ar = rs(x_add ? x_add + 4 * f0 : x, x_add ? nb : 0);
+        for (int base = 0; base < per; base += 64 * DF_U) {
             float4 v[DF_U], u[DF_U], n4[DF_U], a4[DF_U];
 #pragma unroll
             for (int q = 0; q < DF_U; q++) {
-                const int off = (base + 256 * q + 4 * lane) * 4;
+                const int off = (base + 64 * q + lane) * 16;
                 v[q] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 0));
                 u[q] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
                 if (nw) n4[q] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(nr, off, 0, 0));
@@ -184,7 +188,7 @@ __global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ w,
             }
         }
     } else {
-        for (int i = lane; i < in_f; i += 64) {
+        for (int i = threadIdx.x; i < in_f; i += 256) {
             float u = x[i];
             if (x_add) u += x_add[i];
             if (nw) {
@@ -195,11 +199,20 @@ __global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ w,
         }
     }
     acc = wave_sum(acc);
-    if (nw) {
-        sq = wave_sum(sq);
-        acc *= __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(sq, (float)in_f), eps)));
+    if (nw) sq = wave_sum(sq);
+    if (lane == 0) {
+        red[0][wave] = acc;
+        red[1][wave] = sq;
     }
-    if (r < out_f && lane == 0) y[r] = bias ? acc + bias[r] : acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float a = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+        if (nw) {
+            const float s2 = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+            a *= __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(s2, (float)in_f), eps)));
+        }
+        y[r] = bias ? a + bias[r] : a;
+    }
 }
 
 // ---- softmax_inplace (wpc-runtime/src/norm.rs:28-43) ---------------------
@@ -421,7 +434,7 @@ hipError_t launch_dense(const float* w, int out_f, int in_f, int mode, const flo
             hipLaunchKernelGGL(k_dense_exact, dim3((out_f + 63) / 64), dim3(64), 0, s, w, x, bias, y,
                                out_f, in_f);
     } else {
-        hipLaunchKernelGGL(k_dense_fast, dim3((out_f + 3) / 4), dim3(256), 0, s, w, x, bias, y,
+        hipLaunchKernelGGL(k_dense_fast, dim3(out_f), dim3(256), 0, s, w, x, bias, y,
                            out_f, in_f, nw, eps, x_add);
     }
     return hipGetLastError();
