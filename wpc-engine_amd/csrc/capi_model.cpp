@@ -64,6 +64,9 @@ struct wpcg_model {
     // o_proj's second K-slice when its two slices are left to the readers
     // of the residual (the router, gate/up and down add it as they read)
     float* o2 = nullptr;
+    // the dense down projection's K-slices 1 and 2, left the same way to the
+    // next layer's q/k/v and o_proj, or to the head
+    float* d2 = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     int graph_mode = -1;
@@ -168,6 +171,25 @@ GemvJob fast_job(wpcg_linear* lin, const float* x, float* y, const float* nw, fl
     return J;
 }
 
+// Whether FAST mode leaves the dense down projection's K-slices to their
+// readers: every reader folds the RMSNorm into its GEMV (one K-slice each)
+// or is the merging o_proj, and the down has 2 or 3 slices.
+bool defer_down(const wpcg_model* m)
+{
+    const wpcg_model_config& c = m->cfg;
+    if (m->mode != WPCG_MODE_FAST || c.n_experts || !m->part_o || !m->d2) return false;
+    const wpcg_linear* head = c.tied ? m->embed : m->lm_head;
+    if (head->plan.kg != 1 || head->m.nb == 0) return false;
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        const Layer& L = m->layers[l];
+        for (const wpcg_linear* r : {L.q, L.k, L.v})
+            if (r->plan.kg != 1 || r->m.nb == 0) return false;
+        if (L.down->plan.kg < 2 || L.down->plan.kg > 3 || L.gate->plan.kg != 1 || L.up->plan.kg != 1)
+            return false;
+    }
+    return true;
+}
+
 // One decode step on stream s: the token at tokens[pos] through every layer,
 // logits, argmax, position + 1. FAST mode folds the RMSNorms into the
 // GEMVs that read them and runs the MoE layer as three launches (moe_run);
@@ -180,6 +202,9 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
     const bool fast = mode == WPCG_MODE_FAST;
     const float scale = 1.0f / std::sqrt((float)hd);  // model.rs: 1/sqrt(head_dim) in f32
     WPCG_HIP(launch_embed_tok(m->embed->m, m->tokens, m->st, m->residual, s));
+    const bool defer_d = defer_down(m);
+    const float* d2 = nullptr;  // the previous down's deferred slices, if any
+    int n_d2 = 1;
     for (uint32_t l = 0; l < c.n_layers; l++) {
         Layer& L = m->layers[l];
         bool fused = fast;
@@ -187,9 +212,14 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
         GemvJob qkv_jobs[3] = {fast_job(L.q, m->residual, m->q, L.in_ln, c.eps, fused),
                                fast_job(L.k, m->residual, m->k, L.in_ln, c.eps, fused),
                                fast_job(L.v, m->residual, m->v, L.in_ln, c.eps, fused)};
+        for (GemvJob& J : qkv_jobs) {
+            J.x_add = d2;
+            J.n_xa = n_d2;
+        }
         if (fused) {
             WPCG_HIP(launch_gemv_fast(qkv_jobs, 3, s));
         } else {
+            if (d2) return fail(WPCG_E_UNSUPPORTED, "deferred down slices without a FAST reader");
             WPCG_HIP(launch_rms_norm(mode, m->residual, L.in_ln, H, c.eps, m->normed, s));
             wpcg_linear* qkv[3] = {L.q, L.k, L.v};
             const float* xs[3] = {m->normed, m->normed, m->normed};
@@ -213,8 +243,11 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
             // residual + o2 (a handoff of three device-scope round trips
             // cost ~1-2 us at the end of the launch).
             if (L.o->plan.kg == 2) o.y2 = m->o2;
+            o.bias2 = d2;  // the residual's deferred down slices join it here
+            o.n_b2 = n_d2;
             WPCG_HIP(launch_gemv_fast(&o, 1, s));
             o2 = o.y2;
+            d2 = nullptr;
         } else {
             WPCG_HIP(launch_attention(mode, m->q, m->k, m->v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale,
                                       m->cos_t, m->sin_t, m->st, kc, vc, m->attn, s));
@@ -240,6 +273,13 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
                 down.xform = XF_SILU;
                 down.x2 = m->u;
                 down.bias2 = o2;
+                // its K-slices 1.. go to the next layer's q/k/v and o_proj (or
+                // the head) instead of a handoff at the end of the launch
+                if (defer_d) {
+                    down.y2 = m->d2;
+                    d2 = m->d2;
+                    n_d2 = L.down->plan.kg - 1;
+                }
                 WPCG_HIP(launch_gemv_fast(&down, 1, s));
                 continue;
             }
@@ -264,6 +304,9 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
     wpcg_linear* head = c.tied ? m->embed : m->lm_head;
     bool fused = fast;
     GemvJob head_job = fast_job(head, m->residual, m->logits, m->final_norm, c.eps, fused);
+    head_job.x_add = d2;
+    head_job.n_xa = n_d2;
+    if (d2 && !fused) return fail(WPCG_E_UNSUPPORTED, "deferred down slices without a FAST reader");
     if (fused) {
         WPCG_HIP(launch_gemv_fast(&head_job, 1, s));
     } else {
@@ -565,6 +608,7 @@ int wpcg_model_create(wpcg_ctx* ctx, int scheme, const wpcg_model_config* cfg, w
         dev((void**)&m->part_o, (size_t)ATTN_CHUNKS * qd * 4);
         dev((void**)&m->part_ml, (size_t)ATTN_CHUNKS * c.n_heads * 2 * 4);
         dev((void**)&m->o2, (size_t)c.hidden * 4);
+        dev((void**)&m->d2, (size_t)2 * c.hidden * 4);
     }
     if (rc == WPCG_OK) {
         // RoPE angles as rope.rs:29-33 computes them: f64 pow, sin, cos, cast to f32

@@ -308,11 +308,13 @@ struct FastProblem {
     // workgroup / kg as a multiply-high (exact for workgroups < 2^16)
     int nbk, ltw;
     uint32_t kg_inv;
-    // deferred K-split (kg = 2): slice 1 writes its sum to y2; XF_NORM adds
-    // x_add to x; the bias is bias + bias2
+    // deferred K-split: slice k >= 1 writes its sum to y2 + (k-1)*rows;
+    // XF_NORM adds the n_xa vectors at x_add (stride nb*128) to x; the bias
+    // is bias + the n_b2 vectors at bias2 (stride rows)
     float* y2;
     const float* x_add;
     const float* bias2;
+    int n_xa, n_b2;
 };
 struct FastBatch {
     FastProblem p[MAX_JOBS];
@@ -549,9 +551,10 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
         const int i0 = XF == XF_MERGE ? P.head_dim : KIND == FK_ROUTE ? P.n_exp : KIND == FK_ROUTED ? P.enb : 0;
         const int i1 = XF == XF_MERGE ? P.n_heads : KIND != FK_PLAIN ? P.top_k : 0;
         const int i2 = KIND == FK_ROUTE ? P.norm_topk : 0, i3 = KIND == FK_ROUTE ? P.sel_k : 0;
+        const int i4 = XF == XF_NORM ? P.n_xa : 0;
         asm volatile("" ::"s"(nb), "s"(kg), "s"(tw), "s"(nwg), "s"(rows_pad), "s"(codes), "s"(hplane),
                      "s"(params), "s"(x0), "s"(nbk_), "s"(ltw_), "s"(kg_inv_), "s"(f0), "s"(f1), "s"(f2), "s"(i0),
-                     "s"(i1), "s"(i2), "s"(i3));
+                     "s"(i1), "s"(i2), "s"(i3), "s"(i4));
     }
     if (local >= nwg) return;  // past this problem's workgroups
     const int tg = kg == 1 ? local : (int)__umulhi((uint32_t)local, kg_inv_), kgi = local - tg * kg;  // tile group, K-slice
@@ -588,20 +591,27 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     // across the memory round trip.
     constexpr int XP0 = 2;
     const auto xrs = buf_rsrc(xp, nbl * 512);
-    u32x4 xv[XP], x2v[XP], xav[XP];
+    u32x4 xv[XP], x2v[XP], xav[XP], xav2[XP];
     if constexpr (xform != XF_MERGE) {
 #pragma unroll
         for (int i = 0; i < XP; i++)
             if (XF != XF_NONE || i < XP0)
                 xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
     }
-    const bool has_xa = XF == XF_NORM && P.x_add;  // the deferred slice, with x's loads
+    // the deferred slices, with x's loads
+    const bool has_xa = XF == XF_NORM && P.x_add, has_xa2 = has_xa && P.n_xa > 1;
     if constexpr (XF == XF_NORM) {
         if (has_xa) {
             const auto ars = buf_rsrc(P.x_add + (size_t)b0 * 128, nbl * 512);
 #pragma unroll
             for (int i = 0; i < XP; i++)
                 xav[i] = __builtin_amdgcn_raw_buffer_load_b128(ars, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
+        }
+        if (has_xa2) {
+            const auto ars = buf_rsrc(P.x_add + (size_t)nb * 128 + (size_t)b0 * 128, nbl * 512);
+#pragma unroll
+            for (int i = 0; i < XP; i++)
+                xav2[i] = __builtin_amdgcn_raw_buffer_load_b128(ars, (wave + 8 * i) * 1024 + lane * 16, 0, 0);
         }
     }
     // XF_MERGE: the chunk states of x pair p = wave + 8i: for every chunk
@@ -804,6 +814,10 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
                     v[0] += __uint_as_float(xav[i].x); v[1] += __uint_as_float(xav[i].y);
                     v[2] += __uint_as_float(xav[i].z); v[3] += __uint_as_float(xav[i].w);
                 }
+                if (has_xa2) {
+                    v[0] += __uint_as_float(xav2[i].x); v[1] += __uint_as_float(xav2[i].y);
+                    v[2] += __uint_as_float(xav2[i].z); v[3] += __uint_as_float(xav2[i].w);
+                }
 #pragma unroll
                 for (int e = 0; e < 4; e++) sq = fmaf(v[e], v[e], sq);
                 v[0] *= __uint_as_float(x2v[i].x); v[1] *= __uint_as_float(x2v[i].y);
@@ -985,12 +999,21 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
             sum *= __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(s2, (float)(nb * 128)), P.eps)));
         }
     }
-    if (kg == 1 || P.y2) {  // one slice, or the deferred split: slice 1 to y2
+    if (kg == 1 || P.y2) {  // one slice, or the deferred split: slices k >= 1 to y2
         if (mine && orow < (size_t)P.rows) {
-            if (kgi == 0)
-                P.y[orow] = P.bias ? sum + (P.bias2 ? P.bias[orow] + P.bias2[orow] : P.bias[orow]) : sum;
-            else
-                P.y2[orow] = sum;
+            if (kgi == 0) {
+                if (P.bias) {
+                    float b = P.bias[orow];
+                    if (P.bias2) {
+                        b += P.bias2[orow];
+                        if (P.n_b2 > 1) b += P.bias2[(size_t)P.rows + orow];
+                    }
+                    sum += b;
+                }
+                P.y[orow] = sum;
+            } else {
+                P.y2[(size_t)(kgi - 1) * P.rows + orow] = sum;
+            }
         }
         return;
     }
@@ -1226,6 +1249,8 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         P.y2 = J.y2;
         P.x_add = J.x_add;
         P.bias2 = J.bias2;
+        P.n_xa = J.n_xa;
+        P.n_b2 = J.n_b2;
         P.head_dim = J.head_dim;
         P.n_heads = J.n_heads;
         if (J.routed) {  // the chosen experts' rows side by side
@@ -1238,8 +1263,9 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         if (J.xform == XF_NORM && (P.kg != 1 || !J.nw)) return hipErrorInvalidValue;
         if (J.xform == XF_SILU && !J.x2) return hipErrorInvalidValue;
         // the deferred split: two slices and no routing; x_add with the norm; bias2 with a bias
-        if (J.y2 && (P.kg != 2 || J.routed)) return hipErrorInvalidValue;
+        if (J.y2 && (P.kg < 2 || J.routed)) return hipErrorInvalidValue;
         if ((J.x_add && J.xform != XF_NORM) || (J.bias2 && !J.bias)) return hipErrorInvalidValue;
+        if (J.n_xa < 1 || J.n_xa > 2 || J.n_b2 < 1 || J.n_b2 > 2) return hipErrorInvalidValue;
         if (J.xform == XF_MERGE && (!J.x2 || !J.st || (J.head_dim != 64 && J.head_dim != 128) ||
                                     (uint64_t)J.n_heads * J.head_dim != m.cols))
             return hipErrorInvalidValue;

@@ -113,14 +113,18 @@ struct GemvJob {
     float eps = 0.0f;
     const DecodeState* st = nullptr;  // XF_MERGE: checked present (the merge reads every chunk)
     int head_dim = 0, n_heads = 0;    // XF_MERGE
-    // Deferred K-split (plan->kg == 2, not routed): slice 0 writes its sum
-    // (+ bias) to y and slice 1 its sum to y2, with no handoff between the
-    // slices; the consumer adds y2 (x_add, bias2 below).
+    // Deferred K-split (plan->kg >= 2, not routed): slice 0 writes its sum
+    // (+ bias) to y and slice k >= 1 its sum to y2 + (k-1)*rows, with no
+    // handoff between the slices; the readers add them (x_add, bias2 below).
     float* y2 = nullptr;
-    // XF_NORM: x + x_add is the vector normalised (the deferred slice)
+    // XF_NORM: x + x_add[0] + ... + x_add[n_xa-1] (vectors of cols floats,
+    // added in that order) is the vector normalised; n_xa <= 2
     const float* x_add = nullptr;
-    // with bias: y = sum + (bias + bias2)
+    int n_xa = 1;
+    // with bias: y = sum + (bias + bias2[0] + ... + bias2[n_b2-1]) (vectors
+    // of rows floats); n_b2 <= 2
     const float* bias2 = nullptr;
+    int n_b2 = 1;
     // routed: the rows of experts sel[0..top_k) side by side as one K of
     // top_k * cols (one K-slice: plan->kg = 1), x of slot k at x + k*cols
     // (g) and x2 + k*cols (u), scaled by rw[k]; y = bias + the row sum
