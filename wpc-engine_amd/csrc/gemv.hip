@@ -929,6 +929,17 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     if (threadIdx.x < 4) xs[nbl + threadIdx.x] = make_float2(0.0f, 0.0f);  // == prep's value if written
     __syncthreads();
 
+    // XF_NORM: RMSNorm's scale of the row x, 1 / sqrt(mean(x^2) + eps), taken
+    // here so that its dependent divisions and square root overlap the
+    // matrix-core phase rather than follow the final sum (the empty asm keeps
+    // the compiler from sinking it there)
+    float rscale = 1.0f;
+    if constexpr (xform == XF_NORM) {
+        const float s2 = ((ssq[0] + ssq[1]) + (ssq[2] + ssq[3])) + ((ssq[4] + ssq[5]) + (ssq[6] + ssq[7]));
+        rscale = __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(s2, (float)(nb * 128)), P.eps)));
+        asm volatile("" ::"v"(rscale));
+    }
+
     // ---- matrix-core phase
     float acc = 0.f, zacc = 0.f;
     {
@@ -994,10 +1005,7 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     if (mine) {  // the tile's parts in order
         sum = red[tt * kw][rr];
         for (int k = 1; k < kw; k++) sum += red[tt * kw + k][rr];
-        if constexpr (xform == XF_NORM) {  // RMSNorm's scale of the row x
-            const float s2 = ((ssq[0] + ssq[1]) + (ssq[2] + ssq[3])) + ((ssq[4] + ssq[5]) + (ssq[6] + ssq[7]));
-            sum *= __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(s2, (float)(nb * 128)), P.eps)));
-        }
+        if constexpr (xform == XF_NORM) sum *= rscale;
     }
     if (kg == 1 || P.y2) {  // one slice, or the deferred split: slices k >= 1 to y2
         if (mine && orow < (size_t)P.rows) {
