@@ -48,6 +48,15 @@ QWEN3_4B_2L = dict(n_layers=2, hidden=2560, n_heads=32, n_kv_heads=8, head_dim=1
 ODD_OPROJ = dict(n_layers=2, hidden=256, n_heads=6, n_kv_heads=2, head_dim=64, inter=384, vocab=1000,
                  n_experts=0, top_k=0, moe_inter=0, norm_topk=1, tied=1, max_pos=96, eps=1e-6,
                  rope_theta=1e6)
+# Long contexts: past 16 x 32 = 512 positions each FAST attention chunk holds
+# a second block of 32 positions, past 1024 a third. LONG: head_dim 64 with
+# 2 query heads per key head (the 512-thread attention); LONG_REP8: head_dim
+# 128 with 8 query heads per key head (the 256-thread attention, as in the
+# Qwen3-30B-A3B shape).
+LONG = dict(DENSE, max_pos=1100)
+LONG_REP8 = dict(n_layers=1, hidden=512, n_heads=16, n_kv_heads=2, head_dim=128, inter=512, vocab=1000,
+                 n_experts=0, top_k=0, moe_inter=0, norm_topk=1, tied=1, max_pos=1100, eps=1e-6,
+                 rope_theta=1e6)
 
 
 @pytest.fixture(scope="module")
@@ -128,27 +137,41 @@ def test_exact_decode_is_bit_identical(ctx, name, cfg, n_prompt, n_new, seed):
 @pytest.mark.parametrize("name,cfg,n_steps,seed", [("dense", DENSE, 90, 111), ("moe", MOE, 90, 212),
                                                     ("qwen3-moe-2L", QWEN3_MOE_2L, 78, 313),
                                                     ("qwen3-4b-2L", QWEN3_4B_2L, 90, 414),
-                                                    ("odd-oproj", ODD_OPROJ, 90, 515)])
+                                                    ("odd-oproj", ODD_OPROJ, 90, 515),
+                                                    ("long", LONG, 1060, 616),
+                                                    ("long-rep8", LONG_REP8, 1060, 717)])
 def test_fast_decode_tracks_the_reference(ctx, name, cfg, n_steps, seed):
     """FAST mode step by step on the oracle's greedy tokens: every step's
     logits within FAST_TOL of the logit range of the oracle's, and the same
-    argmax. The steps run past many chunk boundaries of the FAST attention
-    (16 chunks of ceil((pos+1)/16) positions), so the chunk merge and the
-    key/value appends of every chunk are exercised."""
+    argmax. The FAST attention splits the positions into blocks of 32, chunk
+    c holding blocks c, c + 16, ...; the steps cross many block boundaries
+    (and, in the long cases, the second and third rounds of blocks), so the
+    chunk merge, empty chunks and the key/value appends of every chunk are
+    exercised."""
     print(f"[gpu] fast decode {name}: building", flush=True)
     m, ref = build(ctx, cfg, seed)
     m.set_mode(wpcg.MODE_FAST)
     tok = int(np.random.default_rng(5).integers(0, cfg["vocab"]))
     worst = 0.0
+    ties = 0
     for step in range(n_steps):
         r = ref.forward_token(tok)
         g, a = m.forward_token(tok)
-        err = float(np.max(np.abs(g - r))) / float(r.max() - r.min())
+        span = float(r.max() - r.min())
+        err = float(np.max(np.abs(g - r))) / span
         worst = max(worst, err)
         assert err <= FAST_TOL, f"{name}: step {step} logits off by {err:.2e} of the range"
         tok = O.argmax(r)
-        assert a == tok, f"{name}: step {step} argmax {a} vs the oracle's {tok}"
-    print(f"[gpu] fast decode {name}: {n_steps} steps, worst logit error {worst:.2e} of the range", flush=True)
+        if a != tok:
+            # only a near-tie may differ: the oracle's top two logits closer
+            # than the two-sided tolerance band (the next step still takes
+            # the oracle's token)
+            top2 = np.sort(r)[-2:]
+            assert float(top2[1] - top2[0]) <= 2 * FAST_TOL * span, \
+                f"{name}: step {step} argmax {a} vs the oracle's {tok}"
+            ties += 1
+    print(f"[gpu] fast decode {name}: {n_steps} steps, worst logit error {worst:.2e} of the range, "
+          f"{ties} near-tie argmax differences", flush=True)
     m.close()
     ref.close()
 

@@ -61,6 +61,9 @@ struct wpcg_model {
     // FAST attention's chunk states, merged by the o_proj GEMV (null: the
     // head shape needs the one-workgroup-per-head kernel)
     float *part_o = nullptr, *part_ml = nullptr;
+    // the step's RoPE row (cos, sin at the position), which the step's
+    // embedding launch copies for the FAST attention launches
+    float* rope = nullptr;
     // o_proj's second K-slice when its two slices are left to the readers
     // of the residual (the router, gate/up and down add it as they read)
     float* o2 = nullptr;
@@ -201,7 +204,11 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
     const int mode = m->mode;
     const bool fast = mode == WPCG_MODE_FAST;
     const float scale = 1.0f / std::sqrt((float)hd);  // model.rs: 1/sqrt(head_dim) in f32
-    WPCG_HIP(launch_embed_tok(m->embed->m, m->tokens, m->st, m->residual, s));
+    if (fast && m->part_o)
+        WPCG_HIP(launch_embed_tok(m->embed->m, m->tokens, m->st, m->residual, s, m->cos_t, m->sin_t, hd / 2,
+                                  m->rope));
+    else
+        WPCG_HIP(launch_embed_tok(m->embed->m, m->tokens, m->st, m->residual, s));
     const bool defer_d = defer_down(m);
     const float* d2 = nullptr;  // the previous down's deferred slices, if any
     int n_d2 = 1;
@@ -231,7 +238,7 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
         if (fast && m->part_o) {
             // chunked attention; o_proj merges the chunks, residual += o_proj(attn)
             WPCG_HIP(launch_attention_chunks(m->q, m->k, m->v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale,
-                                             m->cos_t, m->sin_t, m->st, kc, vc, m->part_o, m->part_ml, s));
+                                             m->rope, (int)c.max_pos, m->st, kc, vc, m->part_o, m->part_ml, s));
             GemvJob o{&L.o->m, &L.o->plan, m->part_o, m->residual, m->residual};
             o.xform = XF_MERGE;
             o.x2 = m->part_ml;
@@ -607,6 +614,7 @@ int wpcg_model_create(wpcg_ctx* ctx, int scheme, const wpcg_model_config* cfg, w
     if (attention_fast_ok((int)c.n_heads, (int)c.n_kv_heads, (int)hd)) {
         dev((void**)&m->part_o, (size_t)ATTN_CHUNKS * qd * 4);
         dev((void**)&m->part_ml, (size_t)ATTN_CHUNKS * c.n_heads * 2 * 4);
+        dev((void**)&m->rope, (size_t)hd * 4);
         dev((void**)&m->o2, (size_t)c.hidden * 4);
         dev((void**)&m->d2, (size_t)2 * c.hidden * 4);
     }

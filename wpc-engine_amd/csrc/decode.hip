@@ -26,6 +26,14 @@ namespace {
 // OCML's rounded-operation mode, is the bare estimate (up to 1 ulp off).
 __device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
 
+// A buffer resource over [base, base + bytes): loads past the end return
+// zeros without touching memory.
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
 // ---- rms_norm (wpc-runtime/src/norm.rs:4-13) -------------------------------
 // mean_sq = (sum x_i^2) / n; scale = 1 / sqrt(mean_sq + eps);
 // out_i = x_i * scale * w_i. One workgroup of NW threads.
@@ -407,20 +415,28 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
 
 // ---- FAST attention step: positions split into chunks across workgroups ----
 // Workgroup (j, c) takes kv head j's query heads (n_rep = nh/nkv of them)
-// over chunk c of the n = pos + 1 positions: FA_NCH chunks of
-// ceil(n / FA_NCH) positions each, so the launch has a fixed shape (a HIP
-// graph replays it at every position). The chunk's keys and values pass
-// through LDS in blocks of FA_C positions, shared by all n_rep heads (the
-// next block's loads are in flight while the current one is used), with a
-// running (online) softmax: max m, sum l of exp(s - m), o = sum exp(s_t - m)
-// v_t. Each workgroup applies q_norm + RoPE to its heads itself; the chunk
-// that holds `pos` computes the current key (k_norm + RoPE) and value and
-// appends them to the caches. Each chunk leaves its state for the o_proj
-// GEMV, which merges the chunks as it reads its input (attention_merge,
-// XF_MERGE): o at part_o[c][h][d], (m, l) at part_ml[c][h][0..1], h the
-// query head. Sums are fixed-order trees and fused multiply-adds:
-// deterministic, not the reference's operation order. head_dim HD is 64
-// or 128, n_rep <= FA_MAXREP.
+// over chunk c of the n = pos + 1 positions: positions are dealt round
+// robin, chunk c holding positions c, c + FA_NCH, c + 2 FA_NCH, ..., taken
+// FA_C at a time as blocks (block b: positions c + FA_NCH (FA_C b + t),
+// t < FA_C). The launch has a fixed shape (a HIP graph replays it at every
+// position), no chunk holds more than ceil(n / FA_NCH) positions (the
+// launch takes as long as its fullest chunk), and a chunk's first block
+// does not depend on the position: its keys and values can be requested at
+// entry, with the query rows, before the position is known (each row is
+// one contiguous head_dim vector; see the FD_WG note below). The chunk's
+// keys and values pass through LDS one block at a time,
+// shared by all n_rep heads (the next block's loads are in flight while
+// the current one is used), with a running (online) softmax: max m,
+// sum l of exp(s - m), o = sum exp(s_t - m) v_t. Each workgroup applies
+// q_norm + RoPE to its heads itself, with the step's RoPE row (cos, sin at
+// the position, copied to a fixed buffer by the step's embedding launch);
+// the chunk that holds `pos` computes the current key (k_norm + RoPE) and
+// value and appends them to the caches. Each chunk leaves its state for
+// the o_proj GEMV, which merges the chunks as it reads its input
+// (attention_merge, XF_MERGE): o at part_o[c][h][d], (m, l) at
+// part_ml[c][h][0..1], h the query head. Sums are fixed-order trees and
+// fused multiply-adds: deterministic, not the reference's operation order.
+// head_dim HD is 64 or 128, n_rep <= FA_MAXREP.
 constexpr int FA_WG = 256;  // the batched prefill's attention
 constexpr int FA_C = 32;
 constexpr int FA_NCH = ATTN_CHUNKS;
@@ -454,6 +470,12 @@ __device__ __forceinline__ void fa_norm_rope(const float* x, const float* w, flo
 // FD_WG threads: 256, or 512 for at most 4 query heads per key head (two
 // waves per SIMD instead of one; dense Qwen3-4B decode 694 -> 722 tok/s,
 // while 8 heads per key head, Qwen3-30B-A3B, ran 1.5% slower at 512).
+// The 256-thread launch requests its first block of keys and values before
+// the position is known, every row of it (Qwen3-30B-A3B shape: 6.69 ->
+// 6.34 us per launch); the 512-thread launch, with twice the key heads per
+// query head and so twice the bytes per speculated row, requests only the
+// rows before the position, once it is known (speculating took the dense
+// Qwen3-4B-shaped launch from 5.21 to 5.42 us).
 template <int HD, int FD_WG>
 __global__ __launch_bounds__(FD_WG) void k_attention_fast(const float* __restrict__ qp,
                                                           const float* __restrict__ kp,
@@ -461,8 +483,7 @@ __global__ __launch_bounds__(FD_WG) void k_attention_fast(const float* __restric
                                                           const float* __restrict__ qn,
                                                           const float* __restrict__ kn, int nh, int nkv,
                                                           float eps, float scale,
-                                                          const float* __restrict__ cos_t,
-                                                          const float* __restrict__ sin_t,
+                                                          const float* __restrict__ rope, int cache_pos,
                                                           const DecodeState* __restrict__ st,
                                                           float* __restrict__ kc, float* __restrict__ vc,
                                                           float* __restrict__ part_o, float* __restrict__ part_ml)
@@ -478,17 +499,97 @@ __global__ __launch_bounds__(FD_WG) void k_attention_fast(const float* __restric
     __shared__ float ps[FA_MAXREP][FA_C];                     // scores, head-major
     __shared__ __align__(16) float pt[FA_C][FA_MAXREP + 4];   // exp weights, position-major
     __shared__ float s_m[FA_MAXREP], s_l[FA_MAXREP], s_corr[FA_MAXREP];
+    // every argument the loads below need, in one round trip (each read
+    // where it is first used was a further dependent round trip)
+    asm volatile("" ::"s"(qp), "s"(kp), "s"(vp), "s"(qn), "s"(kn), "s"(nh), "s"(nkv), "s"(rope), "s"(cache_pos),
+                 "s"(st), "s"(kc), "s"(vc));
     const int j = blockIdx.x / FA_NCH, c = blockIdx.x % FA_NCH;
-    const uint32_t pos = st->pos, max_pos = st->max_pos;
-    const int n = (int)pos + 1, n_rep = nh / nkv;
-    const int len = (n + FA_NCH - 1) / FA_NCH;
-    const int tb = c * len;
-    if (tb >= n || pos >= max_pos) {
+    const int n_rep = nh / nkv;
+    // row t of this chunk's block b is position base(b) + FA_NCH t
+    auto base = [&](int b) { return c + b * FA_C * FA_NCH; };
+    auto row_pos = [&](int b, int t) { return base(b) + t * FA_NCH; };
+    float* kb = kc + (size_t)j * cache_pos * HD;
+    float* vb = vc + (size_t)j * cache_pos * HD;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+
+    // The state (pos, n_prompt, max_pos, last), loaded first and through the
+    // constant address space (nothing in the launch writes it), which lets
+    // the compiler issue the loads below before using it: the test on the
+    // position then waits for this load alone (vector loads return in
+    // order). Read as an ordinary load, the compiler waited for it before
+    // issuing any other.
+    typedef const __attribute__((address_space(4))) u32x4* StatePtr;
+    const u32x4 sv = *(StatePtr)st;
+    // q heads (and the current key and value, in the chunk that holds pos):
+    // wave w takes rows r = w, w + 4, ... (row n_rep is the key). Every load
+    // of the wave's rows, the norm weights and the step's RoPE row is issued
+    // before any is used (one memory round trip, in parallel with the
+    // position's), then each row is RMS-normalised and rotated as
+    // fa_norm_rope does it. These go out before the cached keys and values,
+    // which vector loads return in order after them.
+    constexpr int half = HD / 2, NWV = FD_WG / 64;
+    constexpr int RW = (FA_MAXREP + NWV) / NWV;  // rows per wave at most
+    const bool on = lane < half;
+    const int li = on ? lane : 0;  // every address in bounds; off lanes' values are discarded
+    float x1[RW], x2[RW];
+#pragma unroll
+    for (int i = 0; i < RW; i++) {
+        const int r = wave + i * NWV;
+        const float* src = r < n_rep ? qp + (size_t)(j * n_rep + r) * HD : kp + (size_t)j * HD;
+        x1[i] = src[li];
+        x2[i] = src[li + half];
+    }
+    const float c1 = rope[li], s1 = rope[half + li];
+    const float qw1 = qn[li], qw2 = qn[li + half], kw1 = kn[li], kw2 = kn[li + half];
+    float vv[HD / 64];
+#pragma unroll
+    for (int u = 0; u < HD / 64; u++) vv[u] = vp[(size_t)j * HD + lane + 64 * u];
+
+    // A block's cached keys and values, rows t < lim: thread i, 16 bytes of
+    // row i / HD4, through buffer loads over this head's cache, so that every
+    // load may be unconditional: a row at or past lim gets an offset past
+    // the range and reads zeros without a memory access, as does a row past
+    // the cache; a speculated row past the step's position is read and never
+    // used (the scores and the output take rows t < nt only); the current
+    // position's row comes from kcur / vcur.
+    constexpr bool SPEC = FD_WG == 256;
+    const auto krs = buf_rsrc(kb, cache_pos * HD * 4), vrs = buf_rsrc(vb, cache_pos * HD * 4);
+    u32x4 kr[NKV], vr[NKV];
+    auto load_block = [&](int b, int lim) {
+#pragma unroll
+        for (int u = 0; u < NKV; u++) {
+            const int i = threadIdx.x + u * FD_WG, t = i / HD4;
+            const int off = t < lim ? (row_pos(b, t) * HD + 4 * (i % HD4)) * 4 : 0x40000000;
+            kr[u] = __builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0);
+            vr[u] = __builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0);
+        }
+    };
+    if constexpr (SPEC) load_block(0, FA_C);
+
+    const uint32_t pos = sv.x, max_pos = sv.z;
+    const int n = (int)pos + 1;
+    if ((c >= n) | (pos >= max_pos) | (pos >= (uint32_t)cache_pos)) {
         // An empty chunk leaves the neutral state (m = -inf, l = 0, o = 0),
         // so the merge in o_proj takes every chunk without knowing the
         // position: an empty chunk's weight exp(-inf - M) is 0. (Past the
         // cache, pos >= max_pos, every chunk is empty and chunk 0 leaves
         // m = 0, l = 1: the merged output is 0 rather than 0/0.)
+        // The loads above are consumed here too (their bits into an empty
+        // asm operand): with uses on both sides of this branch they stay
+        // ahead of it; used on one side only, the compiler moved them into
+        // the non-empty path, behind the position's round trip.
+        uint32_t used = 0;
+        if constexpr (SPEC) {
+#pragma unroll
+            for (int u = 0; u < NKV; u++) used |= kr[u].x | vr[u].x;
+        }
+#pragma unroll
+        for (int i = 0; i < RW; i++) used |= __float_as_uint(x1[i]) | __float_as_uint(x2[i]);
+#pragma unroll
+        for (int u = 0; u < HD / 64; u++) used |= __float_as_uint(vv[u]);
+        used |= __float_as_uint(c1) | __float_as_uint(s1) | __float_as_uint(qw1) | __float_as_uint(qw2) |
+                __float_as_uint(kw1) | __float_as_uint(kw2);
+        asm volatile("" ::"v"(used));
         const bool unit = c == 0;
         for (int i = threadIdx.x; i < n_rep * HD; i += FD_WG)
             part_o[((size_t)c * nh + j * n_rep) * HD + i] = 0.0f;
@@ -497,52 +598,12 @@ __global__ __launch_bounds__(FD_WG) void k_attention_fast(const float* __restric
                 (threadIdx.x & 1) ? (unit ? 1.0f : 0.0f) : (unit ? 0.0f : -INFINITY);
         return;
     }
-    const int te = min(tb + len, n);
-    const float* cs = cos_t + (size_t)pos * (HD / 2);
-    const float* sn = sin_t + (size_t)pos * (HD / 2);
-    float* kb = kc + (size_t)j * max_pos * HD;
-    float* vb = vc + (size_t)j * max_pos * HD;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-
-    // the block's cached keys and values: thread i, 16 bytes of row i / HD4
-    // (the current position's row comes from kcur / vcur)
-    float4 kr[NKV], vr[NKV];
-    auto load_block = [&](int t0) {
-#pragma unroll
-        for (int u = 0; u < NKV; u++) {
-            const int i = threadIdx.x + u * FD_WG, t = t0 + i / HD4, d = 4 * (i % HD4);
-            if (t < te && t != (int)pos) {
-                kr[u] = *reinterpret_cast<const float4*>(kb + (size_t)t * HD + d);
-                vr[u] = *reinterpret_cast<const float4*>(vb + (size_t)t * HD + d);
-            }
-        }
-    };
-    load_block(tb);
-    // q heads (and the current key and value, in the chunk that holds pos):
-    // wave w takes rows r = w, w + 4, ... (row n_rep is the key). Every load
-    // of the wave's rows, the norm weights and this position's RoPE table is
-    // issued before any is used (one memory round trip), then each row is
-    // RMS-normalised and rotated as fa_norm_rope does it.
-    const bool has_pos = te == n;
+    // the rows of block b before n (a prefix: positions grow with t)
+    auto rows = [&](int b) { return min(FA_C, (n - base(b) + FA_NCH - 1) / FA_NCH); };
+    if constexpr (!SPEC) load_block(0, rows(0));
+    const bool has_pos = (int)(pos % FA_NCH) == c;
     {
-        constexpr int half = HD / 2, NWV = FD_WG / 64;
-        constexpr int RW = (FA_MAXREP + NWV) / NWV;  // rows per wave at most
         const int nrows = n_rep + (has_pos ? 1 : 0);
-        const bool on = lane < half;
-        const int li = on ? lane : 0;  // every address in bounds; off lanes' values are discarded
-        float x1[RW], x2[RW];
-#pragma unroll
-        for (int i = 0; i < RW; i++) {
-            const int r = wave + i * NWV;
-            const float* src = r < n_rep ? qp + (size_t)(j * n_rep + r) * HD : kp + (size_t)j * HD;
-            x1[i] = src[li];
-            x2[i] = src[li + half];
-        }
-        const float c1 = cs[li], s1 = sn[li];
-        const float qw1 = qn[li], qw2 = qn[li + half], kw1 = kn[li], kw2 = kn[li + half];
-        float vv[HD / 64];
-#pragma unroll
-        for (int u = 0; u < HD / 64; u++) vv[u] = vp[(size_t)j * HD + lane + 64 * u];
 #pragma unroll
         for (int i = 0; i < RW; i++) {
             const int r = wave + i * NWV;
@@ -585,21 +646,21 @@ __global__ __launch_bounds__(FD_WG) void k_attention_fast(const float* __restric
     for (int u = 0; u < NOUT; u++) o[u] = 0.0f;
     __syncthreads();  // qs, kcur, vcur, s_m, s_l written
 
-    for (int t0 = tb; t0 < te; t0 += FA_C) {
-        const int nt = min(FA_C, te - t0);
+    for (int b = 0; base(b) < n; b++) {
+        const int nt = rows(b);
 #pragma unroll
         for (int u = 0; u < NKV; u++) {
             const int i = threadIdx.x + u * FD_WG, t = i / HD4, d = 4 * (i % HD4);
             if (t < nt) {
-                const bool cur = t0 + t == (int)pos;
-                const float4 kv = cur ? *reinterpret_cast<const float4*>(kcur + d) : kr[u];
-                const float4 vv = cur ? *reinterpret_cast<const float4*>(vcur + d) : vr[u];
-                *reinterpret_cast<float4*>(&ks[t][d]) = kv;
-                *reinterpret_cast<float4*>(&vs[t][d]) = vv;
+                const bool cur = row_pos(b, t) == (int)pos;
+                const u32x4 k4 = cur ? *reinterpret_cast<const u32x4*>(kcur + d) : kr[u];
+                const u32x4 v4 = cur ? *reinterpret_cast<const u32x4*>(vcur + d) : vr[u];
+                *reinterpret_cast<u32x4*>(&ks[t][d]) = k4;
+                *reinterpret_cast<u32x4*>(&vs[t][d]) = v4;
             }
         }
         __syncthreads();
-        if (t0 + FA_C < te) load_block(t0 + FA_C);  // in flight during this block
+        if (base(b + 1) < n) load_block(b + 1, rows(b + 1));  // in flight during this block
         // scores s[r][t] = (q_r . k_t) * scale
         for (int i = threadIdx.x; i < n_rep * FA_C; i += FD_WG) {
             const int r = i / FA_C, t = i % FA_C;
@@ -983,14 +1044,15 @@ hipError_t launch_attention(int mode, const float* q, const float* k, const floa
 
 hipError_t launch_attention_chunks(const float* q, const float* k, const float* v, const float* qn,
                                    const float* kn, int nh, int nkv, int hd, float eps, float scale,
-                                   const float* cos_t, const float* sin_t, const DecodeState* st, float* kc,
+                                   const float* rope, int cache_pos, const DecodeState* st, float* kc,
                                    float* vc, float* part_o, float* part_ml, hipStream_t s)
 {
-    if (!attention_fast_ok(nh, nkv, hd)) return hipErrorInvalidValue;
+    if (!attention_fast_ok(nh, nkv, hd) || !rope || cache_pos < 1 || (size_t)cache_pos * hd * 4 > 0x7fffffffu)
+        return hipErrorInvalidValue;
     (void)hipGetLastError();
 #define WPCG_ATT(HD, WG)                                                                                  \
     hipLaunchKernelGGL((k_attention_fast<HD, WG>), dim3(nkv * FA_NCH), dim3(WG), 0, s, q, k, v, qn, kn, nh, nkv, \
-                       eps, scale, cos_t, sin_t, st, kc, vc, part_o, part_ml)
+                       eps, scale, rope, cache_pos, st, kc, vc, part_o, part_ml)
     const bool wide = nh / nkv <= 4;
     if (hd == 128) {
         if (wide) WPCG_ATT(128, 512);

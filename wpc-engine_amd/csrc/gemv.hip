@@ -1098,8 +1098,16 @@ __global__ __launch_bounds__(256) void k_embed_tok(const uint8_t* __restrict__ c
                                                    float* __restrict__ out,
                                                    const uint32_t* __restrict__ tokens,
                                                    const DecodeState* __restrict__ st, int nb,
-                                                   uint32_t rows)
+                                                   uint32_t rows, const float* __restrict__ cos_t,
+                                                   const float* __restrict__ sin_t, int half,
+                                                   float* __restrict__ rope)
 {
+    // The step's RoPE row, cos then sin at the position, for the FAST
+    // attention launches of the step (a fixed address they read at entry).
+    if (rope && blockIdx.x == 0 && (int)threadIdx.x < 2 * half) {
+        const uint32_t p = st->pos, i = threadIdx.x;
+        if (p < st->max_pos) rope[i] = (int)i < half ? cos_t[(size_t)p * half + i] : sin_t[(size_t)p * half + i - half];
+    }
     const int k = blockIdx.x * 256 + threadIdx.x;
     if (k >= nb * 128) return;
     const uint32_t row = min(tokens[st->pos], rows - 1);  // ids are checked on the host
@@ -1337,16 +1345,18 @@ hipError_t launch_embed(const DeviceMatrix& m, uint32_t row, float* out, hipStre
 }
 
 hipError_t launch_embed_tok(const DeviceMatrix& m, const uint32_t* tokens, const DecodeState* st,
-                            float* out, hipStream_t s)
+                            float* out, hipStream_t s, const float* cos_t, const float* sin_t, int half,
+                            float* rope)
 {
+    if (rope && (!cos_t || !sin_t || half < 1 || 2 * half > 256)) return hipErrorInvalidValue;
     dim3 grid((unsigned)((m.cols + 255) / 256));
     (void)hipGetLastError();  // report only this launch
     if (m.scheme == 4)
         hipLaunchKernelGGL(k_embed_tok<4>, grid, dim3(256), 0, s, m.codes, m.hp, m.params, out, tokens,
-                           st, (int)m.nb, (uint32_t)m.rows);
+                           st, (int)m.nb, (uint32_t)m.rows, cos_t, sin_t, half, rope);
     else
         hipLaunchKernelGGL(k_embed_tok<3>, grid, dim3(256), 0, s, m.codes, m.hp, m.params, out, tokens,
-                           st, (int)m.nb, (uint32_t)m.rows);
+                           st, (int)m.nb, (uint32_t)m.rows, cos_t, sin_t, half, rope);
     return hipGetLastError();
 }
 

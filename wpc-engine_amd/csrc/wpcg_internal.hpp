@@ -293,8 +293,11 @@ int moe_run(wpcg_moe* m, const float* x, float* out, const float* add, hipStream
             const float* nw = nullptr, float eps = 0.0f, const float* x_add = nullptr);
 
 // ---- decode step (decode.hip) ----------------------------------------------
+// With rope set, workgroup 0 also copies the RoPE row at the position
+// (cos_t / sin_t rows of `half` floats) to rope: cos then sin.
 hipError_t launch_embed_tok(const DeviceMatrix& m, const uint32_t* tokens, const DecodeState* st,
-                            float* out, hipStream_t s);
+                            float* out, hipStream_t s, const float* cos_t = nullptr,
+                            const float* sin_t = nullptr, int half = 0, float* rope = nullptr);
 hipError_t launch_rms_norm(int mode, const float* x, const float* w, int n, float eps, float* out,
                            hipStream_t s);
 // q/k RMSNorm + RoPE, KV append, scores, softmax and output of one layer's
@@ -308,11 +311,13 @@ hipError_t launch_attention(int mode, const float* q, const float* k, const floa
 // softmax state goes to part_o [ATTN_CHUNKS][nh][hd] (unnormalised output)
 // and part_ml [ATTN_CHUNKS][nh][2] (max, sum of exps); the o_proj GEMV
 // merges them (XF_MERGE). Needs attention_fast_ok (head_dim 64 or 128).
+// rope: the step's RoPE row, cos then sin at the position (hd floats, as
+// launch_embed_tok leaves it); cache_pos: positions per head in kc / vc.
 constexpr int ATTN_CHUNKS = 16;
 bool attention_fast_ok(int nh, int nkv, int hd);
 hipError_t launch_attention_chunks(const float* q, const float* k, const float* v, const float* qn,
                                    const float* kn, int nh, int nkv, int hd, float eps, float scale,
-                                   const float* cos_t, const float* sin_t, const DecodeState* st, float* kc,
+                                   const float* rope, int cache_pos, const DecodeState* st, float* kc,
                                    float* vc, float* part_o, float* part_ml, hipStream_t s);
 hipError_t launch_add(float* x, const float* y, int n, hipStream_t s);
 // ---- batched prefill (decode.hip, gemv.hip, moe.hip, prefill.hip) ---------
