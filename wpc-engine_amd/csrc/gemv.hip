@@ -360,35 +360,34 @@ __device__ __forceinline__ float lane_of(float v, int l)
 }
 
 // Softmax of n <= PER*64 router scores and the top-k selection of route()
-// (qwen3_moe_model.rs:376-402) by a workgroup, into LDS: ids[k], w[k] for
-// k < top_k. Every thread of the workgroup calls it. Wave 0 computes the
-// probabilities (softmax_inplace's arithmetic, norm.rs:28-43, with the
-// libm-exact exp and a tree sum for the denominator: FAST mode, whose
-// router scores are FAST themselves) and a key per expert,
-// bits(p) << 32 | ~index (p >= 0: larger p first, then the lower index);
-// the rank of a key is how many keys beat it, which is the order of
-// route()'s repeated strict-`>` scans. The eight waves count the
-// comparisons for one eighth of the keys each. NaN is never chosen;
-// unfilled slots get id -1, weight 0; with norm_topk the chosen weights are
-// divided by their sum taken in chosen order when it is positive.
-// LDS: key (PER*64 keys), rk (PER*64 counts), tab (the exp table).
+// (qwen3_moe_model.rs:376-402) by the workgroup, into LDS: ids[k], w[k] for
+// k < top_k (id -1, weight 0 for a slot no selectable expert fills); every
+// thread calls it. Wave 0 computes the probabilities (softmax_inplace's
+// arithmetic, norm.rs:28-43, with the libm-exact exp and a tree sum for the
+// denominator: FAST mode, whose router scores are FAST themselves) and a key
+// per expert, bits(p) << 32 | ~index (p >= 0: larger p first, then the lower
+// index; NaN never chosen, key 0); the rank of a key is how many keys beat
+// it, which is the order of route()'s repeated strict-`>` scans. Each wave
+// ranks an eighth of the keys: a lane counts the keys of one part of the
+// array that beat its key (LDS reads every lane of a group shares), the
+// parts' counts are added across lanes, and a selectable key of rank
+// r < top_k writes slot r. The exp table entry comes from lane
+// (index & 31), whose registers tlo, thi hold the bits of 2^((lane & 31)/32).
+// Returns the number of selectable experts (wave 0; others 0).
+// LDS: key (PER*64 keys).
 __constant__ double k_exp_tab[32] = REF_EXPF_TABLE;
 
 template <int PER>
-__device__ __forceinline__ void route_wg(const float* __restrict__ scores, int n, int top_k, int norm_topk,
-                                         uint64_t* key, int* rk, int32_t* ids, float* w, double* tab,
-                                         int* s_selectable)
+__device__ __forceinline__ int route_wg(const float* __restrict__ scores, int n, int top_k, uint32_t tlo,
+                                        uint32_t thi, uint64_t* key_lds, int32_t* ids, float* w)
 {
-    constexpr int N = PER * 64;
+    constexpr int N = PER * 64, KPW = N / 8, G = 64 / KPW;  // keys per wave, lane groups
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float v[PER];
-    uint64_t mine[PER];
+    int selectable = 0;
     if (wave == 0) {
-        // the scores and the exp table are requested together (one round trip)
+        float v[PER];
 #pragma unroll
         for (int q = 0; q < PER; q++) v[q] = scores[min(lane + 64 * q, n - 1)];
-        const double t = k_exp_tab[lane & 31];
-        if (lane < 32) tab[lane] = t;
         float m = -INFINITY;
 #pragma unroll
         for (int q = 0; q < PER; q++) {
@@ -399,70 +398,53 @@ __device__ __forceinline__ void route_wg(const float* __restrict__ scores, int n
         float sum = 0.0f;
 #pragma unroll
         for (int q = 0; q < PER; q++) {
-            v[q] = lane + 64 * q < n ? ref_expf_tab(__fsub_rn(v[q], m), tab) : 0.0f;
+            // ref_expf_tab's steps, the entry from another lane (every lane
+            // takes part in the exchange, special inputs included)
+            const float x = __fsub_rn(v[q], m);
+            uint64_t ki;
+            const double r = ref_expf_reduce(x, &ki);
+            const int src = (int)(ki & 31) << 2;
+            const uint64_t t = ((uint64_t)(uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)thi) << 32) |
+                               (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)tlo);
+            float y;
+            const float e = ref_expf_special(x, &y) ? y : ref_expf_finish(r, ki, t);
+            v[q] = lane + 64 * q < n ? e : 0.0f;
             sum += v[q];
         }
         sum = wave_sum(sum);
-        int selectable = 0;
 #pragma unroll
         for (int q = 0; q < PER; q++) {
             const int i = lane + 64 * q;
             if (sum > 0.0f) v[q] = __fdiv_rn(v[q], sum);
             const bool ok = i < n && v[q] > -INFINITY;  // NaN fails
-            selectable += ok ? 1 : 0;
-            mine[q] = ok ? ((uint64_t)__float_as_uint(v[q]) << 32) | (0xFFFFFFFFu - (uint32_t)i) : 0ull;
-            key[i] = mine[q];
-            rk[i] = 0;
-        }
-        selectable = wave_sum_i(selectable);
-        if (lane == 0) *s_selectable = selectable;
-    }
-    __syncthreads();
-    // wave w counts, for every key, the keys [w*N/8, (w+1)*N/8) that beat it
-    {
-        uint64_t all[PER];
-#pragma unroll
-        for (int q = 0; q < PER; q++) all[q] = key[lane + 64 * q];
-        int part[PER];
-#pragma unroll
-        for (int q = 0; q < PER; q++) part[q] = 0;
-        const int t0 = wave * (N / 8);
-#pragma unroll
-        for (int u = 0; u < N / 8; u += 2) {
-            const ulonglong2 pr = *reinterpret_cast<const ulonglong2*>(key + t0 + u);
-#pragma unroll
-            for (int q = 0; q < PER; q++) part[q] += (pr.x > all[q] ? 1 : 0) + (pr.y > all[q] ? 1 : 0);
-        }
-#pragma unroll
-        for (int q = 0; q < PER; q++)
-            if (part[q]) atomicAdd(rk + lane + 64 * q, part[q]);
-    }
-    __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-        for (int q = 0; q < PER; q++) {
-            const int r = rk[lane + 64 * q];
-            if (mine[q] && r < top_k) {
-                ids[r] = lane + 64 * q;
-                w[r] = v[q];
-            }
-        }
-        // Lane k < top_k finishes slot k (this wave's own LDS writes above
-        // are in place for its reads): one read per lane, the chosen
-        // weights' sum in chosen order through lane reads, the divisions in
-        // parallel (one lane doing all of it serially through LDS took 1.2 us)
-        const int got = __builtin_amdgcn_readfirstlane(min(top_k, *s_selectable));
-        float wk = lane < got ? w[lane] : 0.0f;
-        if (norm_topk) {
-            float sw = 0.0f;
-            for (int k = 0; k < got; k++) sw = __fadd_rn(sw, lane_of(wk, k));
-            if (sw > 0.0f) wk = __fdiv_rn(wk, sw);
+            key_lds[i] = ok ? ((uint64_t)__float_as_uint(v[q]) << 32) | (0xFFFFFFFFu - (uint32_t)i) : 0ull;
+            selectable += __popcll(__ballot(ok));
         }
         if (lane < top_k) {
-            if (lane >= got) ids[lane] = -1;
-            w[lane] = lane < got ? wk : 0.0f;
+            ids[lane] = -1;
+            w[lane] = 0.0f;
         }
     }
+    __syncthreads();
+    {
+        const int i = wave * KPW + lane % KPW;
+        const uint64_t mine = key_lds[i];
+        const uint64_t* part = key_lds + (lane / KPW) * (N / G);
+        int cnt = 0;
+#pragma unroll
+        for (int u = 0; u < N / G; u += 2) {
+            const ulonglong2 pr = *reinterpret_cast<const ulonglong2*>(part + u);
+            cnt += (pr.x > mine ? 1 : 0) + (pr.y > mine ? 1 : 0);
+        }
+        if constexpr (G >= 4) cnt += __shfl_xor(cnt, 16);
+        if constexpr (G >= 2) cnt += __shfl_xor(cnt, 32);
+        if (lane < KPW && mine && cnt < top_k) {
+            ids[cnt] = i;
+            w[cnt] = __uint_as_float((uint32_t)(mine >> 32));
+        }
+    }
+    __syncthreads();
+    return selectable;
 }
 
 // A workgroup of 8 waves computes tw (1, 2 or 4) 16-row tiles over one K-slice
@@ -516,11 +498,17 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     __shared__ int32_t route_ids[MAX_JOBS];                     // FK_ROUTE: the routing
     __shared__ float route_w[MAX_JOBS];
     __shared__ int s_last;
-    // FK_ROUTE's keys and exp table live in xq, which routing finishes
-    // with before the barrier that precedes the x prep
+    // FK_ROUTE's keys live in xq, which routing finishes with before the
+    // barrier that ends it (the x prep writes xq after it)
     uint64_t* const route_key = reinterpret_cast<uint64_t*>(xq);
-    double* const route_tab = reinterpret_cast<double*>(xq + ROUTE_MAXN * 8);
-    int* const route_rk = reinterpret_cast<int*>(xq + ROUTE_MAXN * 8 + 32 * 8);
+    // FK_ROUTE: lane l's copy of the exp table entry 2^((l & 31)/32), as
+    // bits, requested first (its address needs no kernel argument)
+    uint32_t tlo = 0, thi = 0;
+    if constexpr (KIND == FK_ROUTE) {
+        const uint64_t tb = (uint64_t)__double_as_longlong(k_exp_tab[threadIdx.x & 31]);
+        tlo = (uint32_t)tb;
+        thi = (uint32_t)(tb >> 32);
+    }
 
     // Workgroup (x, y) is workgroup x of problem y: the problem index comes
     // from the grid, so the problem's fields are read in one round trip (a
@@ -675,17 +663,24 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
         }
     }
     if constexpr (KIND == FK_ROUTE) {  // this workgroup routes itself
-        if (P.n_exp <= 128)
-            route_wg<2>(P.scores, P.n_exp, P.top_k, P.norm_topk, route_key, route_rk, route_ids, route_w,
-                        route_tab, &s_last);
-        else
-            route_wg<4>(P.scores, P.n_exp, P.top_k, P.norm_topk, route_key, route_rk, route_ids, route_w,
-                        route_tab, &s_last);
-        __syncthreads();
+        const int selectable =
+            P.n_exp <= 128 ? route_wg<2>(P.scores, P.n_exp, P.top_k, tlo, thi, route_key, route_ids, route_w)
+                           : route_wg<4>(P.scores, P.n_exp, P.top_k, tlo, thi, route_key, route_ids, route_w);
         e = route_ids[P.sel_k];
-        if (local == 0 && blockIdx.y == 0 && (int)threadIdx.x < P.top_k) {
-            P.ids_out[threadIdx.x] = route_ids[threadIdx.x];
-            P.w_out[threadIdx.x] = route_w[threadIdx.x];
+        if (local == 0 && blockIdx.y == 0 && wave == 0) {
+            // the routing for the down projection: slot k on lane k, the
+            // weights divided by their sum in chosen order (norm_topk)
+            const int got = __builtin_amdgcn_readfirstlane(min(P.top_k, selectable));
+            float wk = lane < got ? route_w[lane] : 0.0f;
+            if (P.norm_topk) {
+                float sw = 0.0f;
+                for (int k = 0; k < got; k++) sw = __fadd_rn(sw, lane_of(wk, k));
+                if (sw > 0.0f) wk = __fdiv_rn(wk, sw);
+            }
+            if (lane < P.top_k) {
+                P.ids_out[lane] = lane < got ? route_ids[lane] : -1;
+                P.w_out[lane] = wk;
+            }
         }
     } else if constexpr (KIND == FK_PLAIN) {
         if (P.sel) e = P.sel[P.sel_k];
