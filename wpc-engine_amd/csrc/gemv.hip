@@ -29,8 +29,6 @@
 
 #include <type_traits>
 
-#define REF_EXPF_FN __device__ __forceinline__
-#include "ref_expf.h"
 #include "wpcg_internal.hpp"
 #include "wave.h"
 
@@ -363,23 +361,20 @@ __device__ __forceinline__ float lane_of(float v, int l)
 // (qwen3_moe_model.rs:376-402) by the workgroup, into LDS: ids[k], w[k] for
 // k < top_k (id -1, weight 0 for a slot no selectable expert fills); every
 // thread calls it. Wave 0 computes the probabilities (softmax_inplace's
-// arithmetic, norm.rs:28-43, with the libm-exact exp and a tree sum for the
-// denominator: FAST mode, whose router scores are FAST themselves) and a key
+// steps, norm.rs:28-43, in FAST arithmetic like the router scores
+// themselves: the hardware exp of x log2(e) and one reciprocal of the tree
+// sum; EXACT's k_softmax_route keeps the reference's arithmetic) and a key
 // per expert, bits(p) << 32 | ~index (p >= 0: larger p first, then the lower
 // index; NaN never chosen, key 0); the rank of a key is how many keys beat
 // it, which is the order of route()'s repeated strict-`>` scans. Each wave
 // ranks an eighth of the keys: a lane counts the keys of one part of the
 // array that beat its key (LDS reads every lane of a group shares), the
 // parts' counts are added across lanes, and a selectable key of rank
-// r < top_k writes slot r. The exp table entry comes from lane
-// (index & 31), whose registers tlo, thi hold the bits of 2^((lane & 31)/32).
-// Returns the number of selectable experts (wave 0; others 0).
-// LDS: key (PER*64 keys).
-__constant__ double k_exp_tab[32] = REF_EXPF_TABLE;
-
+// r < top_k writes slot r. Returns the number of selectable experts
+// (wave 0; others 0). LDS: key (PER*64 keys).
 template <int PER>
-__device__ __forceinline__ int route_wg(const float* __restrict__ scores, int n, int top_k, uint32_t tlo,
-                                        uint32_t thi, uint64_t* key_lds, int32_t* ids, float* w)
+__device__ __forceinline__ int route_wg(const float* __restrict__ scores, int n, int top_k, uint64_t* key_lds,
+                                        int32_t* ids, float* w)
 {
     constexpr int N = PER * 64, KPW = N / 8, G = 64 / KPW;  // keys per wave, lane groups
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -398,24 +393,15 @@ __device__ __forceinline__ int route_wg(const float* __restrict__ scores, int n,
         float sum = 0.0f;
 #pragma unroll
         for (int q = 0; q < PER; q++) {
-            // ref_expf_tab's steps, the entry from another lane (every lane
-            // takes part in the exchange, special inputs included)
-            const float x = __fsub_rn(v[q], m);
-            uint64_t ki;
-            const double r = ref_expf_reduce(x, &ki);
-            const int src = (int)(ki & 31) << 2;
-            const uint64_t t = ((uint64_t)(uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)thi) << 32) |
-                               (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)tlo);
-            float y;
-            const float e = ref_expf_special(x, &y) ? y : ref_expf_finish(r, ki, t);
-            v[q] = lane + 64 * q < n ? e : 0.0f;
+            v[q] = lane + 64 * q < n ? __expf(__fsub_rn(v[q], m)) : 0.0f;
             sum += v[q];
         }
         sum = wave_sum(sum);
+        const float rs = sum > 0.0f ? __builtin_amdgcn_rcpf(sum) : 1.0f;
 #pragma unroll
         for (int q = 0; q < PER; q++) {
             const int i = lane + 64 * q;
-            if (sum > 0.0f) v[q] = __fdiv_rn(v[q], sum);
+            v[q] *= rs;
             const bool ok = i < n && v[q] > -INFINITY;  // NaN fails
             key_lds[i] = ok ? ((uint64_t)__float_as_uint(v[q]) << 32) | (0xFFFFFFFFu - (uint32_t)i) : 0ull;
             selectable += __popcll(__ballot(ok));
@@ -501,14 +487,6 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     // FK_ROUTE's keys live in xq, which routing finishes with before the
     // barrier that ends it (the x prep writes xq after it)
     uint64_t* const route_key = reinterpret_cast<uint64_t*>(xq);
-    // FK_ROUTE: lane l's copy of the exp table entry 2^((l & 31)/32), as
-    // bits, requested first (its address needs no kernel argument)
-    uint32_t tlo = 0, thi = 0;
-    if constexpr (KIND == FK_ROUTE) {
-        const uint64_t tb = (uint64_t)__double_as_longlong(k_exp_tab[threadIdx.x & 31]);
-        tlo = (uint32_t)tb;
-        thi = (uint32_t)(tb >> 32);
-    }
 
     // Workgroup (x, y) is workgroup x of problem y: the problem index comes
     // from the grid, so the problem's fields are read in one round trip (a
@@ -664,8 +642,8 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     }
     if constexpr (KIND == FK_ROUTE) {  // this workgroup routes itself
         const int selectable =
-            P.n_exp <= 128 ? route_wg<2>(P.scores, P.n_exp, P.top_k, tlo, thi, route_key, route_ids, route_w)
-                           : route_wg<4>(P.scores, P.n_exp, P.top_k, tlo, thi, route_key, route_ids, route_w);
+            P.n_exp <= 128 ? route_wg<2>(P.scores, P.n_exp, P.top_k, route_key, route_ids, route_w)
+                           : route_wg<4>(P.scores, P.n_exp, P.top_k, route_key, route_ids, route_w);
         e = route_ids[P.sel_k];
         if (local == 0 && blockIdx.y == 0 && wave == 0) {
             // the routing for the down projection: slot k on lane k, the

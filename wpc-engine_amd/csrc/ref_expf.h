@@ -31,61 +31,37 @@
      0x1.ae89f995ad3adp+0, 0x1.b7f76f2fb5e47p+0, 0x1.c199bdd85529cp+0, 0x1.cb720dcef9069p+0, \
      0x1.d5818dcfba487p+0, 0x1.dfc97337b9b5fp+0, 0x1.ea4afa2a490dap+0, 0x1.f50765b6e4540p+0}
 
-// The method in three steps around its table lookup, so that a caller can
-// fetch the table entry its own way (GPU code: from another lane's
-// register):
-//   ref_expf_special  1 and *y for the inputs the method does not take
-//                     (|x| >= 88, inf, nan), else 0;
-//   ref_expf_reduce   r and k (*ki); the entry is 2^((k & 31)/32);
-//   ref_expf_finish   the result from r, k and the entry's bits.
-REF_EXPF_FN int ref_expf_special(float x, float* y)
-{
-    uint32_t ux;
-    memcpy(&ux, &x, 4);
-    if (((ux >> 20) & 0x7ff) >= 0x42b) {   // |x| >= 88, inf or nan
-        if (ux == 0xff800000u) { *y = 0.0f; return 1; }                 // -inf
-        if (((ux >> 20) & 0x7ff) >= 0x7f8) { *y = x + x; return 1; }    // +inf, nan
-        if (x > 0x1.62e42ep6f) { *y = (float)INFINITY; return 1; }      // overflow
-        if (x < -0x1.9fe368p6f) { *y = 0.0f; return 1; }                // underflow
-    }
-    return 0;
-}
-
-REF_EXPF_FN double ref_expf_reduce(float x, uint64_t* ki)
+// The same with the 32-entry table read from `tab` (e.g. a copy in GPU LDS,
+// where a lookup is cheaper than a read of the constant array).
+REF_EXPF_FN float ref_expf_tab(float x, const double* tab)
 {
     const double inv_ln2_32 = 0x1.71547652b82fep+0 * 32;
     const double shift = 0x1.8p+52;
-    const double xd = (double)x;
-    const double z = inv_ln2_32 * xd;
-    double kd = z + shift;
-    memcpy(ki, &kd, 8);
-    kd -= shift;
-    return fma(inv_ln2_32, xd, -kd);
-}
-
-REF_EXPF_FN float ref_expf_finish(double r, uint64_t ki, uint64_t t)
-{
     const double c0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
     const double c1 = 0x1.ebfce50fac4f3p-3 / 32 / 32;
     const double c2 = 0x1.62e42ff0c52d6p-1 / 32;
+    uint32_t ux;
+    memcpy(&ux, &x, 4);
+    if (((ux >> 20) & 0x7ff) >= 0x42b) {   // |x| >= 88, inf or nan
+        if (ux == 0xff800000u) return 0.0f; // -inf
+        if (((ux >> 20) & 0x7ff) >= 0x7f8) return x + x;  // +inf, nan
+        if (x > 0x1.62e42ep6f) return (float)INFINITY;     // overflow
+        if (x < -0x1.9fe368p6f) return 0.0f;               // underflow
+    }
+    const double xd = (double)x;
+    const double z = inv_ln2_32 * xd;
+    double kd = z + shift;
+    uint64_t ki;
+    memcpy(&ki, &kd, 8);
+    kd -= shift;
+    const double r = fma(inv_ln2_32, xd, -kd);
+    uint64_t t;
+    memcpy(&t, &tab[ki & 31], 8);
     t += (ki >> 5) << 52;  // 2^(k/32) = 2^(k>>5) * 2^((k&31)/32)
     double s;
     memcpy(&s, &t, 8);
     const double p = fma(fma(c0, r, c1), r * r, fma(c2, r, 1.0));
     return (float)(p * s);
-}
-
-// The same with the 32-entry table read from `tab` (e.g. a copy in GPU LDS,
-// where a lookup is cheaper than a read of the constant array).
-REF_EXPF_FN float ref_expf_tab(float x, const double* tab)
-{
-    float y;
-    if (ref_expf_special(x, &y)) return y;
-    uint64_t ki;
-    const double r = ref_expf_reduce(x, &ki);
-    uint64_t t;
-    memcpy(&t, &tab[ki & 31], 8);
-    return ref_expf_finish(r, ki, t);
 }
 
 REF_EXPF_FN float ref_expf(float x)

@@ -53,18 +53,6 @@ __device__ __forceinline__ float wave_max(float v)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// unsigned maximum (0 is the identity the masked DPP steps bring in)
-__device__ __forceinline__ uint32_t wave_umax(uint32_t v)
-{
-    v = max(v, (uint32_t)wave_dpp_i<WDPP_XOR1>(0, (int)v));
-    v = max(v, (uint32_t)wave_dpp_i<WDPP_XOR2>(0, (int)v));
-    v = max(v, (uint32_t)wave_dpp_i<WDPP_HALF_MIRROR>(0, (int)v));
-    v = max(v, (uint32_t)wave_dpp_i<WDPP_MIRROR>(0, (int)v));
-    v = max(v, (uint32_t)wave_dpp_i<WDPP_BCAST15, 0xA>(0, (int)v));
-    v = max(v, (uint32_t)wave_dpp_i<WDPP_BCAST31, 0xC>(0, (int)v));
-    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
-}
-
 __device__ __forceinline__ int wave_sum_i(int v)
 {
     v += wave_dpp_i<WDPP_XOR1>(0, v);
