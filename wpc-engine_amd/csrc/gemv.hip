@@ -507,6 +507,16 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     // these loads go out together, before the exit test below needs nwg
     const int nbk_ = P.nbk, ltw_ = P.ltw;
     const uint32_t kg_inv_ = P.kg_inv;
+    // The fields the end phase reads. The plain GEMV requests them with the
+    // others (read at the end, each was a dependent scalar round trip in the
+    // launch's tail: cfg1 step 29.59 -> 29.40 us); the transform kinds, which
+    // hold more fields already, read them at the end (requested here too,
+    // they made the dense Qwen3-4B-shaped decode 739 -> 724 tok/s).
+    float* const out_y = P.y;
+    const float* const out_bias = P.bias;
+    float* const out_y2 = P.y2;
+    const float* const out_bias2 = P.bias2;
+    const int out_rows = P.rows, out_nb2 = P.n_b2;
     // With them, the fields each kind reads before its weight loads (read
     // where they are used, each was a further dependent round trip): one
     // statement, so that one wait covers them all.
@@ -518,9 +528,15 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
         const int i1 = XF == XF_MERGE ? P.n_heads : KIND != FK_PLAIN ? P.top_k : 0;
         const int i2 = KIND == FK_ROUTE ? P.norm_topk : 0, i3 = KIND == FK_ROUTE ? P.sel_k : 0;
         const int i4 = XF == XF_NORM ? P.n_xa : 0;
-        asm volatile("" ::"s"(nb), "s"(kg), "s"(tw), "s"(nwg), "s"(rows_pad), "s"(codes), "s"(hplane),
-                     "s"(params), "s"(x0), "s"(nbk_), "s"(ltw_), "s"(kg_inv_), "s"(f0), "s"(f1), "s"(f2), "s"(i0),
-                     "s"(i1), "s"(i2), "s"(i3), "s"(i4));
+        if constexpr (XF == XF_NONE)
+            asm volatile("" ::"s"(nb), "s"(kg), "s"(tw), "s"(nwg), "s"(rows_pad), "s"(codes), "s"(hplane),
+                         "s"(params), "s"(x0), "s"(nbk_), "s"(ltw_), "s"(kg_inv_), "s"(f0), "s"(f1), "s"(f2),
+                         "s"(i0), "s"(i1), "s"(i2), "s"(i3), "s"(i4), "s"(out_y), "s"(out_bias), "s"(out_y2),
+                         "s"(out_bias2), "s"(out_rows), "s"(out_nb2));
+        else
+            asm volatile("" ::"s"(nb), "s"(kg), "s"(tw), "s"(nwg), "s"(rows_pad), "s"(codes), "s"(hplane),
+                         "s"(params), "s"(x0), "s"(nbk_), "s"(ltw_), "s"(kg_inv_), "s"(f0), "s"(f1), "s"(f2),
+                         "s"(i0), "s"(i1), "s"(i2), "s"(i3), "s"(i4));
     }
     if (local >= nwg) return;  // past this problem's workgroups
     const int tg = kg == 1 ? local : (int)__umulhi((uint32_t)local, kg_inv_), kgi = local - tg * kg;  // tile group, K-slice
@@ -980,20 +996,20 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
         for (int k = 1; k < kw; k++) sum += red[tt * kw + k][rr];
         if constexpr (xform == XF_NORM) sum *= rscale;
     }
-    if (kg == 1 || P.y2) {  // one slice, or the deferred split: slices k >= 1 to y2
-        if (mine && orow < (size_t)P.rows) {
+    if (kg == 1 || out_y2) {  // one slice, or the deferred split: slices k >= 1 to y2
+        if (mine && orow < (size_t)out_rows) {
             if (kgi == 0) {
-                if (P.bias) {
-                    float b = P.bias[orow];
-                    if (P.bias2) {
-                        b += P.bias2[orow];
-                        if (P.n_b2 > 1) b += P.bias2[(size_t)P.rows + orow];
+                if (out_bias) {
+                    float b = out_bias[orow];
+                    if (out_bias2) {
+                        b += out_bias2[orow];
+                        if (out_nb2 > 1) b += out_bias2[(size_t)out_rows + orow];
                     }
                     sum += b;
                 }
-                P.y[orow] = sum;
+                out_y[orow] = sum;
             } else {
-                P.y2[(size_t)(kgi - 1) * P.rows + orow] = sum;
+                out_y2[(size_t)(kgi - 1) * out_rows + orow] = sum;
             }
         }
         return;
@@ -1023,12 +1039,12 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     }
     __syncthreads();
     if (!s_last) return;
-    if (mine && orow < (size_t)P.rows) {
+    if (mine && orow < (size_t)out_rows) {
         float acc = __hip_atomic_load(P.part + orow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         for (int k = 1; k < kg; k++)
             acc += __hip_atomic_load(P.part + (size_t)k * P.rows_pad + orow, __ATOMIC_RELAXED,
                                      __HIP_MEMORY_SCOPE_AGENT);
-        P.y[orow] = P.bias ? acc + P.bias[orow] : acc;
+        out_y[orow] = out_bias ? acc + out_bias[orow] : acc;
     }
     if (t == 0) __hip_atomic_store(P.counters + tg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
