@@ -239,12 +239,23 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
             // chunked attention; o_proj merges the chunks, residual += o_proj(attn)
             WPCG_HIP(launch_attention_chunks(m->q, m->k, m->v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale,
                                              m->rope, (int)c.max_pos, m->st, kc, vc, m->part_o, m->part_ml, s));
-            GemvJob o{&L.o->m, &L.o->plan, m->part_o, m->residual, m->residual};
-            o.xform = XF_MERGE;
-            o.x2 = m->part_ml;
-            o.st = m->st;
-            o.head_dim = hd;
-            o.n_heads = nh;
+            // The dense model merges the chunks once, in a launch of its own,
+            // and runs o_proj as a plain GEMV: its o_proj is unsplit (32
+            // blocks per workgroup), so each of its 160 workgroups merged
+            // the chunk states of every head, 43 MB of reads per launch
+            // (o_proj 9.3 us; merge 2.x us + plain GEMV). The MoE model's
+            // two-slice o_proj merges half the heads per workgroup and keeps
+            // the merge in its prep.
+            const bool merge_apart = !c.n_experts;
+            if (merge_apart) WPCG_HIP(launch_attention_merge(m->part_o, m->part_ml, nh, hd, m->attn, s));
+            GemvJob o{&L.o->m, &L.o->plan, merge_apart ? m->attn : m->part_o, m->residual, m->residual};
+            if (!merge_apart) {
+                o.xform = XF_MERGE;
+                o.x2 = m->part_ml;
+                o.st = m->st;
+                o.head_dim = hd;
+                o.n_heads = nh;
+            }
             // Two K-slices: no handoff between them. Slice 0 adds its sum to
             // the residual in place, slice 1 writes o2, and the next ops read
             // residual + o2 (a handoff of three device-scope round trips

@@ -920,6 +920,39 @@ __global__ __launch_bounds__(256) void k_add(float* __restrict__ x, const float*
     if (i < n) x[i] = __fadd_rn(x[i], y[i]);
 }
 
+// ---- the FAST attention's chunk states merged into its output -------------
+// out[h][d] = sum_c e^(m_c - M) o_c[h][d] / sum_c e^(m_c - M) l_c[h] with
+// M = max_c m_c: the merge the o_proj GEMV's XF_MERGE prep does as it reads
+// x, with the same operations in the same order (chunk order, fused
+// multiply-adds, one correctly rounded reciprocal), done once per head for
+// a plain GEMV that follows. Workgroup h, thread d < hd.
+__global__ __launch_bounds__(128) void k_attention_merge(const float* __restrict__ part_o,
+                                                         const float* __restrict__ part_ml, int nh, int hd,
+                                                         float* __restrict__ out)
+{
+    const int h = blockIdx.x, d = threadIdx.x;
+    if (d >= hd) return;
+    const size_t stride = (size_t)nh * hd;
+    float m[ATTN_CHUNKS], l[ATTN_CHUNKS], o[ATTN_CHUNKS];
+#pragma unroll
+    for (int cc = 0; cc < ATTN_CHUNKS; cc++) {
+        m[cc] = part_ml[((size_t)cc * nh + h) * 2];
+        l[cc] = part_ml[((size_t)cc * nh + h) * 2 + 1];
+        o[cc] = part_o[cc * stride + (size_t)h * hd + d];
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int cc = 0; cc < ATTN_CHUNKS; cc++) M = fmaxf(M, m[cc]);
+    float L = 0.0f, a = 0.0f;
+#pragma unroll
+    for (int cc = 0; cc < ATTN_CHUNKS; cc++) {
+        const float w = __expf(m[cc] - M);  // 0 for a chunk that held no position
+        L = fmaf(w, l[cc], L);
+        a = fmaf(w, o[cc], a);
+    }
+    out[(size_t)h * hd + d] = a * __fdiv_rn(1.0f, L);
+}
+
 // ---- argmax (sampling.rs:3-14) and the next step's input -------------------
 // First index of the largest logit (strict >, so NaN never wins; 0 when no
 // logit beats -inf).
@@ -1083,6 +1116,15 @@ hipError_t launch_prefill_attention(float* Q, const float* Kx, const float* Vx, 
         hipLaunchKernelGGL(k_pf_attention<64>, dim3(nkv, n), dim3(FA_WG), 0, s, Q, nh, nkv, scale, pos0, max_pos,
                            kc, vc, out);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_attention_merge(const float* part_o, const float* part_ml, int nh, int hd, float* out,
+                                  hipStream_t s)
+{
+    if (nh < 1 || hd < 1 || hd > 128) return hipErrorInvalidValue;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k_attention_merge, dim3(nh), dim3(128), 0, s, part_o, part_ml, nh, hd, out);
     return hipGetLastError();
 }
 

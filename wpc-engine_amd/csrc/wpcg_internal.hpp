@@ -319,6 +319,10 @@ hipError_t launch_attention_chunks(const float* q, const float* k, const float* 
                                    const float* kn, int nh, int nkv, int hd, float eps, float scale,
                                    const float* rope, int cache_pos, const DecodeState* st, float* kc,
                                    float* vc, float* part_o, float* part_ml, hipStream_t s);
+// The chunk states of launch_attention_chunks merged into out [nh][hd], as
+// the XF_MERGE transform merges them (hd <= 128).
+hipError_t launch_attention_merge(const float* part_o, const float* part_ml, int nh, int hd, float* out,
+                                  hipStream_t s);
 hipError_t launch_add(float* x, const float* y, int n, hipStream_t s);
 // ---- batched prefill (decode.hip, gemv.hip, moe.hip, prefill.hip) ---------
 // n tokens at positions pos0 .. pos0+n-1, row t of every batch buffer being
