@@ -1023,6 +1023,33 @@ __global__ __launch_bounds__(AM_WG) void k_argmax_next(const float* __restrict__
     }
 }
 
+// The same from the keys of a FAST GEMV's workgroups (GemvJob::amax): the
+// largest key names the first largest logit (0 when no logit beat -inf).
+__global__ __launch_bounds__(AM_WG) void k_argmax_keys_next(const uint64_t* __restrict__ keys, int n,
+                                                            DecodeState* __restrict__ st,
+                                                            uint32_t* __restrict__ tokens)
+{
+    __shared__ uint64_t sk[AM_WG / 64];
+    uint64_t k = 0;
+    for (int i = threadIdx.x; i < n; i += AM_WG) k = max(k, keys[i]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t k2 = ((uint64_t)(uint32_t)__shfl_xor((int)(k >> 32), o) << 32) |
+                            (uint32_t)__shfl_xor((int)(uint32_t)k, o);
+        k = max(k, k2);
+    }
+    if ((threadIdx.x & 63) == 0) sk[threadIdx.x >> 6] = k;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < AM_WG / 64; w++) k = max(k, sk[w]);
+        const uint32_t next = k ? 0xFFFFFFFFu - (uint32_t)k : 0u;
+        const uint32_t p = st->pos + 1;
+        st->last = next;
+        if (p >= st->n_prompt && p <= st->max_pos) tokens[p] = next;
+        st->pos = p;
+    }
+}
+
 // out[r] = argmax of row r of logits [rows][n] (0 when none beats -inf).
 __global__ __launch_bounds__(AM_WG) void k_argmax_rows(const float* __restrict__ logits, int n,
                                                        uint32_t* __restrict__ out)
@@ -1139,6 +1166,15 @@ hipError_t launch_argmax_rows(const float* logits, int n, int rows, uint32_t* ou
 {
     (void)hipGetLastError();
     hipLaunchKernelGGL(k_argmax_rows, dim3(rows), dim3(AM_WG), 0, s, logits, n, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax_keys_next(const uint64_t* keys, int n, DecodeState* st, uint32_t* tokens,
+                                   hipStream_t s)
+{
+    if (n < 1) return hipErrorInvalidValue;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k_argmax_keys_next, dim3(1), dim3(AM_WG), 0, s, keys, n, st, tokens);
     return hipGetLastError();
 }
 

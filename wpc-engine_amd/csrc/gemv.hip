@@ -313,6 +313,7 @@ struct FastProblem {
     const float* x_add;
     const float* bias2;
     int n_xa, n_b2;
+    uint64_t* amax;  // one K-slice: workgroup w's key of its first largest row
 };
 struct FastBatch {
     FastProblem p[MAX_JOBS];
@@ -997,7 +998,8 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
         if constexpr (xform == XF_NORM) sum *= rscale;
     }
     if (kg == 1 || out_y2) {  // one slice, or the deferred split: slices k >= 1 to y2
-        if (mine && orow < (size_t)out_rows) {
+        const bool row_ok = mine && orow < (size_t)out_rows;
+        if (row_ok) {
             if (kgi == 0) {
                 if (out_bias) {
                     float b = out_bias[orow];
@@ -1011,6 +1013,25 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
             } else {
                 out_y2[(size_t)(kgi - 1) * out_rows + orow] = sum;
             }
+        }
+        // the argmax key of this workgroup's rows (one slice: every output
+        // row is a thread of wave 0): (order-preserving bits of the value,
+        // -0 read as +0) << 32 | ~row, 0 for a value that does not beat -inf
+        if (P.amax && wave == 0) {
+            uint64_t key = 0;
+            const float v = __fadd_rn(sum, 0.0f);
+            if (row_ok && v > -INFINITY) {
+                const uint32_t b = __float_as_uint(v);
+                key = ((uint64_t)((b & 0x80000000u) ? ~b : (b | 0x80000000u)) << 32) |
+                      (0xFFFFFFFFu - (uint32_t)orow);
+            }
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) {
+                const uint64_t k2 = ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), o) << 32) |
+                                    (uint32_t)__shfl_xor((int)(uint32_t)key, o);
+                key = k2 > key ? k2 : key;
+            }
+            if (lane == 0) P.amax[tg] = key;
         }
         return;
     }
@@ -1256,6 +1277,7 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         P.bias2 = J.bias2;
         P.n_xa = J.n_xa;
         P.n_b2 = J.n_b2;
+        P.amax = J.amax;
         P.head_dim = J.head_dim;
         P.n_heads = J.n_heads;
         if (J.routed) {  // the chosen experts' rows side by side
@@ -1271,6 +1293,7 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         if (J.y2 && (P.kg < 2 || J.routed)) return hipErrorInvalidValue;
         if ((J.x_add && J.xform != XF_NORM) || (J.bias2 && !J.bias)) return hipErrorInvalidValue;
         if (J.n_xa < 1 || J.n_xa > 2 || J.n_b2 < 1 || J.n_b2 > 2) return hipErrorInvalidValue;
+        if (J.amax && (P.kg != 1 || J.routed)) return hipErrorInvalidValue;
         if (J.xform == XF_MERGE && (!J.x2 || !J.st || (J.head_dim != 64 && J.head_dim != 128) ||
                                     (uint64_t)J.n_heads * J.head_dim != m.cols))
             return hipErrorInvalidValue;

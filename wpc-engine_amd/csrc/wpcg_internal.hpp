@@ -136,6 +136,9 @@ struct GemvJob {
     int n_exp = 0, top_k = 0, norm_topk = 0;
     int32_t* ids_out = nullptr;
     float* w_out = nullptr;
+    // one K-slice, not routed: workgroup w also stores at amax[w] the key of
+    // the first largest of its output rows (see launch_argmax_keys_next)
+    uint64_t* amax = nullptr;
 };
 // FAST mode: a workgroup computes fast_tiles_per_wg 16-row tiles over a
 // K-slice of at most fast_max_slice blocks (the slice's x digits live in LDS).
@@ -351,6 +354,12 @@ hipError_t launch_pf_combine(float* X, const float* D, const float* w, const int
 // Y = X W^T (+ res) for M rows of fp32 X with the linear's batched kernels
 // (x_mode GX_*), its workspace made on first use (not under capture).
 int linear_gemm(wpcg_linear* L, const float* x, int x_mode, uint32_t M, const float* res, float* y, hipStream_t s);
+// The same from the keys a FAST GEMV's workgroups left (GemvJob::amax), one
+// per workgroup in row order: a row's key is (its value's order-preserving
+// bits, -0 read as +0) << 32 | ~row, 0 for a value that does not beat -inf
+// (NaN included), so the largest key is the first largest value.
+hipError_t launch_argmax_keys_next(const uint64_t* keys, int n, DecodeState* st, uint32_t* tokens,
+                                   hipStream_t s);
 hipError_t launch_argmax_next(const float* logits, int n, DecodeState* st, uint32_t* tokens,
                               hipStream_t s);
 // out[r] = the first index of the largest logit of row r (logits [rows][n]).
