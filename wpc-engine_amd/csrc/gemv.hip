@@ -1015,21 +1015,21 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
             }
         }
         // the argmax key of this workgroup's rows (one slice: every output
-        // row is a thread of wave 0): (order-preserving bits of the value,
-        // -0 read as +0) << 32 | ~row, 0 for a value that does not beat -inf
+        // row is a thread of wave 0, rows growing with the lane):
+        // (order-preserving bits of the largest value, -0 read as +0) << 32 |
+        // ~(its first row), 0 when no value beats -inf (NaN never does). The
+        // largest value by a DPP maximum and its first row by a ballot: a
+        // 64-bit maximum by lane exchanges (twelve LDS-crossbar round trips)
+        // cost the 2374-workgroup lm_head 1.7 us.
         if (P.amax && wave == 0) {
+            const float v = row_ok && sum > -INFINITY ? sum : -INFINITY;
+            const float vmax = wave_max(v);
             uint64_t key = 0;
-            const float v = __fadd_rn(sum, 0.0f);
-            if (row_ok && v > -INFINITY) {
-                const uint32_t b = __float_as_uint(v);
-                key = ((uint64_t)((b & 0x80000000u) ? ~b : (b | 0x80000000u)) << 32) |
-                      (0xFFFFFFFFu - (uint32_t)orow);
-            }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const uint64_t k2 = ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), o) << 32) |
-                                    (uint32_t)__shfl_xor((int)(uint32_t)key, o);
-                key = k2 > key ? k2 : key;
+            if (vmax > -INFINITY) {
+                const uint64_t at = __ballot(v == vmax);  // -0 == +0: the first of them
+                const uint32_t row = (uint32_t)__builtin_amdgcn_readlane((int)orow, __ffsll((long long)at) - 1);
+                const uint32_t b = __float_as_uint(__fadd_rn(vmax, 0.0f));
+                key = ((uint64_t)((b & 0x80000000u) ? ~b : (b | 0x80000000u)) << 32) | (0xFFFFFFFFu - row);
             }
             if (lane == 0) P.amax[tg] = key;
         }
