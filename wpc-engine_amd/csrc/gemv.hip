@@ -518,6 +518,7 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     float* const out_y2 = P.y2;
     const float* const out_bias2 = P.bias2;
     const int out_rows = P.rows, out_nb2 = P.n_b2;
+    uint64_t* const out_amax = P.amax;
     // With them, the fields each kind reads before its weight loads (read
     // where they are used, each was a further dependent round trip): one
     // statement, so that one wait covers them all.
@@ -533,7 +534,7 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
             asm volatile("" ::"s"(nb), "s"(kg), "s"(tw), "s"(nwg), "s"(rows_pad), "s"(codes), "s"(hplane),
                          "s"(params), "s"(x0), "s"(nbk_), "s"(ltw_), "s"(kg_inv_), "s"(f0), "s"(f1), "s"(f2),
                          "s"(i0), "s"(i1), "s"(i2), "s"(i3), "s"(i4), "s"(out_y), "s"(out_bias), "s"(out_y2),
-                         "s"(out_bias2), "s"(out_rows), "s"(out_nb2));
+                         "s"(out_bias2), "s"(out_rows), "s"(out_nb2), "s"(out_amax));
         else
             asm volatile("" ::"s"(nb), "s"(kg), "s"(tw), "s"(nwg), "s"(rows_pad), "s"(codes), "s"(hplane),
                          "s"(params), "s"(x0), "s"(nbk_), "s"(ltw_), "s"(kg_inv_), "s"(f0), "s"(f1), "s"(f2),
@@ -1021,7 +1022,7 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
         // largest value by a DPP maximum and its first row by a ballot: a
         // 64-bit maximum by lane exchanges (twelve LDS-crossbar round trips)
         // cost the 2374-workgroup lm_head 1.7 us.
-        if (P.amax && wave == 0) {
+        if (out_amax && wave == 0) {
             const float v = row_ok && sum > -INFINITY ? sum : -INFINITY;
             const float vmax = wave_max(v);
             uint64_t key = 0;
@@ -1031,7 +1032,7 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
                 const uint32_t b = __float_as_uint(__fadd_rn(vmax, 0.0f));
                 key = ((uint64_t)((b & 0x80000000u) ? ~b : (b | 0x80000000u)) << 32) | (0xFFFFFFFFu - row);
             }
-            if (lane == 0) P.amax[tg] = key;
+            if (lane == 0) out_amax[tg] = key;
         }
         return;
     }
