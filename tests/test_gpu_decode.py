@@ -176,6 +176,47 @@ def test_fast_decode_tracks_the_reference(ctx, name, cfg, n_steps, seed):
     ref.close()
 
 
+@pytest.mark.parametrize("factor,nan_rows,answers", [(2.0, (3,), (0, 70)), (0.5, (0, 3), (1, 70))])
+def test_fast_argmax_ties_and_nan(ctx, factor, nan_rows, answers):
+    """The FAST head leaves one argmax key per workgroup and the argmax
+    reduces the keys; it must still return the first index of the largest
+    logit and never a NaN one, as the reference's argmax (sampling.rs:3-14)
+    scans. The tied embedding here holds one base row everywhere, that row
+    with its zero points and scales times `factor` (every logit exactly
+    scaled, in the oracle and on the GPU) at rows 70 and 900, in different
+    workgroups of the head, and NaN scales at `nan_rows`. So the largest
+    logit ties exactly, either between rows 70 and 900 or among every base
+    row, and the answer is 70 or the first base row that is not NaN."""
+    cfg = dict(DENSE)
+    tensors = dict(synth.model_tensors(cfg, 4, 818, wpcg.encode))
+    name = "model.embed_tokens.weight"
+    emb = tensors[name].reshape(cfg["vocab"], -1, 68).copy()
+    emb[:] = emb[1]
+    params = emb[70, :, 0:4].copy().view(np.float16) * np.float16(factor)
+    emb[70, :, 0:4] = emb[900, :, 0:4] = params.view(np.uint8)
+    for r in nan_rows:
+        emb[r, :, 2:4] = np.frombuffer(np.float16(np.nan).tobytes(), np.uint8)
+    tensors[name] = emb.reshape(-1)
+    m = wpcg.Model(ctx, 4, wpcg.ModelConfig(**cfg))
+    for k, arr in tensors.items():
+        m.set_tensor(k, arr)
+    kern = O.KERNEL_AVX2 if O.have_avx2() else O.KERNEL_FUSED
+    ref = O.Model(cfg, tensors, cfg["max_pos"], kern, 16)
+    m.set_mode(wpcg.MODE_FAST)
+    tok, seen = 2, set()
+    for step in range(20):
+        r = ref.forward_token(tok)
+        g, a = m.forward_token(tok)
+        assert all(np.isnan(r[i]) and np.isnan(g[i]) for i in nan_rows), step
+        tok = O.argmax(r)
+        assert tok in answers, f"step {step}: the oracle's argmax {tok}"
+        assert a == tok, f"step {step}: FAST argmax {a} vs the oracle's {tok}"
+        seen.add(tok)
+    print(f"[gpu] argmax keys (x{factor}): 20 steps equal to the oracle's, answers {sorted(seen)}", flush=True)
+    m.close()
+    ref.close()
+
+
 def test_decode_errors(ctx):
     cfg = dict(DENSE)
     m = wpcg.Model(ctx, 4, wpcg.ModelConfig(**cfg))
