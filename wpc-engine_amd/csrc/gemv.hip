@@ -467,12 +467,16 @@ __device__ __forceinline__ int route_wg(const float* __restrict__ scores, int n,
 // XF: the input transform (XF_NONE, XF_NORM, XF_SILU), also shared by the
 // launch's problems.
 constexpr int FK_PLAIN = 0, FK_ROUTE = 1, FK_ROUTED = 2;
-template <int SCHEME, int KIND, int XF>
+// XPN: x pairs (two blocks) per wave the registers hold, MAXBK / 16 for a
+// full slice; the norm-folding plain GEMV of slices of at most 32 blocks
+// (the decode's q/k/v, gate/up and lm_head) uses 2, which fits six waves per
+// SIMD (three workgroups per CU) without spilling.
+template <int SCHEME, int KIND, int XF, int XPN = MAXBK / 16>
 // The plain GEMV asks for 6 waves per SIMD (at most 80 VGPRs): three
 // workgroups per CU instead of two, so a launch of up to 768 workgroups
 // runs in one round (2x9728x2560 v3: 12.5 -> 11.1 us). The routing kinds
 // keep their registers (their routing state would spill).
-__global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1) void k_gemv_fast(const FastBatch B)
+__global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && (XF == XF_NONE || (XF == XF_NORM && XPN == 2)) ? 6 : 1) void k_gemv_fast(const FastBatch B)
 {
     // A wave's last group of MG may reach up to MG-1 blocks past the slice:
     // those blocks' codes are zero, their digits are never written (any
@@ -569,7 +573,7 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && XF == XF_NONE ? 6 : 1)
     // FK_ROUTE, routing runs between the x loads and the weight loads.)
     // x pair p = wave + 8*i: blocks 2p, 2p+1; lane l holds x[4(l&31) .. +3]
     // of block 2p + (l>>5).
-    constexpr int XP = MAXBK / 16;  // pairs per wave
+    constexpr int XP = XPN;  // x pairs per wave at most
     // The plain GEMV loads XP0 pairs up front and the rest only when its
     // slice has them (slices of more than 32 blocks): fewer registers held
     // across the memory round trip.
@@ -1321,12 +1325,18 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
     for (int i = 1; i < n; i++)
         if ((jobs[i].routed ? FK_ROUTED : jobs[i].scores ? FK_ROUTE : FK_PLAIN) != kind || jobs[i].xform != xf)
             return hipErrorInvalidValue;
+    // every problem's K-slice within 32 blocks: two x pairs per wave suffice
+    bool short_slices = true;
+    for (int i = 0; i < n; i++)
+        if (B.p[i].nbk > 32) short_slices = false;
     (void)hipGetLastError();  // report only this launch
     const dim3 grid(wgs, n), block(FAST_WG);
 #define WPCG_FAST(S, K, X) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<S, K, X>), grid, block, 0, s, B)
+#define WPCG_FAST2(S, K, X) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<S, K, X, 2>), grid, block, 0, s, B)
 #define WPCG_FAST_S(S)                                                               \
     do {                                                                             \
         if (kind == FK_PLAIN && xf == XF_NONE) WPCG_FAST(S, FK_PLAIN, XF_NONE);      \
+        else if (kind == FK_PLAIN && xf == XF_NORM && short_slices) WPCG_FAST2(S, FK_PLAIN, XF_NORM); \
         else if (kind == FK_PLAIN && xf == XF_NORM) WPCG_FAST(S, FK_PLAIN, XF_NORM); \
         else if (kind == FK_PLAIN && xf == XF_SILU) WPCG_FAST(S, FK_PLAIN, XF_SILU); \
         else if (kind == FK_PLAIN && xf == XF_MERGE) WPCG_FAST(S, FK_PLAIN, XF_MERGE); \
@@ -1340,6 +1350,7 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
     else
         WPCG_FAST_S(3);
 #undef WPCG_FAST_S
+#undef WPCG_FAST2
 #undef WPCG_FAST
     return hipGetLastError();
 }
