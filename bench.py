@@ -805,7 +805,7 @@ def main():
     decode_dense = decode_bench(ctx, wpcg, synth, "decode_dense", args.dense_prompt, args.decode_new,
                                 cpu_tokens, args.decode_eager) if "decode_dense" in sections else None
 
-    kname = f"k_gemv_exact<{scheme}>" if mode == wpcg.MODE_EXACT else f"k_gemv_fast<{scheme}, 0, 0>"
+    kname = f"k_gemv_exact<{scheme}>" if mode == wpcg.MODE_EXACT else f"k_gemv_fast<{scheme}, 0, 0, 4>"
     rec = {
         "metric": METRIC,
         "value": round(value, 2),
