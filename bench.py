@@ -53,7 +53,7 @@ BPB = {3: 100, 4: 68}
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (bench.py --pmc-pass) and scaled by
 # the same counters' reading for a copy kernel of known size; see
 # profiles/k_gemv_fast_cfg1_v3_traffic.txt. None where not measured.
-TRAFFIC = {(3, "fast"): 20049196}
+TRAFFIC = {(3, "fast"): 20051404}
 TRAFFIC_SOURCE = ("profiles/k_gemv_fast_cfg1_v3_traffic.txt: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE "
                   "passes over bench.py --pmc-pass (the workload rotated over >= 1 GB, HBM-cold), scaled by "
                   "a 256 MiB device copy's readings")
