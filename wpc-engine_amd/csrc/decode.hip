@@ -247,6 +247,7 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
 constexpr int AT_WG = 256;
 constexpr int AT_MAXPOS = 4096;
 constexpr int AT_VB = 32;  // value rows per LDS block of the output step
+constexpr int AT_VD = 4;   // value blocks whose loads are in flight at once
 
 template <int MODE>
 __device__ void head_rms_rope(const float* x, const float* w, float* y, float* red, int hd,
@@ -296,6 +297,28 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
     __syncthreads();
     const float* kb = kc + (size_t)j * max_pos * hd;
     const float* vb = vc + (size_t)j * max_pos * hd;
+    // The cached value rows (t < pos) for the output step: blocks of AT_VB
+    // positions, AT_VD of them in flight in registers; the first AT_VD are
+    // requested here, before this workgroup's cache write (row pos, which
+    // no block reads), so they arrive during the scores and the softmax.
+    const int nv = (int)pos, nblk = (nv + AT_VB - 1) / AT_VB, f4 = AT_VB * hd / 4;
+    constexpr int VPER = AT_VB * 256 / 4 / AT_WG;  // float4s per thread per block (hd <= 256)
+    // Every block issues VPER range-checked loads per thread, so the count
+    // in flight is fixed and each wait is for one block only: rows t >= pos,
+    // blocks past the last and lanes past the block's f4 float4s read zeros
+    // (their offsets are out of range, which moves no data).
+    const auto vrs = buf_rsrc(vb, nv * hd * 4);
+    u32x4 vr[AT_VD][VPER];
+    auto vload = [&](int bk, u32x4(&r)[VPER]) {
+#pragma unroll
+        for (int u = 0; u < VPER; u++) {
+            const int i = threadIdx.x + u * AT_WG;  // float4 of the block
+            r[u] = __builtin_amdgcn_raw_buffer_load_b128(vrs, i < f4 ? (bk * AT_VB * hd + 4 * i) * 4 : 0x7ffffff0,
+                                                         0, 0);
+        }
+    };
+#pragma unroll
+    for (int r = 0; r < AT_VD; r++) vload(r, vr[r]);
     if (h % n_rep == 0)
         for (int i = threadIdx.x; i < hd; i += AT_WG) {
             kc[((size_t)j * max_pos + pos) * hd + i] = ks[i];
@@ -360,27 +383,16 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
     if (ssum > 0.0f)
         for (int t = threadIdx.x; t < n; t += AT_WG) w[t] = __fdiv_rn(w[t], ssum);
     __syncthreads();
-    // out[d] = sum_t w_t v_t[d], position order; thread d. The cached value
-    // rows (t < pos) pass through LDS in blocks of AT_VB positions, double
-    // buffered: the whole workgroup issues the next block's 16-byte loads
-    // before the current block's chains; t = pos comes from vs.
-    const int nv = (int)pos, nblk = (nv + AT_VB - 1) / AT_VB, f4 = AT_VB * hd / 4;
-    constexpr int VPER = AT_VB * 256 / 4 / AT_WG;  // float4s per thread per block (hd <= 256)
-    float4 vr[VPER];
-    auto vload = [&](int bk) {
-#pragma unroll
-        for (int u = 0; u < VPER; u++) {
-            const int i = threadIdx.x + u * AT_WG;  // float4 of the block
-            const int t = bk * AT_VB + 4 * i / hd;
-            vr[u] = i < f4 && t < nv ? *reinterpret_cast<const float4*>(vb + (size_t)bk * AT_VB * hd + 4 * i)
-                                     : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-    };
-    auto vstore = [&](int b) {
+    // out[d] = sum_t w_t v_t[d], position order; thread d. The value blocks
+    // pass from the register ring through LDS, double buffered: block bk is
+    // read from LDS while block bk + 1 is stored there and the loads of
+    // block bk + AT_VD take the registers block bk held; t = pos comes
+    // from vs.
+    auto vstore = [&](int b, const u32x4(&r)[VPER]) {
 #pragma unroll
         for (int u = 0; u < VPER; u++) {
             const int i = threadIdx.x + u * AT_WG;
-            if (i < f4) *reinterpret_cast<float4*>(&vsh[b][4 * i]) = vr[u];
+            if (i < f4) *reinterpret_cast<u32x4*>(&vsh[b][4 * i]) = r[u];
         }
     };
     const int d = threadIdx.x;
@@ -388,24 +400,26 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
     auto step = [&](float wt, float v) {
         acc = MODE == WPCG_MODE_EXACT ? __fadd_rn(acc, __fmul_rn(wt, v)) : fmaf(wt, v, acc);
     };
-    if (nblk > 0) {
-        vload(0);
-        vstore(0);
-    }
+    if (nblk > 0) vstore(0, vr[0]);
     __syncthreads();
-    for (int bk = 0; bk < nblk; bk++) {
-        const int b = bk & 1, t0 = bk * AT_VB;
-        if (bk + 1 < nblk) vload(bk + 1);
-        if (d < hd) {
-            if (t0 + AT_VB <= nv) {
+    for (int bk0 = 0; bk0 < nblk; bk0 += AT_VD) {
 #pragma unroll
-                for (int u = 0; u < AT_VB; u++) step(w[t0 + u], vsh[b][u * hd + d]);
-            } else {
-                for (int u = 0; u < nv - t0; u++) step(w[t0 + u], vsh[b][u * hd + d]);
+        for (int r = 0; r < AT_VD; r++) {  // block bk sits in vr[r], so the ring index is static
+            const int bk = bk0 + r;
+            if (bk >= nblk) break;  // uniform
+            const int b = bk & 1, t0 = bk * AT_VB;
+            vload(bk + AT_VD, vr[r]);
+            if (d < hd) {
+                if (t0 + AT_VB <= nv) {
+#pragma unroll
+                    for (int u = 0; u < AT_VB; u++) step(w[t0 + u], vsh[b][u * hd + d]);
+                } else {
+                    for (int u = 0; u < nv - t0; u++) step(w[t0 + u], vsh[b][u * hd + d]);
+                }
             }
+            if (bk + 1 < nblk) vstore(b ^ 1, vr[(r + 1) % AT_VD]);
+            __syncthreads();
         }
-        if (bk + 1 < nblk) vstore(b ^ 1);
-        __syncthreads();
     }
     if (d < hd) {
         step(w[pos], vs[d]);
