@@ -174,15 +174,18 @@ def kv_bytes_per_token(c, n_prompt, n_new):
     return per_pos * mean_len
 
 
-def decode_bench(ctx, wpcg, synth, key, n_prompt, n_new, cpu_tokens, eager=False, n_exact=64):
+def decode_bench(ctx, wpcg, synth, key, n_prompt, n_new, cpu_tokens, eager=False, n_exact=64,
+                 prefill_timing=True):
     """Greedy decode of a config-2/3 model: seeded weights ~N(0, 0.02)
     encoded as the artifact compiler does (layer 0 from fresh draws, later
     layers seeded row permutations of it: distinct weights, every token
     reads all its bytes from HBM), FAST generation of n_new tokens after an
     n_prompt-token prompt timed with HIP events around the replayed steps,
     EXACT generation of n_exact tokens and the number of leading ids the two
-    share, the batched prefill of the prompt, and the oracle's CPU decode of
-    the same model on a bounded sample. Returns the record's object."""
+    share, the batched prefill of the prompt, and (cpu_tokens > 0) the
+    oracle's decode of the same model at the same positions: bit identity of
+    EXACT's logits and the CPU baseline (oracle_check). Returns the
+    record's object."""
     import numpy as np
     cfg, desc = DECODE_MODELS[key]
     t0 = time.perf_counter()
@@ -200,19 +203,23 @@ def decode_bench(ctx, wpcg, synth, key, n_prompt, n_new, cpu_tokens, eager=False
         model.set_graphs(False)
     out = {}
     for mode, mk, n in ((wpcg.MODE_FAST, "fast", n_new), (wpcg.MODE_EXACT, "exact", n_exact)):
+        if n < 2:
+            continue
         model.set_mode(mode)
         model.generate(prompt, n)            # warm-up (graph capture)
         ids, ms = model.generate(prompt, n)
         out[mk] = ((n - 1) / (ms / 1e3), ms / (n - 1), ids)
         log(f"{key} {mk}: {out[mk][0]:.1f} tok/s ({out[mk][1]:.3f} ms/token, {n - 1} steps)")
     m = min(n_new, n_exact)
-    same = int(np.argmax(np.concatenate([out["fast"][2][:m] != out["exact"][2][:m], [True]])))
-    log(f"{key}: FAST greedy ids equal EXACT's for {same} of {m}")
+    same = None
+    if "exact" in out:
+        same = int(np.argmax(np.concatenate([out["fast"][2][:m] != out["exact"][2][:m], [True]])))
+        log(f"{key}: FAST greedy ids equal EXACT's for {same} of {m}")
     # the prompt alone: batched prefill (FAST) against the same tokens step
     # by step, each timed from an empty cache to the last token's logits
     model.set_mode(wpcg.MODE_FAST)
     pre = {}
-    for pk, batched in (("batched", True), ("steps", False)):
+    for pk, batched in (("batched", True), ("steps", False)) if prefill_timing else ():
         model.set_prefill(batched)
         model.reset()
         model.prefill(prompt, want_logits=False)  # warm-up
@@ -221,8 +228,9 @@ def decode_bench(ctx, wpcg, synth, key, n_prompt, n_new, cpu_tokens, eager=False
         _, first = model.prefill(prompt, want_logits=False)
         pre[pk] = (time.perf_counter() - t1, first)
     model.set_prefill(True)
-    log(f"{key} prefill of {n_prompt} tokens: batched {pre['batched'][0] * 1e3:.1f} ms, "
-        f"step by step {pre['steps'][0] * 1e3:.1f} ms")
+    if pre:
+        log(f"{key} prefill of {n_prompt} tokens: batched {pre['batched'][0] * 1e3:.1f} ms, "
+            f"step by step {pre['steps'][0] * 1e3:.1f} ms")
     tok_bytes = decode_token_bytes(cfg)
     kv = kv_bytes_per_token(cfg, n_prompt, n_new)
     rec = {
@@ -232,12 +240,12 @@ def decode_bench(ctx, wpcg, synth, key, n_prompt, n_new, cpu_tokens, eager=False
         "new_tokens": int(n_new),
         "tok_s": round(out["fast"][0], 2),
         "ms_per_token": round(out["fast"][1], 4),
-        "exact_tok_s": round(out["exact"][0], 2),
-        "fast_ids_equal_exact": f"{same} of {m}",
+        "exact_tok_s": round(out["exact"][0], 2) if "exact" in out else None,
+        "fast_ids_equal_exact": f"{same} of {m}" if same is not None else None,
         "prefill": {"tokens": int(n_prompt), "ms": round(pre["batched"][0] * 1e3, 2),
                     "tok_s": round(n_prompt / pre["batched"][0], 1),
                     "stepwise_ms": round(pre["steps"][0] * 1e3, 2),
-                    "first_token_equal_stepwise": bool(pre["batched"][1] == pre["steps"][1])},
+                    "first_token_equal_stepwise": bool(pre["batched"][1] == pre["steps"][1])} if pre else None,
         "weight_bytes_per_token": tok_bytes,
         "kv_bytes_per_token_mean": round(kv),
         "achieved_gbps": round((tok_bytes + kv) * out["fast"][0] / 1e9, 1),
@@ -248,29 +256,88 @@ def decode_bench(ctx, wpcg, synth, key, n_prompt, n_new, cpu_tokens, eager=False
                 "permutations of it), norms 1.0, prompt of random ids",
     }
     if cpu_tokens:
-        import oracle as O
-        kern = O.KERNEL_AVX2 if O.have_avx2() else O.KERNEL_FUSED
-        hi = host_info()
-        res = {}
-        for tk, threads, n in (("all", hi["threads_all"], cpu_tokens), ("one", 1, max(1, cpu_tokens // 4))):
-            ref = O.Model(cfg, keep, cfg["max_pos"], kern, threads)
-            ref.forward_token(int(prompt[0]))    # warm-up
-            t1 = time.perf_counter()
-            for i in range(n):
-                ref.forward_token(int(prompt[1 + i]))
-            res[tk] = (n / (time.perf_counter() - t1), n, threads)
-            ref.close()
-        rec["cpu_baseline"] = {
-            "tok_s": round(res["all"][0], 3), "cores": res["all"][2], "kind": "port",
-            "one_core_tok_s": round(res["one"][0], 3), "nproc": hi["nproc"], "cpu_model": hi["cpu_model"],
-            "sample": (f"{res['all'][1]} forward_token steps at positions 1..{res['all'][1]} on "
-                       f"{res['all'][2]} threads and {res['one'][1]} on 1 thread, the same model on the "
-                       f"host (oracle restatement, {'AVX2' if kern == O.KERNEL_AVX2 else 'scalar'} GEMV, "
-                       f"rows split over threads as rayon does)")}
-        log(f"{key} CPU baseline {res['all'][0]:.3f} tok/s on {res['all'][2]} threads, "
-            f"{res['one'][0]:.3f} on 1")
+        rec.update(oracle_check(model, wpcg, cfg, keep, prompt, key, cpu_tokens))
     model.close()
     return rec
+
+
+def oracle_check(model, wpcg, cfg, keep, prompt, key, n_steps):
+    """The full-depth model against the oracle (the CPU restatement of the
+    reference's forward_token, model.rs:419-547 / qwen3_moe_model.rs:406-542)
+    at the positions the GPU decode runs: the oracle runs the prompt on all
+    host threads, then n_steps greedy steps, timed (the CPU baseline, at
+    positions n_prompt .. n_prompt + n_steps - 1), then two more steps on
+    one thread. The GPU model in EXACT mode runs the same prompt and steps,
+    each step's logits compared with the oracle's bit for bit; in FAST mode
+    the same, each step's logits within 1e-5 of the oracle's range and the
+    greedy ids compared. Returns the record's fields."""
+    import numpy as np
+    import oracle as O
+    kern = O.KERNEL_AVX2 if O.have_avx2() else O.KERNEL_FUSED
+    hi = host_info()
+    n_prompt = len(prompt)
+    ref = O.Model(cfg, keep, cfg["max_pos"], kern, hi["threads_all"])
+    t0 = time.perf_counter()
+    for t in prompt[:-1]:
+        ref.forward_token(int(t))
+    t_prompt = time.perf_counter() - t0
+    r_last = ref.forward_token(int(prompt[-1]))
+    ref_logits, ids = [], []
+    tok = O.argmax(r_last)
+    t1 = time.perf_counter()
+    for _ in range(n_steps):
+        ids.append(tok)
+        r = ref.forward_token(tok)
+        ref_logits.append(r)
+        tok = O.argmax(r)
+    t_all = time.perf_counter() - t1
+    n_one = 2
+    t2 = time.perf_counter()
+    for _ in range(n_one):
+        r = ref.forward_token(tok, threads=1)
+        tok = O.argmax(r)
+    t_one = time.perf_counter() - t2
+    ref.close()
+    log(f"{key} oracle: prompt of {n_prompt} in {t_prompt:.1f} s, {n_steps} steps "
+        f"{n_steps / t_all:.3f} tok/s on {hi['threads_all']} threads, {n_one / t_one:.3f} on 1")
+    u32 = lambda a: np.ascontiguousarray(a, np.float32).view(np.uint32)  # noqa: E731
+    out = {}
+    for mode, mk in ((wpcg.MODE_EXACT, "exact"), (wpcg.MODE_FAST, "fast")):
+        model.set_mode(mode)
+        model.reset()
+        g_last, _ = model.prefill(prompt, want_logits=True)
+        same, worst, ids_same = [], 0.0, 0
+        for i in range(n_steps):
+            g, a = model.forward_token(ids[i])
+            r = ref_logits[i]
+            same.append(bool(np.array_equal(u32(g), u32(r))))
+            span = float(r.max() - r.min())
+            worst = max(worst, float(np.max(np.abs(g.astype(np.float64) - r))) / span)
+            ids_same += int(a == (ids[i + 1] if i + 1 < n_steps else O.argmax(r)))
+        prompt_same = bool(np.array_equal(u32(g_last), u32(r_last)))
+        out[mk] = (sum(same), worst, ids_same, prompt_same)
+        log(f"{key} {mk} vs oracle at positions {n_prompt}..{n_prompt + n_steps - 1}: "
+            f"{sum(same)} of {n_steps} steps bit-identical, worst {worst:.2e} of the logit range, "
+            f"{ids_same} of {n_steps} greedy ids equal; last prompt logits "
+            f"{'bit-identical' if prompt_same else 'differ'}")
+    model.set_mode(wpcg.MODE_FAST)
+    return {
+        "exact_equal_oracle": f"{out['exact'][0]} of {n_steps}",
+        "exact_prompt_logits_equal_oracle": out["exact"][3],
+        "fast_vs_oracle": {"max_err_of_logit_range": float(f"{out['fast'][1]:.3e}"),
+                           "greedy_ids_equal": f"{out['fast'][2]} of {n_steps}"},
+        "oracle_check": (f"full depth ({cfg['n_layers']} layers): the oracle ran the {n_prompt}-token "
+                         f"prompt and {n_steps} greedy steps (positions {n_prompt}..{n_prompt + n_steps - 1}); "
+                         f"the GPU model ran the same prompt and the oracle's ids, logits compared per step"),
+        "cpu_baseline": {
+            "tok_s": round(n_steps / t_all, 3), "cores": hi["threads_all"], "kind": "port",
+            "one_core_tok_s": round(n_one / t_one, 3), "nproc": hi["nproc"], "cpu_model": hi["cpu_model"],
+            "sample": (f"{n_steps} forward_token steps at positions {n_prompt}..{n_prompt + n_steps - 1} on "
+                       f"{hi['threads_all']} threads, then {n_one} at the next positions on 1 thread, after the "
+                       f"{n_prompt}-token prompt: the same model on the host (oracle restatement, "
+                       f"{'AVX2' if kern == O.KERNEL_AVX2 else 'scalar'} GEMV, rows split over threads as "
+                       f"rayon does)")},
+    }
 
 
 GEMMA_12B = [("gate/up_proj", 15360, 3840), ("down_proj", 3840, 15360)]
@@ -620,7 +687,13 @@ def main():
     ap.add_argument("--decode-prompt", type=int, default=256)
     ap.add_argument("--decode-new", type=int, default=256)
     ap.add_argument("--dense-prompt", type=int, default=128)
-    ap.add_argument("--decode-cpu-tokens", type=int, default=8)
+    ap.add_argument("--decode-cpu-tokens", type=int, default=8,
+                    help="oracle steps after the prompt: the full-depth bit-identity check and the "
+                         "CPU baseline (0: neither)")
+    ap.add_argument("--decode-exact", type=int, default=64,
+                    help="EXACT-mode decode steps timed and compared with FAST's ids (< 2: none)")
+    ap.add_argument("--no-prefill-timing", action="store_true",
+                    help="skip the batched-vs-stepwise prefill timing of the decode sections")
     ap.add_argument("--decode-eager", action="store_true",
                     help="decode steps launch by launch instead of graph replays (for kernel traces)")
     ap.add_argument("--no-gemm", action="store_true", help="skip the batched GEMM (config 4) lines")
@@ -801,9 +874,11 @@ def main():
     gemm = gemm_bench(ctx, wpcg, synth, not args.no_cpu_baseline) if "gemm" in sections else None
     cpu_tokens = 0 if args.no_cpu_baseline else args.decode_cpu_tokens
     decode = decode_bench(ctx, wpcg, synth, "decode", args.decode_prompt, args.decode_new, cpu_tokens,
-                          args.decode_eager) if "decode" in sections else None
+                          args.decode_eager, args.decode_exact, not args.no_prefill_timing) \
+        if "decode" in sections else None
     decode_dense = decode_bench(ctx, wpcg, synth, "decode_dense", args.dense_prompt, args.decode_new,
-                                cpu_tokens, args.decode_eager) if "decode_dense" in sections else None
+                                cpu_tokens, args.decode_eager, args.decode_exact, not args.no_prefill_timing) \
+        if "decode_dense" in sections else None
 
     kname = f"k_gemv_exact<{scheme}>" if mode == wpcg.MODE_EXACT else f"k_gemv_fast<{scheme}, 0, 0, 4>"
     rec = {

@@ -328,8 +328,11 @@ int wpcg_safetensors_read_f32(wpcg_safetensors* st, const char* name, float* out
 /* Config::load / Config::from_json_str (wpc-runtime/src/config.rs:85-95)
  * into a model config: required vocab_size, hidden_size,
  * num_hidden_layers, num_attention_heads, num_key_value_heads,
- * intermediate_size, rope_theta, rms_norm_eps; tie_word_embeddings
- * defaults to true; head_dim falls back to hidden_size /
+ * intermediate_size, rope_theta, rms_norm_eps; tie_word_embeddings is
+ * type-checked but does not choose the head: `tied` is 1 for a dense
+ * decoder (qwen3_model.rs:187-206 builds no lm_head, model.rs:545 calls
+ * embed.logits) and 0 for Qwen3-MoE (qwen3_moe_model.rs:337-343 always
+ * loads lm_head.weight); head_dim falls back to hidden_size /
  * num_attention_heads (Config::head_dim, config.rs:59-62). model_type
  * "qwen3_moe" selects the MoE decoder, as wpc-runtime/src/main.rs:73-77
  * does, with the fields of moe_dims (qwen3_moe_model.rs:121-135: each
@@ -358,12 +361,17 @@ struct wpcg_model_config_s {
     uint32_t vocab;
     uint32_t n_experts, top_k, moe_inter;    /* Qwen3-MoE (n_experts > 0)          */
     int32_t norm_topk;                       /* renormalise the top-k weights      */
-    int32_t tied;                            /* logits from the embedding table    */
+    int32_t tied;                            /* logits from the embedding table: 1 */
+                                             /* exactly when n_experts == 0 (the   */
+                                             /* reference's loaders; see below)    */
     uint32_t max_pos;                        /* KV-cache length                    */
     float eps;                               /* RMSNorm epsilon                    */
     double rope_theta;
 };
 typedef struct wpcg_model wpcg_model;
+/* E_UNSUPPORTED when cfg->tied is not (n_experts == 0): the head is the
+ * embedding table for a dense decoder and lm_head for Qwen3-MoE, as the
+ * reference's loaders build them. */
 int wpcg_model_create(wpcg_ctx* ctx, int scheme, const wpcg_model_config* cfg, wpcg_model** out);
 int wpcg_model_destroy(wpcg_model* m);
 /* A tensor by the reference's name: quantized matrices (model.embed_tokens,
@@ -440,8 +448,13 @@ int wpcg_model_generate(wpcg_model* m, const uint32_t* prompt, uint32_t n_prompt
  * decode step's device buffers as the last step left them. which: 0
  * residual, 1 normed (after the final norm; EXACT mode), 2 q (the
  * projection), 3 k and 4 v (the last layer's projections), 5 attention
- * output (EXACT mode; FAST merges it inside o_proj), 7 logits, 9 K cache,
- * 10 V cache ([layer][kv_head][max_pos][head_dim]). */
+ * output (EXACT mode, and FAST dense models, which merge the attention
+ * chunks in a launch of their own; FAST Qwen3-MoE merges them inside
+ * o_proj and leaves this buffer unwritten), 7 logits, 9 K cache, 10 V
+ * cache ([layer][kv_head][max_pos][head_dim]). In FAST dense models whose
+ * down projection defers its K-slices to its readers, the residual (0)
+ * excludes the last layer's deferred slices: the head adds them as it
+ * reads the residual. */
 int wpcg_model_debug_read(wpcg_model* m, int which, float* out, uint64_t n);
 
 /* ---- HIP graphs over the context stream (no reference counterpart) ----

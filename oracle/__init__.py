@@ -323,7 +323,7 @@ def moe_ffn_v4(router_w, experts, x, top_k: int, norm_topk: bool = True,
 class _Cfg(C.Structure):
     _fields_ = [(f, C.c_size_t) for f in ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim",
                                           "inter", "vocab", "n_exp", "top_k", "moe_inter")] + [
-        ("norm_topk", C.c_int), ("tied", C.c_int), ("rope_theta", C.c_double), ("eps", C.c_float)]
+        ("norm_topk", C.c_int), ("rope_theta", C.c_double), ("eps", C.c_float)]
 
 
 class _Layer(C.Structure):
@@ -369,15 +369,16 @@ class Model:
                 lay.down = ptr(p + "mlp.down_proj.weight")
         c = _Cfg(cfg["n_layers"], cfg["hidden"], cfg["n_heads"], cfg["n_kv_heads"], cfg["head_dim"],
                  cfg["inter"], cfg["vocab"], cfg["n_experts"], cfg["top_k"], cfg["moe_inter"],
-                 int(cfg["norm_topk"]), int(cfg["tied"]), float(cfg["rope_theta"]), float(cfg["eps"]))
+                 int(cfg["norm_topk"]), float(cfg["rope_theta"]), float(cfg["eps"]))
         self.model = _Model(c, ptr("model.embed_tokens.weight"), ptr("lm_head.weight"),
                             ptr("model.norm.weight"), C.cast(self.layers, C.c_void_p))
         self.cache = lib().or_kv_cache_new(C.byref(self.model.cfg), max_pos)
 
-    def forward_token(self, token: int) -> np.ndarray:
+    def forward_token(self, token: int, threads: int | None = None) -> np.ndarray:
+        """One step; `threads` overrides the model's thread count for this call."""
         logits = np.empty(self.cfg["vocab"], np.float32)
         rc = lib().or_forward_token_v4(C.byref(self.model), token, self.cache, logits, self.kernel,
-                                       self.threads)
+                                       self.threads if threads is None else threads)
         assert rc == 0, rc
         return logits
 

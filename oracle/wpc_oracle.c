@@ -22,6 +22,9 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+#ifdef OR_POOL_STALL_US
+#include <unistd.h>
+#endif
 
 #if defined(__x86_64__)
 #include <immintrin.h>
@@ -499,16 +502,23 @@ static void* pool_worker(void* arg)
     pthread_mutex_unlock(&g_pool.mu);
     for (;;) {
         for (int i = 0; i < POOL_SPIN && atomic_load(&g_pool.gen) == seen; i++) cpu_pause();
-        if (atomic_load(&g_pool.gen) == seen) {
-            pthread_mutex_lock(&g_pool.mu);
-            while (atomic_load(&g_pool.gen) == seen) pthread_cond_wait(&g_pool.cv_job, &g_pool.mu);
-            pthread_mutex_unlock(&g_pool.mu);
-        }
-        /* job and want are stored before the generation's increment, and no
-         * new job starts before this one's pending count reaches zero */
+        /* The generation, `want` and the job are read together under the
+         * lock the caller holds while it publishes all three. Read without
+         * it, a worker that sits a job out could read the generation, stall,
+         * and then read the next call's `want` and job: it would run that
+         * job under the old generation and, seeing the new one on its next
+         * loop, run it a second time, counting `pending` down twice. A
+         * worker counted in a job always sees that job's generation: no new
+         * job is published before `pending` reaches zero. */
+        pthread_mutex_lock(&g_pool.mu);
+        while (atomic_load(&g_pool.gen) == seen) pthread_cond_wait(&g_pool.cv_job, &g_pool.mu);
         seen = atomic_load(&g_pool.gen);
+#ifdef OR_POOL_STALL_US /* stress builds only: widen the window between the reads */
+        usleep(OR_POOL_STALL_US);
+#endif
         const int take = id < atomic_load(&g_pool.want);
         par_job* j = atomic_load(&g_pool.job);
+        pthread_mutex_unlock(&g_pool.mu);
         if (!take) continue;
         par_worker(j);
         if (atomic_fetch_sub(&g_pool.pending, 1) == 1) {
@@ -810,8 +820,11 @@ void or_kv_cache_free(or_kv_cache* c)
 size_t or_kv_cache_len(const or_kv_cache* c) { return c->len; }
 
 /* Model::forward_token (model.rs:419-547) when cfg.n_exp == 0 (dense Qwen3:
- * q_norm/k_norm present, tied logits through embed.logits), and
- * Qwen3MoeModel::forward_token (qwen3_moe_model.rs:406-542) otherwise. */
+ * q_norm/k_norm present, logits through embed.logits, model.rs:545, whatever
+ * the checkpoint's tie_word_embeddings: qwen3_model.rs:187-206 builds no
+ * lm_head), and Qwen3MoeModel::forward_token (qwen3_moe_model.rs:406-542)
+ * otherwise, whose logits always come from lm_head (:337-343, :540).
+ * Returns -1 for a MoE model without lm_head. */
 int or_forward_token_v4(const or_model_v4* m, uint32_t token, or_kv_cache* cache,
                         float* logits, int kernel, int threads)
 {
@@ -819,6 +832,8 @@ int or_forward_token_v4(const or_model_v4* m, uint32_t token, or_kv_cache* cache
     size_t h = cfg->hidden, hd = cfg->head_dim, nh = cfg->n_heads, nkv = cfg->n_kv_heads;
     size_t n_rep = nh / nkv, pos = cache->len;
     if (pos >= cache->max_pos || token >= cfg->vocab) return -1;
+    const uint8_t* head = cfg->n_exp ? m->lm_head : m->embed;
+    if (!head) return -1;
     float eps = cfg->eps;
     size_t qd = nh * hd, kvd = nkv * hd;
     size_t inter = cfg->n_exp ? cfg->moe_inter : cfg->inter;
@@ -897,7 +912,6 @@ int or_forward_token_v4(const or_model_v4* m, uint32_t token, or_kv_cache* cache
     }
     cache->len += 1;
     or_rms_norm(residual, m->final_norm, h, eps, normed);
-    const uint8_t* head = (cfg->tied || !m->lm_head) ? m->embed : m->lm_head;
     or_linear_v4_matvec(head, cfg->vocab, h, normed, NULL, logits, kernel, threads);
 
     free(residual); free(normed); free(q); free(k); free(v); free(tmp); free(attn);

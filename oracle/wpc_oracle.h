@@ -127,7 +127,6 @@ typedef struct {
     size_t n_layers, hidden, n_heads, n_kv_heads, head_dim, inter, vocab;
     size_t n_exp, top_k, moe_inter; /* n_exp == 0 -> dense SwiGLU */
     int norm_topk;
-    int tied; /* 1: logits from the embedding table (dense Qwen3) */
     double rope_theta;
     float eps;
 } or_model_cfg;
@@ -146,7 +145,7 @@ typedef struct {
 typedef struct {
     or_model_cfg cfg;
     const uint8_t* embed;   /* [vocab, hidden] v4 */
-    const uint8_t* lm_head; /* [vocab, hidden] v4, NULL when tied */
+    const uint8_t* lm_head; /* [vocab, hidden] v4: the MoE head; a dense model ignores it */
     const float* final_norm;
     const or_layer_v4* layers;
 } or_model_v4;

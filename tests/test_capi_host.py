@@ -199,3 +199,60 @@ def test_fast_split_plan_never_makes_an_empty_slice():
     with pytest.raises(wpcg.WpcgError) as e:
         wpcg.plan_kslices(4, 100)
     assert e.value.code == wpcg.E_SHAPE
+
+
+def test_model_create_refuses_a_head_the_reference_never_builds():
+    """wpcg_model_create checks the head before it needs a device: `tied`
+    must be 1 for a dense decoder (the reference's dense loader builds no
+    lm_head and always calls embed.logits: qwen3_model.rs:187-206,
+    model.rs:545) and 0 for Qwen3-MoE (lm_head always: qwen3_moe_model.rs:
+    337-343). Either mismatch is E_UNSUPPORTED; the consistent configs pass
+    that check and fail only on the missing context (E_ARG)."""
+    base = dict(n_layers=1, hidden=128, n_heads=2, n_kv_heads=1, head_dim=64, inter=256, vocab=64,
+                n_experts=0, top_k=0, moe_inter=0, norm_topk=1, tied=1, max_pos=16, eps=1e-6,
+                rope_theta=1e6)
+    moe = dict(base, inter=0, n_experts=4, top_k=2, moe_inter=128, tied=0)
+    h = C.c_void_p()
+    for cfg, want in ((base, wpcg.E_ARG), (dict(base, tied=0), wpcg.E_UNSUPPORTED),
+                      (moe, wpcg.E_ARG), (dict(moe, tied=1), wpcg.E_UNSUPPORTED)):
+        c = wpcg.ModelConfig(**cfg)
+        rc = wpcg.lib.wpcg_model_create(None, 4, C.byref(c), C.byref(h))
+        assert rc == want, (cfg["n_experts"], cfg["tied"], rc, wpcg.last_error())
+        if want == wpcg.E_UNSUPPORTED:
+            assert "logits" in wpcg.last_error()
+
+
+def test_deferred_split_shape_check():
+    """The FAST launcher refuses a deferred K-split (slices k >= 1 written to
+    a vector each, added by the readers) of more than three slices: readers
+    add at most two deferred vectors and a model's deferral buffer holds two,
+    so a fourth slice would write past it. Compiled from the library's own
+    internal header with the host compiler; no GPU."""
+    import shutil
+    import tempfile
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("no host C++ compiler")
+    src = r'''
+#include "wpcg_internal.hpp"
+#include <cstdio>
+int main() {
+    int bad = 0;
+    for (int kg = 0; kg <= 8; kg++)
+        for (int routed = 0; routed <= 1; routed++) {
+            const bool want = kg >= 2 && kg <= 3 && !routed;
+            if (wpcg::deferred_split_ok(kg, routed != 0) != want) { std::printf("kg %d routed %d\n", kg, routed); bad++; }
+        }
+    return bad;
+}
+'''
+    csrc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "wpc-engine_amd", "csrc")
+    with tempfile.TemporaryDirectory() as d:
+        cpp, exe = os.path.join(d, "t.cpp"), os.path.join(d, "t")
+        with open(cpp, "w") as f:
+            f.write(src)
+        r = subprocess.run([gxx, "-std=c++17", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", "-I", csrc,
+                            cpp, "-o", exe], capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr[-2000:]
+        r = subprocess.run([exe], capture_output=True, text=True)
+        assert r.returncode == 0, r.stdout

@@ -232,19 +232,36 @@ def test_decode_errors(ctx):
     m.close()
 
 
-@pytest.mark.parametrize("name,cfg,scheme,dtype,shards,seed", [("dense-v4-bf16", DENSE, 4, "BF16", 1, 121),
-                                                               ("dense-v3-bf16-sharded", DENSE, 3, "BF16", 2, 131),
-                                                               ("moe-v4-f16-sharded", MOE, 4, "F16", 3, 222)])
-def test_model_loads_from_checkpoint(ctx, tmp_path, name, cfg, scheme, dtype, shards, seed):
+@pytest.mark.parametrize("name,cfg,scheme,dtype,shards,seed,tie,lm_head", [
+    ("dense-v4-bf16", DENSE, 4, "BF16", 1, 121, "auto", None),
+    ("dense-v3-bf16-sharded", DENSE, 3, "BF16", 2, 131, "auto", None),
+    ("moe-v4-f16-sharded", MOE, 4, "F16", 3, 222, "auto", None),
+    ("dense-v4-untied-with-lm_head", DENSE, 4, "BF16", 1, 141, False, True),
+    ("moe-v4-no-tie-key", MOE, 4, "F32", 1, 242, None, None),
+    ("moe-v4-tie-true", MOE, 4, "BF16", 2, 252, True, None)])
+def test_model_loads_from_checkpoint(ctx, tmp_path, name, cfg, scheme, dtype, shards, seed, tie, lm_head):
     """load_wpc_v{3,4} end to end: config.json, the norms and routers from
     safetensors (non-unit norms stored in `dtype`), the matrices from the
     artifact. v4: EXACT logits bit-identical to the oracle's decode step on
     the tensors as the checkpoint holds them. v3 (the oracle's decode step
     is v4 only): bit-identical to the same model given every tensor through
-    set_tensor, i.e. the loader places every tensor where set_tensor does."""
+    set_tensor, i.e. the loader places every tensor where set_tensor does.
+    The head is the reference's whatever config.json's tie_word_embeddings
+    says: a dense checkpoint declaring itself untied and holding an
+    lm_head.weight still decodes through the embedding table
+    (qwen3_model.rs:187-206, model.rs:545), and a MoE config with the key
+    absent (serde's default true) or true still uses lm_head.weight
+    (qwen3_moe_model.rs:337-343); the oracle chooses the same way, pinned
+    against transformers on the CPU."""
     print(f"[gpu] checkpoint load {name}", flush=True)
     tensors = synth.write_checkpoint(str(tmp_path / "model"), str(tmp_path / "wpc"), cfg, scheme, seed,
-                                     wpcg.encode, dtype, shards)
+                                     wpcg.encode, dtype, shards, tie_word_embeddings=tie, lm_head=lm_head)
+    if lm_head and not cfg["n_experts"]:
+        assert "lm_head.weight" in tensors  # in the artifact, never read
+    import json
+    with open(tmp_path / "model" / "config.json") as f:
+        declared = json.load(f).get("tie_word_embeddings")
+    assert declared == (None if tie is None else (not cfg["n_experts"]) if tie == "auto" else tie)
     m = wpcg.Model.load_wpc(ctx, scheme, tmp_path / "model", tmp_path / "wpc", cfg["max_pos"])
     assert m.cfg.as_dict()["n_experts"] == cfg["n_experts"]
     if scheme == 4:

@@ -17,13 +17,25 @@ oracle's restatement of matvec_v{3,4}_fused) and the float64 truth y_true:
     error measures fp32 summation order alone, and the reference kernel
     itself (the oracle's AVX2 restatement) is 1.45e-3 from float64 on the v3
     q_proj shape with the literal 1e-6 floor, 6.2e-4 with a floor of 0.1% of
-    the rms output. The same figure against the reference kernel's result,
-    and the reference kernel's own, are printed beside it.
+    the rms output.
+and against the reference kernel's own result y_ref (the oracle's AVX2
+restatement, the same intrinsics in the same order), the north star's
+"within 1e-4 max relative error with fp32 accumulation":
+  * |y - y_ref| <= 2e-6 * the row's term magnitude: the first bound plus the
+    reference kernel's own fp32 accumulation error (measured <= 3.4e-8 of
+    the term magnitude over every shape below);
+  * max over EVERY row of |y - y_ref| / max(|y_ref|, floor) < 1e-4 with the
+    floor 5% of the rms output. Both kernels accumulate in fp32, in
+    different orders; at a 1% floor the reference kernel is itself 2.0e-4
+    from float64 on these shapes (2560x9728 v4), so no other summation
+    order can be held within 1e-4 of it there. At 5% the reference's own
+    distance from float64 is 4.3e-5, leaving FAST the rest.
 A wrong code, lane or block index moves a row by ~1% of its term magnitude,
 four orders of magnitude above the first bound.
 """
 REL_TOL = 1e-4
 FLOOR_OF_RMS = 1e-2
+REF_FLOOR_OF_RMS = 5e-2
 import numpy as np
 import pytest
 
@@ -79,13 +91,20 @@ def check_fast(y, scheme, blocks, rows, cols, x, what, bias=None):
     assert np.all(err <= 1e-6 * mag), (
         f"{what}: row {worst} |y-y_true|={err[worst]:.3e} > 1e-6*{mag[worst]:.3e}")
     floor = FLOOR_OF_RMS * np.sqrt(np.mean(y_true ** 2))
+    ref_floor = REF_FLOOR_OF_RMS * np.sqrt(np.mean(y_ref ** 2))
     yd = y.astype(np.float64)
     rel = float(np.max(err / np.maximum(np.abs(y_true), floor)))
-    rel_ref = float(np.max(np.abs(yd - y_ref) / np.maximum(np.abs(y_ref), floor)))
-    ref_own = float(np.max(np.abs(y_ref - y_true) / np.maximum(np.abs(y_true), floor)))
-    print(f"[gpu] {what}: max rel error over all {rows} rows (floor {floor:.2e}): {rel:.2e} vs float64, "
-          f"{rel_ref:.2e} vs the reference kernel (whose own is {ref_own:.2e})", flush=True)
+    err_ref = np.abs(yd - y_ref)
+    rel_ref = float(np.max(err_ref / np.maximum(np.abs(y_ref), ref_floor)))
+    ref_own = float(np.max(np.abs(y_ref - y_true) / np.maximum(np.abs(y_true), ref_floor)))
+    print(f"[gpu] {what}: max rel error over all {rows} rows: {rel:.2e} vs float64 (floor {floor:.2e}); "
+          f"{rel_ref:.2e} vs the reference kernel (floor {ref_floor:.2e}; the reference's own vs float64 "
+          f"{ref_own:.2e})", flush=True)
     assert rel < REL_TOL, f"{what}: max relative error {rel:.3e} vs float64 (floor {floor:.2e})"
+    worst_r = int(np.argmax(err_ref / mag))
+    assert np.all(err_ref <= 2e-6 * mag), (
+        f"{what}: row {worst_r} |y-y_ref|={err_ref[worst_r]:.3e} > 2e-6*{mag[worst_r]:.3e}")
+    assert rel_ref < REL_TOL, f"{what}: max relative error {rel_ref:.3e} vs the reference kernel"
     return rel, float((err / mag).max())
 
 

@@ -39,7 +39,7 @@ import oracle as O
 from wpcg import synth
 
 # |oracle - HF| <= LOGIT_TOL * (max - min of HF's logits) at every step.
-# Measured worst: 3.3e-7 (dense, tied), 4.1e-7 (dense, untied), 3.8e-7 (MoE):
+# Measured worst: 3.3e-7 (dense), 3.8e-7 (MoE):
 # the oracle is fp32 throughout.
 LOGIT_TOL = 1e-5
 
@@ -65,9 +65,10 @@ def dequant_v4(blocks, rows, cols):
     return (zp + codes * sc).astype(np.float32).reshape(rows, cols)
 
 
-def _tensors(cfg, seed):
-    """The synthetic model's tensors, with random non-unit norm weights."""
-    t = dict(synth.model_tensors(cfg, 4, seed, lambda s, w: O.encode_tensor_v4(w)))
+def _tensors(cfg, seed, lm_head=None):
+    """The synthetic model's tensors, with random non-unit norm weights
+    (lm_head: as synth.model_tensors takes it)."""
+    t = dict(synth.model_tensors(cfg, 4, seed, lambda s, w: O.encode_tensor_v4(w), lm_head=lm_head))
     rng = np.random.default_rng(seed + 1)
     for n in list(t):
         if n.endswith("norm.weight") or n.endswith("layernorm.weight"):
@@ -89,13 +90,17 @@ def _shape(cfg, name):
 
 
 def hf_model(cfg, tensors):
-    """A float64 transformers model holding the oracle's weights."""
+    """A float64 transformers model holding the oracle's weights, with the
+    head the reference's loaders take: tied to the embedding for a dense
+    model (an lm_head.weight among the tensors is not loaded, as
+    qwen3_model.rs:187-206 never reads it), its own lm_head for MoE."""
     torch, tf = _hf()
+    tie = not cfg["n_experts"]
     common = dict(vocab_size=cfg["vocab"], hidden_size=cfg["hidden"],
                   num_hidden_layers=cfg["n_layers"], num_attention_heads=cfg["n_heads"],
                   num_key_value_heads=cfg["n_kv_heads"], head_dim=cfg["head_dim"],
                   rope_theta=cfg["rope_theta"], rms_norm_eps=cfg["eps"],
-                  tie_word_embeddings=bool(cfg["tied"]), max_position_embeddings=4096,
+                  tie_word_embeddings=tie, max_position_embeddings=4096,
                   attention_bias=False, hidden_act="silu", attn_implementation="eager")
     if cfg["n_experts"]:
         hc = tf.Qwen3MoeConfig(intermediate_size=cfg["moe_inter"], moe_intermediate_size=cfg["moe_inter"],
@@ -127,11 +132,11 @@ def hf_model(cfg, tensors):
     params = dict(model.named_parameters())
     with torch.no_grad():
         for name, a in sd.items():
-            if name == "lm_head.weight" and cfg["tied"]:
+            if name == "lm_head.weight" and tie:
                 continue
             p = params[name]
             p.copy_(torch.from_numpy(np.asarray(a, np.float64).reshape(tuple(p.shape))))
-        loaded = set(sd) | ({"lm_head.weight"} if cfg["tied"] else set())
+        loaded = set(sd) | ({"lm_head.weight"} if tie else set())
         missing = [n for n in params if n not in loaded]
         assert not missing, missing
     return model
@@ -150,11 +155,16 @@ def _greedy_oracle(cfg, tensors, prompt, n_new):
     return seq, np.stack(logits)
 
 
-@pytest.mark.parametrize("name,cfg,seed", [("dense-tied", DENSE, 41), ("moe", MOE, 42),
-                                           ("dense-untied", dict(DENSE, tied=0), 43)])
-def test_forward_token_matches_transformers(name, cfg, seed):
+@pytest.mark.parametrize("name,cfg,seed,lm_head", [("dense", DENSE, 41, None), ("moe", MOE, 42, None),
+                                                   ("dense-with-lm_head", DENSE, 43, True)])
+def test_forward_token_matches_transformers(name, cfg, seed, lm_head):
+    """dense-with-lm_head: the tensors also hold an lm_head.weight (an untied
+    dense checkpoint such as Qwen3-8B); the reference's dense decoder still
+    takes its logits from the embedding (model.rs:545), and so must the
+    oracle: HF is built tied, so an oracle that read lm_head would differ at
+    the first step."""
     torch, _ = _hf()
-    tensors = _tensors(cfg, seed)
+    tensors = _tensors(cfg, seed, lm_head)
     model = hf_model(cfg, tensors)
     n_prompt, n_new = 8, 64
     prompt = [int(t) for t in np.random.default_rng(seed).integers(0, cfg["vocab"], n_prompt)]

@@ -314,6 +314,22 @@ def test_dense_config_has_no_moe_fields():
     assert c.tied == 1  # default_true
 
 
+@pytest.mark.parametrize("flag", [True, False, None])
+def test_head_follows_the_model_kind_not_tie_word_embeddings(flag):
+    """The reference's loaders never read tie_word_embeddings for the head:
+    dense load_wpc_v4 builds no lm_head and Model::forward_token always calls
+    embed.logits (qwen3_model.rs:187-206, model.rs:545); Qwen3-MoE always
+    loads lm_head.weight (qwen3_moe_model.rs:337-343). So `tied` is 1 for
+    every dense config and 0 for every MoE config, with the key true, false
+    or absent (serde's default_true)."""
+    for text, tied in ((DENSE_JSON, 1), (QWEN3_JSON, 1), (cfg_with(8, 2, True), 0)):
+        j = json.loads(text)
+        j.pop("tie_word_embeddings", None)
+        if flag is not None:
+            j["tie_word_embeddings"] = flag
+        assert wpcg.config_from_json_str(json.dumps(j), 8).tied == tied, (j.get("model_type"), flag)
+
+
 def test_top_k_beyond_expert_count_is_rejected():
     with pytest.raises(wpcg.WpcgError) as e:
         wpcg.config_from_json_str(cfg_with(4, 8, True), 32)
@@ -350,7 +366,8 @@ def test_config_errors_and_load(tmp_path):
             wpcg.config_from_json_str(json.dumps(jj), 8)
     jj = dict(j, tie_word_embeddings=False, head_dim=None, rope_theta=10000)  # an integer is a valid f64
     c = wpcg.config_from_json_str(json.dumps(jj), 8)
-    assert c.tied == 0 and c.head_dim == 2560 // 32 and c.rope_theta == 10000.0
+    assert c.head_dim == 2560 // 32 and c.rope_theta == 10000.0
+    assert c.tied == 1  # dense: the embedding table is the head whatever the flag says
     p = tmp_path / "config.json"
     p.write_text(QWEN3_JSON)
     assert wpcg.config_load(p, 16).as_dict() == wpcg.config_from_json_str(QWEN3_JSON, 16).as_dict()

@@ -130,12 +130,18 @@ void drop_graph(wpcg_model* m)
     m->graph_mode = -1;
 }
 
+// The logits head as the reference's loaders choose it: the dense decoder
+// always the embedding table (model.rs:545, embed.logits), Qwen3-MoE always
+// its own lm_head (qwen3_moe_model.rs:337-343, 540). wpcg_model_create
+// refuses a config whose `tied` disagrees.
+wpcg_linear* logits_head(const wpcg_model* m) { return m->cfg.n_experts ? m->lm_head : m->embed; }
+
 // First missing tensor, or "" when the model is complete.
 std::string missing(const wpcg_model* m)
 {
     const wpcg_model_config& c = m->cfg;
     if (!m->embed) return "model.embed_tokens.weight";
-    if (!c.tied && !m->lm_head) return "lm_head.weight";
+    if (c.n_experts && !m->lm_head) return "lm_head.weight";
     if (!m->final_norm) return "model.norm.weight";
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const Layer& L = m->layers[l];
@@ -183,7 +189,7 @@ bool defer_down(const wpcg_model* m)
 {
     const wpcg_model_config& c = m->cfg;
     if (m->mode != WPCG_MODE_FAST || c.n_experts || !m->part_o || !m->d2) return false;
-    const wpcg_linear* head = c.tied ? m->embed : m->lm_head;
+    const wpcg_linear* head = logits_head(m);
     if (head->plan.kg != 1 || head->m.nb == 0) return false;
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const Layer& L = m->layers[l];
@@ -321,7 +327,7 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
             if (rc) return rc;
         }
     }
-    wpcg_linear* head = c.tied ? m->embed : m->lm_head;
+    wpcg_linear* head = logits_head(m);
     bool fused = fast;
     GemvJob head_job = fast_job(head, m->residual, m->logits, m->final_norm, c.eps, fused);
     head_job.x_add = d2;
@@ -480,7 +486,7 @@ int prefill_run(wpcg_model* m, uint32_t pos0, uint32_t n, uint32_t n_prompt)
         done += len;
     }
     const float* xl = m->pf.x + (size_t)last * c.hidden;
-    wpcg_linear* head = c.tied ? m->embed : m->lm_head;
+    wpcg_linear* head = logits_head(m);
     bool fused = true;
     GemvJob head_job = fast_job(head, xl, m->logits, m->final_norm, c.eps, fused);
     if (fused) {
@@ -512,7 +518,7 @@ int verify_run(wpcg_model* m, uint32_t pos0, uint32_t n)
         m->allocs.push_back(P.vids);
     }
     if (int rc = prefill_pass(m, pos0, n, s)) return rc;
-    wpcg_linear* head = c.tied ? m->embed : m->lm_head;
+    wpcg_linear* head = logits_head(m);
     WPCG_HIP(launch_rms_norm_rows(WPCG_MODE_FAST, P.x, m->final_norm, (int)c.hidden, (int)n, c.eps, P.xn, s));
     WPCG_HIP(launch_gemm_pack_rows(P.xn, (int)n, (int)c.hidden, P.xf, P.xsum, s));
     WPCG_HIP(launch_gemm_packed_rows(head->m, P.xf, P.xsum, (int)n, head->bias, nullptr, P.vlogits, s));
@@ -594,6 +600,11 @@ int wpcg_model_create(wpcg_ctx* ctx, int scheme, const wpcg_model_config* cfg, w
     if (c.hidden % 128 || (c.n_heads * c.head_dim) % 128 || (c.n_experts == 0 && c.inter % 128))
         return fail(WPCG_E_SHAPE, "matrix input sizes must be multiples of 128");
     if (c.n_experts == 0 && !c.inter) return fail(WPCG_E_ARG, "dense model needs intermediate_size");
+    if (c.tied != (c.n_experts == 0 ? 1 : 0))
+        return fail(WPCG_E_UNSUPPORTED, c.n_experts ? "tied = 1 with experts: Qwen3-MoE takes its logits from "
+                                                      "lm_head.weight (qwen3_moe_model.rs:337-343)"
+                                                    : "tied = 0 without experts: the dense decoder takes its "
+                                                      "logits from the embedding table (model.rs:545)");
     if (int rc = check_ctx(ctx)) return rc;
     std::unique_ptr<wpcg_model> m(new (std::nothrow) wpcg_model);
     if (!m) return fail(WPCG_E_NOMEM, "model allocation");
@@ -688,7 +699,12 @@ int wpcg_model_set_tensor(wpcg_model* m, const char* name_c, const void* data, u
     const std::string name(name_c);
     const uint64_t qd = (uint64_t)c.n_heads * c.head_dim, kvd = (uint64_t)c.n_kv_heads * c.head_dim;
     if (name == "model.embed_tokens.weight") return set_linear(m, &m->embed, data, nbytes, c.vocab, c.hidden, name);
-    if (name == "lm_head.weight") return set_linear(m, &m->lm_head, data, nbytes, c.vocab, c.hidden, name);
+    if (name == "lm_head.weight") {
+        // the reference's dense loader never reads lm_head.weight (qwen3_model.rs:187-206)
+        if (!c.n_experts) return fail(WPCG_E_NOTFOUND, "lm_head.weight: the dense decoder takes its logits "
+                                                       "from model.embed_tokens.weight (model.rs:545)");
+        return set_linear(m, &m->lm_head, data, nbytes, c.vocab, c.hidden, name);
+    }
     if (name == "model.norm.weight") return set_dev_f32(m, &m->final_norm, data, nbytes, c.hidden, name);
     const std::string pre = "model.layers.";
     if (name.compare(0, pre.size(), pre) != 0) return fail(WPCG_E_NOTFOUND, "unknown tensor " + name);
@@ -711,7 +727,6 @@ int wpcg_model_set_tensor(wpcg_model* m, const char* name_c, const void* data, u
     if (t == "self_attn.k_proj.weight") return set_linear(m, &L.k, data, nbytes, kvd, c.hidden, name);
     if (t == "self_attn.v_proj.weight") return set_linear(m, &L.v, data, nbytes, kvd, c.hidden, name);
     if (t == "self_attn.o_proj.weight") {
-        if (int rc = set_linear(m, &L.o, data, nbytes, c.hidden, qd, name)) return rc;
         // FAST mode merges the attention's chunk states while o_proj reads its
         // input. When one workgroup per 16-row tile leaves CUs idle even at
         // two K-slices, split K in two: each workgroup then merges only half
@@ -719,8 +734,12 @@ int wpcg_model_set_tensor(wpcg_model* m, const char* name_c, const void* data, u
         // 430, 4 slices 397; Qwen3-4B, 160 tiles: 1 slice 645, 2 slices 582).
         int cus = 0;
         WPCG_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, m->ctx->device));
+        if (int rc = set_linear(m, &L.o, data, nbytes, c.hidden, qd, name)) return rc;
         const uint64_t tiles = pad_rows(c.hidden) / TILE_ROWS;
-        return 2 * tiles <= (uint64_t)cus ? wpcg_linear_set_kslices(L.o, 2) : WPCG_OK;
+        // The split is a speed choice: when it cannot be planned the linear
+        // keeps its one-slice plan (a valid state) and the tensor counts as set.
+        if (2 * tiles <= (uint64_t)cus) (void)wpcg_linear_set_kslices(L.o, 2);
+        return WPCG_OK;
     }
     if (c.n_experts == 0) {
         if (t == "mlp.gate_proj.weight") return set_linear(m, &L.gate, data, nbytes, c.inter, c.hidden, name);
@@ -768,7 +787,7 @@ int wpcg_model_load_artifact(wpcg_model* m, wpcg_artifact* a)
     if (!m || !a) return fail(WPCG_E_ARG, "null argument");
     if (a->scheme != m->scheme) return fail(WPCG_E_ARG, "artifact scheme differs from the model's");
     std::vector<std::string> names = {"model.embed_tokens.weight"};
-    if (!m->cfg.tied) names.push_back("lm_head.weight");
+    if (m->cfg.n_experts) names.push_back("lm_head.weight");
     for (uint32_t l = 0; l < m->cfg.n_layers; l++) {
         const std::string p = "model.layers." + std::to_string(l) + ".";
         for (const char* t : {"self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",

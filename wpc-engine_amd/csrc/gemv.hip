@@ -1294,8 +1294,8 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         // routing reads at most ROUTE_MAXN scores into MAX_JOBS slots
         if (J.xform == XF_NORM && (P.kg != 1 || !J.nw)) return hipErrorInvalidValue;
         if (J.xform == XF_SILU && !J.x2) return hipErrorInvalidValue;
-        // the deferred split: two slices and no routing; x_add with the norm; bias2 with a bias
-        if (J.y2 && (P.kg < 2 || J.routed)) return hipErrorInvalidValue;
+        // the deferred split: 2 or 3 slices, no routing; x_add with the norm; bias2 with a bias
+        if (J.y2 && !deferred_split_ok(P.kg, J.routed != 0)) return hipErrorInvalidValue;
         if ((J.x_add && J.xform != XF_NORM) || (J.bias2 && !J.bias)) return hipErrorInvalidValue;
         if (J.n_xa < 1 || J.n_xa > 2 || J.n_b2 < 1 || J.n_b2 > 2) return hipErrorInvalidValue;
         if (J.amax && (P.kg != 1 || J.routed)) return hipErrorInvalidValue;

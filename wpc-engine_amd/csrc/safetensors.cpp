@@ -279,11 +279,11 @@ int parse_config(const char* text, size_t n, uint32_t max_pos, wpcg_model_config
         if (int rc = need_size(root, key, *dst)) return rc;
     if (int rc = need_f64(root, "rope_theta", theta)) return rc;
     if (int rc = need_f64(root, "rms_norm_eps", eps)) return rc;
-    bool tied = true;  // #[serde(default = "default_true")]
-    if (const JsonValue* t = root.get("tie_word_embeddings")) {
+    // Config::tie_word_embeddings is parsed (a non-boolean fails as serde
+    // fails) but never decides the head: the reference's loaders choose it by
+    // model kind (below).
+    if (const JsonValue* t = root.get("tie_word_embeddings"))
         if (t->kind != JsonValue::BOOL) return cfg_fail("`tie_word_embeddings` is not a boolean");
-        tied = t->b;
-    }
     for (const char* key : {"eos_token_id", "bos_token_id"}) {  // Option<u32>: type-checked only
         bool has;
         uint64_t v;
@@ -311,7 +311,6 @@ int parse_config(const char* text, size_t n, uint32_t max_pos, wpcg_model_config
     c.head_dim = (uint32_t)(has_hd ? hd : hidden / heads);  // Config::head_dim
     c.inter = (uint32_t)inter;
     c.vocab = (uint32_t)vocab;
-    c.tied = tied ? 1 : 0;
     c.eps = (float)eps;
     c.rope_theta = theta;
     c.max_pos = max_pos;
@@ -330,6 +329,12 @@ int parse_config(const char* text, size_t n, uint32_t max_pos, wpcg_model_config
     } else {
         c.norm_topk = 1;
     }
+    // The logits head as the reference's loaders take it, whatever
+    // tie_word_embeddings says: the dense decoder always multiplies by the
+    // embedding table (qwen3_model.rs:187-206 builds no lm_head; model.rs:545
+    // calls embed.logits), Qwen3-MoE always by lm_head.weight
+    // (qwen3_moe_model.rs:337-343, 540).
+    c.tied = c.n_experts == 0 ? 1 : 0;
     for (uint64_t v : {layers, hidden, heads, kv_heads, inter, vocab, has_hd ? hd : 0, has_ne ? ne : 0,
                        has_k ? k : 0, has_mi ? mi : 0})
         if (v > 0xFFFFFFFFull) return cfg_fail("a size does not fit 32 bits");

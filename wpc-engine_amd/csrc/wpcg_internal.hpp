@@ -140,6 +140,12 @@ struct GemvJob {
     // the first largest of its output rows (see launch_argmax_keys_next)
     uint64_t* amax = nullptr;
 };
+// The deferred K-split's shape: its readers add at most two deferred
+// vectors (n_xa, n_b2 <= 2) and a model's deferral buffer holds two, so a
+// deferred job has 2 or 3 K-slices, and a routed job (one slice per slot)
+// cannot defer.
+inline bool deferred_split_ok(int kg, bool routed) { return kg >= 2 && kg <= 3 && !routed; }
+
 // FAST mode: a workgroup computes fast_tiles_per_wg 16-row tiles over a
 // K-slice of at most fast_max_slice blocks (the slice's x digits live in LDS).
 constexpr int FAST_MAXBK = 64;

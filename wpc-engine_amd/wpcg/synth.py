@@ -290,7 +290,8 @@ def permute_rows(blocks, rows: int, cols: int, scheme: int, perm) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(blocks, np.uint8).reshape(rows, row_bytes)[perm]).ravel()
 
 
-def model_tensors(cfg, scheme: int, seed: int, encode, std: float = 0.02, derive_layers: bool = False):
+def model_tensors(cfg, scheme: int, seed: int, encode, std: float = 0.02, derive_layers: bool = False,
+                  lm_head: bool | None = None):
     """Seeded synthetic weights of a dense Qwen3 / Qwen3-MoE decoder, by the
     reference's tensor names: every matrix ~N(0, std) then encoded with
     `encode(scheme, w)` (the artifact compiler's encoder), norms 1.0, the
@@ -300,7 +301,10 @@ def model_tensors(cfg, scheme: int, seed: int, encode, std: float = 0.02, derive
     of layer 0's (one permutation per layer and matrix), so each layer holds
     distinct weights of the same distribution without encoding every layer
     on the host (15 GB of experts for the Qwen3-30B-A3B shape). Routers are
-    drawn fresh for every layer.
+    drawn fresh for every layer. lm_head.weight is yielded for a MoE model
+    (its head) and, with lm_head=True, for a dense one too (a tensor an
+    untied dense checkpoint holds and the reference's dense loader never
+    reads).
     Yields (name, array)."""
     c = cfg if isinstance(cfg, dict) else cfg.as_dict()
     rng = np.random.default_rng(seed)
@@ -312,7 +316,7 @@ def model_tensors(cfg, scheme: int, seed: int, encode, std: float = 0.02, derive
 
     ones_h = np.ones(H, np.float32)
     yield "model.embed_tokens.weight", mat(V, H)
-    if not c["tied"]:
+    if c["n_experts"] if lm_head is None else lm_head:
         yield "lm_head.weight", mat(V, H)
     yield "model.norm.weight", ones_h
     E = c["n_experts"]
@@ -403,16 +407,23 @@ def widened(dtype: str, a) -> np.ndarray:
     return a.copy()
 
 
-def config_json(cfg) -> dict:
+def config_json(cfg, tie_word_embeddings="auto") -> dict:
     """config.json fields of a wpcg.ModelConfig (or dict of its fields), in
-    the Hugging Face names the reference's Config reads."""
+    the Hugging Face names the reference's Config reads.
+    tie_word_embeddings: "auto" writes what checkpoints of the kind declare
+    (dense Qwen3-4B true, Qwen3-MoE false), True/False that value, None
+    leaves the key out. It never changes the head the reference's loaders
+    take (the embedding table for dense, lm_head for MoE)."""
     c = cfg if isinstance(cfg, dict) else cfg.as_dict()
     j = {"model_type": "qwen3_moe" if c["n_experts"] else "qwen3",
          "vocab_size": c["vocab"], "hidden_size": c["hidden"], "num_hidden_layers": c["n_layers"],
          "num_attention_heads": c["n_heads"], "num_key_value_heads": c["n_kv_heads"],
          "intermediate_size": c["inter"] or 6144, "head_dim": c["head_dim"],
-         "rope_theta": float(c["rope_theta"]), "rms_norm_eps": float(c["eps"]),
-         "tie_word_embeddings": bool(c["tied"])}
+         "rope_theta": float(c["rope_theta"]), "rms_norm_eps": float(c["eps"])}
+    if tie_word_embeddings == "auto":
+        j["tie_word_embeddings"] = not c["n_experts"]
+    elif tie_word_embeddings is not None:
+        j["tie_word_embeddings"] = bool(tie_word_embeddings)
     if c["n_experts"]:
         j.update(num_experts=c["n_experts"], num_experts_per_tok=c["top_k"],
                  moe_intermediate_size=c["moe_inter"], norm_topk_prob=bool(c["norm_topk"]))
@@ -420,18 +431,21 @@ def config_json(cfg) -> dict:
 
 
 def write_checkpoint(model_dir: str, wpc_dir: str, cfg, scheme: int, seed: int, encode,
-                     dtype: str = "BF16", shards: int = 1) -> dict:
+                     dtype: str = "BF16", shards: int = 1, tie_word_embeddings="auto",
+                     lm_head: bool | None = None) -> dict:
     """A model directory as the reference loads it: config.json plus the fp32
     tensors (norms ~1 + N(0, 0.1), routers ~N(0, 0.02)) in safetensors of
     `dtype`, one model.safetensors or `shards` files with an index; and the
-    quantized matrices in a WPC artifact under wpc_dir. Returns every tensor
-    as the decoder sees it (fp32 tensors widened from their storage)."""
+    quantized matrices in a WPC artifact under wpc_dir. tie_word_embeddings
+    goes to config.json as config_json writes it; lm_head as model_tensors
+    takes it. Returns every tensor as the decoder sees it (fp32 tensors
+    widened from their storage)."""
     os.makedirs(model_dir, exist_ok=True)
     with open(os.path.join(model_dir, "config.json"), "w") as f:
-        json.dump(config_json(cfg), f, indent=2)
+        json.dump(config_json(cfg, tie_word_embeddings), f, indent=2)
     rng = np.random.default_rng(seed + 7)
     tensors, dense, quant = {}, [], []
-    for name, arr in model_tensors(cfg, scheme, seed, encode):
+    for name, arr in model_tensors(cfg, scheme, seed, encode, lm_head=lm_head):
         if arr.dtype == np.uint8:
             quant.append((name, None, arr))
             tensors[name] = arr
