@@ -540,14 +540,14 @@ def gemv_series_us(ctx, wpcg, lins, xd, yd, reps=8):
     return us
 
 
-def per_shape_bench(ctx, wpcg, scheme, shapes, blocks, xs, min_bytes):
+def per_shape_bench(ctx, wpcg, scheme, shapes, blocks, xs, min_bytes, fast_kernel=0):
     """Each config-1 GEMV alone (the step's own matrices and x): FAST,
     HBM-cold (rotated over >= min_bytes of device copies of that matrix),
     launch after launch."""
     out = {}
     for i, (name, r, c) in enumerate(shapes):
         base = wpcg.WpcLinear.from_blocks(ctx, scheme, blocks[i], r, c)
-        base.set_mode(wpcg.MODE_FAST)
+        base.set_mode(wpcg.MODE_FAST).set_fast_kernel(fast_kernel)
         n = max(1, -(-int(min_bytes) // base.device_bytes()))
         lins = [base] + [base.clone() for _ in range(n - 1)]
         xd = ctx.upload(xs[c])
@@ -564,7 +564,7 @@ def per_shape_bench(ctx, wpcg, scheme, shapes, blocks, xs, min_bytes):
     return out
 
 
-def cfg0_bench(ctx, wpcg, synth, min_bytes, cpu_budget):
+def cfg0_bench(ctx, wpcg, synth, min_bytes, cpu_budget, fast_kernel=0):
     """Benchmark config 0: the v4 GEMV 4864x896 (Qwen2.5-0.5B MLP up-proj),
     FAST, fp32 x. HBM-cold: launch after launch over >= min_bytes of device
     copies (each launch's weights come from HBM); cache-hot: the same launches
@@ -573,6 +573,7 @@ def cfg0_bench(ctx, wpcg, synth, min_bytes, cpu_budget):
     blocks = synth.wpc_blocks(4, rows, cols, matrix_id=0)  # the configs' PRNG (synth.WPC_SEED)
     x = synth.wpc_x(cols)
     base = wpcg.WpcLinear.from_blocks(ctx, 4, blocks, rows, cols).set_mode(wpcg.MODE_FAST)
+    base.set_fast_kernel(fast_kernel)
     n = max(1, -(-int(min_bytes) // base.device_bytes()))
     lins = [base] + [base.clone() for _ in range(n - 1)]
     xd = ctx.upload(x)
@@ -671,6 +672,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--scheme", type=int, default=3, choices=(3, 4))
     ap.add_argument("--mode", default="fast", choices=("exact", "fast"))
+    ap.add_argument("--fast-kernel", default="mfma", choices=("mfma", "valu"),
+                    help="FAST GEMV kernel of the config-1 step, per-shape and config-0 lines: matrix cores "
+                         "with int8 x digits (mfma) or fp32 on the vector ALU (valu)")
     ap.add_argument("--min-bytes", type=float, default=1.0e9,
                     help="rotated working set, bytes (>= 1 GB defeats the 256 MB MALL)")
     ap.add_argument("--cpu-seconds", type=float, default=6.0)
@@ -747,7 +751,8 @@ def main():
     xs = {c: synth.wpc_x(c) for c in sorted({c for _, _, c in QWEN3_4B})}
 
     ctx = wpcg.Context(0)
-    base = [wpcg.WpcLinear.from_blocks(ctx, scheme, b, r, c)
+    fast_kernel = wpcg.FAST_KERNEL_VALU if args.fast_kernel == "valu" else wpcg.FAST_KERNEL_MFMA
+    base = [wpcg.WpcLinear.from_blocks(ctx, scheme, b, r, c).set_fast_kernel(fast_kernel)
             for b, (_, r, c) in zip(blocks, QWEN3_4B)]
     step_bytes = sum(gemv_bytes(r, c, scheme) for _, r, c in QWEN3_4B)
     weight_bytes = sum(l.device_bytes() for l in base)
@@ -867,9 +872,9 @@ def main():
         for l in lst:
             l.close()
     cpu_budget = 0 if args.no_cpu_baseline else args.cpu_seconds / 2
-    per_shape = per_shape_bench(ctx, wpcg, scheme, QWEN3_4B, blocks, xs, args.min_bytes) \
+    per_shape = per_shape_bench(ctx, wpcg, scheme, QWEN3_4B, blocks, xs, args.min_bytes, fast_kernel) \
         if "per_shape" in sections else None
-    cfg0 = cfg0_bench(ctx, wpcg, synth, args.min_bytes, cpu_budget) if "cfg0" in sections else None
+    cfg0 = cfg0_bench(ctx, wpcg, synth, args.min_bytes, cpu_budget, fast_kernel) if "cfg0" in sections else None
     large = large_gemv_bench(ctx, wpcg, synth) if "large_gemv" in sections else None
     gemm = gemm_bench(ctx, wpcg, synth, not args.no_cpu_baseline) if "gemm" in sections else None
     cpu_tokens = 0 if args.no_cpu_baseline else args.decode_cpu_tokens
@@ -880,7 +885,8 @@ def main():
                                 cpu_tokens, args.decode_eager, args.decode_exact, not args.no_prefill_timing) \
         if "decode_dense" in sections else None
 
-    kname = f"k_gemv_exact<{scheme}>" if mode == wpcg.MODE_EXACT else f"k_gemv_fast<{scheme}, 0, 0, 4>"
+    kname = f"k_gemv_exact<{scheme}>" if mode == wpcg.MODE_EXACT else \
+        f"k_gemv_valu<{scheme}>" if fast_kernel == wpcg.FAST_KERNEL_VALU else f"k_gemv_fast<{scheme}, 0, 0, 4>"
     rec = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -902,6 +908,7 @@ def main():
                          f"copies"),
             "scheme": f"v{scheme}",
             "mode": args.mode,
+            "fast_kernel": args.fast_kernel,
             "bytes_per_step": step_bytes,
             "pct_of_peak": round(100 * value / PEAK_GBPS, 2),
             "launches_per_step": n_launch // steps,

@@ -140,6 +140,18 @@ int wpcg_linear_set_mode(wpcg_linear* lin, int mode);
  * counterpart (a tuning knob). */
 int wpcg_linear_set_kslices(wpcg_linear* lin, int kslices);
 int wpcg_linear_kslices(wpcg_linear* lin, int* kslices);
+/* Which FAST kernel a plain GEMV of this linear runs (no reference
+ * counterpart; the reference's AVX2 row kernel is the one restated):
+ * WPCG_FAST_KERNEL_MFMA (the default) puts the block dot products on the
+ * matrix cores with x as four int8 digits; WPCG_FAST_KERNEL_VALU computes
+ * them on the vector ALU in fp32 with x read as fp32 (codes unpacked by
+ * shift/mask in registers). Both are held to the same bounds against the
+ * reference kernel. Launches with an input transform (the decode step's
+ * folded RMSNorm, SiLU, attention merge, routing) always use the MFMA
+ * kernel. */
+#define WPCG_FAST_KERNEL_MFMA 0
+#define WPCG_FAST_KERNEL_VALU 1
+int wpcg_linear_set_fast_kernel(wpcg_linear* lin, int kernel);
 /* The split wpcg_linear_set_kslices would use for an out_f x in_f matrix
  * (host-only query; every slice is non-empty and within the limits above). */
 int wpcg_plan_kslices(uint64_t out_f, uint64_t in_f, int requested, int* kslices);

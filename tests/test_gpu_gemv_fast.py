@@ -151,6 +151,55 @@ def test_fast_matches_reference_within_tolerance(ctx, scheme, rows, cols):
     assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
 
 
+@pytest.mark.parametrize("scheme,rows,cols", SHAPES)
+def test_valu_kernel_matches_reference_within_tolerance(ctx, scheme, rows, cols):
+    """WPCG_FAST_KERNEL_VALU: the same GEMVs on the vector-ALU kernel (fp32
+    x, codes unpacked by shift/mask, fp32 FMAs in its own order), held to
+    the same bounds against float64 and the reference kernel; deterministic
+    run to run, K-split handoffs included."""
+    print(f"[gpu] valu v{scheme} {rows}x{cols}", flush=True)
+    gen = synth.random_v4_blocks if scheme == 4 else synth.random_v3_blocks
+    blocks = gen(rows, cols, seed=rows + 3 * cols)
+    x = synth.random_x(cols, seed=cols + 5)
+    lin = wpcg.WpcLinear.from_blocks(ctx, scheme, blocks, rows, cols).set_mode(wpcg.MODE_FAST)
+    lin.set_fast_kernel(wpcg.FAST_KERNEL_VALU)
+    y = lin.matvec(x)
+    check_fast(y, scheme, blocks, rows, cols, x, f"valu v{scheme} {rows}x{cols}")
+    y2 = lin.matvec(x)
+    assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+
+
+def test_valu_kernel_bias_extremes_and_groups(ctx):
+    """The vector-ALU kernel with a bias, the extreme inputs of the MFMA
+    test, and grouped launches (q/k/v-shaped problems of one launch) equal to
+    separate launches bit for bit."""
+    rows, cols = 300, 1280
+    blocks = synth.random_v4_blocks(rows, cols, 77)
+    bias = synth.random_x(rows, 78)
+    lin = wpcg.WpcLinear.from_blocks(ctx, 4, blocks, rows, cols, bias=bias).set_mode(wpcg.MODE_FAST)
+    lin.set_fast_kernel(wpcg.FAST_KERNEL_VALU)
+    rng = np.random.default_rng(79)
+    x = rng.standard_normal(cols).astype(np.float32)
+    x[:128] = 0.0
+    x[128:256] = 1e-30
+    x[256:384] *= 1e4
+    x[400] = -7e5
+    check_fast(lin.matvec(x), 4, blocks, rows, cols, x, "valu extremes", bias=bias.astype(np.float64))
+    shapes = [(3, 4096, 2560), (3, 1024, 2560), (3, 1024, 2560)]
+    lins = []
+    for i, (sch, r, c) in enumerate(shapes):
+        b = synth.random_v3_blocks(r, c, seed=900 + i)
+        lins.append(wpcg.WpcLinear.from_blocks(ctx, sch, b, r, c).set_mode(wpcg.MODE_FAST)
+                    .set_fast_kernel(wpcg.FAST_KERNEL_VALU))
+    xg = synth.random_x(2560, seed=905)
+    xd = ctx.upload(xg)
+    ys = [ctx.alloc(4 * r) for _, r, _ in shapes]
+    wpcg.matvec_multi(lins, [xd] * 3, ys)
+    ctx.sync()
+    for l, yb, (_, r, _) in zip(lins, ys, shapes):
+        assert np.array_equal(yb.read(np.float32, r).view(np.uint32), l.matvec(xg).view(np.uint32))
+
+
 def test_fast_with_bias_and_extreme_inputs(ctx):
     rows, cols = 300, 1280
     blocks = synth.random_v4_blocks(rows, cols, 77)

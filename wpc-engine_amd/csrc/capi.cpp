@@ -495,6 +495,15 @@ int wpcg_linear_set_kslices(wpcg_linear* L, int kslices)
     return WPCG_OK;
 }
 
+int wpcg_linear_set_fast_kernel(wpcg_linear* L, int kernel)
+{
+    if (!L) return fail(WPCG_E_ARG, "null linear");
+    if (kernel != WPCG_FAST_KERNEL_MFMA && kernel != WPCG_FAST_KERNEL_VALU)
+        return fail(WPCG_E_ARG, "kernel must be WPCG_FAST_KERNEL_MFMA or WPCG_FAST_KERNEL_VALU");
+    L->plan.valu = kernel == WPCG_FAST_KERNEL_VALU;
+    return WPCG_OK;
+}
+
 int wpcg_linear_kslices(wpcg_linear* L, int* kslices)
 {
     if (!L || !kslices) return fail(WPCG_E_ARG, "null argument");
@@ -642,6 +651,7 @@ int wpcg_linear_clone(wpcg_linear* L, wpcg_linear** out)
         free_plan(c->plan);
         return rc;
     }
+    c->plan.valu = L->plan.valu;
     auto dup = [&](void** dst, const void* src, size_t n) -> hipError_t {
         hipError_t e = hipMalloc(dst, n);
         if (e == hipSuccess) e = hipMemcpyAsync(*dst, src, n, hipMemcpyDeviceToDevice, s);

@@ -1075,6 +1075,249 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && (XF == XF_NONE || (XF 
     if (t == 0) __hip_atomic_store(P.counters + tg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ============================================================ FAST mode, vector-ALU variant
+// k_gemv_valu: the plain FAST GEMV (no input transform, no routing) with the
+// dot products on the vector ALU in fp32 instead of the matrix cores: x is
+// read as fp32 and never digitised, so the prep has no block maximum, no
+// reciprocal and no rounding, only a transposing copy into LDS. Same
+// problems, launch shape, plan (tiles per workgroup, K-slices) and end phase
+// as k_gemv_fast<S, FK_PLAIN, XF_NONE>; the reference's row kernel it
+// restates with another summation order is matvec_v{4,3}_fused
+// (wpc-eval/src/fused_kernel.rs:237-271, 163-189).
+//   prep:  the slice's x goes to LDS transposed by lane group: value k of a
+//          block at xv[blk][k & 3][k >> 2] (groups padded to 36 floats so
+//          that the four groups' 16-byte reads fall in distinct banks), and
+//          each group's sum of its 32 values at xg[blk][k & 3].
+//   dots:  lane (g, j) of a wave holds, per block, the 16 code bytes of row
+//          j that AVX2 lanes g and g+4 read (32 codes, every k = g mod 4),
+//          turns them into floats with shift/mask in registers (v3: the high
+//          plane's two bits or-ed in) and multiplies them with its group's
+//          32 x values: P = sum code*x in fp32, then
+//          acc += scale*P + zp*sum(x of the group).
+//   sum:   the four lane groups of a row by two row swaps, then the waves of
+//          a tile in part order (deterministic).
+constexpr int VX_G = 36;          // floats per lane group of a block in LDS
+constexpr int VX_BLK = 4 * VX_G;  // floats per block
+
+// float of byte b of w (v_cvt_f32_ubyte{0..3})
+template <int B>
+__device__ __forceinline__ float ub(uint32_t w) { return (float)((w >> (8 * B)) & 0xFFu); }
+
+// P += the 8 products of word w's four bytes with x values m0, m0+2, m0+4, m0+6
+__device__ __forceinline__ float dot4(uint32_t w, const float* X, int m0, float P)
+{
+    P = __builtin_fmaf(ub<0>(w), X[m0], P);
+    P = __builtin_fmaf(ub<1>(w), X[m0 + 2], P);
+    P = __builtin_fmaf(ub<2>(w), X[m0 + 4], P);
+    P = __builtin_fmaf(ub<3>(w), X[m0 + 6], P);
+    return P;
+}
+
+template <int SCHEME>
+__global__ __launch_bounds__(FAST_WG, 4) void k_gemv_valu(const FastBatch B)
+{
+    __shared__ __align__(16) float xv[MAXBK * VX_BLK];  // the slice's x, transposed
+    __shared__ __align__(16) float xg[MAXBK * 4];       // per block and lane group: sum of its x
+    __shared__ __align__(16) uint32_t spar[8][QB * TILE_ROWS];
+    __shared__ float red[8][TILE_ROWS];
+    __shared__ int s_last;
+
+    typedef const __attribute__((address_space(4))) FastBatch* KargPtr;
+    const KargPtr kargs = (KargPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    const auto& P = kargs->p[blockIdx.y];
+    const int local = blockIdx.x;
+    const int nb = P.nb, kg = P.kg, tw = P.tw, nwg = P.nwg, rows_pad = P.rows_pad;
+    const uint8_t* codes = P.codes;
+    const uint8_t* hplane = SCHEME == 3 ? P.hp : P.codes;
+    const uint32_t* params = P.params;
+    const float* const x0 = P.x;
+    const int nbk_ = P.nbk, ltw_ = P.ltw;
+    const uint32_t kg_inv_ = P.kg_inv;
+    float* const out_y = P.y;
+    const float* const out_bias = P.bias;
+    const int out_rows = P.rows;
+    const int32_t* const sel = P.sel;
+    asm volatile("" ::"s"(nb), "s"(kg), "s"(tw), "s"(nwg), "s"(rows_pad), "s"(codes), "s"(hplane), "s"(params),
+                 "s"(x0), "s"(nbk_), "s"(ltw_), "s"(kg_inv_), "s"(out_y), "s"(out_bias), "s"(out_rows), "s"(sel));
+    if (local >= nwg) return;  // past this problem's workgroups
+    const int tg = kg == 1 ? local : (int)__umulhi((uint32_t)local, kg_inv_), kgi = local - tg * kg;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int b0 = kgi * nbk_, nbl = max(0, min(nb, b0 + nbk_) - b0);
+    const float* xp = x0 + (size_t)b0 * 128;
+
+    // Loads, all issued before any use, as in k_gemv_fast: x, parameters, weights.
+    // float4 f = threadIdx.x + FAST_WG*u of the slice: block f >> 5, values 4(f & 31) .. +3
+    constexpr int XU = MAXBK * 32 / FAST_WG;
+    const auto xrs = buf_rsrc(xp, nbl * 512);
+    u32x4 xl[XU];
+#pragma unroll
+    for (int u = 0; u < XU; u++) xl[u] = __builtin_amdgcn_raw_buffer_load_b128(xrs, (threadIdx.x + FAST_WG * u) * 16, 0, 0);
+
+    int e = 0;
+    if (sel) e = sel[P.sel_k];
+    const bool live = !sel || e >= 0;
+    if (sel) {
+        const size_t t0 = (size_t)max(e, 0) * (rows_pad / TILE_ROWS) * nb;
+        codes += t0 * CODE_REC;
+        hplane += t0 * HP_REC;
+        params += t0 * TILE_ROWS;
+    }
+    const int ntiles = rows_pad / TILE_ROWS;
+    const int ltw = ltw_, lkw = 3 - ltw, kw = 1 << lkw;
+    const int T = (tg << ltw) + (wave >> lkw), kq = wave & (kw - 1);
+    const int q = (nbl + kw - 1) >> lkw;
+    const int qw = live && T < ntiles ? max(0, min(q, nbl - kq * q)) : 0;
+    const int wb = b0 + kq * q;
+    const int g = lane >> 4, j = lane & 15;
+
+    u32x4 pv;
+    u32x4 c[QB];
+    u32x2 h[QB];
+    {
+        const size_t rec = (size_t)min(T, ntiles - 1) * nb + wb;
+        const auto prs = buf_rsrc(params + rec * TILE_ROWS, qw * 64);
+        pv = __builtin_amdgcn_raw_buffer_load_b128(prs, lane * 16, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        const auto crs = buf_rsrc(codes + rec * CODE_REC, qw * (int)CODE_REC);
+        const auto hrs = buf_rsrc(hplane + rec * HP_REC, SCHEME == 3 ? qw * (int)HP_REC : 0);
+#pragma unroll
+        for (int i = 0; i < QB; i++) {
+            c[i] = __builtin_amdgcn_raw_buffer_load_b128(crs, i * (int)CODE_REC + lane * 16, 0, CPOL_NT);
+            if constexpr (SCHEME == 3)
+                h[i] = __builtin_amdgcn_raw_buffer_load_b64(hrs, i * (int)HP_REC + lane * 8, 0, CPOL_NT);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- x -> LDS, transposed by lane group; each group's sum over a block
+    // by DPP within rows and a row swap (the 32 lanes holding a block are
+    // rows 0-1 or 2-3 of the wave); a fixed tree, the same on every call.
+#pragma unroll
+    for (int u = 0; u < XU; u++) {
+        const int f = threadIdx.x + FAST_WG * u, blk = f >> 5, m = f & 31;
+        if (blk >= nbl) break;  // uniform per half-wave; past the slice from here on
+        float v[4] = {__uint_as_float(xl[u].x), __uint_as_float(xl[u].y), __uint_as_float(xl[u].z),
+                      __uint_as_float(xl[u].w)};
+        float* d = xv + blk * VX_BLK + m;
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) d[gg * VX_G] = v[gg];
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) v[gg] += dpp<DPP_XOR1>(v[gg]);
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) v[gg] += dpp<DPP_XOR2>(v[gg]);
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) v[gg] += dpp<DPP_HALF_MIRROR>(v[gg]);
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) v[gg] += dpp<DPP_MIRROR>(v[gg]);
+#pragma unroll
+        for (int gg = 0; gg < 4; gg++) {  // every lane of the half-wave takes part in the swap
+            const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[gg]), __float_as_uint(v[gg]), false, false);
+            v[gg] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+        }
+        if (m == 0) {
+#pragma unroll
+            for (int gg = 0; gg < 4; gg++) xg[blk * 4 + gg] = v[gg];
+        }
+    }
+    if (lane < QB * 4) *reinterpret_cast<u32x4*>(spar[wave] + lane * 4) = pv;
+    __syncthreads();
+
+    // ---- dots
+    float acc = 0.0f, zacc = 0.0f;
+    {
+        const int lb = kq * q;
+        const float* xw = xv + lb * VX_BLK + g * VX_G;
+        const float* xgw = xg + lb * 4 + g;
+        const uint32_t* sp = spar[wave] + j;
+        const uint32_t M = 0x0F0F0F0Fu;
+#pragma unroll
+        for (int i = 0; i < QB; i++) {
+            if (i < qw) {
+                float X[32];
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const float4 v = *reinterpret_cast<const float4*>(xw + i * VX_BLK + 4 * t);
+                    X[4 * t] = v.x; X[4 * t + 1] = v.y; X[4 * t + 2] = v.z; X[4 * t + 3] = v.w;
+                }
+                const uint32_t pr = sp[i * TILE_ROWS];
+                const float sgrp = xgw[i * 4];
+                // low nibbles: codes k (k < 64), high nibbles: k + 64 (x index m + 16)
+                uint32_t L0 = c[i].x & M, L1 = c[i].y & M, L2 = c[i].z & M, L3 = c[i].w & M;
+                uint32_t H0 = (c[i].x >> 4) & M, H1 = (c[i].y >> 4) & M;
+                uint32_t H2 = (c[i].z >> 4) & M, H3 = (c[i].w >> 4) & M;
+                if constexpr (SCHEME == 3) {
+                    const uint32_t T6 = 0x30303030u, hx = h[i].x, hy = h[i].y;
+                    L0 |= (hx << 4) & T6; L1 |= (hx << 2) & T6;
+                    L2 |= (hy << 4) & T6; L3 |= (hy << 2) & T6;
+                    H0 |= hx & T6;        H1 |= (hx >> 2) & T6;
+                    H2 |= hy & T6;        H3 |= (hy >> 2) & T6;
+                }
+                // byte b of word 0 is k = 8b + g (m = 2b), of word 1 k = 8(b+4) + g
+                // (m = 8 + 2b), of word 2 k = 8b + g + 4 (m = 2b + 1), of word 3
+                // m = 9 + 2b; two chains, added at the end
+                float Pa = 0.0f, Pb = 0.0f;
+                Pa = dot4(L0, X, 0, Pa);
+                Pb = dot4(L2, X, 1, Pb);
+                Pa = dot4(L1, X, 8, Pa);
+                Pb = dot4(L3, X, 9, Pb);
+                Pa = dot4(H0, X, 16, Pa);
+                Pb = dot4(H2, X, 17, Pb);
+                Pa = dot4(H1, X, 24, Pa);
+                Pb = dot4(H3, X, 25, Pb);
+                acc = __builtin_fmaf(Pa + Pb, h2f(pr >> 16), acc);
+                zacc = __builtin_fmaf(h2f(pr & 0xFFFFu), sgrp, zacc);
+            }
+        }
+    }
+    // the four lane groups of row j: rows 0+1 and 2+3 by a 16-lane swap, then the halves
+    float r = acc + zacc;
+    {
+        const auto s1 = __builtin_amdgcn_permlane16_swap(__float_as_uint(r), __float_as_uint(r), false, false);
+        r = __uint_as_float(s1[0]) + __uint_as_float(s1[1]);
+        const auto s2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(r), __float_as_uint(r), false, false);
+        r = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
+    }
+    if (g == 0) red[wave][j] = r;
+    __syncthreads();
+
+    const int t = threadIdx.x;
+    const int tt = t >> 4, rr = t & 15;
+    const bool mine = t < tw * TILE_ROWS && tg * tw + tt < ntiles;
+    const size_t orow = (size_t)(tg * tw + tt) * TILE_ROWS + rr;
+    float sum = 0.0f;
+    if (mine) {
+        sum = red[tt * kw][rr];
+        for (int k = 1; k < kw; k++) sum += red[tt * kw + k][rr];
+    }
+    if (kg == 1) {
+        if (mine && orow < (size_t)out_rows) out_y[orow] = out_bias ? sum + out_bias[orow] : sum;
+        return;
+    }
+    // split K: the handoff of k_gemv_fast (device-scope exchanges, a counter
+    // per tile group, the last workgroup adding the slices in slice order)
+    if (mine) {
+        const float prev = __hip_atomic_exchange(P.part + (size_t)kgi * P.rows_pad + orow, sum,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("" ::"v"(prev));
+    }
+    __syncthreads();
+    if (t == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(P.counters + tg, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == (uint32_t)(kg - 1);
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (mine && orow < (size_t)out_rows) {
+        float a = __hip_atomic_load(P.part + orow, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int k = 1; k < kg; k++)
+            a += __hip_atomic_load(P.part + (size_t)k * P.rows_pad + orow, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        out_y[orow] = out_bias ? a + out_bias[orow] : a;
+    }
+    if (t == 0) __hip_atomic_store(P.counters + tg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ============================================================ decode helpers
 __device__ __forceinline__ uint32_t code_at(const uint8_t* codes, const uint8_t* hp, size_t row,
                                             size_t b, int nb, int kk, int scheme)
@@ -1331,6 +1574,18 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
         if (B.p[i].nbk > 32) short_slices = false;
     (void)hipGetLastError();  // report only this launch
     const dim3 grid(wgs, n), block(FAST_WG);
+    // the vector-ALU variant: plain problems whose linears ask for it, with
+    // no deferred slices, bias vectors or argmax keys
+    bool valu = kind == FK_PLAIN && xf == XF_NONE;
+    for (int i = 0; i < n && valu; i++)
+        valu = jobs[i].plan->valu && !jobs[i].y2 && !jobs[i].bias2 && !jobs[i].amax;
+    if (valu) {
+        if (scheme == 4)
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_valu<4>), grid, block, 0, s, B);
+        else
+            hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_valu<3>), grid, block, 0, s, B);
+        return hipGetLastError();
+    }
 #define WPCG_FAST(S, K, X) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<S, K, X>), grid, block, 0, s, B)
 #define WPCG_FAST2(S, K, X) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gemv_fast<S, K, X, 2>), grid, block, 0, s, B)
 #define WPCG_FAST_S(S)                                                               \

@@ -67,6 +67,7 @@ struct FastPlan {
     int kg = 1;               // K-slices across workgroups
     float* part = nullptr;    // [kg][rows_pad] partial sums (kg > 1)
     uint32_t* counters = nullptr;  // one per workgroup tile group, self-resetting
+    int valu = 0;             // plain GEMVs on the vector-ALU kernel (WPCG_FAST_KERNEL_VALU)
 };
 
 // Host transcodes from the reference's on-disk blocks (AoS) to the planes

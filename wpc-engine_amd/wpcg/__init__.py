@@ -30,6 +30,7 @@ HEADER = os.path.join(os.path.dirname(PKG_ROOT), "include", "wpcg.h")
 OK, E_IO, E_FORMAT, E_SHAPE, E_NOTFOUND, E_DEVICE, E_ARG, E_NOMEM, E_UNSUPPORTED = range(9)
 SCHEME_V3, SCHEME_V4 = 3, 4
 MODE_EXACT, MODE_FAST = 0, 1
+FAST_KERNEL_MFMA, FAST_KERNEL_VALU = 0, 1
 ROUND_FMA, ROUND_TWO = 0, 1
 DTYPE_F32, DTYPE_BF16, DTYPE_F32_SPLIT = 0, 1, 2
 
@@ -83,6 +84,7 @@ _SIGS = {
     "wpcg_linear_shape": (C.c_int, [_p, _u64p, _u64p]),
     "wpcg_linear_set_mode": (C.c_int, [_p, C.c_int]),
     "wpcg_linear_set_kslices": (C.c_int, [_p, C.c_int]),
+    "wpcg_linear_set_fast_kernel": (C.c_int, [_p, C.c_int]),
     "wpcg_linear_kslices": (C.c_int, [_p, C.POINTER(C.c_int)]),
     "wpcg_plan_kslices": (C.c_int, [_u64, _u64, C.c_int, C.POINTER(C.c_int)]),
     "wpcg_linear_device_bytes": (C.c_int, [_p, _u64p]),
@@ -494,6 +496,11 @@ class WpcLinear:
 
     def set_kslices(self, k: int):
         check(lib.wpcg_linear_set_kslices(self.h, k))
+        return self
+
+    def set_fast_kernel(self, kernel: int):
+        """FAST_KERNEL_MFMA (default) or FAST_KERNEL_VALU for plain GEMVs."""
+        check(lib.wpcg_linear_set_fast_kernel(self.h, kernel))
         return self
 
     def kslices(self) -> int:
