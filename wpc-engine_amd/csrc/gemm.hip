@@ -126,8 +126,7 @@ struct GemmArgs {
     float* y;            // [M][rows]
     const float* bias;   // [rows] or null
     const float* res;    // [M][rows] added to Y (may be y itself) or null
-    float* part;         // [kg][NT*16][rows_pad] (kg > 1)
-    uint32_t* counters;  // one per row group (kg > 1), self-resetting
+    float* part;         // [kg][NT*16][rows_pad] (kg > 1), summed by k_gemm_reduce
     int rows, rows_pad, nb, M, kg;
     // column groups: the packed X holds xt tiles per block (groups of NT);
     // with rgs8 > 0 workgroup cg * rgs8 + rg takes row group rg (< rgs) of
@@ -141,6 +140,13 @@ __device__ __forceinline__ float out_val(float v, const float* bias, const float
     if (bias) v += bias[row];
     if (res) v += res[(size_t)m * rows + row];
     return v;
+}
+
+// Eight bf16 of one fragment lane from two consecutive-k pieces: the low
+// (odd = 0) or high (odd = 1) halves of dwords a (slot 2q) and b (slot 2q+1).
+__device__ __forceinline__ uint32_t pick_halves(uint32_t a, uint32_t b, int odd)
+{
+    return odd ? (a >> 16) | (b & 0xFFFF0000u) : (a & 0xFFFFu) | (b << 16);
 }
 
 constexpr int GM_WG = GEMM_WG_THREADS;   // 8 waves, two per SIMD
@@ -201,7 +207,6 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P)
     constexpr int SV = (SN + GM_WG - 1) / GM_WG;
     __shared__ __align__(16) u32x4 xb[2][GM_R * FW];
     __shared__ float xsb[2][SN];
-    __shared__ int s_last;
 
     const int kg = P.kg, nb = P.nb, XT = P.xt;
     int kgi, rg, cg;
@@ -279,19 +284,30 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P)
             if (i < SN) xsb[buf][i] = sr[v];
         }
     };
-    // the fragments of column tile n of block u of a round buffer, and the
-    // tile's column sum for this lane's column
-    auto read_tile = [&](bf16x8 (&B)[4], float& S, int buf, int u, int n) {
+    // the fragments of kstep i of every column tile of block u of a round buffer
+    auto read_kstep = [&](bf16x8 (&B)[NT], int buf, int u, int i) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int n = 0; n < NT; n++) {
             const u32x4 w = xb[buf][u * FW + (n * 4 + i) * 64 + lane];
-            __builtin_memcpy(&B[i], &w, 16);
+            __builtin_memcpy(&B[n], &w, 16);
         }
-        S = xsb[buf][u * NT * 16 + n * 16 + j];
+    };
+    // The zero-point term of a round, sum_b zp(row, b) * S(b, col) over its
+    // GM_R = 4 blocks, is one fp32 matrix-core product per column tile:
+    // lane (g, j) supplies zp_off of row j of block g (A, 16 x 4) and the
+    // block-g sum of column n*16 + j (B, 4 x 16), and the product adds into
+    // the accumulators in their own layout. Zero-point words of round r:
+    // one per lane and row tile.
+    static_assert(GM_R == 4, "a round is the k = 4 of v_mfma_f32_16x16x4_f32");
+    auto load_zp = [&](uint32_t (&z)[RT], int r) {
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+            z[rt] = __builtin_amdgcn_raw_buffer_load_b32(prs[rt], ((r * GM_R + g) * TILE_ROWS + j) * 4, 0, CPOL_NT);
     };
 
     // prologue: round 0 and the first GM_LA blocks of codes, then round 1,
     // in the order the loop keeps (so the wait counts at its head match)
+    uint32_t zc[RT], zn[RT];
     load_round(0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -299,6 +315,7 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P)
         load_codes(u, u);
         __builtin_amdgcn_sched_barrier(0);
     }
+    load_zp(zc, 0);
     store_round(0);
     load_round(1);
     __syncthreads();
@@ -309,22 +326,29 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P)
 #pragma unroll
         for (int n = 0; n < NT; n++) acc[rt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    bf16x8 Bc[4];
-    float Sc;
-    read_tile(Bc, Sc, 0, 0, 0);
+    bf16x8 Bc[NT];
+    read_kstep(Bc, 0, 0, 0);
 
+    // Whole rounds of unconditional steps (guarded steps would merge the
+    // wait-counter state at the loop edge and drain every load in flight).
     // Whole rounds of unconditional steps (guarded steps would merge the
     // wait-counter state at the loop edge and drain every load in flight).
     const int nrounds = (nbl + GM_R - 1) / GM_R;
     for (int r = 0; r < nrounds; r++) {
         const int buf = r & 1;
+        // this round's block sums for the zero-point product, read before the
+        // barrier after which the buffer may be refilled
+        float Sz[NT];
+#pragma unroll
+        for (int n = 0; n < NT; n++) Sz[n] = xsb[buf][g * NT * 16 + n * 16 + j];
         store_round(buf ^ 1);  // round r+1 into the buffer round r-1 left
         load_round(r + 2);
+        load_zp(zn, r + 1);
 #pragma unroll
         for (int u = 0; u < GM_R; u++) {
             const int b = r * GM_R + u;
             bf16x8 A[RT][4];
-            float sc[RT][4], zp[RT][4];
+            float sc[RT][4];
 #pragma unroll
             for (int rt = 0; rt < RT; rt++) {
                 const u32x4 U = cr[u][rt];
@@ -343,43 +367,60 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P)
                 A[rt][2] = codes_bf16(hi.x, hi.y);
                 A[rt][3] = codes_bf16(hi.z, hi.w);
                 const u32x4 p = pr[u][rt];
-                sc[rt][0] = h2f(p.x >> 16); zp[rt][0] = zp_off(p.x);
-                sc[rt][1] = h2f(p.y >> 16); zp[rt][1] = zp_off(p.y);
-                sc[rt][2] = h2f(p.z >> 16); zp[rt][2] = zp_off(p.z);
-                sc[rt][3] = h2f(p.w >> 16); zp[rt][3] = zp_off(p.w);
+                sc[rt][0] = h2f(p.x >> 16);
+                sc[rt][1] = h2f(p.y >> 16);
+                sc[rt][2] = h2f(p.z >> 16);
+                sc[rt][3] = h2f(p.w >> 16);
             }
             load_codes(u, b + GM_LA);
+            // kstep-major: the NT column tiles' products of one kstep are
+            // independent, so the matrix cores take them back to back while
+            // the next kstep's fragments come from LDS (a column tile's four
+            // ksteps in a row would each wait for the one before: M = 64
+            // rounds 3.3 -> 2.9 us)
+            f32x4 D[RT][NT];
 #pragma unroll
-            for (int n = 0; n < NT; n++) {
-                // the next tile's fragments: this round's buffer, or (before
-                // the round's last tile, after the barrier) the next round's
-                bf16x8 Bn[4];
-                float Sn;
-                if (n + 1 < NT) {
-                    read_tile(Bn, Sn, buf, u, n + 1);
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int n = 0; n < NT; n++) D[rt][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                // the next kstep's fragments: this round's buffer, or (before
+                // the round's last kstep, after the barrier) the next round's
+                bf16x8 Bn[NT];
+                if (i + 1 < 4) {
+                    read_kstep(Bn, buf, u, i + 1);
                 } else if (u + 1 < GM_R) {
-                    read_tile(Bn, Sn, buf, u + 1, 0);
+                    read_kstep(Bn, buf, u + 1, 0);
                 } else {
                     __syncthreads();
-                    read_tile(Bn, Sn, buf ^ 1, 0, 0);
+                    read_kstep(Bn, buf ^ 1, 0, 0);
                 }
-                f32x4 D[RT];
+                __builtin_amdgcn_sched_barrier(0);  // the reads go out before this kstep's products
 #pragma unroll
-                for (int rt = 0; rt < RT; rt++) D[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int i = 0; i < 4; i++)
+                for (int n = 0; n < NT; n++)
 #pragma unroll
                     for (int rt = 0; rt < RT; rt++)
-                        D[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[rt][i], Bc[i], D[rt], 0, 0, 0);
+                        D[rt][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[rt][i], Bc[n], D[rt][n], 0, 0, 0);
 #pragma unroll
-                for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-                    for (int q = 0; q < 4; q++)
-                        acc[rt][n][q] = __builtin_fmaf(zp[rt][q], Sc, __builtin_fmaf(sc[rt][q], D[rt][q], acc[rt][n][q]));
-#pragma unroll
-                for (int i = 0; i < 4; i++) Bc[i] = Bn[i];
-                Sc = Sn;
+                for (int n = 0; n < NT; n++) Bc[n] = Bn[n];
+                // keep the kstep's products together (the scheduler would
+                // otherwise regroup them into per-tile chains)
+                __builtin_amdgcn_sched_barrier(0);
             }
+#pragma unroll
+            for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+                for (int n = 0; n < NT; n++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++) acc[rt][n][q] = __builtin_fmaf(sc[rt][q], D[rt][n][q], acc[rt][n][q]);
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+            const float za = zp_off(zc[rt]);
+#pragma unroll
+            for (int n = 0; n < NT; n++) acc[rt][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(za, Sz[n], acc[rt][n], 0, 0, 0);
+            zc[rt] = zn[rt];
         }
     }
 
@@ -408,12 +449,13 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P)
             }
         return;
     }
-    // Split K: publish the slice's partials with coherent stores, then the
-    // last workgroup of the row group adds the kg slices in slice order
-    // (deterministic) and resets the counter. The stores are complete at
-    // the device's coherence point once vmcnt drains, before the barrier
-    // that precedes the counter increment; the last workgroup reads with
-    // coherent loads after it has seen the count.
+    // Split K: the slice's partials go to part[kgi]; k_gemm_reduce, the
+    // next launch on the stream, adds the slices in slice order
+    // (deterministic) with every CU taking part. (A handoff inside this
+    // kernel, the last workgroup of a row group adding all slices after
+    // device-scope publishes and a counter, left that sum to one CU per row
+    // group: 4.1 us of a 22 us M = 64 gate/up launch at 2 slices, 6.7 of 25
+    // us for down_proj at 8.)
     const auto prt = buf_rsrc(P.part, kg * Mp * P.rows_pad * 4);
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
@@ -423,57 +465,29 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P)
             if (T0 + rt < ntiles) {
                 u32x4 v;
                 __builtin_memcpy(&v, &acc[rt][n], 16);
-                __builtin_amdgcn_raw_buffer_store_b128(v, prt, ((kgi * Mp + m) * P.rows_pad + row) * 4, 0, CPOL_SC1);
+                __builtin_amdgcn_raw_buffer_store_b128(v, prt, ((kgi * Mp + m) * P.rows_pad + row) * 4, 0, 0);
             }
         }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = __hip_atomic_fetch_add(P.counters + rg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == (uint32_t)(kg - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    // The slices in slice order. Every load of GM_KC slices (all written
-    // column tiles) is issued before the first add, so a chunk costs one
-    // round trip to the coherence point; slices past kg read as zeros (past
-    // the buffer's range) and are not added.
-    constexpr int GM_KC = 8;
+}
+
+// The split-K sum of k_gemm: Y[m][row] = sum over the kg slices of
+// part[k][m][row] in slice order, then the bias and the residual. One thread
+// per four rows of one column; reads and writes run along the rows.
+__global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ part, int kg, int Mp, int rows_pad,
+                                                     int rows, int M, const float* bias, const float* res,
+                                                     float* y)
+{
+    const int per = rows_pad / 4;
+    const int idx = (int)(blockIdx.x * 256 + threadIdx.x);
+    const int m = idx / per, row = (idx - m * per) * 4;
+    if (m >= M) return;
+    const f32x4* p = reinterpret_cast<const f32x4*>(part + (size_t)m * rows_pad + row);
+    const size_t stride = (size_t)Mp * rows_pad / 4;  // f32x4 per slice
+    f32x4 s = p[0];
+    for (int k = 1; k < kg; k++) s = s + p[k * stride];
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-        const int row = (T0 + rt) * TILE_ROWS + 4 * g;
-        f32x4 s[NW];
-        for (int k0 = 0; k0 < kg; k0 += GM_KC) {
-            u32x4 v[GM_KC][NW];
-#pragma unroll
-            for (int kk = 0; kk < GM_KC; kk++)
-#pragma unroll
-                for (int n = 0; n < NW; n++) {
-                    const int m = n * 16 + j, k = k0 + kk;
-                    v[kk][n] = __builtin_amdgcn_raw_buffer_load_b128(
-                        prt, k < kg ? ((k * Mp + m) * P.rows_pad + row) * 4 : 0x7FFFFFF0, 0, CPOL_SC1);
-                }
-#pragma unroll
-            for (int kk = 0; kk < GM_KC; kk++)
-                if (k0 + kk < kg)
-#pragma unroll
-                    for (int n = 0; n < NW; n++) {
-                        f32x4 f;
-                        __builtin_memcpy(&f, &v[kk][n], 16);
-                        s[n] = k0 + kk == 0 ? f : s[n] + f;
-                    }
-        }
-        if (T0 + rt >= ntiles) continue;
-#pragma unroll
-        for (int n = 0; n < NW; n++) {
-            const int m = mcol0 + n * 16 + j;
-            if (m >= P.M) continue;
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-                if (row + q < P.rows) P.y[(size_t)m * P.rows + row + q] = out_val(s[n][q], P.bias, P.res, P.rows, m, row + q);
-        }
-    }
-    if (threadIdx.x == 0) __hip_atomic_store(P.counters + rg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int q = 0; q < 4; q++)
+        if (row + q < rows) y[(size_t)m * rows + row + q] = out_val(s[q], bias, res, rows, m, row + q);
 }
 
 // ---- M <= 16: one kernel. The workgroup packs its whole K-slice of X
@@ -500,12 +514,6 @@ struct GemmSmallArgs {
     int rows, rows_pad, nb, M, kg;
 };
 
-// Eight bf16 of one fragment lane from two consecutive-k pieces: the low
-// (odd = 0) or high (odd = 1) halves of dwords a (slot 2q) and b (slot 2q+1).
-__device__ __forceinline__ uint32_t pick_halves(uint32_t a, uint32_t b, int odd)
-{
-    return odd ? (a >> 16) | (b & 0xFFFF0000u) : (a & 0xFFFFu) | (b << 16);
-}
 
 // The fp32 value held in a dword minus its bf16 rounding (exact), i.e. the
 // lo part of a SPLIT column.
@@ -1094,7 +1102,6 @@ hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, 
     a.bias = bias;
     a.res = res;
     a.part = w.part;
-    a.counters = w.counters;
     a.rows = (int)m.rows;
     a.rows_pad = (int)m.rows_pad;
     a.nb = nb;
@@ -1102,8 +1109,13 @@ hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, 
     a.kg = w.kg;
     a.xt = ntiles;
     dim3 grid((unsigned)(gemm_row_groups(m.rows) * w.kg));
-    if (split) return m.scheme == 4 ? launch_nt<4, true>(ntiles, grid, s, a) : launch_nt<3, true>(ntiles, grid, s, a);
-    return m.scheme == 4 ? launch_nt<4, false>(ntiles, grid, s, a) : launch_nt<3, false>(ntiles, grid, s, a);
+    if (split) e = m.scheme == 4 ? launch_nt<4, true>(ntiles, grid, s, a) : launch_nt<3, true>(ntiles, grid, s, a);
+    else e = m.scheme == 4 ? launch_nt<4, false>(ntiles, grid, s, a) : launch_nt<3, false>(ntiles, grid, s, a);
+    if (e != hipSuccess || w.kg == 1) return e;
+    const int outs = M * (int)(m.rows_pad / 4);
+    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, w.part, w.kg,
+                       ntiles * 16, (int)m.rows_pad, (int)m.rows, M, bias, res, y);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm_pack_rows(const float* x, int M, int K, void* xf, float* xsum, hipStream_t s)
