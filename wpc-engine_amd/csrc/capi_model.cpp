@@ -357,6 +357,7 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
 // ---- batched prefill (FAST) --------------------------------------------------
 // Rows of tokens per prefill pass; longer prompts run pass after pass.
 constexpr uint32_t PF_CAP = 256;
+static_assert(PF_CAP <= (uint32_t)PF_GROUP_MAXT, "the expert grouping holds PF_GROUP_MAXT tokens");
 
 // Whether the batched path covers this model: FAST attention's head shapes,
 // and for MoE the router width, the pair count and one-slice expert GEMMs.

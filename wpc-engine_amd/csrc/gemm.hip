@@ -35,6 +35,7 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int gk(int i, int g, int s) { return 8 * s + g + 4 * (i & 1) + 64 * (i >> 1); }
 
@@ -772,19 +773,35 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
 }
 
 // ---- expert-grouped GEMM (prefill): one workgroup per work item = one
-// expert's run of at most GEMM_GROUP_COLS (X row, Y row) pairs. The item's X
-// rows are loaded once and packed into LDS as hi and lo bf16 fragments
-// (fragment columns [0, M) and [M, 2M)); then each wave streams whole row
+// expert's run of at most GEMM_GROUP_COLS (X row, Y row) pairs, on the int8
+// matrix cores with the FAST GEMV's representation of x: each 128-value
+// block of a pair's X row is x ~= s_b * Q / 2^21, s_b = max|x_b| / 127,
+// Q = rint(x * 127 * 2^21 / max|x_b|) = d0*2^21 + d1*2^14 + d2*2^7 + d3
+// with int8 digits (d0 = Q >> 21, d1..d3 7-bit fields). The digits of four
+// pairs are the first operand of v_mfma_i32_16x16x64_i8 (row 4p + d: digit d
+// of pair p) and a 16-row tile's codes, exact in int8, the second: lane
+// (g, j) then receives the four digit dots of pair g with weight row j, and
+// a block adds
+//     scale_j * s_b * 2^-7 ((D0 2^7 + D1) + (D2 2^7 + D3) 2^-14) + zp_j * sum(x_b)
+// to the pair's fp32 accumulator for row j (the scale's 2^-7 is folded
+// into s_b). The codes need no conversion
+// (the bf16 form of this kernel spent 16 byte permutes per tile and block
+// turning them into bf16, and 54 vector instructions per 4 matrix-core
+// ones in all). An item holds up to 16 pairs (four groups of four), so an
+// expert's weights are streamed once for most experts of a 256-token
+// prompt (with 8 pairs per item, an expert routed ~16 pairs read its
+// matrices twice: ~270 MB per launch where the experts hold ~110 MB). The
+// item's X rows are digitised once into LDS; each wave streams whole row
 // tiles of the expert (tiles w, w + 8, ...) through the full K, GG_LA
-// blocks of codes in flight across tile boundaries, in whole unguarded
-// rounds (units past the wave's last read zeros and are dropped), and puts
-// each tile's 16 rows x M columns (hi + lo added) into LDS; the workgroup
-// writes Y once at the end, so no global store sits inside the stream to
-// hold up its loads. Items are spread so
-// that consecutive items (one expert's runs) share an XCD and its L2:
-// workgroup b takes item (b % 8) * S + b / 8 with S = ceil(nitems / 8).
+// units of codes in flight, in whole unguarded rounds (units past the
+// wave's last read zeros and are dropped), and writes each finished tile's
+// rows x pairs. Items are spread so that consecutive items (one expert's
+// runs) share an XCD and its L2: workgroup b takes item (b % 8) * S + b / 8
+// with S = ceil(nitems / 8).
 constexpr int GG_WG = 512;
-constexpr int GG_LA = 8;
+constexpr int GG_LA = 8;   // units (tile, block) of codes in flight per wave
+constexpr int GG_CT = 2;   // tiles per chunk: the units of one step
+constexpr int GG_PG = (GEMM_GROUP_COLS + 3) / 4;  // groups of four pairs
 struct GemmGroupArgs {
     const uint8_t* codes;
     const uint8_t* hp;
@@ -798,25 +815,36 @@ struct GemmGroupArgs {
     int rows, rows_pad, nb, xrows;
 };
 
+// Byte of x index k (0..127) of pair p (0..3) digit d in a (block, pair
+// group) digit area: half k >> 6 (1 KiB each), lane group k & 3 (256 B:
+// 16 rows of 16 bytes), row 4p + d, byte ((k >> 3) & 7) + 8 ((k >> 2) & 1):
+// the order in which lane group g's 16-byte code word holds the codes.
+__device__ __forceinline__ int gg_pos(int k, int p, int d)
+{
+    return (k >> 6) * 1024 + (k & 3) * 256 + (4 * p + d) * 16 + ((k >> 3) & 7) + 8 * ((k >> 2) & 1);
+}
+
 template <int SCHEME>
 __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
 {
-    __shared__ __align__(16) u32x4 xb[GEMM_GROUP_MAXBK][4][64];
-    __shared__ float psum[GEMM_GROUP_MAXBK][2][16];
-    __shared__ float ys[GEMM_GROUP_COLS][GEMM_GROUP_MAXROWS];
+    __shared__ __align__(16) int8_t xd[GEMM_GROUP_MAXBK][GG_PG][2048];       // digits
+    __shared__ float2 xs[GEMM_GROUP_MAXBK][GG_PG * 4];                       // {s_b, sum(x_b)}
     const int nitems = *P.nitems;
     const int S = (nitems + 7) / 8;
     const int item = (int)(blockIdx.x % 8) * S + (int)(blockIdx.x / 8);
     if ((int)(blockIdx.x / 8) >= S || item >= nitems) return;  // uniform
     const int e = P.items[3 * item], p0 = P.items[3 * item + 1], M = P.items[3 * item + 2];
-    const int nb = P.nb, K = nb * 128, Mx = 2 * M;
+    const int nb = P.nb, K = nb * 128;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int g = lane >> 4, j = lane & 15;
     const int ntiles = P.rows_pad / TILE_ROWS;
 
-    // this wave's units: (tile wave + 8 * (u / nb), block u % nb)
+    // This wave's tiles are wave, wave + 8, ...; it takes them GG_CT at a
+    // time (a chunk), block by block: step s is block s % nb of chunk s / nb,
+    // and its units are the chunk's tiles at that block, so one read of the
+    // block's digits serves GG_CT tiles.
     const int my_tiles = ntiles > wave ? (ntiles - wave + 7) / 8 : 0;
-    const int nunits = my_tiles * nb;
+    const int nsteps = (my_tiles + GG_CT - 1) / GG_CT * nb;
     const uint8_t* codes = P.codes + (size_t)e * P.ecodes;
     const uint8_t* hpl = P.hp + (size_t)e * P.ehp;
     const uint32_t* params = P.params + (size_t)e * P.eparams;
@@ -824,157 +852,185 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
     const auto crs = buf_rsrc(codes, nrec * (int)CODE_REC);
     const auto hrs = buf_rsrc(SCHEME == 3 ? hpl : codes, SCHEME == 3 ? nrec * (int)HP_REC : 0);
     const auto prs = buf_rsrc(params, nrec * TILE_ROWS * 4);
-    u32x4 cr[GG_LA], pr[GG_LA];
+    u32x4 cr[GG_LA];
     u32x2 hr[GG_LA];
-    // units are requested in order: the next one's record is (lt, lb), its
-    // tile and block; past the wave's units the record index runs past the
-    // range (zeros, never used)
-    int lt = wave, lb = 0;
-    auto load_next = [&](int slot) {
-        const int rec = lt < ntiles ? lt * nb + lb : nrec;
-        cr[slot] = __builtin_amdgcn_raw_buffer_load_b128(crs, rec * (int)CODE_REC + lane * 16, 0, CPOL_NT);
-        if constexpr (SCHEME == 3) hr[slot] = __builtin_amdgcn_raw_buffer_load_b64(hrs, rec * (int)HP_REC + lane * 8, 0, CPOL_NT);
-        pr[slot] = __builtin_amdgcn_raw_buffer_load_b128(prs, rec * 64 + g * 16, 0, CPOL_NT);
+    uint32_t pr[GG_LA];
+    // units are requested in order: the next step's chunk and block are
+    // (lc, lb), unit tt of it tile wave + 8 (GG_CT lc + tt); a tile past the
+    // wave's last (or a step past the end) reads record nrec, past the range
+    // (zeros, never used)
+    int lc = 0, lb = 0;
+    auto load_step = [&](int slot0) {
+#pragma unroll
+        for (int tt = 0; tt < GG_CT; tt++) {
+            const int tl = GG_CT * lc + tt;
+            const int rec = tl < my_tiles ? (wave + 8 * tl) * nb + lb : nrec;
+            const int slot = slot0 + tt;
+            cr[slot] = __builtin_amdgcn_raw_buffer_load_b128(crs, rec * (int)CODE_REC + lane * 16, 0, CPOL_NT);
+            if constexpr (SCHEME == 3)
+                hr[slot] = __builtin_amdgcn_raw_buffer_load_b64(hrs, rec * (int)HP_REC + lane * 8, 0, CPOL_NT);
+            pr[slot] = __builtin_amdgcn_raw_buffer_load_b32(prs, (rec * TILE_ROWS + j) * 4, 0, CPOL_NT);
+        }
         if (++lb == nb) {
             lb = 0;
-            lt += 8;
+            lc++;
         }
     };
 
-    // ---- X: task (row c < M, block blk, half h) loads 64 consecutive k of
-    // X row rowidx[p0 + c] as 16 pieces of 16 bytes (one task per thread)
-    const int ntask = M * nb * 2;
-    const int t = threadIdx.x;
-    const int c = t % M, blk = (t / M) >> 1, h = (t / M) & 1;
-    const int xr = t < ntask ? (P.rowidx ? P.rowidx[p0 + c] : p0 + c) : 0;
+    // ---- X: task (pair c, block blk) is 128 values, 32 lanes with four
+    // consecutive values each; a wave takes two tasks at a time (tasks
+    // 2*(wave + 8i) and +1), every load of every task issued first
+    constexpr int XT = (GEMM_GROUP_COLS * GEMM_GROUP_MAXBK + 15) / 16;  // task pairs per wave at most
+    const int ntask = M * nb;
     const auto xrs = buf_rsrc(P.x, P.xrows * K * 4);
-    u32x4 xv[16];
-    const int base = t < ntask ? (xr * K + blk * 128 + 64 * h) * 4 : 0x7FFFFFF0;
+    const int hi = lane >> 5, k0 = 4 * (lane & 31);
+    u32x4 xv[XT];
 #pragma unroll
-    for (int q = 0; q < 16; q++) xv[q] = __builtin_amdgcn_raw_buffer_load_b128(xrs, base + q * 16, 0, 0);
+    for (int i = 0; i < XT; i++) {
+        const int t = 2 * (wave + 8 * i) + hi;
+        const int c = t % max(M, 1), blk = t / max(M, 1);
+        const int xr = t < ntask ? (P.rowidx ? P.rowidx[p0 + c] : p0 + c) : 0;
+        const int off = t < ntask ? (xr * K + blk * 128 + k0) * 4 : 0x7FFFFFF0;
+        xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
+    }
 #pragma unroll
-    for (int u = 0; u < GG_LA; u++) load_next(u);
+    for (int u = 0; u < GG_LA; u += GG_CT) load_step(u);
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- pack: hi into fragment column c, lo into column M + c; fragment
-    // (i = 2h + ii, lane group gg) slot s <- piece s, element gg + 4 ii
-    if (t < ntask) {
-        uint32_t ph[8][4], pl[8][4];
+    // ---- digits: the block's max |x| and sum over its 32 lanes (DPP inside
+    // rows of 16, then the row swap), then Q and its four digits into LDS
 #pragma unroll
-        for (int q = 0; q < 8; q++) {
-            const u32x4 a = xv[2 * q], b = xv[2 * q + 1];
-            ph[q][0] = pk_bf16(__uint_as_float(a.x), __uint_as_float(a.y));
-            ph[q][1] = pk_bf16(__uint_as_float(a.z), __uint_as_float(a.w));
-            ph[q][2] = pk_bf16(__uint_as_float(b.x), __uint_as_float(b.y));
-            ph[q][3] = pk_bf16(__uint_as_float(b.z), __uint_as_float(b.w));
-            pl[q][0] = pk_bf16(lo_of(a.x), lo_of(a.y));
-            pl[q][1] = pk_bf16(lo_of(a.z), lo_of(a.w));
-            pl[q][2] = pk_bf16(lo_of(b.x), lo_of(b.y));
-            pl[q][3] = pk_bf16(lo_of(b.z), lo_of(b.w));
+    for (int i = 0; i < XT; i++) {
+        const int t0 = 2 * (wave + 8 * i);
+        if (t0 >= ntask) break;  // uniform per wave
+        const int t = t0 + hi;
+        const int c = t % max(M, 1), blk = t / max(M, 1);
+        const float v[4] = {__uint_as_float(xv[i].x), __uint_as_float(xv[i].y), __uint_as_float(xv[i].z),
+                            __uint_as_float(xv[i].w)};
+        uint32_t mb = __float_as_uint(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+        float sm = (v[0] + v[1]) + (v[2] + v[3]);
+        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0xB1, 0xF, 0xF, false));
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
+        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x4E, 0xF, 0xF, false));
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
+        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x141, 0xF, 0xF, false));
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x141, 0xF, 0xF, false));
+        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x140, 0xF, 0xF, false));
+        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x140, 0xF, 0xF, false));
+        const auto mr = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
+        const float Mx = __uint_as_float(max((uint32_t)mr[0], (uint32_t)mr[1]));
+        const auto sr = __builtin_amdgcn_permlane16_swap(__float_as_uint(sm), __float_as_uint(sm), false, false);
+        const float Sx = __uint_as_float(sr[0]) + __uint_as_float(sr[1]);
+        const float inv = Mx > 0.0f ? (127.0f * 2097152.0f) * __builtin_amdgcn_rcpf(Mx) : 0.0f;
+        if (t < ntask) {
+            int8_t* dst = &xd[blk][c >> 2][0];
+            const int p = c & 3;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int Q = (int)rintf(v[q] * inv);
+                const int k = k0 + q;
+                dst[gg_pos(k, p, 0)] = (int8_t)(Q >> 21);
+                dst[gg_pos(k, p, 1)] = (int8_t)((Q >> 14) & 127);
+                dst[gg_pos(k, p, 2)] = (int8_t)((Q >> 7) & 127);
+                dst[gg_pos(k, p, 3)] = (int8_t)(Q & 127);
+            }
+            if ((lane & 31) == 0) xs[blk][c] = make_float2(Mx * (1.0f / 127.0f) * 0x1p-7f, Sx);  // s_b 2^-7
         }
-        float sh = 0.0f, sl = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 8; q++)
-#pragma unroll
-            for (int d = 0; d < 4; d++) {
-                sh += bf16_lo(ph[q][d]) + bf16_hi(ph[q][d]);
-                sl += bf16_lo(pl[q][d]) + bf16_hi(pl[q][d]);
-            }
-        psum[blk][h][c] = sh;
-        psum[blk][h][M + c] = sl;
-#pragma unroll
-        for (int ii = 0; ii < 2; ii++)
-#pragma unroll
-            for (int gg = 0; gg < 4; gg++) {
-                const int d = (gg >> 1) + 2 * ii, odd = gg & 1;
-                u32x4 o;
-                o.x = pick_halves(ph[0][d], ph[1][d], odd);
-                o.y = pick_halves(ph[2][d], ph[3][d], odd);
-                o.z = pick_halves(ph[4][d], ph[5][d], odd);
-                o.w = pick_halves(ph[6][d], ph[7][d], odd);
-                xb[blk][2 * h + ii][gg * 16 + c] = o;
-                o.x = pick_halves(pl[0][d], pl[1][d], odd);
-                o.y = pick_halves(pl[2][d], pl[3][d], odd);
-                o.z = pick_halves(pl[4][d], pl[5][d], odd);
-                o.w = pick_halves(pl[6][d], pl[7][d], odd);
-                xb[blk][2 * h + ii][gg * 16 + M + c] = o;
-            }
     }
-    // zero fragment columns Mx..15 and their sums
-    for (int z = threadIdx.x; z < nb * 2 * (16 - Mx); z += GG_WG) {
-        const int zb = z / (2 * (16 - Mx)), zc = Mx + (z >> 1) % (16 - Mx), zh = z & 1;
-        psum[zb][zh][zc] = 0.0f;
+    // pairs M .. GEMM_GROUP_COLS-1: zero digits and parameters (every pair
+    // group runs unconditionally: a branch per group split the units'
+    // matrix-core chains apart)
+    for (int z = threadIdx.x; z < nb * (GEMM_GROUP_COLS - M) * 128; z += GG_WG) {
+        const int c = M + z / (nb * 128), r = z % (nb * 128), blk = r >> 7, k = r & 127;
+        int8_t* dst = &xd[blk][c >> 2][0];
 #pragma unroll
-        for (int ii = 0; ii < 2; ii++)
-#pragma unroll
-            for (int gg = 0; gg < 4; gg++) xb[zb][2 * zh + ii][gg * 16 + zc] = u32x4{0u, 0u, 0u, 0u};
+        for (int d = 0; d < 4; d++) dst[gg_pos(k, c & 3, d)] = 0;
+        if (k == 0) xs[blk][c] = make_float2(0.0f, 0.0f);
     }
     __syncthreads();
 
-    // ---- the unit stream, whole rounds of GG_LA, two units at a time (two
-    // independent matrix-core chains, then their epilogues in unit order)
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    int ub = 0, ut = wave;  // block and tile of the next unit to finish
-    auto dots = [&](int slot, int blk) -> f32x4 {
-        bf16x8 B[4];
+    // ---- the step stream, whole rounds of GG_LA / GG_CT steps: per step the
+    // block's digits (every pair group, both halves) and {s_b, sum} once, then
+    // the chunk's GG_CT tiles, GG_PG independent matrix-core chains each,
+    // then their epilogues
+    float acc[GG_CT][GG_PG], zacc[GG_CT][GG_PG];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const u32x4 w = xb[blk][i][lane];
-            __builtin_memcpy(&B[i], &w, 16);
+    for (int tt = 0; tt < GG_CT; tt++)
+#pragma unroll
+        for (int q = 0; q < GG_PG; q++) acc[tt][q] = zacc[tt][q] = 0.0f;
+    int ub = 0, uc = 0;  // block and chunk of the next step to finish
+    auto step = [&](int slot0) {
+        v4i A0[GG_PG], A1[GG_PG];
+        float2 sx[GG_PG];
+#pragma unroll
+        for (int pg = 0; pg < GG_PG; pg++) {
+            const int8_t* a = &xd[ub][pg][g * 256 + j * 16];
+            A0[pg] = *reinterpret_cast<const v4i*>(a);
+            A1[pg] = *reinterpret_cast<const v4i*>(a + 1024);
+            sx[pg] = xs[ub][pg * 4 + g];
         }
-        const u32x4 U = cr[slot];
-        const uint32_t MK = 0x0F0F0F0Fu;
-        u32x4 lo = {U.x & MK, U.y & MK, U.z & MK, U.w & MK};
-        u32x4 hi = {(U.x >> 4) & MK, (U.y >> 4) & MK, (U.z >> 4) & MK, (U.w >> 4) & MK};
-        if constexpr (SCHEME == 3) {
-            const uint32_t T6 = 0x30303030u, hx = hr[slot].x, hy = hr[slot].y;
-            lo.x |= (hx << 4) & T6; lo.y |= (hx << 2) & T6;
-            lo.z |= (hy << 4) & T6; lo.w |= (hy << 2) & T6;
-            hi.x |= hx & T6;        hi.y |= (hx >> 2) & T6;
-            hi.z |= hy & T6;        hi.w |= (hy >> 2) & T6;
+        v4i D[GG_CT][GG_PG];
+#pragma unroll
+        for (int tt = 0; tt < GG_CT; tt++) {
+            const int slot = slot0 + tt;
+            const u32x4 U = cr[slot];
+            const uint32_t MK = 0x0F0F0F0Fu;
+            v4i lo = {(int)(U.x & MK), (int)(U.y & MK), (int)(U.z & MK), (int)(U.w & MK)};
+            v4i hi = {(int)((U.x >> 4) & MK), (int)((U.y >> 4) & MK), (int)((U.z >> 4) & MK), (int)((U.w >> 4) & MK)};
+            if constexpr (SCHEME == 3) {
+                // top two bits: group g holds AVX lanes g (h.x) and g+4 (h.y)
+                const uint32_t T6 = 0x30303030u, hx = hr[slot].x, hy = hr[slot].y;
+                lo.x |= (int)((hx << 4) & T6); lo.y |= (int)((hx << 2) & T6);
+                lo.z |= (int)((hy << 4) & T6); lo.w |= (int)((hy << 2) & T6);
+                hi.x |= (int)(hx & T6);        hi.y |= (int)((hx >> 2) & T6);
+                hi.z |= (int)(hy & T6);        hi.w |= (int)((hy >> 2) & T6);
+            }
+#pragma unroll
+            for (int pg = 0; pg < GG_PG; pg++) {
+                D[tt][pg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0[pg], lo, v4i{0, 0, 0, 0}, 0, 0, 0);
+                D[tt][pg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1[pg], hi, D[tt][pg], 0, 0, 0);
+            }
         }
-        f32x4 D = {0.f, 0.f, 0.f, 0.f};
-        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(lo.x, lo.y), B[0], D, 0, 0, 0);
-        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(lo.z, lo.w), B[1], D, 0, 0, 0);
-        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(hi.x, hi.y), B[2], D, 0, 0, 0);
-        D = __builtin_amdgcn_mfma_f32_16x16x32_bf16(codes_bf16(hi.z, hi.w), B[3], D, 0, 0, 0);
-        return D;
-    };
-    auto finish = [&](int slot, const f32x4& D) {
-        const float Sx = psum[ub][0][j] + psum[ub][1][j];
-        const u32x4 pp = pr[slot];
-        acc[0] = __builtin_fmaf(zp_off(pp.x), Sx, __builtin_fmaf(h2f(pp.x >> 16), D[0], acc[0]));
-        acc[1] = __builtin_fmaf(zp_off(pp.y), Sx, __builtin_fmaf(h2f(pp.y >> 16), D[1], acc[1]));
-        acc[2] = __builtin_fmaf(zp_off(pp.z), Sx, __builtin_fmaf(h2f(pp.z >> 16), D[2], acc[2]));
-        acc[3] = __builtin_fmaf(zp_off(pp.w), Sx, __builtin_fmaf(h2f(pp.w >> 16), D[3], acc[3]));
-        if (++ub == nb) {  // the tile is complete: hi + lo into LDS, next tile
 #pragma unroll
-            for (int q = 0; q < 4; q++) acc[q] += __shfl(acc[q], lane + M);
-            if (ut < ntiles && j < M)
+        for (int tt = 0; tt < GG_CT; tt++) {
+            const uint32_t pp = pr[slot0 + tt];
+            const float sc = h2f(pp >> 16), zp = h2f(pp & 0xFFFFu);
 #pragma unroll
-                for (int q = 0; q < 4; q++) ys[j][ut * TILE_ROWS + 4 * g + q] = acc[q];
-            acc = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int pg = 0; pg < GG_PG; pg++) {
+                // D0 2^7 + D1 and D2 2^7 + D3 are exact in int32 (|D| < 2^21),
+                // so the digit sum is two conversions and one fma
+                const v4i& d = D[tt][pg];
+                const float dh = (float)(d.x * 128 + d.y), dl = (float)(d.z * 128 + d.w);
+                const float cd = fmaf(dl, 0x1p-14f, dh);
+                acc[tt][pg] = __builtin_fmaf(cd * sx[pg].x, sc, acc[tt][pg]);
+                zacc[tt][pg] = __builtin_fmaf(zp, sx[pg].y, zacc[tt][pg]);
+            }
+        }
+        if (++ub == nb) {  // the chunk is complete: lane (g, j) has pair pg*4 + g, row j of each tile
+#pragma unroll
+            for (int tt = 0; tt < GG_CT; tt++) {
+                const int tl = GG_CT * uc + tt;
+                const int row = (wave + 8 * tl) * TILE_ROWS + j;
+                if (tl < my_tiles && row < P.rows) {
+#pragma unroll
+                    for (int pg = 0; pg < GG_PG; pg++)
+                        if (pg * 4 + g < M) P.y[(size_t)(p0 + pg * 4 + g) * P.rows + row] = acc[tt][pg] + zacc[tt][pg];
+                }
+#pragma unroll
+                for (int pg = 0; pg < GG_PG; pg++) acc[tt][pg] = zacc[tt][pg] = 0.0f;
+            }
             ub = 0;
-            ut += 8;
+            uc++;
         }
     };
-    static_assert(GG_LA % 2 == 0, "units go in pairs");
-    const int rounds = (nunits + GG_LA - 1) / GG_LA * GG_LA;
-    for (int u0 = 0; u0 < rounds; u0 += GG_LA) {
+    constexpr int SPR = GG_LA / GG_CT;  // steps per round
+    const int rounds = (nsteps + SPR - 1) / SPR * SPR;
+    for (int s0 = 0; s0 < rounds; s0 += SPR) {
 #pragma unroll
-        for (int k = 0; k < GG_LA; k += 2) {
-            const int b1 = ub + 1 == nb ? 0 : ub + 1;  // the second unit's block
-            const f32x4 D0 = dots(k, ub), D1 = dots(k + 1, b1);
-            finish(k, D0);
-            finish(k + 1, D1);
-            load_next(k);
-            load_next(k + 1);
+        for (int k = 0; k < SPR; k++) {
+            step(k * GG_CT);
+            load_step(k * GG_CT);
         }
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < M * P.rows; i += GG_WG) {
-        const int jj = i / P.rows, r = i % P.rows;
-        P.y[(size_t)(p0 + jj) * P.rows + r] = ys[jj][r];
     }
 }
 

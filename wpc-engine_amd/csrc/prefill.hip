@@ -66,27 +66,48 @@ __global__ __launch_bounds__(256) void k_pf_router(const float* __restrict__ X, 
 // sorted position of pair q; work items {expert, first sorted pair, count
 // <= GEMM_GROUP_COLS} cover every expert's run. One workgroup; slots with
 // id < 0 (fewer finite probabilities than top_k) belong to no expert.
+// A token's top_k experts are distinct (route() picks each index at most
+// once), so the pairs of one expert come from distinct tokens, in token
+// order: the rank of pair (t, k) in its expert's run is the number of
+// tokens before t that chose the expert. Each expert keeps a bitmask of
+// the tokens that chose it; a pair's rank is the popcount of the bits below
+// its token, computed by every pair at once. (A stable placement by one
+// ballot per expert and 64 pairs, in order, took 25 us for 2048 pairs.)
 constexpr int GR_WG = 1024;
+constexpr int GR_TW = PF_GROUP_MAXT / 32;          // bitmask words per expert
+constexpr int GR_PT = PF_MAX_PAIRS / GR_WG;        // pairs per thread at most
 __global__ __launch_bounds__(GR_WG) void k_pf_group(const int32_t* __restrict__ ids, int P, int E,
                                                     int top_k, int* __restrict__ pair_tok,
                                                     int* __restrict__ pair_pos, int* __restrict__ items,
                                                     int* __restrict__ nitems)
 {
-    __shared__ int sid[PF_MAX_PAIRS];
-    __shared__ int cnt[ROUTE_MAXN], off[ROUTE_MAXN], ioff[ROUTE_MAXN];
-    for (int e = threadIdx.x; e < E; e += GR_WG) cnt[e] = 0;
-    for (int q = threadIdx.x; q < P; q += GR_WG) sid[q] = ids[q];
+    __shared__ uint32_t tmask[ROUTE_MAXN][GR_TW];
+    __shared__ int off[ROUTE_MAXN], ioff[ROUTE_MAXN];
+    for (int i = threadIdx.x; i < E * GR_TW; i += GR_WG) tmask[i / GR_TW][i % GR_TW] = 0u;
+    int myid[GR_PT];
+#pragma unroll
+    for (int u = 0; u < GR_PT; u++) {
+        const int q = threadIdx.x + u * GR_WG;
+        myid[u] = q < P ? ids[q] : -1;
+    }
     __syncthreads();
-    for (int q = threadIdx.x; q < P; q += GR_WG) {
-        const int e = sid[q];
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+#pragma unroll
+    for (int u = 0; u < GR_PT; u++) {
+        const int q = threadIdx.x + u * GR_WG;
+        if (q >= P) break;
+        const int e = myid[u], t = q / top_k;
+        if (e >= 0 && e < E) atomicOr(&tmask[e][t >> 5], 1u << (t & 31));
         else pair_pos[q] = -1;
     }
     __syncthreads();
     // exclusive prefix sums of the counts and of the item counts (E <= 256:
     // a Hillis-Steele scan over LDS)
     const int e_me = threadIdx.x;
-    int c_me = e_me < E ? cnt[e_me] : 0, i_me = (c_me + GEMM_GROUP_COLS - 1) / GEMM_GROUP_COLS;
+    int c_me = 0;
+    if (e_me < E)
+#pragma unroll
+        for (int w = 0; w < GR_TW; w++) c_me += __popc(tmask[e_me][w]);
+    const int i_me = (c_me + GEMM_GROUP_COLS - 1) / GEMM_GROUP_COLS;
     if (e_me < ROUTE_MAXN) {
         off[e_me] = c_me;
         ioff[e_me] = i_me;
@@ -111,35 +132,25 @@ __global__ __launch_bounds__(GR_WG) void k_pf_group(const int32_t* __restrict__ 
     }
     if (e_me == ROUTE_MAXN - 1) *nitems = ioff[e_me] + i_me;
     __syncthreads();
-    // stable placement: wave w takes experts w, w + 16, ... (at most
-    // ROUTE_MAXN / 16 of them) and walks the pairs 64 at a time; a ballot
-    // per expert gives each match its rank among the earlier matches
-    constexpr int EPW = ROUTE_MAXN / (GR_WG / 64);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    int run[EPW];
+    // every pair's place: its expert's offset plus the tokens before its own
 #pragma unroll
-    for (int u = 0; u < EPW; u++) run[u] = wave + 16 * u < E ? off[wave + 16 * u] : 0;
-    for (int q0 = 0; q0 < P; q0 += 64) {
-        const int q = q0 + lane;
-        const int myid = q < P ? sid[q] : -1;
-#pragma unroll
-        for (int u = 0; u < EPW; u++) {
-            const int e = wave + 16 * u;
-            const bool hit = myid == e;
-            const uint64_t mask = __ballot(hit);
-            if (hit) {
-                const int at = run[u] + __popcll(mask & ((1ull << lane) - 1));
-                pair_tok[at] = q / top_k;
-                pair_pos[q] = at;
-            }
-            run[u] += __popcll(mask);
-        }
+    for (int u = 0; u < GR_PT; u++) {
+        const int q = threadIdx.x + u * GR_WG;
+        if (q >= P) break;
+        const int e = myid[u];
+        if (e < 0 || e >= E) continue;
+        const int t = q / top_k, tw = t >> 5;
+        int rank = __popc(tmask[e][tw] & ((1u << (t & 31)) - 1u));
+        for (int w = 0; w < tw; w++) rank += __popc(tmask[e][w]);
+        const int at = off[e] + rank;
+        pair_tok[at] = t;
+        pair_pos[q] = at;
     }
-    for (int e = threadIdx.x; e < E; e += GR_WG)
-        for (int c = 0, i = ioff[e]; c < cnt[e]; c += GEMM_GROUP_COLS, i++) {
-            items[3 * i] = e;
-            items[3 * i + 1] = off[e] + c;
-            items[3 * i + 2] = min(GEMM_GROUP_COLS, cnt[e] - c);
+    if (e_me < E)
+        for (int c = 0, i = ioff[e_me]; c < c_me; c += GEMM_GROUP_COLS, i++) {
+            items[3 * i] = e_me;
+            items[3 * i + 1] = off[e_me] + c;
+            items[3 * i + 2] = min(GEMM_GROUP_COLS, c_me - c);
         }
 }
 
@@ -173,7 +184,10 @@ hipError_t launch_pf_router(const float* X, const float* W, int T, int E, int K,
 hipError_t launch_pf_group(const int32_t* ids, int P, int E, int top_k, int* pair_tok, int* pair_pos, int* items,
                            int* nitems, hipStream_t s)
 {
-    if (P < 1 || P > PF_MAX_PAIRS || E < 1 || E > ROUTE_MAXN) return hipErrorInvalidValue;
+    // the tokens' bitmasks hold PF_GROUP_MAXT tokens
+    if (P < 1 || P > PF_MAX_PAIRS || E < 1 || E > ROUTE_MAXN || top_k < 1 || P / top_k > PF_GROUP_MAXT ||
+        P % top_k)
+        return hipErrorInvalidValue;
     (void)hipGetLastError();
     hipLaunchKernelGGL(k_pf_group, dim3(1), dim3(GR_WG), 0, s, ids, P, E, top_k, pair_tok, pair_pos, items, nitems);
     return hipGetLastError();

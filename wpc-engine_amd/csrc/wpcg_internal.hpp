@@ -232,9 +232,10 @@ hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, 
 // {expert, first pair p0, count <= GEMM_GROUP_COLS}; its column c reads X
 // row rowidx[p0 + c] (null: row p0 + c, X has xrows rows) and writes Y row
 // p0 + c. *nitems (device) items are live; max_items bounds the grid.
-// Needs m.nb <= GEMM_GROUP_MAXBK (the item's X sits in LDS whole) and
-// m.rows_pad <= GEMM_GROUP_MAXROWS (so does its Y).
-constexpr int GEMM_GROUP_COLS = 8;
+// Needs m.nb <= GEMM_GROUP_MAXBK (the item's X digits sit in LDS whole) and
+// m.rows_pad <= GEMM_GROUP_MAXROWS (keeps every buffer offset of an expert's
+// planes well inside 32 bits).
+constexpr int GEMM_GROUP_COLS = 16;
 constexpr int GEMM_GROUP_MAXBK = 16;
 constexpr int GEMM_GROUP_MAXROWS = 2048;
 // Many rows of fp32 X in the SPLIT mode as one launch per matrix: X packed
@@ -354,6 +355,7 @@ hipError_t launch_pf_router(const float* X, const float* W, int T, int E, int K,
 // (token, slot) pairs sorted by expert for launch_gemm_grouped: pair_tok
 // [P], pair_pos [P], items [3 * (P / GEMM_GROUP_COLS + E)], nitems [1].
 constexpr int PF_MAX_PAIRS = 8192;
+constexpr int PF_GROUP_MAXT = 256;  // tokens per grouping (the prefill pass holds at most 256 rows)
 hipError_t launch_pf_group(const int32_t* ids, int P, int E, int top_k, int* pair_tok, int* pair_pos, int* items,
                            int* nitems, hipStream_t s);
 hipError_t launch_pf_combine(float* X, const float* D, const float* w, const int* pair_pos, int T, int top_k, int H,
