@@ -434,9 +434,12 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
         Layer& L = m->layers[l];
         WPCG_HIP(launch_rms_norm_rows(F, P.x, L.in_ln, H, (int)n, c.eps, P.xn, s));
         WPCG_HIP(launch_gemm_pack_rows(P.xn, (int)n, H, P.xf, P.xsum, s));
-        WPCG_HIP(launch_gemm_packed_rows(L.q->m, P.xf, P.xsum, (int)n, L.q->bias, nullptr, P.q, s));
-        WPCG_HIP(launch_gemm_packed_rows(L.k->m, P.xf, P.xsum, (int)n, L.k->bias, nullptr, P.k, s));
-        WPCG_HIP(launch_gemm_packed_rows(L.v->m, P.xf, P.xsum, (int)n, L.v->bias, nullptr, P.v, s));
+        {
+            const DeviceMatrix* ms[3] = {&L.q->m, &L.k->m, &L.v->m};
+            const float* bs[3] = {L.q->bias, L.k->bias, L.v->bias};
+            float* ys[3] = {P.q, P.k, P.v};
+            WPCG_HIP(launch_gemm_packed_rows_multi(ms, bs, ys, 3, P.xf, P.xsum, (int)n, s));
+        }
         float* kc = m->kc + (size_t)l * nkv * c.max_pos * hd;
         float* vc = m->vc + (size_t)l * nkv * c.max_pos * hd;
         WPCG_HIP(launch_prefill_attention(P.q, P.k, P.v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale, m->cos_t,
@@ -447,8 +450,10 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
         WPCG_HIP(launch_rms_norm_rows(F, P.x, L.post_ln, H, (int)n, c.eps, P.xn, s));
         if (!c.n_experts) {
             WPCG_HIP(launch_gemm_pack_rows(P.xn, (int)n, H, P.xf, P.xsum, s));
-            WPCG_HIP(launch_gemm_packed_rows(L.gate->m, P.xf, P.xsum, (int)n, L.gate->bias, nullptr, P.g, s));
-            WPCG_HIP(launch_gemm_packed_rows(L.up->m, P.xf, P.xsum, (int)n, L.up->bias, nullptr, P.u, s));
+            const DeviceMatrix* ms[2] = {&L.gate->m, &L.up->m};
+            const float* bs[2] = {L.gate->bias, L.up->bias};
+            float* ys[2] = {P.g, P.u};
+            WPCG_HIP(launch_gemm_packed_rows_multi(ms, bs, ys, 2, P.xf, P.xsum, (int)n, s));
             WPCG_HIP(launch_silu_mul(P.g, P.u, P.g, (size_t)n * c.inter, s));
             WPCG_HIP(launch_gemm_pack_rows(P.g, (int)n, (int)c.inter, P.xf, P.xsum, s));
             WPCG_HIP(launch_gemm_packed_rows(L.down->m, P.xf, P.xsum, (int)n, L.down->bias, P.x, P.x, s));
@@ -460,12 +465,13 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
         const int ne = (int)c.n_experts, K = (int)c.top_k, pairs = (int)n * K;
         const int max_items = pairs / GEMM_GROUP_COLS + ne + 1;
         WPCG_HIP(launch_pf_router(P.xn, E->router->w, (int)n, ne, H, P.r, s));
-        WPCG_HIP(launch_softmax_route_rows(P.r, ne, (int)n, K, (int)c.norm_topk, P.ids, P.w, s));
+        WPCG_HIP(launch_route_rows(P.r, ne, (int)n, K, (int)c.norm_topk, P.ids, P.w, s));
         WPCG_HIP(launch_pf_group(P.ids, pairs, ne, K, P.pair_tok, P.pair_pos, P.items, P.nitems, s));
-        WPCG_HIP(launch_gemm_grouped(E->gate, P.xn, (int)n, P.pair_tok, P.items, P.nitems, max_items, P.ge, s));
-        WPCG_HIP(launch_gemm_grouped(E->up, P.xn, (int)n, P.pair_tok, P.items, P.nitems, max_items, P.ue, s));
-        WPCG_HIP(launch_silu_mul(P.ge, P.ue, P.ge, (size_t)pairs * c.moe_inter, s));
-        WPCG_HIP(launch_gemm_grouped(E->down, P.ge, pairs, nullptr, P.items, P.nitems, max_items, P.de, s));
+        WPCG_HIP(launch_gemm_grouped(E->gate, P.xn, nullptr, (int)n, P.pair_tok, P.items, P.nitems, max_items, P.ge,
+                                     s));
+        WPCG_HIP(launch_gemm_grouped(E->up, P.xn, nullptr, (int)n, P.pair_tok, P.items, P.nitems, max_items, P.ue,
+                                     s));
+        WPCG_HIP(launch_gemm_grouped(E->down, P.ge, P.ue, pairs, nullptr, P.items, P.nitems, max_items, P.de, s));
         WPCG_HIP(launch_pf_combine(P.x, P.de, P.w, P.pair_pos, (int)n, K, H, s));
     }
     return WPCG_OK;

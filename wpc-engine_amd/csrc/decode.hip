@@ -451,7 +451,6 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
 // part_ml[c][h][0..1], h the query head. Sums are fixed-order trees and
 // fused multiply-adds: deterministic, not the reference's operation order.
 // head_dim HD is 64 or 128, n_rep <= FA_MAXREP.
-constexpr int FA_WG = 256;  // the batched prefill's attention
 constexpr int FA_C = 32;
 constexpr int FA_NCH = ATTN_CHUNKS;
 constexpr int FA_MAXREP = 16;
@@ -782,150 +781,232 @@ __global__ __launch_bounds__(256) void k_pf_qk_rope(float* __restrict__ Q, const
     }
 }
 
-// Causal attention of query token t (position p = pos0 + t) over positions
-// 0..p of the caches, for the n_rep query heads of kv head j: workgroup
-// (j, t). Keys and values pass through LDS in blocks of FA_C positions
-// (the next block's loads in flight), with a running softmax per head as
-// in k_attention_fast; the output is o / l, written to O [n][nh*HD].
-template <int HD>
-__global__ __launch_bounds__(FA_WG) void k_pf_attention(const float* __restrict__ Q, int nh, int nkv, float scale,
-                                                        int pos0, int max_pos, const float* __restrict__ kc,
-                                                        const float* __restrict__ vc, float* __restrict__ O)
+// ---- the batched prefill's causal attention, on the fp32 matrix cores ----
+// Query token t sits at position pos0 + t and sees positions 0..pos0 + t of
+// the caches. Workgroup (NHW query heads of one key head, block of 16 query
+// rows); its PA_W waves split the block's 16-position key tiles (wave w:
+// tiles w, w + PA_W, ...), each with a running softmax per head, and merge
+// their states pairwise through LDS at the end (a fixed tree: wave w takes
+// wave w + PA_W/2, then w + PA_W/4, ...). Per tile a wave forms each head's scores
+// transposed, S^T = K Q^T, in HD/4 steps of v_mfma_f32_16x16x4_f32: lane
+// (kq, c) supplies key row c of the tile and query row c at the same dim in
+// each step (read straight into registers). The product leaves lane (kq, c)
+// the scores of query row c at tile positions 4kq..4kq+3, which, once
+// exponentiated, are as they lie the second operand of O^T += V^T P^T (four
+// steps of k = 4 positions; lane (kq, c) supplies V[position 4kq + i][a dim
+// of column c] for each output tile): that product leaves lane (kq, c)
+// holding query row c, so the softmax rescale is lane-local and only the
+// row maximum crosses lanes (the row's four lane groups, by the 16- and
+// 32-lane swaps). A wave serves NHW heads of one key head with each tile
+// it loads; the launch uses one (NHW = 2 halves the loads, but doubles the
+// matrix-core work per SIMD, and that, with the load latency, sets the
+// time: 17.5 us for the 256-token, 32-head prefill against 12 with one).
+// Scores are in the log2 domain (Q scaled by scale * log2 e on load) and
+// exponentials are exp2. Rows of the last block past n are computed from
+// row n - 1 and not stored; positions past the block's last are masked and
+// their loads read row pos0 + n - 1. Deterministic; not the stepwise
+// attention's operation order (FAST mode).
+template <int HD, int NHW, int PA_W>
+__global__ __launch_bounds__(PA_W * 64) void k_pf_attention(const float* __restrict__ Q, int nh, int nkv,
+                                                            float scale, int pos0, int n, int max_pos,
+                                                            const float* __restrict__ kc,
+                                                            const float* __restrict__ vc, float* __restrict__ O)
 {
-    constexpr int HD4 = HD / 4, KS = HD + 4;
-    constexpr int NOUT = FA_MAXREP * HD / FA_WG;
-    constexpr int G = FA_WG / HD;
-    constexpr int NKV = FA_C * HD4 / FA_WG;
-    __shared__ __align__(16) float qs[FA_MAXREP][HD];
-    __shared__ __align__(16) float ks[FA_C][KS];
-    __shared__ __align__(16) float vs[FA_C][HD];
-    __shared__ float ps[FA_MAXREP][FA_C];
-    __shared__ __align__(16) float pt[FA_C][FA_MAXREP + 4];
-    __shared__ float s_m[FA_MAXREP], s_l[FA_MAXREP], s_corr[FA_MAXREP];
-    const int j = blockIdx.x, t = blockIdx.y;
-    const int n = pos0 + t + 1, n_rep = nh / nkv;
+    constexpr int DL = HD / 4;    // dims per lane in the score product
+    constexpr int NDT = HD / 16;  // output tiles of 16 dims
+    constexpr int OS = HD + 4;    // LDS row stride of the merge
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    __shared__ float sm_m[PA_W / 2][NHW][16], sm_l[PA_W / 2][NHW][16];
+    __shared__ __align__(16) float so[PA_W / 2][NHW][16][OS];
+    // the longest blocks first, then the shortest: the second half of the
+    // launch (which shares the CUs with the first) in the reverse order, so
+    // that a CU's two workgroups hold about the same work
+    const int ny = (int)gridDim.y, hy = (ny + 1) / 2, y = (int)blockIdx.y;
+    const int h0 = blockIdx.x * NHW, qb = y < hy ? ny - 1 - y : y - hy;
+    const int j = h0 / (nh / nkv);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, kq = lane >> 4, c = lane & 15;
+    const int qpos = pos0 + 16 * qb + c;                   // this lane's query row's position
+    const int last = pos0 + min(16 * qb + 15, n - 1);      // the block's last position
+    const int plim = pos0 + n - 1;                         // last cache row the loads may read
+    const int ntiles = last / 16 + 1;
     const float* kb = kc + (size_t)j * max_pos * HD;
     const float* vb = vc + (size_t)j * max_pos * HD;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 
-    // rows past the last position read row n - 1 (never stored to LDS), so
-    // every load is unconditional
-    // (named registers rather than an array, which the compiler kept in
-    // scratch memory here)
-    static_assert(NKV <= 4, "at most four 16-byte loads per thread and block");
-    float4 kr0, kr1, kr2, kr3, vr0, vr1, vr2, vr3;
-#define PF_LOAD_U(U, T0, KR, VR)                                                                    \
-    if constexpr (U < NKV) {                                                                        \
-        const int i = threadIdx.x + U * FA_WG, tt = min((T0) + i / HD4, n - 1), d = 4 * (i % HD4); \
-        KR = *reinterpret_cast<const float4*>(kb + (size_t)tt * HD + d);                           \
-        VR = *reinterpret_cast<const float4*>(vb + (size_t)tt * HD + d);                           \
-    }
-#define PF_LOAD_BLOCK(T0)             \
-    PF_LOAD_U(0, T0, kr0, vr0)         \
-    PF_LOAD_U(1, T0, kr1, vr1)         \
-    PF_LOAD_U(2, T0, kr2, vr2)         \
-    PF_LOAD_U(3, T0, kr3, vr3)
-#define PF_STORE_U(U, KR, VR)                                                \
-    if constexpr (U < NKV) {                                                 \
-        const int i = threadIdx.x + U * FA_WG, tt = i / HD4, dd = 4 * (i % HD4); \
-        if (tt < nt) {                                                       \
-            *reinterpret_cast<float4*>(&ks[tt][dd]) = KR;                    \
-            *reinterpret_cast<float4*>(&vs[tt][dd]) = VR;                    \
-        }                                                                    \
-    }
-    PF_LOAD_BLOCK(0)
-    for (int i = threadIdx.x; i < n_rep * HD; i += FA_WG)
-        qs[i / HD][i % HD] = Q[((size_t)t * nh + j * n_rep) * HD + i];
-    if (threadIdx.x < FA_MAXREP) {
-        s_m[threadIdx.x] = -INFINITY;
-        s_l[threadIdx.x] = 0.0f;
-    }
-    const int g = threadIdx.x / HD, d = threadIdx.x % HD;
-    const int nper = (n_rep + G - 1) / G, r0 = g * nper;
-    float o[NOUT];
+    // Score step s = 4u + i of lane (kq, c) takes dim 16u + 4kq + i (query
+    // and key alike), and output tile dt = 4u + jj row c dim 64u + 4c + jj,
+    // so that one 16-byte load per lane covers 64 contiguous bytes of each
+    // of 16 key rows, or 256 of each of 4 value rows (lanes reading 16 bytes
+    // at a 128-byte stride cost a cache-line access each).
+    float q[NHW][DL];
+    {
+        const float qs = scale * 1.44269504088896341f;
 #pragma unroll
-    for (int u = 0; u < NOUT; u++) o[u] = 0.0f;
-    __syncthreads();
-
-    for (int t0 = 0; t0 < n; t0 += FA_C) {
-        const int nt = min(FA_C, n - t0);
-        PF_STORE_U(0, kr0, vr0)
-        PF_STORE_U(1, kr1, vr1)
-        PF_STORE_U(2, kr2, vr2)
-        PF_STORE_U(3, kr3, vr3)
-        __syncthreads();
-        if (t0 + FA_C < n) {
-            PF_LOAD_BLOCK(t0 + FA_C)
+        for (int hh = 0; hh < NHW; hh++) {
+            const float* qp = Q + ((size_t)min(16 * qb + c, n - 1) * nh + h0 + hh) * HD + 4 * kq;
+#pragma unroll
+            for (int u = 0; u < DL; u += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(qp + 4 * u);
+                q[hh][u] = v.x * qs;
+                q[hh][u + 1] = v.y * qs;
+                q[hh][u + 2] = v.z * qs;
+                q[hh][u + 3] = v.w * qs;
+            }
         }
-        for (int i = threadIdx.x; i < n_rep * FA_C; i += FA_WG) {
-            const int r = i / FA_C, tt = i % FA_C;
-            float dot = -INFINITY;
-            if (tt < nt) {
-                float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    }
+    // Buffer loads: plain loads of a later tile were sunk by the compiler to
+    // their uses. A tile's keys are requested once its scores are formed and
+    // its values once its outputs are, each for the wave's next tile.
+    const auto krs = buf_rsrc(kb, (plim + 1) * HD * 4), vrs = buf_rsrc(vb, (plim + 1) * HD * 4);
+    u32x4 kr[DL / 4], vr[4][NDT / 4];
+    auto load_k = [&](int tile) {
+        const int ko = (min(tile * 16 + c, plim) * HD + 4 * kq) * 4;
 #pragma unroll
-                for (int dd = 0; dd < HD; dd += 4) {
-                    const float4 q4 = *reinterpret_cast<const float4*>(&qs[r][dd]);
-                    const float4 k4 = *reinterpret_cast<const float4*>(&ks[tt][dd]);
-                    a0 = fmaf(q4.x, k4.x, a0);
-                    a1 = fmaf(q4.y, k4.y, a1);
-                    a2 = fmaf(q4.z, k4.z, a2);
-                    a3 = fmaf(q4.w, k4.w, a3);
+        for (int u = 0; u < DL / 4; u++) kr[u] = __builtin_amdgcn_raw_buffer_load_b128(krs, ko + 64 * u, 0, 0);
+    };
+    auto load_v = [&](int tile) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int vo = (min(tile * 16 + 4 * kq + i, plim) * HD + 4 * c) * 4;
+#pragma unroll
+            for (int u = 0; u < NDT / 4; u++) vr[i][u] = __builtin_amdgcn_raw_buffer_load_b128(vrs, vo + 256 * u, 0, 0);
+        }
+    };
+    f32x4 o[NHW][NDT];
+    float m[NHW], l[NHW];
+#pragma unroll
+    for (int hh = 0; hh < NHW; hh++) {
+        m[hh] = -INFINITY;
+        l[hh] = 0.0f;
+#pragma unroll
+        for (int dt = 0; dt < NDT; dt++) o[hh][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (wave < ntiles) {
+        load_k(wave);
+        load_v(wave);
+    }
+    for (int tile = wave; tile < ntiles; tile += PA_W) {
+        const bool more = tile + PA_W < ntiles;
+        f32x4 s[NHW];
+#pragma unroll
+        for (int hh = 0; hh < NHW; hh++) s[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < DL / 4; u++)
+#pragma unroll
+            for (int hh = 0; hh < NHW; hh++) {
+                s[hh] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kr[u].x), q[hh][4 * u], s[hh], 0, 0, 0);
+                s[hh] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kr[u].y), q[hh][4 * u + 1], s[hh], 0, 0, 0);
+                s[hh] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kr[u].z), q[hh][4 * u + 2], s[hh], 0, 0, 0);
+                s[hh] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(kr[u].w), q[hh][4 * u + 3], s[hh], 0, 0, 0);
+            }
+        if (more) load_k(tile + PA_W);
+        __builtin_amdgcn_sched_barrier(0);
+        const int pb = tile * 16 + 4 * kq;
+        float e[NHW][4];
+#pragma unroll
+        for (int hh = 0; hh < NHW; hh++) {
+            float sv[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) sv[i] = pb + i <= qpos ? s[hh][i] : -INFINITY;
+            float mt = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+            const auto r1 = __builtin_amdgcn_permlane16_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+            mt = fmaxf(__uint_as_float(r1[0]), __uint_as_float(r1[1]));
+            const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+            mt = fmaxf(__uint_as_float(r2[0]), __uint_as_float(r2[1]));
+            const float mn = fmaxf(m[hh], mt);
+            const float mr = mn == -INFINITY ? 0.0f : mn;  // a row with every position so far masked
+            const float corr = __builtin_amdgcn_exp2f(m[hh] - mr);
+#pragma unroll
+            for (int i = 0; i < 4; i++) e[hh][i] = __builtin_amdgcn_exp2f(sv[i] - mr);
+            l[hh] = fmaf(l[hh], corr, (e[hh][0] + e[hh][1]) + (e[hh][2] + e[hh][3]));
+            m[hh] = mn;
+#pragma unroll
+            for (int dt = 0; dt < NDT; dt++) o[hh][dt] *= corr;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int u = 0; u < NDT / 4; u++)
+#pragma unroll
+                for (int hh = 0; hh < NHW; hh++) {
+                    f32x4* oo = &o[hh][4 * u];
+                    oo[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(vr[i][u].x), e[hh][i], oo[0], 0, 0, 0);
+                    oo[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(vr[i][u].y), e[hh][i], oo[1], 0, 0, 0);
+                    oo[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(vr[i][u].z), e[hh][i], oo[2], 0, 0, 0);
+                    oo[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(vr[i][u].w), e[hh][i], oo[3], 0, 0, 0);
                 }
-                dot = ((a0 + a1) + (a2 + a3)) * scale;
+        if (more) load_v(tile + PA_W);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // each row's sum over its four lane groups
+#pragma unroll
+    for (int hh = 0; hh < NHW; hh++) {
+        const auto r1 = __builtin_amdgcn_permlane16_swap(__float_as_uint(l[hh]), __float_as_uint(l[hh]), false, false);
+        l[hh] = __uint_as_float(r1[0]) + __uint_as_float(r1[1]);
+        const auto r2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(l[hh]), __float_as_uint(l[hh]), false, false);
+        l[hh] = __uint_as_float(r2[0]) + __uint_as_float(r2[1]);
+    }
+    // the waves' states merged pairwise: wave w + half into wave w, for
+    // half = PA_W/2, ..., 1; lane (kq, c), output register i of tile dt = 4u + jj:
+    // query row c, dim 64u + 4 (4kq + i) + jj
+#pragma unroll
+    for (int half = PA_W / 2; half >= 1; half >>= 1) {
+        if (wave >= half && wave < 2 * half) {
+            const int sl = wave - half;
+#pragma unroll
+            for (int hh = 0; hh < NHW; hh++) {
+                if (kq == 0) {
+                    sm_m[sl][hh][c] = m[hh];
+                    sm_l[sl][hh][c] = l[hh];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int u = 0; u < NDT / 4; u++)
+                        *reinterpret_cast<float4*>(&so[sl][hh][c][64 * u + 16 * kq + 4 * i]) =
+                            make_float4(o[hh][4 * u][i], o[hh][4 * u + 1][i], o[hh][4 * u + 2][i],
+                                        o[hh][4 * u + 3][i]);
             }
-            ps[r][tt] = dot;
         }
         __syncthreads();
-        for (int r = wave; r < n_rep; r += FA_WG / 64) {
-            const float v = lane < FA_C ? ps[r][lane] : -INFINITY;
-            const float m = wave_max(v);
-            const float mo = s_m[r], mn = fmaxf(mo, m);
-            const float e = lane < nt ? __expf(v - mn) : 0.0f;
-            const float l = wave_sum(e);
-            const float corr = __expf(mo - mn);
-            if (lane < FA_C) pt[lane][r] = e;
-            if (lane == 0) {
-                s_m[r] = mn;
-                s_l[r] = fmaf(s_l[r], corr, l);
-                s_corr[r] = corr;
-            }
-        }
-        __syncthreads();
+        if (wave < half) {
 #pragma unroll
-        for (int u = 0; u < NOUT; u++)
-            if (u < nper && r0 + u < n_rep) o[u] *= s_corr[r0 + u];
-        if ((nper & 3) == 0) {  // four heads' weights per 16-byte read
-#pragma unroll 4
-            for (int tt = 0; tt < nt; tt++) {
-                const float v = vs[tt][d];
+            for (int hh = 0; hh < NHW; hh++) {
+                const float mb = sm_m[wave][hh][c], lb = sm_l[wave][hh][c];
+                const float M = fmaxf(m[hh], mb);
+                const float Mr = M == -INFINITY ? 0.0f : M;
+                const float fa = __builtin_amdgcn_exp2f(m[hh] - Mr), fb = __builtin_amdgcn_exp2f(mb - Mr);
+                m[hh] = M;
+                l[hh] = fmaf(fa, l[hh], fb * lb);
 #pragma unroll
-                for (int u = 0; u < NOUT; u += 4)
-                    if (u < nper) {
-                        const float4 w4 = *reinterpret_cast<const float4*>(&pt[tt][r0 + u]);
-                        o[u] = fmaf(w4.x, v, o[u]);
-                        o[u + 1] = fmaf(w4.y, v, o[u + 1]);
-                        o[u + 2] = fmaf(w4.z, v, o[u + 2]);
-                        o[u + 3] = fmaf(w4.w, v, o[u + 3]);
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int u = 0; u < NDT / 4; u++) {
+                        const float4 b = *reinterpret_cast<const float4*>(&so[wave][hh][c][64 * u + 16 * kq + 4 * i]);
+                        o[hh][4 * u][i] = fmaf(fa, o[hh][4 * u][i], fb * b.x);
+                        o[hh][4 * u + 1][i] = fmaf(fa, o[hh][4 * u + 1][i], fb * b.y);
+                        o[hh][4 * u + 2][i] = fmaf(fa, o[hh][4 * u + 2][i], fb * b.z);
+                        o[hh][4 * u + 3][i] = fmaf(fa, o[hh][4 * u + 3][i], fb * b.w);
                     }
             }
-        } else {
-            for (int tt = 0; tt < nt; tt++) {
-                const float v = vs[tt][d];
-#pragma unroll
-                for (int u = 0; u < NOUT; u++)
-                    if (u < nper) o[u] = fmaf(pt[tt][r0 + u], v, o[u]);
-            }
         }
         __syncthreads();
     }
+    // wave 0 holds position 0 of every row, so the maximum is finite and l > 0
+    const int t = 16 * qb + c;
+    if (wave != 0 || t >= n) return;
 #pragma unroll
-    for (int u = 0; u < NOUT; u++)
-        if (u < nper && r0 + u < n_rep)
-            O[((size_t)t * nh + j * n_rep + r0 + u) * HD + d] = __fdiv_rn(o[u], s_l[r0 + u]);
+    for (int hh = 0; hh < NHW; hh++) {
+        const float rl = 1.0f / l[hh];
+        float* op = O + ((size_t)t * nh + h0 + hh) * HD + 16 * kq;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int u = 0; u < NDT / 4; u++)
+                *reinterpret_cast<float4*>(op + 64 * u + 4 * i) =
+                    make_float4(o[hh][4 * u][i] * rl, o[hh][4 * u + 1][i] * rl, o[hh][4 * u + 2][i] * rl,
+                                o[hh][4 * u + 3][i] * rl);
+    }
 }
-#undef PF_LOAD_BLOCK
-#undef PF_LOAD_U
-#undef PF_STORE_U
 
 // x[i] += y[i] (residual updates the GEMV epilogues do not cover)
 __global__ __launch_bounds__(256) void k_add(float* __restrict__ x, const float* __restrict__ y, int n)
@@ -1139,6 +1220,16 @@ hipError_t launch_attention_chunks(const float* q, const float* k, const float* 
     return hipGetLastError();
 }
 
+// one head per wave, four waves per workgroup (grid: heads x query blocks)
+constexpr int PA_W = 4;
+template <int HD>
+void launch_pf_attention_t(const float* Q, int nh, int nkv, float scale, int pos0, int n, int max_pos,
+                           const float* kc, const float* vc, float* out, hipStream_t s)
+{
+    hipLaunchKernelGGL((k_pf_attention<HD, 1, PA_W>), dim3(nh, (n + 15) / 16), dim3(PA_W * 64), 0, s, Q, nh, nkv,
+                       scale, pos0, n, max_pos, kc, vc, out);
+}
+
 hipError_t launch_prefill_attention(float* Q, const float* Kx, const float* Vx, const float* qn, const float* kn,
                                     int nh, int nkv, int hd, float eps, float scale, const float* cos_t,
                                     const float* sin_t, int pos0, int n, int max_pos, float* kc, float* vc,
@@ -1149,13 +1240,11 @@ hipError_t launch_prefill_attention(float* Q, const float* Kx, const float* Vx, 
     if (hd == 128) {
         hipLaunchKernelGGL(k_pf_qk_rope<128>, dim3(n), dim3(256), 0, s, Q, Kx, Vx, qn, kn, nh, nkv, eps, cos_t,
                            sin_t, pos0, max_pos, kc, vc);
-        hipLaunchKernelGGL(k_pf_attention<128>, dim3(nkv, n), dim3(FA_WG), 0, s, Q, nh, nkv, scale, pos0, max_pos,
-                           kc, vc, out);
+        launch_pf_attention_t<128>(Q, nh, nkv, scale, pos0, n, max_pos, kc, vc, out, s);
     } else {
         hipLaunchKernelGGL(k_pf_qk_rope<64>, dim3(n), dim3(256), 0, s, Q, Kx, Vx, qn, kn, nh, nkv, eps, cos_t,
                            sin_t, pos0, max_pos, kc, vc);
-        hipLaunchKernelGGL(k_pf_attention<64>, dim3(nkv, n), dim3(FA_WG), 0, s, Q, nh, nkv, scale, pos0, max_pos,
-                           kc, vc, out);
+        launch_pf_attention_t<64>(Q, nh, nkv, scale, pos0, n, max_pos, kc, vc, out, s);
     }
     return hipGetLastError();
 }

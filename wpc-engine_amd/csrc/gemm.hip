@@ -118,6 +118,18 @@ __global__ __launch_bounds__(256) void k_gemm_pack(const void* __restrict__ X, i
             (red[0][threadIdx.x] + red[1][threadIdx.x]) + (red[2][threadIdx.x] + red[3][threadIdx.x]);
 }
 
+// Another matrix of a launch that shares X (and K) with the first: its
+// workgroups start at wg0 (a multiple of 8, so each matrix's row groups keep
+// their XCDs).
+struct GemmMat {
+    const uint8_t* codes;
+    const uint8_t* hp;
+    const uint32_t* params;
+    float* y;
+    const float* bias;
+    int rows, rows_pad, rgs, rgs8, wg0;
+};
+constexpr int GEMM_MAX_MATS = 3;
 struct GemmArgs {
     const uint8_t* codes;
     const uint8_t* hp;
@@ -133,6 +145,8 @@ struct GemmArgs {
     // with rgs8 > 0 workgroup cg * rgs8 + rg takes row group rg (< rgs) of
     // column group cg, kg = 1 (the groups of one row group share an XCD's L2)
     int xt, rgs, rgs8;
+    int nmore;  // further matrices over the same X (rgs8 > 0 only)
+    GemmMat more[GEMM_MAX_MATS - 1];
 };
 
 // The value written for output (m, row): the sum, the bias, the residual.
@@ -197,7 +211,7 @@ __device__ __forceinline__ float zp_off(uint32_t p) { return __builtin_fmaf(-128
 // of the same NT/2 column tiles (k_gemm_pack<*, true>); after the loop the
 // wave adds each lo tile's sums to its hi tile's and writes the hi tiles.
 template <int SCHEME, int NT, bool SPLIT>
-__global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P)
+__global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P0)
 {
     static_assert(!SPLIT || NT % 2 == 0, "split needs hi and lo tiles");
     constexpr int RT = GM_RT;
@@ -209,16 +223,34 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P)
     __shared__ __align__(16) u32x4 xb[2][GM_R * FW];
     __shared__ float xsb[2][SN];
 
+    // this workgroup's matrix (uniform)
+    GemmArgs P = P0;
+    int bid = (int)blockIdx.x;
+    for (int e = P0.nmore - 1; e >= 0; e--)
+        if (bid >= P0.more[e].wg0) {
+            const GemmMat& mm = P0.more[e];
+            P.codes = mm.codes;
+            P.hp = mm.hp;
+            P.params = mm.params;
+            P.y = mm.y;
+            P.bias = mm.bias;
+            P.rows = mm.rows;
+            P.rows_pad = mm.rows_pad;
+            P.rgs = mm.rgs;
+            P.rgs8 = mm.rgs8;
+            bid -= mm.wg0;
+            break;
+        }
     const int kg = P.kg, nb = P.nb, XT = P.xt;
     int kgi, rg, cg;
     if (P.rgs8) {
-        rg = blockIdx.x % P.rgs8;
-        cg = blockIdx.x / P.rgs8;
+        rg = bid % P.rgs8;
+        cg = bid / P.rgs8;
         kgi = 0;
         if (rg >= P.rgs) return;  // padding of the row groups, uniform
     } else {
-        kgi = blockIdx.x % kg;
-        rg = blockIdx.x / kg;
+        kgi = bid % kg;
+        rg = bid / kg;
         cg = 0;
     }
     const int mcol0 = cg * (SPLIT ? NT / 2 : NT) * 16;  // the group's first output column
@@ -807,6 +839,7 @@ struct GemmGroupArgs {
     const uint8_t* hp;
     const uint32_t* params;
     const float* x;      // [xrows][K]
+    const float* xu;     // SILU: X = silu(x) * xu, same shape
     float* y;            // [pairs][rows]
     const int* rowidx;   // X row of pair p (null: row p)
     const int* items;    // [3 * n]: expert, first pair, count
@@ -824,7 +857,7 @@ __device__ __forceinline__ int gg_pos(int k, int p, int d)
     return (k >> 6) * 1024 + (k & 3) * 256 + (4 * p + d) * 16 + ((k >> 3) & 7) + 8 * ((k >> 2) & 1);
 }
 
-template <int SCHEME>
+template <int SCHEME, bool SILU>
 __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
 {
     __shared__ __align__(16) int8_t xd[GEMM_GROUP_MAXBK][GG_PG][2048];       // digits
@@ -883,8 +916,9 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
     constexpr int XT = (GEMM_GROUP_COLS * GEMM_GROUP_MAXBK + 15) / 16;  // task pairs per wave at most
     const int ntask = M * nb;
     const auto xrs = buf_rsrc(P.x, P.xrows * K * 4);
+    const auto urs = buf_rsrc(SILU ? P.xu : P.x, SILU ? P.xrows * K * 4 : 0);
     const int hi = lane >> 5, k0 = 4 * (lane & 31);
-    u32x4 xv[XT];
+    u32x4 xv[XT], xw[SILU ? XT : 1];
 #pragma unroll
     for (int i = 0; i < XT; i++) {
         const int t = 2 * (wave + 8 * i) + hi;
@@ -892,6 +926,7 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
         const int xr = t < ntask ? (P.rowidx ? P.rowidx[p0 + c] : p0 + c) : 0;
         const int off = t < ntask ? (xr * K + blk * 128 + k0) * 4 : 0x7FFFFFF0;
         xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
+        if constexpr (SILU) xw[i] = __builtin_amdgcn_raw_buffer_load_b128(urs, off, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < GG_LA; u += GG_CT) load_step(u);
@@ -905,8 +940,14 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
         if (t0 >= ntask) break;  // uniform per wave
         const int t = t0 + hi;
         const int c = t % max(M, 1), blk = t / max(M, 1);
-        const float v[4] = {__uint_as_float(xv[i].x), __uint_as_float(xv[i].y), __uint_as_float(xv[i].z),
-                            __uint_as_float(xv[i].w)};
+        float v[4] = {__uint_as_float(xv[i].x), __uint_as_float(xv[i].y), __uint_as_float(xv[i].z),
+                      __uint_as_float(xv[i].w)};
+        if constexpr (SILU) {  // the FAST steps' silu(g) * u
+            const float u[4] = {__uint_as_float(xw[i].x), __uint_as_float(xw[i].y), __uint_as_float(xw[i].z),
+                                __uint_as_float(xw[i].w)};
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[q] = __fdividef(v[q], 1.0f + __expf(-v[q])) * u[q];
+        }
         uint32_t mb = __float_as_uint(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
         float sm = (v[0] + v[1]) + (v[2] + v[3]);
         mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0xB1, 0xF, 0xF, false));
@@ -1210,8 +1251,52 @@ hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const 
     return m.scheme == 4 ? launch_nt<4, true>(4, grid, s, a) : launch_nt<3, true>(4, grid, s, a);
 }
 
-hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, int xrows, const int* rowidx, const int* items,
-                               const int* nitems, int max_items, float* y, hipStream_t s)
+hipError_t launch_gemm_packed_rows_multi(const DeviceMatrix* const* ms, const float* const* biases, float* const* ys,
+                                         int count, const void* xf, const float* xsum, int M, hipStream_t s)
+{
+    if (M < 1 || count < 1 || count > GEMM_MAX_MATS) return hipErrorInvalidValue;
+    for (int e = 0; e < count; e++)
+        if (ms[e]->nb == 0 || ms[e]->nb != ms[0]->nb || ms[e]->scheme != ms[0]->scheme) return hipErrorInvalidValue;
+    (void)hipGetLastError();
+    const DeviceMatrix& m = *ms[0];
+    GemmArgs a{};
+    a.codes = m.codes;
+    a.hp = m.hp;
+    a.params = m.params;
+    a.xf = static_cast<const u32x4*>(xf);
+    a.xsum = xsum;
+    a.y = ys[0];
+    a.bias = biases[0];
+    a.rows = (int)m.rows;
+    a.rows_pad = (int)m.rows_pad;
+    a.nb = (int)m.nb;
+    a.M = M;
+    a.kg = 1;
+    a.xt = gemm_rows_tiles(M);
+    a.rgs = gemm_row_groups(m.rows);
+    a.rgs8 = (a.rgs + 7) / 8 * 8;
+    int wgs = a.rgs8 * (a.xt / 4);
+    a.nmore = count - 1;
+    for (int e = 1; e < count; e++) {
+        GemmMat& mm = a.more[e - 1];
+        mm.codes = ms[e]->codes;
+        mm.hp = ms[e]->hp;
+        mm.params = ms[e]->params;
+        mm.y = ys[e];
+        mm.bias = biases[e];
+        mm.rows = (int)ms[e]->rows;
+        mm.rows_pad = (int)ms[e]->rows_pad;
+        mm.rgs = gemm_row_groups(ms[e]->rows);
+        mm.rgs8 = (mm.rgs + 7) / 8 * 8;
+        mm.wg0 = wgs;
+        wgs += mm.rgs8 * (a.xt / 4);
+    }
+    const dim3 grid((unsigned)wgs);
+    return m.scheme == 4 ? launch_nt<4, true>(4, grid, s, a) : launch_nt<3, true>(4, grid, s, a);
+}
+
+hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, const float* xu, int xrows, const int* rowidx,
+                               const int* items, const int* nitems, int max_items, float* y, hipStream_t s)
 {
     if (m.nb == 0 || m.nb > (uint64_t)GEMM_GROUP_MAXBK || m.rows_pad > (uint64_t)GEMM_GROUP_MAXROWS || xrows < 1 ||
         max_items < 1)
@@ -1222,6 +1307,7 @@ hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, int xrows,
     a.hp = m.hp;
     a.params = m.params;
     a.x = x;
+    a.xu = xu;
     a.y = y;
     a.rowidx = rowidx;
     a.items = items;
@@ -1235,8 +1321,13 @@ hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, int xrows,
     a.nb = (int)m.nb;
     a.xrows = xrows;
     dim3 grid((unsigned)((max_items + 7) / 8 * 8));
-    if (m.scheme == 4) hipLaunchKernelGGL(k_gemm_grouped<4>, grid, dim3(GG_WG), 0, s, a);
-    else hipLaunchKernelGGL(k_gemm_grouped<3>, grid, dim3(GG_WG), 0, s, a);
+    if (m.scheme == 4) {
+        if (xu) hipLaunchKernelGGL((k_gemm_grouped<4, true>), grid, dim3(GG_WG), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_grouped<4, false>), grid, dim3(GG_WG), 0, s, a);
+    } else {
+        if (xu) hipLaunchKernelGGL((k_gemm_grouped<3, true>), grid, dim3(GG_WG), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_grouped<3, false>), grid, dim3(GG_WG), 0, s, a);
+    }
     return hipGetLastError();
 }
 

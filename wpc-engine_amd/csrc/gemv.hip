@@ -1408,6 +1408,37 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ cod
                                       : __fadd_rn(zp, __fmul_rn((float)code, sc));
 }
 
+// FAST routing of a batch of score rows (the batched prefill): workgroup t
+// routes row t exactly as a FAST one-token projection's FK_ROUTE workgroup
+// does (route_wg, then the chosen weights divided by their sum in chosen
+// order when norm_topk), so each prompt token gets the routing a FAST step
+// would give it from the same scores. ids/w: [rows][top_k].
+__global__ __launch_bounds__(512) void k_route_rows(const float* __restrict__ scores, int n, int top_k,
+                                                    int norm_topk, int32_t* __restrict__ ids,
+                                                    float* __restrict__ w)
+{
+    __shared__ uint64_t key[ROUTE_MAXN];
+    __shared__ int32_t rid[MAX_JOBS];
+    __shared__ float rw[MAX_JOBS];
+    scores += (size_t)blockIdx.x * n;
+    const int selectable = n <= 128 ? route_wg<2>(scores, n, top_k, key, rid, rw)
+                                    : route_wg<4>(scores, n, top_k, key, rid, rw);
+    if (threadIdx.x < 64) {  // wave 0 holds the count
+        const int lane = threadIdx.x;
+        const int got = __builtin_amdgcn_readfirstlane(min(top_k, selectable));
+        float wk = lane < got ? rw[lane] : 0.0f;
+        if (norm_topk) {
+            float sw = 0.0f;
+            for (int k = 0; k < got; k++) sw = __fadd_rn(sw, lane_of(wk, k));
+            if (sw > 0.0f) wk = __fdiv_rn(wk, sw);
+        }
+        if (lane < top_k) {
+            ids[(size_t)blockIdx.x * top_k + lane] = lane < got ? rid[lane] : -1;
+            w[(size_t)blockIdx.x * top_k + lane] = wk;
+        }
+    }
+}
+
 }  // namespace
 
 // ============================================================ launchers
@@ -1607,6 +1638,15 @@ hipError_t launch_gemv_fast(const GemvJob* jobs, int n, hipStream_t s)
 #undef WPCG_FAST_S
 #undef WPCG_FAST2
 #undef WPCG_FAST
+    return hipGetLastError();
+}
+
+hipError_t launch_route_rows(const float* scores, int n, int rows, int top_k, int norm_topk, int32_t* ids, float* w,
+                             hipStream_t s)
+{
+    if (n < 1 || n > ROUTE_MAXN || top_k < 1 || top_k > MAX_JOBS || rows < 1) return hipErrorInvalidValue;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k_route_rows, dim3(rows), dim3(512), 0, s, scores, n, top_k, norm_topk, ids, w);
     return hipGetLastError();
 }
 

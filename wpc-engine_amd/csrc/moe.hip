@@ -482,12 +482,4 @@ hipError_t launch_softmax_route(const float* scores, int n, int top_k, int norm_
     return hipGetLastError();
 }
 
-hipError_t launch_softmax_route_rows(const float* scores, int n, int rows, int top_k, int norm_topk, int32_t* ids,
-                                     float* w, hipStream_t s)
-{
-    (void)hipGetLastError();
-    hipLaunchKernelGGL(k_softmax_route, dim3(rows), dim3(64), 0, s, scores, n, top_k, norm_topk, ids, w);
-    return hipGetLastError();
-}
-
 }  // namespace wpcg

@@ -13,45 +13,54 @@ namespace wpcg {
 namespace {
 
 // R[t][e] = sum_k X[t][k] * W[e][k] on the fp32 matrix cores: workgroup
-// (16 experts, 16 rows), each of its 4 waves one quarter of K, then the
-// quarters added in order through LDS. Lane (q, r) of a wave reads 16 bytes
-// of X row t0 + r and of W row e0 + r at k0 + 4q; with component i of
-// both, v_mfma_f32_16x16x4_f32 adds X[r][k0 + 4kk + i] * W[c][k0 + 4kk + i]
-// over kk, so four instructions cover k0 .. k0 + 15. Rows past T or E read
-// row 0 and are never written. K % 64 == 0.
+// (16 experts, 16 rows), each of its 8 waves one eighth of K with every
+// 16-byte load of its slice in flight at once (RU per operand and lane: a
+// whole eighth of a 2048-wide row), then the eighths added in order through
+// LDS. Lane (q, r) of a wave reads 16 bytes of X row t0 + r and of W row
+// e0 + r at k0 + 4q; with component i of both, v_mfma_f32_16x16x4_f32 adds
+// X[r][k0 + 4kk + i] * W[c][k0 + 4kk + i] over kk, so four instructions
+// cover k0 .. k0 + 15 (two accumulators, alternate 16-value groups). Rows
+// past T or E read row 0 and are never written. K % 128 == 0. (Four waves
+// with four loads in flight each waited on eight load round trips in a row:
+// 9.4 us for 256 rows of 2048 over 128 experts.)
 typedef float f32x4v __attribute__((ext_vector_type(4)));
-__global__ __launch_bounds__(256) void k_pf_router(const float* __restrict__ X, const float* __restrict__ W,
-                                                   int T, int E, int K, float* __restrict__ R)
+constexpr int RT_WG = 512, RT_U = 16;
+__global__ __launch_bounds__(RT_WG) void k_pf_router(const float* __restrict__ X, const float* __restrict__ W,
+                                                     int T, int E, int K, float* __restrict__ R)
 {
-    __shared__ f32x4v red[4][64];
+    __shared__ f32x4v red[8][64];
     const int e0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
-    const int kq = K / 4, kb = wave * kq;
+    const int kq = K / 8, kb = wave * kq;
     const float4* xp = reinterpret_cast<const float4*>(X + (size_t)(t0 + r < T ? t0 + r : 0) * K + kb + 4 * q);
     const float4* wp = reinterpret_cast<const float4*>(W + (size_t)(e0 + r < E ? e0 + r : 0) * K + kb + 4 * q);
-    f32x4v d = {0.f, 0.f, 0.f, 0.f};
-    constexpr int U = 4;  // 16-byte loads in flight per operand
-    for (int k = 0; k < kq; k += 16 * U) {
-        float4 a[U], b[U];
+    f32x4v d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
+    for (int k = 0; k < kq; k += 16 * RT_U) {
+        float4 a[RT_U], b[RT_U];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
+        for (int u = 0; u < RT_U; u++) {
             const bool in = k + 16 * u < kq;
             a[u] = in ? xp[(k + 16 * u) / 4] : make_float4(0.f, 0.f, 0.f, 0.f);
             b[u] = in ? wp[(k + 16 * u) / 4] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x, b[u].x, d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].y, b[u].y, d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].z, b[u].z, d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w, b[u].w, d, 0, 0, 0);
+        for (int u = 0; u < RT_U; u += 2) {
+            d0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x, b[u].x, d0, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u + 1].x, b[u + 1].x, d1, 0, 0, 0);
+            d0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].y, b[u].y, d0, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u + 1].y, b[u + 1].y, d1, 0, 0, 0);
+            d0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].z, b[u].z, d0, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u + 1].z, b[u + 1].z, d1, 0, 0, 0);
+            d0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w, b[u].w, d0, 0, 0, 0);
+            d1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u + 1].w, b[u + 1].w, d1, 0, 0, 0);
         }
     }
-    red[wave][lane] = d;
+    red[wave][lane] = d0 + d1;
     __syncthreads();
     if (wave == 0) {
         // lane (g, j) holds rows (tokens) 4g..4g+3 of column (expert) j
-        const f32x4v s4 = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+        const f32x4v s4 = ((red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane])) +
+                          ((red[4][lane] + red[5][lane]) + (red[6][lane] + red[7][lane]));
         const int g = lane >> 4, j = lane & 15;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -176,8 +185,8 @@ __global__ __launch_bounds__(256) void k_pf_combine(float* __restrict__ X, const
 hipError_t launch_pf_router(const float* X, const float* W, int T, int E, int K, float* R, hipStream_t s)
 {
     (void)hipGetLastError();
-    if (K % 64) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_pf_router, dim3((E + 15) / 16, (T + 15) / 16), dim3(256), 0, s, X, W, T, E, K, R);
+    if (K % 128 || T < 1 || E < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pf_router, dim3((E + 15) / 16, (T + 15) / 16), dim3(RT_WG), 0, s, X, W, T, E, K, R);
     return hipGetLastError();
 }
 

@@ -247,8 +247,15 @@ inline int gemm_rows_tiles(int M) { return (M + 31) / 32 * 4; }
 hipError_t launch_gemm_pack_rows(const float* x, int M, int K, void* xf, float* xsum, hipStream_t s);
 hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const float* xsum, int M, const float* bias,
                                    const float* res, float* y, hipStream_t s);
-hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, int xrows, const int* rowidx, const int* items,
-                               const int* nitems, int max_items, float* y, hipStream_t s);
+// Up to three matrices of the same K and scheme over one packed X in one
+// launch (the projections that share an input: q, k, v; gate, up); no
+// residual.
+hipError_t launch_gemm_packed_rows_multi(const DeviceMatrix* const* ms, const float* const* biases, float* const* ys,
+                                         int count, const void* xf, const float* xsum, int M, hipStream_t s);
+// xu non-null: the X rows are silu(x) * xu (the FAST steps' arithmetic),
+// x and xu of the same shape.
+hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, const float* xu, int xrows, const int* rowidx,
+                               const int* items, const int* nitems, int max_items, float* y, hipStream_t s);
 
 // ---- the no-allocation workspace (scratch.hip) --------------------------------
 // scratch_setup(device) looks up the device address of the library's fixed
@@ -348,8 +355,10 @@ hipError_t launch_prefill_attention(float* Q, const float* Kx, const float* Vx, 
                                     int nh, int nkv, int hd, float eps, float scale, const float* cos_t,
                                     const float* sin_t, int pos0, int n, int max_pos, float* kc, float* vc,
                                     float* out, hipStream_t s);
-hipError_t launch_softmax_route_rows(const float* scores, int n, int rows, int top_k, int norm_topk, int32_t* ids,
-                                     float* w, hipStream_t s);
+// FAST routing of score rows [rows][n]: the FAST one-token projection's own
+// routing per row (n <= ROUTE_MAXN, top_k <= MAX_JOBS).
+hipError_t launch_route_rows(const float* scores, int n, int rows, int top_k, int norm_topk, int32_t* ids, float* w,
+                             hipStream_t s);
 // R[t][e] = X[t] . W[e] (fp32 router rows), R is [T][E].
 hipError_t launch_pf_router(const float* X, const float* W, int T, int E, int K, float* R, hipStream_t s);
 // (token, slot) pairs sorted by expert for launch_gemm_grouped: pair_tok
