@@ -432,8 +432,7 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
     WPCG_HIP(launch_embed_rows(m->embed->m, m->tokens + pos0, (int)n, P.x, s));
     for (uint32_t l = 0; l < c.n_layers; l++) {
         Layer& L = m->layers[l];
-        WPCG_HIP(launch_rms_norm_rows(F, P.x, L.in_ln, H, (int)n, c.eps, P.xn, s));
-        WPCG_HIP(launch_gemm_pack_rows(P.xn, (int)n, H, P.xf, P.xsum, s));
+        WPCG_HIP(launch_rms_pack_rows(P.x, L.in_ln, (int)n, H, c.eps, P.xf, P.xsum, s));
         {
             const DeviceMatrix* ms[3] = {&L.q->m, &L.k->m, &L.v->m};
             const float* bs[3] = {L.q->bias, L.k->bias, L.v->bias};
@@ -443,13 +442,13 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
         float* kc = m->kc + (size_t)l * nkv * c.max_pos * hd;
         float* vc = m->vc + (size_t)l * nkv * c.max_pos * hd;
         WPCG_HIP(launch_prefill_attention(P.q, P.k, P.v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale, m->cos_t,
-                                          m->sin_t, (int)pos0, (int)n, (int)c.max_pos, kc, vc, P.attn, s));
-        // residual += o_proj(attn)
-        WPCG_HIP(launch_gemm_pack_rows(P.attn, (int)n, nh * hd, P.xf, P.xsum, s));
+                                          m->sin_t, (int)pos0, (int)n, (int)c.max_pos, kc, vc, P.attn, P.xf, P.xsum,
+                                          s));
+        // residual += o_proj(attn); 128-wide heads leave the attention packed
+        if (hd != 128) WPCG_HIP(launch_gemm_pack_rows(P.attn, (int)n, nh * hd, P.xf, P.xsum, s));
         WPCG_HIP(launch_gemm_packed_rows(L.o->m, P.xf, P.xsum, (int)n, L.o->bias, P.x, P.x, s));
-        WPCG_HIP(launch_rms_norm_rows(F, P.x, L.post_ln, H, (int)n, c.eps, P.xn, s));
         if (!c.n_experts) {
-            WPCG_HIP(launch_gemm_pack_rows(P.xn, (int)n, H, P.xf, P.xsum, s));
+            WPCG_HIP(launch_rms_pack_rows(P.x, L.post_ln, (int)n, H, c.eps, P.xf, P.xsum, s));
             const DeviceMatrix* ms[2] = {&L.gate->m, &L.up->m};
             const float* bs[2] = {L.gate->bias, L.up->bias};
             float* ys[2] = {P.g, P.u};
@@ -461,6 +460,7 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
         }
         // experts: route every row, sort the (row, slot) pairs by expert, one
         // grouped launch per projection, then the ordered combine
+        WPCG_HIP(launch_rms_norm_rows(F, P.x, L.post_ln, H, (int)n, c.eps, P.xn, s));
         wpcg_moe* E = L.moe;
         const int ne = (int)c.n_experts, K = (int)c.top_k, pairs = (int)n * K;
         const int max_items = pairs / GEMM_GROUP_COLS + ne + 1;
@@ -526,8 +526,7 @@ int verify_run(wpcg_model* m, uint32_t pos0, uint32_t n)
     }
     if (int rc = prefill_pass(m, pos0, n, s)) return rc;
     wpcg_linear* head = logits_head(m);
-    WPCG_HIP(launch_rms_norm_rows(WPCG_MODE_FAST, P.x, m->final_norm, (int)c.hidden, (int)n, c.eps, P.xn, s));
-    WPCG_HIP(launch_gemm_pack_rows(P.xn, (int)n, (int)c.hidden, P.xf, P.xsum, s));
+    WPCG_HIP(launch_rms_pack_rows(P.x, m->final_norm, (int)n, (int)c.hidden, c.eps, P.xf, P.xsum, s));
     WPCG_HIP(launch_gemm_packed_rows(head->m, P.xf, P.xsum, (int)n, head->bias, nullptr, P.vlogits, s));
     WPCG_HIP(launch_argmax_rows(P.vlogits, (int)c.vocab, (int)n, P.vids, s));
     WPCG_HIP(hipStreamSynchronize(s));

@@ -17,6 +17,7 @@
 #include "ref_expf.h"
 #include "wpcg_internal.hpp"
 #include "wave.h"
+#include "xpack.h"
 
 namespace wpcg {
 namespace {
@@ -810,7 +811,9 @@ template <int HD, int NHW, int PA_W>
 __global__ __launch_bounds__(PA_W * 64) void k_pf_attention(const float* __restrict__ Q, int nh, int nkv,
                                                             float scale, int pos0, int n, int max_pos,
                                                             const float* __restrict__ kc,
-                                                            const float* __restrict__ vc, float* __restrict__ O)
+                                                            const float* __restrict__ vc, float* __restrict__ O,
+                                                            uint32_t* __restrict__ xf, float* __restrict__ xsum,
+                                                            int XT)
 {
     constexpr int DL = HD / 4;    // dims per lane in the score product
     constexpr int NDT = HD / 16;  // output tiles of 16 dims
@@ -993,6 +996,25 @@ __global__ __launch_bounds__(PA_W * 64) void k_pf_attention(const float* __restr
     }
     // wave 0 holds position 0 of every row, so the maximum is finite and l > 0
     const int t = 16 * qb + c;
+    if constexpr (HD == 128 && NHW == 1 && PA_W == 4) {
+        // a head is one 128-value block of o_proj's input: the workgroup
+        // writes its 16 rows of it as the GEMM's packed X (block h0, column
+        // tile qb) instead of fp32 rows for a packing launch
+        __shared__ float pk_red[2][4][16];
+        if (wave == 0) {
+            const float rl = 1.0f / l[0];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int u = 0; u < NDT / 4; u++)
+                    *reinterpret_cast<float4*>(&so[0][0][c][64 * u + 16 * kq + 4 * i]) =
+                        make_float4(o[0][4 * u][i] * rl, o[0][4 * u + 1][i] * rl, o[0][4 * u + 2][i] * rl,
+                                    o[0][4 * u + 3][i] * rl);
+        }
+        __syncthreads();
+        pack_tile_split(&so[0][0][0][0], OS, min(16, n - 16 * qb), h0, qb, XT, xf, xsum, pk_red);
+        return;
+    }
     if (wave != 0 || t >= n) return;
 #pragma unroll
     for (int hh = 0; hh < NHW; hh++) {
@@ -1224,27 +1246,28 @@ hipError_t launch_attention_chunks(const float* q, const float* k, const float* 
 constexpr int PA_W = 4;
 template <int HD>
 void launch_pf_attention_t(const float* Q, int nh, int nkv, float scale, int pos0, int n, int max_pos,
-                           const float* kc, const float* vc, float* out, hipStream_t s)
+                           const float* kc, const float* vc, float* out, void* xf, float* xsum, hipStream_t s)
 {
     hipLaunchKernelGGL((k_pf_attention<HD, 1, PA_W>), dim3(nh, (n + 15) / 16), dim3(PA_W * 64), 0, s, Q, nh, nkv,
-                       scale, pos0, n, max_pos, kc, vc, out);
+                       scale, pos0, n, max_pos, kc, vc, out, static_cast<uint32_t*>(xf), xsum, gemm_rows_tiles(n));
 }
 
 hipError_t launch_prefill_attention(float* Q, const float* Kx, const float* Vx, const float* qn, const float* kn,
                                     int nh, int nkv, int hd, float eps, float scale, const float* cos_t,
                                     const float* sin_t, int pos0, int n, int max_pos, float* kc, float* vc,
-                                    float* out, hipStream_t s)
+                                    float* out, void* xf, float* xsum, hipStream_t s)
 {
     if (!attention_fast_ok(nh, nkv, hd) || n < 1 || pos0 + n > max_pos) return hipErrorInvalidValue;
+    if (hd == 128 ? !xf || !xsum : !out) return hipErrorInvalidValue;
     (void)hipGetLastError();
     if (hd == 128) {
         hipLaunchKernelGGL(k_pf_qk_rope<128>, dim3(n), dim3(256), 0, s, Q, Kx, Vx, qn, kn, nh, nkv, eps, cos_t,
                            sin_t, pos0, max_pos, kc, vc);
-        launch_pf_attention_t<128>(Q, nh, nkv, scale, pos0, n, max_pos, kc, vc, out, s);
+        launch_pf_attention_t<128>(Q, nh, nkv, scale, pos0, n, max_pos, kc, vc, out, xf, xsum, s);
     } else {
         hipLaunchKernelGGL(k_pf_qk_rope<64>, dim3(n), dim3(256), 0, s, Q, Kx, Vx, qn, kn, nh, nkv, eps, cos_t,
                            sin_t, pos0, max_pos, kc, vc);
-        launch_pf_attention_t<64>(Q, nh, nkv, scale, pos0, n, max_pos, kc, vc, out, s);
+        launch_pf_attention_t<64>(Q, nh, nkv, scale, pos0, n, max_pos, kc, vc, out, xf, xsum, s);
     }
     return hipGetLastError();
 }

@@ -25,19 +25,16 @@
 #include <algorithm>
 
 #include "wpcg_internal.hpp"
+#include "xpack.h"
 
 namespace wpcg {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 typedef int v4i __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ int gk(int i, int g, int s) { return 8 * s + g + 4 * (i & 1) + 64 * (i >> 1); }
 
 __device__ __forceinline__ float h2f(uint32_t bits)
 {
@@ -47,27 +44,12 @@ __device__ __forceinline__ float h2f(uint32_t bits)
     return (float)h;
 }
 
-// Two floats to packed bf16 (round to nearest even), low half first.
-__device__ __forceinline__ uint32_t pk_bf16(float a, float b)
-{
-    const f32x2 f = {a, b};
-    const bf16x2 h = __builtin_convertvector(f, bf16x2);
-    uint32_t r;
-    __builtin_memcpy(&r, &h, 4);
-    return r;
-}
-__device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
-
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes)
 {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 constexpr int CPOL_NT = 2;   // streamed once
 constexpr int CPOL_SC1 = 16; // coherent across the device's L2s (agent scope)
-
-// x rounded to bf16 (nearest even), as a float
-__device__ __forceinline__ float bf16_round(float v) { return bf16_lo(pk_bf16(v, 0.0f)); }
 
 // ---- X -> bf16 fragments in k(i, g, s) order, plus per-block column sums
 // of the rounded values. One workgroup per (block, column tile): wave i is

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include "wpcg_internal.hpp"
+#include "xpack.h"
 
 namespace wpcg {
 namespace {
@@ -67,6 +68,59 @@ __global__ __launch_bounds__(RT_WG) void k_pf_router(const float* __restrict__ X
             const int t = t0 + 4 * g + i, e = e0 + j;
             if (t < T && e < E) R[(size_t)t * E + e] = s4[i];
         }
+    }
+}
+
+// RMSNorm of rows of X (FAST arithmetic: fused multiply-add squares,
+// 1 / sqrt(mean + eps), then (x * scale) * w) written straight as the
+// GEMM's packed X, with no fp32 copy and no packing launch: workgroup
+// (16-row tile q, block b). Every workgroup of a tile computes its 16 row
+// norms itself (each row is read from L2 once per block: 256 workgroups for
+// 256 rows of 2048 beat 64 workgroups of four blocks each, 15 us), then
+// stages its block of the normed rows in LDS and packs it.
+constexpr int RP_BG = 1;
+__global__ __launch_bounds__(256) void k_rms_pack(const float* __restrict__ X, const float* __restrict__ w, int n,
+                                                  int H, float eps, int XT, uint32_t* __restrict__ xf,
+                                                  float* __restrict__ xsum)
+{
+    __shared__ float rstd[16];
+    __shared__ __align__(16) float tile[16][132];
+    __shared__ float red[2][4][16];
+    const int q = blockIdx.x, r = threadIdx.x >> 4, p = threadIdx.x & 15;
+    const int row = 16 * q + r;
+    // row r's squares by its 16 threads (lanes 16r..16r+15 of one wave)
+    float ss = 0.0f;
+    if (row < n)
+#pragma unroll 8
+        for (int k = 4 * p; k < H; k += 64) {
+            const float4 v = *reinterpret_cast<const float4*>(X + (size_t)row * H + k);
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
+        }
+    ss += __shfl_xor(ss, 8);
+    ss += __shfl_xor(ss, 4);
+    ss += __shfl_xor(ss, 2);
+    ss += __shfl_xor(ss, 1);
+    if (p == 0) rstd[r] = __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(ss, (float)H), eps)));
+    __syncthreads();
+    const int b1 = min(H / 128, (int)(blockIdx.y + 1) * RP_BG);
+    const int rr = threadIdx.x >> 4, cc = (threadIdx.x & 15) * 8, mrow = 16 * q + rr;
+    for (int b = blockIdx.y * RP_BG; b < b1; b++) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int k = b * 128 + cc + 4 * h;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (mrow < n) v = *reinterpret_cast<const float4*>(X + (size_t)mrow * H + k);
+            const float4 g = *reinterpret_cast<const float4*>(w + k);
+            const float sc = rstd[rr];
+            *reinterpret_cast<float4*>(&tile[rr][cc + 4 * h]) =
+                make_float4(__fmul_rn(__fmul_rn(v.x, sc), g.x), __fmul_rn(__fmul_rn(v.y, sc), g.y),
+                            __fmul_rn(__fmul_rn(v.z, sc), g.z), __fmul_rn(__fmul_rn(v.w, sc), g.w));
+        }
+        __syncthreads();
+        pack_tile_split(&tile[0][0], 132, min(16, n - 16 * q), b, q, XT, xf, xsum, red);
     }
 }
 
@@ -187,6 +241,17 @@ hipError_t launch_pf_router(const float* X, const float* W, int T, int E, int K,
     (void)hipGetLastError();
     if (K % 128 || T < 1 || E < 1) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_pf_router, dim3((E + 15) / 16, (T + 15) / 16), dim3(RT_WG), 0, s, X, W, T, E, K, R);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_pack_rows(const float* X, const float* w, int n, int H, float eps, void* xf, float* xsum,
+                                hipStream_t s)
+{
+    if (n < 1 || H < 128 || H % 128) return hipErrorInvalidValue;
+    (void)hipGetLastError();
+    const dim3 grid((unsigned)((n + 15) / 16), (unsigned)((H / 128 + RP_BG - 1) / RP_BG));
+    hipLaunchKernelGGL(k_rms_pack, grid, dim3(256), 0, s, X, w, n, H, eps, gemm_rows_tiles(n),
+                       static_cast<uint32_t*>(xf), xsum);
     return hipGetLastError();
 }
 

@@ -349,16 +349,21 @@ hipError_t launch_embed_rows(const DeviceMatrix& m, const uint32_t* tokens, int 
 hipError_t launch_rms_norm_rows(int mode, const float* x, const float* w, int n, int rows, float eps, float* out,
                                 hipStream_t s);
 // q_norm/k_norm + RoPE (Q in place, keys into kc), values into vc, then
-// causal attention of every row over positions 0..pos0+t into out [n][nh*hd].
-// Needs attention_fast_ok.
+// causal attention of every row over positions 0..pos0+t: with head_dim 128
+// written as o_proj's packed X (xf, xsum: launch_gemm_pack_rows's layout for
+// n rows of nh*128), with 64 into out [n][nh*hd]. Needs attention_fast_ok.
 hipError_t launch_prefill_attention(float* Q, const float* Kx, const float* Vx, const float* qn, const float* kn,
                                     int nh, int nkv, int hd, float eps, float scale, const float* cos_t,
                                     const float* sin_t, int pos0, int n, int max_pos, float* kc, float* vc,
-                                    float* out, hipStream_t s);
+                                    float* out, void* xf, float* xsum, hipStream_t s);
 // FAST routing of score rows [rows][n]: the FAST one-token projection's own
 // routing per row (n <= ROUTE_MAXN, top_k <= MAX_JOBS).
 hipError_t launch_route_rows(const float* scores, int n, int rows, int top_k, int norm_topk, int32_t* ids, float* w,
                              hipStream_t s);
+// RMSNorm (FAST) of n rows of H into the GEMM's packed X (xf, xsum in
+// launch_gemm_pack_rows's layout), H % 128 == 0.
+hipError_t launch_rms_pack_rows(const float* X, const float* w, int n, int H, float eps, void* xf, float* xsum,
+                                hipStream_t s);
 // R[t][e] = X[t] . W[e] (fp32 router rows), R is [T][E].
 hipError_t launch_pf_router(const float* X, const float* W, int T, int E, int K, float* R, hipStream_t s);
 // (token, slot) pairs sorted by expert for launch_gemm_grouped: pair_tok
