@@ -38,6 +38,7 @@ struct Prefill {
     float *ge = nullptr, *ue = nullptr, *de = nullptr;  // per sorted pair: [P][moe_inter] x2, [P][hidden]
     void* xf = nullptr;       // packed X of the batched GEMMs (launch_gemm_pack_rows)
     float* xsum = nullptr;
+    float* part = nullptr;    // K-slice partials of o_proj / the dense down
     float* vlogits = nullptr;  // verification: [WPCG_VERIFY_MAX][vocab], made on first use
     uint32_t* vids = nullptr;  // [WPCG_VERIFY_MAX]
 };
@@ -357,6 +358,7 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
 // ---- batched prefill (FAST) --------------------------------------------------
 // Rows of tokens per prefill pass; longer prompts run pass after pass.
 constexpr uint32_t PF_CAP = 256;
+constexpr int PF_MAX_KG = 4;  // K-slices of the prefill's hidden-size GEMMs
 static_assert(PF_CAP <= (uint32_t)PF_GROUP_MAXT, "the expert grouping holds PF_GROUP_MAXT tokens");
 
 // Whether the batched path covers this model: FAST attention's head shapes,
@@ -399,6 +401,7 @@ int make_prefill(wpcg_model* m)
     const size_t kmax = std::max<size_t>({H, qd, c.n_experts ? 0 : (size_t)c.inter});
     dev((void**)&P.xf, kmax / 128 * gemm_rows_tiles((int)cap) * 4096);
     dev((void**)&P.xsum, kmax / 128 * gemm_rows_tiles((int)cap) * 16 * 4);
+    dev((void**)&P.part, (size_t)PF_MAX_KG * (gemm_rows_tiles((int)cap) / 4 * 32) * pad_rows(H) * 4);
     if (c.n_experts) {
         const size_t pairs = cap * c.top_k, E = c.n_experts, I = c.moe_inter;
         dev((void**)&P.r, cap * E * 4);
@@ -417,6 +420,16 @@ int make_prefill(wpcg_model* m)
     }
     if (rc == WPCG_OK) P.cap = (uint32_t)cap;
     return rc;
+}
+
+// K-slices of a packed-rows GEMM of the prefill whose rows are the hidden
+// size (o_proj, the dense down): enough for about 256 workgroups, slices of
+// at least 8 blocks (o_proj of the Qwen3-30B-A3B shape at 256 rows: 128
+// workgroups of 32 blocks took 26.3 us, 256 of 16 plus the slice sum ~18).
+int pf_kslices(const DeviceMatrix& m, int n)
+{
+    const int live = gemm_row_groups(m.rows) * (gemm_rows_tiles(n) / 4);
+    return std::max(1, std::min({256 / std::max(live, 1), (int)m.nb / 8, PF_MAX_KG}));
 }
 
 // Tokens tokens[pos0 .. pos0+n-1] (already on the device) through every
@@ -446,7 +459,8 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
                                           s));
         // residual += o_proj(attn); 128-wide heads leave the attention packed
         if (hd != 128) WPCG_HIP(launch_gemm_pack_rows(P.attn, (int)n, nh * hd, P.xf, P.xsum, s));
-        WPCG_HIP(launch_gemm_packed_rows(L.o->m, P.xf, P.xsum, (int)n, L.o->bias, P.x, P.x, s));
+        WPCG_HIP(launch_gemm_packed_rows(L.o->m, P.xf, P.xsum, (int)n, L.o->bias, P.x, P.x, s,
+                                         pf_kslices(L.o->m, (int)n), P.part));
         if (!c.n_experts) {
             WPCG_HIP(launch_rms_pack_rows(P.x, L.post_ln, (int)n, H, c.eps, P.xf, P.xsum, s));
             const DeviceMatrix* ms[2] = {&L.gate->m, &L.up->m};
@@ -455,7 +469,8 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
             WPCG_HIP(launch_gemm_packed_rows_multi(ms, bs, ys, 2, P.xf, P.xsum, (int)n, s));
             WPCG_HIP(launch_silu_mul(P.g, P.u, P.g, (size_t)n * c.inter, s));
             WPCG_HIP(launch_gemm_pack_rows(P.g, (int)n, (int)c.inter, P.xf, P.xsum, s));
-            WPCG_HIP(launch_gemm_packed_rows(L.down->m, P.xf, P.xsum, (int)n, L.down->bias, P.x, P.x, s));
+            WPCG_HIP(launch_gemm_packed_rows(L.down->m, P.xf, P.xsum, (int)n, L.down->bias, P.x, P.x, s,
+                                             pf_kslices(L.down->m, (int)n), P.part));
             continue;
         }
         // experts: route every row, sort the (row, slot) pairs by expert, one

@@ -225,10 +225,11 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P0)
         }
     const int kg = P.kg, nb = P.nb, XT = P.xt;
     int kgi, rg, cg;
-    if (P.rgs8) {
+    if (P.rgs8) {  // workgroup (kgi * ncg + cg) * rgs8 + rg
+        const int ncg = P.xt / NT;
         rg = bid % P.rgs8;
-        cg = bid / P.rgs8;
-        kgi = 0;
+        cg = (bid / P.rgs8) % ncg;
+        kgi = bid / P.rgs8 / ncg;
         if (rg >= P.rgs) return;  // padding of the row groups, uniform
     } else {
         kgi = bid % kg;
@@ -448,8 +449,9 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P0)
     // the column tiles this wave writes: [0, NW) (SPLIT: the hi tiles)
     constexpr int NW = SPLIT ? NT / 2 : NT;
 
-    // lane (g, j) holds rows 4g..4g+3 of each tile for column n*16 + j
-    const int Mp = NT * 16;
+    // lane (g, j) holds rows 4g..4g+3 of each tile for column n*16 + j;
+    // the split-K partials have Mp columns (every column group's with rgs8)
+    const int Mp = P.rgs8 ? P.xt / NT * NW * 16 : NT * 16;
     if (kg == 1) {
 #pragma unroll
         for (int rt = 0; rt < RT; rt++)
@@ -476,7 +478,7 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P0)
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int n = 0; n < NW; n++) {
-            const int m = n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
+            const int m = mcol0 + n * 16 + j, row = (T0 + rt) * TILE_ROWS + 4 * g;
             if (T0 + rt < ntiles) {
                 u32x4 v;
                 __builtin_memcpy(&v, &acc[rt][n], 16);
@@ -806,13 +808,17 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
 // prompt (with 8 pairs per item, an expert routed ~16 pairs read its
 // matrices twice: ~270 MB per launch where the experts hold ~110 MB). The
 // item's X rows are digitised once into LDS; each wave streams whole row
-// tiles of the expert (tiles w, w + 8, ...) through the full K, GG_LA
+// tiles of the expert (tiles w, w + GG_NW, ...; GG_NW waves) through the full K, GG_LA
 // units of codes in flight, in whole unguarded rounds (units past the
 // wave's last read zeros and are dropped), and writes each finished tile's
 // rows x pairs. Items are spread so that consecutive items (one expert's
 // runs) share an XCD and its L2: workgroup b takes item (b % 8) * S + b / 8
 // with S = ceil(nitems / 8).
-constexpr int GG_WG = 512;
+// Waves per workgroup: 8, or 16 for v4 down projections (SILU; 128 row
+// tiles: 8 per wave instead of 16, 41.2 -> 37.0 us per launch, where gate
+// and up, 48 tiles, ran slower with 16: 45.2 -> 47.4; v3 spills at 16).
+template <int SCHEME, bool SILU>
+constexpr int gg_waves() { return SCHEME == 4 && SILU ? 16 : 8; }
 constexpr int GG_LA = 8;   // units (tile, block) of codes in flight per wave
 constexpr int GG_CT = 2;   // tiles per chunk: the units of one step
 constexpr int GG_PG = (GEMM_GROUP_COLS + 3) / 4;  // groups of four pairs
@@ -840,8 +846,9 @@ __device__ __forceinline__ int gg_pos(int k, int p, int d)
 }
 
 template <int SCHEME, bool SILU>
-__global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
+__global__ __launch_bounds__((gg_waves<SCHEME, SILU>() * 64)) void k_gemm_grouped(const GemmGroupArgs P)
 {
+    constexpr int GG_NW = gg_waves<SCHEME, SILU>(), GG_WG = GG_NW * 64;
     __shared__ __align__(16) int8_t xd[GEMM_GROUP_MAXBK][GG_PG][2048];       // digits
     __shared__ float2 xs[GEMM_GROUP_MAXBK][GG_PG * 4];                       // {s_b, sum(x_b)}
     const int nitems = *P.nitems;
@@ -854,11 +861,11 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
     const int g = lane >> 4, j = lane & 15;
     const int ntiles = P.rows_pad / TILE_ROWS;
 
-    // This wave's tiles are wave, wave + 8, ...; it takes them GG_CT at a
+    // This wave's tiles are wave, wave + GG_NW, ...; it takes them GG_CT at a
     // time (a chunk), block by block: step s is block s % nb of chunk s / nb,
     // and its units are the chunk's tiles at that block, so one read of the
     // block's digits serves GG_CT tiles.
-    const int my_tiles = ntiles > wave ? (ntiles - wave + 7) / 8 : 0;
+    const int my_tiles = ntiles > wave ? (ntiles - wave + GG_NW - 1) / GG_NW : 0;
     const int nsteps = (my_tiles + GG_CT - 1) / GG_CT * nb;
     const uint8_t* codes = P.codes + (size_t)e * P.ecodes;
     const uint8_t* hpl = P.hp + (size_t)e * P.ehp;
@@ -871,7 +878,7 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
     u32x2 hr[GG_LA];
     uint32_t pr[GG_LA];
     // units are requested in order: the next step's chunk and block are
-    // (lc, lb), unit tt of it tile wave + 8 (GG_CT lc + tt); a tile past the
+    // (lc, lb), unit tt of it tile wave + GG_NW (GG_CT lc + tt); a tile past the
     // wave's last (or a step past the end) reads record nrec, past the range
     // (zeros, never used)
     int lc = 0, lb = 0;
@@ -879,7 +886,7 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
 #pragma unroll
         for (int tt = 0; tt < GG_CT; tt++) {
             const int tl = GG_CT * lc + tt;
-            const int rec = tl < my_tiles ? (wave + 8 * tl) * nb + lb : nrec;
+            const int rec = tl < my_tiles ? (wave + GG_NW * tl) * nb + lb : nrec;
             const int slot = slot0 + tt;
             cr[slot] = __builtin_amdgcn_raw_buffer_load_b128(crs, rec * (int)CODE_REC + lane * 16, 0, CPOL_NT);
             if constexpr (SCHEME == 3)
@@ -894,8 +901,8 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
 
     // ---- X: task (pair c, block blk) is 128 values, 32 lanes with four
     // consecutive values each; a wave takes two tasks at a time (tasks
-    // 2*(wave + 8i) and +1), every load of every task issued first
-    constexpr int XT = (GEMM_GROUP_COLS * GEMM_GROUP_MAXBK + 15) / 16;  // task pairs per wave at most
+    // 2*(wave + GG_NW i) and +1), every load of every task issued first
+    constexpr int XT = (GEMM_GROUP_COLS * GEMM_GROUP_MAXBK + 2 * GG_NW - 1) / (2 * GG_NW);  // task pairs per wave at most
     const int ntask = M * nb;
     const auto xrs = buf_rsrc(P.x, P.xrows * K * 4);
     const auto urs = buf_rsrc(SILU ? P.xu : P.x, SILU ? P.xrows * K * 4 : 0);
@@ -903,7 +910,7 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
     u32x4 xv[XT], xw[SILU ? XT : 1];
 #pragma unroll
     for (int i = 0; i < XT; i++) {
-        const int t = 2 * (wave + 8 * i) + hi;
+        const int t = 2 * (wave + GG_NW * i) + hi;
         const int c = t % max(M, 1), blk = t / max(M, 1);
         const int xr = t < ntask ? (P.rowidx ? P.rowidx[p0 + c] : p0 + c) : 0;
         const int off = t < ntask ? (xr * K + blk * 128 + k0) * 4 : 0x7FFFFFF0;
@@ -918,7 +925,7 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
     // rows of 16, then the row swap), then Q and its four digits into LDS
 #pragma unroll
     for (int i = 0; i < XT; i++) {
-        const int t0 = 2 * (wave + 8 * i);
+        const int t0 = 2 * (wave + GG_NW * i);
         if (t0 >= ntask) break;  // uniform per wave
         const int t = t0 + hi;
         const int c = t % max(M, 1), blk = t / max(M, 1);
@@ -1033,7 +1040,7 @@ __global__ __launch_bounds__(GG_WG) void k_gemm_grouped(const GemmGroupArgs P)
 #pragma unroll
             for (int tt = 0; tt < GG_CT; tt++) {
                 const int tl = GG_CT * uc + tt;
-                const int row = (wave + 8 * tl) * TILE_ROWS + j;
+                const int row = (wave + GG_NW * tl) * TILE_ROWS + j;
                 if (tl < my_tiles && row < P.rows) {
 #pragma unroll
                     for (int pg = 0; pg < GG_PG; pg++)
@@ -1208,9 +1215,9 @@ hipError_t launch_gemm_pack_rows(const float* x, int M, int K, void* xf, float* 
 }
 
 hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const float* xsum, int M, const float* bias,
-                                   const float* res, float* y, hipStream_t s)
+                                   const float* res, float* y, hipStream_t s, int kg, float* part)
 {
-    if (M < 1 || m.nb == 0) return hipErrorInvalidValue;
+    if (M < 1 || m.nb == 0 || kg < 1 || kg > (int)m.nb || (kg > 1 && !part)) return hipErrorInvalidValue;
     (void)hipGetLastError();
     GemmArgs a{};
     a.codes = m.codes;
@@ -1225,12 +1232,18 @@ hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const 
     a.rows_pad = (int)m.rows_pad;
     a.nb = (int)m.nb;
     a.M = M;
-    a.kg = 1;
+    a.kg = kg;
+    a.part = part;
     a.xt = gemm_rows_tiles(M);
     a.rgs = gemm_row_groups(m.rows);
     a.rgs8 = (a.rgs + 7) / 8 * 8;
-    dim3 grid((unsigned)(a.rgs8 * (a.xt / 4)));
-    return m.scheme == 4 ? launch_nt<4, true>(4, grid, s, a) : launch_nt<3, true>(4, grid, s, a);
+    dim3 grid((unsigned)(a.rgs8 * (a.xt / 4) * kg));
+    hipError_t e = m.scheme == 4 ? launch_nt<4, true>(4, grid, s, a) : launch_nt<3, true>(4, grid, s, a);
+    if (e != hipSuccess || kg == 1) return e;
+    const int Mp = a.xt / 4 * 32, outs = M * (int)(m.rows_pad / 4);
+    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, part, kg, Mp,
+                       (int)m.rows_pad, (int)m.rows, M, bias, res, y);
+    return hipGetLastError();
 }
 
 hipError_t launch_gemm_packed_rows_multi(const DeviceMatrix* const* ms, const float* const* biases, float* const* ys,
@@ -1304,11 +1317,11 @@ hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, const floa
     a.xrows = xrows;
     dim3 grid((unsigned)((max_items + 7) / 8 * 8));
     if (m.scheme == 4) {
-        if (xu) hipLaunchKernelGGL((k_gemm_grouped<4, true>), grid, dim3(GG_WG), 0, s, a);
-        else hipLaunchKernelGGL((k_gemm_grouped<4, false>), grid, dim3(GG_WG), 0, s, a);
+        if (xu) hipLaunchKernelGGL((k_gemm_grouped<4, true>), grid, dim3(gg_waves<4, true>() * 64), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_grouped<4, false>), grid, dim3(gg_waves<4, false>() * 64), 0, s, a);
     } else {
-        if (xu) hipLaunchKernelGGL((k_gemm_grouped<3, true>), grid, dim3(GG_WG), 0, s, a);
-        else hipLaunchKernelGGL((k_gemm_grouped<3, false>), grid, dim3(GG_WG), 0, s, a);
+        if (xu) hipLaunchKernelGGL((k_gemm_grouped<3, true>), grid, dim3(gg_waves<3, true>() * 64), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_grouped<3, false>), grid, dim3(gg_waves<3, false>() * 64), 0, s, a);
     }
     return hipGetLastError();
 }

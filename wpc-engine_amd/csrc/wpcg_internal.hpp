@@ -245,8 +245,10 @@ constexpr int GEMM_GROUP_MAXROWS = 2048;
 // floats.
 inline int gemm_rows_tiles(int M) { return (M + 31) / 32 * 4; }
 hipError_t launch_gemm_pack_rows(const float* x, int M, int K, void* xf, float* xsum, hipStream_t s);
+// kg > 1: K in kg slices whose partials go to part (kg * (gemm_rows_tiles(M) /
+// 4 * 32) * m.rows_pad floats), added in slice order by a second launch.
 hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const float* xsum, int M, const float* bias,
-                                   const float* res, float* y, hipStream_t s);
+                                   const float* res, float* y, hipStream_t s, int kg = 1, float* part = nullptr);
 // Up to three matrices of the same K and scheme over one packed X in one
 // launch (the projections that share an input: q, k, v; gate, up); no
 // residual.
