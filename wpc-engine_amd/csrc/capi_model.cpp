@@ -459,8 +459,12 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
                                           s));
         // residual += o_proj(attn); 128-wide heads leave the attention packed
         if (hd != 128) WPCG_HIP(launch_gemm_pack_rows(P.attn, (int)n, nh * hd, P.xf, P.xsum, s));
-        WPCG_HIP(launch_gemm_packed_rows(L.o->m, P.xf, P.xsum, (int)n, L.o->bias, P.x, P.x, s,
-                                         pf_kslices(L.o->m, (int)n), P.part));
+        // o_proj in K-slices; for the MoE model the slice sum joins the
+        // post-attention RMSNorm (the router and the experts read fp32 rows)
+        const int okg = pf_kslices(L.o->m, (int)n);
+        const bool fuse_norm = c.n_experts && okg > 1 && H <= PF_NORM_MAXH;
+        WPCG_HIP(launch_gemm_packed_rows(L.o->m, P.xf, P.xsum, (int)n, L.o->bias, P.x, P.x, s, okg, P.part,
+                                         !fuse_norm));
         if (!c.n_experts) {
             WPCG_HIP(launch_rms_pack_rows(P.x, L.post_ln, (int)n, H, c.eps, P.xf, P.xsum, s));
             const DeviceMatrix* ms[2] = {&L.gate->m, &L.up->m};
@@ -475,7 +479,11 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
         }
         // experts: route every row, sort the (row, slot) pairs by expert, one
         // grouped launch per projection, then the ordered combine
-        WPCG_HIP(launch_rms_norm_rows(F, P.x, L.post_ln, H, (int)n, c.eps, P.xn, s));
+        if (fuse_norm)
+            WPCG_HIP(launch_pf_reduce_norm(P.part, okg, (int)n, H, (int)L.o->m.rows_pad, L.o->bias, P.x, L.post_ln,
+                                           c.eps, P.xn, s));
+        else
+            WPCG_HIP(launch_rms_norm_rows(F, P.x, L.post_ln, H, (int)n, c.eps, P.xn, s));
         wpcg_moe* E = L.moe;
         const int ne = (int)c.n_experts, K = (int)c.top_k, pairs = (int)n * K;
         const int max_items = pairs / GEMM_GROUP_COLS + ne + 1;

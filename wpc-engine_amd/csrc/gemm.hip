@@ -1215,7 +1215,7 @@ hipError_t launch_gemm_pack_rows(const float* x, int M, int K, void* xf, float* 
 }
 
 hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const float* xsum, int M, const float* bias,
-                                   const float* res, float* y, hipStream_t s, int kg, float* part)
+                                   const float* res, float* y, hipStream_t s, int kg, float* part, bool reduce)
 {
     if (M < 1 || m.nb == 0 || kg < 1 || kg > (int)m.nb || (kg > 1 && !part)) return hipErrorInvalidValue;
     (void)hipGetLastError();
@@ -1239,7 +1239,7 @@ hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const 
     a.rgs8 = (a.rgs + 7) / 8 * 8;
     dim3 grid((unsigned)(a.rgs8 * (a.xt / 4) * kg));
     hipError_t e = m.scheme == 4 ? launch_nt<4, true>(4, grid, s, a) : launch_nt<3, true>(4, grid, s, a);
-    if (e != hipSuccess || kg == 1) return e;
+    if (e != hipSuccess || kg == 1 || !reduce) return e;
     const int Mp = a.xt / 4 * 32, outs = M * (int)(m.rows_pad / 4);
     hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s, part, kg, Mp,
                        (int)m.rows_pad, (int)m.rows, M, bias, res, y);

@@ -7,6 +7,7 @@
 //   expert loop, combine  qwen3_moe_model.rs:509-530
 #include <hip/hip_runtime.h>
 
+#include "wave.h"
 #include "wpcg_internal.hpp"
 #include "xpack.h"
 
@@ -121,6 +122,50 @@ __global__ __launch_bounds__(256) void k_rms_pack(const float* __restrict__ X, c
         }
         __syncthreads();
         pack_tile_split(&tile[0][0], 132, min(16, n - 16 * q), b, q, XT, xf, xsum, red);
+    }
+}
+
+// o_proj's K-slices added in slice order with its bias and the residual into
+// X (the new residual, as k_gemm_reduce writes it), and that row's RMSNorm
+// (FAST, as k_rms_norm rows computes it: each thread's squares by fused
+// multiply-adds, the wave sums, the four waves in a fixed order) into XN:
+// one workgroup of 256 threads per row, H <= 256 * RN_MAXV.
+constexpr int RN_MAXV = PF_NORM_MAXH / 256;
+__global__ __launch_bounds__(256) void k_pf_reduce_norm(const float* __restrict__ part, int kg, int Mp,
+                                                        int rows_pad, int H, const float* __restrict__ bias,
+                                                        float* __restrict__ X, const float* __restrict__ w,
+                                                        float eps, float* __restrict__ XN)
+{
+    __shared__ float red[4];
+    const int m = blockIdx.x;
+    const size_t slice = (size_t)Mp * rows_pad;
+    float v[RN_MAXV];
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RN_MAXV; i++) {
+        const int k = threadIdx.x + 256 * i;
+        if (k < H) {
+            const float* p = part + (size_t)m * rows_pad + k;
+            float s = p[0];
+            for (int q = 1; q < kg; q++) s = s + p[q * slice];
+            if (bias) s += bias[k];
+            s += X[(size_t)m * H + k];
+            v[i] = s;
+            sq = fmaf(s, s, sq);
+        }
+    }
+    sq = wave_sum(sq);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
+    __syncthreads();
+    const float total = (red[0] + red[1]) + (red[2] + red[3]);
+    const float scale = __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(total, (float)H), eps)));
+#pragma unroll
+    for (int i = 0; i < RN_MAXV; i++) {
+        const int k = threadIdx.x + 256 * i;
+        if (k < H) {
+            X[(size_t)m * H + k] = v[i];
+            XN[(size_t)m * H + k] = __fmul_rn(__fmul_rn(v[i], scale), w[k]);
+        }
     }
 }
 
@@ -252,6 +297,16 @@ hipError_t launch_rms_pack_rows(const float* X, const float* w, int n, int H, fl
     const dim3 grid((unsigned)((n + 15) / 16), (unsigned)((H / 128 + RP_BG - 1) / RP_BG));
     hipLaunchKernelGGL(k_rms_pack, grid, dim3(256), 0, s, X, w, n, H, eps, gemm_rows_tiles(n),
                        static_cast<uint32_t*>(xf), xsum);
+    return hipGetLastError();
+}
+
+hipError_t launch_pf_reduce_norm(const float* part, int kg, int M, int H, int rows_pad, const float* bias, float* X,
+                                 const float* w, float eps, float* XN, hipStream_t s)
+{
+    if (M < 1 || kg < 1 || H < 1 || H > 256 * RN_MAXV || rows_pad < H) return hipErrorInvalidValue;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k_pf_reduce_norm, dim3((unsigned)M), dim3(256), 0, s, part, kg, gemm_rows_tiles(M) / 4 * 32,
+                       rows_pad, H, bias, X, w, eps, XN);
     return hipGetLastError();
 }
 

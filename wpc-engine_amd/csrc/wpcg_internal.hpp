@@ -246,9 +246,11 @@ constexpr int GEMM_GROUP_MAXROWS = 2048;
 inline int gemm_rows_tiles(int M) { return (M + 31) / 32 * 4; }
 hipError_t launch_gemm_pack_rows(const float* x, int M, int K, void* xf, float* xsum, hipStream_t s);
 // kg > 1: K in kg slices whose partials go to part (kg * (gemm_rows_tiles(M) /
-// 4 * 32) * m.rows_pad floats), added in slice order by a second launch.
+// 4 * 32) * m.rows_pad floats), added in slice order by a second launch
+// (reduce), or left there for launch_pf_reduce_norm (bias, res, y unused).
 hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const float* xsum, int M, const float* bias,
-                                   const float* res, float* y, hipStream_t s, int kg = 1, float* part = nullptr);
+                                   const float* res, float* y, hipStream_t s, int kg = 1, float* part = nullptr,
+                                   bool reduce = true);
 // Up to three matrices of the same K and scheme over one packed X in one
 // launch (the projections that share an input: q, k, v; gate, up); no
 // residual.
@@ -366,6 +368,12 @@ hipError_t launch_route_rows(const float* scores, int n, int rows, int top_k, in
 // launch_gemm_pack_rows's layout), H % 128 == 0.
 hipError_t launch_rms_pack_rows(const float* X, const float* w, int n, int H, float eps, void* xf, float* xsum,
                                 hipStream_t s);
+// A K-sliced packed-rows GEMM's partials (launch_gemm_packed_rows with
+// reduce = false) summed with bias and the residual into X [M][H], then each
+// row's FAST RMSNorm with weights w into XN; H <= PF_NORM_MAXH.
+constexpr int PF_NORM_MAXH = 4096;
+hipError_t launch_pf_reduce_norm(const float* part, int kg, int M, int H, int rows_pad, const float* bias, float* X,
+                                 const float* w, float eps, float* XN, hipStream_t s);
 // R[t][e] = X[t] . W[e] (fp32 router rows), R is [T][E].
 hipError_t launch_pf_router(const float* X, const float* W, int T, int E, int K, float* R, hipStream_t s);
 // (token, slot) pairs sorted by expert for launch_gemm_grouped: pair_tok
