@@ -36,6 +36,11 @@ MOE = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, inter=0
 QWEN3_MOE_2L = dict(n_layers=2, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=128, inter=0,
                     vocab=151936, n_experts=128, top_k=8, moe_inter=768, norm_topk=1, tied=0,
                     max_pos=320, eps=1e-6, rope_theta=1e6)
+# Qwen3-4B shapes (config 2) with two of the 36 layers: 128-wide heads (the
+# attention writes o_proj's packed input), o_proj and down in K-slices
+QWEN3_DENSE_2L = dict(n_layers=2, hidden=2560, n_heads=32, n_kv_heads=8, head_dim=128, inter=9728,
+                      vocab=151936, n_experts=0, top_k=0, moe_inter=0, norm_topk=1, tied=1,
+                      max_pos=192, eps=1e-6, rope_theta=1e6)
 # measured: 3e-6 of the logit range, 9e-6 of the cache magnitude
 TOL = 5e-5
 
@@ -99,6 +104,7 @@ def greedy(m, first, steps):
     ("moe-one-pass", MOE, 0, 200, 21),
     ("moe-two-passes", MOE, 3, 290, 22),
     ("qwen3-moe-2L", QWEN3_MOE_2L, 0, 256, 31),
+    ("qwen3-dense-2L", QWEN3_DENSE_2L, 5, 128, 32),
 ])
 def test_fast_prefill_matches_steps(ctx, name, cfg, n_pre, n, seed):
     print(f"[gpu] prefill {name}: {n_pre} steps then {n} tokens", flush=True)
