@@ -39,6 +39,9 @@ struct Prefill {
     void* xf = nullptr;       // packed X of the batched GEMMs (launch_gemm_pack_rows)
     float* xsum = nullptr;
     float* part = nullptr;    // K-slice partials of o_proj / the dense down
+    int cus = 0;              // the device's CUs: the expert-grouped GEMMs' workgroups
+    void* dg = nullptr;       // the expert-grouped GEMMs' X digits (launch_pf_digits)
+    float* dxs = nullptr;
     float* vlogits = nullptr;  // verification: [WPCG_VERIFY_MAX][vocab], made on first use
     uint32_t* vids = nullptr;  // [WPCG_VERIFY_MAX]
 };
@@ -380,6 +383,7 @@ int make_prefill(wpcg_model* m)
     Prefill& P = m->pf;
     if (P.cap) return WPCG_OK;
     const wpcg_model_config& c = m->cfg;
+    WPCG_HIP(hipDeviceGetAttribute(&P.cus, hipDeviceAttributeMultiprocessorCount, m->ctx->device));
     const size_t cap = std::min(PF_CAP, c.max_pos), H = c.hidden, qd = (size_t)c.n_heads * c.head_dim,
                  kvd = (size_t)c.n_kv_heads * c.head_dim;
     int rc = WPCG_OK;
@@ -414,6 +418,9 @@ int make_prefill(wpcg_model* m)
         dev((void**)&P.ge, pairs * I * 4);
         dev((void**)&P.ue, pairs * I * 4);
         dev((void**)&P.de, pairs * H * 4);
+        const size_t dvals = std::max(cap * H, pairs * I);  // gate/up's token rows, then down's pair rows
+        dev(&P.dg, dvals * 4);
+        dev((void**)&P.dxs, dvals / 128 * 8);
     } else {
         dev((void**)&P.g, cap * c.inter * 4);
         dev((void**)&P.u, cap * c.inter * 4);
@@ -478,7 +485,8 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
             continue;
         }
         // experts: route every row, sort the (row, slot) pairs by expert, one
-        // grouped launch per projection, then the ordered combine
+        // grouped launch for gate and up and one for down, then the ordered
+        // combine
         if (fuse_norm)
             WPCG_HIP(launch_pf_reduce_norm(P.part, okg, (int)n, H, (int)L.o->m.rows_pad, L.o->bias, P.x, L.post_ln,
                                            c.eps, P.xn, s));
@@ -486,15 +494,15 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
             WPCG_HIP(launch_rms_norm_rows(F, P.x, L.post_ln, H, (int)n, c.eps, P.xn, s));
         wpcg_moe* E = L.moe;
         const int ne = (int)c.n_experts, K = (int)c.top_k, pairs = (int)n * K;
-        const int max_items = pairs / GEMM_GROUP_COLS + ne + 1;
         WPCG_HIP(launch_pf_router(P.xn, E->router->w, (int)n, ne, H, P.r, s));
         WPCG_HIP(launch_route_rows(P.r, ne, (int)n, K, (int)c.norm_topk, P.ids, P.w, s));
         WPCG_HIP(launch_pf_group(P.ids, pairs, ne, K, P.pair_tok, P.pair_pos, P.items, P.nitems, s));
-        WPCG_HIP(launch_gemm_grouped(E->gate, P.xn, nullptr, (int)n, P.pair_tok, P.items, P.nitems, max_items, P.ge,
-                                     s));
-        WPCG_HIP(launch_gemm_grouped(E->up, P.xn, nullptr, (int)n, P.pair_tok, P.items, P.nitems, max_items, P.ue,
-                                     s));
-        WPCG_HIP(launch_gemm_grouped(E->down, P.ge, P.ue, pairs, nullptr, P.items, P.nitems, max_items, P.de, s));
+        WPCG_HIP(launch_pf_digits(P.xn, nullptr, (int)n, H, P.dg, P.dxs, s));
+        WPCG_HIP(launch_gemm_grouped(E->gate, &E->up, P.dg, P.dxs, (int)n, P.pair_tok, P.items, P.nitems, P.cus,
+                                     P.ge, P.ue, s));
+        WPCG_HIP(launch_pf_digits(P.ge, P.ue, pairs, (int)c.moe_inter, P.dg, P.dxs, s));
+        WPCG_HIP(launch_gemm_grouped(E->down, nullptr, P.dg, P.dxs, pairs, nullptr, P.items, P.nitems, P.cus, P.de,
+                                     nullptr, s));
         WPCG_HIP(launch_pf_combine(P.x, P.de, P.w, P.pair_pos, (int)n, K, H, s));
     }
     return WPCG_OK;

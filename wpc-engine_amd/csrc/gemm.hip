@@ -788,10 +788,9 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
     if (threadIdx.x == 0) __hip_atomic_store(P.counters + rg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// ---- expert-grouped GEMM (prefill): one workgroup per work item = one
-// expert's run of at most GEMM_GROUP_COLS (X row, Y row) pairs, on the int8
-// matrix cores with the FAST GEMV's representation of x: each 128-value
-// block of a pair's X row is x ~= s_b * Q / 2^21, s_b = max|x_b| / 127,
+// ---- expert-grouped GEMM (prefill) on the int8 matrix cores, with the
+// FAST GEMV's representation of x: each 128-value block of an X row is
+// x ~= s_b * Q / 2^21, s_b = max|x_b| / 127,
 // Q = rint(x * 127 * 2^21 / max|x_b|) = d0*2^21 + d1*2^14 + d2*2^7 + d3
 // with int8 digits (d0 = Q >> 21, d1..d3 7-bit fields). The digits of four
 // pairs are the first operand of v_mfma_i32_16x16x64_i8 (row 4p + d: digit d
@@ -803,263 +802,343 @@ __global__ __launch_bounds__(GS_WG) void k_gemm_small(const GemmSmallArgs P)
 // into s_b). The codes need no conversion
 // (the bf16 form of this kernel spent 16 byte permutes per tile and block
 // turning them into bf16, and 54 vector instructions per 4 matrix-core
-// ones in all). An item holds up to 16 pairs (four groups of four), so an
-// expert's weights are streamed once for most experts of a 256-token
-// prompt (with 8 pairs per item, an expert routed ~16 pairs read its
-// matrices twice: ~270 MB per launch where the experts hold ~110 MB). The
-// item's X rows are digitised once into LDS; each wave streams whole row
-// tiles of the expert (tiles w, w + GG_NW, ...; GG_NW waves) through the full K, GG_LA
-// units of codes in flight, in whole unguarded rounds (units past the
-// wave's last read zeros and are dropped), and writes each finished tile's
-// rows x pairs. Items are spread so that consecutive items (one expert's
-// runs) share an XCD and its L2: workgroup b takes item (b % 8) * S + b / 8
-// with S = ceil(nitems / 8).
-// Waves per workgroup: 8, or 16 for v4 down projections (SILU; 128 row
-// tiles: 8 per wave instead of 16, 41.2 -> 37.0 us per launch, where gate
-// and up, 48 tiles, ran slower with 16: 45.2 -> 47.4; v3 spills at 16).
-template <int SCHEME, bool SILU>
-constexpr int gg_waves() { return SCHEME == 4 && SILU ? 16 : 8; }
-constexpr int GG_LA = 8;   // units (tile, block) of codes in flight per wave
+// ones in all). A work item is one expert's run of at most 16 pairs (four
+// groups of four), so an expert's weights are streamed once for most
+// experts of a 256-token prompt (with 8 pairs per item, an expert routed
+// ~16 pairs read its matrices twice: ~270 MB per launch where the experts
+// hold ~110 MB).
+//
+// The digits are made once per X row by k_pf_digits, as records of 512 B
+// per (row, block) in the order the LDS operand wants them: piece (h, q, d)
+// of 16 B holds digit d of the values k = 64 h + q + 4 m of the block, m in
+// the byte order of lane group q's 16-byte code word. (Digitising inside
+// this kernel, per item and pair, cost ~13 us of every workgroup's start:
+// a gate/up pair's token row was digitised once per item that held it.)
+//
+// Work is split evenly over a fixed grid (one workgroup per CU), not one
+// workgroup per item: a unit is (item, matrix, row tile), units are
+// numbered item-major, and workgroup b takes units [b U / G, (b + 1) U / G)
+// of the U = items x matrices x tiles. A 256-token prompt routes ~165 items
+// over 128 experts: with one workgroup per item (its X digits, 128 KiB of
+// LDS, allow one per CU) 91 CUs sat idle and every CU that worked ran a
+// whole item. A workgroup's range covers one item or the end of one and the
+// start of the next (segments): per item it copies the item's digit records
+// into LDS once, and its waves stream the segment's units (tile s0 + w,
+// s0 + w + GG_NW, ... for wave w) through the full K, GG_LA units of codes in
+// flight, in whole unguarded rounds (units past the wave's last read zeros
+// and are dropped), writing each finished tile's rows x pairs. Two matrices
+// of one shape over the same X (gate and up) share a launch and each
+// item's digits.
 constexpr int GG_CT = 2;   // tiles per chunk: the units of one step
 constexpr int GG_PG = (GEMM_GROUP_COLS + 3) / 4;  // groups of four pairs
 struct GemmGroupArgs {
-    const uint8_t* codes;
-    const uint8_t* hp;
-    const uint32_t* params;
-    const float* x;      // [xrows][K]
-    const float* xu;     // SILU: X = silu(x) * xu, same shape
-    float* y;            // [pairs][rows]
+    const uint8_t* codes[2];
+    const uint8_t* hp[2];
+    const uint32_t* params[2];
+    float* y[2];         // [pairs][rows] per matrix
+    const uint8_t* dg;   // X digits, [xrows][nb] records of 512 B (launch_pf_digits)
+    const float2* dxs;   // [xrows][nb] {s_b 2^-7, sum}
     const int* rowidx;   // X row of pair p (null: row p)
     const int* items;    // [3 * n]: expert, first pair, count
     const int* nitems;
     size_t ecodes, ehp, eparams;
-    int rows, rows_pad, nb, xrows;
+    int rows, rows_pad, nb, xrows, nmat;
 };
 
-// Byte of x index k (0..127) of pair p (0..3) digit d in a (block, pair
-// group) digit area: half k >> 6 (1 KiB each), lane group k & 3 (256 B:
-// 16 rows of 16 bytes), row 4p + d, byte ((k >> 3) & 7) + 8 ((k >> 2) & 1):
-// the order in which lane group g's 16-byte code word holds the codes.
-__device__ __forceinline__ int gg_pos(int k, int p, int d)
+// Byte of value k (0..127) of a block, digit d, in its 512-byte record:
+// piece (h = k >> 6, q = k & 3, d), byte ((k >> 3) & 7) + 8 ((k >> 2) & 1),
+// the order in which lane group q's 16-byte code word holds the codes.
+__device__ __forceinline__ int dg_pos(int k, int d)
 {
-    return (k >> 6) * 1024 + (k & 3) * 256 + (4 * p + d) * 16 + ((k >> 3) & 7) + 8 * ((k >> 2) & 1);
+    return (k >> 6) * 256 + (k & 3) * 64 + d * 16 + ((k >> 3) & 7) + 8 * ((k >> 2) & 1);
 }
 
-template <int SCHEME, bool SILU>
-__global__ __launch_bounds__((gg_waves<SCHEME, SILU>() * 64)) void k_gemm_grouped(const GemmGroupArgs P)
+// X rows to digit records (the grouped GEMM's X): workgroup (row, group of
+// eight blocks), 32 lanes per block with four consecutive values each.
+// SILU: X = silu(x) * xu (the FAST steps' arithmetic). The block's max |x|
+// and sum over its 32 lanes by DPP inside rows of 16 and the row swap; the
+// digits are staged in LDS and leave as whole 16-byte pieces.
+template <bool SILU>
+__global__ __launch_bounds__(256) void k_pf_digits(const float* __restrict__ X, const float* __restrict__ XU, int K,
+                                                   uint8_t* __restrict__ dg, float2* __restrict__ dxs)
 {
-    constexpr int GG_NW = gg_waves<SCHEME, SILU>(), GG_WG = GG_NW * 64;
+    __shared__ __align__(16) uint8_t stage[8][512];
+    const int row = blockIdx.x, nb = K / 128, bl = threadIdx.x >> 5, b = blockIdx.y * 8 + bl;
+    const int lane = threadIdx.x & 63, k0 = 4 * (lane & 31);
+    const bool ok = b < nb;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (ok) {
+        const float4 x = *reinterpret_cast<const float4*>(X + (size_t)row * K + b * 128 + k0);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+        if constexpr (SILU) {
+            const float4 u = *reinterpret_cast<const float4*>(XU + (size_t)row * K + b * 128 + k0);
+            const float uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) v[q] = __fdividef(v[q], 1.0f + __expf(-v[q])) * uu[q];
+        }
+    }
+    uint32_t mb = __float_as_uint(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    float sm = (v[0] + v[1]) + (v[2] + v[3]);
+    mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0xB1, 0xF, 0xF, false));
+    sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
+    mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x4E, 0xF, 0xF, false));
+    sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
+    mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x141, 0xF, 0xF, false));
+    sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x141, 0xF, 0xF, false));
+    mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x140, 0xF, 0xF, false));
+    sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x140, 0xF, 0xF, false));
+    const auto mr = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
+    const float Mx = __uint_as_float(max((uint32_t)mr[0], (uint32_t)mr[1]));
+    const auto sr = __builtin_amdgcn_permlane16_swap(__float_as_uint(sm), __float_as_uint(sm), false, false);
+    const float Sx = __uint_as_float(sr[0]) + __uint_as_float(sr[1]);
+    const float inv = Mx > 0.0f ? (127.0f * 2097152.0f) * __builtin_amdgcn_rcpf(Mx) : 0.0f;
+    uint8_t* st = stage[bl];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int Q = (int)rintf(v[q] * inv);
+        const int k = k0 + q;
+        st[dg_pos(k, 0)] = (uint8_t)(Q >> 21);
+        st[dg_pos(k, 1)] = (uint8_t)((Q >> 14) & 127);
+        st[dg_pos(k, 2)] = (uint8_t)((Q >> 7) & 127);
+        st[dg_pos(k, 3)] = (uint8_t)(Q & 127);
+    }
+    if (ok && (lane & 31) == 0)
+        dxs[(size_t)row * nb + b] = make_float2(Mx * (1.0f / 127.0f) * 0x1p-7f, Sx);  // s_b 2^-7
+    __syncthreads();
+    // thread t: piece t % 32 of block t / 32 of the group
+    if (ok)
+        *reinterpret_cast<u32x4*>(dg + ((size_t)row * nb + b) * 512 + (threadIdx.x & 31) * 16) =
+            *reinterpret_cast<const u32x4*>(&stage[bl][(threadIdx.x & 31) * 16]);
+}
+
+template <int SCHEME, int GG_NW>
+__global__ __launch_bounds__(GG_NW * 64) void k_gemm_grouped(const GemmGroupArgs P)
+{
+    constexpr int GG_WG = GG_NW * 64;
+    constexpr bool PIPE = GG_NW == 8;  // two product sets fit in the registers of 8 waves
+    constexpr int GG_LA = PIPE ? 8 : 6;  // units (tile, block) of codes in flight per wave
     __shared__ __align__(16) int8_t xd[GEMM_GROUP_MAXBK][GG_PG][2048];       // digits
     __shared__ float2 xs[GEMM_GROUP_MAXBK][GG_PG * 4];                       // {s_b, sum(x_b)}
-    const int nitems = *P.nitems;
-    const int S = (nitems + 7) / 8;
-    const int item = (int)(blockIdx.x % 8) * S + (int)(blockIdx.x / 8);
-    if ((int)(blockIdx.x / 8) >= S || item >= nitems) return;  // uniform
-    const int e = P.items[3 * item], p0 = P.items[3 * item + 1], M = P.items[3 * item + 2];
-    const int nb = P.nb, K = nb * 128;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int g = lane >> 4, j = lane & 15;
-    const int ntiles = P.rows_pad / TILE_ROWS;
-
-    // This wave's tiles are wave, wave + GG_NW, ...; it takes them GG_CT at a
-    // time (a chunk), block by block: step s is block s % nb of chunk s / nb,
-    // and its units are the chunk's tiles at that block, so one read of the
-    // block's digits serves GG_CT tiles.
-    const int my_tiles = ntiles > wave ? (ntiles - wave + GG_NW - 1) / GG_NW : 0;
-    const int nsteps = (my_tiles + GG_CT - 1) / GG_CT * nb;
-    const uint8_t* codes = P.codes + (size_t)e * P.ecodes;
-    const uint8_t* hpl = P.hp + (size_t)e * P.ehp;
-    const uint32_t* params = P.params + (size_t)e * P.eparams;
+    const int nb = P.nb;
+    const int ntiles = P.rows_pad / TILE_ROWS, nmat = P.nmat;
+    const int64_t total = (int64_t)(*P.nitems) * nmat * ntiles;
+    const int ub0 = (int)(total * blockIdx.x / gridDim.x), ub1 = (int)(total * (blockIdx.x + 1) / gridDim.x);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nrec = ntiles * nb;
-    const auto crs = buf_rsrc(codes, nrec * (int)CODE_REC);
-    const auto hrs = buf_rsrc(SCHEME == 3 ? hpl : codes, SCHEME == 3 ? nrec * (int)HP_REC : 0);
-    const auto prs = buf_rsrc(params, nrec * TILE_ROWS * 4);
-    u32x4 cr[GG_LA];
-    u32x2 hr[GG_LA];
-    uint32_t pr[GG_LA];
-    // units are requested in order: the next step's chunk and block are
-    // (lc, lb), unit tt of it tile wave + GG_NW (GG_CT lc + tt); a tile past the
-    // wave's last (or a step past the end) reads record nrec, past the range
-    // (zeros, never used)
-    int lc = 0, lb = 0;
-    auto load_step = [&](int slot0) {
-#pragma unroll
-        for (int tt = 0; tt < GG_CT; tt++) {
-            const int tl = GG_CT * lc + tt;
-            const int rec = tl < my_tiles ? (wave + GG_NW * tl) * nb + lb : nrec;
-            const int slot = slot0 + tt;
-            cr[slot] = __builtin_amdgcn_raw_buffer_load_b128(crs, rec * (int)CODE_REC + lane * 16, 0, CPOL_NT);
-            if constexpr (SCHEME == 3)
-                hr[slot] = __builtin_amdgcn_raw_buffer_load_b64(hrs, rec * (int)HP_REC + lane * 8, 0, CPOL_NT);
-            pr[slot] = __builtin_amdgcn_raw_buffer_load_b32(prs, (rec * TILE_ROWS + j) * 4, 0, CPOL_NT);
-        }
-        if (++lb == nb) {
-            lb = 0;
-            lc++;
-        }
-    };
+    const auto drs = buf_rsrc(P.dg, P.xrows * nb * 512);
 
-    // ---- X: task (pair c, block blk) is 128 values, 32 lanes with four
-    // consecutive values each; a wave takes two tasks at a time (tasks
-    // 2*(wave + GG_NW i) and +1), every load of every task issued first
-    constexpr int XT = (GEMM_GROUP_COLS * GEMM_GROUP_MAXBK + 2 * GG_NW - 1) / (2 * GG_NW);  // task pairs per wave at most
-    const int ntask = M * nb;
-    const auto xrs = buf_rsrc(P.x, P.xrows * K * 4);
-    const auto urs = buf_rsrc(SILU ? P.xu : P.x, SILU ? P.xrows * K * 4 : 0);
-    const int hi = lane >> 5, k0 = 4 * (lane & 31);
-    u32x4 xv[XT], xw[SILU ? XT : 1];
-#pragma unroll
-    for (int i = 0; i < XT; i++) {
-        const int t = 2 * (wave + GG_NW * i) + hi;
-        const int c = t % max(M, 1), blk = t / max(M, 1);
-        const int xr = t < ntask ? (P.rowidx ? P.rowidx[p0 + c] : p0 + c) : 0;
-        const int off = t < ntask ? (xr * K + blk * 128 + k0) * 4 : 0x7FFFFFF0;
-        xv[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
-        if constexpr (SILU) xw[i] = __builtin_amdgcn_raw_buffer_load_b128(urs, off, 0, 0);
-    }
-#pragma unroll
-    for (int u = 0; u < GG_LA; u += GG_CT) load_step(u);
-    __builtin_amdgcn_sched_barrier(0);
+    // the segments: matrix mt of item it, row tiles [s0, s1) (a
+    // workgroup-uniform loop); the X digits are read when the item changes
+    int cur = -1;
+    for (int sg = ub0 / ntiles; ub0 < ub1 && sg * ntiles < ub1; sg++) {
+        // the lane index passes through an empty asm so that nothing derived
+        // from it (LDS and buffer offsets) is hoisted out of this loop and
+        // held in registers across the step stream (182 VGPRs against 128)
+        int lane = (int)threadIdx.x & 63;
+        asm volatile("" : "+v"(lane));
+        const int g = lane >> 4, j = lane & 15;
+        const int s0 = max(ub0 - sg * ntiles, 0), s1 = min(ub1 - sg * ntiles, ntiles);
+        const int it = sg / nmat, mt = sg - it * nmat;
+        const int e = P.items[3 * it], p0 = P.items[3 * it + 1], M = P.items[3 * it + 2];
+        const bool fresh = it != cur;
+        if (fresh && cur >= 0) __syncthreads();  // the previous item's digits are no longer read
 
-    // ---- digits: the block's max |x| and sum over its 32 lanes (DPP inside
-    // rows of 16, then the row swap), then Q and its four digits into LDS
-#pragma unroll
-    for (int i = 0; i < XT; i++) {
-        const int t0 = 2 * (wave + GG_NW * i);
-        if (t0 >= ntask) break;  // uniform per wave
-        const int t = t0 + hi;
-        const int c = t % max(M, 1), blk = t / max(M, 1);
-        float v[4] = {__uint_as_float(xv[i].x), __uint_as_float(xv[i].y), __uint_as_float(xv[i].z),
-                      __uint_as_float(xv[i].w)};
-        if constexpr (SILU) {  // the FAST steps' silu(g) * u
-            const float u[4] = {__uint_as_float(xw[i].x), __uint_as_float(xw[i].y), __uint_as_float(xw[i].z),
-                                __uint_as_float(xw[i].w)};
-#pragma unroll
-            for (int q = 0; q < 4; q++) v[q] = __fdividef(v[q], 1.0f + __expf(-v[q])) * u[q];
-        }
-        uint32_t mb = __float_as_uint(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-        float sm = (v[0] + v[1]) + (v[2] + v[3]);
-        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0xB1, 0xF, 0xF, false));
-        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
-        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x4E, 0xF, 0xF, false));
-        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
-        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x141, 0xF, 0xF, false));
-        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x141, 0xF, 0xF, false));
-        mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x140, 0xF, 0xF, false));
-        sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x140, 0xF, 0xF, false));
-        const auto mr = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
-        const float Mx = __uint_as_float(max((uint32_t)mr[0], (uint32_t)mr[1]));
-        const auto sr = __builtin_amdgcn_permlane16_swap(__float_as_uint(sm), __float_as_uint(sm), false, false);
-        const float Sx = __uint_as_float(sr[0]) + __uint_as_float(sr[1]);
-        const float inv = Mx > 0.0f ? (127.0f * 2097152.0f) * __builtin_amdgcn_rcpf(Mx) : 0.0f;
-        if (t < ntask) {
-            int8_t* dst = &xd[blk][c >> 2][0];
-            const int p = c & 3;
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int Q = (int)rintf(v[q] * inv);
-                const int k = k0 + q;
-                dst[gg_pos(k, p, 0)] = (int8_t)(Q >> 21);
-                dst[gg_pos(k, p, 1)] = (int8_t)((Q >> 14) & 127);
-                dst[gg_pos(k, p, 2)] = (int8_t)((Q >> 7) & 127);
-                dst[gg_pos(k, p, 3)] = (int8_t)(Q & 127);
-            }
-            if ((lane & 31) == 0) xs[blk][c] = make_float2(Mx * (1.0f / 127.0f) * 0x1p-7f, Sx);  // s_b 2^-7
-        }
-    }
-    // pairs M .. GEMM_GROUP_COLS-1: zero digits and parameters (every pair
-    // group runs unconditionally: a branch per group split the units'
-    // matrix-core chains apart)
-    for (int z = threadIdx.x; z < nb * (GEMM_GROUP_COLS - M) * 128; z += GG_WG) {
-        const int c = M + z / (nb * 128), r = z % (nb * 128), blk = r >> 7, k = r & 127;
-        int8_t* dst = &xd[blk][c >> 2][0];
-#pragma unroll
-        for (int d = 0; d < 4; d++) dst[gg_pos(k, c & 3, d)] = 0;
-        if (k == 0) xs[blk][c] = make_float2(0.0f, 0.0f);
-    }
-    __syncthreads();
-
-    // ---- the step stream, whole rounds of GG_LA / GG_CT steps: per step the
-    // block's digits (every pair group, both halves) and {s_b, sum} once, then
-    // the chunk's GG_CT tiles, GG_PG independent matrix-core chains each,
-    // then their epilogues
-    float acc[GG_CT][GG_PG], zacc[GG_CT][GG_PG];
-#pragma unroll
-    for (int tt = 0; tt < GG_CT; tt++)
-#pragma unroll
-        for (int q = 0; q < GG_PG; q++) acc[tt][q] = zacc[tt][q] = 0.0f;
-    int ub = 0, uc = 0;  // block and chunk of the next step to finish
-    auto step = [&](int slot0) {
-        v4i A0[GG_PG], A1[GG_PG];
-        float2 sx[GG_PG];
-#pragma unroll
-        for (int pg = 0; pg < GG_PG; pg++) {
-            const int8_t* a = &xd[ub][pg][g * 256 + j * 16];
-            A0[pg] = *reinterpret_cast<const v4i*>(a);
-            A1[pg] = *reinterpret_cast<const v4i*>(a + 1024);
-            sx[pg] = xs[ub][pg * 4 + g];
-        }
-        v4i D[GG_CT][GG_PG];
-#pragma unroll
-        for (int tt = 0; tt < GG_CT; tt++) {
-            const int slot = slot0 + tt;
-            const u32x4 U = cr[slot];
-            const uint32_t MK = 0x0F0F0F0Fu;
-            v4i lo = {(int)(U.x & MK), (int)(U.y & MK), (int)(U.z & MK), (int)(U.w & MK)};
-            v4i hi = {(int)((U.x >> 4) & MK), (int)((U.y >> 4) & MK), (int)((U.z >> 4) & MK), (int)((U.w >> 4) & MK)};
-            if constexpr (SCHEME == 3) {
-                // top two bits: group g holds AVX lanes g (h.x) and g+4 (h.y)
-                const uint32_t T6 = 0x30303030u, hx = hr[slot].x, hy = hr[slot].y;
-                lo.x |= (int)((hx << 4) & T6); lo.y |= (int)((hx << 2) & T6);
-                lo.z |= (int)((hy << 4) & T6); lo.w |= (int)((hy << 2) & T6);
-                hi.x |= (int)(hx & T6);        hi.y |= (int)((hx >> 2) & T6);
-                hi.z |= (int)(hy & T6);        hi.w |= (int)((hy >> 2) & T6);
-            }
-#pragma unroll
-            for (int pg = 0; pg < GG_PG; pg++) {
-                D[tt][pg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0[pg], lo, v4i{0, 0, 0, 0}, 0, 0, 0);
-                D[tt][pg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1[pg], hi, D[tt][pg], 0, 0, 0);
-            }
-        }
-#pragma unroll
-        for (int tt = 0; tt < GG_CT; tt++) {
-            const uint32_t pp = pr[slot0 + tt];
-            const float sc = h2f(pp >> 16), zp = h2f(pp & 0xFFFFu);
-#pragma unroll
-            for (int pg = 0; pg < GG_PG; pg++) {
-                // D0 2^7 + D1 and D2 2^7 + D3 are exact in int32 (|D| < 2^21),
-                // so the digit sum is two conversions and one fma
-                const v4i& d = D[tt][pg];
-                const float dh = (float)(d.x * 128 + d.y), dl = (float)(d.z * 128 + d.w);
-                const float cd = fmaf(dl, 0x1p-14f, dh);
-                acc[tt][pg] = __builtin_fmaf(cd * sx[pg].x, sc, acc[tt][pg]);
-                zacc[tt][pg] = __builtin_fmaf(zp, sx[pg].y, zacc[tt][pg]);
-            }
-        }
-        if (++ub == nb) {  // the chunk is complete: lane (g, j) has pair pg*4 + g, row j of each tile
+        // This wave's tiles are s0 + wave, s0 + wave + GG_NW, ...; it takes
+        // them GG_CT at a time (a chunk), block by block: step s is block
+        // s % nb of chunk s / nb, and its units are the chunk's tiles at that
+        // block, so one read of the block's digits serves GG_CT tiles.
+        const int my_tiles = s1 - s0 > wave ? (s1 - s0 - wave + GG_NW - 1) / GG_NW : 0;
+        const int nsteps = (my_tiles + GG_CT - 1) / GG_CT * nb;
+        const auto crs = buf_rsrc(P.codes[mt] + (size_t)e * P.ecodes, nrec * (int)CODE_REC);
+        const auto hrs = buf_rsrc(SCHEME == 3 ? P.hp[mt] + (size_t)e * P.ehp : P.codes[mt],
+                                  SCHEME == 3 ? nrec * (int)HP_REC : 0);
+        const auto prs = buf_rsrc(P.params[mt] + (size_t)e * P.eparams, nrec * TILE_ROWS * 4);
+        float* const y = P.y[mt];
+        u32x4 cr[GG_LA];
+        u32x2 hr[GG_LA];
+        uint32_t pr[GG_LA];
+        // units are requested in order: the next step's chunk and block are
+        // (lc, lb), unit tt of it tile s0 + wave + GG_NW (GG_CT lc + tt); a
+        // tile past the wave's last (or a step past the end) reads record
+        // nrec, past the range (zeros, never used)
+        int lc = 0, lb = 0;
+        auto load_step = [&](int slot0) {
 #pragma unroll
             for (int tt = 0; tt < GG_CT; tt++) {
-                const int tl = GG_CT * uc + tt;
-                const int row = (wave + GG_NW * tl) * TILE_ROWS + j;
-                if (tl < my_tiles && row < P.rows) {
+                const int tl = GG_CT * lc + tt;
+                const int rec = tl < my_tiles ? (s0 + wave + GG_NW * tl) * nb + lb : nrec;
+                const int slot = slot0 + tt;
+                cr[slot] = __builtin_amdgcn_raw_buffer_load_b128(crs, rec * (int)CODE_REC + lane * 16, 0, CPOL_NT);
+                if constexpr (SCHEME == 3)
+                    hr[slot] = __builtin_amdgcn_raw_buffer_load_b64(hrs, rec * (int)HP_REC + lane * 8, 0, CPOL_NT);
+                pr[slot] = __builtin_amdgcn_raw_buffer_load_b32(prs, (rec * TILE_ROWS + j) * 4, 0, CPOL_NT);
+            }
+            if (++lb == nb) {
+                lb = 0;
+                lc++;
+            }
+        };
+
+        if (!fresh) {  // the digits in LDS are this item's
 #pragma unroll
-                    for (int pg = 0; pg < GG_PG; pg++)
-                        if (pg * 4 + g < M) P.y[(size_t)(p0 + pg * 4 + g) * P.rows + row] = acc[tt][pg] + zacc[tt][pg];
+            for (int u = 0; u < GG_LA; u += GG_CT) load_step(u);
+        } else {
+            // ---- the item's X digits into LDS: record (pair c, block blk) is
+            // 32 pieces of 16 B, piece (h, q, d) to xd[blk][c / 4] at
+            // h KiB + q * 256 + (4 (c % 4) + d) * 16; slot u of a thread
+            // holds pair c = u * GG_WG / 512 + threadIdx.x / 512 (uniform
+            // per wave: one scalar load of its X row), block
+            // (threadIdx.x / 32) % 16, piece threadIdx.x % 32. Pairs past M
+            // keep whatever the LDS holds: their products are never stored.
+            constexpr int PS = GEMM_GROUP_COLS * GEMM_GROUP_MAXBK * 32 / GG_WG;  // slots per thread
+            constexpr int CPS = GG_WG / 512;                                     // pairs per slot
+            const int blk = (threadIdx.x >> 5) & 15, pc = threadIdx.x & 31;
+            const int c0 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 9);
+            // lane l < 16 of every wave: the X row of pair l
+            const int vrow = (lane & 15) < M ? (P.rowidx ? P.rowidx[p0 + (lane & 15)] : p0 + (lane & 15)) : 0;
+#pragma unroll
+            for (int u = 0; u < GG_LA; u += GG_CT) load_step(u);
+            u32x4 pv[PS];
+#pragma unroll
+            for (int u = 0; u < PS; u++) {
+                const int c = u * CPS + c0;
+                const int r = __builtin_amdgcn_readlane(vrow, c & 15);
+                const bool ok = c < M && blk < nb;
+                pv[u] = __builtin_amdgcn_raw_buffer_load_b128(drs, ok ? ((r * nb + blk) * 512 + pc * 16) : 0x7FFFFFF0, 0,
+                                                              0);
+            }
+            // {s_b, sum} of (pair t / 16, block t % 16), threads t < 256
+            const int sc_ = (threadIdx.x >> 4) & 15, sb_ = threadIdx.x & 15;
+            const bool sok = threadIdx.x < 256 && sc_ < M && sb_ < nb;
+            const int srow = __builtin_amdgcn_ds_bpermute(4 * sc_, vrow);
+            const float2 sv = sok ? P.dxs[(size_t)srow * nb + sb_] : make_float2(0.0f, 0.0f);
+            // every slot is written (zeros past M and nb: harmless), so no
+            // load is left pending on any path into the step loop
+#pragma unroll
+            for (int u = 0; u < PS; u++) {
+                const int c = u * CPS + c0;
+                *reinterpret_cast<u32x4*>(&xd[blk][c >> 2][(pc >> 4) * 1024 + ((pc >> 2) & 3) * 256 +
+                                                           (4 * (c & 3) + (pc & 3)) * 16]) = pv[u];
+            }
+            if (threadIdx.x < 256) xs[sb_][sc_] = sv;
+            __syncthreads();
+            cur = it;
+        }
+
+        // ---- the step stream, whole rounds of GG_LA / GG_CT steps: per step
+        // the block's digits (every pair group, both halves) and {s_b, sum}
+        // once, then the chunk's GG_CT tiles, GG_PG independent matrix-core
+        // chains each, then their epilogues. Software-pipelined by one step:
+        // step s + 1's products are issued before step s's epilogue, so the
+        // epilogue's vector instructions run while the matrix cores work
+        // (D and {s_b, sum} in two sets, by step parity).
+        float acc[GG_CT][GG_PG], zacc[GG_CT][GG_PG];
+#pragma unroll
+        for (int tt = 0; tt < GG_CT; tt++)
+#pragma unroll
+            for (int q = 0; q < GG_PG; q++) acc[tt][q] = zacc[tt][q] = 0.0f;
+        int ub = 0, uc = 0;  // block and chunk of the next step to finish
+        int mb = 0;          // block of the next step to multiply
+        v4i D[2][GG_CT][GG_PG];
+        float2 sx[2][GG_PG];
+        auto products = [&](int slot0, int par) {
+            v4i A0[GG_PG], A1[GG_PG];
+#pragma unroll
+            for (int pg = 0; pg < GG_PG; pg++) {
+                const int8_t* a = &xd[mb][pg][g * 256 + j * 16];
+                A0[pg] = *reinterpret_cast<const v4i*>(a);
+                A1[pg] = *reinterpret_cast<const v4i*>(a + 1024);
+                sx[par][pg] = xs[mb][pg * 4 + g];
+            }
+            if (++mb == nb) mb = 0;
+#pragma unroll
+            for (int tt = 0; tt < GG_CT; tt++) {
+                const int slot = slot0 + tt;
+                const u32x4 W = cr[slot];
+                const uint32_t MK = 0x0F0F0F0Fu;
+                v4i lo = {(int)(W.x & MK), (int)(W.y & MK), (int)(W.z & MK), (int)(W.w & MK)};
+                v4i hi4 = {(int)((W.x >> 4) & MK), (int)((W.y >> 4) & MK), (int)((W.z >> 4) & MK),
+                           (int)((W.w >> 4) & MK)};
+                if constexpr (SCHEME == 3) {
+                    // top two bits: group g holds AVX lanes g (h.x) and g+4 (h.y)
+                    const uint32_t T6 = 0x30303030u, hx = hr[slot].x, hy = hr[slot].y;
+                    lo.x |= (int)((hx << 4) & T6); lo.y |= (int)((hx << 2) & T6);
+                    lo.z |= (int)((hy << 4) & T6); lo.w |= (int)((hy << 2) & T6);
+                    hi4.x |= (int)(hx & T6);       hi4.y |= (int)((hx >> 2) & T6);
+                    hi4.z |= (int)(hy & T6);       hi4.w |= (int)((hy >> 2) & T6);
                 }
 #pragma unroll
-                for (int pg = 0; pg < GG_PG; pg++) acc[tt][pg] = zacc[tt][pg] = 0.0f;
+                for (int pg = 0; pg < GG_PG; pg++) {
+                    D[par][tt][pg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A0[pg], lo, v4i{0, 0, 0, 0}, 0, 0, 0);
+                    D[par][tt][pg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A1[pg], hi4, D[par][tt][pg], 0, 0, 0);
+                }
             }
-            ub = 0;
-            uc++;
-        }
-    };
-    constexpr int SPR = GG_LA / GG_CT;  // steps per round
-    const int rounds = (nsteps + SPR - 1) / SPR * SPR;
-    for (int s0 = 0; s0 < rounds; s0 += SPR) {
+        };
+        auto epilogue = [&](int slot0, int par) {
 #pragma unroll
-        for (int k = 0; k < SPR; k++) {
-            step(k * GG_CT);
-            load_step(k * GG_CT);
+            for (int tt = 0; tt < GG_CT; tt++) {
+                const uint32_t pp = pr[slot0 + tt];
+                const float sc = h2f(pp >> 16), zp = h2f(pp & 0xFFFFu);
+#pragma unroll
+                for (int pg = 0; pg < GG_PG; pg++) {
+                    // D0 2^7 + D1 and D2 2^7 + D3 are exact in int32 (|D| < 2^21),
+                    // so the digit sum is two conversions and one fma
+                    const v4i& d = D[par][tt][pg];
+                    const float dh = (float)(d.x * 128 + d.y), dl = (float)(d.z * 128 + d.w);
+                    const float cd = fmaf(dl, 0x1p-14f, dh);
+                    acc[tt][pg] = __builtin_fmaf(cd * sx[par][pg].x, sc, acc[tt][pg]);
+                    zacc[tt][pg] = __builtin_fmaf(zp, sx[par][pg].y, zacc[tt][pg]);
+                }
+            }
+            // the next step's products, one matrix-core instruction between
+            // every six vector ones (the code unpack and this epilogue)
+            if constexpr (PIPE) {
+#pragma unroll
+                for (int i = 0; i < 2 * GG_CT * GG_PG; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+                }
+            }
+            if (++ub == nb) {  // the chunk is complete: lane (g, j) has pair pg*4 + g, row j of each tile
+#pragma unroll
+                for (int tt = 0; tt < GG_CT; tt++) {
+                    const int tl = GG_CT * uc + tt;
+                    const int row = (s0 + wave + GG_NW * tl) * TILE_ROWS + j;
+                    if (tl < my_tiles && row < P.rows) {
+#pragma unroll
+                        for (int pg = 0; pg < GG_PG; pg++)
+                            if (pg * 4 + g < M) y[(size_t)(p0 + pg * 4 + g) * P.rows + row] = acc[tt][pg] + zacc[tt][pg];
+                    }
+#pragma unroll
+                    for (int pg = 0; pg < GG_PG; pg++) acc[tt][pg] = zacc[tt][pg] = 0.0f;
+                }
+                ub = 0;
+                uc++;
+            }
+        };
+        constexpr int SPR = GG_LA / GG_CT;  // steps per round (even when pipelined: step k's set is k & 1)
+        static_assert(!PIPE || SPR % 2 == 0, "step parity must be static");
+        const int nst = (nsteps + SPR - 1) / SPR * SPR;  // whole rounds
+        if constexpr (PIPE) {
+            if (nst > 0) products(0, 0);
+            for (int st = 0; st < nst; st += SPR) {
+#pragma unroll
+                for (int k = 0; k < SPR; k++) {
+                    // (past the last step: products of zeros, never used)
+                    products(((k + 1) % SPR) * GG_CT, (k + 1) & 1);
+                    epilogue(k * GG_CT, k & 1);
+                    load_step(k * GG_CT);
+                }
+            }
+        } else {
+            for (int st = 0; st < nst; st += SPR) {
+#pragma unroll
+                for (int k = 0; k < SPR; k++) {
+                    products(k * GG_CT, 0);
+                    epilogue(k * GG_CT, 0);
+                    load_step(k * GG_CT);
+                }
+            }
         }
     }
 }
@@ -1290,20 +1369,41 @@ hipError_t launch_gemm_packed_rows_multi(const DeviceMatrix* const* ms, const fl
     return m.scheme == 4 ? launch_nt<4, true>(4, grid, s, a) : launch_nt<3, true>(4, grid, s, a);
 }
 
-hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, const float* xu, int xrows, const int* rowidx,
-                               const int* items, const int* nitems, int max_items, float* y, hipStream_t s)
+hipError_t launch_pf_digits(const float* x, const float* xu, int rows, int K, void* dg, float* dxs, hipStream_t s)
+{
+    if (rows < 1 || K < 128 || K % 128) return hipErrorInvalidValue;
+    (void)hipGetLastError();
+    const dim3 grid((unsigned)rows, (unsigned)((K / 128 + 7) / 8));
+    if (xu)
+        hipLaunchKernelGGL(k_pf_digits<true>, grid, dim3(256), 0, s, x, xu, K, static_cast<uint8_t*>(dg),
+                           reinterpret_cast<float2*>(dxs));
+    else
+        hipLaunchKernelGGL(k_pf_digits<false>, grid, dim3(256), 0, s, x, xu, K, static_cast<uint8_t*>(dg),
+                           reinterpret_cast<float2*>(dxs));
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_grouped(const DeviceMatrix& m, const DeviceMatrix* m2, const void* dg, const float* dxs,
+                               int xrows, const int* rowidx, const int* items, const int* nitems, int wgs, float* y,
+                               float* y2, hipStream_t s)
 {
     if (m.nb == 0 || m.nb > (uint64_t)GEMM_GROUP_MAXBK || m.rows_pad > (uint64_t)GEMM_GROUP_MAXROWS || xrows < 1 ||
-        max_items < 1)
+        (uint64_t)xrows * m.nb * 512 > 0x7FFFFFF0ull || wgs < 1 || !y || (m2 != nullptr) != (y2 != nullptr))
+        return hipErrorInvalidValue;
+    if (m2 && (m2->scheme != m.scheme || m2->rows != m.rows || m2->rows_pad != m.rows_pad || m2->nb != m.nb))
         return hipErrorInvalidValue;
     (void)hipGetLastError();
     GemmGroupArgs a{};
-    a.codes = m.codes;
-    a.hp = m.hp;
-    a.params = m.params;
-    a.x = x;
-    a.xu = xu;
-    a.y = y;
+    const DeviceMatrix* ms[2] = {&m, m2 ? m2 : &m};
+    for (int i = 0; i < 2; i++) {
+        a.codes[i] = ms[i]->codes;
+        a.hp[i] = ms[i]->hp;
+        a.params[i] = ms[i]->params;
+    }
+    a.y[0] = y;
+    a.y[1] = m2 ? y2 : y;
+    a.dg = static_cast<const uint8_t*>(dg);
+    a.dxs = reinterpret_cast<const float2*>(dxs);
     a.rowidx = rowidx;
     a.items = items;
     a.nitems = nitems;
@@ -1315,13 +1415,15 @@ hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, const floa
     a.rows_pad = (int)m.rows_pad;
     a.nb = (int)m.nb;
     a.xrows = xrows;
-    dim3 grid((unsigned)((max_items + 7) / 8 * 8));
-    if (m.scheme == 4) {
-        if (xu) hipLaunchKernelGGL((k_gemm_grouped<4, true>), grid, dim3(gg_waves<4, true>() * 64), 0, s, a);
-        else hipLaunchKernelGGL((k_gemm_grouped<4, false>), grid, dim3(gg_waves<4, false>() * 64), 0, s, a);
+    a.nmat = m2 ? 2 : 1;
+    const dim3 grid((unsigned)wgs);
+    // 16 waves for one matrix of 128+ row tiles (a down projection), else 8
+    if (!m2 && tiles >= 128) {
+        if (m.scheme == 4) hipLaunchKernelGGL((k_gemm_grouped<4, 16>), grid, dim3(1024), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_grouped<3, 16>), grid, dim3(1024), 0, s, a);
     } else {
-        if (xu) hipLaunchKernelGGL((k_gemm_grouped<3, true>), grid, dim3(gg_waves<3, true>() * 64), 0, s, a);
-        else hipLaunchKernelGGL((k_gemm_grouped<3, false>), grid, dim3(gg_waves<3, false>() * 64), 0, s, a);
+        if (m.scheme == 4) hipLaunchKernelGGL((k_gemm_grouped<4, 8>), grid, dim3(512), 0, s, a);
+        else hipLaunchKernelGGL((k_gemm_grouped<3, 8>), grid, dim3(512), 0, s, a);
     }
     return hipGetLastError();
 }

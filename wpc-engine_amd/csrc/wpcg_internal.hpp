@@ -226,12 +226,15 @@ constexpr int GX_F32 = 0, GX_BF16 = 1, GX_SPLIT = 2;
 constexpr int GEMM_MAX_M_SPLIT = 32;
 hipError_t launch_gemm(const DeviceMatrix& m, const GemmWork& w, const void* x, int x_mode, int M,
                        const float* bias, const float* res, float* y, hipStream_t s);
-// Expert-grouped GEMM in the SPLIT mode, one launch for every expert of a
-// stack: m is one expert's shape, its planes the first of the stack
-// (expert e at e * its plane sizes). Work item i = items[3i..3i+2] =
-// {expert, first pair p0, count <= GEMM_GROUP_COLS}; its column c reads X
-// row rowidx[p0 + c] (null: row p0 + c, X has xrows rows) and writes Y row
-// p0 + c. *nitems (device) items are live; max_items bounds the grid.
+// Expert-grouped GEMM, one launch for every expert of a stack (or of two
+// stacks of one shape over the same X: m2 and y2, else null): m is one
+// expert's shape, its planes the first of the stack (expert e at e * its
+// plane sizes). X comes as launch_pf_digits' records of its xrows rows.
+// Work item i = items[3i..3i+2] = {expert, first pair p0, count <=
+// GEMM_GROUP_COLS}; its column c reads X row rowidx[p0 + c] (null: row
+// p0 + c) and writes Y row p0 + c. *nitems (device) items are live; their
+// (item, matrix, row tile) units are split evenly over wgs workgroups (one
+// per CU).
 // Needs m.nb <= GEMM_GROUP_MAXBK (the item's X digits sit in LDS whole) and
 // m.rows_pad <= GEMM_GROUP_MAXROWS (keeps every buffer offset of an expert's
 // planes well inside 32 bits).
@@ -256,10 +259,14 @@ hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const 
 // residual.
 hipError_t launch_gemm_packed_rows_multi(const DeviceMatrix* const* ms, const float* const* biases, float* const* ys,
                                          int count, const void* xf, const float* xsum, int M, hipStream_t s);
-// xu non-null: the X rows are silu(x) * xu (the FAST steps' arithmetic),
-// x and xu of the same shape.
-hipError_t launch_gemm_grouped(const DeviceMatrix& m, const float* x, const float* xu, int xrows, const int* rowidx,
-                               const int* items, const int* nitems, int max_items, float* y, hipStream_t s);
+// The grouped GEMM's X: rows x rows of K fp32 (xu non-null: silu(x) * xu,
+// the FAST steps' arithmetic, xu of x's shape) to int8 digits, dg
+// rows * K * 4 bytes, and per 128-value block {s_b 2^-7, sum}, dxs
+// rows * K / 128 * 2 floats.
+hipError_t launch_pf_digits(const float* x, const float* xu, int rows, int K, void* dg, float* dxs, hipStream_t s);
+hipError_t launch_gemm_grouped(const DeviceMatrix& m, const DeviceMatrix* m2, const void* dg, const float* dxs,
+                               int xrows, const int* rowidx, const int* items, const int* nitems, int wgs, float* y,
+                               float* y2, hipStream_t s);
 
 // ---- the no-allocation workspace (scratch.hip) --------------------------------
 // scratch_setup(device) looks up the device address of the library's fixed
