@@ -288,17 +288,16 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P0)
                 srs, ((r * GM_R + i / (NT * 16)) * XT * 16 + i % (NT * 16)) * 4, 0, 0));
         }
     };
+    // Every thread stores every word it loaded: a thread past the end holds
+    // a copy of the last word (its load index was clamped) and writes it to
+    // the same place. A store under a condition would leave that load
+    // pending on one path into the round loop, and the wait counts merged at
+    // the loop edge would then drain every load in flight each round.
     auto store_round = [&](int buf) {
 #pragma unroll
-        for (int v = 0; v < XV; v++) {
-            const int i = threadIdx.x + v * GM_WG;
-            if (i < GM_R * FW) xb[buf][i] = xr[v];
-        }
+        for (int v = 0; v < XV; v++) xb[buf][min((int)threadIdx.x + v * GM_WG, GM_R * FW - 1)] = xr[v];
 #pragma unroll
-        for (int v = 0; v < SV; v++) {
-            const int i = threadIdx.x + v * GM_WG;
-            if (i < SN) xsb[buf][i] = sr[v];
-        }
+        for (int v = 0; v < SV; v++) xsb[buf][min((int)threadIdx.x + v * GM_WG, SN - 1)] = sr[v];
     };
     // the fragments of kstep i of every column tile of block u of a round buffer
     auto read_kstep = [&](bf16x8 (&B)[NT], int buf, int u, int i) {
@@ -345,8 +344,6 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P0)
     bf16x8 Bc[NT];
     read_kstep(Bc, 0, 0, 0);
 
-    // Whole rounds of unconditional steps (guarded steps would merge the
-    // wait-counter state at the loop edge and drain every load in flight).
     // Whole rounds of unconditional steps (guarded steps would merge the
     // wait-counter state at the loop edge and drain every load in flight).
     const int nrounds = (nbl + GM_R - 1) / GM_R;

@@ -14,6 +14,13 @@
 namespace wpcg {
 namespace {
 
+// A buffer resource over [base, base + bytes): loads past the end return
+// zeros without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
 // R[t][e] = sum_k X[t][k] * W[e][k] on the fp32 matrix cores: workgroup
 // (16 experts, 16 rows), each of its 8 waves one eighth of K with every
 // 16-byte load of its slice in flight at once (RU per operand and lane: a
@@ -22,10 +29,14 @@ namespace {
 // e0 + r at k0 + 4q; with component i of both, v_mfma_f32_16x16x4_f32 adds
 // X[r][k0 + 4kk + i] * W[c][k0 + 4kk + i] over kk, so four instructions
 // cover k0 .. k0 + 15 (two accumulators, alternate 16-value groups). Rows
-// past T or E read row 0 and are never written. K % 128 == 0. (Four waves
-// with four loads in flight each waited on eight load round trips in a row:
-// 9.4 us for 256 rows of 2048 over 128 experts.)
+// past T or E read row 0 and are never written. K % 128 == 0. The loads
+// are range-checked buffer loads: a load past the wave's eighth reads
+// zeros, with no branch between the loads (a guarded load per 16 values
+// made the compiler wait for each before the next: 10.5 us for 256 rows of
+// 2048 over 128 experts). (Four waves with four loads in flight each waited
+// on eight load round trips in a row: 9.4 us.)
 typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef unsigned rt_u32x4 __attribute__((ext_vector_type(4)));
 constexpr int RT_WG = 512, RT_U = 16;
 __global__ __launch_bounds__(RT_WG) void k_pf_router(const float* __restrict__ X, const float* __restrict__ W,
                                                      int T, int E, int K, float* __restrict__ R)
@@ -34,17 +45,22 @@ __global__ __launch_bounds__(RT_WG) void k_pf_router(const float* __restrict__ X
     const int e0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane & 15, q = lane >> 4;
     const int kq = K / 8, kb = wave * kq;
-    const float4* xp = reinterpret_cast<const float4*>(X + (size_t)(t0 + r < T ? t0 + r : 0) * K + kb + 4 * q);
-    const float4* wp = reinterpret_cast<const float4*>(W + (size_t)(e0 + r < E ? e0 + r : 0) * K + kb + 4 * q);
+    // the tile's rows (uniform resources); rows past T or E read row 0
+    const auto xrs = buf_rsrc(X + (size_t)t0 * K, min(16, T - t0) * K * 4);
+    const auto wrs = buf_rsrc(W + (size_t)e0 * K, min(16, E - e0) * K * 4);
+    const int xo = (t0 + r < T ? r : 0) * K + kb + 4 * q, wo = (e0 + r < E ? r : 0) * K + kb + 4 * q;
     f32x4v d0 = {0.f, 0.f, 0.f, 0.f}, d1 = d0;
     for (int k = 0; k < kq; k += 16 * RT_U) {
         float4 a[RT_U], b[RT_U];
 #pragma unroll
         for (int u = 0; u < RT_U; u++) {
             const bool in = k + 16 * u < kq;
-            a[u] = in ? xp[(k + 16 * u) / 4] : make_float4(0.f, 0.f, 0.f, 0.f);
-            b[u] = in ? wp[(k + 16 * u) / 4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const rt_u32x4 av = __builtin_amdgcn_raw_buffer_load_b128(xrs, in ? (xo + k + 16 * u) * 4 : 0x7FFFFFF0, 0, 0);
+            const rt_u32x4 bv = __builtin_amdgcn_raw_buffer_load_b128(wrs, in ? (wo + k + 16 * u) * 4 : 0x7FFFFFF0, 0, 0);
+            __builtin_memcpy(&a[u], &av, 16);
+            __builtin_memcpy(&b[u], &bv, 16);
         }
+        __builtin_amdgcn_sched_barrier(0);  // every load out before the first product
 #pragma unroll
         for (int u = 0; u < RT_U; u += 2) {
             d0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x, b[u].x, d0, 0, 0, 0);
