@@ -487,9 +487,12 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
         // experts: route every row, sort the (row, slot) pairs by expert, one
         // grouped launch for gate and up and one for down, then the ordered
         // combine
+        // (the fused slice sum + norm also writes the experts' X digits)
+        const bool digits_done = fuse_norm && H % 128 == 0;
         if (fuse_norm)
             WPCG_HIP(launch_pf_reduce_norm(P.part, okg, (int)n, H, (int)L.o->m.rows_pad, L.o->bias, P.x, L.post_ln,
-                                           c.eps, P.xn, s));
+                                           c.eps, P.xn, digits_done ? P.dg : nullptr,
+                                           digits_done ? P.dxs : nullptr, s));
         else
             WPCG_HIP(launch_rms_norm_rows(F, P.x, L.post_ln, H, (int)n, c.eps, P.xn, s));
         wpcg_moe* E = L.moe;
@@ -497,7 +500,7 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
         WPCG_HIP(launch_pf_router(P.xn, E->router->w, (int)n, ne, H, P.r, s));
         WPCG_HIP(launch_route_rows(P.r, ne, (int)n, K, (int)c.norm_topk, P.ids, P.w, s));
         WPCG_HIP(launch_pf_group(P.ids, pairs, ne, K, P.pair_tok, P.pair_pos, P.items, P.nitems, s));
-        WPCG_HIP(launch_pf_digits(P.xn, nullptr, (int)n, H, P.dg, P.dxs, s));
+        if (!digits_done) WPCG_HIP(launch_pf_digits(P.xn, nullptr, (int)n, H, P.dg, P.dxs, s));
         WPCG_HIP(launch_gemm_grouped(E->gate, &E->up, P.dg, P.dxs, (int)n, P.pair_tok, P.items, P.nitems, P.cus,
                                      P.ge, P.ue, s));
         WPCG_HIP(launch_pf_digits(P.ge, P.ue, pairs, (int)c.moe_inter, P.dg, P.dxs, s));

@@ -25,6 +25,7 @@
 #include <algorithm>
 
 #include "wpcg_internal.hpp"
+#include "xdigits.h"
 #include "xpack.h"
 
 namespace wpcg {
@@ -850,18 +851,9 @@ struct GemmGroupArgs {
     int rows, rows_pad, nb, xrows, nmat;
 };
 
-// Byte of value k (0..127) of a block, digit d, in its 512-byte record:
-// piece (h = k >> 6, q = k & 3, d), byte ((k >> 3) & 7) + 8 ((k >> 2) & 1),
-// the order in which lane group q's 16-byte code word holds the codes.
-__device__ __forceinline__ int dg_pos(int k, int d)
-{
-    return (k >> 6) * 256 + (k & 3) * 64 + d * 16 + ((k >> 3) & 7) + 8 * ((k >> 2) & 1);
-}
-
-// X rows to digit records (the grouped GEMM's X): workgroup (row, group of
-// eight blocks), 32 lanes per block with four consecutive values each.
-// SILU: X = silu(x) * xu (the FAST steps' arithmetic). The block's max |x|
-// and sum over its 32 lanes by DPP inside rows of 16 and the row swap; the
+// X rows to digit records (the grouped GEMM's X, xdigits.h): workgroup
+// (row, group of eight blocks), 32 lanes per block with four consecutive
+// values each. SILU: X = silu(x) * xu (the FAST steps' arithmetic). The
 // digits are staged in LDS and leave as whole 16-byte pieces.
 template <bool SILU>
 __global__ __launch_bounds__(256) void k_pf_digits(const float* __restrict__ X, const float* __restrict__ XU, int K,
@@ -882,33 +874,8 @@ __global__ __launch_bounds__(256) void k_pf_digits(const float* __restrict__ X, 
             for (int q = 0; q < 4; q++) v[q] = __fdividef(v[q], 1.0f + __expf(-v[q])) * uu[q];
         }
     }
-    uint32_t mb = __float_as_uint(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-    float sm = (v[0] + v[1]) + (v[2] + v[3]);
-    mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0xB1, 0xF, 0xF, false));
-    sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0xB1, 0xF, 0xF, false));
-    mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x4E, 0xF, 0xF, false));
-    sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x4E, 0xF, 0xF, false));
-    mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x141, 0xF, 0xF, false));
-    sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x141, 0xF, 0xF, false));
-    mb = max(mb, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mb, 0x140, 0xF, 0xF, false));
-    sm += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(sm), 0x140, 0xF, 0xF, false));
-    const auto mr = __builtin_amdgcn_permlane16_swap(mb, mb, false, false);
-    const float Mx = __uint_as_float(max((uint32_t)mr[0], (uint32_t)mr[1]));
-    const auto sr = __builtin_amdgcn_permlane16_swap(__float_as_uint(sm), __float_as_uint(sm), false, false);
-    const float Sx = __uint_as_float(sr[0]) + __uint_as_float(sr[1]);
-    const float inv = Mx > 0.0f ? (127.0f * 2097152.0f) * __builtin_amdgcn_rcpf(Mx) : 0.0f;
-    uint8_t* st = stage[bl];
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-        const int Q = (int)rintf(v[q] * inv);
-        const int k = k0 + q;
-        st[dg_pos(k, 0)] = (uint8_t)(Q >> 21);
-        st[dg_pos(k, 1)] = (uint8_t)((Q >> 14) & 127);
-        st[dg_pos(k, 2)] = (uint8_t)((Q >> 7) & 127);
-        st[dg_pos(k, 3)] = (uint8_t)(Q & 127);
-    }
-    if (ok && (lane & 31) == 0)
-        dxs[(size_t)row * nb + b] = make_float2(Mx * (1.0f / 127.0f) * 0x1p-7f, Sx);  // s_b 2^-7
+    const float2 sx = digit_block(v, stage[bl]);
+    if (ok && (lane & 31) == 0) dxs[(size_t)row * nb + b] = sx;
     __syncthreads();
     // thread t: piece t % 32 of block t / 32 of the group
     if (ok)

@@ -9,6 +9,7 @@
 
 #include "wave.h"
 #include "wpcg_internal.hpp"
+#include "xdigits.h"
 #include "xpack.h"
 
 namespace wpcg {
@@ -145,14 +146,19 @@ __global__ __launch_bounds__(256) void k_rms_pack(const float* __restrict__ X, c
 // X (the new residual, as k_gemm_reduce writes it), and that row's RMSNorm
 // (FAST, as k_rms_norm rows computes it: each thread's squares by fused
 // multiply-adds, the wave sums, the four waves in a fixed order) into XN:
-// one workgroup of 256 threads per row, H <= 256 * RN_MAXV.
+// one workgroup of 256 threads per row, H <= 256 * RN_MAXV. With dg, the
+// normed row also as the expert GEMM's X digits (xdigits.h; the values
+// k_pf_digits would read from XN), staged in LDS.
 constexpr int RN_MAXV = PF_NORM_MAXH / 256;
 __global__ __launch_bounds__(256) void k_pf_reduce_norm(const float* __restrict__ part, int kg, int Mp,
                                                         int rows_pad, int H, const float* __restrict__ bias,
                                                         float* __restrict__ X, const float* __restrict__ w,
-                                                        float eps, float* __restrict__ XN)
+                                                        float eps, float* __restrict__ XN, uint8_t* __restrict__ dg,
+                                                        float2* __restrict__ dxs)
 {
     __shared__ float red[4];
+    __shared__ float xn_s[PF_NORM_MAXH];
+    __shared__ __align__(16) uint8_t rec[PF_NORM_MAXH / 128 + 1][512];  // the last: blocks past the row
     const int m = blockIdx.x;
     const size_t slice = (size_t)Mp * rows_pad;
     float v[RN_MAXV];
@@ -179,10 +185,30 @@ __global__ __launch_bounds__(256) void k_pf_reduce_norm(const float* __restrict_
     for (int i = 0; i < RN_MAXV; i++) {
         const int k = threadIdx.x + 256 * i;
         if (k < H) {
+            const float xn = __fmul_rn(__fmul_rn(v[i], scale), w[k]);
             X[(size_t)m * H + k] = v[i];
-            XN[(size_t)m * H + k] = __fmul_rn(__fmul_rn(v[i], scale), w[k]);
+            XN[(size_t)m * H + k] = xn;
+            xn_s[k] = xn;
         }
     }
+    if (!dg) return;  // uniform
+    __syncthreads();
+    // half wave hw takes blocks hw, hw + 8, ... (whole passes: a block past
+    // the row is digitised from zeros into the spare record)
+    const int nb = H / 128, hw = threadIdx.x >> 5, k0 = 4 * (threadIdx.x & 31);
+    for (int b0 = 0; b0 < nb; b0 += 8) {
+        const int b = b0 + hw;
+        const bool ok = b < nb;
+        float v4[4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) v4[q] = ok ? xn_s[b * 128 + k0 + q] : 0.0f;
+        const float2 sx = digit_block(v4, rec[ok ? b : PF_NORM_MAXH / 128]);
+        if (ok && (threadIdx.x & 31) == 0) dxs[(size_t)m * nb + b] = sx;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nb * 32; i += 256)
+        *reinterpret_cast<rt_u32x4*>(dg + (size_t)m * nb * 512 + i * 16) =
+            *reinterpret_cast<const rt_u32x4*>(&rec[i >> 5][(i & 31) * 16]);
 }
 
 // The P = T * top_k pairs q = t * top_k + k, sorted by expert, ties in pair
@@ -317,12 +343,13 @@ hipError_t launch_rms_pack_rows(const float* X, const float* w, int n, int H, fl
 }
 
 hipError_t launch_pf_reduce_norm(const float* part, int kg, int M, int H, int rows_pad, const float* bias, float* X,
-                                 const float* w, float eps, float* XN, hipStream_t s)
+                                 const float* w, float eps, float* XN, void* dg, float* dxs, hipStream_t s)
 {
-    if (M < 1 || kg < 1 || H < 1 || H > 256 * RN_MAXV || rows_pad < H) return hipErrorInvalidValue;
+    if (M < 1 || kg < 1 || H < 1 || H > 256 * RN_MAXV || rows_pad < H || (dg && (H % 128 || !dxs)))
+        return hipErrorInvalidValue;
     (void)hipGetLastError();
     hipLaunchKernelGGL(k_pf_reduce_norm, dim3((unsigned)M), dim3(256), 0, s, part, kg, gemm_rows_tiles(M) / 4 * 32,
-                       rows_pad, H, bias, X, w, eps, XN);
+                       rows_pad, H, bias, X, w, eps, XN, static_cast<uint8_t*>(dg), reinterpret_cast<float2*>(dxs));
     return hipGetLastError();
 }
 

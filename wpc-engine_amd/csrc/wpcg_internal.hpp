@@ -377,10 +377,11 @@ hipError_t launch_rms_pack_rows(const float* X, const float* w, int n, int H, fl
                                 hipStream_t s);
 // A K-sliced packed-rows GEMM's partials (launch_gemm_packed_rows with
 // reduce = false) summed with bias and the residual into X [M][H], then each
-// row's FAST RMSNorm with weights w into XN; H <= PF_NORM_MAXH.
+// row's FAST RMSNorm with weights w into XN; H <= PF_NORM_MAXH. dg non-null:
+// XN's rows also as launch_pf_digits writes them (dg, dxs), H % 128 == 0.
 constexpr int PF_NORM_MAXH = 4096;
 hipError_t launch_pf_reduce_norm(const float* part, int kg, int M, int H, int rows_pad, const float* bias, float* X,
-                                 const float* w, float eps, float* XN, hipStream_t s);
+                                 const float* w, float eps, float* XN, void* dg, float* dxs, hipStream_t s);
 // R[t][e] = X[t] . W[e] (fp32 router rows), R is [T][E].
 hipError_t launch_pf_router(const float* X, const float* W, int T, int E, int K, float* R, hipStream_t s);
 // (token, slot) pairs sorted by expert for launch_gemm_grouped: pair_tok
