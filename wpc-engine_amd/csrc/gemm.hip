@@ -959,9 +959,10 @@ __global__ __launch_bounds__(GG_NW * 64) void k_gemm_grouped(const GemmGroupArgs
             // 32 pieces of 16 B, piece (h, q, d) to xd[blk][c / 4] at
             // h KiB + q * 256 + (4 (c % 4) + d) * 16; slot u of a thread
             // holds pair c = u * GG_WG / 512 + threadIdx.x / 512 (uniform
-            // per wave: one scalar load of its X row), block
-            // (threadIdx.x / 32) % 16, piece threadIdx.x % 32. Pairs past M
-            // keep whatever the LDS holds: their products are never stored.
+            // per wave: its X row is read from lane c of one vector load of
+            // the item's rows), block (threadIdx.x / 32) % 16, piece
+            // threadIdx.x % 32. Pairs past M keep whatever the LDS holds:
+            // their products are never stored.
             constexpr int PS = GEMM_GROUP_COLS * GEMM_GROUP_MAXBK * 32 / GG_WG;  // slots per thread
             constexpr int CPS = GG_WG / 512;                                     // pairs per slot
             const int blk = (threadIdx.x >> 5) & 15, pc = threadIdx.x & 31;
@@ -1000,10 +1001,10 @@ __global__ __launch_bounds__(GG_NW * 64) void k_gemm_grouped(const GemmGroupArgs
         // ---- the step stream, whole rounds of GG_LA / GG_CT steps: per step
         // the block's digits (every pair group, both halves) and {s_b, sum}
         // once, then the chunk's GG_CT tiles, GG_PG independent matrix-core
-        // chains each, then their epilogues. Software-pipelined by one step:
-        // step s + 1's products are issued before step s's epilogue, so the
-        // epilogue's vector instructions run while the matrix cores work
-        // (D and {s_b, sum} in two sets, by step parity).
+        // chains each, then their epilogues. With 8 waves (PIPE) it is
+        // software-pipelined by one step: step s + 1's products are issued
+        // before step s's epilogue, interleaved with its vector
+        // instructions (D and {s_b, sum} in two sets, by step parity).
         float acc[GG_CT][GG_PG], zacc[GG_CT][GG_PG];
 #pragma unroll
         for (int tt = 0; tt < GG_CT; tt++)
