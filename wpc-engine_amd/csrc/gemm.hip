@@ -894,7 +894,12 @@ __global__ __launch_bounds__(GG_NW * 64) void k_gemm_grouped(const GemmGroupArgs
     const int nb = P.nb;
     const int ntiles = P.rows_pad / TILE_ROWS, nmat = P.nmat;
     const int64_t total = (int64_t)(*P.nitems) * nmat * ntiles;
-    const int ub0 = (int)(total * blockIdx.x / gridDim.x), ub1 = (int)(total * (blockIdx.x + 1) / gridDim.x);
+    // share v of the units, v = (b % 8) * G / 8 + b / 8 for workgroup b:
+    // neighbouring shares (an expert's two items, which read the same
+    // weights) run on one XCD and meet in its L2
+    const int G = (int)gridDim.x, b = (int)blockIdx.x;
+    const int v = G % 8 ? b : (b % 8) * (G / 8) + b / 8;
+    const int ub0 = (int)(total * v / G), ub1 = (int)(total * (v + 1) / G);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nrec = ntiles * nb;
     const auto drs = buf_rsrc(P.dg, P.xrows * nb * 512);
