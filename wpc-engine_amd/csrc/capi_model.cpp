@@ -453,17 +453,22 @@ int prefill_pass(wpcg_model* m, uint32_t pos0, uint32_t n, hipStream_t s)
     for (uint32_t l = 0; l < c.n_layers; l++) {
         Layer& L = m->layers[l];
         WPCG_HIP(launch_rms_pack_rows(P.x, L.in_ln, (int)n, H, c.eps, P.xf, P.xsum, s));
+        float* kc = m->kc + (size_t)l * nkv * c.max_pos * hd;
+        float* vc = m->vc + (size_t)l * nkv * c.max_pos * hd;
+        // 128-wide heads: the q/k/v GEMM's epilogue applies the head norms
+        // and the rotation and appends the keys and values to the caches
+        const bool qk_fused = hd == 128;
         {
             const DeviceMatrix* ms[3] = {&L.q->m, &L.k->m, &L.v->m};
             const float* bs[3] = {L.q->bias, L.k->bias, L.v->bias};
             float* ys[3] = {P.q, P.k, P.v};
-            WPCG_HIP(launch_gemm_packed_rows_multi(ms, bs, ys, 3, P.xf, P.xsum, (int)n, s));
+            GemmRope rope{{GEMM_ROPE_Q, GEMM_ROPE_K, GEMM_ROPE_V}, {nullptr, kc, vc}, {L.q_norm, L.k_norm, nullptr},
+                          m->cos_t, m->sin_t, (int)pos0, (int)c.max_pos, c.eps};
+            WPCG_HIP(launch_gemm_packed_rows_multi(ms, bs, ys, 3, P.xf, P.xsum, (int)n, s, qk_fused ? &rope : nullptr));
         }
-        float* kc = m->kc + (size_t)l * nkv * c.max_pos * hd;
-        float* vc = m->vc + (size_t)l * nkv * c.max_pos * hd;
         WPCG_HIP(launch_prefill_attention(P.q, P.k, P.v, L.q_norm, L.k_norm, nh, nkv, hd, c.eps, scale, m->cos_t,
                                           m->sin_t, (int)pos0, (int)n, (int)c.max_pos, kc, vc, P.attn, P.xf, P.xsum,
-                                          s));
+                                          s, qk_fused));
         // residual += o_proj(attn); 128-wide heads leave the attention packed
         if (hd != 128) WPCG_HIP(launch_gemm_pack_rows(P.attn, (int)n, nh * hd, P.xf, P.xsum, s));
         // o_proj in K-slices; for the MoE model the slice sum joins the

@@ -1255,14 +1255,15 @@ void launch_pf_attention_t(const float* Q, int nh, int nkv, float scale, int pos
 hipError_t launch_prefill_attention(float* Q, const float* Kx, const float* Vx, const float* qn, const float* kn,
                                     int nh, int nkv, int hd, float eps, float scale, const float* cos_t,
                                     const float* sin_t, int pos0, int n, int max_pos, float* kc, float* vc,
-                                    float* out, void* xf, float* xsum, hipStream_t s)
+                                    float* out, void* xf, float* xsum, hipStream_t s, bool qk_done)
 {
     if (!attention_fast_ok(nh, nkv, hd) || n < 1 || pos0 + n > max_pos) return hipErrorInvalidValue;
-    if (hd == 128 ? !xf || !xsum : !out) return hipErrorInvalidValue;
+    if (hd == 128 ? !xf || !xsum : !out || qk_done) return hipErrorInvalidValue;
     (void)hipGetLastError();
     if (hd == 128) {
-        hipLaunchKernelGGL(k_pf_qk_rope<128>, dim3(n), dim3(256), 0, s, Q, Kx, Vx, qn, kn, nh, nkv, eps, cos_t,
-                           sin_t, pos0, max_pos, kc, vc);
+        if (!qk_done)
+            hipLaunchKernelGGL(k_pf_qk_rope<128>, dim3(n), dim3(256), 0, s, Q, Kx, Vx, qn, kn, nh, nkv, eps, cos_t,
+                               sin_t, pos0, max_pos, kc, vc);
         launch_pf_attention_t<128>(Q, nh, nkv, scale, pos0, n, max_pos, kc, vc, out, xf, xsum, s);
     } else {
         hipLaunchKernelGGL(k_pf_qk_rope<64>, dim3(n), dim3(256), 0, s, Q, Kx, Vx, qn, kn, nh, nkv, eps, cos_t,

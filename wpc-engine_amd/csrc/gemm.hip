@@ -111,8 +111,12 @@ struct GemmMat {
     float* y;
     const float* bias;
     int rows, rows_pad, rgs, rgs8, wg0;
+    int rope;            // GEMM_ROPE_*: the prefill's q, k or v epilogue
+    float* cache;        // k, v: the layer's cache [head][max_pos][128]
+    const float* nw;     // q, k: the head norm's weights [128]
 };
 constexpr int GEMM_MAX_MATS = 3;
+static_assert(GEMM_MAX_MATS == sizeof(GemmRope::mode) / sizeof(int), "GemmRope holds every matrix of a launch");
 struct GemmArgs {
     const uint8_t* codes;
     const uint8_t* hp;
@@ -130,6 +134,15 @@ struct GemmArgs {
     int xt, rgs, rgs8;
     int nmore;  // further matrices over the same X (rgs8 > 0 only)
     GemmMat more[GEMM_MAX_MATS - 1];
+    // the prefill's q/k/v epilogue (GemmRope): this matrix's mode, cache and
+    // norm weights, and the rotation tables of every matrix
+    int rope;
+    float* cache;
+    const float* nw;
+    const float* cos_t;  // [max_pos][64]
+    const float* sin_t;
+    int pos0, max_pos;
+    float eps;
 };
 
 // The value written for output (m, row): the sum, the bias, the residual.
@@ -170,6 +183,78 @@ __device__ __forceinline__ bf16x8 codes_bf16(uint32_t a, uint32_t b)
 }
 // zero point of the offset codes: zp - 128 * scale
 __device__ __forceinline__ float zp_off(uint32_t p) { return __builtin_fmaf(-128.0f, h2f(p >> 16), h2f(p & 0xFFFFu)); }
+
+// The prefill's q/k/v epilogue (kg = 1, a row group of 8 waves x 16 rows =
+// one 128-wide head, 32 columns = tokens mcol0 ..): q and k get the head
+// RMSNorm (FAST: the squares of each lane's four rows by fused multiply-adds,
+// the lane groups by exchanges, the eight waves through LDS in a fixed
+// order; then (x * scale) * w) and the rotation at each token's position
+// (rows d < 64 and d + 64 are a pair: y c - y' s and y' c + y s, as
+// fa_norm_rope). The normed rows are staged in LDS as [token][d] and leave
+// as whole 16-byte pieces of a token's row (thread t: token t / 16, rows
+// 4 (t % 16) .. +3 and the same + 64): q into Y, k and v (v as computed)
+// into the cache rows of their position. The bias is added first.
+template <typename Acc>
+__device__ __forceinline__ void rope_epilogue(const GemmArgs& P, const Acc& acc, int rg, int wave, int g, int j,
+                                              int mcol0, float* ex)
+{
+    constexpr int TOK = 32, EXS = 132;  // ex: [TOK][EXS], rows 16-byte aligned
+    float* rsum = ex + TOK * EXS;       // [8][TOK] sums of squares
+    const int mode = P.rope;
+    float v[2][4];
+#pragma unroll
+    for (int n = 0; n < 2; n++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int d = wave * 16 + 4 * g + q;
+            v[n][q] = acc[0][n][q] + (P.bias ? P.bias[rg * 128 + d] : 0.0f);
+        }
+    __syncthreads();  // every wave is done with the X buffers
+    float sc[2] = {1.0f, 1.0f};
+    if (mode != GEMM_ROPE_V) {
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            float ss = fmaf(v[n][3], v[n][3], fmaf(v[n][2], v[n][2], fmaf(v[n][1], v[n][1], v[n][0] * v[n][0])));
+            ss += __shfl_xor(ss, 16);
+            ss += __shfl_xor(ss, 32);
+            if (g == 0) rsum[wave * TOK + n * 16 + j] = ss;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int n = 0; n < 2; n++) {
+            const float* r = rsum + n * 16 + j;
+            const float tot = ((r[0] + r[TOK]) + (r[2 * TOK] + r[3 * TOK])) +
+                              ((r[4 * TOK] + r[5 * TOK]) + (r[6 * TOK] + r[7 * TOK]));
+            sc[n] = __fdiv_rn(1.0f, __builtin_sqrtf(__fadd_rn(__fdiv_rn(tot, 128.0f), P.eps)));
+        }
+    }
+#pragma unroll
+    for (int n = 0; n < 2; n++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int d = wave * 16 + 4 * g + q;
+            ex[(n * 16 + j) * EXS + d] = mode != GEMM_ROPE_V ? (v[n][q] * sc[n]) * P.nw[d] : v[n][q];
+        }
+    __syncthreads();
+    const int tok = threadIdx.x >> 4, d1 = 4 * (threadIdx.x & 15), m = mcol0 + tok;
+    if (m >= P.M) return;
+    const int pos = P.pos0 + m;
+    const float4 y1 = *reinterpret_cast<const float4*>(&ex[tok * EXS + d1]);
+    const float4 y2 = *reinterpret_cast<const float4*>(&ex[tok * EXS + d1 + 64]);
+    float4 o1 = y1, o2 = y2;
+    if (mode != GEMM_ROPE_V) {
+        const float4 c = *reinterpret_cast<const float4*>(P.cos_t + (size_t)pos * 64 + d1);
+        const float4 sn = *reinterpret_cast<const float4*>(P.sin_t + (size_t)pos * 64 + d1);
+        o1 = make_float4(fmaf(y1.x, c.x, -(y2.x * sn.x)), fmaf(y1.y, c.y, -(y2.y * sn.y)),
+                         fmaf(y1.z, c.z, -(y2.z * sn.z)), fmaf(y1.w, c.w, -(y2.w * sn.w)));
+        o2 = make_float4(fmaf(y2.x, c.x, y1.x * sn.x), fmaf(y2.y, c.y, y1.y * sn.y), fmaf(y2.z, c.z, y1.z * sn.z),
+                         fmaf(y2.w, c.w, y1.w * sn.w));
+    }
+    float* dst = mode == GEMM_ROPE_Q ? P.y + (size_t)m * P.rows + rg * 128
+                                     : P.cache + ((size_t)rg * P.max_pos + pos) * 128;
+    *reinterpret_cast<float4*>(dst + d1) = o1;
+    *reinterpret_cast<float4*>(dst + d1 + 64) = o2;
+}
 
 // A workgroup of 8 waves (two per SIMD, so one wave's waits are filled by the
 // other's work) computes one row group (8 row tiles) for all NT*16 columns
@@ -221,6 +306,9 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P0)
             P.rows_pad = mm.rows_pad;
             P.rgs = mm.rgs;
             P.rgs8 = mm.rgs8;
+            P.rope = mm.rope;
+            P.cache = mm.cache;
+            P.nw = mm.nw;
             bid -= mm.wg0;
             break;
         }
@@ -450,6 +538,12 @@ __global__ __launch_bounds__(GM_WG) void k_gemm(const GemmArgs P0)
     // lane (g, j) holds rows 4g..4g+3 of each tile for column n*16 + j;
     // the split-K partials have Mp columns (every column group's with rgs8)
     const int Mp = P.rgs8 ? P.xt / NT * NW * 16 : NT * 16;
+    if constexpr (SPLIT && RT == 1 && NW == 2) {
+        if (P.rope) {  // uniform: the row group is one 128-wide head
+            rope_epilogue(P, acc, rg, wave, g, j, mcol0, reinterpret_cast<float*>(&xb[0][0]));
+            return;
+        }
+    }
     if (kg == 1) {
 #pragma unroll
         for (int rt = 0; rt < RT; rt++)
@@ -1304,11 +1398,22 @@ hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const 
 }
 
 hipError_t launch_gemm_packed_rows_multi(const DeviceMatrix* const* ms, const float* const* biases, float* const* ys,
-                                         int count, const void* xf, const float* xsum, int M, hipStream_t s)
+                                         int count, const void* xf, const float* xsum, int M, hipStream_t s,
+                                         const GemmRope* rope)
 {
     if (M < 1 || count < 1 || count > GEMM_MAX_MATS) return hipErrorInvalidValue;
     for (int e = 0; e < count; e++)
         if (ms[e]->nb == 0 || ms[e]->nb != ms[0]->nb || ms[e]->scheme != ms[0]->scheme) return hipErrorInvalidValue;
+    if (rope) {  // whole 128-row heads; q and k have norm weights, k and v a cache
+        if (!rope->cos_t || !rope->sin_t || rope->pos0 < 0 || rope->pos0 + M > rope->max_pos)
+            return hipErrorInvalidValue;
+        for (int e = 0; e < count; e++) {
+            const int md = rope->mode[e];
+            if (md < 0 || md > GEMM_ROPE_V || (md && ms[e]->rows % 128) || (md && md != GEMM_ROPE_V && !rope->nw[e]) ||
+                ((md == GEMM_ROPE_K || md == GEMM_ROPE_V) && !rope->cache[e]))
+                return hipErrorInvalidValue;
+        }
+    }
     (void)hipGetLastError();
     const DeviceMatrix& m = *ms[0];
     GemmArgs a{};
@@ -1319,6 +1424,16 @@ hipError_t launch_gemm_packed_rows_multi(const DeviceMatrix* const* ms, const fl
     a.xsum = xsum;
     a.y = ys[0];
     a.bias = biases[0];
+    if (rope) {
+        a.rope = rope->mode[0];
+        a.cache = rope->cache[0];
+        a.nw = rope->nw[0];
+        a.cos_t = rope->cos_t;
+        a.sin_t = rope->sin_t;
+        a.pos0 = rope->pos0;
+        a.max_pos = rope->max_pos;
+        a.eps = rope->eps;
+    }
     a.rows = (int)m.rows;
     a.rows_pad = (int)m.rows_pad;
     a.nb = (int)m.nb;
@@ -1341,6 +1456,11 @@ hipError_t launch_gemm_packed_rows_multi(const DeviceMatrix* const* ms, const fl
         mm.rgs = gemm_row_groups(ms[e]->rows);
         mm.rgs8 = (mm.rgs + 7) / 8 * 8;
         mm.wg0 = wgs;
+        if (rope) {
+            mm.rope = rope->mode[e];
+            mm.cache = rope->cache[e];
+            mm.nw = rope->nw[e];
+        }
         wgs += mm.rgs8 * (a.xt / 4);
     }
     const dim3 grid((unsigned)wgs);

@@ -256,9 +256,25 @@ hipError_t launch_gemm_packed_rows(const DeviceMatrix& m, const void* xf, const 
                                    bool reduce = true);
 // Up to three matrices of the same K and scheme over one packed X in one
 // launch (the projections that share an input: q, k, v; gate, up); no
-// residual.
+// residual. With rope, matrix e's epilogue per mode[e] (128-wide heads,
+// rows % 128 == 0; M rows of X are the tokens at positions pos0 ..):
+// GEMM_ROPE_Q the head RMSNorm (weights nw[e]) and the rotation (cos_t /
+// sin_t [max_pos][64]) into Y, GEMM_ROPE_K the same into cache[e]
+// ([head][max_pos][128]), GEMM_ROPE_V the rows as computed into cache[e];
+// 0 the plain output.
+constexpr int GEMM_ROPE_Q = 1, GEMM_ROPE_K = 2, GEMM_ROPE_V = 3;
+struct GemmRope {
+    int mode[3];
+    float* cache[3];
+    const float* nw[3];
+    const float* cos_t;
+    const float* sin_t;
+    int pos0, max_pos;
+    float eps;
+};
 hipError_t launch_gemm_packed_rows_multi(const DeviceMatrix* const* ms, const float* const* biases, float* const* ys,
-                                         int count, const void* xf, const float* xsum, int M, hipStream_t s);
+                                         int count, const void* xf, const float* xsum, int M, hipStream_t s,
+                                         const GemmRope* rope = nullptr);
 // The grouped GEMM's X: rows x rows of K fp32 (xu non-null: silu(x) * xu,
 // the FAST steps' arithmetic, xu of x's shape) to int8 digits, dg
 // rows * K * 4 bytes, and per 128-value block {s_b 2^-7, sum}, dxs
@@ -359,14 +375,15 @@ hipError_t launch_add(float* x, const float* y, int n, hipStream_t s);
 hipError_t launch_embed_rows(const DeviceMatrix& m, const uint32_t* tokens, int n, float* out, hipStream_t s);
 hipError_t launch_rms_norm_rows(int mode, const float* x, const float* w, int n, int rows, float eps, float* out,
                                 hipStream_t s);
-// q_norm/k_norm + RoPE (Q in place, keys into kc), values into vc, then
+// q_norm/k_norm + RoPE (Q in place, keys into kc), values into vc (unless
+// qk_done: the q/k/v GEMM's epilogue did that, head_dim 128 only), then
 // causal attention of every row over positions 0..pos0+t: with head_dim 128
 // written as o_proj's packed X (xf, xsum: launch_gemm_pack_rows's layout for
 // n rows of nh*128), with 64 into out [n][nh*hd]. Needs attention_fast_ok.
 hipError_t launch_prefill_attention(float* Q, const float* Kx, const float* Vx, const float* qn, const float* kn,
                                     int nh, int nkv, int hd, float eps, float scale, const float* cos_t,
                                     const float* sin_t, int pos0, int n, int max_pos, float* kc, float* vc,
-                                    float* out, void* xf, float* xsum, hipStream_t s);
+                                    float* out, void* xf, float* xsum, hipStream_t s, bool qk_done = false);
 // FAST routing of score rows [rows][n]: the FAST one-token projection's own
 // routing per row (n <= ROUTE_MAXN, top_k <= MAX_JOBS).
 hipError_t launch_route_rows(const float* scores, int n, int rows, int top_k, int norm_topk, int32_t* ids, float* w,
