@@ -105,6 +105,9 @@ def greedy(m, first, steps):
     ("moe-two-passes", MOE, 3, 290, 22),
     ("qwen3-moe-2L", QWEN3_MOE_2L, 0, 256, 31),
     ("qwen3-dense-2L", QWEN3_DENSE_2L, 5, 128, 32),
+    # a ragged batch at a non-zero start: the q/k/v epilogue's partial
+    # column group and rotation offsets, the expert GEMM's small items
+    ("qwen3-moe-2L-ragged", QWEN3_MOE_2L, 3, 77, 34),
 ])
 def test_fast_prefill_matches_steps(ctx, name, cfg, n_pre, n, seed):
     print(f"[gpu] prefill {name}: {n_pre} steps then {n} tokens", flush=True)
