@@ -78,42 +78,33 @@ __device__ __forceinline__ float ordered_sumsq(const float* v, int n)
 
 // ((0 + q0) + q1) + ... in index order, by one thread, from 16-byte aligned
 // LDS (q = the squares, rounded, already computed by the whole workgroup and
-// padded with +0.0 to a multiple of 64 values: adding +0.0 to the sum, which
+// padded with +0.0 to os_padded(n) values: adding +0.0 to the sum, which
 // starts at +0.0 and never becomes -0.0, changes nothing). The chain is one
-// addition per value; each group of 32 values is read from LDS a whole group
-// ahead of its additions (two register sets, the reads pinned in place).
-constexpr int OS_GROUP = 8;  // float4s per group
+// addition per value, in chunks of 128: a chunk's 32 16-byte reads all go
+// out, then its 128 additions run as the reads return. (Groups of 32 values
+// read a group ahead measured 10-13 clocks per addition on one lane: the
+// compiler copies the look-ahead registers at the loop edge and waits for
+// every read there; whole chunks of 128 run at ~7, a chain from registers
+// at ~4.6.)
+constexpr int OS_CHUNK = 32;  // float4s per chunk
+__device__ __forceinline__ int os_padded(int n) { return (n + 4 * OS_CHUNK - 1) / (4 * OS_CHUNK) * (4 * OS_CHUNK); }
 __device__ __forceinline__ float ordered_sum_lds(const float* q, int n)
 {
     const float4* q4 = reinterpret_cast<const float4*>(q);
-    const int ng = (n + 4 * OS_GROUP - 1) / (4 * OS_GROUP);  // groups of 32 values
+    const int nc = os_padded(n) / (4 * OS_CHUNK);
     float s = 0.0f;
-    float4 A[OS_GROUP], B[OS_GROUP];
-    auto add = [&](const float4 (&v)[OS_GROUP]) {
+    for (int c = 0; c < nc; c++) {
+        float4 v[OS_CHUNK];
 #pragma unroll
-        for (int u = 0; u < OS_GROUP; u++) {
+        for (int u = 0; u < OS_CHUNK; u++) v[u] = q4[c * OS_CHUNK + u];
+#pragma unroll
+        for (int u = 0; u < OS_CHUNK; u++) {
             s = __fadd_rn(s, v[u].x);
             s = __fadd_rn(s, v[u].y);
             s = __fadd_rn(s, v[u].z);
             s = __fadd_rn(s, v[u].w);
         }
-    };
-#pragma unroll
-    for (int u = 0; u < OS_GROUP; u++) A[u] = q4[u];
-    int g = 0;
-    for (; g + 2 <= ng; g += 2) {
-#pragma unroll
-        for (int u = 0; u < OS_GROUP; u++) B[u] = q4[(g + 1) * OS_GROUP + u];
-        __builtin_amdgcn_sched_barrier(0);
-        add(A);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int u = 0; u < OS_GROUP; u++) A[u] = q4[(g + 2) * OS_GROUP + u];
-        __builtin_amdgcn_sched_barrier(0);
-        add(B);
-        __builtin_amdgcn_sched_barrier(0);
     }
-    if (g < ng) add(A);  // an odd last group
     return s;
 }
 
@@ -123,9 +114,9 @@ template <int MODE>
 __device__ float sum_squares(const float* x, int n, float* red)
 {
     __shared__ float s_total;
-    __shared__ __align__(16) float s_sq[MODE == WPCG_MODE_EXACT ? 256 + 96 : 4];
+    __shared__ __align__(16) float s_sq[MODE == WPCG_MODE_EXACT ? 256 : 4];
     if (MODE == WPCG_MODE_EXACT) {
-        for (int i = threadIdx.x; i < (n + 63) / 64 * 64 + 32; i += blockDim.x)
+        for (int i = threadIdx.x; i < os_padded(n); i += blockDim.x)
             s_sq[i] = i < n ? __fmul_rn(x[i], x[i]) : 0.0f;
         __syncthreads();
         if (threadIdx.x == 0) s_total = ordered_sum_lds(s_sq, n);
@@ -159,7 +150,7 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
     __shared__ __align__(16) float xs[RN_LDS];
     // the squares, padded with zeros to a multiple of 64 and one group past
     // that (the chain reads one group ahead)
-    __shared__ __align__(16) float sq[MODE == WPCG_MODE_EXACT ? RN_LDS + 96 : 4];
+    __shared__ __align__(16) float sq[MODE == WPCG_MODE_EXACT ? RN_LDS : 4];
     __shared__ float red[NW / 64];
     __shared__ float s_total;
     const bool staged = n <= RN_LDS;
@@ -187,7 +178,7 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
                                                     __fmul_rn(v.z, v.z), __fmul_rn(v.w, v.w)};
             }
         }
-        for (int i = n + threadIdx.x; i < (n + 63) / 64 * 64 + 32; i += NW) sq[i] = 0.0f;
+        for (int i = n + threadIdx.x; i < os_padded(n); i += NW) sq[i] = 0.0f;
         __syncthreads();
         if (threadIdx.x == 0) s_total = ordered_sum_lds(sq, n);
         __syncthreads();
@@ -216,7 +207,7 @@ __global__ __launch_bounds__(NW) void k_rms_norm(const float* __restrict__ x,
     }
     if (MODE == WPCG_MODE_EXACT) {
         if (staged)
-            for (int i = n + threadIdx.x; i < (n + 63) / 64 * 64 + 32; i += NW) sq[i] = 0.0f;
+            for (int i = n + threadIdx.x; i < os_padded(n); i += NW) sq[i] = 0.0f;
         __syncthreads();
         if (threadIdx.x == 0) s_total = staged ? ordered_sum_lds(sq, n) : ordered_sumsq(x, n);
     } else {
@@ -283,7 +274,7 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
                                                      float* __restrict__ out)
 {
     __shared__ __align__(16) float qs[256], ks[256], vs[256];
-    __shared__ __align__(16) float w[AT_MAXPOS + 96];  // zero padded for the ordered sum
+    __shared__ __align__(16) float w[AT_MAXPOS + 128];  // zero padded for the ordered sum
     __shared__ __align__(16) float vsh[2][AT_VB * 256];
     __shared__ float red[AT_WG / 64];
     __shared__ float s_sum;
@@ -367,7 +358,7 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
     for (int t = threadIdx.x; t < n; t += AT_WG) w[t] = ref_expf(__fsub_rn(w[t], m));
     __syncthreads();
     if (MODE == WPCG_MODE_EXACT) {
-        for (int t = n + threadIdx.x; t < (n + 63) / 64 * 64 + 32; t += AT_WG) w[t] = 0.0f;
+        for (int t = n + threadIdx.x; t < os_padded(n); t += AT_WG) w[t] = 0.0f;
         __syncthreads();
         if (threadIdx.x == 0) s_sum = ordered_sum_lds(w, n);
     } else {

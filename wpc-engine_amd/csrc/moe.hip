@@ -50,11 +50,13 @@ __global__ __launch_bounds__(64) void k_dense_exact(const float* __restrict__ w,
 // reference rounds it before adding) into LDS, double buffered, while lanes
 // 0..15 of wave 0 add their rows' products in index order: one addition per
 // value. A row's stride is 4 floats past a multiple of 32, so the sixteen
-// rows' 16-byte reads hit distinct banks. Each lane reads a group of 32
-// products a whole group ahead of its chain (two register sets); a chunk's
-// products past in_f are zeros (adding them changes nothing: the sum starts
-// at +0.0 and never becomes -0.0).
-constexpr int DE_ROWS = 16, DE_K = 512, DE_G = 8;  // DE_G float4s per group
+// rows' 16-byte reads hit distinct banks. Each lane adds runs of 128
+// products: the run's 32 reads go out, then its additions (runs of 32
+// read a run ahead cost ~2x per addition: the compiler waited for every
+// read in flight at the loop edge); a chunk's products past in_f are zeros
+// (adding them changes nothing: the sum starts at +0.0 and never becomes
+// -0.0).
+constexpr int DE_ROWS = 16, DE_K = 512, DE_RUN = 32;  // DE_RUN float4s per run
 __global__ __launch_bounds__(256) void k_dense_exact_lds(const float* __restrict__ w,
                                                         const float* __restrict__ x,
                                                         const float* __restrict__ bias,
@@ -92,36 +94,22 @@ __global__ __launch_bounds__(256) void k_dense_exact_lds(const float* __restrict
         const int b = c & 1;
         if (c + 1 < nch) load(c + 1);
         if (t < DE_ROWS) {
+            // whole runs of 128 products: 32 reads out, then 128 additions
             const int len = min(DE_K, in_f - c * DE_K);
-            const int ng = (len + 4 * DE_G - 1) / (4 * DE_G);  // groups of 32 values
+            const int nr = (len + 4 * DE_RUN - 1) / (4 * DE_RUN);
             const float4* pr = reinterpret_cast<const float4*>(&ws[b][t][0]);
-            float4 A[DE_G], B[DE_G];
-            auto read = [&](float4 (&V)[DE_G], int g) {
+            for (int g = 0; g < nr; g++) {
+                float4 V[DE_RUN];
 #pragma unroll
-                for (int u = 0; u < DE_G; u++) V[u] = pr[g * DE_G + u];
-            };
-            auto add = [&](const float4 (&V)[DE_G]) {
+                for (int u = 0; u < DE_RUN; u++) V[u] = pr[g * DE_RUN + u];
 #pragma unroll
-                for (int u = 0; u < DE_G; u++) {
+                for (int u = 0; u < DE_RUN; u++) {
                     acc = __fadd_rn(acc, V[u].x);
                     acc = __fadd_rn(acc, V[u].y);
                     acc = __fadd_rn(acc, V[u].z);
                     acc = __fadd_rn(acc, V[u].w);
                 }
-            };
-            read(A, 0);
-            int g = 0;
-            for (; g + 2 <= ng; g += 2) {
-                read(B, g + 1);
-                __builtin_amdgcn_sched_barrier(0);
-                add(A);
-                __builtin_amdgcn_sched_barrier(0);
-                if (g + 2 < ng) read(A, g + 2);
-                __builtin_amdgcn_sched_barrier(0);
-                add(B);
-                __builtin_amdgcn_sched_barrier(0);
             }
-            if (g < ng) add(A);  // an odd last group
         }
         if (c + 1 < nch) store(b ^ 1);
         __syncthreads();
