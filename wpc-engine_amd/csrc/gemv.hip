@@ -56,6 +56,16 @@ __device__ __forceinline__ float h2f(uint32_t bits)
     return (float)h;
 }
 
+// A pointer that is the same in every lane, as a wave-uniform value.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p)
+{
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (T*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
 // Buffer resource over [base, base + bytes): raw buffer loads at offsets
 // past `bytes` return zeros and access no memory.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, int bytes)
@@ -155,7 +165,7 @@ __device__ __forceinline__ void gemv_exact_tile(const uint8_t* __restrict__ code
                                                 int tile, float* xs)
 {
     if (sel) {
-        const int e = sel[sel_k];
+        const int e = __builtin_amdgcn_readfirstlane(sel[sel_k]);
         if (e < 0) {
             const int r = tile * (EX_WG / 8) + (threadIdx.x >> 3);
             if (r < rows && (threadIdx.x & 7) == 0) y[r] = 0.0f;
@@ -166,6 +176,14 @@ __device__ __forceinline__ void gemv_exact_tile(const uint8_t* __restrict__ code
         if (SCHEME == 3) hp += t0 * HP_REC;
         params += t0 * TILE_ROWS;
     }
+    // The planes' addresses are the same for every lane, but the early exit
+    // above (a store by some lanes, then return) makes the compiler carry
+    // them in lane registers; buffer resources built from those made every
+    // load of the batched kernel a loop over lanes (q/k/v: 4.8 us to issue
+    // them). Taken from the first lane they are uniform again.
+    codes = uniform_ptr(codes);
+    hp = uniform_ptr(hp);
+    params = uniform_ptr(params);
     const int L = threadIdx.x & 7;
     const int r16 = threadIdx.x >> 3;  // row within the tile
     const int row = tile * (EX_WG / 8) + r16;
