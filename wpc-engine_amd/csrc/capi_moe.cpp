@@ -271,8 +271,11 @@ int wpcg_moe_create(wpcg_ctx* ctx, int scheme, uint32_t n_exp, uint32_t hidden, 
     dev((void**)&m->ys, (size_t)top_k * hidden * 4);
     dev((void**)&m->xn, (size_t)hidden * 4);
     // the FAST path's routed down projection: the chosen experts' rows side
-    // by side must fit one K-slice
-    m->routed = (uint64_t)top_k * (inter / 128) <= fast_max_slice(hidden, (uint64_t)top_k * (inter / 128));
+    // by side must fit one K-slice, and the stack's parameters are addressed
+    // with 32-bit offsets below 2^31 bytes
+    const uint64_t down_params = (uint64_t)n_exp * (m->down.rows_pad / TILE_ROWS) * m->down.nb * TILE_ROWS * 4;
+    m->routed = (uint64_t)top_k * (inter / 128) <= fast_max_slice(hidden, (uint64_t)top_k * (inter / 128)) &&
+                down_params < 0x7FFFFFF0ull;
     if (rc == WPCG_OK && e != hipSuccess) rc = hip_fail(e, "moe workspace");
     if (rc != WPCG_OK) {
         free_moe(m.get());

@@ -765,8 +765,13 @@ __global__ __launch_bounds__(FAST_WG, KIND == FK_PLAIN && (XF == XF_NONE || (XF 
 #pragma unroll
             for (int i = 1; i < QB; i++)
                 if (bi == i) { rb = recs[i]; okb = ok[i]; }
-            const auto prs = buf_rsrc(params + rb * TILE_ROWS, bi < QB && okb ? 64 : 0);
-            pv = __builtin_amdgcn_raw_buffer_load_b128(prs, (lane & 3) * 16, 0, 0);
+            // one resource over the stack's parameters (its size is checked
+            // below 2^31 bytes when the routed path is chosen) and a lane
+            // offset: a resource per lane group made the load a loop over
+            // the lane groups; a lane without a block reads past the range
+            const auto prs = buf_rsrc(params, 0x7FFFFFF0);
+            const uint32_t po = bi < QB && okb ? (uint32_t)(rb * TILE_ROWS * 4) + (lane & 3) * 16 : 0x7FFFFFF0u;
+            pv = __builtin_amdgcn_raw_buffer_load_b128(prs, po, 0, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll

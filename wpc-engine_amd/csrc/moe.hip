@@ -134,7 +134,9 @@ __global__ __launch_bounds__(256) void k_dense_fast(const float* __restrict__ w,
                                                     const float* __restrict__ x_add)
 {
     __shared__ float red[2][4];
-    const int r = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // the wave index as a uniform value: read per lane it made the row
+    // slices' buffer resources lane-varying, and every load a loop over lanes
+    const int r = blockIdx.x, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const float* row = w + (size_t)r * in_f;
     float acc = 0.0f, sq = 0.0f;
     if ((in_f & 3) == 0) {
