@@ -97,7 +97,11 @@ int wpcg::moe_run(wpcg_moe* m, const float* x_dev, float* out_dev, const float* 
         x_dev = m->xn;
     }
     WPCG_HIP(launch_dense(m->router->w, (int)m->n_exp, H, m->mode, x_dev, nullptr, m->scores, s));
-    WPCG_HIP(launch_softmax_route(m->scores, (int)m->n_exp, K, m->norm_topk, m->ids, m->w, s));
+    // EXACT: the gate/up launch routes itself when it holds every chosen
+    // expert's two GEMVs (one launch); otherwise a routing launch first
+    const bool self_route = m->mode == WPCG_MODE_EXACT && 2 * K <= MAX_JOBS;
+    if (!self_route)
+        WPCG_HIP(launch_softmax_route(m->scores, (int)m->n_exp, K, m->norm_topk, m->ids, m->w, s));
     // gate and up of the chosen experts, then SiLU(gate) * up
     if (m->mode == WPCG_MODE_FAST) {
         GemvJob jobs[MAX_JOBS];
@@ -112,6 +116,17 @@ int wpcg::moe_run(wpcg_moe* m, const float* x_dev, float* out_dev, const float* 
             jobs[2 * k] = GemvJob{&m->gate, &m->plan, x_dev, nullptr, m->g + (size_t)k * I, m->ids, k};
             jobs[2 * k + 1] = GemvJob{&m->up, &m->plan, x_dev, nullptr, m->u + (size_t)k * I, m->ids, k};
         }
+        if (self_route)
+            for (int j = 0; j < 2 * K; j++) {
+                GemvJob& J = jobs[j];
+                J.sel = nullptr;
+                J.scores = m->scores;
+                J.n_exp = (int)m->n_exp;
+                J.top_k = K;
+                J.norm_topk = m->norm_topk;
+                J.ids_out = m->ids;
+                J.w_out = m->w;
+            }
         for (int j0 = 0; j0 < 2 * K; j0 += MAX_JOBS)
             WPCG_HIP(launch_gemv_exact_multi(jobs + j0, std::min(MAX_JOBS, 2 * K - j0), s));
     }

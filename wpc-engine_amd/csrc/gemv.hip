@@ -29,6 +29,7 @@
 
 #include <type_traits>
 
+#include "route_exact.h"
 #include "wpcg_internal.hpp"
 #include "wave.h"
 
@@ -262,6 +263,14 @@ struct ExactProblem {
     float* y;
     const int32_t* sel;
     int rows, nb, sel_k, rows_pad, nwg;
+    // With scores set the workgroup routes itself (softmax and top_k of the
+    // n_exp router scores, the reference's arithmetic) and takes slot sel_k
+    // of the result as its expert; workgroup (0, 0) also stores the ids and
+    // weights at ids_out / w_out for the launches after it.
+    const float* scores;
+    int32_t* ids_out;
+    float* w_out;
+    int n_exp, top_k, norm_topk;
 };
 struct ExactBatch {
     ExactProblem p[MAX_JOBS];
@@ -273,6 +282,10 @@ template <int SCHEME>
 __global__ __launch_bounds__(EX_WG) void k_gemv_exact_multi(const ExactBatch B)
 {
     __shared__ __align__(16) float xs[EX_SEG * XS_BLK];
+    __shared__ __align__(16) float route_e[64 * RT_PER];
+    __shared__ int32_t route_ids[MAX_JOBS];
+    __shared__ float route_w[MAX_JOBS];
+    __shared__ double route_tab[32];
     // (the problem is read through the kernel-argument segment: indexing the
     // by-value argument with a variable would copy it to scratch memory)
     typedef const __attribute__((address_space(4))) ExactBatch* KargPtr;
@@ -285,7 +298,20 @@ __global__ __launch_bounds__(EX_WG) void k_gemv_exact_multi(const ExactBatch B)
     // these loads go out together, before the exit test below needs nwg
     asm volatile("" ::"s"(codes), "s"(params), "s"(x), "s"(nb), "s"(rows_pad), "s"(nwg));
     if ((int)blockIdx.x >= nwg) return;  // past this problem's tiles
-    gemv_exact_tile<SCHEME>(codes, P.hp, params, x, P.bias, P.y, P.rows, nb, P.sel, P.sel_k, rows_pad, blockIdx.x,
+    const int32_t* sel = P.sel;
+    if (const float* scores = P.scores) {  // uniform: this workgroup routes itself
+        // (in place of a routing launch before this one, 8.6 us per MoE
+        // layer; here it runs before the weight loads can be addressed)
+        if (threadIdx.x < 64)
+            softmax_route_wave(scores, P.n_exp, P.top_k, P.norm_topk, route_ids, route_w, route_e, route_tab);
+        __syncthreads();
+        if (blockIdx.x == 0 && blockIdx.y == 0 && (int)threadIdx.x < P.top_k) {
+            P.ids_out[threadIdx.x] = route_ids[threadIdx.x];
+            P.w_out[threadIdx.x] = route_w[threadIdx.x];
+        }
+        sel = route_ids;
+    }
+    gemv_exact_tile<SCHEME>(codes, P.hp, params, x, P.bias, P.y, P.rows, nb, sel, P.sel_k, rows_pad, blockIdx.x,
                             xs);
 }
 
@@ -1519,6 +1545,18 @@ hipError_t launch_gemv_exact_multi(const GemvJob* jobs, int n, hipStream_t s)
         P.nb = (int)m.nb;
         P.rows_pad = (int)m.rows_pad;
         P.nwg = (int)(m.rows_pad / (EX_WG / 8));
+        const GemvJob& J = jobs[i];
+        if (J.scores) {  // routing reads at most 64 * RT_PER scores into MAX_JOBS slots
+            if (J.n_exp < 1 || J.n_exp > 64 * RT_PER || J.top_k < 1 || J.top_k > MAX_JOBS ||
+                J.sel_k >= J.top_k || !J.ids_out || !J.w_out || J.sel)
+                return hipErrorInvalidValue;
+            P.scores = J.scores;
+            P.ids_out = J.ids_out;
+            P.w_out = J.w_out;
+            P.n_exp = J.n_exp;
+            P.top_k = J.top_k;
+            P.norm_topk = J.norm_topk;
+        }
         wgs = std::max(wgs, P.nwg);
     }
     if (wgs == 0) return hipSuccess;

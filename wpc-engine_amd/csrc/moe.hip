@@ -12,6 +12,7 @@
 
 #define REF_EXPF_FN __device__ __forceinline__
 #include "ref_expf.h"
+#include "route_exact.h"
 #include "wpcg_internal.hpp"
 #include "wave.h"
 
@@ -238,7 +239,6 @@ __global__ __launch_bounds__(SM_WG) void k_softmax(float* __restrict__ x, int n)
 // at -inf). With norm_topk the chosen weights are divided by their sum
 // (taken in chosen order) when it is positive. Unfilled slots get id -1,
 // weight 0. One wave; n <= 64*RT_PER.
-constexpr int RT_PER = 8;
 __global__ __launch_bounds__(64) void k_route(const float* __restrict__ p, int n, int top_k,
                                               int norm_topk, int32_t* __restrict__ ids,
                                               float* __restrict__ w)
@@ -283,101 +283,18 @@ __global__ __launch_bounds__(64) void k_route(const float* __restrict__ p, int n
     }
 }
 
-// ((e[0] + e[1]) + e[2]) + ... + e[n-1], each sum rounded: the index-order
-// sum of norm.rs:36-38. The LDS reads go out 16 bytes and 32 values at a
-// time so the chain of additions does not wait on each read.
-__device__ __forceinline__ float ordered_sum(const float* e, int n)
-{
-    float s = 0.0f;
-    int i = 0;
-    for (; i + 32 <= n; i += 32) {
-        float4 v[8];
-#pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = reinterpret_cast<const float4*>(e + i)[u];
-#pragma unroll
-        for (int u = 0; u < 8; u++) {
-            s = __fadd_rn(s, v[u].x);
-            s = __fadd_rn(s, v[u].y);
-            s = __fadd_rn(s, v[u].z);
-            s = __fadd_rn(s, v[u].w);
-        }
-    }
-    for (; i < n; i++) s = __fadd_rn(s, e[i]);
-    return s;
-}
-
 // ---- softmax_inplace + route in one wave (the MoE router's tail) ----------
-// Same arithmetic as k_softmax then k_route: the exps go through LDS so
-// lane 0 can add them in index order; the top-k scan runs on the
-// probabilities in registers.
+// Same arithmetic as k_softmax then k_route (softmax_route_wave).
 __global__ __launch_bounds__(64) void k_softmax_route(const float* __restrict__ scores, int n,
                                                       int top_k, int norm_topk,
                                                       int32_t* __restrict__ ids,
                                                       float* __restrict__ w)
 {
-    scores += (size_t)blockIdx.x * n;  // row blockIdx.x of a batch (one row: 0)
-    ids += (size_t)blockIdx.x * top_k;
-    w += (size_t)blockIdx.x * top_k;
     __shared__ __align__(16) float e[64 * RT_PER];
-    __shared__ float chosen[64];
-    __shared__ float s_sum;
-    const int lane = threadIdx.x;
-    float v[RT_PER];
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < RT_PER; j++) {
-        const int i = lane + 64 * j;
-        v[j] = i < n ? scores[i] : -INFINITY;
-        m = fmaxf(m, v[j]);
-    }
-    m = wave_max(m);
-#pragma unroll
-    for (int j = 0; j < RT_PER; j++) {
-        const int i = lane + 64 * j;
-        if (i < n) {
-            v[j] = ref_expf(__fsub_rn(v[j], m));
-            e[i] = v[j];
-        }
-    }
-    __syncthreads();
-    if (lane == 0) s_sum = ordered_sum(e, n);
-    __syncthreads();
-    const float s = s_sum;
-#pragma unroll
-    for (int j = 0; j < RT_PER; j++) {
-        const int i = lane + 64 * j;
-        if (i < n) {
-            if (s > 0.0f) v[j] = __fdiv_rn(v[j], s);
-            if (!(v[j] > -INFINITY)) v[j] = -INFINITY;  // NaN is never chosen
-        }
-    }
-    int got = 0;
-    for (int k = 0; k < top_k; k++) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < RT_PER; j++)
-            if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int oi = __shfl_xor(bi, o);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
-        if (!(bv > -INFINITY)) break;
-#pragma unroll
-        for (int j = 0; j < RT_PER; j++)
-            if (lane + 64 * j == bi) v[j] = -INFINITY;
-        if (lane == 0) { ids[k] = bi; chosen[k] = bv; }
-        got = k + 1;
-    }
-    if (lane == 0) {
-        float sw = 0.0f;
-        if (norm_topk)
-            for (int k = 0; k < got; k++) sw = __fadd_rn(sw, chosen[k]);
-        for (int k = 0; k < got; k++) w[k] = (norm_topk && sw > 0.0f) ? __fdiv_rn(chosen[k], sw) : chosen[k];
-        for (int k = got; k < top_k; k++) { ids[k] = -1; w[k] = 0.0f; }
-    }
+    __shared__ double tab[32];
+    // row blockIdx.x of a batch (one row: 0)
+    softmax_route_wave(scores + (size_t)blockIdx.x * n, n, top_k, norm_topk, ids + (size_t)blockIdx.x * top_k,
+                       w + (size_t)blockIdx.x * top_k, e, tab);
 }
 
 // ---- SiLU(g) * u (qwen3_moe_model.rs:518-522, model.rs:527-531) ----------
