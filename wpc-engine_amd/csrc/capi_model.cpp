@@ -224,6 +224,17 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
     const bool defer_d = defer_down(m);
     const float* d2 = nullptr;  // the previous down's deferred slices, if any
     int n_d2 = 1;
+    // EXACT MoE: the last layer's expert combine, left to the next RMSNorm of
+    // the residual (one launch fewer per layer)
+    const wpcg_moe* pend = nullptr;
+    auto norm_residual = [&](const float* nw) -> hipError_t {
+        if (const wpcg_moe* p = pend) {
+            pend = nullptr;
+            return launch_rms_norm_combine(m->residual, nw, H, c.eps, m->normed, p->ys, p->ids, p->w,
+                                           (int)p->top_k, s);
+        }
+        return launch_rms_norm(mode, m->residual, nw, H, c.eps, m->normed, s);
+    };
     for (uint32_t l = 0; l < c.n_layers; l++) {
         Layer& L = m->layers[l];
         bool fused = fast;
@@ -239,7 +250,7 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
             WPCG_HIP(launch_gemv_fast(qkv_jobs, 3, s));
         } else {
             if (d2) return fail(WPCG_E_UNSUPPORTED, "deferred down slices without a FAST reader");
-            WPCG_HIP(launch_rms_norm(mode, m->residual, L.in_ln, H, c.eps, m->normed, s));
+            WPCG_HIP(norm_residual(L.in_ln));
             wpcg_linear* qkv[3] = {L.q, L.k, L.v};
             const float* xs[3] = {m->normed, m->normed, m->normed};
             float* ys[3] = {m->q, m->k, m->v};
@@ -315,9 +326,12 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
             }
         }
         if (o2) return fail(WPCG_E_UNSUPPORTED, "deferred o_proj slice without a FAST reader");
-        WPCG_HIP(launch_rms_norm(mode, m->residual, L.post_ln, H, c.eps, m->normed, s));
+        WPCG_HIP(norm_residual(L.post_ln));
         if (c.n_experts) {
-            if (int rc = moe_run(L.moe, m->normed, m->residual, m->residual, s)) return rc;
+            const bool defer = mode == WPCG_MODE_EXACT && rms_norm_combine_ok(H, (int)L.moe->top_k);
+            if (int rc = moe_run(L.moe, m->normed, m->residual, m->residual, s, nullptr, 0.0f, nullptr, defer))
+                return rc;
+            if (defer) pend = L.moe;
         } else {
             wpcg_linear* gu[2] = {L.gate, L.up};
             const float* x2[2] = {m->normed, m->normed};
@@ -351,7 +365,7 @@ int enqueue_step(wpcg_model* m, hipStream_t s)
             return WPCG_OK;
         }
     } else {
-        WPCG_HIP(launch_rms_norm(mode, m->residual, m->final_norm, H, c.eps, m->normed, s));
+        WPCG_HIP(norm_residual(m->final_norm));
         if (int rc = wpcg_linear_matvec(head, m->normed, m->logits, s)) return rc;
     }
     WPCG_HIP(launch_argmax_next(m->logits, (int)c.vocab, m->st, m->tokens, s));

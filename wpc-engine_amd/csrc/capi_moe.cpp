@@ -56,7 +56,7 @@ DeviceMatrix expert_view(int scheme, uint64_t rows, uint64_t cols)
 // K-slice of the GEMV that wrote x; the router and gate/up add it as they
 // read x, and the down projection adds it to `add`.
 int wpcg::moe_run(wpcg_moe* m, const float* x_dev, float* out_dev, const float* add, hipStream_t s,
-                  const float* nw, float eps, const float* x_add)
+                  const float* nw, float eps, const float* x_add, bool defer_combine)
 {
     const int K = (int)m->top_k, H = (int)m->hidden, I = (int)m->inter;
     if (x_add && !(m->mode == WPCG_MODE_FAST && m->routed && nw && add))
@@ -144,6 +144,7 @@ int wpcg::moe_run(wpcg_moe* m, const float* x_dev, float* out_dev, const float* 
             jobs[k] = GemvJob{&m->down, &m->plan, m->h + (size_t)k * I, nullptr, m->ys + (size_t)k * H, m->ids, k};
         WPCG_HIP(launch_gemv_exact_multi(jobs, K, s));
     }
+    if (defer_combine && m->mode == WPCG_MODE_EXACT) return WPCG_OK;  // folded into the caller's next norm
     WPCG_HIP(launch_combine(m->ys, m->ids, m->w, K, out_dev, H, add, s));
     return WPCG_OK;
 }

@@ -1166,6 +1166,85 @@ __global__ __launch_bounds__(AM_WG) void k_argmax_rows(const float* __restrict__
     if (threadIdx.x == 0) out[blockIdx.x] = bi >= 0 ? (uint32_t)bi : 0u;
 }
 
+// EXACT: the MoE layer's weighted combine folded into the next RMSNorm of
+// the residual. x (the residual) becomes x + sum_k w_k y_k, the sum taken
+// in chosen order from 0 over the slots that ran (ids[k] >= 0), each
+// product and sum rounded (qwen3_moe_model.rs:526-533, as k_combine); the
+// kernel writes it back to x, then RMSNorms it into out exactly as
+// k_rms_norm<EXACT> does. One workgroup; n % 4 == 0, n <= RC_MAXN,
+// top_k <= RC_MAXK. (In place of a combine launch before the norm.)
+constexpr int RC_MAXN = 4096, RC_MAXK = 8;
+__global__ __launch_bounds__(NW) void k_rms_norm_combine(float* __restrict__ x, const float* __restrict__ w,
+                                                         int n, float eps, float* __restrict__ out,
+                                                         const float* __restrict__ ys,
+                                                         const int32_t* __restrict__ ids,
+                                                         const float* __restrict__ cw, int top_k)
+{
+    constexpr int V = RC_MAXN / 4 / NW;
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    __shared__ __align__(16) float sq[RC_MAXN];
+    __shared__ float s_total;
+    // every load first: x, the norm weights, the slots' outputs (range
+    // checked, none past n), then the slots' ids and weights
+    const auto xr = buf_rsrc(x, n * 4), wr = buf_rsrc(w, n * 4);
+    f4 xv[V], wv[V], yv[RC_MAXK][V];
+#pragma unroll
+    for (int u = 0; u < V; u++) {
+        xv[u] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(xr, (threadIdx.x + u * NW) * 16, 0, 0));
+        wv[u] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(wr, (threadIdx.x + u * NW) * 16, 0, 0));
+    }
+#pragma unroll
+    for (int k = 0; k < RC_MAXK; k++) {
+        const auto yr = buf_rsrc(ys + (size_t)k * n, k < top_k ? n * 4 : 0);
+#pragma unroll
+        for (int u = 0; u < V; u++)
+            yv[k][u] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(yr, (threadIdx.x + u * NW) * 16, 0, 0));
+    }
+    int idk[RC_MAXK];
+    float wk[RC_MAXK];
+#pragma unroll
+    for (int k = 0; k < RC_MAXK; k++) {
+        idk[k] = k < top_k ? ids[k] : -1;
+        wk[k] = k < top_k ? cw[k] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < V; u++) {
+        f4 acc = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int k = 0; k < RC_MAXK; k++)
+            if (idk[k] >= 0) {
+                acc.x = __fadd_rn(acc.x, __fmul_rn(wk[k], yv[k][u].x));
+                acc.y = __fadd_rn(acc.y, __fmul_rn(wk[k], yv[k][u].y));
+                acc.z = __fadd_rn(acc.z, __fmul_rn(wk[k], yv[k][u].z));
+                acc.w = __fadd_rn(acc.w, __fmul_rn(wk[k], yv[k][u].w));
+            }
+        xv[u] = f4{__fadd_rn(xv[u].x, acc.x), __fadd_rn(xv[u].y, acc.y), __fadd_rn(xv[u].z, acc.z),
+                   __fadd_rn(xv[u].w, acc.w)};
+        const int i = 4 * (threadIdx.x + u * NW);
+        if (i < n) {
+            *reinterpret_cast<f4*>(&x[i]) = xv[u];
+            *reinterpret_cast<f4*>(&sq[i]) = f4{__fmul_rn(xv[u].x, xv[u].x), __fmul_rn(xv[u].y, xv[u].y),
+                                                __fmul_rn(xv[u].z, xv[u].z), __fmul_rn(xv[u].w, xv[u].w)};
+        }
+    }
+    for (int i = n + threadIdx.x; i < os_padded(n); i += NW) sq[i] = 0.0f;
+    __syncthreads();
+    if (threadIdx.x == 0) s_total = ordered_sum_lds(sq, n);
+    __syncthreads();
+    const float mean_sq = __fdiv_rn(s_total, (float)n);
+    const float scale = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(mean_sq, eps)));
+#pragma unroll
+    for (int u = 0; u < V; u++) {
+        const int i = 4 * (threadIdx.x + u * NW);
+        if (i < n) {
+            out[i] = __fmul_rn(__fmul_rn(xv[u].x, scale), wv[u].x);
+            out[i + 1] = __fmul_rn(__fmul_rn(xv[u].y, scale), wv[u].y);
+            out[i + 2] = __fmul_rn(__fmul_rn(xv[u].z, scale), wv[u].z);
+            out[i + 3] = __fmul_rn(__fmul_rn(xv[u].w, scale), wv[u].w);
+        }
+    }
+}
+
 }  // namespace
 
 // ---- launchers ---------------------------------------------------------------
@@ -1177,6 +1256,17 @@ hipError_t launch_rms_norm(int mode, const float* x, const float* w, int n, floa
         hipLaunchKernelGGL(k_rms_norm<WPCG_MODE_EXACT>, dim3(1), dim3(NW), 0, s, x, w, n, eps, out);
     else
         hipLaunchKernelGGL(k_rms_norm<WPCG_MODE_FAST>, dim3(1), dim3(NW), 0, s, x, w, n, eps, out);
+    return hipGetLastError();
+}
+
+bool rms_norm_combine_ok(int n, int top_k) { return n > 0 && n % 4 == 0 && n <= RC_MAXN && top_k >= 1 && top_k <= RC_MAXK; }
+
+hipError_t launch_rms_norm_combine(float* x, const float* w, int n, float eps, float* out, const float* ys,
+                                   const int32_t* ids, const float* cw, int top_k, hipStream_t s)
+{
+    if (!rms_norm_combine_ok(n, top_k)) return hipErrorInvalidValue;
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(k_rms_norm_combine, dim3(1), dim3(NW), 0, s, x, w, n, eps, out, ys, ids, cw, top_k);
     return hipGetLastError();
 }
 

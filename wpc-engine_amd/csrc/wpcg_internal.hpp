@@ -334,8 +334,11 @@ hipError_t launch_softmax_route(const float* scores, int n, int top_k, int norm_
 // folds the norm in), and one routed down projection whose K-slices are
 // the chosen experts (SiLU*up and the routing weight folded into its x,
 // the combine and the residual into its ordered split-K sum).
+// defer_combine (EXACT): the combine is left out; the caller folds it into
+// the next RMSNorm of `out` (launch_rms_norm_combine with ys, ids and w).
 int moe_run(wpcg_moe* m, const float* x, float* out, const float* add, hipStream_t s,
-            const float* nw = nullptr, float eps = 0.0f, const float* x_add = nullptr);
+            const float* nw = nullptr, float eps = 0.0f, const float* x_add = nullptr,
+            bool defer_combine = false);
 
 // ---- decode step (decode.hip) ----------------------------------------------
 // With rope set, workgroup 0 also copies the RoPE row at the position
@@ -345,6 +348,12 @@ hipError_t launch_embed_tok(const DeviceMatrix& m, const uint32_t* tokens, const
                             const float* sin_t = nullptr, int half = 0, float* rope = nullptr);
 hipError_t launch_rms_norm(int mode, const float* x, const float* w, int n, float eps, float* out,
                            hipStream_t s);
+// EXACT: x += the MoE combine sum_k cw[k] * ys[k] (chosen order, slots with
+// ids[k] >= 0; as the combine launch), then out = RMSNorm(x) as
+// launch_rms_norm in EXACT mode, in one launch.
+bool rms_norm_combine_ok(int n, int top_k);
+hipError_t launch_rms_norm_combine(float* x, const float* w, int n, float eps, float* out, const float* ys,
+                                   const int32_t* ids, const float* cw, int top_k, hipStream_t s);
 // q/k RMSNorm + RoPE, KV append, scores, softmax and output of one layer's
 // attention at the state's position; max_pos <= attention_max_pos().
 int attention_max_pos();
