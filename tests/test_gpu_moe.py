@@ -93,7 +93,7 @@ def test_silu_mul_bit_identical_over_the_float_range(ctx):
 def test_route_matches_the_reference_scan(ctx, n, top_k):
     print(f"[gpu] route n={n} top_k={top_k}", flush=True)
     rng = np.random.default_rng(n + top_k)
-    for case in range(4):
+    for case in range(5):
         p = rng.random(n).astype(np.float32)
         if case == 1 and n > 4:     # ties: lowest index first
             p[:] = np.float32(0.25)
@@ -103,6 +103,10 @@ def test_route_matches_the_reference_scan(ctx, n, top_k):
             p[3] = -np.inf
         if case == 3:
             p = O.softmax((rng.standard_normal(n) * 3).astype(np.float32))
+        if case == 4:               # +0 and -0 tie: the lower index first
+            p = np.where(rng.random(n) < 0.5, np.float32(0.0), np.float32(-0.0)).astype(np.float32)
+            if n > 2:
+                p[n - 1] = np.float32(0.125)
         for norm in (True, False):
             ids, w = wpcg.route(ctx, p, top_k, norm)
             rid, rw = O.route(p, top_k, norm)

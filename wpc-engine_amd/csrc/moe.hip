@@ -259,12 +259,7 @@ __global__ __launch_bounds__(64) void k_route(const float* __restrict__ p, int n
 #pragma unroll
         for (int j = 0; j < RT_PER; j++)
             if (v[j] > bv) { bv = v[j]; bi = lane + 64 * j; }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int oi = __shfl_xor(bi, o);
-            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-        }
+        wave_argmax(bv, bi);  // the scan of softmax_route_wave
         if (!(bv > -INFINITY)) break;  // nothing left to choose
 #pragma unroll
         for (int j = 0; j < RT_PER; j++)
