@@ -115,43 +115,67 @@ __device__ __forceinline__ void load16(const float* xl, float xv[16])
     }
 }
 
+// float of byte B of w (one v_cvt_f32_ubyteB)
+template <int B>
+__device__ __forceinline__ float byte_f(uint32_t w) { return (float)((w >> (8 * B)) & 0xFFu); }
+// the same as one instruction the compiler keeps: from a masked word it
+// would otherwise extract each nibble again (bit-field extract + convert)
+template <int B>
+__device__ __forceinline__ float byte_cvt(uint32_t w)
+{
+    float r;
+    if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w));
+    else if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w));
+    else if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(w));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(w));
+    return r;
+}
+
 // AVX2 lane L of matvec_v4_fused over one block: for g in 0..8, the low
 // nibble of ref byte g*8+L (activation G = g), then its high nibble (G = 8+g).
+// The nibbles are masked four at a time into bytes, each then one byte
+// conversion (per block 22 instructions for the 16 codes instead of 28
+// bit-field extracts and conversions).
 __device__ __forceinline__ float v4_exact_block(uint2 c, uint32_t p, const float* xl, float acc)
 {
     const float zp = h2f(p & 0xFFFFu), sc = h2f(p >> 16);
     float xv[16];
     load16(xl, xv);
+    const uint32_t M = 0x0F0F0F0Fu;
+    const uint32_t lx = c.x & M, ly = c.y & M, hx = (c.x >> 4) & M, hy = (c.y >> 4) & M;
+    const float lo[8] = {byte_cvt<0>(lx), byte_cvt<1>(lx), byte_cvt<2>(lx), byte_cvt<3>(lx),
+                         byte_cvt<0>(ly), byte_cvt<1>(ly), byte_cvt<2>(ly), byte_cvt<3>(ly)};
+    const float hi[8] = {byte_cvt<0>(hx), byte_cvt<1>(hx), byte_cvt<2>(hx), byte_cvt<3>(hx),
+                         byte_cvt<0>(hy), byte_cvt<1>(hy), byte_cvt<2>(hy), byte_cvt<3>(hy)};
 #pragma unroll
     for (int g = 0; g < 8; g++) {
-        const uint32_t w = g < 4 ? c.x : c.y;
-        const uint32_t byte = (w >> (8 * (g & 3))) & 0xFFu;
-        const float lo = (float)(byte & 15u), hi = (float)(byte >> 4);
-        acc = __builtin_fmaf(__builtin_fmaf(lo, sc, zp), xv[g], acc);
-        acc = __builtin_fmaf(__builtin_fmaf(hi, sc, zp), xv[8 + g], acc);
+        acc = __builtin_fmaf(__builtin_fmaf(lo[g], sc, zp), xv[g], acc);
+        acc = __builtin_fmaf(__builtin_fmaf(hi[g], sc, zp), xv[8 + g], acc);
     }
     return acc;
 }
 
 // AVX2 lane L of matvec_v3_fused over one block: codes k = G*8+L for G in
 // 0..16, natural order. Low 4 bits: low-plane byte G (G < 8, low nibble) or
-// G-8 (high nibble); top 2 bits: high-plane byte G&3, bits 2*(G>>2).
+// G-8 (high nibble); top 2 bits: high-plane byte G&3, bits 2*(G>>2). Four
+// codes are assembled per dword (nibbles masked, top bits shifted into bits
+// 4-5 of each byte), each then one byte conversion.
 __device__ __forceinline__ float v3_exact_block(uint2 c, uint32_t h, uint32_t p, const float* xl,
                                                 float acc)
 {
     const float zp = h2f(p & 0xFFFFu), sc = h2f(p >> 16);
     float xv[16];
     load16(xl, xv);
+    const uint32_t M = 0x0F0F0F0Fu, T = 0x30303030u;
+    // G = 0..3, 4..7, 8..11, 12..15
+    const uint32_t d0 = (c.x & M) | ((h << 4) & T), d1 = (c.y & M) | ((h << 2) & T);
+    const uint32_t d2 = ((c.x >> 4) & M) | (h & T), d3 = ((c.y >> 4) & M) | ((h >> 2) & T);
+    const float code[16] = {byte_f<0>(d0), byte_f<1>(d0), byte_f<2>(d0), byte_f<3>(d0),
+                            byte_f<0>(d1), byte_f<1>(d1), byte_f<2>(d1), byte_f<3>(d1),
+                            byte_f<0>(d2), byte_f<1>(d2), byte_f<2>(d2), byte_f<3>(d2),
+                            byte_f<0>(d3), byte_f<1>(d3), byte_f<2>(d3), byte_f<3>(d3)};
 #pragma unroll
-    for (int G = 0; G < 16; G++) {
-        const int gb = G & 7;
-        const uint32_t w = gb < 4 ? c.x : c.y;
-        const uint32_t byte = (w >> (8 * (gb & 3))) & 0xFFu;
-        const uint32_t nib = G < 8 ? (byte & 15u) : (byte >> 4);
-        const uint32_t top = (h >> (8 * (G & 3) + 2 * (G >> 2))) & 3u;
-        const float code = (float)(nib | (top << 4));
-        acc = __builtin_fmaf(__builtin_fmaf(code, sc, zp), xv[G], acc);
-    }
+    for (int G = 0; G < 16; G++) acc = __builtin_fmaf(__builtin_fmaf(code[G], sc, zp), xv[G], acc);
     return acc;
 }
 
