@@ -264,6 +264,42 @@ __device__ void head_rms_rope(const float* x, const float* w, float* y, float* r
     __syncthreads();
 }
 
+// EXACT q and k head norms + RoPE together: the two index-order sums of
+// squares run at once, on lanes of different waves (one after the other,
+// each was a chain behind two barriers).
+__device__ void head_rms_rope_qk_exact(const float* xq, const float* wq, float* yq, const float* xk,
+                                       const float* wk, float* yk, int hd, float eps, const float* c,
+                                       const float* sn)
+{
+    __shared__ __align__(16) float sq[2][256];
+    __shared__ float s_tot[2];
+    __shared__ float s_tmp[2][256];
+    for (int i = threadIdx.x; i < os_padded(hd); i += blockDim.x) {
+        sq[0][i] = i < hd ? __fmul_rn(xq[i], xq[i]) : 0.0f;
+        sq[1][i] = i < hd ? __fmul_rn(xk[i], xk[i]) : 0.0f;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) s_tot[0] = ordered_sum_lds(sq[0], hd);
+    if (threadIdx.x == 64) s_tot[1] = ordered_sum_lds(sq[1], hd);
+    __syncthreads();
+    const float scq = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(s_tot[0], (float)hd), eps)));
+    const float sck = __fdiv_rn(1.0f, sqrt_rn(__fadd_rn(__fdiv_rn(s_tot[1], (float)hd), eps)));
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
+        s_tmp[0][i] = __fmul_rn(__fmul_rn(xq[i], scq), wq[i]);
+        s_tmp[1][i] = __fmul_rn(__fmul_rn(xk[i], sck), wk[i]);
+    }
+    __syncthreads();
+    const int half = hd / 2;
+    for (int i = threadIdx.x; i < 2 * half; i += blockDim.x) {
+        const int r = i / half, e = i - r * half;
+        float* y = r ? yk : yq;
+        const float x1 = s_tmp[r][e], x2 = s_tmp[r][e + half];
+        y[e] = __fsub_rn(__fmul_rn(x1, c[e]), __fmul_rn(x2, sn[e]));
+        y[e + half] = __fadd_rn(__fmul_rn(x2, c[e]), __fmul_rn(x1, sn[e]));
+    }
+    __syncthreads();
+}
+
 template <int MODE>
 __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ qp,
                                                      const float* __restrict__ kp,
@@ -287,8 +323,12 @@ __global__ __launch_bounds__(AT_WG) void k_attention(const float* __restrict__ q
     const int half = hd / 2;
     const float* c = cos_t + (size_t)pos * half;
     const float* sn = sin_t + (size_t)pos * half;
-    head_rms_rope<MODE>(qp + (size_t)h * hd, qn, qs, red, hd, eps, c, sn);
-    head_rms_rope<MODE>(kp + (size_t)j * hd, kn, ks, red, hd, eps, c, sn);
+    if constexpr (MODE == WPCG_MODE_EXACT) {
+        head_rms_rope_qk_exact(qp + (size_t)h * hd, qn, qs, kp + (size_t)j * hd, kn, ks, hd, eps, c, sn);
+    } else {
+        head_rms_rope<MODE>(qp + (size_t)h * hd, qn, qs, red, hd, eps, c, sn);
+        head_rms_rope<MODE>(kp + (size_t)j * hd, kn, ks, red, hd, eps, c, sn);
+    }
     for (int i = threadIdx.x; i < hd; i += AT_WG) vs[i] = vp[(size_t)j * hd + i];
     __syncthreads();
     const float* kb = kc + (size_t)j * max_pos * hd;
